@@ -1,0 +1,184 @@
+"""Regrow benchmark: bit-exact requantization of BF16 weights (with the imatrix) on one MI355X.
+
+A step is one pass of the hot path over one batch of synthetic input: the configuration-2 workload
+-- the K-quant family Q2_K, Q3_K, Q4_K, Q5_K, Q6_K with an imatrix, on
+the two Qwen3-0.6B-shaped BF16 tensors token_embd 151936x1024 and ffn_down 1024x3072 (10 launches
+per step, inputs resident in HBM before timing starts).
+
+value = BF16 bytes consumed per step / step time (GB/s), i.e. the requant throughput of the family.
+Per-type throughput, the HBM-bound legacy types (Q8_0 / Q4_0 on configuration 1 and on the
+embedding) and the reference's own C quantizers on the host cores (cpu_baseline) are reported in the
+same JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+KTYPES = [10, 11, 12, 13, 14]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def alg_bytes(t, nw, npr, imx):
+    """algorithmic HBM bytes of one requant launch: BF16 in + quant out + imatrix"""
+    from seedpack_amd.requant import QFUN
+    _, qk, bs = QFUN[t]
+    return 2 * nw + nw // qk * bs + (4 * npr if imx else 0)
+
+
+def cpu_baseline(tensors, target_s=12.0):
+    """the reference's C quantizers (oracle/_ref) on the host cores, on the first rows of the
+    embedding (a bounded sample of the same workload)"""
+    from oracle import ref
+    from seedpack_amd import synth
+    if not ref.available():
+        return None
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    (w_emb, imx_emb) = tensors["token_embd"]
+    (w_dn, imx_dn) = tensors["ffn_down"]
+    x = synth.bf16_to_f32(w_dn).reshape(w_dn.shape)
+    t0 = time.perf_counter()
+    for t in KTYPES:
+        ref.quantize(t, x, imx_dn, threads=threads)
+    rate = 5 * x.size / (time.perf_counter() - t0)             # weights/s over the family
+    rows = int(min(w_emb.shape[0], max(1024, target_s * rate / 5 / w_emb.shape[1])))
+    xe = synth.bf16_to_f32(w_emb[:rows]).reshape(rows, w_emb.shape[1])
+    t0 = time.perf_counter()
+    for t in KTYPES:
+        ref.quantize(t, xe, imx_emb, threads=threads)
+    dt = time.perf_counter() - t0
+    return {"value": round(5 * 2 * xe.size / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "reference",
+            "sample": f"token_embd rows 0..{rows} ({xe.size} weights) x Q2_K..Q6_K with imatrix, "
+                      f"oracle/_ref built from the reference's ggml-quants.c, {threads} threads, {dt:.1f} s",
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the path shards by rows "
+              "with no exchange, so N GPUs is N independent copies of this run", file=sys.stderr)
+        sys.exit(2)
+
+    from seedpack_amd import device as dev
+    from seedpack_amd import synth
+    from seedpack_amd.gpuquant import quantize_into
+    from seedpack_amd.requant import NAMES, row_size
+
+    log("bench: generating synthetic inputs")
+    tensors = {"token_embd": synth.tensor(2, 0), "ffn_down": synth.tensor(2, 1)}
+    stream = dev.Stream()
+    dsrc, dimx, dout = {}, {}, {}
+    for name, (w, imx) in tensors.items():
+        dsrc[name] = dev.DeviceArray.from_host(w.reshape(-1), stream.handle)
+        dimx[name] = dev.DeviceArray.from_host(imx, stream.handle)
+        for t in KTYPES:
+            dout[(name, t)] = dev.DeviceArray(w.shape[0] * row_size(t, w.shape[1]), np.uint8)
+    launches = [(t, name) for t in KTYPES for name in tensors]
+    ev = {k: (dev.Event(), dev.Event()) for k in launches}
+
+    def step(record):
+        for (t, name) in launches:
+            w = tensors[name][0]
+            if record:
+                ev[(t, name)][0].record(stream.handle)
+            quantize_into(t, dsrc[name], w.shape[1], dout[(name, t)], dimx[name], 0, stream.handle)
+            if record:
+                ev[(t, name)][1].record(stream.handle)
+
+    log("bench: warmup")
+    for _ in range(a.warmup):
+        step(False)
+    stream.synchronize()
+    dev.synchronize()
+    per = {k: 0.0 for k in launches}
+    log(f"bench: timing {a.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step(True)
+        stream.synchronize()
+        for k in launches:
+            per[k] += ev[k][0].elapsed_ms(ev[k][1])
+    dev.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / a.steps
+    bf16_bytes = sum(2 * tensors[n][0].size for (_, n) in launches)
+    value = bf16_bytes / (ms_step / 1e3) / 1e9
+
+    per_type = {}
+    for t in KTYPES:
+        ms = sum(per[(t, n)] for n in tensors) / a.steps
+        nb = sum(2 * tensors[n][0].size for n in tensors)
+        per_type[NAMES[t]] = {"GB_s": round(nb / (ms / 1e3) / 1e9, 2), "ms": round(ms, 3)}
+    dom = max(launches, key=lambda k: per[k])
+    t, n = dom
+    w = tensors[n][0]
+    dom_ms = per[dom] / a.steps
+    ab = alg_bytes(t, w.size, w.shape[1], True)
+    achieved = ab / (dom_ms / 1e3) / 1e9
+    roofline = {"bound": "hbm", "kernel": f"k_kquant<{NAMES[t]}> on {n} {w.shape[0]}x{w.shape[1]}",
+                "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 5), "traffic": None,
+                "algorithmic_bytes": ab, "avg_launch_ms": round(dom_ms, 4),
+                "note": "search-bound K-quant (VALU); HBM fraction reported as the contract asks"}
+
+    # HBM-bound legacy types: configuration 1 tensor and the embedding, Q8_0 / Q4_0 without imatrix
+    legacy = {}
+    w1, _ = synth.tensor(1, 0)
+    d1 = dev.DeviceArray.from_host(w1.reshape(-1), stream.handle)
+    for t in (8, 2):
+        for name, src, shape in (("cfg1", d1, w1.shape), ("token_embd", dsrc["token_embd"], tensors["token_embd"][0].shape)):
+            out = dev.DeviceArray(shape[0] * row_size(t, shape[1]), np.uint8)
+            e0, e1 = dev.Event(), dev.Event()
+            for _ in range(2):
+                quantize_into(t, src, shape[1], out, None, 0, stream.handle)
+            reps = 20
+            e0.record(stream.handle)
+            for _ in range(reps):
+                quantize_into(t, src, shape[1], out, None, 0, stream.handle)
+            e1.record(stream.handle)
+            ms = e0.elapsed_ms(e1) / reps
+            nw = shape[0] * shape[1]
+            legacy[f"{NAMES[t]}_{name}"] = {"GB_s_bf16_in": round(2 * nw / (ms / 1e3) / 1e9, 1), "ms": round(ms, 4),
+                                           "hbm_frac": round(alg_bytes(t, nw, shape[1], False) / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+    cpu = None if a.no_cpu else cpu_baseline(tensors)
+    line = {"metric": "requant GB/s (BF16 in), K-quant family Q2_K..Q6_K with imatrix", "value": round(value, 3),
+            "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 3),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (seeded N(0,0.02) BF16, LogNormal(0,1) imatrix)",
+            "config": {"workload": "cfg2: Q2_K,Q3_K,Q4_K,Q5_K,Q6_K (imatrix) on token_embd 151936x1024 + ffn_down 1024x3072",
+                       "bf16_bytes_per_step": bf16_bytes, "launches_per_step": len(launches)},
+            "per_type": per_type, "legacy_hbm_types": legacy, "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,781 @@
+"""ORACLE -- test infrastructure only. Never imported by the product (seedpack_amd/).
+
+A CPU restatement, in numpy, of llama.cpp's quantizers as vendored by the reference
+(/root/reference/seedpack/ggml/ggml-quants.c, cited per function as ggml-quants.c:LINES).
+
+Formulation: every block (or sub-block) is a row of a 2-D float32 array and all blocks are processed
+together; inside a block every reduction runs over the element index in order (seqsum: a
+left-to-right float32 accumulation starting at +0.0, as the C loops do), every product is taken in
+the C expression's order, and comparisons keep the C code's strict/non-strict sense. numpy float32
+arithmetic is IEEE single with no contraction, which is what the reference's -ffp-contract=off
+build computes.
+
+Pinned by: tests/test_oracle.py checks every function here byte-for-byte against the reference's
+own C build (oracle/_ref, from oracle/Makefile) on seeded inputs, and against the committed golden
+fixtures in tests/golden/ (written from that build).
+"""
+import numpy as np
+
+F = np.float32
+GROUP_MAX_EPS = F(1e-15)       # ggml-quants.c:20
+
+QK = {2: 32, 3: 32, 6: 32, 7: 32, 8: 32, 10: 256, 11: 256, 12: 256, 13: 256, 14: 256, 16: 256, 17: 256,
+      18: 256, 19: 256, 20: 32, 21: 256, 22: 256, 23: 256, 29: 256, 42: 64}
+BS = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 16: 66, 17: 74,
+      18: 98, 19: 50, 20: 18, 21: 110, 22: 82, 23: 136, 29: 56, 42: 18}
+
+
+# ------------------------------------------------------------------ scalar primitives
+
+def seqsum(a):
+    """left-to-right float32 sum along the last axis, starting from +0.0 (the C `s = 0; s += a[i]`)"""
+    a = np.asarray(a, F)
+    z = np.zeros(a.shape[:-1] + (1,), F)
+    return np.add.accumulate(np.concatenate([z, a], axis=-1), axis=-1, dtype=F)[..., -1]
+
+
+def nearest_int(v):
+    """ggml-quants.c:621-626: bits of (v + 12582912.f), low 23 bits minus 2^22"""
+    with np.errstate(all="ignore"):
+        t = (np.asarray(v, F) + F(12582912.0)).astype(F)
+    return (t.view(np.int32) & 0x007FFFFF) - 0x00400000
+
+
+def fp16_bits(v):
+    """f32 -> IEEE half bits, round to nearest even (numpy's conversion); NaN -> 0x7E00 | sign
+    (ggml-impl.h:417-443)"""
+    v = np.asarray(v, F)
+    with np.errstate(all="ignore"):
+        h = v.astype(np.float16).view(np.uint16)
+    nan = np.isnan(v)
+    if nan.any():
+        h = np.where(nan, (v.view(np.uint32) >> 16).astype(np.uint16) & 0x8000 | 0x7E00, h).astype(np.uint16)
+    return h
+
+
+def fp16_to_f32(h):
+    return np.asarray(h, np.uint16).view(np.float16).astype(F)
+
+
+def roundf(v):
+    """C roundf: half away from zero"""
+    v = np.asarray(v, F)
+    t = np.trunc(v)
+    return np.where(np.abs(v - t) >= F(0.5), t + np.sign(v), t).astype(F)
+
+
+def f2i_trunc(v):
+    """C float -> int conversion (truncation toward zero), in range"""
+    return np.trunc(np.asarray(v, F)).astype(np.int64)
+
+
+def i8(v):
+    """C conversion of an int to int8_t (wraps)"""
+    return ((np.asarray(v, np.int64) + 128) & 0xFF) - 128
+
+
+def u8(v):
+    return np.asarray(v, np.int64) & 0xFF
+
+
+def _errs():
+    return np.errstate(divide="ignore", invalid="ignore", over="ignore")
+
+
+# ------------------------------------------------------------------ search helpers (rows = blocks)
+
+def make_qx_quants(X, nmax, QW):
+    """ggml-quants.c:628-695 with rmse_type = 1; QW None means w = x*x. Returns (scale, L int)."""
+    X = np.asarray(X, F)
+    R, n = X.shape
+    W = (X * X) if QW is None else np.asarray(QW, F)
+    amax = np.zeros(R, F)
+    mx = np.zeros(R, F)
+    for i in range(n):
+        ax = np.abs(X[:, i])
+        up = ax > amax
+        amax = np.where(up, ax, amax)
+        mx = np.where(up, X[:, i], mx)
+    zero = amax < GROUP_MAX_EPS
+    with _errs():
+        iscale = F(-nmax) / mx
+
+        def levels(isc):
+            return np.clip(nearest_int(isc[:, None] * X), -nmax, nmax - 1)
+
+        def sums(l):
+            lf = l.astype(F)
+            return seqsum(W * X * lf), seqsum(W * lf * lf)
+
+        l = levels(iscale)
+        sumlx, suml2 = sums(l)
+        scale = np.where(suml2 != 0, sumlx / suml2, F(0)).astype(F)
+        best = (scale * sumlx).astype(F)
+        best_is = iscale.copy()
+        for is_ in range(-9, 10):
+            if is_ == 0:
+                continue
+            isc = (-(F(nmax) + F(0.1) * F(is_)) / mx).astype(F)
+            sx, s2 = sums(levels(isc))
+            up = (s2 > 0) & (sx * sx > best * s2)
+            best_is = np.where(up, isc, best_is)
+            scale = np.where(up, sx / s2, scale).astype(F)
+            best = np.where(up, scale * sx, best).astype(F)
+        L = nmax + levels(best_is)
+    scale = np.where(zero, F(0), scale).astype(F)
+    L[zero] = 0
+    return scale, L
+
+
+def make_qkx2_quants(X, W, nmax, rmin, rdelta, nstep, use_mad):
+    """ggml-quants.c:799-878. Returns (scale, the_min, L)."""
+    X = np.asarray(X, F)
+    W = np.asarray(W, F)
+    R, n = X.shape
+    mn, mx = X[:, 0].copy(), X[:, 0].copy()
+    sum_w = W[:, 0].copy()
+    sum_x = (sum_w * X[:, 0]).astype(F)
+    for i in range(1, n):
+        mn = np.where(X[:, i] < mn, X[:, i], mn)
+        mx = np.where(X[:, i] > mx, X[:, i], mx)
+        sum_w = (sum_w + W[:, i]).astype(F)
+        sum_x = (sum_x + W[:, i] * X[:, i]).astype(F)
+    mn = np.where(mn > 0, F(0), mn).astype(F)
+    degen = mx == mn
+    err = (lambda d: np.abs(d)) if use_mad else (lambda d: d * d)
+    with _errs():
+        iscale = (F(nmax) / (mx - mn)).astype(F)
+        scale = (F(1) / iscale).astype(F)
+        L = np.clip(nearest_int(iscale[:, None] * (X - mn[:, None])), 0, nmax)
+        best = seqsum(W * err(scale[:, None] * L.astype(F) + mn[:, None] - X))
+        for is_ in range(nstep + 1):
+            iscale = ((F(rmin) + F(rdelta) * F(is_) + F(nmax)) / (mx - mn)).astype(F)
+            l = np.clip(nearest_int(iscale[:, None] * (X - mn[:, None])), 0, nmax)
+            lf = l.astype(F)
+            sum_l = seqsum(W * lf)
+            sum_l2 = seqsum(W * lf * lf)
+            sum_xl = seqsum(W * lf * X)
+            D = (sum_w * sum_l2 - sum_l * sum_l).astype(F)
+            ok = D > 0
+            ts = ((sum_w * sum_xl - sum_x * sum_l) / D).astype(F)
+            tm = ((sum_l2 * sum_x - sum_l * sum_xl) / D).astype(F)
+            pos = tm > 0
+            tm = np.where(pos, F(0), tm).astype(F)
+            ts = np.where(pos, sum_xl / sum_l2, ts).astype(F)
+            cur = seqsum(W * err(ts[:, None] * lf + tm[:, None] - X))
+            up = ok & (cur < best)
+            L = np.where(up[:, None], l, L)
+            best = np.where(up, cur, best).astype(F)
+            scale = np.where(up, ts, scale).astype(F)
+            mn = np.where(up, tm, mn).astype(F)
+    if nstep < 1:
+        raise NotImplementedError
+    scale = np.where(degen, F(0), scale).astype(F)
+    L[degen] = 0
+    return scale, (-mn).astype(F), L
+
+
+def make_qkx3_quants(X, W, nmax, rmin, rdelta, nstep):
+    """ggml-quants.c:993-1075 with weights given and use_mad = false. The running `min` enters every
+    later step's iscale and levels. Returns (scale, the_min, L)."""
+    X = np.asarray(X, F)
+    W = np.asarray(W, F)
+    R, n = X.shape
+    mn, mx = X[:, 0].copy(), X[:, 0].copy()
+    sum_w = W[:, 0].copy()
+    sum_x = (sum_w * X[:, 0]).astype(F)
+    for i in range(1, n):
+        mn = np.where(X[:, i] < mn, X[:, i], mn)
+        mx = np.where(X[:, i] > mx, X[:, i], mx)
+        sum_w = (sum_w + W[:, i]).astype(F)
+        sum_x = (sum_x + W[:, i] * X[:, i]).astype(F)
+    mn = np.where(mn > 0, F(0), mn).astype(F)
+    degen = mx <= mn
+    with _errs():
+        iscale = (F(nmax) / (mx - mn)).astype(F)
+        scale = (F(1) / iscale).astype(F)
+        L = np.clip(nearest_int(iscale[:, None] * (X - mn[:, None])), 0, nmax)
+        d0 = scale[:, None] * L.astype(F) + mn[:, None] - X
+        best = seqsum(W * (d0 * d0))
+        for is_ in range(nstep + 1):
+            iscale = ((F(rmin) + F(rdelta) * F(is_) + F(nmax)) / (mx - mn)).astype(F)
+            v = (iscale[:, None] * (X - mn[:, None])).astype(F)
+            vc = np.where(v < F(nmax), v, F(nmax))
+            l = np.where(v > 0, nearest_int(vc), 0)
+            lf = l.astype(F)
+            wl = W * lf
+            sum_l = seqsum(wl)
+            sum_l2 = seqsum(wl * lf)
+            sum_xl = seqsum(wl * X)
+            D = (sum_w * sum_l2 - sum_l * sum_l).astype(F)
+            ok = D > 0
+            ts = ((sum_w * sum_xl - sum_x * sum_l) / D).astype(F)
+            tm = ((sum_l2 * sum_x - sum_l * sum_xl) / D).astype(F)
+            pos = tm > 0
+            tm = np.where(pos, F(0), tm).astype(F)
+            ts = np.where(pos, sum_xl / sum_l2, ts).astype(F)
+            d = ts[:, None] * lf + tm[:, None] - X
+            mad = seqsum(W * (d * d))
+            up = ok & (mad < best)
+            L = np.where(up[:, None], l, L)
+            best = np.where(up, mad, best).astype(F)
+            scale = np.where(up, ts, scale).astype(F)
+            mn = np.where(up, tm, mn).astype(F)
+    scale = np.where(degen, F(0), scale).astype(F)
+    L[degen] = 0
+    return scale, (-mn).astype(F), L
+
+
+def make_qp_quants(X, nmax, QW):
+    """ggml-quants.c:1077-1148. L is uint8_t in C (stores wrap). Returns (scale, L)."""
+    X = np.asarray(X, F)
+    QW = np.asarray(QW, F)
+    R, n = X.shape
+    mx = np.zeros(R, F)
+    for i in range(n):
+        mx = np.where(mx > X[:, i], mx, X[:, i])
+    zero = mx < GROUP_MAX_EPS
+    with _errs():
+        iscale = (F(nmax) / mx).astype(F)
+        L = u8(nearest_int(iscale[:, None] * X))
+        scale = (F(1) / iscale).astype(F)
+        diff = X - scale[:, None] * L.astype(F)
+        best = seqsum(QW * diff * diff)
+        for is_ in range(-4, 5):
+            if is_ == 0:
+                continue
+            isc = ((F(0.1) * F(is_) + F(nmax)) / mx).astype(F)
+            sc = (F(1) / isc).astype(F)
+            l = np.minimum(nmax, nearest_int(isc[:, None] * X))
+            diff = X - sc[:, None] * l.astype(F)
+            mse = seqsum(QW * diff * diff)
+            up = mse < best
+            best = np.where(up, mse, best).astype(F)
+            iscale = np.where(up, isc, iscale).astype(F)
+        L = u8(np.minimum(nmax, nearest_int(iscale[:, None] * X)))
+        Lf = L.astype(F)
+        sumlx = seqsum(QW * X * Lf)
+        suml2 = seqsum(QW * Lf * Lf)
+        active = np.ones(R, bool)
+        for _ in range(5):
+            changed = np.zeros(R, bool)
+            for i in range(n):
+                w, x, li = QW[:, i], X[:, i], L[:, i].astype(F)
+                slx = (sumlx - w * x * li).astype(F)
+                sl2 = (suml2 - w * li * li).astype(F)
+                c1 = active & (slx > 0) & (sl2 > 0)
+                new_l = np.minimum(nmax, nearest_int(x * sl2 / slx))
+                c2 = c1 & (new_l != L[:, i])
+                nf = new_l.astype(F)
+                slx2 = (slx + w * x * nf).astype(F)
+                sl22 = (sl2 + w * nf * nf).astype(F)
+                c3 = c2 & (slx2 * slx2 * suml2 > sumlx * sumlx * sl22)
+                L[:, i] = np.where(c3, u8(new_l), L[:, i])
+                sumlx = np.where(c3, slx2, sumlx).astype(F)
+                suml2 = np.where(c3, sl22, suml2).astype(F)
+                changed |= c3
+            active &= changed
+            if not active.any():
+                break
+        res = np.where(suml2 > 0, sumlx / suml2, F(0)).astype(F)
+    res = np.where(zero, F(0), res).astype(F)
+    L[zero] = 0
+    return res, L
+
+
+def make_q3_quants(X, nmax):
+    """ggml-quants.c:697-754 with do_rmse = true. Returns (scale, L)."""
+    X = np.asarray(X, F)
+    R, n = X.shape
+    amax = np.zeros(R, F)
+    mx = np.zeros(R, F)
+    for i in range(n):
+        ax = np.abs(X[:, i])
+        up = ax > amax
+        amax = np.where(up, ax, amax)
+        mx = np.where(up, X[:, i], mx)
+    zero = amax < GROUP_MAX_EPS
+    with _errs():
+        iscale = (F(-nmax) / mx).astype(F)
+        L = np.clip(nearest_int(iscale[:, None] * X), -nmax, nmax - 1)
+        Wt = X * X
+        Lf = L.astype(F)
+        sumlx = seqsum(Wt * X * Lf)
+        suml2 = seqsum(Wt * Lf * Lf)
+        active = np.ones(R, bool)
+        for _ in range(5):
+            changed = np.zeros(R, bool)
+            for i in range(n):
+                w, x, li = Wt[:, i], X[:, i], L[:, i].astype(F)
+                slx = (sumlx - w * x * li).astype(F)
+                c1 = active & (slx > 0)
+                sl2 = (suml2 - w * li * li).astype(F)
+                new_l = np.clip(nearest_int(x * sl2 / slx), -nmax, nmax - 1)
+                c2 = c1 & (new_l != L[:, i])
+                nf = new_l.astype(F)
+                slx2 = (slx + w * x * nf).astype(F)
+                sl22 = (sl2 + w * nf * nf).astype(F)
+                c3 = c2 & (sl22 > 0) & (slx2 * slx2 * suml2 > sumlx * sumlx * sl22)
+                L[:, i] = np.where(c3, new_l, L[:, i])
+                sumlx = np.where(c3, slx2, sumlx).astype(F)
+                suml2 = np.where(c3, sl22, suml2).astype(F)
+                changed |= c3
+            active &= changed
+            if not active.any():
+                break
+        res = np.where(suml2 > 0, sumlx / suml2, F(0)).astype(F)
+    L = L + nmax
+    res = np.where(zero, F(0), res).astype(F)
+    L[zero] = 0
+    return res, L
+
+
+# ------------------------------------------------------------------ legacy 32/64 blocks
+
+def _blocks(x, qk):
+    x = np.ascontiguousarray(x, F)
+    return x.reshape(-1, qk)
+
+
+def _row_weights(x, imx, qk):
+    """qw * sqrtf(sigma2 + x*x) with sigma2 = (row sum of x*x, in order) / n_per_row
+    (ggml-quants.c:2082-2090)"""
+    x = np.ascontiguousarray(x, F)
+    nrows, npr = x.shape
+    sigma2 = (seqsum(x * x) / F(npr)).astype(F)
+    qw = np.broadcast_to(np.asarray(imx, F)[None, :], x.shape)
+    w = (qw * np.sqrt(sigma2[:, None] + x * x)).astype(F)
+    return w.reshape(-1, qk)
+
+
+def _pack_nibbles(lo, hi):
+    return (u8(lo) | u8(u8(hi) << 4)).astype(np.uint8)
+
+
+def _out(nb, bs):
+    return np.zeros((nb, bs), np.uint8)
+
+
+def _put16(out, off, h):
+    h = np.asarray(h, np.uint16)
+    out[:, off] = h & 0xFF
+    out[:, off + 1] = h >> 8
+
+
+def q8_0(x, imx=None):
+    """quantize_row_q8_0_ref -- ggml-quants.c:276-299 (imatrix ignored, :2296-2301)"""
+    X = _blocks(x, 32)
+    amax = np.zeros(len(X), F)
+    for j in range(32):
+        a = np.abs(X[:, j])
+        amax = np.where(amax > a, amax, a)
+    with _errs():
+        d = (amax / F(127)).astype(F)
+        idv = np.where(d != 0, F(1) / d, F(0)).astype(F)
+    out = _out(len(X), 34)
+    _put16(out, 0, fp16_bits(d))
+    out[:, 2:] = u8(f2i_trunc(roundf(X * idv[:, None]))).astype(np.uint8)
+    return out.reshape(-1)
+
+
+def _absmax_signed(X):
+    amax = np.zeros(len(X), F)
+    mx = np.zeros(len(X), F)
+    for j in range(X.shape[1]):
+        a = np.abs(X[:, j])
+        up = amax < a
+        amax = np.where(up, a, amax)
+        mx = np.where(up, X[:, j], mx)
+    return mx
+
+
+def q4_0_ref(X):
+    """quantize_row_q4_0_ref -- ggml-quants.c:113-148"""
+    mx = _absmax_signed(X)
+    with _errs():
+        d = (mx / F(-8)).astype(F)
+        idv = np.where(d != 0, F(1) / d, F(0)).astype(F)
+    xi = np.minimum(15, i8(f2i_trunc((X * idv[:, None]).astype(F) + F(8.5))))
+    out = _out(len(X), 18)
+    _put16(out, 0, fp16_bits(d))
+    out[:, 2:] = _pack_nibbles(xi[:, :16], xi[:, 16:])
+    return out
+
+
+def q4_1_ref(X):
+    """quantize_row_q4_1_ref -- ggml-quants.c:150-182"""
+    mn = np.full(len(X), np.finfo(F).max, F)
+    mx = np.full(len(X), -np.finfo(F).max, F)
+    for j in range(32):
+        mn = np.where(X[:, j] < mn, X[:, j], mn)
+        mx = np.where(X[:, j] > mx, X[:, j], mx)
+    with _errs():
+        d = ((mx - mn) / F(15)).astype(F)
+        idv = np.where(d != 0, F(1) / d, F(0)).astype(F)
+    xi = np.minimum(15, i8(f2i_trunc(((X - mn[:, None]) * idv[:, None]).astype(F) + F(0.5))))
+    out = _out(len(X), 20)
+    _put16(out, 0, fp16_bits(d))
+    _put16(out, 2, fp16_bits(mn))
+    out[:, 4:] = _pack_nibbles(xi[:, :16], xi[:, 16:])
+    return out
+
+
+def _q5_bits(out, off, xi):
+    xi = u8(xi)
+    qh = np.zeros(len(xi), np.int64)
+    for j in range(16):
+        qh |= ((xi[:, j] & 0x10) >> 4) << j
+        qh |= ((xi[:, j + 16] & 0x10) >> 4) << (j + 16)
+    for k in range(4):
+        out[:, off + k] = (qh >> (8 * k)) & 0xFF
+    out[:, off + 4:off + 20] = (u8(xi[:, :16] & 0x0F) | u8((xi[:, 16:] & 0x0F) << 4)).astype(np.uint8)
+
+
+def q5_0_ref(X):
+    """quantize_row_q5_0_ref -- ggml-quants.c:185-226"""
+    mx = _absmax_signed(X)
+    with _errs():
+        d = (mx / F(-16)).astype(F)
+        idv = np.where(d != 0, F(1) / d, F(0)).astype(F)
+    xi = np.minimum(31, i8(f2i_trunc((X * idv[:, None]).astype(F) + F(16.5))))
+    out = _out(len(X), 22)
+    _put16(out, 0, fp16_bits(d))
+    _q5_bits(out, 2, xi)
+    return out
+
+
+def q5_1_ref(X):
+    """quantize_row_q5_1_ref -- ggml-quants.c:228-271"""
+    mn = np.full(len(X), np.finfo(F).max, F)
+    mx = np.full(len(X), -np.finfo(F).max, F)
+    for j in range(32):
+        mn = np.where(X[:, j] < mn, X[:, j], mn)
+        mx = np.where(X[:, j] > mx, X[:, j], mx)
+    with _errs():
+        d = ((mx - mn) / F(31)).astype(F)
+        idv = np.where(d != 0, F(1) / d, F(0)).astype(F)
+    xi = u8(f2i_trunc(((X - mn[:, None]) * idv[:, None]).astype(F) + F(0.5)))
+    out = _out(len(X), 24)
+    _put16(out, 0, fp16_bits(d))
+    _put16(out, 2, fp16_bits(mn))
+    _q5_bits(out, 4, xi)
+    return out
+
+
+def q2_0(x, imx=None):
+    """quantize_row_q2_0_ref -- ggml-quants.c:74-110 (imatrix ignored, :2114-2127)"""
+    X = _blocks(x, 64)
+    amax = np.zeros(len(X), F)
+    for j in range(64):
+        a = np.abs(X[:, j])
+        amax = np.where(a > amax, a, amax)
+    with _errs():
+        idv = np.where(amax > 0, F(1) / amax, F(0)).astype(F)
+    q = np.clip(f2i_trunc(roundf(X * idv[:, None])) + 1, 0, 3)
+    out = _out(len(X), 18)
+    _put16(out, 0, fp16_bits(amax))
+    q4 = q.reshape(len(X), 16, 4)
+    out[:, 2:] = (q4[:, :, 0] | (q4[:, :, 1] << 2) | (q4[:, :, 2] << 4) | (q4[:, :, 3] << 6)).astype(np.uint8)
+    return out.reshape(-1)
+
+
+def _legacy(ref, impl_nmax, kind, bs):
+    """quantize_q4_0/q4_1/q5_0/q5_1 -- ggml-quants.c:2129-2294: NULL imatrix -> _ref, else _impl"""
+    def f(x, imx=None):
+        X = _blocks(x, 32)
+        if imx is None:
+            return ref(X).reshape(-1)
+        W = _row_weights(x, imx, 32)
+        out = _out(len(X), bs)
+        if kind == "qx":                       # make_qx_quants(32, nmax, x, L, 1, weight)
+            d, L = make_qx_quants(X, impl_nmax, W)
+            _put16(out, 0, fp16_bits(d))
+            if bs == 18:
+                out[:, 2:] = _pack_nibbles(L[:, :16], L[:, 16:])
+            else:
+                _q5_bits(out, 2, L)
+        else:                                  # make_qkx3_quants(32, nmax, ..., -0.9f, 0.05f, 36)
+            d, mn, L = make_qkx3_quants(X, W, impl_nmax, -0.9, 0.05, 36)
+            _put16(out, 0, fp16_bits(d))
+            _put16(out, 2, fp16_bits(-mn))
+            if bs == 20:
+                out[:, 4:] = _pack_nibbles(L[:, :16], L[:, 16:])
+            else:
+                _q5_bits(out, 4, L)
+        return out.reshape(-1)
+    return f
+
+
+q4_0 = _legacy(q4_0_ref, 8, "qx", 18)
+q4_1 = _legacy(q4_1_ref, 15, "qkx3", 20)
+q5_0 = _legacy(q5_0_ref, 16, "qx", 22)
+q5_1 = _legacy(q5_1_ref, 31, "qkx3", 24)
+
+
+# ------------------------------------------------------------------ K-quants (256 super-blocks)
+
+def _sb(x, imx):
+    x = np.ascontiguousarray(x, F)
+    nrows, npr = x.shape
+    X = x.reshape(-1, 256)
+    QW = None
+    if imx is not None:
+        QW = np.broadcast_to(np.asarray(imx, F).reshape(1, npr // 256, 256), (nrows, npr // 256, 256)).reshape(-1, 256)
+    return X, QW
+
+
+def _scale_min_k4(j, q):
+    """get_scale_min_k4 -- ggml-quants.c:880-887"""
+    if j < 4:
+        return q[:, j] & 63, q[:, j + 4] & 63
+    return (q[:, j + 4] & 0xF) | ((q[:, j - 4] >> 6) << 4), (q[:, j + 4] >> 4) | ((q[:, j] >> 6) << 4)
+
+
+def _pack_k4(Ls, Lm):
+    """6-bit scale/min bytes of Q4_K/Q5_K -- ggml-quants.c:1590-1601"""
+    sc = np.zeros((len(Ls), 12), np.int64)
+    for j in range(8):
+        ls, lm = u8(Ls[:, j]), u8(Lm[:, j])
+        if j < 4:
+            sc[:, j] = ls
+            sc[:, j + 4] = lm
+        else:
+            sc[:, j + 4] = u8((ls & 0xF) | ((lm & 0xF) << 4))
+            sc[:, j - 4] = u8(sc[:, j - 4] | ((ls >> 4) << 6))
+            sc[:, j] = u8(sc[:, j] | ((lm >> 4) << 6))
+    return sc
+
+
+def q4_5_K(x, imx, nmax):
+    """quantize_q4_K / quantize_q5_K: _impl (ggml-quants.c:1554-1625, :1759-1850) with an imatrix,
+    _ref (:1458-1528, :1645-1731) without"""
+    X, QW = _sb(x, imx)
+    nsb = len(X)
+    Xs = X.reshape(nsb * 8, 32)
+    with _errs():
+        if QW is not None:
+            sigma2 = (F(2) * seqsum(X * X) / F(256)).astype(F)
+            W = (QW * np.sqrt(np.repeat(sigma2, 256).reshape(nsb, 256) + X * X)).astype(F).reshape(nsb * 8, 32)
+            sw = seqsum(W).reshape(nsb, 8)
+            scales, mins, L = make_qkx3_quants(Xs, W, nmax, -0.9, 0.05, 36)
+            scales, mins = scales.reshape(nsb, 8), mins.reshape(nsb, 8)
+            d_block, Ls = make_qp_quants(scales, 63, sw)
+            m_block, Lm = make_qp_quants(mins, 63, sw)
+            if nmax == 31:
+                Ls, Lm = np.minimum(63, u8(Ls)), np.minimum(63, u8(Lm))
+            sc = _pack_k4(Ls, Lm)
+            dh, mh = fp16_bits(d_block), fp16_bits(m_block)
+        else:
+            av = np.sqrt(seqsum(Xs * Xs) / F(32)).astype(F)
+            W = (av[:, None] + np.abs(Xs)).astype(F)
+            if nmax == 15:
+                scales, mins, L = make_qkx2_quants(Xs, W, 15, -1.0, 0.1, 20, False)
+            else:
+                scales, mins, L = make_qkx2_quants(Xs, W, 31, -0.5, 0.1, 15, False)
+            scales, mins = scales.reshape(nsb, 8), mins.reshape(nsb, 8)
+            max_scale = np.zeros(nsb, F)
+            max_min = np.zeros(nsb, F)
+            for j in range(8):
+                max_scale = np.where(scales[:, j] > max_scale, scales[:, j], max_scale)
+                max_min = np.where(mins[:, j] > max_min, mins[:, j], max_min)
+            inv_s = np.where(max_scale > 0, F(63) / max_scale, F(0)).astype(F)
+            inv_m = np.where(max_min > 0, F(63) / max_min, F(0)).astype(F)
+            Ls = np.minimum(63, u8(nearest_int(inv_s[:, None] * scales)))
+            Lm = np.minimum(63, u8(nearest_int(inv_m[:, None] * mins)))
+            sc = _pack_k4(Ls, Lm)
+            dh, mh = fp16_bits(max_scale / F(63)), fp16_bits(max_min / F(63))
+        L = L.reshape(nsb, 256)
+        dmf, mmf = fp16_to_f32(dh), fp16_to_f32(mh)
+        for j in range(8):
+            s, m = _scale_min_k4(j, sc)
+            d = (dmf * s.astype(F)).astype(F)
+            dm = (mmf * m.astype(F)).astype(F)
+            l = np.clip(nearest_int((X[:, 32 * j:32 * j + 32] + dm[:, None]) / d[:, None]), 0, nmax)
+            L[:, 32 * j:32 * j + 32] = np.where((d != 0)[:, None], l, L[:, 32 * j:32 * j + 32])
+    bs = 144 if nmax == 15 else 176
+    out = _out(nsb, bs)
+    _put16(out, 0, dh)
+    _put16(out, 2, mh)
+    out[:, 4:16] = sc.astype(np.uint8)
+    if nmax == 15:
+        for j in range(4):
+            out[:, 16 + 32 * j:48 + 32 * j] = _pack_nibbles(L[:, 64 * j:64 * j + 32], L[:, 64 * j + 32:64 * j + 64])
+    else:
+        qh = np.zeros((nsb, 32), np.int64)
+        for n in range(4):
+            lo, hi = L[:, 64 * n:64 * n + 32], L[:, 64 * n + 32:64 * n + 64]
+            qh |= ((lo > 15).astype(np.int64) << (2 * n)) | ((hi > 15).astype(np.int64) << (2 * n + 1))
+            out[:, 48 + 32 * n:80 + 32 * n] = _pack_nibbles(np.where(lo > 15, lo - 16, lo), np.where(hi > 15, hi - 16, hi))
+        out[:, 16:48] = qh.astype(np.uint8)
+    return out.reshape(-1)
+
+
+def _pack2(L):
+    """2-bit packing of 256 levels into 64 bytes -- ggml-quants.c:1202-1206"""
+    q = np.zeros((len(L), 64), np.int64)
+    for j in range(0, 256, 128):
+        q[:, j // 4:j // 4 + 32] = (L[:, j:j + 32] | (L[:, j + 32:j + 64] << 2) | (L[:, j + 64:j + 96] << 4)
+                                    | (L[:, j + 96:j + 128] << 6)) & 0xFF
+    return q.astype(np.uint8)
+
+
+def q2_K(x, imx=None):
+    """quantize_q2_K: _impl (ggml-quants.c:1150-1210) / _ref (:891-960)"""
+    X, QW = _sb(x, imx)
+    nsb = len(X)
+    Xs = X.reshape(nsb * 16, 16)
+    with _errs():
+        if QW is not None:
+            sigma2 = (seqsum(X * X) / F(256)).astype(F)
+            W = (QW * np.sqrt(np.repeat(sigma2, 256).reshape(nsb, 256) + X * X)).astype(F).reshape(nsb * 16, 16)
+            sw = seqsum(W).reshape(nsb, 16)
+            scales, mins, L = make_qkx3_quants(Xs, W, 3, -0.9, 0.05, 36)
+            dm, Ls = make_qp_quants(scales.reshape(nsb, 16), 15, sw)
+            mm, Lm = make_qp_quants(mins.reshape(nsb, 16), 15, sw)
+            dh, mh = fp16_bits(dm), fp16_bits(mm)
+            sc = u8(u8(Ls) | (u8(Lm) << 4))
+        else:
+            W = np.abs(Xs)
+            scales, mins, L = make_qkx2_quants(Xs, W, 3, -0.5, 0.1, 15, True)
+            scales, mins = scales.reshape(nsb, 16), mins.reshape(nsb, 16)
+            max_scale = np.zeros(nsb, F)
+            max_min = np.zeros(nsb, F)
+            for j in range(16):
+                max_scale = np.where(scales[:, j] > max_scale, scales[:, j], max_scale)
+                max_min = np.where(mins[:, j] > max_min, mins[:, j], max_min)
+            isc = np.where(max_scale > 0, F(15) / max_scale, F(0)).astype(F)
+            sc = np.where((max_scale > 0)[:, None], u8(nearest_int(isc[:, None] * scales)), 0)
+            dh = np.where(max_scale > 0, fp16_bits(max_scale / F(15)), fp16_bits(F(0)))
+            imn = np.where(max_min > 0, F(15) / max_min, F(0)).astype(F)
+            sc = np.where((max_min > 0)[:, None], u8(sc | (nearest_int(imn[:, None] * mins) << 4)), sc)
+            mh = np.where(max_min > 0, fp16_bits(max_min / F(15)), fp16_bits(F(0)))
+        L = L.reshape(nsb, 256)
+        dmf, mmf = fp16_to_f32(dh), fp16_to_f32(mh)
+        for j in range(16):
+            d = (dmf * (sc[:, j] & 0xF).astype(F)).astype(F)
+            m = (mmf * (sc[:, j] >> 4).astype(F)).astype(F)
+            l = np.clip(nearest_int((X[:, 16 * j:16 * j + 16] + m[:, None]) / d[:, None]), 0, 3)
+            L[:, 16 * j:16 * j + 16] = np.where((d != 0)[:, None], l, L[:, 16 * j:16 * j + 16])
+    out = _out(nsb, 84)
+    out[:, :16] = sc.astype(np.uint8)
+    out[:, 16:80] = _pack2(L)
+    _put16(out, 80, dh)
+    _put16(out, 82, mh)
+    return out.reshape(-1)
+
+
+def q3_K(x, imx=None):
+    """quantize_q3_K: _impl (ggml-quants.c:1356-1438) / _ref (:1230-1305)"""
+    X, QW = _sb(x, imx)
+    nsb = len(X)
+    Xs = X.reshape(nsb * 16, 16)
+    sc = np.zeros((nsb, 12), np.int64)
+
+    def put_scale(j, l):
+        if j < 8:
+            sc[:, j] = l & 0xF
+        else:
+            sc[:, j - 8] = u8(sc[:, j - 8] | ((l & 0xF) << 4))
+        sc[:, j % 4 + 8] = u8(sc[:, j % 4 + 8] | ((l >> 4) << (2 * (j // 4))))
+
+    with _errs():
+        if QW is not None:
+            sigma2 = (F(2) * seqsum(X * X) / F(256)).astype(F)
+            W = (QW * np.sqrt(np.repeat(sigma2, 256).reshape(nsb, 256) + X * X)).astype(F).reshape(nsb * 16, 16)
+            sw = seqsum(W).reshape(nsb, 16)
+            scales, L = make_qx_quants(Xs, 4, W)
+            d_block, Ls = make_qx_quants(scales.reshape(nsb, 16), 32, sw)
+            for j in range(16):
+                put_scale(j, Ls[:, j])
+            dh = fp16_bits(d_block)
+        else:
+            scales, L = make_q3_quants(Xs, 4)
+            scales = scales.reshape(nsb, 16)
+            amax = np.zeros(nsb, F)
+            max_scale = np.zeros(nsb, F)
+            for j in range(16):
+                a = np.abs(scales[:, j])
+                up = a > amax
+                amax = np.where(up, a, amax)
+                max_scale = np.where(up, scales[:, j], max_scale)
+            nz = max_scale != 0
+            isc = (F(-32) / max_scale).astype(F)
+            for j in range(16):
+                l = np.clip(i8(nearest_int(isc * scales[:, j])), -32, 31) + 32
+                l = np.where(nz, l, 0)
+                put_scale(j, l)
+            sc[~nz] = 0
+            dh = np.where(nz, fp16_bits(F(1) / isc), fp16_bits(F(0)))
+        L = L.reshape(nsb, 256)
+        df = fp16_to_f32(dh)
+        for j in range(16):
+            s = (sc[:, j] & 0xF) if j < 8 else (sc[:, j - 8] >> 4)
+            s = i8((s | (((sc[:, 8 + j % 4] >> (2 * (j // 4))) & 3) << 4)) - 32)
+            d = (df * s.astype(F)).astype(F)
+            l = np.clip(nearest_int(X[:, 16 * j:16 * j + 16] / d[:, None]), -4, 3) + 4
+            L[:, 16 * j:16 * j + 16] = np.where((d != 0)[:, None], l, L[:, 16 * j:16 * j + 16])
+    out = _out(nsb, 110)
+    hm = np.zeros((nsb, 32), np.int64)
+    for k in range(8):
+        hm |= (L[:, 32 * k:32 * k + 32] > 3).astype(np.int64) << k
+    out[:, :32] = hm.astype(np.uint8)
+    out[:, 32:96] = _pack2(L & 3)
+    out[:, 96:108] = sc.astype(np.uint8)
+    _put16(out, 108, dh)
+    return out.reshape(-1)
+
+
+def q6_K(x, imx=None):
+    """quantize_q6_K: _impl (ggml-quants.c:1971-2053, weights = raw imatrix) / _ref (:1870-1938, x*x)"""
+    X, QW = _sb(x, imx)
+    nsb = len(X)
+    Xs = X.reshape(nsb * 16, 16)
+    with _errs():
+        scales, L = make_qx_quants(Xs, 32, None if QW is None else QW.reshape(nsb * 16, 16))
+        scales = scales.reshape(nsb, 16)
+        L = L.reshape(nsb, 256)
+        amax = np.zeros(nsb, F)
+        max_scale = np.zeros(nsb, F)
+        for j in range(16):
+            a = np.abs(scales[:, j])
+            up = a > amax
+            amax = np.where(up, a, amax)
+            max_scale = np.where(up, scales[:, j], max_scale)
+        zero = amax < GROUP_MAX_EPS
+        isc = (F(-128) / max_scale).astype(F)
+        dh = fp16_bits(F(1) / isc)
+        sc = i8(np.minimum(127, nearest_int(isc[:, None] * scales)))
+        df = fp16_to_f32(dh)
+        for j in range(16):
+            d = (df * sc[:, j].astype(F)).astype(F)
+            l = np.clip(nearest_int(X[:, 16 * j:16 * j + 16] / d[:, None]), -32, 31) + 32
+            L[:, 16 * j:16 * j + 16] = np.where((d != 0)[:, None], l, L[:, 16 * j:16 * j + 16])
+    out = _out(nsb, 210)
+    for j in range(0, 256, 128):
+        q1, q2 = L[:, j:j + 32] & 0xF, L[:, j + 32:j + 64] & 0xF
+        q3, q4 = L[:, j + 64:j + 96] & 0xF, L[:, j + 96:j + 128] & 0xF
+        out[:, j // 2:j // 2 + 32] = u8(q1 | (q3 << 4))
+        out[:, j // 2 + 32:j // 2 + 64] = u8(q2 | (q4 << 4))
+        out[:, 128 + j // 4:128 + j // 4 + 32] = u8((L[:, j:j + 32] >> 4) | ((L[:, j + 32:j + 64] >> 4) << 2)
+                                                    | ((L[:, j + 64:j + 96] >> 4) << 4) | ((L[:, j + 96:j + 128] >> 4) << 6))
+    out[:, 192:208] = u8(sc).astype(np.uint8)
+    _put16(out, 208, dh)
+    out[zero] = 0
+    return out.reshape(-1)
+
+
+FUNCS = {
+    8: q8_0, 2: q4_0, 3: q4_1, 6: q5_0, 7: q5_1, 42: q2_0,
+    10: q2_K, 11: q3_K, 12: lambda x, imx=None: q4_5_K(x, imx, 15), 13: lambda x, imx=None: q4_5_K(x, imx, 31),
+    14: q6_K,
+}
+
+
+def quantize(ttype, x, imatrix=None, variant=0):
+    """float32 (nrows, n_per_row) -> quantized bytes (uint8), as quantize_<type>(x, dst, nrows,
+    n_per_row, imatrix)"""
+    if ttype not in FUNCS or variant != 0:
+        raise NotImplementedError(f"oracle: type {ttype} variant {variant}")
+    x = np.ascontiguousarray(x, F)
+    assert x.ndim == 2 and x.shape[1] % QK[ttype] == 0
+    return FUNCS[ttype](x, imatrix)

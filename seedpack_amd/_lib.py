@@ -1,0 +1,72 @@
+"""ctypes binding of libseedpack_amd.so (the C ABI declared in include/seedpack_amd.h).
+
+The library is the product path: there is no CPU fallback. If the shared object is missing or a
+HIP call fails, the error is raised, never papered over.
+"""
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libseedpack_amd.so")
+
+_lib = None
+_lock = threading.Lock()
+
+c_void_p, c_int, c_int64, c_size_t, c_float = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+
+# name -> (restype, argtypes); every symbol of include/seedpack_amd.h
+SIGNATURES = {
+    "spa_last_error": (ctypes.c_char_p, []),
+    "spa_device_count": (c_int, [ctypes.POINTER(c_int)]),
+    "spa_set_device": (c_int, [c_int]),
+    "spa_malloc": (c_int, [ctypes.POINTER(c_void_p), c_size_t]),
+    "spa_free": (c_int, [c_void_p]),
+    "spa_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "spa_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "spa_memcpy_d2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "spa_memset": (c_int, [c_void_p, c_int, c_size_t, c_void_p]),
+    "spa_stream_create": (c_int, [ctypes.POINTER(c_void_p)]),
+    "spa_stream_destroy": (c_int, [c_void_p]),
+    "spa_stream_synchronize": (c_int, [c_void_p]),
+    "spa_device_synchronize": (c_int, []),
+    "spa_event_create": (c_int, [ctypes.POINTER(c_void_p)]),
+    "spa_event_destroy": (c_int, [c_void_p]),
+    "spa_event_record": (c_int, [c_void_p, c_void_p]),
+    "spa_event_elapsed_ms": (c_int, [ctypes.POINTER(c_float), c_void_p, c_void_p]),
+    "spa_mem_info": (c_int, [ctypes.POINTER(c_size_t), ctypes.POINTER(c_size_t)]),
+    "spa_row_size": (c_size_t, [c_int, c_int64]),
+    "spa_type_variants": (c_int, [c_int]),
+    "spa_quantize": (c_int, [c_int, c_int, c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+}
+
+
+class SpaError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+def lib():
+    """the loaded library (raises if it has not been built)"""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m seedpack_amd.build` "
+                                       "(the HIP path has no CPU fallback)")
+                L = ctypes.CDLL(LIB_PATH)
+                for name, (res, args) in SIGNATURES.items():
+                    f = getattr(L, name)
+                    f.restype = res
+                    f.argtypes = args
+                _lib = L
+    return _lib
+
+
+def check(code):
+    """raise SpaError for a negative status"""
+    if code < 0:
+        raise SpaError(code, lib().spa_last_error().decode(errors="replace"))
+    return code

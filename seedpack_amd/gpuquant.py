@@ -1,0 +1,97 @@
+"""Host side of the regrow quantizers: the reference's GPUQuant interface over the HIP C ABI.
+
+Mirrors seedpack/gpuquant.py:284-456 (GPUQuant.quantize_tensors / quantize_batch): same argument
+meaning and result layout. Differences that follow from the MI355X design:
+  * weights are widened BF16/F16 -> f32 inside the quantizer's load (no f32 staging buffer, so
+    `max_weights` only bounds how many weights one call hands to the GPU at a time);
+  * every tensor is one launch of one kernel over its contiguous run of blocks (the reference runs
+    one thread per row, gpuquant.py:432-456).
+"""
+import numpy as np
+
+from . import device as dev
+from ._lib import check, lib
+from .requant import NEED_IMATRIX, QFUN, VARIANTS
+
+SRC_BF16, SRC_F16, SRC_F32 = 0, 1, 2
+
+
+def _src_kind(a):
+    dt = np.dtype(a.dtype)
+    if dt == np.uint16:
+        return SRC_BF16
+    if dt == np.float16:
+        return SRC_F16
+    if dt == np.float32:
+        return SRC_F32
+    raise TypeError(f"weights must be bf16 bits (uint16), float16 or float32, not {dt}")
+
+
+def quantize_into(ttype, src, n_per_row, dst, imatrix=None, variant=0, stream=None):
+    """one tensor: src DeviceArray (nrows*n_per_row weights) -> dst DeviceArray (bytes); enqueue only"""
+    if ttype not in QFUN:
+        raise ValueError(f"unknown ggml type {ttype}")
+    nrows = src.size // n_per_row
+    assert nrows * n_per_row == src.size, "tensor size is not a whole number of rows"
+    need = nrows * (n_per_row // QFUN[ttype][1]) * QFUN[ttype][2]
+    assert dst.nbytes >= need, (dst.nbytes, need)
+    check(lib().spa_quantize(ttype, variant, src.ptr, _src_kind(src), nrows, n_per_row,
+                             None if imatrix is None else imatrix.ptr, dst.ptr, stream))
+    return dst
+
+
+class GPUQuant:
+    """llama.cpp quantizers on the MI355X, byte-identical to the CPU library (gpuquant.py:284)."""
+
+    def __init__(self, fmad=False, stream=None):
+        if fmad:
+            raise ValueError("fmad=True (FMA-contracted quantizers) is not built: every kernel is compiled "
+                             "with -ffp-contract=off")
+        lib()
+        self.stream = stream
+
+    @staticmethod
+    def _dev(a):
+        return a if isinstance(a, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(a))
+
+    def _imx(self, imx, npr):
+        if imx is None:
+            return None
+        if isinstance(imx, dev.DeviceArray):
+            return imx
+        imx = np.ascontiguousarray(imx, np.float32).reshape(-1)
+        assert imx.size == npr, (imx.size, npr)
+        return dev.DeviceArray.from_host(imx)
+
+    def quantize_tensors(self, ttype, srcs, imatrices, variant=0, max_weights=1 << 28, on_result=None, device=False):
+        """srcs: list of (weights as bf16 bits (uint16) / f16 / f32, device or host array, n_per_row).
+        Returns the quantized bytes of every tensor (host numpy arrays, DeviceArrays with `device`),
+        or with on_result calls on_result(index, bytes) per tensor and returns None."""
+        if ttype in NEED_IMATRIX and any(m is None for m in imatrices):
+            raise ValueError(f"type {ttype} requires an imatrix")
+        if variant >= VARIANTS.get(ttype, 1):
+            raise ValueError(f"type {ttype} has no variant {variant}")
+        _, qk, bs = QFUN[ttype]
+        out = []
+        for i, ((a, npr), imx) in enumerate(zip(srcs, imatrices)):
+            x = self._dev(a)
+            w = self._imx(imx, npr)
+            nrow = x.size // npr
+            rb = npr // qk * bs
+            y = dev.DeviceArray(nrow * rb, np.uint8)
+            step = max(1, max_weights // npr)
+            for r0 in range(0, nrow, step):
+                r1 = min(nrow, r0 + step)
+                xs = x.view(r0 * npr * x.dtype.itemsize, (r1 - r0) * npr, x.dtype)
+                ys = y.view(r0 * rb, (r1 - r0) * rb, np.uint8)
+                quantize_into(ttype, xs, npr, ys, w, variant, self.stream)
+            res = y if device else y.to_host(stream=self.stream)
+            if on_result:
+                on_result(i, res)
+            else:
+                out.append(res)
+        return None if on_result else out
+
+    def quantize_batch(self, ttype, xs, imatrices, variant=0):
+        """xs: list of float32 arrays (nrows, n_per_row); returns device uint8 arrays (gpuquant.py:424-430)"""
+        return self.quantize_tensors(ttype, [(x, x.shape[-1]) for x in xs], imatrices, variant, device=True)

@@ -1,0 +1,103 @@
+"""Writes the golden quantizer vectors from the reference's own C build (oracle/_ref, made by
+`make -C oracle` from /root/reference/seedpack/ggml). Run in the build container:
+
+    python tests/golden/make_golden.py            # small vectors (quant_small.npz)
+    python tests/golden/make_golden.py --full     # + SHA-256 of full-size config tensors
+
+quant_small.npz holds seeded inputs (as bf16 bits) and the reference bytes for every type, with and
+without an imatrix. quant_sha256.json holds SHA-256 digests of the reference bytes of the benchmark
+tensors (seedpack_amd.synth), which the GPU tests compare against at full size.
+"""
+import argparse
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from oracle import ref  # noqa: E402
+from seedpack_amd import synth  # noqa: E402
+
+TYPES = sorted(ref.QFUN)
+NEED_IMX = {16, 17, 19, 29}
+
+
+def small_inputs():
+    g = np.random.Generator(np.random.PCG64(0x60D0))
+    ins = {}
+    ins["normal"] = synth.normal_bf16(g, (8, 512), 0.02, outlier_frac=0.01)
+    ins["student"] = synth.student_t_bf16(g, (8, 512))
+    x = synth.bf16_to_f32(synth.normal_bf16(g, (16, 512), 0.02)).reshape(16, 512).copy()
+    x[0] = 0                                   # all-zero row
+    x[1, :256] = 0                             # one zero super-block
+    x[2] = 0.01                                # constant row
+    x[3, ::2] = -0.5                           # ties in |x|
+    x[4, :32] = 1e-30                          # tiny block
+    x[5] = np.round(x[5] * 100) / 100          # coarse grid of values
+    x[6, :256] = np.tile([0.1, -0.1], 128)     # alternating signs
+    x[7] = np.abs(x[7])                        # all positive
+    x[8] = -np.abs(x[8])                       # all negative
+    x[9, 5] = 3.0                              # one large outlier
+    x[10, :16] = 1e-41                         # subnormal inputs
+    x[11] = (np.arange(512) % 7 - 3) * 0.01    # repeating levels
+    x[12] = 60000.0 * np.sign(x[12])           # near the fp16 limit
+    x[13] = 1e-8 * np.sign(x[13])              # tiny, signed
+    x[14, 100] = -2.0                          # negative outlier
+    ins["edge"] = synth.bf16_bits(x.astype(np.float32))
+    imx = g.lognormal(0.0, 1.0, 512).astype(np.float32)
+    return ins, imx
+
+
+def make_small(path):
+    ins, imx = small_inputs()
+    out = {"imatrix": imx}
+    for name, b in ins.items():
+        out[f"in_{name}"] = b
+        x = synth.bf16_to_f32(b).reshape(b.shape)
+        for t in TYPES:
+            for variant in range(2 if t == 29 else 1):
+                for use in (False, True):
+                    if not use and t in NEED_IMX:
+                        continue
+                    with np.errstate(all="ignore"):
+                        y = ref.quantize(t, x, imx if use else None, variant=variant)
+                    out[f"q_{name}_{t}_{variant}_{'imx' if use else 'none'}"] = y
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({len(out)} arrays, {os.path.getsize(path)} bytes)")
+
+
+# full-size tensors whose reference bytes are pinned by digest: (config, tensor index, types)
+FULL = [(1, 0, [8, 2]), (2, 1, [10, 11, 12, 13, 14]), (2, 0, [10, 11, 12, 13, 14])]
+
+
+def make_full(path):
+    man = {}
+    if os.path.exists(path):
+        man = json.load(open(path))
+    for cfg, ti, types in FULL:
+        w, imx = synth.tensor(cfg, ti)
+        x = synth.bf16_to_f32(w).reshape(w.shape)
+        for t in types:
+            key = f"cfg{cfg}_t{ti}_{t}_0"
+            if key in man:
+                continue
+            y = ref.quantize(t, x, imx)
+            man[key] = {"sha256": hashlib.sha256(y.tobytes()).hexdigest(), "nbytes": int(y.size),
+                        "shape": list(w.shape), "imatrix": imx is not None}
+            print(key, man[key]["sha256"][:16], flush=True)
+            json.dump(man, open(path, "w"), indent=1, sort_keys=True)
+    return man
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--full", action="store_true")
+    a = ap.parse_args()
+    make_small(os.path.join(HERE, "quant_small.npz"))
+    if a.full:
+        make_full(os.path.join(HERE, "quant_sha256.json"))

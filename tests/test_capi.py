@@ -1,0 +1,49 @@
+"""The C-ABI library loads and exports every symbol include/seedpack_amd.h declares (no GPU calls)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from seedpack_amd import _lib
+from seedpack_amd.requant import QFUN
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            src = open(os.path.join(ROOT, "include", fn)).read()
+            names |= set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(spa_\w+)\s*\(", src, re.M))
+    return names
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in declared_symbols():
+        assert hasattr(L, name), name
+        assert ctypes.cast(getattr(L, name), ctypes.c_void_p).value
+
+
+@pytest.mark.parametrize("t", sorted(QFUN))
+def test_row_size_matches_type_table(t):
+    _, qk, bs = QFUN[t]
+    L = _lib.lib()
+    assert L.spa_row_size(t, 4096 // qk * qk * 3) == (4096 // qk * 3) * bs
+    assert L.spa_row_size(t, qk + 1) == 0
+
+
+def test_bad_arguments_fail_before_any_device_call():
+    L = _lib.lib()
+    assert L.spa_quantize(99, 0, None, 0, 1, 256, None, None, None) == -2
+    assert b"unknown ggml type" in L.spa_last_error()
+    assert L.spa_quantize(12, 0, None, 0, 1, 100, None, None, None) == -4
+    assert L.spa_quantize(12, 1, None, 0, 1, 256, None, None, None) == -2       # no variant 1 for Q4_K
+    assert L.spa_quantize(16, 0, None, 0, 1, 256, None, None, None) == -4       # null src first
+    assert L.spa_type_variants(29) == 2 and L.spa_type_variants(12) == 1 and L.spa_type_variants(99) == 0

@@ -1,0 +1,117 @@
+"""HIP quantizers vs the golden vectors, the oracle and the reference digests (runs on the MI355X)."""
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import quants
+from seedpack_amd import device as dev
+from seedpack_amd import synth
+from seedpack_amd.gpuquant import GPUQuant, quantize_into
+from seedpack_amd.requant import QFUN, row_size
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HIP_TYPES = [8, 2, 3, 6, 7, 42, 10, 11, 12, 13, 14]
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+@pytest.fixture(scope="module")
+def gq():
+    return GPUQuant()
+
+
+def hip(gq, t, bits, imx, variant=0):
+    return gq.quantize_tensors(t, [(bits.reshape(-1), bits.shape[-1])], [imx], variant)[0]
+
+
+@pytest.mark.parametrize("t", HIP_TYPES)
+def test_hip_matches_golden_small(golden_small, gq, t):
+    for name in ("normal", "student", "edge"):
+        b = golden_small[f"in_{name}"]
+        for use in ("none", "imx"):
+            key = f"q_{name}_{t}_0_{use}"
+            if key not in golden_small:
+                continue
+            say("case", key)
+            got = hip(gq, t, b, golden_small["imatrix"] if use == "imx" else None)
+            want = golden_small[key]
+            bad = np.flatnonzero(got != want)
+            assert bad.size == 0, f"{key}: {bad.size} bytes differ, first at {bad[:8]}"
+
+
+@pytest.mark.parametrize("t", HIP_TYPES)
+def test_hip_matches_oracle_seeded(gq, t):
+    g = np.random.Generator(np.random.PCG64(0xA11CE + t))
+    b = synth.normal_bf16(g, (96, 2048), 0.02, outlier_frac=0.002)
+    imx = g.lognormal(0, 1, 2048).astype(np.float32)
+    x = synth.bf16_to_f32(b).reshape(b.shape)
+    for w in (None, imx):
+        say("case seeded", t, "imx" if w is not None else "none")
+        got = hip(gq, t, b, w)
+        want = quants.quantize(t, x, w)
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, f"{bad.size} bytes differ, first at {bad[:8]}"
+
+
+def _manifest():
+    p = os.path.join(ROOT, "tests", "golden", "quant_sha256.json")
+    return json.load(open(p)) if os.path.exists(p) else {}
+
+
+@pytest.mark.parametrize("key", sorted(_manifest()))
+def test_hip_full_size_matches_reference_digest(gq, key):
+    ent = _manifest()[key]
+    cfg, ti, t, variant = key.split("_")
+    cfg, ti, t, variant = int(cfg[3:]), int(ti[1:]), int(t), int(variant)
+    if t not in HIP_TYPES:
+        pytest.skip(f"type {t} not built")
+    say("case full", key)
+    w, imx = synth.tensor(cfg, ti)
+    got = hip(gq, t, w, imx)
+    assert got.size == ent["nbytes"]
+    assert hashlib.sha256(got.tobytes()).hexdigest() == ent["sha256"]
+
+
+@pytest.mark.parametrize("t", [8, 2, 12, 14])
+def test_source_kinds_agree(gq, t):
+    """bf16 bits, f32 and f16 copies of the same values give the same bytes"""
+    g = np.random.Generator(np.random.PCG64(77))
+    b = synth.normal_bf16(g, (16, 1024), 0.02)
+    x = synth.bf16_to_f32(b).reshape(b.shape)
+    imx = g.lognormal(0, 1, 1024).astype(np.float32)
+    ref_bytes = hip(gq, t, b, imx)
+    assert hip(gq, t, x, imx).tobytes() == ref_bytes.tobytes()
+    xh = x.astype(np.float16)
+    if np.array_equal(xh.astype(np.float32), x):
+        assert hip(gq, t, xh, imx).tobytes() == ref_bytes.tobytes()
+
+
+@pytest.mark.parametrize("t", [8, 2, 10, 12])
+def test_row_split_invariance(gq, t):
+    """rows are quantized independently: any split of the rows gives the same bytes"""
+    g = np.random.Generator(np.random.PCG64(5))
+    b = synth.normal_bf16(g, (37, 512), 0.02)
+    imx = g.lognormal(0, 1, 512).astype(np.float32)
+    whole = hip(gq, t, b, imx)
+    rb = row_size(t, 512)
+    for k in (1, 13, 36):
+        a = hip(gq, t, b[:k], imx)
+        c = hip(gq, t, b[k:], imx)
+        assert np.concatenate([a, c]).tobytes() == whole.tobytes()
+        assert a.size == k * rb
+
+
+def test_zero_rows_is_a_no_op():
+    src = dev.DeviceArray(512, np.uint16).zero()
+    dst = dev.DeviceArray(16, np.uint8)
+    quantize_into(12, dev.DeviceArray(0, np.uint16), 256, dst)
+    dev.synchronize()
+    del src
