@@ -65,6 +65,15 @@ def cpu_baseline(tensors, target_s=12.0):
             "cpu_model": _cpu_model()}
 
 
+def _profiled_traffic(kernel):
+    """HBM bytes per launch of a kernel on the embedding, from the rocprofv3 FETCH_SIZE/WRITE_SIZE
+    passes summarised in profiles/ (scaled by the copy-kernel factors recorded there)"""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(p):
+        return None
+    return json.load(open(p))["bytes_per_launch"].get(kernel)
+
+
 def _cpu_model():
     try:
         for ln in open("/proc/cpuinfo"):
@@ -75,13 +84,45 @@ def _cpu_model():
     return None
 
 
+def profile_pass():
+    """each kernel of the step once, after one warm-up launch, plus the copy yardstick"""
+    from seedpack_amd import device as dev
+    from seedpack_amd import synth
+    from seedpack_amd._lib import check, lib
+    from seedpack_amd.gpuquant import quantize_into
+    from seedpack_amd.requant import NAMES, row_size
+
+    w, imx = synth.tensor(2, 0)
+    src = dev.DeviceArray.from_host(w.reshape(-1))
+    dimx = dev.DeviceArray.from_host(imx)
+    for t in [8, 2] + KTYPES:
+        out = dev.DeviceArray(w.shape[0] * row_size(t, w.shape[1]), np.uint8)
+        m = None if t in (8, 2) else dimx
+        for _ in range(2):
+            quantize_into(t, src, w.shape[1], out, m)
+        dev.synchronize()
+        log(f"profile: {NAMES[t]} token_embd {w.shape[0]}x{w.shape[1]} x2 launches, "
+            f"algorithmic bytes/launch {alg_bytes(t, w.size, w.shape[1], m is not None)}")
+    nb = 512 << 20
+    a, b = dev.DeviceArray(nb, np.uint8), dev.DeviceArray(nb, np.uint8)
+    for _ in range(2):
+        check(lib().spa_copy(b.ptr, a.ptr, nb, None))
+    dev.synchronize()
+    log(f"profile: k_copy16 {nb} bytes x2 launches (reads {nb}, writes {nb})")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="one launch of each kernel (K-quants and Q8_0/Q4_0 on token_embd) plus a 512 MiB copy, "
+                         "for rocprofv3 counter runs; prints the launch list, no JSON line")
     a = ap.parse_args()
+    if a.profile_pass:
+        return profile_pass()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the path shards by rows "
               "with no exchange, so N GPUs is N independent copies of this run", file=sys.stderr)
@@ -143,9 +184,10 @@ def main():
     dom_ms = per[dom] / a.steps
     ab = alg_bytes(t, w.size, w.shape[1], True)
     achieved = ab / (dom_ms / 1e3) / 1e9
+    traffic = _profiled_traffic(NAMES[t].replace("_", "")) if n == "token_embd" else None
     roofline = {"bound": "hbm", "kernel": f"k_kquant<{NAMES[t]}> on {n} {w.shape[0]}x{w.shape[1]}",
                 "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 5), "traffic": None,
+                "frac": round(achieved / PEAK_HBM_GBS, 5), "traffic": traffic,
                 "algorithmic_bytes": ab, "avg_launch_ms": round(dom_ms, 4),
                 "note": "search-bound K-quant (VALU); HBM fraction reported as the contract asks"}
 

@@ -52,6 +52,9 @@ int spa_event_destroy(void* event);
 int spa_event_record(void* event, void* stream);
 int spa_event_elapsed_ms(float* ms, void* start, void* stop);
 int spa_mem_info(size_t* free_bytes, size_t* total_bytes);
+/* Device-to-device copy by a plain streaming kernel (16-byte multiples); the HBM yardstick the
+ * traffic counters of the other kernels are scaled against. No reference counterpart. */
+int spa_copy(void* dst, const void* src, size_t nbytes, void* stream);
 
 /* ---- quantizers ---- */
 

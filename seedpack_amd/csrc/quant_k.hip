@@ -49,15 +49,6 @@ __device__ __forceinline__ void group_gather(float v, float (&all)[G]) {
     for (int k = 0; k < G; ++k) all[k] = __shfl(v, k, G);
 }
 
-// a[idx] for a lane-varying idx, as a chain of selects (keeps `a` in registers).
-template <int N, typename T>
-__device__ __forceinline__ T pick(const T (&a)[N], int idx) {
-    T v = a[0];
-#pragma unroll
-    for (int k = 1; k < N; ++k) v = idx == k ? a[k] : v;
-    return v;
-}
-
 template <int SUB>
 __device__ __forceinline__ void park_levels(uint8_t* lt, const int (&L)[SUB]) {
     uint32_t* p = reinterpret_cast<uint32_t*>(lt);
@@ -67,14 +58,16 @@ __device__ __forceinline__ void park_levels(uint8_t* lt, const int (&L)[SUB]) {
                    ((uint32_t)(L[i + 3] & 0xff) << 24);
 }
 
-// get_scale_min_k4 -- ggml-quants.c:880-887 (j varies per lane)
-__device__ __forceinline__ void scale_min_k4(int j, const uint32_t (&q)[16], uint32_t& d, uint32_t& m) {
+// get_scale_min_k4 -- ggml-quants.c:880-887 (j is a compile-time index after unrolling)
+__device__ __forceinline__ uint32_t scale_min_k4(int j, const uint32_t (&q)[16]) {
+    uint32_t d, m;
     if (j < 4) {
-        d = pick(q, j) & 63; m = pick(q, j + 4) & 63;
+        d = q[j] & 63; m = q[j + 4] & 63;
     } else {
-        d = (pick(q, j + 4) & 0xF) | ((pick(q, j - 4) >> 6) << 4);
-        m = (pick(q, j + 4) >> 4) | ((pick(q, j) >> 6) << 4);
+        d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4);
     }
+    return (d & 0xff) | ((m & 0xff) << 8);
 }
 
 // 6-bit scale/min packing of Q4_K/Q5_K (ggml-quants.c:1491-1501, :1590-1601).
@@ -102,12 +95,13 @@ struct Q45K {
     static constexpr int G = 8, SUB = 32;
     // quantize_row_q4_K_impl (ggml-quants.c:1554-1625) / quantize_row_q5_K_impl (:1759-1850), and the
     // NULL-imatrix rows quantize_row_q4_K_ref (:1458-1528) / quantize_row_q5_K_ref (:1645-1731).
-    __device__ __forceinline__ static KHeader quant(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB]) {
+    template <bool IMX>
+    __device__ __forceinline__ static KHeader search(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB]) {
         KHeader h;
         h.zero = false;
         float scale, min;
         float w[SUB];
-        if (qw) {
+        if constexpr (IMX) {
             const float sum_x2 = group_sumsq<G, SUB>(x, sub);
             const float sigma2 = 2 * sum_x2 / 256;
 #pragma unroll
@@ -164,19 +158,21 @@ struct Q45K {
             h.d = f32_to_f16(max_scale / 63.f);
             h.dmin = f32_to_f16(max_min / 63.f);
         }
-        // requantize this sub-block with the stored scales
-        uint32_t sc, m;
-        scale_min_k4(sub, h.sc, sc, m);
-        const float d = f16_to_f32(h.d) * (float)sc;
+        return h;
+    }
+    // decoded (scale, min) levels of sub-block j, as get_scale_min_k4 reads them back
+    __device__ __forceinline__ static uint32_t info(const KHeader& h, int j) { return scale_min_k4(j, h.sc); }
+    // requantize this sub-block with the stored scales (ggml-quants.c:1607-1616)
+    __device__ __forceinline__ static void requant(const float (&x)[SUB], const KHeader& h, uint32_t inf, int (&L)[SUB]) {
+        const float d = f16_to_f32(h.d) * (float)(inf & 0xff);
         if (d != 0.f) {
-            const float dm = f16_to_f32(h.dmin) * (float)m;
+            const float dm = f16_to_f32(h.dmin) * (float)(inf >> 8);
 #pragma unroll
             for (int ii = 0; ii < SUB; ++ii) {
                 const int l = nearest_int((x[ii] + dm) / d);
                 L[ii] = tmax(0, tmin(NMAX, l));
             }
         }
-        return h;
     }
     __device__ __forceinline__ static void pack(const KHeader& h, const uint8_t* L, TileOut o) {
         o.put16(0, h.d);
@@ -216,11 +212,12 @@ struct Q45K {
 struct Q2K {
     static constexpr int G = 16, SUB = 16, BS = 84;
     // quantize_row_q2_K_impl (ggml-quants.c:1150-1210) and quantize_row_q2_K_ref (:891-960).
-    __device__ __forceinline__ static KHeader quant(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB]) {
+    template <bool IMX>
+    __device__ __forceinline__ static KHeader search(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB]) {
         KHeader h;
         h.zero = false;
         float dmf, mmf;
-        if (qw) {
+        if constexpr (IMX) {
             const float sumx2 = group_sumsq<G, SUB>(x, sub);
             const float sigma2 = sumx2 / 256;
             float w[SUB];
@@ -280,17 +277,20 @@ struct Q2K {
             dmf = f16_to_f32(h.d);
             mmf = f16_to_f32(h.dmin);
         }
-        const uint32_t scj = pick(h.sc, sub);
-        const float d = dmf * (float)(scj & 0xF);
+        (void)dmf; (void)mmf;
+        return h;
+    }
+    __device__ __forceinline__ static uint32_t info(const KHeader& h, int j) { return h.sc[j]; }
+    __device__ __forceinline__ static void requant(const float (&x)[SUB], const KHeader& h, uint32_t scj, int (&L)[SUB]) {
+        const float d = f16_to_f32(h.d) * (float)(scj & 0xF);
         if (d != 0.f) {
-            const float m = mmf * (float)(scj >> 4);
+            const float m = f16_to_f32(h.dmin) * (float)(scj >> 4);
 #pragma unroll
             for (int ii = 0; ii < SUB; ++ii) {
                 const int l = nearest_int((x[ii] + m) / d);
                 L[ii] = tmax(0, tmin(3, l));
             }
         }
-        return h;
     }
     __device__ __forceinline__ static void pack(const KHeader& h, const uint8_t* L, TileOut o) {
 #pragma unroll
@@ -364,12 +364,13 @@ __device__ __forceinline__ float make_q3_quants16(const float (&x)[16], int (&L)
 struct Q3K {
     static constexpr int G = 16, SUB = 16, BS = 110;
     // quantize_row_q3_K_impl (ggml-quants.c:1356-1438) and quantize_row_q3_K_ref (:1230-1305).
-    __device__ __forceinline__ static KHeader quant(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB]) {
+    template <bool IMX>
+    __device__ __forceinline__ static KHeader search(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB]) {
         KHeader h;
         h.zero = false;
 #pragma unroll
         for (int j = 0; j < 16; ++j) h.sc[j] = 0;
-        if (qw) {
+        if constexpr (IMX) {
             const float sumx2 = group_sumsq<G, SUB>(x, sub);
             const float sigma2 = 2 * sumx2 / 256;
             float w[SUB];
@@ -419,10 +420,16 @@ struct Q3K {
                 h.d = f32_to_f16(0.f);
             }
         }
-        const int j = sub;
-        int sc = j < 8 ? (int)(pick(h.sc, j) & 0xF) : (int)(pick(h.sc, j - 8) >> 4);
-        sc = (int)(int8_t)((sc | (int)(((pick(h.sc, 8 + j % 4) >> (2 * (j / 4))) & 3) << 4)) - 32);
-        const float d = f16_to_f32(h.d) * (float)sc;
+        return h;
+    }
+    // the signed 6-bit scale of sub-block j as read back from the packed bytes (ggml-quants.c:1411-1413)
+    __device__ __forceinline__ static uint32_t info(const KHeader& h, int j) {
+        int sc = j < 8 ? (int)(h.sc[j] & 0xF) : (int)(h.sc[j - 8] >> 4);
+        sc = (int)(int8_t)((sc | (int)(((h.sc[8 + j % 4] >> (2 * (j / 4))) & 3) << 4)) - 32);
+        return (uint32_t)sc;
+    }
+    __device__ __forceinline__ static void requant(const float (&x)[SUB], const KHeader& h, uint32_t inf, int (&L)[SUB]) {
+        const float d = f16_to_f32(h.d) * (float)(int)inf;
         if (d != 0.f) {
 #pragma unroll
             for (int ii = 0; ii < SUB; ++ii) {
@@ -431,7 +438,6 @@ struct Q3K {
                 L[ii] = l + 4;
             }
         }
-        return h;
     }
     __device__ __forceinline__ static void pack(const KHeader& h, const uint8_t* L, TileOut o) {
         // hmask[32] at 0, qs[64] at 32, scales[12] at 96, d at 108 (ggml-quants.c:1410-1435). Levels are
@@ -465,11 +471,12 @@ struct Q6K {
     static constexpr int G = 16, SUB = 16, BS = 210;
     // quantize_row_q6_K_impl (ggml-quants.c:1971-2053) and quantize_row_q6_K_ref (:1870-1938): the
     // imatrix path weights by the raw imatrix, the NULL path by x*x.
-    __device__ __forceinline__ static KHeader quant(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB]) {
+    template <bool IMX>
+    __device__ __forceinline__ static KHeader search(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB]) {
         KHeader h;
         h.zero = false;
         float scale;
-        if (qw) {
+        if constexpr (IMX) {
             float w[SUB];
 #pragma unroll
             for (int l = 0; l < SUB; ++l) w[l] = qw[l];
@@ -495,7 +502,12 @@ struct Q6K {
         h.d = f32_to_f16(1 / iscale);
 #pragma unroll
         for (int ib = 0; ib < G; ++ib) h.sc[ib] = (uint32_t)tmin(127, nearest_int(iscale * scales[ib])) & 0xff;
-        const float d = f16_to_f32(h.d) * (float)(int)(int8_t)pick(h.sc, sub);
+        return h;
+    }
+    __device__ __forceinline__ static uint32_t info(const KHeader& h, int j) { return h.zero ? 0u : h.sc[j]; }
+    __device__ __forceinline__ static void requant(const float (&x)[SUB], const KHeader& h, uint32_t scj, int (&L)[SUB]) {
+        if (h.zero) return;
+        const float d = f16_to_f32(h.d) * (float)(int)(int8_t)scj;
         if (d != 0.f) {
 #pragma unroll
             for (int ii = 0; ii < SUB; ++ii) {
@@ -504,7 +516,6 @@ struct Q6K {
                 L[ii] = l + 32;
             }
         }
-        return h;
     }
     __device__ __forceinline__ static void pack(const KHeader& h, const uint8_t* L, TileOut o) {
         // ql[128] at 0, qh[64] at 128, scales[16] at 192, d at 208 (ggml-quants.c:1922-1935)
@@ -537,12 +548,13 @@ struct Q6K {
 struct Q4K : Q45K<15> { static constexpr int BS = 144; };
 struct Q5K : Q45K<31> { static constexpr int BS = 176; };
 
-template <class Op>
+template <class Op, bool IMX>
 __global__ __launch_bounds__(WG) void k_kquant(const void* __restrict__ src, int kind, uint8_t* __restrict__ dst,
                                                int64_t nsb, int64_t sb_per_row, const float* __restrict__ imx) {
     constexpr int G = Op::G, SUB = Op::SUB, SBW = WG / G;
     __shared__ __align__(16) uint8_t ltile[SBW * 256];
     __shared__ __align__(16) uint16_t otile[SBW * Op::BS / 2];
+    __shared__ uint32_t ginfo[SBW][G];
     const int lsb = threadIdx.x / G, sub = threadIdx.x % G;
     const int64_t sb0 = (int64_t)blockIdx.x * SBW;
     const int64_t sb = sb0 + lsb;
@@ -551,12 +563,19 @@ __global__ __launch_bounds__(WG) void k_kquant(const void* __restrict__ src, int
     float x[SUB];
     load_weights<SUB>(src, kind, sbc * 256 + sub * SUB, x);
     const float* qw = nullptr;
-    if (imx) {
+    if (IMX) {
         const int64_t row = sbc / sb_per_row;
         qw = imx + (sbc - row * sb_per_row) * 256 + sub * SUB;
     }
     int L[SUB];
-    const KHeader h = Op::quant(x, qw, sub, L);
+    const KHeader h = Op::template search<IMX>(x, qw, sub, L);
+    // every lane of the group holds the same header; lane 0 publishes the per-sub-block decode
+    if (sub == 0) {
+#pragma unroll
+        for (int k = 0; k < G; ++k) ginfo[lsb][k] = Op::info(h, k);
+    }
+    __syncthreads();
+    Op::requant(x, h, ginfo[lsb][sub], L);
     park_levels<SUB>(ltile + lsb * 256 + sub * SUB, L);
     __syncthreads();
     if (active && sub == 0) Op::pack(h, ltile + lsb * 256, TileOut{otile + lsb * (Op::BS / 2)});
@@ -571,8 +590,12 @@ int run(const QuantArgs& a) {
     if (nsb == 0) return 0;
     constexpr int SBW = WG / Op::G;
     const int64_t grid = (nsb + SBW - 1) / SBW;
-    hipLaunchKernelGGL((k_kquant<Op>), dim3((unsigned)grid), dim3(WG), 0, a.stream, a.src, a.src_kind,
-                       (uint8_t*)a.dst, nsb, a.n_per_row / 256, a.imatrix);
+    if (a.imatrix)
+        hipLaunchKernelGGL((k_kquant<Op, true>), dim3((unsigned)grid), dim3(WG), 0, a.stream, a.src, a.src_kind,
+                           (uint8_t*)a.dst, nsb, a.n_per_row / 256, a.imatrix);
+    else
+        hipLaunchKernelGGL((k_kquant<Op, false>), dim3((unsigned)grid), dim3(WG), 0, a.stream, a.src, a.src_kind,
+                           (uint8_t*)a.dst, nsb, a.n_per_row / 256, a.imatrix);
     SPA_HIP_TRY(hipGetLastError());
     return 0;
 }

@@ -145,6 +145,10 @@ __device__ __forceinline__ float make_qkx2_quants(const float (&x)[N], const flo
 // make_qkx3_quants with non-NULL weights and use_mad = false -- ggml-quants.c:993-1075 (every
 // imatrix K-quant and Q4_1/Q5_1 call site passes weights and use_mad = false).
 // Note the running `min`: a step that wins changes the offset used by every later step.
+// The levels of a step are a pure function of (iscale, min), so only the winning pair is kept and
+// L is produced once at the end. Inside the step loop, nearest_int(MIN(v, nmax)) for 0 < v <= nmax
+// is computed as rintf(fminf(v, nmax)): both round half to even and return the same integer (the
+// magic-number form is exact for |v| < 2^22); v <= 0 and NaN give 0 as in the C code.
 template <int N, int NMAX>
 __device__ __forceinline__ float make_qkx3_quants(const float (&x)[N], const float (&w)[N], int (&L)[N], float& the_min,
                                                   float rmin, float rdelta, int nstep) {
@@ -165,27 +169,27 @@ __device__ __forceinline__ float make_qkx3_quants(const float (&x)[N], const flo
         the_min = -min;
         return 0.f;
     }
-    float iscale = (float)NMAX / (max - min);
-    float scale = 1 / iscale;
+    const float iscale0 = (float)NMAX / (max - min);
+    float scale = 1 / iscale0;
     float best_mad = 0;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-        const int l = nearest_int(iscale * (x[i] - min));
-        L[i] = tmax(0, tmin(NMAX, l));
-        float diff = scale * (float)L[i] + min - x[i];
+        const int l = tmax(0, tmin(NMAX, nearest_int(iscale0 * (x[i] - min))));
+        float diff = scale * (float)l + min - x[i];
         diff = diff * diff;
         best_mad += w[i] * diff;
     }
-    if (nstep < 1) { the_min = -min; return scale; }
+    const float min0 = min;
+    float best_iscale = iscale0, best_min = min0;   // (iscale, min) that produced the kept levels
+    bool from_step = false;
     for (int is = 0; is <= nstep; ++is) {
-        iscale = (rmin + rdelta * (float)is + (float)NMAX) / (max - min);
+        const float iscale = (rmin + rdelta * (float)is + (float)NMAX) / (max - min);
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
         float Lf[N];
 #pragma unroll
         for (int i = 0; i < N; ++i) {
             const float v = iscale * (x[i] - min);
-            const int l = v > 0 ? nearest_int(v < (float)NMAX ? v : (float)NMAX) : 0;
-            const float fl = (float)l;
+            const float fl = v > 0.f ? rintf(fminf(v, (float)NMAX)) : 0.f;
             Lf[i] = fl;
             const float wl = w[i] * fl;
             sum_l += wl;
@@ -208,12 +212,22 @@ __device__ __forceinline__ float make_qkx3_quants(const float (&x)[N], const flo
                 mad += w[i] * diff;
             }
             if (mad < best_mad) {
-#pragma unroll
-                for (int i = 0; i < N; ++i) L[i] = (int)Lf[i];
+                best_iscale = iscale;
+                best_min = min;
+                from_step = true;
                 best_mad = mad;
                 scale = this_scale;
                 min = this_min;
             }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if (from_step) {
+            const float v = best_iscale * (x[i] - best_min);
+            L[i] = v > 0.f ? (int)rintf(fminf(v, (float)NMAX)) : 0;
+        } else {
+            L[i] = tmax(0, tmin(NMAX, nearest_int(best_iscale * (x[i] - best_min))));
         }
     }
     the_min = -min;
