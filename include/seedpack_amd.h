@@ -73,6 +73,46 @@ int spa_type_variants(int ggml_type);
 int spa_quantize(int ggml_type, int variant, const void* src, int src_kind, int64_t nrows, int64_t n_per_row,
                  const float* imatrix, void* dst, void* stream);
 
+/* ---- QR residual coder (non-grid quant types; seedpack/qr.py) ----
+ * Batch descriptors are device arrays with the reference's byte layout (qr.py:898-900):
+ *   tm: one 32-byte record per tensor {i64 blk0, i64 seed_off, i32 seed_type, i32 cols, i64 imx_off}
+ *   sg: one 16-byte record per segment {i32 t, i32 nb, i64 b0}
+ * F, P: the batch's file and predicted blocks back to back; seed: the seed tensors (BF16 = type 30,
+ * F32 = 0, F16 = 1) addressed by seed_off. gk / imx are for the grid types (not built yet; pass NULL).
+ * mv: the model version recorded with the batch (2 for new batches, 1 for archives before 0.3.0). */
+
+/* Blocks per rANS segment of a type: max(16, 16384 / QK) (qr.py:952-954); 0 if not a QR type. */
+int spa_qr_seg_blocks(int ggml_type);
+
+/* Symbol histogram of the batch into counts[294][256] (u32, accumulated: zero it first).
+ * Replaces the qr_hist kernel (qr.py:674-710). */
+int spa_qr_hist(int ggml_type, const void* F, const void* P, const void* seed, const void* tm, const void* sg,
+                int nseg, uint32_t* counts, const uint16_t* gk, const float* imx, int mv, void* stream);
+
+/* rANS-encodes each segment backwards into its own `cap`-byte slot of out (nseg * cap bytes), the
+ * stream ending at the slot's end; out_len[s] = bytes used, or 0xFFFFFFFF if the slot overflowed
+ * (the caller retries with a larger cap). remap[294] maps a context to its table row (-1 unused),
+ * freq[n][256] (u16, rows sum to 4096), cum[n][257]. Replaces qr_enc (qr.py:712-758). */
+int spa_qr_encode(int ggml_type, const void* F, const void* P, const void* seed, const void* tm, const void* sg,
+                  int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap,
+                  uint32_t* out_len, const uint16_t* gk, const float* imx, int mv, void* stream);
+
+/* Decodes every segment (stream bytes of segment s start at in + in_off[s]) into F (the batch's
+ * blocks). lut[n][4096] from spa_rans_build_lut. Replaces qr_dec (qr.py:760-807). */
+int spa_qr_decode(int ggml_type, const void* in, const uint64_t* in_off, const void* P, const void* seed,
+                  const void* tm, const void* sg, int nseg, const int* remap, const uint16_t* freq,
+                  const uint32_t* cum, const uint8_t* lut, void* F, const uint16_t* gk, const float* imx, int mv,
+                  void* stream);
+
+/* Compacts the segment slots into one stream: dst[off[s] ..] = the last len[s] bytes of slot s.
+ * Replaces gather (qr.py:880-887, gpu2.py:264-271). */
+int spa_qr_gather(const void* src, uint64_t cap, const uint32_t* len, const uint64_t* off, int nseg, void* dst,
+                  void* stream);
+
+/* lut[t][slot] = the symbol whose cumulative range holds slot, for ntab tables of 4096 slots.
+ * Replaces build_lut (qr.py:889-895, gpu2.py:273-279). */
+int spa_rans_build_lut(const uint32_t* cum, int ntab, uint8_t* lut, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

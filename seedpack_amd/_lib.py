@@ -39,6 +39,15 @@ SIGNATURES = {
     "spa_row_size": (c_size_t, [c_int, c_int64]),
     "spa_type_variants": (c_int, [c_int]),
     "spa_quantize": (c_int, [c_int, c_int, c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "spa_qr_seg_blocks": (c_int, [c_int]),
+    "spa_qr_hist": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                            c_void_p, c_int, c_void_p]),
+    "spa_qr_encode": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                              c_void_p, c_void_p, ctypes.c_uint64, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "spa_qr_decode": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
+                              c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "spa_qr_gather": (c_int, [c_void_p, ctypes.c_uint64, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "spa_rans_build_lut": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
 }
 
 

@@ -1,0 +1,385 @@
+// QR residual coder kernels for the non-grid quant types: histogram, interleaved-segment rANS
+// encode and decode, segment gather and decode lookup tables (seedpack/qr.py:674-895 semantics).
+//
+// Stream format (fixed by the archive): a batch of blocks is cut into segments of
+// max(16, 16384/QK) blocks; each segment is one rANS stream (PB = 12, RANS_L = 2^23, byte-wise
+// renormalisation) coded backwards, ending with the 4-byte state; decoding reads forward.
+//
+// Mapping on the MI355X:
+//   * histogram: one lane per block (not per segment), so every block of the batch is modelled in
+//     parallel; counts are integer sums (order-free), aggregated across the wave before each
+//     global atomic (one atomic per distinct counter per wave step);
+//   * encode / decode: one lane per segment -- the coder state is inherently serial within a
+//     segment; the decoder assembles each block in a per-lane LDS slot and stores it whole.
+#include <stdio.h>
+
+#include "../../include/seedpack_amd.h"
+#include "launch.h"
+#include "qr_model.h"
+
+namespace spa {
+namespace qr {
+namespace {
+
+__device__ __forceinline__ void hadd(uint32_t* counts, uint32_t key) {
+    uint64_t pending = __ballot(1);
+    const int lane = __lane_id();
+    while (pending) {
+        const int leader = __ffsll((unsigned long long)pending) - 1;
+        const uint32_t k = __shfl(key, leader);
+        const uint64_t same = __ballot(key == k) & pending;
+        if (lane == leader) atomicAdd(&counts[k], (uint32_t)__popcll(same));
+        pending &= ~same;
+    }
+}
+
+// one lane per block: thread i -> segment i / SEG_BLOCKS, block (i % SEG_BLOCKS) of that segment
+template <int T>
+__global__ __launch_bounds__(256) void k_qr_hist(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
+                                                 const uint8_t* __restrict__ seed, const TM* __restrict__ tm,
+                                                 const SG* __restrict__ sg, int nseg, uint32_t* __restrict__ counts, int mv) {
+    using Y = Ty<T>;
+    constexpr int SEG = SEG_BLOCKS<T>;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t s = gid / SEG;
+    const int j = (int)(gid % SEG);
+    if (s >= nseg) return;
+    const SG g = sg[s];
+    if (j >= g.nb) return;
+    const TM m = tm[g.t];
+    const int64_t b = g.b0 + j;
+    const uint8_t* fb = F + b * Y::BS;
+    const uint8_t* pb = P + b * Y::BS;
+    const bool eq = same_block(fb, pb, Y::BS);
+    const int prev = j > 0 ? (int)same_block(fb - Y::BS, pb - Y::BS, Y::BS) : 1;
+    hadd(counts, (uint32_t)((FLAG + prev) * 256 + (eq ? 1 : 0)));
+    if (eq) return;
+    int tv[Y::NF];
+#pragma unroll
+    for (int k = 0; k < Y::NF; ++k) tv[k] = get_field<T>(fb, k);
+    int any = 0;
+#pragma unroll
+    for (int k = 0; k < Y::NF; ++k) {
+        const int kd = fkind<T>(k);
+        const int pr = fpred<T>(mv, pb, k, tv[0], Y::NF > 1 ? tv[1] : 0), dlt = tv[k] - pr;
+        if (kd < 2 && (dlt < -127 || dlt > 127)) {
+            hadd(counts, (uint32_t)((kd * 2 + any) * 256 + 128));
+            hadd(counts, (uint32_t)(FESC_LO * 256 + (tv[k] & 255)));
+            hadd(counts, (uint32_t)(FESC_HI * 256 + (tv[k] >> 8)));
+        } else {
+            hadd(counts, (uint32_t)((kd * 2 + any) * 256 + (dlt & 255)));
+        }
+        any |= dlt != 0;
+    }
+    const uint8_t* sbase = seed + m.seed_off;
+    const int64_t gw0 = (b - m.blk0) * Y::QK;
+    const int64_t col0 = m.cols > 0 ? gw0 % m.cols : 0;
+    float a = 0.f, c = 0.f;
+    for (int w = 0; w < Y::QK; ++w) {
+        if (w % Y::SUBLEN == 0) wscale<T>(fb, w, a, c);
+        float x, h;
+        seed_val(m.seed_type, sbase, gw0 + w, x, h);
+        int r, sg_, ctx;
+        predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
+        hadd(counts, (uint32_t)(ctx * 256 + ((sg_ * (get_code<T>(fb, w) - r)) & 255)));
+    }
+}
+
+struct Enc {
+    uint32_t x;
+    uint8_t* ptr;
+    const int* remap;
+    const uint16_t* freq;
+    const uint32_t* cum;
+    __device__ __forceinline__ void put(int tab, uint32_t sym) {
+        const int tt = remap[tab];
+        const uint32_t f = freq[tt * 256 + sym], c = cum[tt * 257 + sym];
+        const uint32_t xm = ((RANS_L >> PB) << 8) * f;
+        while (x >= xm) { *--ptr = (uint8_t)(x & 0xff); x >>= 8; }
+        x = ((x / f) << PB) + (x % f) + c;
+    }
+};
+
+template <int T>
+__global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
+                                               const uint8_t* __restrict__ seed, const TM* __restrict__ tm,
+                                               const SG* __restrict__ sg, int nseg, const int* __restrict__ remap,
+                                               const uint16_t* __restrict__ freq, const uint32_t* __restrict__ cum,
+                                               uint8_t* __restrict__ out, uint64_t cap, uint32_t* __restrict__ out_len, int mv) {
+    using Y = Ty<T>;
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    const SG g = sg[s];
+    const TM m = tm[g.t];
+    const uint8_t* sbase = seed + m.seed_off;
+    uint8_t* const base = out + (uint64_t)s * cap;
+    uint8_t* const end = base + cap;
+    Enc e{RANS_L, end, remap, freq, cum};
+    for (int64_t b = g.b0 + g.nb - 1; b >= g.b0; --b) {
+        const uint8_t* fb = F + b * Y::BS;
+        const uint8_t* pb = P + b * Y::BS;
+        const bool eq = same_block(fb, pb, Y::BS);
+        const int prev = b > g.b0 ? (int)same_block(fb - Y::BS, pb - Y::BS, Y::BS) : 1;
+        if (eq) { e.put(FLAG + prev, 1); continue; }
+        const int64_t gw0 = (b - m.blk0) * Y::QK;
+        const int64_t col0 = m.cols > 0 ? gw0 % m.cols : 0;
+        float a = 0.f, c = 0.f;
+        int sub = -1;
+        for (int w = Y::QK - 1; w >= 0; --w) {
+            if (w / Y::SUBLEN != sub) { sub = w / Y::SUBLEN; wscale<T>(fb, w, a, c); }
+            float x, h;
+            seed_val(m.seed_type, sbase, gw0 + w, x, h);
+            int r, sg_, ctx;
+            predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
+            e.put(ctx, (uint32_t)((sg_ * (get_code<T>(fb, w) - r)) & 255));
+            if (e.ptr - base < 8) { out_len[s] = 0xffffffffu; return; }
+        }
+        int tv[Y::NF], dl[Y::NF], anyk[Y::NF];
+#pragma unroll
+        for (int k = 0; k < Y::NF; ++k) tv[k] = get_field<T>(fb, k);
+        int any = 0;
+#pragma unroll
+        for (int k = 0; k < Y::NF; ++k) {
+            dl[k] = tv[k] - fpred<T>(mv, pb, k, tv[0], Y::NF > 1 ? tv[1] : 0);
+            anyk[k] = any;
+            any |= dl[k] != 0;
+        }
+#pragma unroll
+        for (int k = Y::NF - 1; k >= 0; --k) {
+            const int kd = fkind<T>(k);
+            if (kd < 2 && (dl[k] < -127 || dl[k] > 127)) {
+                e.put(FESC_HI, (uint32_t)(tv[k] >> 8));
+                e.put(FESC_LO, (uint32_t)(tv[k] & 255));
+                e.put(kd * 2 + anyk[k], 128);
+            } else {
+                e.put(kd * 2 + anyk[k], (uint32_t)(dl[k] & 255));
+            }
+        }
+        e.put(FLAG + prev, 0);
+    }
+    for (int i = 0; i < 4; ++i) { *--e.ptr = (uint8_t)(e.x & 0xff); e.x >>= 8; }
+    out_len[s] = (uint32_t)(end - e.ptr);
+}
+
+struct Dec {
+    uint32_t x;
+    const uint8_t* ptr;
+    const int* remap;
+    const uint16_t* freq;
+    const uint32_t* cum;
+    const uint8_t* lut;
+    __device__ __forceinline__ int get(int tab) {
+        const int tt = remap[tab];
+        const uint32_t slot = x & (PSCALE - 1);
+        const int v = lut[(size_t)tt * PSCALE + slot];
+        x = freq[tt * 256 + v] * (x >> PB) + slot - cum[tt * 257 + v];
+        while (x < RANS_L) x = (x << 8) | *ptr++;
+        return v;
+    }
+};
+
+constexpr int DEC_WG = 64;
+
+template <int T>
+__global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ in, const uint64_t* __restrict__ in_off,
+                                                   const uint8_t* __restrict__ P, const uint8_t* __restrict__ seed,
+                                                   const TM* __restrict__ tm, const SG* __restrict__ sg, int nseg,
+                                                   const int* __restrict__ remap, const uint16_t* __restrict__ freq,
+                                                   const uint32_t* __restrict__ cum, const uint8_t* __restrict__ lut,
+                                                   uint8_t* __restrict__ F, int mv) {
+    using Y = Ty<T>;
+    constexpr int BSP = (Y::BS + 3) & ~3;
+    __shared__ __align__(4) uint8_t blk[DEC_WG * BSP];
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= nseg) return;
+    uint8_t* fb = blk + threadIdx.x * BSP;
+    const SG g = sg[s];
+    const TM m = tm[g.t];
+    const uint8_t* sbase = seed + m.seed_off;
+    Dec d{0, in + in_off[s], remap, freq, cum, lut};
+    for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | *d.ptr++;
+    int prev = 1;
+    for (int64_t b = g.b0; b < g.b0 + g.nb; ++b) {
+        const uint8_t* pb = P + b * Y::BS;
+        uint8_t* dst = F + b * Y::BS;
+        const int eq = d.get(FLAG + prev);
+        prev = eq;
+        if (eq) {
+            for (int i = 0; i < Y::BS; ++i) dst[i] = pb[i];
+            continue;
+        }
+        for (int i = 0; i < Y::BS; ++i) fb[i] = 0;
+        int vals[Y::NF];
+        int any = 0;
+#pragma unroll
+        for (int k = 0; k < Y::NF; ++k) {
+            const int kd = fkind<T>(k);
+            const int pr = fpred<T>(mv, pb, k, k > 0 ? vals[0] : 0, k > 1 ? vals[Y::NF > 1 ? 1 : 0] : 0);
+            const int sym = d.get(kd * 2 + any);
+            int t;
+            if (kd < 2 && sym == 128) {
+                const int lo = d.get(FESC_LO), hi = d.get(FESC_HI);
+                t = lo | (hi << 8);
+            } else {
+                t = pr + s8((uint32_t)sym);
+                if (kd < 2) t &= 0xffff;
+                else if (T == 14) t = s8((uint32_t)t);
+            }
+            vals[k] = t;
+            any |= t != pr;
+        }
+        set_fields<T>(fb, vals);
+        const int64_t gw0 = (b - m.blk0) * Y::QK;
+        const int64_t col0 = m.cols > 0 ? gw0 % m.cols : 0;
+        float a = 0.f, c = 0.f;
+        for (int w = 0; w < Y::QK; ++w) {
+            if (w % Y::SUBLEN == 0) wscale<T>(fb, w, a, c);
+            float x, h;
+            seed_val(m.seed_type, sbase, gw0 + w, x, h);
+            int r, sg_, ctx;
+            predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
+            const int v = d.get(ctx);
+            int q = r + sg_ * s8((uint32_t)v);
+            if (T == 8) q = s8((uint32_t)q);
+            put_code<T>(fb, w, q);
+        }
+        for (int i = 0; i < Y::BS; ++i) dst[i] = fb[i];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_qr_gather(const uint8_t* __restrict__ src, uint64_t cap, const uint32_t* __restrict__ len,
+                                                   const uint64_t* __restrict__ off, int nseg, uint8_t* __restrict__ dst) {
+    const int s = blockIdx.x;
+    if (s >= nseg) return;
+    const uint8_t* a = src + (uint64_t)(s + 1) * cap - len[s];
+    uint8_t* d = dst + off[s];
+    for (uint32_t i = threadIdx.x; i < len[s]; i += blockDim.x) d[i] = a[i];
+}
+
+__global__ __launch_bounds__(256) void k_build_lut(const uint32_t* __restrict__ cum, int ntab, uint8_t* __restrict__ lut) {
+    const int tb = blockIdx.x;
+    if (tb >= ntab) return;
+    for (int sym = threadIdx.x; sym < 256; sym += blockDim.x)
+        for (uint32_t i = cum[tb * 257 + sym]; i < cum[tb * 257 + sym + 1]; ++i) lut[(size_t)tb * PSCALE + i] = (uint8_t)sym;
+}
+
+template <template <int> class K, class... A>
+int dispatch(int T, A&&... args) {
+    switch (T) {
+        case 2: return K<2>::run(args...);
+        case 3: return K<3>::run(args...);
+        case 6: return K<6>::run(args...);
+        case 7: return K<7>::run(args...);
+        case 8: return K<8>::run(args...);
+        case 10: return K<10>::run(args...);
+        case 11: return K<11>::run(args...);
+        case 12: return K<12>::run(args...);
+        case 13: return K<13>::run(args...);
+        case 14: return K<14>::run(args...);
+        case 20: return K<20>::run(args...);
+        case 23: return K<23>::run(args...);
+        case 42: return K<42>::run(args...);
+    }
+    return fail(SPA_ERR_TYPE, "QR: type %d is not a non-grid QR type", T);
+}
+
+template <int T> struct Hist {
+    static int run(const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,
+                   uint32_t* counts, int mv, hipStream_t st) {
+        const int64_t n = (int64_t)nseg * SEG_BLOCKS<T>;
+        hipLaunchKernelGGL(k_qr_hist<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint8_t*)F,
+                           (const uint8_t*)P, (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, counts, mv);
+        SPA_HIP_TRY(hipGetLastError());
+        return 0;
+    }
+};
+template <int T> struct Encode {
+    static int run(const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, const int* remap,
+                   const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, int mv, hipStream_t st) {
+        hipLaunchKernelGGL(k_qr_enc<T>, dim3((unsigned)((nseg + 63) / 64)), dim3(64), 0, st, (const uint8_t*)F,
+                           (const uint8_t*)P, (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, remap, freq, cum,
+                           (uint8_t*)out, cap, out_len, mv);
+        SPA_HIP_TRY(hipGetLastError());
+        return 0;
+    }
+};
+template <int T> struct Decode {
+    static int run(const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
+                   int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F, int mv,
+                   hipStream_t st) {
+        hipLaunchKernelGGL(k_qr_dec<T>, dim3((unsigned)((nseg + DEC_WG - 1) / DEC_WG)), dim3(DEC_WG), 0, st,
+                           (const uint8_t*)in, in_off, (const uint8_t*)P, (const uint8_t*)seed, (const TM*)tm, (const SG*)sg,
+                           nseg, remap, freq, cum, lut, (uint8_t*)F, mv);
+        SPA_HIP_TRY(hipGetLastError());
+        return 0;
+    }
+};
+
+bool grid_type(int T) { return T == 16 || T == 17 || T == 18 || T == 19 || T == 21 || T == 22 || T == 29; }
+
+int check_common(int T, int nseg, int mv, const void* gk, const float* imx) {
+    if (grid_type(T)) return fail(SPA_ERR_TYPE, "QR: grid type %d is not built yet", T);
+    if (nseg < 0) return fail(SPA_ERR_ARG, "QR: negative segment count");
+    if (mv != 1 && mv != 2) return fail(SPA_ERR_ARG, "QR: unknown model %d", mv);
+    (void)gk; (void)imx;
+    return 0;
+}
+
+}  // namespace
+}  // namespace qr
+}  // namespace spa
+
+using namespace spa::qr;
+
+extern "C" {
+
+int spa_qr_seg_blocks(int T) {
+    switch (T) {
+        case 2: case 3: case 6: case 7: case 8: case 20: return 512;
+        case 42: return 256;
+        case 10: case 11: case 12: case 13: case 14: case 23: case 16: case 17: case 18: case 19: case 21: case 22: case 29:
+            return 64;
+    }
+    return 0;
+}
+
+int spa_qr_hist(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,
+                uint32_t* counts, const uint16_t* gk, const float* imx, int mv, void* stream) {
+    if (int e = check_common(T, nseg, mv, gk, imx)) return e;
+    if (nseg == 0) return 0;
+    return dispatch<Hist>(T, F, P, seed, tm, sg, nseg, counts, mv, (hipStream_t)stream);
+}
+
+int spa_qr_encode(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,
+                  const int* remap, const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len,
+                  const uint16_t* gk, const float* imx, int mv, void* stream) {
+    if (int e = check_common(T, nseg, mv, gk, imx)) return e;
+    if (cap < 1024) return spa::fail(SPA_ERR_ARG, "QR: segment capacity %llu too small", (unsigned long long)cap);
+    if (nseg == 0) return 0;
+    return dispatch<Encode>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, mv, (hipStream_t)stream);
+}
+
+int spa_qr_decode(int T, const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm,
+                  const void* sg, int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut,
+                  void* F, const uint16_t* gk, const float* imx, int mv, void* stream) {
+    if (int e = check_common(T, nseg, mv, gk, imx)) return e;
+    if (nseg == 0) return 0;
+    return dispatch<Decode>(T, in, in_off, P, seed, tm, sg, nseg, remap, freq, cum, lut, F, mv, (hipStream_t)stream);
+}
+
+int spa_qr_gather(const void* src, uint64_t cap, const uint32_t* len, const uint64_t* off, int nseg, void* dst, void* stream) {
+    if (nseg <= 0) return 0;
+    hipLaunchKernelGGL(k_qr_gather, dim3((unsigned)nseg), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src, cap, len,
+                       off, nseg, (uint8_t*)dst);
+    SPA_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int spa_rans_build_lut(const uint32_t* cum, int ntab, uint8_t* lut, void* stream) {
+    if (ntab <= 0) return 0;
+    hipLaunchKernelGGL(k_build_lut, dim3((unsigned)ntab), dim3(256), 0, (hipStream_t)stream, cum, ntab, lut);
+    SPA_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+}  // extern "C"

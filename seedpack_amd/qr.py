@@ -1,0 +1,261 @@
+"""Host side of the QR residual coder over the HIP C ABI (the reference's seedpack/qr.py interface).
+
+encode(T, items, seed_dev, imx_dev=None, mv=None) -> bytes and decode(T, buf, items, seed_dev,
+imx_dev=None) -> device array keep qr.py:1007-1090's argument meaning and the coded batch format:
+pack({"t": zstd(u32 n, u32 used deltas, u16 freq[n][256]), "l": zstd(u32 segment lengths),
+"s": stream, "v": model}). The symbol model, the rANS coding, the gather and the decode lookup tables
+run as HIP kernels; the table normalisation runs on the host, as in the reference (it is a loop over
+a few hundred rows).
+
+items (encode): (file bytes, predicted bytes, seed byte offset, seed type[, weights per row,
+imatrix offset]); (decode): the same without the file bytes. Bytes are numpy uint8 arrays or
+DeviceArrays; seeds are device arrays (BF16 = type 30, F32 = 0, F16 = 1).
+"""
+import struct
+
+import numpy as np
+
+from . import device as dev
+from . import zstd
+from ._lib import check, lib
+
+SELF_TYPES = {2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 20, 23, 42}
+GRID_TYPES = {16, 17, 18, 19, 21, 22, 29}
+QR_TYPES = SELF_TYPES | GRID_TYPES
+BS = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 20: 18, 23: 136, 42: 18,
+      16: 66, 17: 74, 18: 98, 19: 50, 21: 110, 22: 82, 29: 56}
+QK = {t: (32 if t in (2, 3, 6, 7, 8, 20) else 64 if t == 42 else 256) for t in QR_TYPES}
+NSB_MAX = 20
+NTAB2 = NSB_MAX + 64 + 2 + 208
+MODEL = 2
+PB = 12
+BATCH = 384 << 20                                   # bytes per coding batch (qr.py:56)
+
+TM_DT = np.dtype([("blk0", "<i8"), ("seed_off", "<i8"), ("seed_type", "<i4"), ("cols", "<i4"), ("imx_off", "<i8")])
+SG_DT = np.dtype([("t", "<i4"), ("nb", "<i4"), ("b0", "<i8")])
+
+
+def seg_blocks(T):
+    """blocks per rANS segment: max(16, 16384 // QK) (part of the stream format)"""
+    return max(16, 16384 // QK[T])
+
+
+def layout(T, nblocks):
+    """tensors' block counts -> (TM records without the seed fields, SG records, total blocks)"""
+    sb = seg_blocks(T)
+    tm = np.zeros(len(nblocks), TM_DT)
+    starts, b0 = [], 0
+    for i, nb in enumerate(nblocks):
+        tm[i]["blk0"] = b0
+        starts += [(i, min(sb, nb - o), b0 + o) for o in range(0, nb, sb)]
+        b0 += nb
+    return tm, np.array(starts, SG_DT) if starts else np.zeros(0, SG_DT), b0
+
+
+def batches(T, sizes):
+    """tensor indices split into coding batches of about BATCH bytes (the same split on both sides)"""
+    out, cur, n = [], [], 0
+    for i, s in enumerate(sizes):
+        if cur and n + s > BATCH:
+            out.append(cur)
+            cur, n = [], 0
+        cur.append(i)
+        n += s
+    if cur:
+        out.append(cur)
+    return out
+
+
+def normalize(counts, scale=1 << PB):
+    """(rows, 256) counts -> (u16 frequencies of the used rows, used row ids); each row sums to
+    `scale`, every seen symbol keeps a frequency >= 1. The rounding error is settled on the largest
+    entry, one step at a time, as qr.py:904-923 does."""
+    c = np.asarray(counts, np.int64)
+    tot = c.sum(1)
+    used = np.flatnonzero(tot)
+    rows = c[used]
+    f = np.where(rows > 0, np.maximum(1, rows * scale // tot[used, None]), 0)
+    for k in range(len(used)):
+        fr = f[k]
+        diff = scale - int(fr.sum())
+        while diff:
+            j = int(np.argmax(fr))
+            step = diff if diff > 0 else -min(-diff, int(fr[j]) - 1)
+            if step == 0:                       # the largest is 1: take from the first entry > 1
+                j = int(np.argmax(fr > 1))
+                step = -1
+            fr[j] += step
+            diff -= step
+    return f.astype(np.uint16), used.astype(np.int32)
+
+
+def cum_of(freq):
+    cum = np.zeros((freq.shape[0], 257), np.uint32)
+    cum[:, 1:] = np.cumsum(freq.astype(np.uint32), axis=1)
+    return cum
+
+
+def store_tables(freq, used):
+    """table chunk: u32 row count, u32 deltas of the used row ids, u16 frequencies (gpu2.py:489-492)"""
+    u = np.asarray(used, np.int64)
+    du = np.diff(u, prepend=0).astype(np.uint32)
+    return zstd.compress(struct.pack("<I", len(u)) + du.tobytes() + np.asarray(freq, np.uint16).tobytes(), 19)
+
+
+def load_tables(buf):
+    raw = zstd.decompress(buf)
+    (n,) = struct.unpack_from("<I", raw)
+    used = np.cumsum(np.frombuffer(raw, np.uint32, n, 4).astype(np.int64))
+    freq = np.frombuffer(raw, np.uint16, n * 256, 4 + 4 * n).reshape(n, 256)
+    return freq, used
+
+
+def pack(chunks):
+    """u32 count, then per chunk: u16 name length, name, u64 length, data (codecs_gguf.py:33-56)"""
+    out = [struct.pack("<I", len(chunks))]
+    for name, data in chunks.items():
+        nb = name.encode()
+        out += [struct.pack("<H", len(nb)), nb, struct.pack("<Q", len(data)), bytes(data)]
+    return b"".join(out)
+
+
+def unpack(buf):
+    (n,), pos, chunks = struct.unpack_from("<I", buf), 4, {}
+    for _ in range(n):
+        (ln,) = struct.unpack_from("<H", buf, pos)
+        pos += 2
+        name = bytes(buf[pos:pos + ln]).decode()
+        pos += ln
+        (dl,) = struct.unpack_from("<Q", buf, pos)
+        pos += 8
+        chunks[name] = buf[pos:pos + dl]
+        pos += dl
+    return chunks
+
+
+def _gather(arrs, stream=None):
+    """host or device uint8 arrays -> one device array, each copied to its place"""
+    if len(arrs) == 1 and isinstance(arrs[0], dev.DeviceArray):
+        return arrs[0]
+    n = sum(a.nbytes if isinstance(a, dev.DeviceArray) else len(a) for a in arrs)
+    out = dev.DeviceArray(max(n, 1), np.uint8)
+    o = 0
+    for a in arrs:
+        if isinstance(a, dev.DeviceArray):
+            check(lib().spa_memcpy_d2d(out.ptr + o, a.ptr, a.nbytes, stream))
+            o += a.nbytes
+        else:
+            a = np.ascontiguousarray(a, np.uint8)
+            check(lib().spa_memcpy_h2d(out.ptr + o, a.ctypes.data, a.nbytes, stream))
+            o += a.nbytes
+    return out
+
+
+def _nbytes(a):
+    return a.nbytes if isinstance(a, dev.DeviceArray) else len(a)
+
+
+def _descriptors(T, nbs, meta):
+    tm, sg, nb = layout(T, nbs)
+    tm["seed_off"] = [m[0] for m in meta]
+    tm["seed_type"] = [m[1] for m in meta]
+    tm["cols"] = [m[2] if len(m) > 2 else 0 for m in meta]
+    tm["imx_off"] = [m[3] if len(m) > 3 else -1 for m in meta]
+    return tm, sg, nb
+
+
+def _check_type(T):
+    if T in GRID_TYPES:
+        raise NotImplementedError(f"QR for grid type {T} is not built yet")
+    if T not in SELF_TYPES:
+        raise ValueError(f"type {T} is not a QR type")
+
+
+def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
+    """the coded batch before framing: dict(counts, freq, used, lens, stream, mv)"""
+    _check_type(T)
+    mv = MODEL if mv is None else mv
+    bs = BS[T]
+    tm, sg, nb = _descriptors(T, [_nbytes(it[0]) // bs for it in items], [it[2:] for it in items])
+    F = _gather([it[0] for it in items], stream)
+    P = _gather([it[1] for it in items], stream)
+    nseg = len(sg)
+    tm_d = dev.DeviceArray.from_host(tm.view(np.uint8), stream)
+    sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if nseg else np.zeros(16, np.uint8), stream)
+    counts = dev.DeviceArray((NTAB2, 256), np.uint32).zero(stream)
+    imx = None if imx_dev is None else imx_dev.ptr
+    check(lib().spa_qr_hist(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, counts.ptr, None, imx, mv, stream))
+    counts_h = counts.to_host(stream=stream)
+    freq, used = normalize(counts_h)
+    remap = np.full(NTAB2, -1, np.int32)
+    remap[used] = np.arange(len(used), dtype=np.int32)
+    cum = cum_of(freq)
+    remap_d, freq_d, cum_d = (dev.DeviceArray.from_host(a, stream) for a in (remap, freq, cum))
+    cap = seg_blocks(T) * (3 * BS[T] if T in GRID_TYPES else (QK[T] + NSB_MAX) * 2) + 1024
+    for _ in range(3):
+        out = dev.DeviceArray(max(1, nseg * cap), np.uint8)
+        out_len = dev.DeviceArray(max(1, nseg), np.uint32).zero(stream)
+        check(lib().spa_qr_encode(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr, freq_d.ptr,
+                                  cum_d.ptr, out.ptr, cap, out_len.ptr, None, imx, mv, stream))
+        lens = out_len.to_host(stream=stream)[:nseg]
+        if not (lens == 0xFFFFFFFF).any():
+            break
+        cap *= 2                                 # an overflowing segment: retry with twice the room
+    else:
+        raise RuntimeError("QR segment overflow")
+    offs = np.zeros(nseg + 1, np.uint64)
+    offs[1:] = np.cumsum(lens.astype(np.uint64))
+    total = int(offs[-1])
+    dst = dev.DeviceArray(max(1, total), np.uint8)
+    offs_d = dev.DeviceArray.from_host(offs, stream)
+    check(lib().spa_qr_gather(out.ptr, cap, out_len.ptr, offs_d.ptr, nseg, dst.ptr, stream))
+    data = dst.to_host(stream=stream)[:total]
+    return {"counts": counts_h, "freq": freq, "used": used, "lens": lens.astype(np.uint32), "stream": data, "mv": mv}
+
+
+def encode(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
+    """one coded batch (qr.py:1007-1061) -> bytes"""
+    p = encode_parts(T, items, seed_dev, imx_dev, mv, stream)
+    out = {"t": store_tables(p["freq"], p["used"]), "l": zstd.compress(p["lens"].astype(np.uint32).tobytes(), 19),
+           "s": p["stream"].tobytes()}
+    if p["mv"] != 1:
+        out["v"] = bytes([p["mv"]])
+    return pack(out)
+
+
+def decode_parts(T, freq, used, lens, stream_bytes, items, seed_dev, imx_dev=None, mv=MODEL, stream=None):
+    """the batch's tensors (device uint8, back to back) from its coded parts"""
+    _check_type(T)
+    bs = BS[T]
+    tm, sg, nb = _descriptors(T, [_nbytes(it[0]) // bs for it in items], [it[1:] for it in items])
+    nseg = len(sg)
+    P = _gather([it[0] for it in items], stream)
+    F = dev.DeviceArray(max(1, nb * bs), np.uint8)
+    freq = np.ascontiguousarray(freq, np.uint16)
+    cum = cum_of(freq)
+    remap = np.full(NTAB2, -1, np.int32)
+    remap[np.asarray(used, np.int64)] = np.arange(len(used), dtype=np.int32)
+    freq_d, cum_d, remap_d = (dev.DeviceArray.from_host(a, stream) for a in (freq, cum, remap))
+    lut = dev.DeviceArray((max(1, len(freq)), 1 << PB), np.uint8)
+    check(lib().spa_rans_build_lut(cum_d.ptr, len(freq), lut.ptr, stream))
+    lens = np.asarray(lens, np.uint64)
+    offs = np.zeros(max(1, nseg), np.uint64)
+    offs[1:nseg] = np.cumsum(lens)[:-1]
+    s = np.frombuffer(bytes(stream_bytes), np.uint8)
+    s_d = dev.DeviceArray.from_host(s if len(s) else np.zeros(1, np.uint8), stream)
+    tm_d = dev.DeviceArray.from_host(tm.view(np.uint8), stream)
+    sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if nseg else np.zeros(16, np.uint8), stream)
+    offs_d = dev.DeviceArray.from_host(offs, stream)
+    imx = None if imx_dev is None else imx_dev.ptr
+    check(lib().spa_qr_decode(T, s_d.ptr, offs_d.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr,
+                              freq_d.ptr, cum_d.ptr, lut.ptr, F.ptr, None, imx, mv, stream))
+    return F
+
+
+def decode(T, buf, items, seed_dev, imx_dev=None, stream=None):
+    """one coded batch -> device uint8 array of its tensors back to back (qr.py:1064-1090)"""
+    ch = unpack(buf)
+    mv = bytes(ch["v"])[0] if "v" in ch else 1      # batches without it predate model 2
+    freq, used = load_tables(ch["t"])
+    lens = np.frombuffer(zstd.decompress(ch["l"]), np.uint32)
+    return decode_parts(T, freq, used, lens, ch["s"], items, seed_dev, imx_dev, mv, stream)
