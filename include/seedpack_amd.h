@@ -73,6 +73,15 @@ int spa_type_variants(int ggml_type);
 int spa_quantize(int ggml_type, int variant, const void* src, int src_kind, int64_t nrows, int64_t n_per_row,
                  const float* imatrix, void* dst, void* stream);
 
+/* Host view of IQ lattice table `index` (0 IQ2_XXS, 1 IQ2_XS, 2 IQ1_S/IQ1_M, 3 IQ2_S, 4 IQ3_XXS,
+ * 5 IQ3_S), built by the library on first use: the codebook as coordinate bytes (8 or 4 per point),
+ * the level-index map and the neighbour lists, equal to what llama.cpp's iq2xs_init_impl /
+ * iq3xs_init_impl build (ggml-quants.c:2854-3259, :3704-3903; the reference ships them as
+ * seedpack/ggml/iqtables.npz and uploads them, gpuquant.py:311-326). Pointers stay valid for the
+ * process. */
+int spa_iq_table_host(int index, const void** grid, int* grid_bytes, const int32_t** map, int* map_n,
+                      const uint16_t** neighbours, int* nb_n);
+
 /* ---- QR residual coder (non-grid quant types; seedpack/qr.py) ----
  * Batch descriptors are device arrays with the reference's byte layout (qr.py:898-900):
  *   tm: one 32-byte record per tensor {i64 blk0, i64 seed_off, i32 seed_type, i32 cols, i64 imx_off}

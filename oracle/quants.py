@@ -764,10 +764,120 @@ def q6_K(x, imx=None):
     return out.reshape(-1)
 
 
+# ------------------------------------------------------------------ IQ4_NL / IQ4_XS
+
+KVALUES = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], F)   # ggml-common.h:1120
+
+
+def best_index_iq4(x):
+    """best_index_int8(16, kvalues_iq4nl, x) -- ggml-quants.c:28-37 (mu = first value above x; ties
+    go to the upper value)"""
+    x = np.asarray(x, F)
+    with np.errstate(invalid="ignore"):
+        mu = np.clip(np.searchsorted(KVALUES, x, side="right"), 1, 15)
+        lo = (x - KVALUES[mu - 1]).astype(F)
+        hi = (KVALUES[mu] - x).astype(F)
+        r = np.where(lo < hi, mu - 1, mu)
+        r = np.where(x >= KVALUES[15], 15, r)
+        r = np.where(x <= KVALUES[0], 0, r)
+    return r.astype(np.int64)
+
+
+def _iq4_block_scales(X, W):
+    """the per-block scale search of quantize_row_iq4_nl_impl with ntry = 7 (ggml-quants.c:4962-5010)"""
+    amax = np.zeros(len(X), F)
+    mx = np.zeros(len(X), F)
+    for j in range(X.shape[1]):
+        a = np.abs(X[:, j])
+        up = a > amax
+        amax = np.where(up, a, amax)
+        mx = np.where(up, X[:, j], mx)
+    zero = amax < GROUP_MAX_EPS
+    with _errs():
+        d = (-mx / KVALUES[0]).astype(F)
+        idv = (F(1) / d).astype(F)
+
+        def sums(idv):
+            q = KVALUES[best_index_iq4(idv[:, None] * X)]
+            return seqsum(W * q * X), seqsum(W * q * q)
+
+        sqx, sq2 = sums(idv)
+        d = np.where(sq2 > 0, sqx / sq2, F(0)).astype(F)
+        best = (d * sqx).astype(F)
+        for itry in range(-7, 8):
+            idv = (F(itry + int(KVALUES[0])) / mx).astype(F)
+            sqx, sq2 = sums(idv)
+            up = (sq2 > 0) & (sqx * sqx > best * sq2)
+            d = np.where(up, sqx / sq2, d).astype(F)
+            best = np.where(up, d * sqx, best).astype(F)
+    return np.where(zero, F(0), d).astype(F)
+
+
+def iq4_nl(x, imx=None):
+    """quantize_iq4_nl -- ggml-quants.c:5049-5069 (quantize_row_iq4_nl_impl, 32/32, ntry 7)"""
+    x = np.ascontiguousarray(x, F)
+    X = x.reshape(-1, 32)
+    with _errs():
+        sigma2 = (seqsum(X * X) * (F(2) / F(32))).astype(F)
+        if imx is None:
+            W = (X * X).astype(F)
+        else:
+            qw = np.broadcast_to(np.asarray(imx, F).reshape(1, -1, 32), (x.shape[0], x.shape[1] // 32, 32)).reshape(-1, 32)
+            W = (qw * np.sqrt(sigma2[:, None] + X * X)).astype(F)
+        d = _iq4_block_scales(X, W)
+        idv = np.where(d != 0, F(1) / d, F(0)).astype(F)
+        L = best_index_iq4(idv[:, None] * X)
+    out = _out(len(X), 18)
+    _put16(out, 0, fp16_bits(d))
+    out[:, 2:] = _pack_nibbles(L[:, :16], L[:, 16:])
+    return out.reshape(-1)
+
+
+def iq4_xs(x, imx=None):
+    """quantize_iq4_xs -- ggml-quants.c:5087-5105 (quantize_row_iq4_nl_impl, 256/32, ntry 7)"""
+    x = np.ascontiguousarray(x, F)
+    X = x.reshape(-1, 256)
+    nsb = len(X)
+    Xs = X.reshape(-1, 32)
+    with _errs():
+        sigma2 = (seqsum(X * X) * (F(2) / F(256))).astype(F)
+        if imx is None:
+            W = (Xs * Xs).astype(F)
+        else:
+            qw = np.broadcast_to(np.asarray(imx, F).reshape(1, -1, 256), (x.shape[0], x.shape[1] // 256, 256)).reshape(-1, 32)
+            W = (qw * np.sqrt(np.repeat(sigma2, 256)[:, None].reshape(-1, 32) + Xs * Xs)).astype(F)
+        sc = _iq4_block_scales(Xs, W).reshape(nsb, 8)
+        amax = np.zeros(nsb, F)
+        mxs = np.zeros(nsb, F)
+        for j in range(8):
+            a = np.abs(sc[:, j])
+            up = a > amax
+            amax = np.where(up, a, amax)
+            mxs = np.where(up, sc[:, j], mxs)
+        d = (-mxs / F(32)).astype(F)
+        idv = np.where(d != 0, F(1) / d, F(0)).astype(F)
+        l = np.clip(nearest_int(idv[:, None] * sc), -32, 31)
+        dl = (d[:, None] * l.astype(F)).astype(F)
+        idl = np.where(dl != 0, F(1) / dl, F(0)).astype(F).reshape(-1)
+        L = best_index_iq4(idl[:, None] * Xs).reshape(nsb, 256)
+    l = l + 32
+    out = _out(nsb, 136)
+    _put16(out, 0, fp16_bits(d))
+    sh = np.zeros(nsb, np.int64)
+    for ib in range(8):
+        sh |= (l[:, ib] >> 4) << (2 * ib)
+    _put16(out, 2, sh.astype(np.uint16))
+    for ib in range(0, 8, 2):
+        out[:, 4 + ib // 2] = u8((l[:, ib] & 0xF) | ((l[:, ib + 1] & 0xF) << 4))
+    for i in range(8):
+        out[:, 8 + 16 * i:24 + 16 * i] = _pack_nibbles(L[:, 32 * i:32 * i + 16], L[:, 32 * i + 16:32 * i + 32])
+    return out.reshape(-1)
+
+
 FUNCS = {
     8: q8_0, 2: q4_0, 3: q4_1, 6: q5_0, 7: q5_1, 42: q2_0,
     10: q2_K, 11: q3_K, 12: lambda x, imx=None: q4_5_K(x, imx, 15), 13: lambda x, imx=None: q4_5_K(x, imx, 31),
-    14: q6_K,
+    14: q6_K, 20: iq4_nl, 23: iq4_xs,
 }
 
 

@@ -1,0 +1,20 @@
+// Device copies of the IQ lattice tables (built once per process, uploaded once per device).
+#pragma once
+
+#include <stdint.h>
+
+namespace spa {
+
+struct IqDeviceTable {
+    const uint8_t* grid;      // size x (8 or 4) coordinate values 2l+1
+    const int32_t* map;       // level index -> grid point, or -(offset+1) into nb
+    const uint16_t* nb;       // neighbour lists: count, then grid point indices
+    int size;
+};
+
+// 0 IQ2_XXS, 1 IQ2_XS, 2 IQ1_S/IQ1_M, 3 IQ2_S, 4 IQ3_XXS, 5 IQ3_S; -1 otherwise
+int iq_table_index(int ggml_type);
+// the tables of `idx` on the current device (uploads them on first use); 0 or an SPA_ERR_* code
+int iq_device_table(int idx, IqDeviceTable* out);
+
+}  // namespace spa

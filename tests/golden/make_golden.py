@@ -94,10 +94,19 @@ def make_full(path):
     return man
 
 
+def make_iqtables_digests(path, src="/root/reference/seedpack/ggml/iqtables.npz"):
+    """SHA-256 of every array of the reference's IQ table fixture (grids, maps, neighbour lists)"""
+    tb = np.load(src)
+    man = {k: {"sha256": hashlib.sha256(tb[k].tobytes()).hexdigest(), "dtype": str(tb[k].dtype), "n": int(tb[k].size)}
+           for k in sorted(tb.files)}
+    json.dump(man, open(path, "w"), indent=1)
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--full", action="store_true")
     a = ap.parse_args()
     make_small(os.path.join(HERE, "quant_small.npz"))
+    make_iqtables_digests(os.path.join(HERE, "iqtables_sha256.json"))
     if a.full:
         make_full(os.path.join(HERE, "quant_sha256.json"))

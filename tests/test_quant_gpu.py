@@ -16,7 +16,7 @@ from seedpack_amd.requant import QFUN, row_size
 pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HIP_TYPES = [8, 2, 3, 6, 7, 42, 10, 11, 12, 13, 14]
+HIP_TYPES = [8, 2, 3, 6, 7, 42, 10, 11, 12, 13, 14, 20, 23]
 
 
 def say(*a):
