@@ -109,8 +109,8 @@ int spa_quantize(int t, int variant, const void* src, int src_kind, int64_t nrow
     if ((reinterpret_cast<uintptr_t>(src) & 15u) || (reinterpret_cast<uintptr_t>(dst) & 1u))
         return fail(SPA_ERR_ARG, "spa_quantize: src must be 16-byte and dst 2-byte aligned");
     if (imatrix && (reinterpret_cast<uintptr_t>(imatrix) & 3u)) return fail(SPA_ERR_ARG, "spa_quantize: misaligned imatrix");
-    // IQ2_XXS, IQ2_XS, IQ1_S, IQ1_M assert an imatrix (ggml-quants.c:3300, :3478, :4514, :4698)
-    if (!imatrix && (t == 16 || t == 17 || t == 19 || t == 29))
+    // IQ2_XXS, IQ2_XS, IQ1_S assert an imatrix (ggml-quants.c:3303, :3481, :4528)
+    if (!imatrix && (t == 16 || t == 17 || t == 19))
         return fail(SPA_ERR_ASSERT, "spa_quantize: type %d requires an imatrix", t);
     spa::QuantArgs a{t, variant, src, src_kind, nrows, npr, imatrix, dst, (hipStream_t)stream};
     switch (t) {

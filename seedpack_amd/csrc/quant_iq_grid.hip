@@ -1,6 +1,931 @@
-// Grid i-quants (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M): not built yet.
+// Grid i-quants: IQ2_XXS, IQ2_XS, IQ2_S (8-dimensional lattice groups), IQ3_XXS, IQ3_S
+// (4-dimensional groups), IQ1_S, IQ1_M (8-dimensional ternary groups), bit-exact with
+// ggml-quants.c (cited per type).
+//
+// Mapping: one lane per sub-block (32 or 16 weights), G = 256/sub lanes per super-block, 256-lane
+// workgroups. Per workgroup the lattice codebook is copied to LDS; the level-index map and the
+// neighbour lists stay in global memory (43,692 x int32 and up to 1.4 M x uint16: L2-resident).
+// The super-block sum of squares (and IQ1_M's final scale refit) is one left-to-right float sum:
+// it is handed from lane to lane of the group by shuffles. Every sub-block search (trial scales,
+// lattice lookups, neighbour searches; IQ1: sorting and the exhaustive split search) runs in its own
+// lane. Lane 0 of each group packs the block from the per-lane results parked in LDS.
+#include "../../include/seedpack_amd.h"
+#include "common.h"
+#include "iq_tables.h"
 #include "launch.h"
+#include "search.h"
 
 namespace spa {
-int launch_iqgrid(const QuantArgs& a) { return fail(-2, "grid i-quant type %d not built yet", a.type); }
+namespace {
+
+constexpr int WG = 256;
+constexpr float FLT_BIG = 3.402823466e+38F;   // FLT_MAX
+
+// ---------------------------------------------------------------- shared helpers
+
+// sum of v[] over the G lanes of a group, lane 0's terms first: one left-to-right float sum
+template <int G, int N>
+__device__ __forceinline__ float group_sum(const float (&v)[N], int sub) {
+    float s = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        if (sub == g) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) s += v[i];
+        }
+        s = __shfl(s, g, G);
+    }
+    return s;
+}
+
+// grid point j's coordinate values (2l+1) from the LDS codebook
+template <int D>
+__device__ __forceinline__ void grid_point(const uint8_t* grid, int j, int (&q)[D]) {
+    if constexpr (D == 8) {
+        const uint2 v = reinterpret_cast<const uint2*>(grid)[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { q[i] = (v.x >> (8 * i)) & 0xff; q[4 + i] = (v.y >> (8 * i)) & 0xff; }
+    } else {
+        const uint32_t v = reinterpret_cast<const uint32_t*>(grid)[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = (v >> (8 * i)) & 0xff;
+    }
+}
+
+// iq2_find_best_neighbour / iq3_find_best_neighbour (ggml-quants.c:3271-3293, :3915-3937): among the
+// listed neighbours, the first with the smallest weighted squared error at `scale`; its levels go to
+// L[off..off+D). The list always holds at least one point.
+template <int D, int N>
+__device__ __forceinline__ int best_neighbour(const uint16_t* __restrict__ nb, const uint8_t* grid, const float (&xval)[N],
+                                              const float (&w)[N], int off, float scale, int (&L)[N]) {
+    const int n = nb[0];
+    float best_d2 = FLT_BIG;
+    int gi = nb[1];
+    for (int jj = 1; jj <= n; ++jj) {
+        const int j = nb[jj];
+        int q[D];
+        grid_point<D>(grid, j, q);
+        float d2 = 0;
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const float diff = scale * (float)q[i] - xval[off + i];
+            d2 += w[off + i] * diff * diff;
+        }
+        if (d2 < best_d2) { best_d2 = d2; gi = j; }
+    }
+    int q[D];
+    grid_point<D>(grid, gi, q);
+#pragma unroll
+    for (int i = 0; i < D; ++i) L[off + i] = (q[i] - 1) / 2;
+    return gi;
+}
+
+// |x| per group of 8 and the sign bits; with PARITY (IQ2_XXS, IQ2_XS, IQ3_XXS) an odd count of
+// negatives leaves the least important weight's sign flipped and keeps 7 bits
+// (ggml-quants.c:3336-3356); without it (IQ2_S, IQ3_S) all 8 bits are kept (:4222-4231)
+template <int N, bool PARITY>
+__device__ __forceinline__ void make_signs(const float (&x)[N], const float (&w)[N], float (&xval)[N], uint32_t (&sg)[N / 8]) {
+#pragma unroll
+    for (int k = 0; k < N / 8; ++k) {
+        int nflip = 0;
+        uint32_t s = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (x[8 * k + i] >= 0) xval[8 * k + i] = x[8 * k + i];
+            else { xval[8 * k + i] = -x[8 * k + i]; ++nflip; s |= 1u << i; }
+        }
+        if (PARITY && (nflip % 2)) {
+            int imin = 0;
+            float mn = w[8 * k] * x[8 * k] * x[8 * k];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) {
+                const float ax = w[8 * k + i] * x[8 * k + i] * x[8 * k + i];
+                if (ax < mn) { mn = ax; imin = i; }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (i == imin) xval[8 * k + i] = -xval[8 * k + i];
+            s ^= 1u << imin;
+        }
+        sg[k] = PARITY ? (s & 127) : s;
+    }
+}
+
+// level index of a lattice group (2 bits per coordinate for D = 8, 3 bits for D = 4)
+template <int D, int N>
+__device__ __forceinline__ int level_index(const int (&L)[N], int off) {
+    constexpr int B = D == 8 ? 2 : 3;
+    int u = 0;
+#pragma unroll
+    for (int i = 0; i < D; ++i) u |= L[off + i] << (B * i);
+    return u;
+}
+
+template <int N>
+__device__ __forceinline__ void sums_2l1(const float (&xval)[N], const float (&w)[N], const int (&L)[N], float& sumqx, float& sumq2) {
+    sumqx = 0; sumq2 = 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float q = (float)(2 * L[i] + 1);
+        sumqx += w[i] * xval[i] * q;
+        sumq2 += w[i] * q * q;
+    }
+}
+
+// ---------------------------------------------------------------- the lattice types (IQ2_*, IQ3_*)
+
+// Result of one sub-block. An empty sub-block (its early exit in the reference) writes no bytes:
+// gidx and signs stay zero and `empty` is set.
+struct SubOut {
+    float scale;
+    int shift;          // IQ1_S: +1 / -1; IQ1_M: sign combination 0..3
+    bool empty;
+    int gidx[8];        // grid point per lattice group
+    uint32_t signs[4];  // per 8 weights
+};
+
+// The trial search of IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S: trial scales id = (2 kMaxQ - 1 + is*step)/max,
+// levels by rounding, groups off the grid snapped to their best neighbour; the best trial's levels
+// are kept; then the groups that were off the grid (REFIT_ALL: every group) are requantized at the
+// best scale and the scale refitted (ggml-quants.c:3540-3616, :5176-5252, :4014-4086, :4250-4322).
+// SET_L_IN_REFIT: the refit writes the rounded levels before the map lookup (IQ2_XS, IQ2_S);
+// otherwise the levels come from the grid point (IQ3_*): the same values either way.
+template <int N, int D, int KMAXQ, int IS_LO, int IS_HI, bool ONGRID_INIT, bool REFIT_ALL, bool SET_L_IN_REFIT>
+__device__ __forceinline__ float lattice_search(const float (&xval)[N], const float (&w)[N], const float (&waux)[N],
+                                                float max, float step, const IqDeviceTable& tab, const uint8_t* grid,
+                                                int (&L)[N]) {
+    constexpr int NG = N / D;
+    bool on[NG];
+#pragma unroll
+    for (int k = 0; k < NG; ++k) on[k] = ONGRID_INIT;
+    float scale = max / (float)(2 * KMAXQ - 1);
+    float best = 0;
+    for (int is = IS_LO; is <= IS_HI; ++is) {
+        const float id = ((float)(2 * KMAXQ - 1) + (float)is * step) / max;
+        const float this_scale = 1 / id;
+        int La[N];
+        bool ona[NG];
+#pragma unroll
+        for (int k = 0; k < NG; ++k) {
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                const int l = nearest_int(0.5f * (id * xval[D * k + i] - 1));
+                La[D * k + i] = tmax(0, tmin(KMAXQ - 1, l));
+            }
+            const int gi = tab.map[level_index<D, N>(La, D * k)];
+            ona[k] = gi >= 0;
+            if (gi < 0) best_neighbour<D, N>(tab.nb - gi - 1, grid, xval, waux, D * k, this_scale, La);
+        }
+        float sumqx, sumq2;
+        sums_2l1<N>(xval, w, La, sumqx, sumq2);
+        if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+            scale = sumqx / sumq2;
+            best = scale * sumqx;
+#pragma unroll
+            for (int i = 0; i < N; ++i) L[i] = La[i];
+#pragma unroll
+            for (int k = 0; k < NG; ++k) on[k] = ona[k];
+        }
+    }
+    int n_off = 0;
+#pragma unroll
+    for (int k = 0; k < NG; ++k) n_off += on[k] ? 0 : 1;
+    if (n_off > 0 && scale > 0) {
+        const float id = 1 / scale;
+#pragma unroll
+        for (int k = 0; k < NG; ++k) {
+            if (!REFIT_ALL && on[k]) continue;
+            int lv[N];
+#pragma unroll
+            for (int i = 0; i < D; ++i) {
+                const int l = nearest_int(0.5f * (id * xval[D * k + i] - 1));
+                lv[D * k + i] = tmax(0, tmin(KMAXQ - 1, l));
+                if (SET_L_IN_REFIT) L[D * k + i] = lv[D * k + i];
+            }
+            const int gi = tab.map[level_index<D, N>(lv, D * k)];
+            if (gi < 0) {
+                best_neighbour<D, N>(tab.nb - gi - 1, grid, xval, waux, D * k, scale, L);
+            } else if (!SET_L_IN_REFIT) {
+#pragma unroll
+                for (int i = 0; i < D; ++i) L[D * k + i] = lv[D * k + i];
+            }
+        }
+        float sumqx, sumq2;
+        sums_2l1<N>(xval, w, L, sumqx, sumq2);
+        if (sumq2 > 0) scale = sumqx / sumq2;
+    }
+    return scale;
+}
+
+// IQ2_XXS -- quantize_row_iq2_xxs_impl (ggml-quants.c:3295-3471): 32-weight sub-blocks, 4 groups of 8
+__device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float (&w)[32], const IqDeviceTable& tab,
+                                              const uint8_t* grid) {
+    constexpr int KMAXQ = 3;
+    SubOut o{};
+    float waux[32], xval[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) waux[i] = sqrtf(w[i]);
+    uint32_t sg[4];
+    make_signs<32, true>(x, w, xval, sg);
+    float max = xval[0];
+#pragma unroll
+    for (int i = 1; i < 32; ++i) max = tmax(max, xval[i]);
+    o.empty = true;
+    if (max < GROUP_MAX_EPS) return o;
+    int L[32];
+    float scale = make_qp_quants<32>(KMAXQ + 1, xval, L, w);
+    const float eff_max = scale * KMAXQ;
+    if (eff_max <= 0) return o;
+    o.empty = false;
+    float best = 0;
+    for (int is = -6; is <= 6; ++is) {
+        const float id = ((float)(2 * KMAXQ - 1) + (float)is * 0.1f) / eff_max;
+        const float this_scale = 1 / id;
+        int La[32];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int l = nearest_int(0.5f * (id * xval[8 * k + i] - 1));
+                La[8 * k + i] = tmax(0, tmin(KMAXQ - 1, l));
+            }
+            const int gi = tab.map[level_index<8, 32>(La, 8 * k)];
+            if (gi < 0) best_neighbour<8, 32>(tab.nb - gi - 1, grid, xval, waux, 8 * k, this_scale, La);
+        }
+        float sumqx, sumq2;
+        sums_2l1<32>(xval, w, La, sumqx, sumq2);
+        if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+            scale = sumqx / sumq2;
+            best = scale * sumqx;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) L[i] = La[i];
+        }
+    }
+    if (scale > 0) {
+        // every group requantized at the best scale (ggml-quants.c:3411-3432)
+        const float id = 1 / scale;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            int lv[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int l = nearest_int(0.5f * (id * xval[8 * k + i] - 1));
+                lv[8 * k + i] = tmax(0, tmin(KMAXQ - 1, l));
+            }
+            const int gi = tab.map[level_index<8, 32>(lv, 8 * k)];
+            if (gi < 0) {
+                best_neighbour<8, 32>(tab.nb - gi - 1, grid, xval, waux, 8 * k, scale, L);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) L[8 * k + i] = lv[8 * k + i];
+            }
+        }
+        float sumqx, sumq2;
+        sums_2l1<32>(xval, w, L, sumqx, sumq2);
+        if (sumq2 > 0) scale = sumqx / sumq2;
+    }
+    if (scale < 0) {
+        scale = -scale;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sg[k] = (~sg[k]) & 127;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { o.gidx[k] = tab.map[level_index<8, 32>(L, 8 * k)]; o.signs[k] = sg[k]; }
+    o.scale = scale;
+    return o;
+}
+
+// IQ2_XS -- quantize_row_iq2_xs_impl (ggml-quants.c:3473-3651); IQ2_S -- quantize_row_iq2_s_impl
+// (:5114-5280): 16-weight sub-blocks, 2 lattice groups of 8
+template <bool XS>
+__device__ __forceinline__ SubOut iq2_16_sub(const float (&x)[16], const float (&w)[16], const IqDeviceTable& tab,
+                                             const uint8_t* grid) {
+    SubOut o{};
+    float waux[16], xval[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) waux[i] = sqrtf(w[i]);
+    uint32_t sg[2];
+    make_signs<16, XS>(x, w, xval, sg);
+    float max = xval[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) max = tmax(max, xval[i]);
+    o.empty = true;
+    if (max < (XS ? GROUP_MAX_EPS : 1e-8f)) return o;   // GROUP_MAX_EPS_IQ2_S = 1e-8f
+    o.empty = false;
+    int L[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) L[i] = 0;
+    float scale = lattice_search<16, 8, 3, -9, 9, true, false, true>(xval, w, waux, max, 0.1f, tab, grid, L);
+    if (scale < 0) {
+        scale = -scale;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) sg[k] = XS ? ((~sg[k]) & 127) : ((~sg[k]) & 255);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) { o.gidx[k] = tab.map[level_index<8, 16>(L, 8 * k)]; o.signs[k] = sg[k]; }
+    o.scale = scale;
+    return o;
+}
+
+// IQ3_XXS -- quantize_row_iq3_xxs_impl(256) (ggml-quants.c:3939-4151); IQ3_S -- quantize_row_iq3_s_impl
+// (:4170-4353): 32-weight sub-blocks, 8 lattice groups of 4
+template <bool XXS>
+__device__ __forceinline__ SubOut iq3_sub(const float (&x)[32], const float (&w)[32], const IqDeviceTable& tab,
+                                          const uint8_t* grid) {
+    SubOut o{};
+    float waux[32], xval[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) waux[i] = sqrtf(w[i]);
+    uint32_t sg[4];
+    make_signs<32, XXS>(x, w, xval, sg);
+    float max = xval[0];
+#pragma unroll
+    for (int i = 1; i < 32; ++i) max = tmax(max, xval[i]);
+    o.empty = true;
+    if (XXS ? (max < 1e-8f) : (max == 0.f)) return o;   // GROUP_MAX_EPS_IQ3_XXS = 1e-8f; IQ3_S: !max
+    o.empty = false;
+    int L[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) L[i] = 0;
+    float scale;
+    if constexpr (XXS) scale = lattice_search<32, 4, 8, -15, 15, true, false, false>(xval, w, waux, max, 0.2f, tab, grid, L);
+    else scale = lattice_search<32, 4, 8, -9, 9, false, true, false>(xval, w, waux, max, 0.2f, tab, grid, L);
+    if (scale < 0) {
+        scale = -scale;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sg[k] = XXS ? ((~sg[k]) & 127) : ((~sg[k]) & 255);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o.gidx[k] = tab.map[level_index<4, 32>(L, 4 * k)];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o.signs[k] = sg[k];
+    o.scale = scale;
+    return o;
+}
+
+// ---------------------------------------------------------------- IQ1_S / IQ1_M
+
+// Ascending order of (x, original index): a bitonic network on the composite key. This is the order
+// of a stable sort by x, which is what glibc's qsort (a merge sort) gives the reference
+// (ggml-quants.c:4567, :4761); -0 and +0 compare equal. w travels with its x.
+template <int N>
+__device__ __forceinline__ void sort_pairs(float (&x)[N], int (&ix)[N], float (&w)[N]) {
+#pragma unroll
+    for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const bool up = (i & k) == 0;
+                    const bool gt = x[i] > x[l] || (x[i] == x[l] && ix[i] > ix[l]);
+                    if (gt == up) {
+                        const float tx = x[i]; x[i] = x[l]; x[l] = tx;
+                        const int ti = ix[i]; ix[i] = ix[l]; ix[l] = ti;
+                        const float tw = w[i]; w[i] = w[l]; w[l] = tw;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// level (0, 1, 2) of every weight from the split points b1 <= b2 of the sorted order: weight i's
+// position in the stable order is the count of weights before it
+template <int N>
+__device__ __forceinline__ void split_levels(const float (&x)[N], int b1, int b2, int (&L)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        int rank = 0;
+#pragma unroll
+        for (int j = 0; j < N; ++j) rank += (x[j] < x[i] || (x[j] == x[i] && j < i)) ? 1 : 0;
+        L[i] = rank < b1 ? 0 : (rank < b2 ? 1 : 2);
+    }
+}
+
+constexpr float IQ1S_DELTA = 0.125f;    // ggml-common.h IQ1S_DELTA
+constexpr float IQ1M_DELTA = 0.125f;    // ggml-common.h IQ1M_DELTA
+
+__device__ __forceinline__ float pick3(int lv, float a, float b, float c) { return lv == 0 ? a : (lv == 1 ? b : c); }
+
+// iq1_find_best_neighbour2 (ggml-quants.c:4444-4499) over the listed neighbours, distance with the
+// level values g0, g1, g2. The reference scans the whole grid when no listed point gives a distance
+// below FLT_MAX and aborts if that scan finds none; with finite inputs a listed point always wins.
+__device__ __forceinline__ int iq1_neighbour(const uint16_t* __restrict__ nb, const uint8_t* grid, const float (&xv)[8],
+                                             const float (&wv)[8], float scale, float g0, float g1, float g2, int (&Lg)[8]) {
+    const int n = nb[0];
+    float best = FLT_BIG;
+    int gi = nb[1];
+    for (int jj = 1; jj <= n; ++jj) {
+        const int j = nb[jj];
+        int q[8];
+        grid_point<8>(grid, j, q);
+        float d2 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float diff = scale * pick3((q[i] - 1) / 2, g0, g1, g2) - xv[i];
+            d2 += wv[i] * diff * diff;
+        }
+        if (d2 < best) { best = d2; gi = j; }
+    }
+    int q[8];
+    grid_point<8>(grid, gi, q);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) Lg[i] = (q[i] - 1) / 2;
+    return gi;
+}
+
+// snap the groups of 8 to the grid, then refit the scale if any group was off the grid
+// (ggml-quants.c:4602-4629 for IQ1_S, :4824-4852 for IQ1_M, where each group has its own signs)
+template <int N>
+__device__ __forceinline__ float iq1_snap(const float (&x)[N], const float (&w)[N], int (&L)[N], float scale, const bool (&pos)[N / 8],
+                                          const IqDeviceTable& tab, const uint8_t* grid, int (&gidx)[8]) {
+    constexpr float XP0 = -1 + IQ1S_DELTA, XP1 = IQ1S_DELTA, XP2 = 1 + IQ1S_DELTA;
+    constexpr float XM0 = -1 - IQ1S_DELTA, XM1 = -IQ1S_DELTA, XM2 = 1 - IQ1S_DELTA;
+    bool all_on = true;
+#pragma unroll
+    for (int k = 0; k < N / 8; ++k) {
+        int gi = tab.map[level_index<8, N>(L, 8 * k)];
+        if (gi < 0) {
+            all_on = false;
+            float xv[8], wv[8];
+            int Lg[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { xv[i] = x[8 * k + i]; wv[i] = w[8 * k + i]; }
+            gi = pos[k] ? iq1_neighbour(tab.nb - gi - 1, grid, xv, wv, scale, XP0, XP1, XP2, Lg)
+                        : iq1_neighbour(tab.nb - gi - 1, grid, xv, wv, scale, XM0, XM1, XM2, Lg);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) L[8 * k + i] = Lg[i];
+        }
+        gidx[k] = gi;
+    }
+    if (!all_on) {
+        float sumqx = 0, sumq2 = 0;
+#pragma unroll
+        for (int k = 0; k < N / 8; ++k) {
+            int q[8];
+            grid_point<8>(grid, gidx[k], q);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int lv = (q[j] - 1) / 2;
+                const float qq = pos[k] ? pick3(lv, XP0, XP1, XP2) : pick3(lv, XM0, XM1, XM2);
+                sumqx += w[8 * k + j] * qq * x[8 * k + j];
+                sumq2 += w[8 * k + j] * qq * qq;
+            }
+        }
+        if (sumqx > 0 && sumq2 > 0) scale = sumqx / sumq2;
+    }
+    return scale;
+}
+
+// IQ1_S sub-block of 32 -- quantize_row_iq1_s_impl (ggml-quants.c:4509-4671)
+__device__ __forceinline__ SubOut iq1_s_sub(const float (&x)[32], const float (&w)[32], const IqDeviceTable& tab,
+                                            const uint8_t* grid) {
+    constexpr float XP0 = -1 + IQ1S_DELTA, XP1 = IQ1S_DELTA, XP2 = 1 + IQ1S_DELTA;
+    constexpr float XM0 = -1 - IQ1S_DELTA, XM1 = -IQ1S_DELTA, XM2 = 1 - IQ1S_DELTA;
+    SubOut o{};
+    o.empty = true;
+    o.shift = 1;
+    float max = fabsf(x[0]);
+#pragma unroll
+    for (int i = 1; i < 32; ++i) max = tmax(max, fabsf(x[i]));
+    if (max < 1e-12f) return o;   // GROUP_MAX_EPS_IQ1_S
+    float sx[32], sw[32];
+    int si[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) { sx[i] = x[i]; si[i] = i; sw[i] = w[i]; }
+    sort_pairs<32>(sx, si, sw);
+    float sumx[33], sumw[33];
+    sumx[0] = sumw[0] = 0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) { sumx[j + 1] = sumx[j] + sw[j] * sx[j]; sumw[j + 1] = sumw[j] + sw[j]; }
+    float best_score = -FLT_BIG, scale = max;
+    int b1 = -1, b2 = -1, best_shift = 0;
+    // every split i1 <= i2 in the reference's order; i1 is the same in every lane, so the prefix
+    // sums at i1 are picked once per i1 and the inner loop indexes registers by constants
+    for (int i1 = 0; i1 <= 32; ++i1) {
+        float x1 = 0, w1 = 0;
+#pragma unroll
+        for (int t = 0; t <= 32; ++t)
+            if (t == i1) { x1 = sumx[t]; w1 = sumw[t]; }
+#pragma unroll
+        for (int i2 = 0; i2 <= 32; ++i2) {
+            if (i2 < i1) continue;
+            float sumqx = (x1 - sumx[0]) * XP0 + (sumx[i2] - x1) * XP1 + (sumx[32] - sumx[i2]) * XP2;
+            float sumq2 = (w1 - sumw[0]) * XP0 * XP0 + (sumw[i2] - w1) * XP1 * XP1 + (sumw[32] - sumw[i2]) * XP2 * XP2;
+            if (sumq2 > 0 && sumqx * sumqx > best_score * sumq2) {
+                scale = sumqx / sumq2; best_score = scale * sumqx; b1 = i1; b2 = i2; best_shift = 1;
+            }
+            sumqx = (x1 - sumx[0]) * XM0 + (sumx[i2] - x1) * XM1 + (sumx[32] - sumx[i2]) * XM2;
+            sumq2 = (w1 - sumw[0]) * XM0 * XM0 + (sumw[i2] - w1) * XM1 * XM1 + (sumw[32] - sumw[i2]) * XM2 * XM2;
+            if (sumq2 > 0 && sumqx * sumqx > best_score * sumq2) {
+                scale = sumqx / sumq2; best_score = scale * sumqx; b1 = i1; b2 = i2; best_shift = -1;
+            }
+        }
+    }
+    if (b1 < 0 || b2 < 0 || best_shift == 0) return o;
+    o.empty = false;
+    int L[32];
+    split_levels<32>(x, b1, b2, L);
+    if (scale < 0) {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) L[j] = 2 - L[j];
+        scale = -scale;
+        best_shift = -best_shift;
+    }
+    const bool p = best_shift == 1;
+    const bool pos[4] = {p, p, p, p};
+    o.scale = iq1_snap<32>(x, w, L, scale, pos, tab, grid, o.gidx);
+    o.shift = best_shift;
+    return o;
+}
+
+// IQ1_M sub-block of 16 -- quantize_row_iq1_m_impl (ggml-quants.c:4693-4916); VARIANT 1 is the
+// earlier search that sums every split directly (variants/ggml-quants.pre-f95b0d9539.c:4773-4860)
+template <int VARIANT>
+__device__ __forceinline__ SubOut iq1_m_sub(const float (&x)[16], const float (&w)[16], const IqDeviceTable& tab,
+                                            const uint8_t* grid) {
+    constexpr float XP0 = -1 + IQ1M_DELTA, XP1 = IQ1M_DELTA, XP2 = 1 + IQ1M_DELTA;
+    constexpr float XM0 = -1 - IQ1M_DELTA, XM1 = -IQ1M_DELTA, XM2 = 1 - IQ1M_DELTA;
+    SubOut o{};
+    o.empty = true;
+    o.shift = 0;
+    float max = fabsf(x[0]);
+#pragma unroll
+    for (int i = 1; i < 16; ++i) max = tmax(max, fabsf(x[i]));
+    if (max < 1e-7f) return o;   // GROUP_MAX_EPS_IQ1_M
+    float sx[16], sw[16];
+    int si[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { sx[i] = x[i]; si[i] = i; sw[i] = w[i]; }
+    sort_pairs<16>(sx, si, sw);
+    float best_score = -FLT_BIG, scale = max;
+    int b1 = -1, b2 = -1, best_k = -1;
+    float sumqx[4], sumq2[4];
+    if constexpr (VARIANT == 0) {
+        // prefix sums per half of the sub-block (ggml-quants.c:4774-4820)
+        float px0[17], px1[17], pw0[17], pw1[17];
+        px0[0] = px1[0] = pw0[0] = pw1[0] = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const bool h1 = si[j] >= 8;
+            const float a = sw[j] * sx[j];
+            px0[j + 1] = h1 ? px0[j] : px0[j] + a;
+            px1[j + 1] = h1 ? px1[j] + a : px1[j];
+            pw0[j + 1] = h1 ? pw0[j] : pw0[j] + sw[j];
+            pw1[j + 1] = h1 ? pw1[j] + sw[j] : pw1[j];
+        }
+        const float tx0 = px0[16], tx1 = px1[16], tw0 = pw0[16], tw1 = pw1[16];
+        constexpr float P2 = XP2, M2 = XM2;
+        const float cp1 = XP0 * XP0 - XP1 * XP1, cp2 = XP1 * XP1 - XP2 * XP2;
+        const float cm1 = XM0 * XM0 - XM1 * XM1, cm2 = XM1 * XM1 - XM2 * XM2;
+        for (int i1 = 0; i1 <= 16; ++i1) {
+            float a0 = 0, a1 = 0, c0 = 0, c1 = 0;
+#pragma unroll
+            for (int t = 0; t <= 16; ++t)
+                if (t == i1) { a0 = px0[t]; a1 = px1[t]; c0 = pw0[t]; c1 = pw1[t]; }
+#pragma unroll
+            for (int i2 = 0; i2 <= 16; ++i2) {
+                if (i2 < i1) continue;
+                const float s0 = a0 + px0[i2], s1 = a1 + px1[i2];
+                const float qx_p0 = tx0 * P2 - s0, qx_m0 = tx0 * M2 - s0;
+                const float qx_p1 = tx1 * P2 - s1, qx_m1 = tx1 * M2 - s1;
+                const float q2_p0 = tw0 * P2 * P2 + c0 * cp1 + pw0[i2] * cp2;
+                const float q2_m0 = tw0 * M2 * M2 + c0 * cm1 + pw0[i2] * cm2;
+                const float q2_p1 = tw1 * P2 * P2 + c1 * cp1 + pw1[i2] * cp2;
+                const float q2_m1 = tw1 * M2 * M2 + c1 * cm1 + pw1[i2] * cm2;
+                sumqx[0] = qx_p0 + qx_p1; sumqx[1] = qx_p0 + qx_m1;
+                sumqx[2] = qx_m0 + qx_p1; sumqx[3] = qx_m0 + qx_m1;
+                sumq2[0] = q2_p0 + q2_p1; sumq2[1] = q2_p0 + q2_m1;
+                sumq2[2] = q2_m0 + q2_p1; sumq2[3] = q2_m0 + q2_m1;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (sumq2[k] > 0 && sumqx[k] * sumqx[k] > best_score * sumq2[k]) {
+                        scale = sumqx[k] / sumq2[k]; best_score = scale * sumqx[k];
+                        b1 = i1; b2 = i2; best_k = k;
+                    }
+                }
+            }
+        }
+    } else {
+        for (int i1 = 0; i1 <= 16; ++i1) {
+            for (int i2 = i1; i2 <= 16; ++i2) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) { sumqx[k] = 0; sumq2[k] = 0; }
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int lv = j < i1 ? 0 : (j < i2 ? 1 : 2);
+                    const float vp = pick3(lv, XP0, XP1, XP2), vm = pick3(lv, XM0, XM1, XM2);
+                    const float ap = sw[j] * vp * sx[j], am = sw[j] * vm * sx[j];
+                    const float bp = sw[j] * vp * vp, bm = sw[j] * vm * vm;
+                    if (si[j] < 8) {
+                        sumqx[0] += ap; sumqx[1] += ap; sumqx[2] += am; sumqx[3] += am;
+                        sumq2[0] += bp; sumq2[1] += bp; sumq2[2] += bm; sumq2[3] += bm;
+                    } else {
+                        sumqx[0] += ap; sumqx[2] += ap; sumqx[1] += am; sumqx[3] += am;
+                        sumq2[0] += bp; sumq2[2] += bp; sumq2[1] += bm; sumq2[3] += bm;
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (sumq2[k] > 0 && sumqx[k] * sumqx[k] > best_score * sumq2[k]) {
+                        scale = sumqx[k] / sumq2[k]; best_score = scale * sumqx[k];
+                        b1 = i1; b2 = i2; best_k = k;
+                    }
+                }
+            }
+        }
+    }
+    if (b1 < 0 || b2 < 0 || best_k < 0) return o;
+    o.empty = false;
+    int L[16];
+    split_levels<16>(x, b1, b2, L);
+    if (scale < 0) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) L[j] = 2 - L[j];
+        scale = -scale;
+        best_k = 3 - best_k;
+    }
+    const bool pos[2] = {best_k < 2, best_k % 2 == 0};
+    o.scale = iq1_snap<16>(x, w, L, scale, pos, tab, grid, o.gidx);
+    o.shift = best_k;
+    return o;
+}
+
+// ---------------------------------------------------------------- kernels
+
+// per-lane results parked for the packing lane
+struct Park {
+    float scale;
+    int l;              // sub-block scale code
+    int shift;
+    int empty;
+    int gidx[8];
+    uint32_t signs[4];
+};
+
+enum Kind { K_IQ2_XXS, K_IQ2_XS, K_IQ2_S, K_IQ3_XXS, K_IQ3_S, K_IQ1_S, K_IQ1_M0, K_IQ1_M1 };
+
+// N: sub-block; BS: block bytes; GBYTES: codebook bytes; TWO: sigma2 = 2 sumx2 / 256 (else sumx2 / 256)
+template <int K> struct Cfg;
+template <> struct Cfg<K_IQ2_XXS> { static constexpr int N = 32, BS = 66, GBYTES = 256 * 8; static constexpr bool TWO = false; };
+template <> struct Cfg<K_IQ2_XS> { static constexpr int N = 16, BS = 74, GBYTES = 512 * 8; static constexpr bool TWO = false; };
+template <> struct Cfg<K_IQ2_S> { static constexpr int N = 16, BS = 82, GBYTES = 1024 * 8; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ3_XXS> { static constexpr int N = 32, BS = 98, GBYTES = 256 * 4; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ3_S> { static constexpr int N = 32, BS = 110, GBYTES = 512 * 4; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ1_S> { static constexpr int N = 32, BS = 50, GBYTES = 2048 * 8; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ1_M0> { static constexpr int N = 16, BS = 56, GBYTES = 2048 * 8; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ1_M1> { static constexpr int N = 16, BS = 56, GBYTES = 2048 * 8; static constexpr bool TWO = true; };
+
+template <int K>
+__global__ __launch_bounds__(WG) void k_iqgrid(const void* __restrict__ src, int kind, uint8_t* __restrict__ dst, int64_t nsb,
+                                               int64_t sbpr, const float* __restrict__ imx, IqDeviceTable tab) {
+    using C = Cfg<K>;
+    constexpr int N = C::N, G = 256 / N, SBW = WG / G;
+    constexpr bool IQ1 = K == K_IQ1_S || K == K_IQ1_M0 || K == K_IQ1_M1;
+    __shared__ __align__(16) uint8_t grid[C::GBYTES];
+    __shared__ __align__(16) uint16_t otile[SBW * C::BS / 2];
+    __shared__ Park park[SBW][G];
+    for (int i = threadIdx.x; i < C::GBYTES / 16; i += WG)
+        reinterpret_cast<uint4*>(grid)[i] = reinterpret_cast<const uint4*>(tab.grid)[i];
+    __syncthreads();
+    const int lsb = threadIdx.x / G, sub = threadIdx.x % G;
+    const int64_t sb0 = (int64_t)blockIdx.x * SBW;
+    const int64_t sb = sb0 + lsb;
+    const bool active = sb < nsb;
+    const int64_t sbc = active ? sb : nsb - 1;
+    float x[N];
+    load_weights<N>(src, kind, sbc * 256 + sub * N, x);
+    float sq[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) sq[i] = x[i] * x[i];
+    const float sumx2 = group_sum<G, N>(sq, sub);
+    const float sigma2 = C::TWO ? 2 * sumx2 / 256 : sumx2 / 256;
+    float w[N];
+    if (imx) {
+        const float* qw = imx + (sbc % sbpr) * 256 + sub * N;
+#pragma unroll
+        for (int i = 0; i < N; ++i) w[i] = qw[i] * sqrtf(sigma2 + x[i] * x[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) w[i] = K == K_IQ2_S ? 0.25f * sigma2 + x[i] * x[i] : x[i] * x[i];
+    }
+    SubOut r;
+    if constexpr (K == K_IQ2_XXS) r = iq2_xxs_sub(x, w, tab, grid);
+    else if constexpr (K == K_IQ2_XS) r = iq2_16_sub<true>(x, w, tab, grid);
+    else if constexpr (K == K_IQ2_S) r = iq2_16_sub<false>(x, w, tab, grid);
+    else if constexpr (K == K_IQ3_XXS) r = iq3_sub<true>(x, w, tab, grid);
+    else if constexpr (K == K_IQ3_S) r = iq3_sub<false>(x, w, tab, grid);
+    else if constexpr (K == K_IQ1_S) r = iq1_s_sub(x, w, tab, grid);
+    else r = iq1_m_sub<K == K_IQ1_M1 ? 1 : 0>(x, w, tab, grid);
+    // super-block scale: MAX over the sub-block scales in sub-block order (empty ones count as 0)
+    const float s_own = r.empty ? 0.f : r.scale;
+    float max_scale = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) max_scale = tmax(max_scale, __shfl(s_own, g, G));
+    const bool nz = max_scale != 0.f;   // the reference's `if (!max_scale)` exit
+    constexpr float DIV = IQ1 ? 15.f : 31.f;
+    constexpr int LMAX = IQ1 ? 7 : 15;
+    const float d = max_scale / DIV;
+    int l = 0;
+    if (nz) {
+        const float id = 1 / d;
+        l = tmax(0, tmin(LMAX, nearest_int(0.5f * (id * s_own - 1))));
+    }
+    float dfinal = d;
+    if constexpr (K == K_IQ1_M0 || K == K_IQ1_M1) {
+        // refit of the super-scale over all 256 weights in order, empty sub-blocks included as grid
+        // point 0 with signs (+, +) (ggml-quants.c:4884-4910)
+        constexpr float XP0 = -1 + IQ1M_DELTA, XP1 = IQ1M_DELTA, XP2 = 1 + IQ1M_DELTA;
+        constexpr float XM0 = -1 - IQ1M_DELTA, XM1 = -IQ1M_DELTA, XM2 = 1 - IQ1M_DELTA;
+        float aqx[16], aq2[16];
+        const int shift = r.empty ? 0 : r.shift;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const bool p = k == 0 ? shift < 2 : shift % 2 == 0;
+            int q[8];
+            grid_point<8>(grid, r.empty ? 0 : r.gidx[k], q);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int lv = (q[j] - 1) / 2;
+                const float qq = (p ? pick3(lv, XP0, XP1, XP2) : pick3(lv, XM0, XM1, XM2)) * (float)(2 * l + 1);
+                aqx[8 * k + j] = w[8 * k + j] * qq * x[8 * k + j];
+                aq2[8 * k + j] = w[8 * k + j] * qq * qq;
+            }
+        }
+        float sqx = 0.f, sq2 = 0.f;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if (sub == g) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) { sqx += aqx[i]; sq2 += aq2[i]; }
+            }
+            sqx = __shfl(sqx, g, G);
+            sq2 = __shfl(sq2, g, G);
+        }
+        if (sq2 > 0) dfinal = sqx / sq2;
+    }
+    Park pk;
+    pk.scale = s_own;
+    pk.l = l;
+    pk.shift = r.empty ? (K == K_IQ1_S ? 1 : 0) : r.shift;
+    pk.empty = r.empty ? 1 : 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) pk.gidx[k] = r.empty ? 0 : r.gidx[k];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pk.signs[k] = r.empty ? 0u : r.signs[k];
+    park[lsb][sub] = pk;
+    __syncthreads();
+    if (active && sub == 0) {
+        TileOut o{otile + lsb * (C::BS / 2)};
+        const Park* P = park[lsb];
+        for (int j = 0; j < C::BS; j += 2) o.put16(j, 0);
+        if constexpr (K == K_IQ2_XXS) {
+            // d, then per 32 weights: u32 of 4 grid indices, u32 of 4 x 7 sign bits | scale << 28
+            if (nz) {
+                o.put16(0, f32_to_f16(d));
+                for (int ib = 0; ib < 8; ++ib) {
+                    const uint32_t a = (uint32_t)P[ib].gidx[0] | ((uint32_t)P[ib].gidx[1] << 8) |
+                                       ((uint32_t)P[ib].gidx[2] << 16) | ((uint32_t)P[ib].gidx[3] << 24);
+                    const uint32_t b = P[ib].signs[0] | (P[ib].signs[1] << 7) | (P[ib].signs[2] << 14) |
+                                       (P[ib].signs[3] << 21) | ((uint32_t)P[ib].l << 28);
+                    o.put16(2 + 8 * ib, a & 0xffff); o.put16(4 + 8 * ib, a >> 16);
+                    o.put16(6 + 8 * ib, b & 0xffff); o.put16(8 + 8 * ib, b >> 16);
+                }
+            }
+        } else if constexpr (K == K_IQ2_XS) {
+            // d, per 16 weights two u16 (9-bit grid index | 7 sign bits << 9), scale nibbles
+            if (nz) {
+                o.put16(0, f32_to_f16(d));
+                for (int ib = 0; ib < 16; ++ib)
+                    for (int k = 0; k < 2; ++k) o.put16(2 + 4 * ib + 2 * k, (uint32_t)P[ib].gidx[k] | (P[ib].signs[k] << 9));
+                for (int ib = 0; ib < 16; ib += 4)
+                    o.put2(66 + ib / 2, P[ib].l | (P[ib + 1].l << 4), P[ib + 2].l | (P[ib + 3].l << 4));
+            }
+        } else if constexpr (K == K_IQ2_S) {
+            // d, qs[32] grid low bytes, qs[32] signs, qh[8] (2 high bits per group), scales[8]
+            if (nz) o.put16(0, f32_to_f16(d * 0.9875f));
+            for (int ib = 0; ib < 16; ++ib) {
+                o.put2(2 + 2 * ib, P[ib].gidx[0] & 255, P[ib].gidx[1] & 255);
+                o.put2(34 + 2 * ib, P[ib].signs[0], P[ib].signs[1]);
+            }
+            for (int q = 0; q < 8; q += 2) {
+                uint32_t h[2] = {0, 0};
+                for (int t = 0; t < 2; ++t)
+                    for (int i8 = 4 * (q + t); i8 < 4 * (q + t) + 4; ++i8)
+                        h[t] |= (uint32_t)(P[i8 / 2].gidx[i8 % 2] >> 8) << (2 * (i8 % 4));
+                o.put2(66 + q, h[0], h[1]);
+            }
+            if (nz)
+                for (int ib = 0; ib < 16; ib += 4)
+                    o.put2(74 + ib / 2, P[ib].l | (P[ib + 1].l << 4), P[ib + 2].l | (P[ib + 3].l << 4));
+        } else if constexpr (K == K_IQ3_XXS) {
+            // d, 64 grid indices, per 32 weights u32 of 4 x 7 sign bits | scale << 28
+            if (nz) {
+                o.put16(0, f32_to_f16(d * 1.0125f));
+                for (int ib = 0; ib < 8; ++ib)
+                    for (int k = 0; k < 8; k += 2) o.put2(2 + 8 * ib + k, P[ib].gidx[k], P[ib].gidx[k + 1]);
+                for (int ib = 0; ib < 8; ++ib) {
+                    const uint32_t v = P[ib].signs[0] | (P[ib].signs[1] << 7) | (P[ib].signs[2] << 14) |
+                                       (P[ib].signs[3] << 21) | ((uint32_t)P[ib].l << 28);
+                    o.put16(66 + 4 * ib, v & 0xffff);
+                    o.put16(68 + 4 * ib, v >> 16);
+                }
+            }
+        } else if constexpr (K == K_IQ3_S) {
+            // d, qs[64], qh[8], signs[32], scales[4]. The reference advances its qs and signs cursors
+            // only past sub-blocks that were not empty (ggml-quants.c:4336-4339 sit after the
+            // `continue` of :4237), so later sub-blocks land in the earlier free slots; qh is indexed
+            // by position.
+            if (nz) o.put16(0, f32_to_f16(d * 1.033f));
+            int slot = 0;
+            for (int ib = 0; ib < 8; ++ib) {
+                if (P[ib].empty) continue;
+                for (int k = 0; k < 8; k += 2) o.put2(2 + 8 * slot + k, P[ib].gidx[k] & 255, P[ib].gidx[k + 1] & 255);
+                for (int k = 0; k < 4; k += 2) o.put2(74 + 4 * slot + k, P[ib].signs[k], P[ib].signs[k + 1]);
+                ++slot;
+            }
+            for (int ib = 0; ib < 8; ib += 2) {
+                uint32_t h[2] = {0, 0};
+                for (int t = 0; t < 2; ++t)
+                    for (int k = 0; k < 8; ++k) h[t] |= (uint32_t)(P[ib + t].gidx[k] >> 8) << k;
+                o.put2(66 + ib, h[0], h[1]);
+            }
+            if (nz)
+                for (int ib = 0; ib < 8; ib += 4)
+                    o.put2(106 + ib / 2, P[ib].l | (P[ib + 1].l << 4), P[ib + 2].l | (P[ib + 3].l << 4));
+        } else if constexpr (K == K_IQ1_S) {
+            // d, qs[32] grid low bytes, qh[8] u16: 3 high bits per group | (scale | 8 if shift -1) << 12
+            if (nz) o.put16(0, f32_to_f16(d * 1.125f));
+            for (int ib = 0; ib < 8; ++ib)
+                for (int k = 0; k < 4; k += 2) o.put2(2 + 4 * ib + k, P[ib].gidx[k] & 255, P[ib].gidx[k + 1] & 255);
+            for (int ib = 0; ib < 8; ++ib) {
+                uint32_t h = 0;
+                for (int k = 0; k < 4; ++k) h |= (uint32_t)(P[ib].gidx[k] >> 8) << (3 * k);
+                if (nz) h |= (uint32_t)(P[ib].l | (P[ib].shift == -1 ? 8 : 0)) << 12;
+                o.put16(34 + 2 * ib, h);
+            }
+        } else {
+            // IQ1_M: qs[32], qh[16] (3 high bits per group, sign masks), scales: 3-bit codes and the
+            // f16 super-scale in the top nibbles
+            for (int ib = 0; ib < 16; ++ib) o.put2(2 * ib, P[ib].gidx[0] & 255, P[ib].gidx[1] & 255);
+            const uint32_t masks[4] = {0x00, 0x80, 0x08, 0x88};
+            for (int ib = 0; ib < 16; ib += 2) {
+                uint32_t h[2];
+                for (int t = 0; t < 2; ++t)
+                    h[t] = (uint32_t)((P[ib + t].gidx[0] >> 8) | ((P[ib + t].gidx[1] >> 8) << 4)) |
+                           (nz ? masks[P[ib + t].shift & 3] : 0u);
+                o.put2(32 + ib, h[0], h[1]);
+            }
+            if (nz) {
+                const uint32_t s16 = f32_to_f16(dfinal * 1.1125f);
+                uint32_t sc[4] = {0, 0, 0, 0};
+                for (int ib = 0; ib < 16; ++ib) sc[ib / 4] |= (uint32_t)P[ib].l << (3 * (ib % 4));
+                sc[0] |= (s16 & 0x000f) << 12;
+                sc[1] |= (s16 & 0x00f0) << 8;
+                sc[2] |= (s16 & 0x0f00) << 4;
+                sc[3] |= (s16 & 0xf000);
+                for (int i = 0; i < 4; ++i) o.put16(48 + 2 * i, sc[i] & 0xffff);
+            }
+        }
+    }
+    __syncthreads();
+    const int nb = (int)(nsb - sb0 < SBW ? nsb - sb0 : SBW);
+    store_tile(otile, dst + sb0 * C::BS, nb * C::BS);
+}
+
+template <int K>
+int run(const QuantArgs& a, int table) {
+    IqDeviceTable tab;
+    if (int e = iq_device_table(table, &tab)) return e;
+    constexpr int D = (K == K_IQ3_XXS || K == K_IQ3_S) ? 4 : 8;
+    if ((int64_t)tab.size * D != Cfg<K>::GBYTES)
+        return fail(SPA_ERR_ASSERT, "grid i-quant type %d: codebook of %d points does not fit the kernel", a.type, tab.size);
+    if (a.n_per_row % 256) return fail(SPA_ERR_ARG, "grid i-quant type %d: n_per_row %% 256", a.type);
+    const int64_t nsb = a.nrows * a.n_per_row / 256;
+    if (nsb == 0) return 0;
+    constexpr int SBW = WG / (256 / Cfg<K>::N);
+    hipLaunchKernelGGL(k_iqgrid<K>, dim3((unsigned)((nsb + SBW - 1) / SBW)), dim3(WG), 0, a.stream, a.src, a.src_kind,
+                       (uint8_t*)a.dst, nsb, a.n_per_row / 256, a.imatrix, tab);
+    SPA_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+}  // namespace
+
+int launch_iqgrid(const QuantArgs& a) {
+    const int t = iq_table_index(a.type);
+    switch (a.type) {
+        case 16: return run<K_IQ2_XXS>(a, t);
+        case 17: return run<K_IQ2_XS>(a, t);
+        case 22: return run<K_IQ2_S>(a, t);
+        case 18: return run<K_IQ3_XXS>(a, t);
+        case 21: return run<K_IQ3_S>(a, t);
+        case 19: return run<K_IQ1_S>(a, t);
+        case 29: return a.variant == 1 ? run<K_IQ1_M1>(a, t) : run<K_IQ1_M0>(a, t);
+    }
+    return fail(SPA_ERR_TYPE, "launch_iqgrid: type %d", a.type);
+}
+
 }  // namespace spa

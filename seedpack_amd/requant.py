@@ -14,8 +14,8 @@ QFUN = {2: ("quantize_q4_0", 32, 18), 3: ("quantize_q4_1", 32, 20), 6: ("quantiz
 NAMES = {t: f[len("quantize_"):].upper() for t, (f, _, _) in QFUN.items()}
 BY_NAME = {v: k for k, v in NAMES.items()}
 
-# types whose quantizer asserts an imatrix (ggml-quants.c:3300, :3478, :4514, :4698)
-NEED_IMATRIX = {16, 17, 19, 29}
+# types whose quantizer asserts an imatrix (ggml-quants.c:3303, :3481, :4528)
+NEED_IMATRIX = {16, 17, 19}
 
 # quantizer variants per type (seedpack/gpuquant.py:182-185): IQ1_M also has the pre-f95b0d9539 search
 VARIANTS = {29: 2}

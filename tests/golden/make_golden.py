@@ -24,7 +24,7 @@ from oracle import ref  # noqa: E402
 from seedpack_amd import synth  # noqa: E402
 
 TYPES = sorted(ref.QFUN)
-NEED_IMX = {16, 17, 19, 29}
+NEED_IMX = {16, 17, 19}           # GGML_ASSERT(quant_weights) in ggml-quants.c:3303, :3481, :4528
 
 
 def small_inputs():
@@ -72,7 +72,8 @@ def make_small(path):
 
 
 # full-size tensors whose reference bytes are pinned by digest: (config, tensor index, types)
-FULL = [(1, 0, [8, 2]), (2, 1, [10, 11, 12, 13, 14]), (2, 0, [10, 11, 12, 13, 14])]
+FULL = [(1, 0, [8, 2]), (2, 1, [10, 11, 12, 13, 14]), (2, 0, [10, 11, 12, 13, 14]),
+        (3, 0, [23, 18, 17, 16, 19, 29]), (3, 1, [23, 18, 17, 16, 19, 29])]
 
 
 def make_full(path):
