@@ -252,8 +252,9 @@ def make_qp_quants(X, nmax, QW):
             up = mse < best
             best = np.where(up, mse, best).astype(F)
             iscale = np.where(up, isc, iscale).astype(F)
-        L = u8(np.minimum(nmax, nearest_int(iscale[:, None] * X)))
-        Lf = L.astype(F)
+        lint = np.minimum(nmax, nearest_int(iscale[:, None] * X))
+        L = u8(lint)
+        Lf = lint.astype(F)        # the sums take the int level (:1120-1121); only L wraps
         sumlx = seqsum(QW * X * Lf)
         suml2 = seqsum(QW * Lf * Lf)
         active = np.ones(R, bool)

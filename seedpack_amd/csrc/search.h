@@ -278,7 +278,7 @@ __device__ __forceinline__ float make_qp_quants(int nmax, const float (&x)[N], i
         int l = nearest_int(iscale * x[i]);
         l = tmin(nmax, l);
         L[i] = l & 0xff;
-        const float fl = (float)L[i];
+        const float fl = (float)l;   // the sums take the int level; only L wraps (x < 0 in IQ2_XXS)
         sumlx += qw[i] * x[i] * fl;
         suml2 += qw[i] * fl * fl;
     }
