@@ -111,6 +111,84 @@ def profile_pass():
     log(f"profile: k_copy16 {nb} bytes x2 launches (reads {nb}, writes {nb})")
 
 
+def iquant_cfg3(stream, reps=2):
+    """configuration 3: the i-quants with the imatrix on the 4096x12288 and 12288x4096 Student-t tensors,
+    each type launched once untimed, then `reps` times between HIP events on the bench stream"""
+    from seedpack_amd import device as dev
+    from seedpack_amd import synth
+    from seedpack_amd.gpuquant import quantize_into
+    from seedpack_amd.requant import NAMES, row_size
+    res = {}
+    for ti in (0, 1):
+        w, imx = synth.tensor(3, ti)
+        src = dev.DeviceArray.from_host(w.reshape(-1), stream.handle)
+        dimx = dev.DeviceArray.from_host(imx, stream.handle)
+        for t in synth.TYPES[3]:
+            out = dev.DeviceArray(w.shape[0] * row_size(t, w.shape[1]), np.uint8)
+            quantize_into(t, src, w.shape[1], out, dimx, 0, stream.handle)
+            e0, e1 = dev.Event(), dev.Event()
+            e0.record(stream.handle)
+            for _ in range(reps):
+                quantize_into(t, src, w.shape[1], out, dimx, 0, stream.handle)
+            e1.record(stream.handle)
+            ms = e0.elapsed_ms(e1) / reps
+            key = NAMES[t]
+            ent = res.setdefault(key, {"ms": 0.0, "bf16_bytes": 0})
+            ent["ms"] += ms
+            ent["bf16_bytes"] += 2 * w.size
+            log(f"bench: cfg3 {NAMES[t]} t{ti} {w.shape[0]}x{w.shape[1]}: {ms:.3f} ms/launch")
+            del out
+        del src, dimx
+    for k, e in res.items():
+        e["GB_s"] = round(e["bf16_bytes"] / (e["ms"] / 1e3) / 1e9, 2)
+        e["ms"] = round(e["ms"], 3)
+    return res
+
+
+def qr_cfg1(stream, reps=3):
+    """configuration 1 residual coding: Q8_0 / Q4_0 of the 3072x1024 tensor as the prediction, the file
+    is that with 1% of its blocks perturbed (one byte each); QR encode (histogram, tables, coding, gather)
+    and decode, inputs resident on the device, wall time per call including the host table step"""
+    from seedpack_amd import device as dev
+    from seedpack_amd import qr, synth
+    from seedpack_amd.gpuquant import quantize_into
+    from seedpack_amd.requant import NAMES, row_size
+    w, _ = synth.tensor(1, 0)
+    sd = dev.DeviceArray.from_host(w.reshape(-1).view(np.uint8), stream.handle)
+    src = dev.DeviceArray.from_host(w.reshape(-1), stream.handle)
+    res = {}
+    for t in (8, 2):
+        P = dev.DeviceArray(w.shape[0] * row_size(t, w.shape[1]), np.uint8)
+        quantize_into(t, src, w.shape[1], P, None, 0, stream.handle)
+        Ph = P.to_host(stream=stream.handle)
+        g = np.random.Generator(np.random.PCG64(1234 + t))
+        Fb = Ph.copy().reshape(-1, qr.BS[t])
+        idx = g.choice(len(Fb), size=len(Fb) // 100, replace=False)
+        Fb[idx, g.integers(0, qr.BS[t], len(idx))] ^= np.uint8(0x10)
+        F = dev.DeviceArray.from_host(Fb.reshape(-1), stream.handle)
+        item = [(F, P, 0, 30, w.shape[1], -1)]
+        parts = qr.encode_parts(t, item, sd, stream=stream.handle)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            parts = qr.encode_parts(t, item, sd, stream=stream.handle)
+        enc = (time.perf_counter() - t0) / reps
+        args = (parts["freq"], parts["used"], parts["lens"], parts["stream"].tobytes(), [(P, 0, 30, w.shape[1], -1)], sd)
+        back = qr.decode_parts(t, *args, stream=stream.handle)
+        stream.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            back = qr.decode_parts(t, *args, stream=stream.handle)
+        stream.synchronize()
+        dec = (time.perf_counter() - t0) / reps
+        ok = back.to_host(stream=stream.handle)[:F.nbytes].tobytes() == Fb.tobytes()
+        res[NAMES[t]] = {"file_bytes": int(F.nbytes), "coded_bytes": int(len(parts["stream"])),
+                         "encode_ms": round(enc * 1e3, 3), "decode_ms": round(dec * 1e3, 3),
+                         "encode_GB_s_bf16": round(2 * w.size / enc / 1e9, 2),
+                         "decode_GB_s_bf16": round(2 * w.size / dec / 1e9, 2), "round_trip_ok": ok}
+        log(f"bench: qr cfg1 {NAMES[t]}: {res[NAMES[t]]}")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,6 +289,8 @@ def main():
             legacy[f"{NAMES[t]}_{name}"] = {"GB_s_bf16_in": round(2 * nw / (ms / 1e3) / 1e9, 1), "ms": round(ms, 4),
                                            "hbm_frac": round(alg_bytes(t, nw, shape[1], False) / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
 
+    iq = iquant_cfg3(stream)
+    qrb = qr_cfg1(stream)
     cpu = None if a.no_cpu else cpu_baseline(tensors)
     line = {"metric": "requant GB/s (BF16 in), K-quant family Q2_K..Q6_K with imatrix", "value": round(value, 3),
             "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 3),
@@ -218,7 +298,8 @@ def main():
             "data": "synthetic (seeded N(0,0.02) BF16, LogNormal(0,1) imatrix)",
             "config": {"workload": "cfg2: Q2_K,Q3_K,Q4_K,Q5_K,Q6_K (imatrix) on token_embd 151936x1024 + ffn_down 1024x3072",
                        "bf16_bytes_per_step": bf16_bytes, "launches_per_step": len(launches)},
-            "per_type": per_type, "legacy_hbm_types": legacy, "roofline": roofline, "cpu_baseline": cpu}
+            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "qr_cfg1": qrb,
+            "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
 
 
