@@ -37,6 +37,7 @@ extern "C" {
 const char* spa_last_error(void);
 int spa_device_count(int* n);
 int spa_set_device(int device);
+int spa_get_device(int* device);
 int spa_malloc(void** ptr, size_t nbytes);
 int spa_free(void* ptr);
 int spa_memcpy_h2d(void* dst, const void* src, size_t nbytes, void* stream);

@@ -26,9 +26,21 @@ NTAB2 = NTAB + 208
 FESC_LO, FESC_HI = 8, 9
 
 SELF_TYPES = (2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 20, 23, 42)
-BS = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 20: 18, 23: 136, 42: 18}
-QK = {t: (32 if t in (2, 3, 6, 7, 8, 20) else 64 if t == 42 else 256) for t in SELF_TYPES}
-NFIELD = {2: 1, 6: 1, 8: 1, 20: 1, 42: 1, 3: 2, 7: 2, 10: 34, 11: 17, 14: 17, 12: 18, 13: 18, 23: 9}
+GRID_TYPES = (16, 17, 18, 19, 21, 22, 29)
+BS = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 20: 18, 23: 136, 42: 18,
+      16: 66, 17: 74, 18: 98, 19: 50, 21: 110, 22: 82, 29: 56}
+QK = {t: (32 if t in (2, 3, 6, 7, 8, 20) else 64 if t == 42 else 256) for t in SELF_TYPES + GRID_TYPES}
+NFIELD = {2: 1, 6: 1, 8: 1, 20: 1, 42: 1, 3: 2, 7: 2, 10: 34, 11: 17, 14: 17, 12: 18, 13: 18, 23: 9,
+          16: 9, 18: 9, 19: 9, 21: 9, 17: 17, 22: 17, 29: 17}
+# grid-type contexts (qr.py:386-388, :72-73): rank (model 1), signs (model 1), IQ1_M shift bit,
+# rank and signs by the unit's position in its row (model 2)
+GRID_RANK, GRID_SIGN, GRID_SHIFT = NSB_MAX, NSB_MAX + 8, NSB_MAX + 24
+GRANK2, GSIGN2 = NTAB + 128, NTAB + 144
+TOPK = 16
+GSIZE = {16: 256, 18: 256, 17: 512, 21: 512, 22: 1024, 19: 2048, 29: 2048}
+PARITY = (16, 17, 18)           # 7 stored sign bits per 8, the 8th by even parity
+# x / literal in the QR kernels is x * RN(1 / literal) (the reference's ptxas and --cpu build, cpukernels.py:254-264)
+INV = {22: F32(1) / F32(0.9875), 21: F32(1) / F32(1.033), 19: F32(1) / F32(1.125), 29: F32(1) / F32(1.1125)}
 QMIN = {8: -128}
 QMAX = {10: 3, 42: 3, 11: 7, 6: 31, 7: 31, 13: 31, 14: 63, 8: 127}
 KV = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], F32)   # kvalues_iq4nl
@@ -113,9 +125,14 @@ def fkind(T, k):
         return 0 if k == 0 else 1 if k == 1 else 2 if k < 18 else 3
     if T in (12, 13):
         return 0 if k == 0 else 1 if k == 1 else 2 if k < 10 else 3
-    if T in (11, 14, 23):
+    if T in (11, 14, 23) or T in GRID_TYPES:
         return 0 if k == 0 else 2
     return 0
+
+
+def iq1m_d(B):
+    """IQ1_M: the fp16 super-scale bits kept in the top nibbles of the four scale words (qr.py:200-203)"""
+    return ((_u16(B, 48) >> 12) | ((_u16(B, 50) >> 8) & 0xF0) | ((_u16(B, 52) >> 4) & 0xF00) | (_u16(B, 54) & 0xF000))
 
 
 def get_field(T, B, k):
@@ -141,6 +158,23 @@ def get_field(T, B, k):
             return _u16(B, 0)
         ib = k - 1
         return ((b(4 + ib // 2) >> (4 * (ib % 2))) & 15) | (((_u16(B, 2) >> (2 * ib)) & 3) << 4)
+    # grid types (qr.py:223-230): fp16 d, then the 4-bit (IQ1: 3-bit, IQ1_S with its shift bit) scales
+    if T == 29:
+        if k == 0:
+            return iq1m_d(B)
+        j = k - 1
+        return (_u16(B, 48 + 2 * (j >> 2)) >> (3 * (j & 3))) & 7
+    if k == 0:
+        return _u16(B, 0)
+    j = k - 1
+    if T == 16:
+        return b(2 + 8 * j + 7) >> 4
+    if T == 18:
+        return b(66 + 4 * j + 3) >> 4
+    if T in (17, 22, 21):
+        return (b({17: 66, 22: 74, 21: 106}[T] + j // 2) >> (4 * (j % 2))) & 15
+    if T == 19:
+        return b(34 + 2 * j + 1) >> 4
     raise ValueError(T)
 
 
@@ -148,6 +182,8 @@ def fpred(T, mv, PB_, k, t0, t1):
     """prediction of field k given the true fp16 fields t0, t1 (qr.py:259-283)"""
     pr = get_field(T, PB_, k)
     two = T in (10, 12, 13)
+    if T in GRID_TYPES:
+        return _fpred_grid(T, mv, PB_, k, pr, t0)
     if mv < 2 or T not in (10, 12, 13, 11, 14, 23) or k < (2 if two else 1):
         return pr
     ref = 1 if (two and k >= (18 if T == 10 else 10)) else 0
@@ -162,6 +198,24 @@ def fpred(T, mv, PB_, k, t0, t1):
             v = np.rint((pr.astype(F32) * pv).astype(F32) / tv).astype(F32)
             lo, hi = (-128, 127) if T == 14 else (0, 15 if T == 10 else 63)
             q = np.clip(np.nan_to_num(v, nan=0.0), lo, hi).astype(np.int64)
+    return np.where(ok, q, pr)
+
+
+def _fpred_grid(T, mv, PB_, k, pr, t0):
+    """grid types: the predicted sub-scale rescaled so that d (2 ls + 1) stays the prediction's
+    (qr.py:272-277); IQ1_S keeps its shift bit"""
+    if mv < 2 or k < 1:
+        return pr
+    tv = h2f(t0)
+    pv = h2f(get_field(T, PB_, 0))
+    ok = (tv != 0) & np.isfinite(tv) & np.isfinite(pv)
+    hi = 7 if T in (19, 29) else 15
+    ls = pr & 7 if T == 19 else pr
+    with np.errstate(all="ignore"):
+        v = ((F32(2) * ls.astype(F32) + F32(1)) * pv).astype(F32)     # (float)(2 ls + 1) is exact
+        v = np.rint(((v / tv).astype(F32) - F32(1)).astype(F32) * F32(0.5)).astype(F32)
+        q = np.fmin(np.fmax(v, F32(0)), F32(hi)).astype(np.int64)
+    q = (pr & 8) | q if T == 19 else q
     return np.where(ok, q, pr)
 
 
@@ -263,11 +317,193 @@ def seed_values(seed, seed_type):
     return x, np.zeros_like(x)
 
 
+# ------------------------------------------------------------------ grid types (qr.py:385-646)
+
+def _b(B, i):
+    return int(B[i])
+
+
+def _u16s(B, o):
+    return int(B[o]) | (int(B[o + 1]) << 8)
+
+
+def _u32s(B, o):
+    return _u16s(B, o) | (_u16s(B, o + 2) << 16)
+
+
+def get_gidx(T, B, g):
+    """grid index of group g (8 weights; IQ3: 4) of one block (qr.py:396-407)"""
+    if T == 16:
+        return _b(B, 2 + 8 * (g >> 2) + (g & 3))
+    if T == 17:
+        return _u16s(B, 2 + 2 * g) & 511
+    if T == 22:
+        return _b(B, 2 + g) | ((_b(B, 66 + (g >> 2)) << (8 - 2 * (g & 3))) & 0x300)
+    if T == 18:
+        return _b(B, 2 + g)
+    if T == 21:
+        return _b(B, 2 + g) | ((_b(B, 66 + (g >> 3)) << (8 - (g & 7))) & 256)
+    if T == 19:
+        return _b(B, 2 + g) | (((_u16s(B, 34 + 2 * (g >> 2)) >> (3 * (g & 3))) & 7) << 8)
+    if T == 29:
+        return _b(B, g) | ((_b(B, 32 + 2 * (g >> 2) + ((g & 3) >> 1)) << (4 if g & 1 else 8)) & 0x700)
+    raise ValueError(T)
+
+
+def get_neg(T, B, w):
+    """1 if weight w is stored negative; parity types: the 8th sign of a group from the other 7
+    (qr.py:420-432)"""
+    j = w & 7
+    if T == 16:
+        s7 = (_u32s(B, 2 + 8 * (w >> 5) + 4) >> (7 * ((w >> 3) & 3))) & 127
+    elif T == 17:
+        s7 = _u16s(B, 2 + 2 * (w >> 3)) >> 9
+    elif T == 18:
+        s7 = (_u32s(B, 66 + 4 * (w >> 5)) >> (7 * ((w >> 3) & 3))) & 127
+    elif T == 22:
+        return (_b(B, 34 + (w >> 3)) >> j) & 1
+    elif T == 21:
+        return (_b(B, 74 + (w >> 3)) >> j) & 1
+    else:
+        return 0
+    return (s7 >> j) & 1 if j < 7 else bin(s7).count("1") & 1
+
+
+def get_shift(B, u):
+    """IQ1_M: unit u's shift bit (qr.py:445)"""
+    return (_b(B, 32 + 2 * (u >> 2) + ((u & 3) >> 1)) >> (7 if u & 1 else 3)) & 1
+
+
+def gscale(T, B, u):
+    """(s, dl) of unit u: level l has the value s (2 l + 1) (IQ1: s (l - 1 + dl)); the quantizers'
+    fudge factors on the stored fp16 taken back out (qr.py:449-463)"""
+    dl = F32(0)
+    if T == 29:
+        d = (h2f(iq1m_d(B[None, :]))[0] * INV[29]).astype(F32)
+        j = 2 * (u >> 2) + ((u & 3) >> 1)
+        ls = (_u16s(B, 48 + 2 * (j >> 2)) >> (3 * (j & 3))) & 7
+        dl = F32(-0.125) if get_shift(B, u) else F32(0.125)
+    else:
+        d = h2f(_u16s(B, 0))
+        if T in INV:
+            d = (d * INV[T]).astype(F32)
+        if T == 16:
+            ls = _b(B, 2 + 8 * (u >> 2) + 7) >> 4
+        elif T == 17:
+            ls = (_b(B, 66 + (u >> 2)) >> (4 * ((u & 3) >> 1))) & 15
+        elif T == 22:
+            ls = (_b(B, 74 + (u >> 2)) >> (4 * ((u & 3) >> 1))) & 15
+        elif T == 18:
+            ls = _b(B, 66 + 4 * (u >> 2) + 3) >> 4
+        elif T == 21:
+            ib = u >> 2
+            ls = (_b(B, 106 + (ib >> 1)) >> (4 * (ib & 1))) & 15
+        else:                                   # IQ1_S
+            qh = _u16s(B, 34 + 2 * (u >> 2))
+            ls = (qh >> 12) & 7
+            dl = F32(-0.125) if qh & 0x8000 else F32(0.125)
+    with np.errstate(all="ignore"):
+        return F32(F32(d) * F32(2 * ls + 1)), dl
+
+
+def pos4(col, cols):
+    return 0 if cols <= 0 or col < 256 else 1 + min(2, col * 3 // cols)
+
+
+def grid_distances(T, gk, uu, ww, dl):
+    """weighted squared error of every grid point against the unit's targets: pair tables of level
+    errors (qr.py:505-517), then N/2 lookups summed in pair order, NaN -> inf (qr.py:518-525)"""
+    sgn = T not in (19, 29)
+    n = len(uu)
+    bits = 2 if n == 8 else 3
+    lv = np.arange(1 << bits)
+    qv = (2 * lv + 1).astype(F32) if sgn else ((lv - 1).astype(F32) + dl).astype(F32)
+    d = np.zeros(len(gk), F32)
+    with np.errstate(all="ignore"):
+        for p in range(n // 2):
+            ea = (qv - uu[2 * p]).astype(F32)
+            eb = (qv - uu[2 * p + 1]).astype(F32)
+            # table entry e = la | lb << bits: ww[2p] ea^2 + ww[2p+1] eb^2
+            tab = ((ww[2 * p] * (ea * ea)).astype(F32)[None, :] + (ww[2 * p + 1] * (eb * eb)).astype(F32)[:, None]).astype(F32)
+            tab = tab.reshape(-1)
+            key = (gk.astype(np.int64) >> (2 * bits * p)) & ((1 << 2 * bits) - 1)
+            d = (d + tab[key]).astype(F32)
+    d[np.isnan(d)] = np.inf
+    return d
+
+
+def gapctx(d1, d2):
+    with np.errstate(all="ignore"):
+        g = F32(F32(d2 - d1) / F32(d1 + F32(1e-30)))
+    return int(g >= F32(0.05)) + int(g >= F32(0.2)) + int(g >= F32(0.6))
+
+
+def grid_symbols(T, fb, pb, x, imw, col0, cols, mv, gk):
+    """decode-order symbols of the grid codes of one block (qr.py:553-637): per unit of 8 weights,
+    IQ1_M's shift bit, then per lattice group the rank of the true point among all grid points in
+    (distance, index) order (escape 16 + the index's two bytes beyond rank 15), then the signs"""
+    n = 4 if T in (18, 21) else 8
+    ng = 8 // n
+    sgn = T not in (19, 29)
+    par = T in PARITY
+    sx2 = np.add.accumulate(np.concatenate([[F32(0)], (x * x).astype(F32)]).astype(F32))[-1]
+    sigma2 = F32(sx2 * F32(1 / 256)) if T in (16, 17) else F32(F32(F32(2) * sx2) * F32(1 / 256))
+    out = []
+    for u in range(32):
+        rank0 = GRANK2 + 4 * pos4(col0 + 8 * u, cols) if mv >= 2 else GRID_RANK
+        sign0 = GSIGN2 + 16 * pos4(col0 + 8 * u, cols) if mv >= 2 else GRID_SIGN
+        if T == 29:
+            out.append((GRID_SHIFT, get_shift(fb, u) ^ get_shift(pb, u)))
+        s, dl = gscale(T, fb, u)
+        xu = x[8 * u:8 * u + 8]
+        with np.errstate(all="ignore"):
+            w = np.sqrt((sigma2 + (xu * xu).astype(F32)).astype(F32)).astype(F32)
+            if imw is not None:
+                w = (w * imw[8 * u:8 * u + 8]).astype(F32)
+        pn = (xu < 0).astype(np.int64)
+        v = np.abs(xu) if sgn else xu.copy()
+        if sgn and par and pn.sum() & 1:
+            a = ((w * xu).astype(F32) * xu).astype(F32)
+            im = 0
+            for i in range(1, 8):
+                if a[i] < a[im]:
+                    im = i
+            pn[im] ^= 1
+            v[im] = -v[im]
+        with np.errstate(all="ignore"):
+            uu = (v / s).astype(F32)
+        tg = [get_gidx(T, fb, u * ng + gg) for gg in range(ng)]
+        for gg in range(ng):
+            d = grid_distances(T, gk, uu[gg * n:(gg + 1) * n], w[gg * n:(gg + 1) * n], dl)
+            t = tg[gg]
+            dt = d[t]
+            k = np.arange(len(d))
+            rank = int(((d < dt) | ((d == dt) & (k < t))).sum())
+            srt = np.sort(d)
+            ctx = gapctx(srt[0], srt[1])
+            if rank >= TOPK:
+                out += [(rank0 + ctx, TOPK), (FESC_LO, t & 255), (FESC_HI, t >> 8)]
+            else:
+                out.append((rank0 + ctx, rank))
+        if sgn:
+            bits, mask = (2, 3) if n == 8 else (3, 7)
+            for j in range(8):
+                if par and j == 7:
+                    continue
+                lev = (int(gk[tg[j // n]]) >> (bits * (j % n))) & mask
+                with np.errstate(all="ignore"):
+                    m4 = F32(abs(uu[j]) * F32(4))
+                ctx = (lev == 0) * 8 + (int(m4) if m4 < F32(7) else 7)
+                out.append((sign0 + ctx, get_neg(T, fb, 8 * u + j) ^ int(pn[j])))
+    return out
+
+
 # ------------------------------------------------------------------ symbol sequences
 
-def block_symbols(T, F, P, seed, seed_type, cols, mv=2):
+def block_symbols(T, F, P, seed, seed_type, cols, mv=2, imx=None, gk=None):
     """the forward (decode-order) symbols of every block, as a list of lists of (table, symbol),
-    and the per-block equality flags (qr.py:674-710)"""
+    and the per-block equality flags (qr.py:674-710). Grid types need the grid keys gk (uint16 per
+    grid point: its levels, 2 bits each, IQ3 3 bits) and take the imatrix imx (float32 per column)."""
     bs, qk, nf = BS[T], QK[T], NFIELD[T]
     Fb = np.frombuffer(F, np.uint8).reshape(-1, bs)
     Pb = np.frombuffer(P, np.uint8).reshape(-1, bs)
@@ -287,6 +523,24 @@ def block_symbols(T, F, P, seed, seed_type, cols, mv=2):
         anyv = anyv | (dlt != 0)
     gw0 = np.arange(nb, dtype=np.int64) * qk
     col0 = gw0 % cols if cols > 0 else np.zeros(nb, np.int64)
+    if T in GRID_TYPES:
+        out = []
+        for b in range(nb):
+            if eq[b]:
+                out.append(None)
+                continue
+            seq = []
+            for (tab, sym, esc, t) in fsyms:
+                seq.append((int(tab[b]), int(sym[b])))
+                if esc[b]:
+                    seq.append((FESC_LO, int(t[b]) & 255))
+                    seq.append((FESC_HI, int(t[b]) >> 8))
+            cidx = (gw0[b] + np.arange(qk)) % cols if cols > 0 else None
+            imw = None if imx is None else np.asarray(imx, F32)[cidx]
+            seq += grid_symbols(T, Fb[b], Pb[b], x[gw0[b]:gw0[b] + qk], imw, int(col0[b]), cols, mv,
+                                np.asarray(gk, np.uint16))
+            out.append(seq)
+        return out, eq
     ctxs = np.zeros((nb, qk), np.int64)
     syms = np.zeros((nb, qk), np.int64)
     for w in range(qk):
@@ -328,8 +582,8 @@ def segment_sequence(T, blocks, b0, n):
     return seq
 
 
-def histogram(T, F, P, seed, seed_type, cols, mv=2):
-    blocks, _ = block_symbols(T, F, P, seed, seed_type, cols, mv)
+def histogram(T, F, P, seed, seed_type, cols, mv=2, imx=None, gk=None):
+    blocks, _ = block_symbols(T, F, P, seed, seed_type, cols, mv, imx, gk)
     counts = np.zeros((NTAB2, 256), np.uint32)
     for b0, n in segments(T, len(blocks)):
         for tab, s in segment_sequence(T, blocks, b0, n):
@@ -387,9 +641,9 @@ def rans_encode(seq, remap, freq, cum):
     return bytes(reversed(out))
 
 
-def encode(T, F, P, seed, seed_type, cols, mv=2):
+def encode(T, F, P, seed, seed_type, cols, mv=2, imx=None, gk=None):
     """-> dict(counts, freq, used, lens, stream) of one single-tensor batch"""
-    counts, blocks = histogram(T, F, P, seed, seed_type, cols, mv)
+    counts, blocks = histogram(T, F, P, seed, seed_type, cols, mv, imx, gk)
     freq, used = normalize(counts)
     remap = np.full(NTAB2, -1, np.int32)
     remap[used] = np.arange(len(used), dtype=np.int32)

@@ -20,6 +20,7 @@ SIGNATURES = {
     "spa_last_error": (ctypes.c_char_p, []),
     "spa_device_count": (c_int, [ctypes.POINTER(c_int)]),
     "spa_set_device": (c_int, [c_int]),
+    "spa_get_device": (c_int, [ctypes.POINTER(c_int)]),
     "spa_malloc": (c_int, [ctypes.POINTER(c_void_p), c_size_t]),
     "spa_free": (c_int, [c_void_p]),
     "spa_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),

@@ -49,6 +49,11 @@ int spa_device_count(int* n) {
     return SPA_OK;
 }
 int spa_set_device(int device) { SPA_HIP_TRY(hipSetDevice(device)); return SPA_OK; }
+int spa_get_device(int* device) {
+    if (!device) return fail(SPA_ERR_ARG, "spa_get_device: null out pointer");
+    SPA_HIP_TRY(hipGetDevice(device));
+    return SPA_OK;
+}
 int spa_malloc(void** ptr, size_t nbytes) {
     if (!ptr) return fail(SPA_ERR_ARG, "spa_malloc: null out pointer");
     SPA_HIP_TRY(hipMalloc(ptr, nbytes ? nbytes : 1));

@@ -1,4 +1,4 @@
-// QR residual coder kernels for the non-grid quant types: histogram, interleaved-segment rANS
+// QR residual coder kernels for the non-grid quant types (grid types: qr_grid.hip): histogram, interleaved-segment rANS
 // encode and decode, segment gather and decode lookup tables (seedpack/qr.py:674-895 semantics).
 //
 // Stream format (fixed by the archive): a batch of blocks is cut into segments of
@@ -100,6 +100,10 @@ struct Enc {
     }
 };
 
+// bytes kept free below the coder's write pointer while coding codes: the block's fields (up to three
+// symbols each) and its flag, at most two bytes per symbol
+template <int T> constexpr int64_t FIELD_ROOM = 6 * Ty<T>::NF + 16;
+
 template <int T>
 __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
                                                const uint8_t* __restrict__ seed, const TM* __restrict__ tm,
@@ -120,7 +124,11 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
         const uint8_t* pb = P + b * Y::BS;
         const bool eq = same_block(fb, pb, Y::BS);
         const int prev = b > g.b0 ? (int)same_block(fb - Y::BS, pb - Y::BS, Y::BS) : 1;
-        if (eq) { e.put(FLAG + prev, 1); continue; }
+        if (eq) {
+            e.put(FLAG + prev, 1);
+            if (e.ptr - base < 8) { out_len[s] = 0xffffffffu; return; }
+            continue;
+        }
         const int64_t gw0 = (b - m.blk0) * Y::QK;
         const int64_t col0 = m.cols > 0 ? gw0 % m.cols : 0;
         float a = 0.f, c = 0.f;
@@ -132,7 +140,7 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
             int r, sg_, ctx;
             predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
             e.put(ctx, (uint32_t)((sg_ * (get_code<T>(fb, w) - r)) & 255));
-            if (e.ptr - base < 8) { out_len[s] = 0xffffffffu; return; }
+            if (e.ptr - base < FIELD_ROOM<T>) { out_len[s] = 0xffffffffu; return; }
         }
         int tv[Y::NF], dl[Y::NF], anyk[Y::NF];
 #pragma unroll
@@ -173,7 +181,10 @@ struct Dec {
         const uint32_t slot = x & (PSCALE - 1);
         const int v = lut[(size_t)tt * PSCALE + slot];
         x = freq[tt * 256 + v] * (x >> PB) + slot - cum[tt * 257 + v];
-        while (x < RANS_L) x = (x << 8) | *ptr++;
+        // a valid stream needs at most two bytes here (x >= 2^11 before them); the cap ends the
+        // loop on a damaged stream instead of spinning on zero bytes
+#pragma unroll
+        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | *ptr++;
         return v;
     }
 };
@@ -317,15 +328,25 @@ template <int T> struct Decode {
 
 bool grid_type(int T) { return T == 16 || T == 17 || T == 18 || T == 19 || T == 21 || T == 22 || T == 29; }
 
-int check_common(int T, int nseg, int mv, const void* gk, const float* imx) {
-    if (grid_type(T)) return fail(SPA_ERR_TYPE, "QR: grid type %d is not built yet", T);
+int check_common(int T, int nseg, int mv, const void* gk) {
     if (nseg < 0) return fail(SPA_ERR_ARG, "QR: negative segment count");
     if (mv != 1 && mv != 2) return fail(SPA_ERR_ARG, "QR: unknown model %d", mv);
-    (void)gk; (void)imx;
+    if (grid_type(T) && !gk) return fail(SPA_ERR_ARG, "QR: grid type %d needs its grid keys", T);
     return 0;
 }
 
 }  // namespace
+
+// grid types (qr_grid.hip)
+int grid_hist(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, uint32_t* counts,
+              const uint16_t* gk, const float* imx, int mv, hipStream_t st);
+int grid_encode(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, const int* remap,
+                const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, const uint16_t* gk,
+                const float* imx, int mv, hipStream_t st);
+int grid_decode(int T, const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
+                int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F,
+                const uint16_t* gk, const float* imx, int mv, hipStream_t st);
+
 }  // namespace qr
 }  // namespace spa
 
@@ -345,25 +366,30 @@ int spa_qr_seg_blocks(int T) {
 
 int spa_qr_hist(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,
                 uint32_t* counts, const uint16_t* gk, const float* imx, int mv, void* stream) {
-    if (int e = check_common(T, nseg, mv, gk, imx)) return e;
+    if (int e = check_common(T, nseg, mv, gk)) return e;
     if (nseg == 0) return 0;
+    if (grid_type(T)) return grid_hist(T, F, P, seed, tm, sg, nseg, counts, gk, imx, mv, (hipStream_t)stream);
     return dispatch<Hist>(T, F, P, seed, tm, sg, nseg, counts, mv, (hipStream_t)stream);
 }
 
 int spa_qr_encode(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,
                   const int* remap, const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len,
                   const uint16_t* gk, const float* imx, int mv, void* stream) {
-    if (int e = check_common(T, nseg, mv, gk, imx)) return e;
+    if (int e = check_common(T, nseg, mv, gk)) return e;
     if (cap < 1024) return spa::fail(SPA_ERR_ARG, "QR: segment capacity %llu too small", (unsigned long long)cap);
     if (nseg == 0) return 0;
+    if (grid_type(T))
+        return grid_encode(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, gk, imx, mv, (hipStream_t)stream);
     return dispatch<Encode>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, mv, (hipStream_t)stream);
 }
 
 int spa_qr_decode(int T, const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm,
                   const void* sg, int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut,
                   void* F, const uint16_t* gk, const float* imx, int mv, void* stream) {
-    if (int e = check_common(T, nseg, mv, gk, imx)) return e;
+    if (int e = check_common(T, nseg, mv, gk)) return e;
     if (nseg == 0) return 0;
+    if (grid_type(T))
+        return grid_decode(T, in, in_off, P, seed, tm, sg, nseg, remap, freq, cum, lut, F, gk, imx, mv, (hipStream_t)stream);
     return dispatch<Decode>(T, in, in_off, P, seed, tm, sg, nseg, remap, freq, cum, lut, F, mv, (hipStream_t)stream);
 }
 

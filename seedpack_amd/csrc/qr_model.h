@@ -52,9 +52,18 @@ SPA_QR_TYPE(14, 256, 210, 17, 0, 63, 16) // Q6_K
 SPA_QR_TYPE(20, 32, 18, 1, 0, 15, 32)    // IQ4_NL
 SPA_QR_TYPE(23, 256, 136, 9, 0, 15, 32)  // IQ4_XS
 SPA_QR_TYPE(42, 64, 18, 1, 0, 3, 32)     // Q2_0
+// grid types: codes are lattice points, not integers (QMIN / QMAX / SUBLEN unused)
+SPA_QR_TYPE(16, 256, 66, 9, 0, 0, 32)    // IQ2_XXS
+SPA_QR_TYPE(17, 256, 74, 17, 0, 0, 32)   // IQ2_XS
+SPA_QR_TYPE(18, 256, 98, 9, 0, 0, 32)    // IQ3_XXS
+SPA_QR_TYPE(19, 256, 50, 9, 0, 0, 32)    // IQ1_S
+SPA_QR_TYPE(21, 256, 110, 9, 0, 0, 32)   // IQ3_S
+SPA_QR_TYPE(22, 256, 82, 17, 0, 0, 32)   // IQ2_S
+SPA_QR_TYPE(29, 256, 56, 17, 0, 0, 32)   // IQ1_M
 #undef SPA_QR_TYPE
 
 template <int T> constexpr bool NONLIN = T == 20 || T == 23;
+template <int T> constexpr bool GRIDT = T == 16 || T == 17 || T == 18 || T == 19 || T == 21 || T == 22 || T == 29;
 template <int T> constexpr int SEG_BLOCKS = Ty<T>::QK >= 1024 ? 16 : (16384 / Ty<T>::QK > 16 ? 16384 / Ty<T>::QK : 16);
 
 __device__ __forceinline__ uint32_t rd16(const uint8_t* b) { return (uint32_t)b[0] | ((uint32_t)b[1] << 8); }
@@ -144,8 +153,13 @@ __device__ __forceinline__ int fkind(int k) {
     if constexpr (T == 3 || T == 7) return k == 0 ? 0 : 1;
     if constexpr (T == 10) return k == 0 ? 0 : (k == 1 ? 1 : (k < 18 ? 2 : 3));
     if constexpr (T == 12 || T == 13) return k == 0 ? 0 : (k == 1 ? 1 : (k < 10 ? 2 : 3));
-    if constexpr (T == 11 || T == 14 || T == 23) return k == 0 ? 0 : 2;
+    if constexpr (T == 11 || T == 14 || T == 23 || GRIDT<T>) return k == 0 ? 0 : 2;
     return 0;
+}
+
+// IQ1_M: the fp16 super-scale bits kept in the top nibbles of the four scale words
+__device__ __forceinline__ int iq1m_d(const uint8_t* b) {
+    return (int)((rd16(b + 48) >> 12) | ((rd16(b + 50) >> 8) & 0xf0) | ((rd16(b + 52) >> 4) & 0xf00) | (rd16(b + 54) & 0xf000));
 }
 
 template <int T>
@@ -170,6 +184,19 @@ __device__ __forceinline__ int get_field(const uint8_t* b, int k) {
         const int ib = k - 1, sh = (int)rd16(b + 2);
         return ((b[4 + ib / 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
     }
+    // grid types: fp16 d, then the 4-bit (IQ1: 3-bit; IQ1_S with its shift bit) sub-block scales
+    if constexpr (T == 29) {
+        if (k == 0) return iq1m_d(b);
+        const int j = k - 1;
+        return (int)(rd16(b + 48 + 2 * (j >> 2)) >> (3 * (j & 3))) & 7;
+    }
+    if constexpr (T == 16) return k == 0 ? (int)rd16(b) : b[2 + 8 * (k - 1) + 7] >> 4;
+    if constexpr (T == 18) return k == 0 ? (int)rd16(b) : b[66 + 4 * (k - 1) + 3] >> 4;
+    if constexpr (T == 17 || T == 22 || T == 21) {
+        constexpr int O = T == 17 ? 66 : T == 22 ? 74 : 106;
+        return k == 0 ? (int)rd16(b) : (b[O + (k - 1) / 2] >> (4 * ((k - 1) % 2))) & 15;
+    }
+    if constexpr (T == 19) return k == 0 ? (int)rd16(b) : b[34 + 2 * (k - 1) + 1] >> 4;
     return 0;
 }
 
@@ -219,6 +246,33 @@ __device__ __forceinline__ void set_fields(uint8_t* b, const int (&v)[Ty<T>::NF]
         }
         wr16(b + 2, sh);
     }
+    // grid types: the scale bits share bytes with grid indices and signs, so they are OR-ed in
+    if constexpr (T == 16 || T == 18) {
+        wr16(b, v[0]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) b[(T == 16 ? 2 + 8 * j + 7 : 66 + 4 * j + 3)] |= (v[1 + j] & 15) << 4;
+    }
+    if constexpr (T == 17 || T == 22 || T == 21) {
+        constexpr int O = T == 17 ? 66 : T == 22 ? 74 : 106, NS = T == 21 ? 8 : 16;
+        wr16(b, v[0]);
+#pragma unroll
+        for (int j = 0; j < NS; ++j) b[O + j / 2] |= (v[1 + j] & 15) << (4 * (j % 2));
+    }
+    if constexpr (T == 19) {
+        wr16(b, v[0]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) b[34 + 2 * j + 1] |= (v[1 + j] & 15) << 4;
+    }
+    if constexpr (T == 29) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int sv = (v[1 + j] & 7) << (3 * (j & 3));
+            b[48 + 2 * (j >> 2)] |= sv & 255;
+            b[49 + 2 * (j >> 2)] |= sv >> 8;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b[49 + 2 * i] |= ((v[0] >> (4 * i)) & 15) << 4;
+    }
 }
 
 // prediction of field k, given F's fp16 fields t0 (and t1): model 2 rescales the sub-scales
@@ -226,6 +280,17 @@ __device__ __forceinline__ void set_fields(uint8_t* b, const int (&v)[Ty<T>::NF]
 template <int T>
 __device__ __forceinline__ int fpred(int mv, const uint8_t* pb, int k, int t0, int t1) {
     const int pr = get_field<T>(pb, k);
+    if constexpr (GRIDT<T>) {
+        // the sub-scale rescaled so that d (2 ls + 1) stays the prediction's; IQ1_S keeps its shift bit
+        if (mv < 2 || k < 1) return pr;
+        const float tv = h2f((uint32_t)t0), pv = h2f((uint32_t)get_field<T>(pb, 0));
+        if (tv == 0.f || !isfinite(tv) || !isfinite(pv)) return pr;
+        constexpr float hi = (T == 19 || T == 29) ? 7.f : 15.f;
+        const int ls = T == 19 ? (pr & 7) : pr;
+        const float v = rintf(((((float)(2 * ls + 1) * pv) / tv) - 1.f) * 0.5f);
+        const int q = (int)fminf(fmaxf(v, 0.f), hi);
+        return T == 19 ? ((pr & 8) | q) : q;
+    }
     constexpr bool two = T == 10 || T == 12 || T == 13;
     constexpr bool rescaled = two || T == 11 || T == 14 || T == 23;
     if (mv < 2 || !rescaled || k < (two ? 2 : 1)) return pr;

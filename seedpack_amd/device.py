@@ -75,6 +75,16 @@ def device_count():
     return n.value
 
 
+def current_device():
+    d = ctypes.c_int()
+    check(lib().spa_get_device(ctypes.byref(d)))
+    return d.value
+
+
+def set_device(device):
+    check(lib().spa_set_device(int(device)))
+
+
 def mem_info():
     f, t = ctypes.c_size_t(), ctypes.c_size_t()
     check(lib().spa_mem_info(ctypes.byref(f), ctypes.byref(t)))

@@ -11,6 +11,7 @@ items (encode): (file bytes, predicted bytes, seed byte offset, seed type[, weig
 imatrix offset]); (decode): the same without the file bytes. Bytes are numpy uint8 arrays or
 DeviceArrays; seeds are device arrays (BF16 = type 30, F32 = 0, F16 = 1).
 """
+import ctypes
 import struct
 
 import numpy as np
@@ -33,6 +34,25 @@ BATCH = 384 << 20                                   # bytes per coding batch (qr
 
 TM_DT = np.dtype([("blk0", "<i8"), ("seed_off", "<i8"), ("seed_type", "<i4"), ("cols", "<i4"), ("imx_off", "<i8")])
 SG_DT = np.dtype([("t", "<i4"), ("nb", "<i4"), ("b0", "<i8")])
+
+
+# the library's IQ table holding each grid type's lattice (iq_table_index in the C library)
+GRID_TABLE = {16: 0, 17: 1, 19: 2, 29: 2, 22: 3, 18: 4, 21: 5}
+_GK = {}
+
+
+def grid_keys(T):
+    """numpy uint16 per grid point of grid type T: its coordinate levels (value - 1) / 2, 2 bits each
+    (IQ3: 3 bits) -- what the grid model looks distances up by (qr.py:935-948). Built from the
+    library's own lattice tables."""
+    if T not in _GK:
+        g, n = ctypes.c_void_p(), ctypes.c_int()
+        check(lib().spa_iq_table_host(GRID_TABLE[T], ctypes.byref(g), ctypes.byref(n), None, None, None, None))
+        grid = np.ctypeslib.as_array(ctypes.cast(g, ctypes.POINTER(ctypes.c_uint8)), (n.value,))
+        d, bits = (4, 3) if T in (18, 21) else (8, 2)
+        lev = (grid.reshape(-1, d).astype(np.int64) - 1) // 2
+        _GK[T] = (lev << (bits * np.arange(d))).sum(1).astype(np.uint16)
+    return _GK[T]
 
 
 def seg_blocks(T):
@@ -165,10 +185,21 @@ def _descriptors(T, nbs, meta):
 
 
 def _check_type(T):
-    if T in GRID_TYPES:
-        raise NotImplementedError(f"QR for grid type {T} is not built yet")
-    if T not in SELF_TYPES:
+    if T not in QR_TYPES:
         raise ValueError(f"type {T} is not a QR type")
+
+
+_GK_DEV = {}
+
+
+def _gk_ptr(T):
+    """device grid keys of grid type T (uploaded once per device), or None for the other types"""
+    if T not in GRID_TYPES:
+        return None
+    dev_id = dev.current_device()
+    if (T, dev_id) not in _GK_DEV:
+        _GK_DEV[(T, dev_id)] = dev.DeviceArray.from_host(grid_keys(T))
+    return _GK_DEV[(T, dev_id)].ptr
 
 
 def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
@@ -184,7 +215,8 @@ def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
     sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if nseg else np.zeros(16, np.uint8), stream)
     counts = dev.DeviceArray((NTAB2, 256), np.uint32).zero(stream)
     imx = None if imx_dev is None else imx_dev.ptr
-    check(lib().spa_qr_hist(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, counts.ptr, None, imx, mv, stream))
+    gk = _gk_ptr(T)
+    check(lib().spa_qr_hist(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, counts.ptr, gk, imx, mv, stream))
     counts_h = counts.to_host(stream=stream)
     freq, used = normalize(counts_h)
     remap = np.full(NTAB2, -1, np.int32)
@@ -196,7 +228,7 @@ def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
         out = dev.DeviceArray(max(1, nseg * cap), np.uint8)
         out_len = dev.DeviceArray(max(1, nseg), np.uint32).zero(stream)
         check(lib().spa_qr_encode(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr, freq_d.ptr,
-                                  cum_d.ptr, out.ptr, cap, out_len.ptr, None, imx, mv, stream))
+                                  cum_d.ptr, out.ptr, cap, out_len.ptr, gk, imx, mv, stream))
         lens = out_len.to_host(stream=stream)[:nseg]
         if not (lens == 0xFFFFFFFF).any():
             break
@@ -248,7 +280,7 @@ def decode_parts(T, freq, used, lens, stream_bytes, items, seed_dev, imx_dev=Non
     offs_d = dev.DeviceArray.from_host(offs, stream)
     imx = None if imx_dev is None else imx_dev.ptr
     check(lib().spa_qr_decode(T, s_d.ptr, offs_d.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr,
-                              freq_d.ptr, cum_d.ptr, lut.ptr, F.ptr, None, imx, mv, stream))
+                              freq_d.ptr, cum_d.ptr, lut.ptr, F.ptr, _gk_ptr(T), imx, mv, stream))
     return F
 
 

@@ -62,8 +62,24 @@ def load():
 
 TM_DT = np.dtype([("blk0", "<i8"), ("seed_off", "<i8"), ("seed_type", "<i4"), ("cols", "<i4"), ("imx_off", "<i8")])
 SG_DT = np.dtype([("t", "<i4"), ("nb", "<i4"), ("b0", "<i8")])
-QK = {2: 32, 3: 32, 6: 32, 7: 32, 8: 32, 20: 32, 42: 64, 10: 256, 11: 256, 12: 256, 13: 256, 14: 256, 23: 256}
-BS = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 20: 18, 42: 18, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 23: 136}
+QK = {2: 32, 3: 32, 6: 32, 7: 32, 8: 32, 20: 32, 42: 64, 10: 256, 11: 256, 12: 256, 13: 256, 14: 256, 23: 256,
+      16: 256, 17: 256, 18: 256, 19: 256, 21: 256, 22: 256, 29: 256}
+BS = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 20: 18, 42: 18, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 23: 136,
+      16: 66, 17: 74, 18: 98, 19: 50, 21: 110, 22: 82, 29: 56}
+GRID_TAB = {16: "iq2_data_0", 17: "iq2_data_1", 19: "iq2_data_2", 29: "iq2_data_2", 22: "iq2_data_3",
+            18: "iq3_data_0", 21: "iq3_data_1"}
+
+
+def grid_keys(T):
+    """uint16 per grid point: its levels (grid byte - 1) / 2, 2 bits each (IQ3: 3 bits), as the
+    reference's qr.grid_keys builds them from its table fixture"""
+    if T not in GRID_TAB:
+        return np.zeros(1, np.uint16)
+    tb = np.load(os.path.join(REF, "seedpack", "ggml", "iqtables.npz"))
+    g = tb[GRID_TAB[T] + "_grid"]
+    n, bits = (8, 2) if g.dtype == np.uint64 else (4, 3)
+    lev = np.stack([((g >> np.array(8 * i, g.dtype)) & np.array(255, g.dtype)).astype(np.int64) for i in range(n)], 1)
+    return (((lev - 1) // 2) << (bits * np.arange(n))).sum(1).astype(np.uint16)
 NSB_MAX, NTAB2 = 20, 20 + 64 + 2 + 208
 
 
@@ -96,31 +112,32 @@ def perturb(P, bs, g, frac=0.01):
     return F.reshape(-1)
 
 
-def encode(mod, normalize, T, F, P, seed, cols, mv=2):
+def encode(mod, normalize, T, F, P, seed, cols, mv=2, imx=None):
     """qr.py:1007-1061 without the zstd framing -> dict of the coded parts"""
     tm, sg, nb = layout(T, [len(F) // BS[T]])
     tm["seed_off"] = 0
     tm["seed_type"] = 30
     tm["cols"] = cols
-    tm["imx_off"] = -1
-    gk = np.zeros(1, np.uint16)
-    imx = np.zeros(1, np.float32)
+    tm["imx_off"] = -1 if imx is None else 0
+    gk = grid_keys(T)
+    imx = np.zeros(1, np.float32) if imx is None else np.ascontiguousarray(imx, np.float32)
+    smem = 0 if T not in GRID_TAB else 64 * 4 * (128 if T in (18, 21) else 64)
     nseg = len(sg)
     counts = np.zeros((NTAB2, 256), np.uint32)
     grid = ((nseg + 63) // 64,)
     tmb, sgb = tm.view(np.uint8), sg.view(np.uint8)
     mod.get_function("qr_hist")(grid, (64,), (np.int32(T), F, P, seed, tmb, sgb, np.int32(nseg), counts, gk, imx,
-                                              np.int32(mv)))
+                                              np.int32(mv)), shared_mem=smem)
     freq, used = normalize(counts)
     remap = np.full(NTAB2, -1, np.int32)
     remap[used] = np.arange(len(used), dtype=np.int32)
     cum = np.zeros((len(freq), 257), np.uint32)
     cum[:, 1:] = np.cumsum(freq.astype(np.uint32), axis=1)
-    cap = seg_blocks(T) * (QK[T] + NSB_MAX) * 2 + 1024
+    cap = seg_blocks(T) * (3 * BS[T] if T in GRID_TAB else (QK[T] + NSB_MAX) * 2) + 1024
     out = np.zeros(nseg * cap, np.uint8)
     out_len = np.zeros(nseg, np.uint32)
     mod.get_function("qr_enc")(grid, (64,), (np.int32(T), F, P, seed, tmb, sgb, np.int32(nseg), remap, freq, cum,
-                                             out, np.uint64(cap), out_len, gk, imx, np.int32(mv)))
+                                             out, np.uint64(cap), out_len, gk, imx, np.int32(mv)), shared_mem=smem)
     assert not (out_len == 0xFFFFFFFF).any()
     stream = b"".join(out[(s + 1) * cap - out_len[s]:(s + 1) * cap].tobytes() for s in range(nseg))
     # decode back (qr.py:1064-1090)
@@ -130,7 +147,8 @@ def encode(mod, normalize, T, F, P, seed, cols, mv=2):
     offs[1:] = np.cumsum(out_len.astype(np.uint64))[:-1]
     Fd = np.zeros(nb * BS[T], np.uint8)
     mod.get_function("qr_dec")(grid, (64,), (np.int32(T), np.frombuffer(stream, np.uint8).copy(), offs, P, seed, tmb, sgb,
-                                             np.int32(nseg), remap, freq, cum, lut, Fd, gk, imx, np.int32(mv)))
+                                             np.int32(nseg), remap, freq, cum, lut, Fd, gk, imx, np.int32(mv)),
+                               shared_mem=smem)
     assert Fd.tobytes() == F.tobytes(), "reference decode does not round-trip"
     return {"counts": counts, "freq": freq, "used": used.astype(np.int32), "lens": out_len,
             "stream": np.frombuffer(stream, np.uint8)}
@@ -151,7 +169,8 @@ def main():
         else:                       # the file used the imatrix, the prediction did not
             F = P
             P = qref.quantize(T, x, None)
-        res = encode(mod, normalize, T, F, P, w.reshape(-1).view(np.uint8).copy(), cols)
+        res = encode(mod, normalize, T, F, P, w.reshape(-1).view(np.uint8).copy(), cols,
+                     imx=imx if T in GRID_TAB else None)
         out[f"{name}/T"] = np.array([T, rows, cols, k], np.int64)
         out[f"{name}/seed_sha"] = np.frombuffer(__import__("hashlib").sha256(w.tobytes()).digest(), np.uint8)
         out[f"{name}/P"] = P

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from oracle import qr as oqr
-from tests.golden.qr_cases import CASES, case_seed
+from tests.golden.qr_cases import CASES, GRID, case_seed
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -25,10 +25,20 @@ def case_inputs(vectors, name):
     return T, cols, F, P, w.reshape(-1).view(np.uint8)
 
 
+def case_grid(name):
+    """(imatrix, grid keys) the grid-type cases are coded with; (None, None) for the others"""
+    k = [c[0] for c in CASES].index(name)
+    if CASES[k][1] not in GRID:
+        return None, None
+    from seedpack_amd.qr import grid_keys
+    return case_seed(k)[2], grid_keys(CASES[k][1])
+
+
 @pytest.mark.parametrize("name", [c[0] for c in CASES])
 def test_oracle_qr_matches_reference_kernels(vectors, name):
     T, cols, F, P, seed = case_inputs(vectors, name)
-    res = oqr.encode(T, F.tobytes(), P.tobytes(), seed.tobytes(), 30, cols)
+    imx, gk = case_grid(name)
+    res = oqr.encode(T, F.tobytes(), P.tobytes(), seed.tobytes(), 30, cols, imx=imx, gk=gk)
     assert np.array_equal(res["counts"], vectors[f"{name}/counts"]), "histogram"
     assert np.array_equal(res["used"], vectors[f"{name}/used"]), "used tables"
     assert np.array_equal(res["freq"], vectors[f"{name}/freq"]), "normalised frequencies"

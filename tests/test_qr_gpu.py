@@ -9,8 +9,8 @@ from oracle import qr as oqr
 from seedpack_amd import device as dev
 from seedpack_amd import qr, synth
 from seedpack_amd.gpuquant import GPUQuant
-from tests.golden.qr_cases import CASES
-from tests.test_oracle_qr import case_inputs
+from tests.golden.qr_cases import CASES, GRID
+from tests.test_oracle_qr import case_grid, case_inputs
 
 pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -25,12 +25,19 @@ def vectors():
     return np.load(os.path.join(ROOT, "tests", "golden", "qr_vectors.npz"))
 
 
+def _imx(name):
+    """(device imatrix, its offset) of a grid case; (None, -1) otherwise"""
+    imx, _ = case_grid(name)
+    return (None, -1) if imx is None else (dev.DeviceArray.from_host(imx), 0)
+
+
 @pytest.mark.parametrize("name", [c[0] for c in CASES])
 def test_hip_qr_encode_matches_reference(vectors, name):
     T, cols, F, P, seed = case_inputs(vectors, name)
     say("case qr encode", name)
     sd = dev.DeviceArray.from_host(seed)
-    res = qr.encode_parts(T, [(F, P, 0, 30, cols, -1)], sd)
+    imx, off = _imx(name)
+    res = qr.encode_parts(T, [(F, P, 0, 30, cols, off)], sd, imx)
     assert np.array_equal(res["counts"], vectors[f"{name}/counts"]), "histogram"
     assert np.array_equal(res["used"], vectors[f"{name}/used"])
     assert np.array_equal(res["freq"], vectors[f"{name}/freq"])
@@ -43,8 +50,9 @@ def test_hip_qr_decodes_reference_stream(vectors, name):
     T, cols, F, P, seed = case_inputs(vectors, name)
     say("case qr decode", name)
     sd = dev.DeviceArray.from_host(seed)
+    imx, off = _imx(name)
     out = qr.decode_parts(T, vectors[f"{name}/freq"], vectors[f"{name}/used"], vectors[f"{name}/lens"],
-                          vectors[f"{name}/stream"].tobytes(), [(P, 0, 30, cols, -1)], sd)
+                          vectors[f"{name}/stream"].tobytes(), [(P, 0, 30, cols, off)], sd, imx)
     got = out.to_host()[:len(F)]
     bad = np.flatnonzero(got != F)
     assert bad.size == 0, f"{bad.size} bytes differ, first at {bad[:8]}"
@@ -87,3 +95,38 @@ def test_hip_qr_multi_tensor_batch_round_trip(vectors):
     out = qr.decode(12, buf, [(P, o, 30, cols, -1) for (T, cols, F, P, _), o in zip(ins, off)], sd).to_host()
     want = np.concatenate([i[2] for i in ins])
     assert out[:len(want)].tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("T", sorted(GRID))
+def test_hip_qr_grid_cfg3_rows(T):
+    """configuration-3 rows (256 x 12288 Student-t, imatrix) of every grid type: prediction = the HIP
+    quantizer's bytes, file = 2% of its blocks perturbed; the stream equals the oracle's and decodes
+    back to the file; a second file from drifted weights round-trips too"""
+    w, imx = synth.tensor(3, 0, rows=256)
+    say("case qr grid cfg3", T)
+    gq = GPUQuant()
+    P = gq.quantize_tensors(T, [(w.reshape(-1), w.shape[1])], [imx])[0]
+    g = np.random.Generator(np.random.PCG64(4321 + T))
+    Fb = P.copy().reshape(-1, qr.BS[T])
+    idx = g.choice(len(Fb), size=len(Fb) // 50, replace=False)
+    Fb[idx, g.integers(0, qr.BS[T], len(idx))] ^= np.uint8(0x21)
+    F = Fb.reshape(-1)
+    sd = dev.DeviceArray.from_host(w.reshape(-1).view(np.uint8))
+    dimx = dev.DeviceArray.from_host(imx)
+    item = (F, P, 0, 30, w.shape[1], 0)
+    res = qr.encode_parts(T, [item], sd, dimx)
+    want = oqr.encode(T, F.tobytes(), P.tobytes(), w.reshape(-1).view(np.uint8).tobytes(), 30, w.shape[1],
+                      imx=imx, gk=qr.grid_keys(T))
+    assert np.array_equal(res["counts"], want["counts"]), "histogram"
+    assert np.array_equal(res["lens"], want["lens"])
+    assert res["stream"].tobytes() == want["stream"].tobytes()
+    buf = qr.encode(T, [item], sd, dimx)
+    back = qr.decode(T, buf, [(P, 0, 30, w.shape[1], 0)], sd, dimx).to_host()[:len(F)]
+    assert back.tobytes() == F.tobytes()
+    # drift: most blocks differ
+    x = synth.bf16_to_f32(w).reshape(w.shape)
+    x2 = (x + g.normal(0, 0.002, x.shape)).astype(np.float32)
+    F2 = gq.quantize_tensors(T, [(x2.reshape(-1), w.shape[1])], [imx])[0]
+    buf = qr.encode(T, [(F2, P, 0, 30, w.shape[1], 0)], sd, dimx)
+    back = qr.decode(T, buf, [(P, 0, 30, w.shape[1], 0)], sd, dimx).to_host()[:len(F2)]
+    assert back.tobytes() == F2.tobytes()
