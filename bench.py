@@ -103,6 +103,17 @@ def profile_pass():
         dev.synchronize()
         log(f"profile: {NAMES[t]} token_embd {w.shape[0]}x{w.shape[1]} x2 launches, "
             f"algorithmic bytes/launch {alg_bytes(t, w.size, w.shape[1], m is not None)}")
+    w3, imx3 = synth.tensor(3, 0)
+    src3 = dev.DeviceArray.from_host(w3.reshape(-1))
+    dimx3 = dev.DeviceArray.from_host(imx3)
+    for t in synth.TYPES[3]:
+        out = dev.DeviceArray(w3.shape[0] * row_size(t, w3.shape[1]), np.uint8)
+        for _ in range(2):
+            quantize_into(t, src3, w3.shape[1], out, dimx3)
+        dev.synchronize()
+        log(f"profile: {NAMES[t]} cfg3 {w3.shape[0]}x{w3.shape[1]} x2 launches, "
+            f"algorithmic bytes/launch {alg_bytes(t, w3.size, w3.shape[1], True)}")
+        del out
     nb = 512 << 20
     a, b = dev.DeviceArray(nb, np.uint8), dev.DeviceArray(nb, np.uint8)
     for _ in range(2):
@@ -142,6 +153,50 @@ def iquant_cfg3(stream, reps=2):
     for k, e in res.items():
         e["GB_s"] = round(e["bf16_bytes"] / (e["ms"] / 1e3) / 1e9, 2)
         e["ms"] = round(e["ms"], 3)
+    return res
+
+
+def qr_cfg3(stream, reps=2):
+    """grid-type residual coding on the configuration-3 4096x12288 tensor: prediction = the HIP
+    quantizer's bytes (imatrix), file = 1% of its blocks perturbed (one byte each); QR encode and
+    decode wall time per call with inputs resident on the device"""
+    from seedpack_amd import device as dev
+    from seedpack_amd import qr, synth
+    from seedpack_amd.gpuquant import quantize_into
+    from seedpack_amd.requant import NAMES, row_size
+    w, imx = synth.tensor(3, 0)
+    sd = dev.DeviceArray.from_host(w.reshape(-1).view(np.uint8), stream.handle)
+    dimx = dev.DeviceArray.from_host(imx, stream.handle)
+    res = {}
+    for t in [17, 16, 18, 19, 29]:
+        P = dev.DeviceArray(w.shape[0] * row_size(t, w.shape[1]), np.uint8)
+        quantize_into(t, sd.view(0, (w.size,), np.uint16), w.shape[1], P, dimx, 0, stream.handle)
+        Ph = P.to_host(stream=stream.handle)
+        g = np.random.Generator(np.random.PCG64(77 + t))
+        Fb = Ph.copy().reshape(-1, qr.BS[t])
+        idx = g.choice(len(Fb), size=len(Fb) // 100, replace=False)
+        Fb[idx, g.integers(0, qr.BS[t], len(idx))] ^= np.uint8(0x21)
+        F = dev.DeviceArray.from_host(Fb.reshape(-1), stream.handle)
+        item = [(F, P, 0, 30, w.shape[1], 0)]
+        parts = qr.encode_parts(t, item, sd, dimx, stream=stream.handle)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            parts = qr.encode_parts(t, item, sd, dimx, stream=stream.handle)
+        enc = (time.perf_counter() - t0) / reps
+        args = (parts["freq"], parts["used"], parts["lens"], parts["stream"].tobytes(), [(P, 0, 30, w.shape[1], 0)], sd, dimx)
+        back = qr.decode_parts(t, *args, stream=stream.handle)
+        stream.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            back = qr.decode_parts(t, *args, stream=stream.handle)
+        stream.synchronize()
+        dec = (time.perf_counter() - t0) / reps
+        ok = back.to_host(stream=stream.handle)[:F.nbytes].tobytes() == Fb.tobytes()
+        res[NAMES[t]] = {"file_bytes": int(F.nbytes), "blocks_differing": int(len(idx)), "coded_bytes": int(len(parts["stream"])),
+                         "encode_ms": round(enc * 1e3, 3), "decode_ms": round(dec * 1e3, 3),
+                         "encode_GB_s_bf16": round(2 * w.size / enc / 1e9, 2),
+                         "decode_GB_s_bf16": round(2 * w.size / dec / 1e9, 2), "round_trip_ok": ok}
+        log(f"bench: qr cfg3 {NAMES[t]}: {res[NAMES[t]]}")
     return res
 
 
@@ -196,7 +251,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-pass", action="store_true",
-                    help="one launch of each kernel (K-quants and Q8_0/Q4_0 on token_embd) plus a 512 MiB copy, "
+                    help="two launches of each kernel (K-quants and Q8_0/Q4_0 on token_embd, the configuration-3 "
+                         "i-quants on its 4096x12288 tensor) plus a 512 MiB copy, "
                          "for rocprofv3 counter runs; prints the launch list, no JSON line")
     a = ap.parse_args()
     if a.profile_pass:
@@ -291,6 +347,7 @@ def main():
 
     iq = iquant_cfg3(stream)
     qrb = qr_cfg1(stream)
+    qrg = qr_cfg3(stream)
     cpu = None if a.no_cpu else cpu_baseline(tensors)
     line = {"metric": "requant GB/s (BF16 in), K-quant family Q2_K..Q6_K with imatrix", "value": round(value, 3),
             "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 3),
@@ -298,7 +355,7 @@ def main():
             "data": "synthetic (seeded N(0,0.02) BF16, LogNormal(0,1) imatrix)",
             "config": {"workload": "cfg2: Q2_K,Q3_K,Q4_K,Q5_K,Q6_K (imatrix) on token_embd 151936x1024 + ffn_down 1024x3072",
                        "bf16_bytes_per_step": bf16_bytes, "launches_per_step": len(launches)},
-            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "qr_cfg1": qrb,
+            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "qr_cfg1": qrb, "qr_cfg3": qrg,
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
 

@@ -123,6 +123,26 @@ int spa_qr_gather(const void* src, uint64_t cap, const uint32_t* len, const uint
  * Replaces build_lut (qr.py:889-895, gpu2.py:273-279). */
 int spa_rans_build_lut(const uint32_t* cum, int ntab, uint8_t* lut, void* stream);
 
+/* ---- difference residual (replaces the host-side chunked numpy stage of repo3.py:456-510) ---- */
+
+/* dst = a ^ b over n bytes (dst may be a). nonzero: optional device u64 set to the number of
+ * non-zero bytes of dst. Replaces _xor_async / _xor_chunk (repo3.py:456-467). */
+int spa_xor(void* dst, const void* a, const void* b, size_t n, unsigned long long* nonzero, void* stream);
+
+/* dst = a ^ b ^ c and its non-zero byte count: the residual a file region holding file ^ p0 would
+ * have with prediction c instead. Replaces _xor3 (repo3.py:494-504). */
+int spa_xor3(void* dst, const void* a, const void* b, const void* c, size_t n, unsigned long long* nonzero,
+             void* stream);
+
+/* *count (device u64) = number of bytes where a and b differ (b NULL: non-zero bytes of a).
+ * Replaces _count_diff / _diff_async (repo3.py:476-491). */
+int spa_diff_count(const void* a, const void* b, size_t n, unsigned long long* count, void* stream);
+
+/* Float-tensor prediction from the base weights (src_kind SPA_SRC_*): n values written as the file's
+ * type dst_type = 0 (F32), 1 (F16, round to nearest even) or 30 (BF16, (u + 0x7FFF + ((u >> 16) & 1))
+ * >> 16). Replaces _float_dev (repo3.py:673-689). */
+int spa_float_pred(const void* src, int src_kind, int64_t n, int dst_type, void* dst, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

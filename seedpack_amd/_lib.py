@@ -51,6 +51,10 @@ SIGNATURES = {
                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "spa_qr_gather": (c_int, [c_void_p, ctypes.c_uint64, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "spa_rans_build_lut": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
+    "spa_xor": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "spa_xor3": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "spa_diff_count": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "spa_float_pred": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p]),
 }
 
 

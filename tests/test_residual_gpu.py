@@ -1,0 +1,141 @@
+"""The device residual stage (spa_xor / spa_xor3 / spa_diff_count / spa_float_pred and the
+per-tensor variant choice) on the MI355X, against numpy on the host."""
+import sys
+
+import numpy as np
+import pytest
+
+from seedpack_amd import device as dev
+from seedpack_amd import residual as r
+from seedpack_amd import synth
+from seedpack_amd.gpuquant import GPUQuant
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+@pytest.mark.parametrize("n,off", [(0, 0), (1, 0), (17, 0), (4096, 0), (4096, 3), (1 << 20, 0), ((1 << 20) + 5, 1)])
+def test_xor_and_counts(n, off):
+    say("case residual kernels", n, off)
+    g = np.random.Generator(np.random.PCG64(n + off))
+    a, b, c = (g.integers(0, 256, n + off, dtype=np.uint8) for _ in range(3))
+    b[: (n + off) // 2] = a[: (n + off) // 2]                             # half the bytes equal
+    da, db, dc = (dev.DeviceArray.from_host(x) for x in (a, b, c))
+    va, vb, vc = (x.view(off, (n,), np.uint8) for x in (da, db, dc))
+    want = a[off:] ^ b[off:]
+    assert r.diff_count(va, vb) == int(np.count_nonzero(want))
+    assert r.diff_count(va) == int(np.count_nonzero(a[off:]))
+    dst = dev.DeviceArray(n + off, np.uint8).view(off, (n,), np.uint8)
+    assert r.xor_into(dst, va, vb) == int(np.count_nonzero(want))
+    assert np.array_equal(dst.to_host(), want)
+    w3 = want ^ c[off:]
+    assert r.xor3_into(dst, va, vb, vc) == int(np.count_nonzero(w3))
+    assert np.array_equal(dst.to_host(), w3)
+    assert r.xor_into(va, va, vb) == int(np.count_nonzero(want))         # in place
+    assert np.array_equal(va.to_host(), want)
+
+
+def test_float_predictions():
+    g = np.random.Generator(np.random.PCG64(8))
+    x = np.concatenate([g.normal(0, 1, 5000), [0.0, -0.0, 65504.0, 65520.0, 1e5, -1e5, 6e-8, 1e-9, np.inf, -np.inf]])
+    b = synth.bf16_bits(x.astype(np.float32))
+    xf = synth.bf16_to_f32(b)
+    src = dev.DeviceArray.from_host(b)
+    assert r.float_prediction(src, r.F32).to_host().view(np.float32).tobytes() == xf.tobytes()
+    assert r.float_prediction(src, r.F16).to_host().view(np.uint16).tobytes() == xf.astype(np.float16).view(np.uint16).tobytes()
+    u = xf.view(np.uint32).astype(np.uint64)
+    want = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    assert r.float_prediction(src, r.BF16).to_host().view(np.uint16).tobytes() == want.tobytes()
+    # F32 weights to BF16: the rounding formula on values that are not BF16 already
+    x32 = g.normal(0, 1, 4096).astype(np.float32)
+    u = x32.view(np.uint32).astype(np.uint64)
+    want = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    got = r.float_prediction(dev.DeviceArray.from_host(x32), r.BF16).to_host().view(np.uint16)
+    assert got.tobytes() == want.tobytes()
+
+
+def _case(t_type, rows=64, cols=1024, seed=3):
+    g = np.random.Generator(np.random.PCG64(seed + t_type))
+    w = synth.student_t_bf16(g, (rows, cols)) if t_type in (16, 17, 18, 19, 21, 22, 29) else synth.normal_bf16(g, (rows, cols), 0.02)
+    imx = g.lognormal(0, 1, cols).astype(np.float32)
+    return g, w, imx
+
+
+def _tensor(t_type, file_bytes, w, imx, cols):
+    region = dev.DeviceArray.from_host(file_bytes)
+    base = dev.DeviceArray.from_host(w.reshape(-1))
+    return r.Tensor("t", t_type, cols, region, base, imatrix=imx), region
+
+
+def test_exact_prediction_leaves_zero_residual():
+    gq = GPUQuant()
+    _, w, imx = _case(12)
+    f = gq.quantize_tensors(12, [(w.reshape(-1), 1024)], [imx])[0]
+    t, region = _tensor(12, f, w, imx, 1024)
+    out = r.residual_tensor(t, gq)
+    assert out["kind"] == "rq" and out["variant"] == 0 and not out["nonzero"] and not out["qr"]
+    assert not region.to_host().any()
+
+
+def test_perturbed_goes_to_qr_with_file_bytes_kept():
+    gq = GPUQuant()
+    g, w, imx = _case(12)
+    p = gq.quantize_tensors(12, [(w.reshape(-1), 1024)], [imx])[0]
+    f = p.copy()
+    idx = g.choice(f.size, 40, replace=False)
+    f[idx] ^= 0x11
+    t, region = _tensor(12, f, w, imx, 1024)
+    out = r.residual_tensor(t, gq)
+    assert out["qr"] and out["kind"] == "qr" and out["diff_bytes"] == 40
+    assert region.to_host().tobytes() == f.tobytes()
+    assert out["prediction"].to_host().tobytes() == p.tobytes()
+    # without the QR coder: the XOR residual in place
+    t, region = _tensor(12, f, w, imx, 1024)
+    out = r.residual_tensor(t, gq, use_qr=False)
+    assert out["kind"] == "rq" and out["nonzero"] and not out["qr"]
+    assert region.to_host().tobytes() == (f ^ p).tobytes()
+
+
+def test_iq1_m_older_variant_is_found():
+    """the two IQ1_M searches rarely disagree: configuration 3's first 64 rows hold one such block"""
+    gq = GPUQuant()
+    w, imx = synth.tensor(3, 0, rows=64)
+    cols = w.shape[1]
+    f = gq.quantize_tensors(29, [(w.reshape(-1), cols)], [imx], variant=1)[0]
+    assert f.tobytes() != gq.quantize_tensors(29, [(w.reshape(-1), cols)], [imx])[0].tobytes()
+    t, region = _tensor(29, f, w, imx, cols)
+    out = r.residual_tensor(t, gq)
+    assert out["variant"] == 1 and not out["nonzero"] and not region.to_host().any()
+    # through the XOR route: file ^ p0 ^ p1 = 0 after the retry
+    t, region = _tensor(29, f, w, imx, cols)
+    out = r.residual_tensor(t, gq, use_qr=False)
+    assert out["variant"] == 1 and not out["nonzero"] and not region.to_host().any()
+
+
+def test_no_imatrix_tries_unit_weights_then_unweighted():
+    gq = GPUQuant()
+    _, w, _ = _case(14)
+    f = gq.quantize_tensors(14, [(w.reshape(-1), 1024)], [None])[0]     # the file made without imatrix
+    t, region = _tensor(14, f, w, None, 1024)
+    out = r.residual_tensor(t, gq)
+    assert out["variant"] == 0 and not out["nonzero"] and not region.to_host().any()
+    ones = gq.quantize_tensors(14, [(w.reshape(-1), 1024)], [np.ones(1024, np.float32)])[0]
+    t, region = _tensor(14, ones, w, None, 1024)                           # made with unit weights
+    out = r.residual_tensor(t, gq)
+    assert out["variant"] == r.UNIT_W and not out["nonzero"]
+
+
+def test_float_tensor_xor():
+    gq = GPUQuant()
+    _, w, _ = _case(1)
+    x = synth.bf16_to_f32(w).reshape(-1)
+    f = x.astype(np.float16).view(np.uint8).copy()
+    f[7] ^= 1
+    t = r.Tensor("n", r.F16, 1024, dev.DeviceArray.from_host(f), dev.DeviceArray.from_host(w.reshape(-1)))
+    out = r.residual_tensor(t, gq)
+    assert out["kind"] == "xor" and out["nonzero"]
+    res = t.region.to_host()
+    assert np.flatnonzero(res).tolist() == [7] and res[7] == 1
