@@ -143,6 +143,43 @@ int spa_diff_count(const void* a, const void* b, size_t n, unsigned long long* c
  * >> 16). Replaces _float_dev (repo3.py:673-689). */
 int spa_float_pred(const void* src, int src_kind, int64_t n, int dst_type, void* dst, void* stream);
 
+/* ---- R2 BF16 base codec (replaces the kernels and statistics of bf16v2.py:24-155, :225-271) ----
+ * TB descriptors are 32 bytes {i64 doff, i32 rowlen, rowbase, colbase, tab, rmap, pad} and SG 16 bytes
+ * {i32 t, n, i64 i0}, the layout of bf16v2.py:157-158 TB_DT / SG_DT; segments of 16384 weights. */
+
+/* Side information of one tensor of BF16 bits (nrows x rowlen): rfi[nrows], cfi[rowlen], scl[rowlen]
+ * (BF16v2._stats, bf16v2.py:225-244, with detmath.py's sums, log2 and exp2); row_hash[nrows] (optional)
+ * the 64-bit row fingerprints (row_hash kernel, bf16v2.py:148-155); rfa_work: nrows floats of
+ * workspace; rf_out (optional): the float64 log2 row RMS. */
+int spa_r2_stats(const void* w, int64_t nrows, int rowlen, int16_t* rfi, int16_t* cfi, int8_t* scl, uint64_t* row_hash,
+                 float* rfa_work, double* rf_out, void* stream);
+
+/* Context counts of the coded weights of nseg segments (v2_hist, bf16v2.py:54-75); counts has
+ * (roles x 656) rows of 256 u32 and is added to. */
+int spa_r2_hist(const void* dev, const void* tb, const void* sg, int nseg, const int16_t* rfi, const int16_t* cfi,
+                const int8_t* scl, const int32_t* rowmap, uint32_t* counts, void* stream);
+
+/* rANS encode of nseg segments (v2_enc, bf16v2.py:77-111): slot s of `out` (cap bytes) ends with the
+ * segment's bytes, out_len[s] their count (0xFFFFFFFF: overflow). fc_work: nseg x 16384 x 3 u32 of
+ * workspace. */
+int spa_r2_encode(const void* dev, const void* tb, const void* sg, int nseg, const int16_t* rfi, const int16_t* cfi,
+                  const int8_t* scl, const int32_t* rowmap, const int32_t* remap, const uint16_t* freq,
+                  const uint32_t* cum, uint32_t* fc_work, void* out, uint64_t cap, uint32_t* out_len, void* stream);
+
+/* rANS decode of nseg segments into dev (v2_dec, bf16v2.py:113-137); lut from spa_rans_build_lut_pb
+ * with pb = 15. */
+int spa_r2_decode(const void* in, const uint64_t* in_off, void* dev, const void* tb, const void* sg, int nseg,
+                  const int16_t* rfi, const int16_t* cfi, const int8_t* scl, const int32_t* rowmap,
+                  const int32_t* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* stream);
+
+/* Duplicate rows restored from their sources: rows pairs[2i] = rows pairs[2i+1] of a tensor of rowlen
+ * BF16 weights per row (bf16v2.py:471-476). */
+int spa_r2_copy_rows(void* w, int rowlen, const int64_t* pairs, int npairs, void* stream);
+
+/* Decode lookup tables for precision pb (2^pb slots per table); spa_rans_build_lut is pb = 12.
+ * Replaces build_lut (bf16v2.py:139-145). */
+int spa_rans_build_lut_pb(const uint32_t* cum, int ntab, int pb, uint8_t* lut, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
