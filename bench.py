@@ -200,6 +200,37 @@ def qr_cfg3(stream, reps=2):
     return res
 
 
+def r2_layer(stream):
+    """R2 BF16 base codec on a Qwen-9B-shaped block's attn_q (4096x4096) and ffn_down (12288x4096)
+    BF16 weights (134 MB, N(0, 0.02)), as configuration 4 applies it to the base: compress (statistics,
+    duplicate check, histogram, tables, coding, gather) and decompress, wall time per call"""
+    from seedpack_amd import r2, synth
+    g = np.random.Generator(np.random.PCG64(0x5EED0040))
+    wq = synth.normal_bf16(g, (4096, 4096), 0.02)
+    wd = synth.normal_bf16(g, (4096, 12288), 0.02)
+    hdr = b"\0" * 4096
+    data = hdr + wq.tobytes() + wd.tobytes()
+    layout = r2.layout_of([("blk.0.attn_q.weight", 4096, wq.nbytes, 4096),
+                           ("blk.0.ffn_down.weight", 4096 + wq.nbytes, wd.nbytes, 12288)], len(data))
+    codec = r2.BF16v2(stream=stream.handle)
+    parts = codec.compress(data, layout)
+    t0 = time.perf_counter()
+    parts = codec.compress(data, layout)
+    enc = time.perf_counter() - t0
+    out = codec.decompress(parts)
+    t0 = time.perf_counter()
+    out = codec.decompress(parts)
+    dec = time.perf_counter() - t0
+    nb = wq.nbytes + wd.nbytes
+    ok = out[4096:].tobytes() == data[4096:]
+    res = {"bf16_bytes": nb, "coded_bytes": len(parts["stream"]), "ratio": round(len(parts["stream"]) / nb, 4),
+           "compress_s": round(enc, 3), "decompress_s": round(dec, 3), "compress_GB_s": round(nb / enc / 1e9, 3),
+           "decompress_GB_s": round(nb / dec / 1e9, 3), "round_trip_ok": ok,
+           "note": "host<->device copies included (the file is read from and written to host memory)"}
+    log(f"bench: r2 {res}")
+    return res
+
+
 def qr_cfg1(stream, reps=3):
     """configuration 1 residual coding: Q8_0 / Q4_0 of the 3072x1024 tensor as the prediction, the file
     is that with 1% of its blocks perturbed (one byte each); QR encode (histogram, tables, coding, gather)
@@ -348,6 +379,7 @@ def main():
     iq = iquant_cfg3(stream)
     qrb = qr_cfg1(stream)
     qrg = qr_cfg3(stream)
+    r2b = r2_layer(stream)
     cpu = None if a.no_cpu else cpu_baseline(tensors)
     line = {"metric": "requant GB/s (BF16 in), K-quant family Q2_K..Q6_K with imatrix", "value": round(value, 3),
             "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 3),
@@ -355,7 +387,7 @@ def main():
             "data": "synthetic (seeded N(0,0.02) BF16, LogNormal(0,1) imatrix)",
             "config": {"workload": "cfg2: Q2_K,Q3_K,Q4_K,Q5_K,Q6_K (imatrix) on token_embd 151936x1024 + ffn_down 1024x3072",
                        "bf16_bytes_per_step": bf16_bytes, "launches_per_step": len(launches)},
-            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "qr_cfg1": qrb, "qr_cfg3": qrg,
+            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "qr_cfg1": qrb, "qr_cfg3": qrg, "r2_base": r2b,
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
 

@@ -24,7 +24,10 @@ def lib():
         err = None
         for p in _candidates():
             try:
-                L = ctypes.CDLL(p)
+                # a second libzstd may already be in the global scope (profilers and runtimes link
+                # the system one): bind this copy's internal calls to itself, or its entry points
+                # call into the other version's functions with this version's structures
+                L = ctypes.CDLL(p, mode=os.RTLD_LOCAL | getattr(os, "RTLD_DEEPBIND", 0))
                 break
             except OSError as e:
                 err = e
