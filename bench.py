@@ -231,6 +231,71 @@ def r2_layer(stream):
     return res
 
 
+def cfg4_matrices(layers=36):
+    """configuration 4's 2-D BF16 matrices (name, rows, row length): 36 Qwen3.5-9B-shaped blocks and
+    the 151936-row embedding and output, 8,190,427,136 weights"""
+    t = []
+    for b in range(layers):
+        for name, rows, rl in (("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 4096),
+                               ("attn_output", 4096, 4096), ("ffn_gate", 12288, 4096), ("ffn_up", 12288, 4096),
+                               ("ffn_down", 4096, 12288)):
+            t.append((f"blk.{b}.{name}.weight", rows, rl))
+    return [("token_embd.weight", 151936, 4096)] + t + [("output.weight", 151936, 4096)]
+
+
+def r2_cfg4(stream, layers=36):
+    """R2 BF16 base codec on configuration 4's whole base (every 2-D matrix, 16.4 GB), generated in
+    HBM (N(0, 0.02), a counter-based generator per tensor): compress of the resident file and
+    decompress back into HBM, wall time per call (the coded stream is read back to / sent from host
+    memory, the contract of the reference's compress_parts / decompress), plus the device phases
+    timed with HIP events on the stream; round trip checked on the device"""
+    from seedpack_amd import device as dev
+    from seedpack_amd import r2, residual
+    from seedpack_amd._lib import check, lib
+    mats = cfg4_matrices(layers)
+    pos, ts = 4096, []
+    for name, rows, rl in mats:
+        pos += (-pos) % 32
+        ts.append((name, pos, rows * rl * 2, rl))
+        pos += rows * rl * 2
+    layout = r2.layout_of(ts, pos)
+    d = dev.DeviceArray(pos, np.uint8).zero(stream.handle)
+    for k, (name, off, nb, rl) in enumerate(ts):
+        check(lib().spa_synth_normal_bf16(d.ptr + off, nb // 2, 0x5EED0040 + k, 0.02, stream.handle))
+    stream.synchronize()
+    nb_all = sum(t[2] for t in ts)
+    codec = r2.BF16v2(stream=stream.handle, timing=True)
+    warm = r2.layout_of(ts[1:8], ts[7][1] + ts[7][2])          # one block: loads the kernels
+    codec.decompress(codec.compress(d, warm), device=True)
+    t0 = time.perf_counter()
+    parts = codec.compress(d, layout)
+    enc = time.perf_counter() - t0
+    enc_ph = codec.last_timing
+    del parts["arrays"]
+    t0 = time.perf_counter()
+    back = codec.decompress(parts, device=True)
+    dec = time.perf_counter() - t0
+    dec_ph = codec.last_timing
+    bad = sum(residual.diff_count(d.view(off, (nb,), np.uint8), back.view(off, (nb,), np.uint8), stream.handle)
+              for _, off, nb, _ in ts)
+    coded = len(parts["stream"])
+    enc_dev = sum(enc_ph.values()) / 1e3
+    dec_dev = sum(dec_ph.values()) / 1e3
+    res = {"workload": f"cfg4 base: {len(ts)} matrices ({layers} blocks + token_embd + output)", "bf16_bytes": nb_all,
+           "segments": nb_all // 2 // r2.SEG, "coded_bytes": coded, "ratio": round(coded / nb_all, 4),
+           "compress_s": round(enc, 3), "decompress_s": round(dec, 3),
+           "compress_GB_s": round(nb_all / enc / 1e9, 2), "decompress_GB_s": round(nb_all / dec / 1e9, 2),
+           "compress_device_ms": {k: round(v, 2) for k, v in enc_ph.items()},
+           "decompress_device_ms": {k: round(v, 2) for k, v in dec_ph.items()},
+           "compress_device_GB_s": round(nb_all / enc_dev / 1e9, 2), "decompress_device_GB_s": round(nb_all / dec_dev / 1e9, 2),
+           "round_trip_bytes_differing": int(bad),
+           "note": "wall includes the per-tensor statistics readback, host table normalisation and the stream's "
+                   "host transfers; *_device_* sums the kernel phases"}
+    log(f"bench: r2 cfg4 {res}")
+    del back, d
+    return res
+
+
 def qr_cfg1(stream, reps=3):
     """configuration 1 residual coding: Q8_0 / Q4_0 of the 3072x1024 tensor as the prediction, the file
     is that with 1% of its blocks perturbed (one byte each); QR encode (histogram, tables, coding, gather)
@@ -285,9 +350,20 @@ def main():
                     help="two launches of each kernel (K-quants and Q8_0/Q4_0 on token_embd, the configuration-3 "
                          "i-quants on its 4096x12288 tensor) plus a 512 MiB copy, "
                          "for rocprofv3 counter runs; prints the launch list, no JSON line")
+    ap.add_argument("--codecs", action="store_true",
+                    help="only the coding stages (QR on configurations 1 and 3, the R2 base codec), for rocprofv3 "
+                         "kernel-trace runs; prints their results, no JSON line")
     a = ap.parse_args()
     if a.profile_pass:
         return profile_pass()
+    if a.codecs:
+        from seedpack_amd import device as dev
+        stream = dev.Stream()
+        qr_cfg1(stream)
+        qr_cfg3(stream)
+        r2_layer(stream)
+        r2_cfg4(stream)
+        return None
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the path shards by rows "
               "with no exchange, so N GPUs is N independent copies of this run", file=sys.stderr)
@@ -380,6 +456,7 @@ def main():
     qrb = qr_cfg1(stream)
     qrg = qr_cfg3(stream)
     r2b = r2_layer(stream)
+    r2c = r2_cfg4(stream)
     cpu = None if a.no_cpu else cpu_baseline(tensors)
     line = {"metric": "requant GB/s (BF16 in), K-quant family Q2_K..Q6_K with imatrix", "value": round(value, 3),
             "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 3),
@@ -387,7 +464,7 @@ def main():
             "data": "synthetic (seeded N(0,0.02) BF16, LogNormal(0,1) imatrix)",
             "config": {"workload": "cfg2: Q2_K,Q3_K,Q4_K,Q5_K,Q6_K (imatrix) on token_embd 151936x1024 + ffn_down 1024x3072",
                        "bf16_bytes_per_step": bf16_bytes, "launches_per_step": len(launches)},
-            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "qr_cfg1": qrb, "qr_cfg3": qrg, "r2_base": r2b,
+            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "qr_cfg1": qrb, "qr_cfg3": qrg, "r2_base": r2b, "r2_cfg4": r2c,
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
 

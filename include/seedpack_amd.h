@@ -51,11 +51,16 @@ int spa_device_synchronize(void);
 int spa_event_create(void** event);
 int spa_event_destroy(void* event);
 int spa_event_record(void* event, void* stream);
+/* Work queued on `stream` after this call waits for `event`'s last record. */
+int spa_stream_wait_event(void* stream, void* event);
 int spa_event_elapsed_ms(float* ms, void* start, void* stop);
 int spa_mem_info(size_t* free_bytes, size_t* total_bytes);
 /* Device-to-device copy by a plain streaming kernel (16-byte multiples); the HBM yardstick the
  * traffic counters of the other kernels are scaled against. No reference counterpart. */
 int spa_copy(void* dst, const void* src, size_t nbytes, void* stream);
+/* n synthetic BF16 weights N(0, std) written in place from a counter-based hash of (seed, index), for
+ * benchmark inputs generated on the device. No reference counterpart. */
+int spa_synth_normal_bf16(void* dst, int64_t n, uint64_t seed, float std, void* stream);
 
 /* ---- quantizers ---- */
 
@@ -145,14 +150,19 @@ int spa_float_pred(const void* src, int src_kind, int64_t n, int dst_type, void*
 
 /* ---- R2 BF16 base codec (replaces the kernels and statistics of bf16v2.py:24-155, :225-271) ----
  * TB descriptors are 32 bytes {i64 doff, i32 rowlen, rowbase, colbase, tab, rmap, pad} and SG 16 bytes
- * {i32 t, n, i64 i0}, the layout of bf16v2.py:157-158 TB_DT / SG_DT; segments of 16384 weights. */
+ * {i32 t, n, i64 i0}, the layout of bf16v2.py:157-158 TB_DT / SG_DT; segments of 16384 weights.
+ * TB.pad, unused by the reference, is read by spa_r2_hist only: the first of the 64 exponent contexts
+ * it counts in LDS (clamped to 0..448); any value gives the same counts. */
 
 /* Side information of one tensor of BF16 bits (nrows x rowlen): rfi[nrows], cfi[rowlen], scl[rowlen]
  * (BF16v2._stats, bf16v2.py:225-244, with detmath.py's sums, log2 and exp2); row_hash[nrows] (optional)
- * the 64-bit row fingerprints (row_hash kernel, bf16v2.py:148-155); rfa_work: nrows floats of
- * workspace; rf_out (optional): the float64 log2 row RMS. */
+ * the 64-bit row fingerprints (row_hash kernel, bf16v2.py:148-155); work: device workspace of
+ * work_bytes >= spa_r2_stats_work_bytes(nrows, rowlen); rf_out (optional): the float64 log2 row RMS.
+ * Launches only, on `stream`: tensors given different streams overlap. */
 int spa_r2_stats(const void* w, int64_t nrows, int rowlen, int16_t* rfi, int16_t* cfi, int8_t* scl, uint64_t* row_hash,
-                 float* rfa_work, double* rf_out, void* stream);
+                 void* work, uint64_t work_bytes, double* rf_out, void* stream);
+/* Workspace bytes spa_r2_stats needs for a tensor of nrows x rowlen (0 for an empty one). */
+uint64_t spa_r2_stats_work_bytes(int64_t nrows, int rowlen);
 
 /* Context counts of the coded weights of nseg segments (v2_hist, bf16v2.py:54-75); counts has
  * (roles x 656) rows of 256 u32 and is added to. */
@@ -166,11 +176,17 @@ int spa_r2_encode(const void* dev, const void* tb, const void* sg, int nseg, con
                   const int8_t* scl, const int32_t* rowmap, const int32_t* remap, const uint16_t* freq,
                   const uint32_t* cum, uint32_t* fc_work, void* out, uint64_t cap, uint32_t* out_len, void* stream);
 
-/* rANS decode of nseg segments into dev (v2_dec, bf16v2.py:113-137); lut from spa_rans_build_lut_pb
- * with pb = 15. */
+/* rANS decode of nseg segments into dev (v2_dec, bf16v2.py:113-137); dtab from
+ * spa_r2_build_dec_tables (the reference decodes through build_lut's 2^15-entry tables,
+ * bf16v2.py:139-145; these give the same symbols). */
 int spa_r2_decode(const void* in, const uint64_t* in_off, void* dev, const void* tb, const void* sg, int nseg,
                   const int16_t* rfi, const int16_t* cfi, const int8_t* scl, const int32_t* rowmap,
-                  const int32_t* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* stream);
+                  const int32_t* remap, const uint8_t* dtab, void* stream);
+
+/* Compact decode tables of ntab PB-15 tables (cum: ntab x 257 u32): spa_r2_dec_table_bytes() bytes
+ * each, the symbol at every 128th slot and the cumulative frequencies. */
+int spa_r2_build_dec_tables(const uint32_t* cum, int ntab, uint8_t* dtab, void* stream);
+uint64_t spa_r2_dec_table_bytes(void);
 
 /* Duplicate rows restored from their sources: rows pairs[2i] = rows pairs[2i+1] of a tensor of rowlen
  * BF16 weights per row (bf16v2.py:471-476). */

@@ -14,6 +14,7 @@ _lib = None
 _lock = threading.Lock()
 
 c_void_p, c_int, c_int64, c_size_t, c_float = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+c_uint64 = ctypes.c_uint64
 
 # name -> (restype, argtypes); every symbol of include/seedpack_amd.h
 SIGNATURES = {
@@ -34,9 +35,11 @@ SIGNATURES = {
     "spa_event_create": (c_int, [ctypes.POINTER(c_void_p)]),
     "spa_event_destroy": (c_int, [c_void_p]),
     "spa_event_record": (c_int, [c_void_p, c_void_p]),
+    "spa_stream_wait_event": (c_int, [c_void_p, c_void_p]),
     "spa_event_elapsed_ms": (c_int, [ctypes.POINTER(c_float), c_void_p, c_void_p]),
     "spa_mem_info": (c_int, [ctypes.POINTER(c_size_t), ctypes.POINTER(c_size_t)]),
     "spa_copy": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "spa_synth_normal_bf16": (c_int, [c_void_p, c_int64, c_uint64, c_float, c_void_p]),
     "spa_row_size": (c_size_t, [c_int, c_int64]),
     "spa_type_variants": (c_int, [c_int]),
     "spa_quantize": (c_int, [c_int, c_int, c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
@@ -55,12 +58,16 @@ SIGNATURES = {
     "spa_xor3": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_diff_count": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_float_pred": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p]),
-    "spa_r2_stats": (c_int, [c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "spa_r2_stats": (c_int, [c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p,
+                             c_void_p]),
+    "spa_r2_stats_work_bytes": (c_uint64, [c_int64, c_int]),
     "spa_r2_hist": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "spa_r2_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_uint64, c_void_p, c_void_p]),
     "spa_r2_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
-                              c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+                              c_void_p, c_void_p, c_void_p, c_void_p]),
+    "spa_r2_build_dec_tables": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
+    "spa_r2_dec_table_bytes": (c_uint64, []),
     "spa_r2_copy_rows": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p]),
     "spa_rans_build_lut_pb": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
 }

@@ -82,6 +82,7 @@ int spa_device_synchronize(void) { SPA_HIP_TRY(hipDeviceSynchronize()); return S
 int spa_event_create(void** e) { SPA_HIP_TRY(hipEventCreate((hipEvent_t*)e)); return SPA_OK; }
 int spa_event_destroy(void* e) { SPA_HIP_TRY(hipEventDestroy((hipEvent_t)e)); return SPA_OK; }
 int spa_event_record(void* e, void* s) { SPA_HIP_TRY(hipEventRecord((hipEvent_t)e, (hipStream_t)s)); return SPA_OK; }
+int spa_stream_wait_event(void* s, void* e) { SPA_HIP_TRY(hipStreamWaitEvent((hipStream_t)s, (hipEvent_t)e, 0)); return SPA_OK; }
 int spa_event_elapsed_ms(float* ms, void* a, void* b) {
     SPA_HIP_TRY(hipEventSynchronize((hipEvent_t)b));
     SPA_HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));

@@ -5,6 +5,27 @@
 #include "launch.h"
 
 namespace {
+// Synthetic BF16 weights N(0, std) for benchmark inputs generated in place: a counter-based
+// splitmix64 hash of (seed, index) gives two 24-bit uniforms, Box-Muller's cosine branch a normal
+// deviate, rounded to BF16 to nearest even.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__global__ __launch_bounds__(256) void k_synth_normal_bf16(uint16_t* __restrict__ dst, int64_t n, uint64_t seed, float std) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint64_t h = splitmix64(seed * 0xD1342543DE82EF95ull + (uint64_t)i);
+        const float u1 = ((float)(uint32_t)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+        const float u2 = ((float)(uint32_t)(h & 0xFFFFFFu) + 0.5f) * (1.0f / 16777216.0f);
+        const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2) * std;
+        const uint32_t u = __float_as_uint(z);
+        dst[i] = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+    }
+}
+
 __global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
@@ -19,6 +40,15 @@ extern "C" int spa_copy(void* dst, const void* src, size_t nbytes, void* stream)
     const int64_t blocks = (n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192;
     hipLaunchKernelGGL(k_copy16, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                        (const uint4*)src, (uint4*)dst, n);
+    SPA_HIP_TRY(hipGetLastError());
+    return SPA_OK;
+}
+
+extern "C" int spa_synth_normal_bf16(void* dst, int64_t n, uint64_t seed, float std, void* stream) {
+    if (n < 0 || (n > 0 && !dst)) return spa::fail(SPA_ERR_ARG, "spa_synth_normal_bf16: bad arguments");
+    if (n == 0) return SPA_OK;
+    const int64_t blocks = (n + 255) / 256 < 16384 ? (n + 255) / 256 : 16384;
+    hipLaunchKernelGGL(k_synth_normal_bf16, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (uint16_t*)dst, n, seed, std);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }

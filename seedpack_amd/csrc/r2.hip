@@ -16,8 +16,8 @@
 //     stay coalesced while each lane sums its own row in index order (float64);
 //   * column statistics: one lane per column (loads coalesced across the lanes), chunks of rows
 //     summed as the reference's 16M-weight chunks are;
-//   * histogram: weight-parallel (a workgroup per segment), atomics aggregated across the wave for
-//     the exponent and sign symbols;
+//   * histogram: weight-parallel, counted in LDS per workgroup (a run of segments) and flushed once
+//     per bin with global atomics;
 //   * encode: the table lookups are independent of the coder state, so a weight-parallel pass
 //     writes each symbol's (frequency << 16 | cumulative) word; the serial coder (one lane per
 //     segment, as the format requires) then streams those words;
@@ -97,33 +97,64 @@ __device__ __forceinline__ int16_t to_i16(double v) {
     return (int16_t)(r < -32768.0 ? -32768 : (r > 32767.0 ? 32767 : (r == r ? (int)r : 0)));
 }
 
-// ---- row statistics and fingerprints: 64 rows per workgroup, 64 x 64 tiles through LDS
+// ---- row statistics and fingerprints: a lane per row (its float64 sum and its hash run in index
+// order), 64 rows per workgroup staged through LDS in 64 x 64 tiles. With 16-byte aligned rows the
+// tile is read as 16-byte vectors (eight lanes per 128-byte row piece) and the next tile's loads are
+// issued before the current tile is summed.
 constexpr int RT = 64;
-__global__ __launch_bounds__(RT) void k_rows(const uint16_t* __restrict__ w, int64_t nr, int rl, int16_t* __restrict__ rfi,
+__device__ __forceinline__ void row_step(uint32_t u, double& s, uint64_t& h) {
+    const double v = (double)__uint_as_float(u << 16);
+    s = s + v * v;
+    h ^= u;
+    h *= 1099511628211ull;
+    h ^= h >> 29;
+}
+__global__ __launch_bounds__(RT) void k_rows(const uint16_t* __restrict__ w, int64_t nr, int rl, int vec, int16_t* __restrict__ rfi,
                                              float* __restrict__ rfa, uint64_t* __restrict__ hash, double* __restrict__ rf_out) {
-    __shared__ uint16_t tile[RT][RT + 2];
+    __shared__ uint32_t tile[RT][RT / 2 + 1];
     const int lane = threadIdx.x;
     const int64_t r0 = (int64_t)blockIdx.x * RT, row = r0 + lane;
     double s = 0.0;
     uint64_t h = 1469598103934665603ull;
-    for (int c0 = 0; c0 < rl; c0 += RT) {
-        const int nc = rl - c0 < RT ? rl - c0 : RT;
-        for (int i = 0; i < RT; ++i) {
-            const int64_t r = r0 + i;
-            if (r < nr && lane < nc) tile[i][lane] = w[r * rl + c0 + lane];
+    const int nfull = vec ? rl / RT : 0;                 // tiles read as vectors
+    uint4 v[8];
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int64_t r = r0 + (lane >> 3) + 8 * k;
+            v[k] = r < nr ? *reinterpret_cast<const uint4*>(w + r * rl + c0 + (lane & 7) * 8) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    if (nfull) load(0);
+    for (int t = 0; t < nfull; ++t) {
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            uint32_t* d = &tile[(lane >> 3) + 8 * k][(lane & 7) * 4];
+            d[0] = v[k].x; d[1] = v[k].y; d[2] = v[k].z; d[3] = v[k].w;
         }
         __syncthreads();
+        if (t + 1 < nfull) load((t + 1) * RT);
         if (row < nr) {
-            for (int j = 0; j < nc; ++j) {
-                const uint32_t u = tile[lane][j];
-                const double v = (double)__uint_as_float(u << 16);
-                s = s + v * v;
-                h ^= u;
-                h *= 1099511628211ull;
-                h ^= h >> 29;
+#pragma unroll 8
+            for (int j = 0; j < RT / 2; ++j) {
+                const uint32_t pr = tile[lane][j];
+                row_step(pr & 0xFFFFu, s, h);
+                row_step(pr >> 16, s, h);
             }
         }
+    }
+    uint16_t* t16 = reinterpret_cast<uint16_t*>(&tile[0][0]);
+    for (int c0 = nfull * RT; c0 < rl; c0 += RT) {       // rows not 16-byte aligned, and the last partial tile
+        const int nc = rl - c0 < RT ? rl - c0 : RT;
         __syncthreads();
+        for (int i = 0; i < RT; ++i) {
+            const int64_t r = r0 + i;
+            if (r < nr && lane < nc) t16[i * (RT + 2) + lane] = w[r * rl + c0 + lane];
+        }
+        __syncthreads();
+        if (row < nr)
+            for (int j = 0; j < nc; ++j) row_step(t16[lane * (RT + 2) + j], s, h);
     }
     if (row < nr) {
         const double rf = dm_log2(sqrt(s / (double)rl) + 1e-30);
@@ -134,23 +165,52 @@ __global__ __launch_bounds__(RT) void k_rows(const uint16_t* __restrict__ w, int
     }
 }
 
-// ---- column statistics: one lane per column, rows in chunks of `step` (bf16v2.py:234-238)
-__global__ __launch_bounds__(256) void k_cols(const uint16_t* __restrict__ w, int64_t nr, int rl, int64_t step,
-                                              const float* __restrict__ rfa, int16_t* __restrict__ cfi, int8_t* __restrict__ scl) {
+// ---- column statistics (bf16v2.py:234-238): the reference adds each chunk's column sums, taken
+// in row order, to running totals in chunk order. The chunks are independent, so one launch takes
+// every (chunk, column) pair, a lane summing its column over the chunk's rows with 32 rows'
+// loads issued ahead of their adds; a second pass adds the chunk sums in order per column.
+constexpr int CPF = 32;
+__global__ __launch_bounds__(256) void k_cols_part(const uint16_t* __restrict__ w, int64_t nr, int rl, int64_t step,
+                                                   int64_t nch, const float* __restrict__ rfa, double* __restrict__ part) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= rl) return;
-    double s2 = 0.0, s1 = 0.0;
-    for (int64_t r0 = 0; r0 < nr; r0 += step) {
-        const int64_t r1 = r0 + step < nr ? r0 + step : nr;
+    for (int64_t ch = blockIdx.y; ch < nch; ch += gridDim.y) {
+        const int64_t r0 = ch * step, r1 = r0 + step < nr ? r0 + step : nr;
         double c2 = 0.0, c1 = 0.0;
-        for (int64_t r = r0; r < r1; ++r) {
-            const float x = __uint_as_float((uint32_t)w[r * rl + c] << 16) / rfa[r];
-            const double v = (double)x;
+        int64_t r = r0;
+        for (; r + CPF <= r1; r += CPF) {
+            uint32_t u[CPF];
+            float a[CPF];
+#pragma unroll
+            for (int i = 0; i < CPF; ++i) {
+                u[i] = w[(r + i) * rl + c];
+                a[i] = rfa[r + i];
+            }
+#pragma unroll
+            for (int i = 0; i < CPF; ++i) {
+                const double v = (double)(__uint_as_float(u[i] << 16) / a[i]);
+                c2 = c2 + v * v;
+                c1 = c1 + v;
+            }
+        }
+        for (; r < r1; ++r) {
+            const double v = (double)(__uint_as_float((uint32_t)w[r * rl + c] << 16) / rfa[r]);
             c2 = c2 + v * v;
             c1 = c1 + v;
         }
-        s2 = s2 + c2;
-        s1 = s1 + c1;
+        part[(ch * 2) * rl + c] = c2;
+        part[(ch * 2 + 1) * rl + c] = c1;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_cols_fin(const double* __restrict__ part, int64_t nch, int64_t nr, int rl,
+                                                  int16_t* __restrict__ cfi, int8_t* __restrict__ scl) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= rl) return;
+    double s2 = 0.0, s1 = 0.0;
+    for (int64_t ch = 0; ch < nch; ++ch) {
+        s2 = s2 + part[(ch * 2) * rl + c];
+        s1 = s1 + part[(ch * 2 + 1) * rl + c];
     }
     const double cf = dm_log2(sqrt(s2 / (double)nr) + 1e-30);
     const int16_t ci = to_i16(cf * K);
@@ -160,14 +220,36 @@ __global__ __launch_bounds__(256) void k_cols(const uint16_t* __restrict__ w, in
     scl[c] = (int8_t)(fl < 0.0 ? 0 : (fl > 15.0 ? 15 : (fl == fl ? (int)fl : 0)));
 }
 
+// workspace of the statistics: the rows' float scales, then the chunk sums (2 doubles per chunk and column)
+__host__ __device__ inline int64_t stats_step(int rl) { return (16 << 20) / rl > 0 ? (16 << 20) / rl : 1; }
+inline uint64_t stats_rfa_bytes(int64_t nr) { return ((uint64_t)nr * 4 + 255) / 256 * 256; }
+inline uint64_t stats_work_bytes(int64_t nr, int rl) {
+    const int64_t nch = (nr + stats_step(rl) - 1) / stats_step(rl);
+    return stats_rfa_bytes(nr) + (uint64_t)nch * 2 * (uint64_t)rl * 8;
+}
+
 // ---- symbols
-struct Ctx {
-    int pe, rl, sc;
+// Position of a coded weight: compact row rc and column j (a segment's weights run along the compact
+// rows, duplicate rows left out). Set once per thread and segment, then stepped; the division only
+// runs when a step crosses a row end.
+struct Cursor {
+    int64_t rc;
+    int j;
+    __device__ __forceinline__ void start(int64_t idx, int rl) {
+        rc = idx / rl;
+        j = (int)(idx - rc * rl);
+    }
+    __device__ __forceinline__ void step(int s, int rl) {
+        j += s;
+        if (j >= rl) {
+            const int q = j / rl;
+            rc += q;
+            j -= q * rl;
+        }
+    }
 };
-__device__ __forceinline__ void weight_at(const uint8_t* dev, const TB& T, const int32_t* rowmap, int64_t idx, int64_t& orow, int& j) {
-    const int64_t rc = idx / T.rowlen;
-    j = (int)(idx - rc * T.rowlen);
-    orow = T.rmap >= 0 ? rowmap[T.rmap + rc] : rc;
+__device__ __forceinline__ int64_t orig_row(const TB& T, const int32_t* rowmap, int64_t rc) {
+    return T.rmap >= 0 ? rowmap[T.rmap + rc] : rc;
 }
 __device__ __forceinline__ void contexts(const TB& T, int64_t orow, int j, uint32_t u, const int16_t* rfi, const int16_t* cfi,
                                          const int8_t* scl, int& ex, int& man, int& sgn, int& pe, int& rlc, int& sc) {
@@ -180,48 +262,72 @@ __device__ __forceinline__ void contexts(const TB& T, int64_t orow, int j, uint3
     sc = scl[T.colbase + j];
 }
 
-// one workgroup per segment, weight-parallel
-__global__ __launch_bounds__(256) void k_hist(const uint8_t* __restrict__ dev, const TB* __restrict__ tb, const SG* __restrict__ sg,
-                                              const int16_t* __restrict__ rfi, const int16_t* __restrict__ cfi,
-                                              const int8_t* __restrict__ scl, const int32_t* __restrict__ rowmap,
-                                              uint32_t* __restrict__ counts) {
-    const SG g = sg[blockIdx.x];
-    const TB T = tb[g.t];
-    const uint16_t* W = reinterpret_cast<const uint16_t*>(dev + T.doff);
-    for (int k0 = 0; k0 < g.n; k0 += 256) {
-        const int k = k0 + threadIdx.x;
-        const bool on = k < g.n;
-        int ex = 0, man = 0, sgn = 0, pe = 0, rlc = 0, sc = 0;
-        if (on) {
-            int64_t orow;
-            int j;
-            weight_at(dev, T, rowmap, g.i0 + k, orow, j);
-            contexts(T, orow, j, W[orow * T.rowlen + j], rfi, cfi, scl, ex, man, sgn, pe, rlc, sc);
+// Histogram: a workgroup takes a run of consecutive segments and counts into LDS (mantissa 128 x 128,
+// a window of HEW exponent contexts starting at the tensor's TB.pad, sign 16 x 2), flushing the
+// non-zero bins with global atomics when the table block (role, window) changes and at the end.
+// Exponent contexts outside the window count straight into global memory, so any window base gives
+// the same counts.
+constexpr int HT = 1024;            // threads per histogram workgroup
+constexpr int HEW = 64;             // exponent contexts held in LDS
+
+__device__ __forceinline__ void hist_flush(uint32_t* hm, uint32_t* he, uint32_t* hs, int tab, int pe0, uint32_t* counts) {
+    for (int i = threadIdx.x; i < 128 * 128; i += HT) {
+        const uint32_t v = hm[i];
+        if (v) { atomicAdd(&counts[(uint32_t)(tab + 512 + (i >> 7)) * 256 + (i & 127)], v); hm[i] = 0; }
+    }
+    for (int i = threadIdx.x; i < HEW * 256; i += HT) {
+        const uint32_t v = he[i];
+        if (v) { atomicAdd(&counts[(uint32_t)(tab + pe0 + (i >> 8)) * 256 + (i & 255)], v); he[i] = 0; }
+    }
+    if (threadIdx.x < 32) {
+        const uint32_t v = hs[threadIdx.x];
+        if (v) { atomicAdd(&counts[(uint32_t)(tab + 640 + (threadIdx.x >> 1)) * 256 + (threadIdx.x & 1)], v); hs[threadIdx.x] = 0; }
+    }
+}
+
+__global__ __launch_bounds__(HT) void k_hist(const uint8_t* __restrict__ dev, const TB* __restrict__ tb, const SG* __restrict__ sg,
+                                             int nseg, int spw, const int16_t* __restrict__ rfi, const int16_t* __restrict__ cfi,
+                                             const int8_t* __restrict__ scl, const int32_t* __restrict__ rowmap,
+                                             uint32_t* __restrict__ counts) {
+    __shared__ uint32_t hm[128 * 128];
+    __shared__ uint32_t he[HEW * 256];
+    __shared__ uint32_t hs[32];
+    for (int i = threadIdx.x; i < 128 * 128; i += HT) hm[i] = 0;
+    for (int i = threadIdx.x; i < HEW * 256; i += HT) he[i] = 0;
+    if (threadIdx.x < 32) hs[threadIdx.x] = 0;
+    __syncthreads();
+    const int s0 = blockIdx.x * spw, s1 = min(nseg, s0 + spw);
+    int tab = -1, pe0 = 0;
+    for (int s = s0; s < s1; ++s) {
+        const SG g = sg[s];
+        const TB T = tb[g.t];
+        const int wpe = clampi(T.pad, 0, 512 - HEW);
+        if (T.tab != tab || wpe != pe0) {
+            if (tab >= 0) {
+                __syncthreads();
+                hist_flush(hm, he, hs, tab, pe0, counts);
+                __syncthreads();
+            }
+            tab = T.tab;
+            pe0 = wpe;
         }
-        if (on) atomicAdd(&counts[(uint32_t)(T.tab + 512 + rlc) * 256 + man], 1u);
-        const uint32_t ke = on ? (uint32_t)(T.tab + pe) * 256 + ex : 0xffffffffu;
-        const uint32_t ks = on ? (uint32_t)(T.tab + 640 + sc) * 256 + sgn : 0xffffffffu;
-        // wave-aggregated adds for the concentrated exponent and sign symbols
-        {
-            uint64_t pending = __ballot(on);
-            const int lane = __lane_id();
-            while (pending) {
-                const int leader = __ffsll((unsigned long long)pending) - 1;
-                const uint32_t kk = __shfl(ke, leader);
-                const uint64_t same = __ballot(ke == kk) & pending;
-                if (lane == leader) atomicAdd(&counts[kk], (uint32_t)__popcll(same));
-                pending &= ~same;
-            }
-            pending = __ballot(on);
-            while (pending) {
-                const int leader = __ffsll((unsigned long long)pending) - 1;
-                const uint32_t kk = __shfl(ks, leader);
-                const uint64_t same = __ballot(ks == kk) & pending;
-                if (lane == leader) atomicAdd(&counts[kk], (uint32_t)__popcll(same));
-                pending &= ~same;
-            }
+        const uint16_t* W = reinterpret_cast<const uint16_t*>(dev + T.doff);
+        Cursor cur;
+        cur.start(g.i0 + threadIdx.x, T.rowlen);
+        for (int k = threadIdx.x; k < g.n; k += HT, cur.step(HT, T.rowlen)) {
+            int ex, man, sgn, pe, rlc, sc;
+            const int64_t orow = orig_row(T, rowmap, cur.rc);
+            const int j = cur.j;
+            contexts(T, orow, j, W[orow * T.rowlen + j], rfi, cfi, scl, ex, man, sgn, pe, rlc, sc);
+            atomicAdd(&hm[rlc * 128 + man], 1u);
+            const int e = pe - pe0;
+            if ((unsigned)e < (unsigned)HEW) atomicAdd(&he[e * 256 + ex], 1u);
+            else atomicAdd(&counts[(uint32_t)(T.tab + pe) * 256 + ex], 1u);
+            atomicAdd(&hs[sc * 2 + sgn], 1u);
         }
     }
+    __syncthreads();
+    if (tab >= 0) hist_flush(hm, he, hs, tab, pe0, counts);
 }
 
 // the (freq << 16 | cum) word of each of a segment's symbols, in forward order, at fc + s * SEG * 3
@@ -234,10 +340,12 @@ __global__ __launch_bounds__(256) void k_fc(const uint8_t* __restrict__ dev, con
     const TB T = tb[g.t];
     const uint16_t* W = reinterpret_cast<const uint16_t*>(dev + T.doff);
     uint32_t* o = fc + (int64_t)blockIdx.x * SEG * 3;
-    for (int k = threadIdx.x; k < g.n; k += 256) {
-        int64_t orow;
-        int j, ex, man, sgn, pe, rlc, sc;
-        weight_at(dev, T, rowmap, g.i0 + k, orow, j);
+    Cursor cur;
+    cur.start(g.i0 + threadIdx.x, T.rowlen);
+    for (int k = threadIdx.x; k < g.n; k += 256, cur.step(256, T.rowlen)) {
+        int ex, man, sgn, pe, rlc, sc;
+        const int64_t orow = orig_row(T, rowmap, cur.rc);
+        const int j = cur.j;
         contexts(T, orow, j, W[orow * T.rowlen + j], rfi, cfi, scl, ex, man, sgn, pe, rlc, sc);
         const int t0 = remap[T.tab + pe], t1 = remap[T.tab + 512 + rlc], t2 = remap[T.tab + 640 + sc];
         o[3 * k + 0] = ((uint32_t)freq[t0 * 256 + ex] << 16) | cum[t0 * 257 + ex];
@@ -270,12 +378,46 @@ __global__ __launch_bounds__(64) void k_enc(const SG* __restrict__ sg, int nseg,
     out_len[s] = (uint32_t)(end - ptr);
 }
 
+// Decode tables, DT_BYTES per table: the symbol holding slot 128 b for b < 256 (u8), then the
+// cumulative frequencies (257 x u16). A slot's symbol is the coarse entry stepped forward while the
+// next cumulative frequency is still <= the slot: the same symbol as a full 2^15-entry lookup table,
+// from 770 bytes per table instead of 32 KB, so a role's tables stay in the caches.
+constexpr int DT_BYTES = 1024;
+__device__ __forceinline__ int dec_sym(const uint8_t* dt, uint32_t slot, uint32_t& c0, uint32_t& f) {
+    const uint16_t* cum = reinterpret_cast<const uint16_t*>(dt + 256);
+    int s = dt[slot >> 7];
+    uint32_t lo = cum[s], hi = cum[s + 1];
+    while (hi <= slot && s < 255) {
+        ++s;
+        lo = hi;
+        hi = cum[s + 1];
+    }
+    c0 = lo;
+    f = hi - lo;
+    return s;
+}
+
+__global__ __launch_bounds__(256) void k_dtab(const uint32_t* __restrict__ cum, uint8_t* __restrict__ dt) {
+    const uint32_t* c = cum + (size_t)blockIdx.x * 257;
+    uint8_t* o = dt + (size_t)blockIdx.x * DT_BYTES;
+    uint16_t* oc = reinterpret_cast<uint16_t*>(o + 256);
+    for (int i = threadIdx.x; i < 257; i += 256) oc[i] = (uint16_t)(c[i] < 65535u ? c[i] : 65535u);
+    const uint32_t slot = (uint32_t)threadIdx.x << 7;
+    int lo = 0, hi = 256;                       // the last symbol s <= 255 with cum[s] <= slot
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (c[mid] <= slot) lo = mid;
+        else hi = mid;
+    }
+    o[threadIdx.x] = (uint8_t)lo;
+}
+
+// one lane per segment (the format's unit of sequential decoding)
 __global__ __launch_bounds__(64) void k_dec(const uint8_t* __restrict__ in, const uint64_t* __restrict__ in_off,
                                             uint8_t* __restrict__ dev, const TB* __restrict__ tb, const SG* __restrict__ sg,
                                             int nseg, const int16_t* __restrict__ rfi, const int16_t* __restrict__ cfi,
                                             const int8_t* __restrict__ scl, const int32_t* __restrict__ rowmap,
-                                            const int32_t* __restrict__ remap, const uint16_t* __restrict__ freq,
-                                            const uint32_t* __restrict__ cum, const uint8_t* __restrict__ lut) {
+                                            const int32_t* __restrict__ remap, const uint8_t* __restrict__ dtab) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
     const SG g = sg[s];
@@ -284,27 +426,39 @@ __global__ __launch_bounds__(64) void k_dec(const uint8_t* __restrict__ in, cons
     const uint8_t* ptr = in + in_off[s];
     uint32_t x = 0;
     for (int i = 0; i < 4; ++i) x = (x << 8) | *ptr++;
-    auto get = [&](int tab) {
-        const int tt = remap[tab] < 0 ? 0 : remap[tab];            // unused contexts only on damaged streams
+    const int32_t* rm = remap + T.tab;
+    const int16_t* cf = cfi + T.colbase;
+    const int8_t* sc = scl + T.colbase;
+    auto get = [&](int ctx) {
+        const int tt = rm[ctx] < 0 ? 0 : rm[ctx];            // unused contexts only on damaged streams
         const uint32_t slot = x & (PSCALE - 1);
-        const int v = lut[(size_t)tt * PSCALE + slot];
-        x = freq[tt * 256 + v] * (x >> PB) + slot - cum[tt * 257 + v];
+        uint32_t c0, f;
+        const int v = dec_sym(dtab + (size_t)tt * DT_BYTES, slot, c0, f);
+        x = f * (x >> PB) + slot - c0;
         // a valid stream needs at most two bytes here; the cap ends the loop on a damaged one
 #pragma unroll
         for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | *ptr++;
         return v;
     };
+    Cursor cur;
+    cur.start(g.i0, T.rowlen);
+    int64_t orow = orig_row(T, rowmap, cur.rc);
+    int rf = rfi[T.rowbase + orow];
+    uint16_t* Wr = W + orow * T.rowlen;
     for (int k = 0; k < g.n; ++k) {
-        int64_t orow;
-        int j;
-        weight_at(dev, T, rowmap, g.i0 + k, orow, j);
-        const int pred = rfi[T.rowbase + orow] + cfi[T.colbase + j];
-        const int pe = clampi(pred + 256, 0, 511);
-        const int ex = get(T.tab + pe);
-        const int rlc = clampi(8 * ex - pred - 1016 + 64, 0, 127);
-        const int man = get(T.tab + 512 + rlc);
-        const int sgn = get(T.tab + 640 + scl[T.colbase + j]);
-        W[orow * T.rowlen + j] = (uint16_t)((sgn << 15) | (ex << 7) | man);
+        const int j = cur.j;
+        const int pred = rf + cf[j];
+        const int ex = get(clampi(pred + 256, 0, 511));
+        const int man = get(512 + clampi(8 * ex - pred - 1016 + 64, 0, 127));
+        const int sgn = get(640 + sc[j]);
+        Wr[j] = (uint16_t)((sgn << 15) | (ex << 7) | man);
+        if (++cur.j == T.rowlen && k + 1 < g.n) {
+            cur.j = 0;
+            ++cur.rc;
+            orow = orig_row(T, rowmap, cur.rc);
+            rf = rfi[T.rowbase + orow];
+            Wr = W + orow * T.rowlen;
+        }
     }
 }
 
@@ -332,16 +486,28 @@ using namespace spa::r2;
 
 extern "C" {
 
+uint64_t spa_r2_stats_work_bytes(int64_t nrows, int rowlen) {
+    return nrows > 0 && rowlen > 0 ? stats_work_bytes(nrows, rowlen) : 0;
+}
+
 int spa_r2_stats(const void* w, int64_t nrows, int rowlen, int16_t* rfi, int16_t* cfi, int8_t* scl, uint64_t* row_hash,
-                 float* rfa_work, double* rf_out, void* stream) {
+                 void* work, uint64_t work_bytes, double* rf_out, void* stream) {
     if (nrows <= 0 || rowlen <= 0) return fail(SPA_ERR_ARG, "spa_r2_stats: empty tensor");
-    if (!w || !rfi || !cfi || !scl || !rfa_work) return fail(SPA_ERR_ARG, "spa_r2_stats: null pointer");
+    if (!w || !rfi || !cfi || !scl || !work) return fail(SPA_ERR_ARG, "spa_r2_stats: null pointer");
+    if (work_bytes < stats_work_bytes(nrows, rowlen))
+        return fail(SPA_ERR_ARG, "spa_r2_stats: workspace of %llu bytes, %llu needed", (unsigned long long)work_bytes,
+                    (unsigned long long)stats_work_bytes(nrows, rowlen));
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_rows, dim3((unsigned)((nrows + RT - 1) / RT)), dim3(RT), 0, st, (const uint16_t*)w, nrows, rowlen, rfi,
-                       rfa_work, row_hash, rf_out);
-    const int64_t step = (16 << 20) / rowlen > 0 ? (16 << 20) / rowlen : 1;
-    hipLaunchKernelGGL(k_cols, dim3((unsigned)((rowlen + 255) / 256)), dim3(256), 0, st, (const uint16_t*)w, nrows, rowlen, step,
-                       (const float*)rfa_work, cfi, scl);
+    float* rfa = (float*)work;
+    double* part = (double*)((uint8_t*)work + stats_rfa_bytes(nrows));
+    const int vec = (rowlen % 8 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
+    hipLaunchKernelGGL(k_rows, dim3((unsigned)((nrows + RT - 1) / RT)), dim3(RT), 0, st, (const uint16_t*)w, nrows, rowlen, vec,
+                       rfi, rfa, row_hash, rf_out);
+    const int64_t step = stats_step(rowlen), nch = (nrows + step - 1) / step;
+    const unsigned gx = (unsigned)((rowlen + 255) / 256), gy = (unsigned)(nch < 65535 ? nch : 65535);
+    hipLaunchKernelGGL(k_cols_part, dim3(gx, gy), dim3(256), 0, st, (const uint16_t*)w, nrows, rowlen, step, nch,
+                       (const float*)rfa, part);
+    hipLaunchKernelGGL(k_cols_fin, dim3(gx), dim3(256), 0, st, (const double*)part, nch, nrows, rowlen, cfi, scl);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }
@@ -350,8 +516,10 @@ int spa_r2_hist(const void* dev, const void* tb, const void* sg, int nseg, const
                 const int8_t* scl, const int32_t* rowmap, uint32_t* counts, void* stream) {
     if (nseg < 0) return fail(SPA_ERR_ARG, "spa_r2_hist: negative segment count");
     if (nseg == 0) return SPA_OK;
-    hipLaunchKernelGGL(k_hist, dim3((unsigned)nseg), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)dev, (const TB*)tb,
-                       (const SG*)sg, rfi, cfi, scl, rowmap, counts);
+    // about 512 workgroups (two per CU) however many segments, each a run of consecutive segments
+    const int spw = (nseg + 511) / 512;
+    hipLaunchKernelGGL(k_hist, dim3((unsigned)((nseg + spw - 1) / spw)), dim3(HT), 0, (hipStream_t)stream, (const uint8_t*)dev,
+                       (const TB*)tb, (const SG*)sg, nseg, spw, rfi, cfi, scl, rowmap, counts);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }
@@ -372,12 +540,22 @@ int spa_r2_encode(const void* dev, const void* tb, const void* sg, int nseg, con
 }
 
 int spa_r2_decode(const void* in, const uint64_t* in_off, void* dev, const void* tb, const void* sg, int nseg, const int16_t* rfi,
-                  const int16_t* cfi, const int8_t* scl, const int32_t* rowmap, const int32_t* remap, const uint16_t* freq,
-                  const uint32_t* cum, const uint8_t* lut, void* stream) {
+                  const int16_t* cfi, const int8_t* scl, const int32_t* rowmap, const int32_t* remap, const uint8_t* dtab,
+                  void* stream) {
     if (nseg < 0) return fail(SPA_ERR_ARG, "spa_r2_decode: negative segment count");
     if (nseg == 0) return SPA_OK;
     hipLaunchKernelGGL(k_dec, dim3((unsigned)((nseg + 63) / 64)), dim3(64), 0, (hipStream_t)stream, (const uint8_t*)in, in_off,
-                       (uint8_t*)dev, (const TB*)tb, (const SG*)sg, nseg, rfi, cfi, scl, rowmap, remap, freq, cum, lut);
+                       (uint8_t*)dev, (const TB*)tb, (const SG*)sg, nseg, rfi, cfi, scl, rowmap, remap, dtab);
+    SPA_HIP_TRY(hipGetLastError());
+    return SPA_OK;
+}
+
+uint64_t spa_r2_dec_table_bytes(void) { return DT_BYTES; }
+
+int spa_r2_build_dec_tables(const uint32_t* cum, int ntab, uint8_t* dtab, void* stream) {
+    if (ntab < 0) return fail(SPA_ERR_ARG, "spa_r2_build_dec_tables: negative table count");
+    if (ntab == 0) return SPA_OK;
+    hipLaunchKernelGGL(k_dtab, dim3((unsigned)ntab), dim3(256), 0, (hipStream_t)stream, cum, dtab);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }

@@ -100,6 +100,10 @@ class Stream:
     def synchronize(self):
         check(lib().spa_stream_synchronize(self.handle))
 
+    def wait(self, event):
+        """work queued here from now on waits for the event's last record"""
+        check(lib().spa_stream_wait_event(self.handle, event.handle))
+
     def __del__(self):
         if getattr(self, "handle", None):
             try:

@@ -3,8 +3,7 @@
 compress(data, layout) -> parts and decompress(parts) -> the tensors' bytes keep BF16v2's
 algorithm and stream format (bf16v2.py:185-486): side information per tensor (rfi, cfi, scl),
 exact duplicate rows coded once, per-role frequency tables (656 per role: 512 exponent, 128
-mantissa, 16 sign contexts) normalised to 2^15, and rANS segments of 16384 weights, the tensors
-processed in groups of at most `group_bytes`. The statistics, fingerprints, histogram, symbol
+mantissa, 16 sign contexts) normalised to 2^15, and rANS segments of 16384 weights. The statistics, fingerprints, histogram, symbol
 lookups, coding, gather and decoding run as HIP kernels; the duplicate-row check, the table
 normalisation (gpu2.normalize_gpu, a loop over a few hundred rows) and the framing run on the host.
 
@@ -74,16 +73,25 @@ def bases(layout):
     return rb, cb, rowbase, colbase
 
 
-def plan(layout, grp, nrows_c, rmap_off):
+HEW = 64                           # exponent contexts the histogram kernel counts in LDS
+
+
+def plan(layout, grp, nrows_c, rmap_off, rfi=None, cfi=None):
     """(TB, SG) descriptors of one group, device offsets relative to the group's first tensor
-    (bf16v2.py:208-220)"""
+    (bf16v2.py:208-220). With the side information given, TB.pad holds the base of the histogram
+    kernel's LDS window of exponent contexts, centred on the tensor's median context (the counts
+    do not depend on it)."""
     rb, cb, _, _ = bases(layout)
     tb = np.zeros(len(grp), TB_DT)
     segs = []
     a = layout["t"][grp[0]][0]
     for k, i in enumerate(grp):
         off, nb, rl, _ = layout["t"][i]
-        tb[k] = (off - a, rl, rb[i], cb[i], layout["role"][i] * TPT, rmap_off.get(i, -1), 0)
+        pe0 = 0
+        if rfi is not None:
+            mid = int(np.median(rfi[rb[i]:rb[i] + nb // 2 // rl])) + int(np.median(cfi[cb[i]:cb[i] + rl])) + 256
+            pe0 = min(max(mid - HEW // 2, 0), NE - HEW)
+        tb[k] = (off - a, rl, rb[i], cb[i], layout["role"][i] * TPT, rmap_off.get(i, -1), pe0)
         n = nrows_c[i] * rl
         for i0 in range(0, n, SEG):
             segs.append((k, min(SEG, n - i0), i0))
@@ -136,18 +144,19 @@ def load_tables(buf):
     return freq, used
 
 
-def _dups(hashes, u_host, rl):
+def _dups(hashes, rows, rl):
     """(rows kept (sorted) or None, [(duplicate row, source row)]) from the row fingerprints and a
-    byte check of every candidate (bf16v2.py:246-271)"""
+    byte check of every candidate (bf16v2.py:246-271); `rows(ids)` returns those rows' BF16 bits"""
     nr = len(hashes)
     order = np.argsort(hashes, kind="stable")
     hs = hashes[order]
     same = np.flatnonzero(hs[1:] == hs[:-1])
     if len(same) == 0:
         return None, []
-    hu = u_host.reshape(-1, rl)
+    ks = np.unique(np.concatenate([same, same + 1]))
+    hu = dict(zip(order[ks].tolist(), rows(order[ks])))
     pairs, isdup, first = [], np.zeros(nr, bool), {}
-    for k in np.unique(np.concatenate([same, same + 1])):
+    for k in ks:
         r = int(order[k])
         cands = first.setdefault(int(hs[k]), [])
         src = next((c for c in cands if np.array_equal(hu[c], hu[r])), None)
@@ -165,105 +174,186 @@ def _p(a):
     return None if a is None else a.ptr
 
 
-class BF16v2:
-    """R2 codec core on the MI355X (bf16v2.py:170-617)"""
+class _Timer:
+    """HIP events around the device phases of one call (kernel time with inputs resident)"""
 
-    def __init__(self, group_bytes=400 << 20, dedup=True, stream=None):
+    def __init__(self, on, stream):
+        self.on, self.stream, self.marks = on, stream, []
+
+    def mark(self, name):
+        if self.on:
+            e = dev.Event()
+            e.record(self.stream)
+            self.marks.append((name, e))
+
+    def result(self):
+        out = {}
+        for (name, e0), (_, e1) in zip(self.marks, self.marks[1:]):
+            if name:
+                out[name] = out.get(name, 0.0) + e0.elapsed_ms(e1)
+        return out
+
+
+class BF16v2:
+    """R2 codec core on the MI355X (bf16v2.py:170-617).
+
+    The reference works through the file in groups of `group_bytes` (bf16v2.py:178); the groups do
+    not enter the format (the tables are per role over the whole file, the segments never cross a
+    tensor and the stream is the segments in tensor order), so here the whole coded region is
+    resident in HBM at once and each kernel runs over every segment of the file in one launch
+    (encode in batches of `enc_batch` segments, for its 12-byte-per-weight symbol workspace).
+    `group_bytes` is kept for the reference's interface."""
+
+    def __init__(self, group_bytes=400 << 20, dedup=True, stream=None, enc_batch=131072, timing=False):
         self.group_bytes, self.dedup, self.stream = group_bytes, dedup, stream
+        self.enc_batch, self.timing, self.last_timing = enc_batch, timing, {}
 
     def stats(self, w_dev, rl, with_hash=True):
         """(rfi, cfi, scl, row hashes or None) of one tensor's BF16 bits on the device, as numpy"""
         nr = w_dev.nbytes // 2 // rl
         rfi, cfi, scl = dev.DeviceArray(nr, np.int16), dev.DeviceArray(rl, np.int16), dev.DeviceArray(rl, np.int8)
         h = dev.DeviceArray(nr, np.uint64) if with_hash else None
-        work = dev.DeviceArray(nr, np.float32)
-        check(lib().spa_r2_stats(w_dev.ptr, nr, rl, rfi.ptr, cfi.ptr, scl.ptr, _p(h), work.ptr, None, self.stream))
+        wb = lib().spa_r2_stats_work_bytes(nr, rl)
+        work = dev.DeviceArray(wb, np.uint8)
+        check(lib().spa_r2_stats(w_dev.ptr, nr, rl, rfi.ptr, cfi.ptr, scl.ptr, _p(h), work.ptr, wb, None, self.stream))
         s = self.stream
         return (rfi.to_host(stream=s), cfi.to_host(stream=s), scl.to_host(stream=s),
                 h.to_host(stream=s) if h is not None else None)
+
+    NAUX = 4                        # streams the per-tensor statistics are spread over
+
+    def _side_info(self, d, a, layout, nrow, ncol):
+        """every tensor's statistics (and row fingerprints) on the device: the launches forked onto
+        NAUX streams so the small tensors overlap, joined back into the codec's stream; returns the
+        device arrays (all tensors, at their row / column bases) and their host copies"""
+        st = self.stream
+        rb, cb, _, _ = bases(layout)
+        if not hasattr(self, "_aux"):
+            self._aux = [dev.Stream() for _ in range(self.NAUX)]
+        rfi_d, cfi_d = dev.DeviceArray(max(nrow, 1), np.int16), dev.DeviceArray(max(ncol, 1), np.int16)
+        scl_d = dev.DeviceArray(max(ncol, 1), np.int8)
+        h_d = dev.DeviceArray(max(nrow, 1), np.uint64) if self.dedup else None
+        wb = max(lib().spa_r2_stats_work_bytes(nb // 2 // rl, rl) for _, nb, rl, _ in layout["t"])
+        works = [dev.DeviceArray(wb, np.uint8) for _ in self._aux]
+        fork = dev.Event()
+        fork.record(st)
+        for s in self._aux:
+            s.wait(fork)
+        for i, (off, nb, rl, _) in enumerate(layout["t"]):
+            k = i % len(self._aux)
+            check(lib().spa_r2_stats(d.ptr + off - a, nb // 2 // rl, rl, rfi_d.ptr + 2 * rb[i], cfi_d.ptr + 2 * cb[i],
+                                     scl_d.ptr + cb[i], None if h_d is None else h_d.ptr + 8 * rb[i], works[k].ptr, wb,
+                                     None, self._aux[k].handle))
+        joins = []
+        for s in self._aux:
+            e = dev.Event()
+            e.record(s.handle)
+            check(lib().spa_stream_wait_event(st, e.handle))
+            joins.append(e)
+        host = [x.to_host(stream=st) for x in (rfi_d, cfi_d, scl_d)]
+        hh = h_d.to_host(stream=st) if h_d is not None else None
+        del works, joins
+        return (rfi_d, cfi_d, scl_d), host[0][:nrow], host[1][:ncol], host[2][:ncol], hh
 
     def compress(self, data, layout):
         """the coded parts of the file's 2-D BF16 tensors: dict(meta, side, tables, lens, stream) as
         bytes in the reference's chunk format, and the arrays they hold (rfi, cfi, scl, counts, freq,
         used, lens, nrows_c, dups)"""
         st = self.stream
-        host = np.frombuffer(data, np.uint8)
+        tm = _Timer(self.timing, st)
         rb, cb, nrow, ncol = bases(layout)
+        nt = len(layout["t"])
         rfi = np.zeros(nrow, np.int16); cfi = np.zeros(ncol, np.int16); scl = np.zeros(ncol, np.int8)
-        grps = groups(layout, self.group_bytes)
-        nrows_c, dup_pairs, rmap_all, nrm = {}, {}, [], 0
-        per_group = []
-        for grp in grps:
-            a = layout["t"][grp[0]][0]
-            b = layout["t"][grp[-1]][0] + layout["t"][grp[-1]][1]
-            d = dev.DeviceArray.from_host(host[a:b], st)
-            rmap_off, mine = {}, []
-            for i in grp:
-                off, nb, rl, _ = layout["t"][i]
-                r_, c_, s_, h = self.stats(d.view(off - a, (nb,), np.uint8), rl, self.dedup)
-                rfi[rb[i]:rb[i] + len(r_)] = r_; cfi[cb[i]:cb[i] + rl] = c_; scl[cb[i]:cb[i] + rl] = s_
-                keep, pairs = _dups(h, host[off:off + nb].view(np.uint16), rl) if self.dedup else (None, [])
-                nrows_c[i] = nb // 2 // rl if keep is None else len(keep)
-                if keep is not None:
-                    rmap_off[i] = nrm; nrm += len(keep); rmap_all.append(keep); mine.append(keep)
-                    dup_pairs[i] = pairs
-            per_group.append((d, a, rmap_off, mine))
-        side_dev = [dev.DeviceArray.from_host(x, st) for x in (rfi, cfi, scl)]
+        nrows_c, dup_pairs, rmap_all, rmap_off, nrm = {}, {}, [], {}, 0
+        if isinstance(data, dev.DeviceArray):           # the file already resident (compress_dev)
+            d, a, host = data, 0, None
+        else:
+            host = np.frombuffer(data, np.uint8)
+            a = layout["t"][0][0] if nt else 0
+            b = max((off + nb for off, nb, _, _ in layout["t"]), default=0)
+            d = dev.DeviceArray.from_host(host[a:b] if b > a else np.zeros(1, np.uint8), st)
+
+        def rows_of(off, rl):
+            """the BF16 bits of some rows of the tensor at file offset `off`"""
+            if host is not None:
+                return lambda ids: [host[off + 2 * rl * int(r):off + 2 * rl * (int(r) + 1)].view(np.uint16) for r in ids]
+            return lambda ids: [d.view(off - a + 2 * rl * int(r), (rl,), np.uint16).to_host(stream=st) for r in ids]
+
+        tm.mark("stats")
+        if nt:
+            side_dev, rfi, cfi, scl, hh = self._side_info(d, a, layout, nrow, ncol)
+        else:
+            side_dev, hh = [dev.DeviceArray(1, x.dtype) for x in (rfi, cfi, scl)], None
+        tm.mark(None)
+        for i in range(nt):
+            off, nb, rl, _ = layout["t"][i]
+            nr = nb // 2 // rl
+            keep, pairs = _dups(hh[rb[i]:rb[i] + nr], rows_of(off, rl), rl) if self.dedup else (None, [])
+            nrows_c[i] = nr if keep is None else len(keep)
+            if keep is not None:
+                rmap_off[i] = nrm; nrm += len(keep); rmap_all.append(keep)
+                dup_pairs[i] = pairs
         counts = dev.DeviceArray((layout["nroles"] * TPT, 256), np.uint32).zero(st)
-        plans = []
-        for grp, (d, a, rmap_off, mine) in zip(grps, per_group):
-            tb, sg = plan(layout, grp, nrows_c, rmap_off)
-            if mine:
-                tb = tb.copy(); m = tb["rmap"] >= 0; tb["rmap"][m] -= min(rmap_off.values())
-                rm = np.concatenate(mine).astype(np.int32)
-            else:
-                rm = np.zeros(1, np.int32)
-            tb_d = dev.DeviceArray.from_host(tb.view(np.uint8), st)
-            sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if len(sg) else np.zeros(16, np.uint8), st)
-            rm_d = dev.DeviceArray.from_host(rm, st)
-            check(lib().spa_r2_hist(d.ptr, tb_d.ptr, sg_d.ptr, len(sg), side_dev[0].ptr, side_dev[1].ptr, side_dev[2].ptr,
-                                    rm_d.ptr, counts.ptr, st))
-            plans.append((tb_d, sg_d, rm_d, len(sg)))
+        tb, sg = plan(layout, list(range(nt)), nrows_c, rmap_off, rfi, cfi) if nt else (np.zeros(0, TB_DT), np.zeros(0, SG_DT))
+        if nt:
+            tb["doff"] += layout["t"][0][0] - a
+        nseg = len(sg)
+        rowmap = np.concatenate(rmap_all).astype(np.int32) if rmap_all else np.zeros(1, np.int32)
+        tb_d = dev.DeviceArray.from_host(tb.view(np.uint8) if nt else np.zeros(32, np.uint8), st)
+        sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if nseg else np.zeros(16, np.uint8), st)
+        rm_d = dev.DeviceArray.from_host(rowmap, st)
+        tm.mark("hist")
+        check(lib().spa_r2_hist(d.ptr, tb_d.ptr, sg_d.ptr, nseg, side_dev[0].ptr, side_dev[1].ptr, side_dev[2].ptr,
+                                rm_d.ptr, counts.ptr, st))
+        tm.mark(None)
         counts_h = counts.to_host(stream=st)
         freq, used = normalize(counts_h)
         remap = np.full(counts_h.shape[0], -1, np.int32)
         remap[used] = np.arange(len(used), dtype=np.int32)
         remap_d, freq_d, cum_d = (dev.DeviceArray.from_host(x, st) for x in (remap, freq, cum_of(freq)))
         streams, lens_all = [], []
-        for (d, a, _, _), (tb_d, sg_d, rm_d, nseg) in zip(per_group, plans):
-            if nseg == 0:
-                continue
-            fc = dev.DeviceArray(nseg * SEG * 3, np.uint32)
-            out = dev.DeviceArray(nseg * CAP, np.uint8)
-            out_len = dev.DeviceArray(nseg, np.uint32).zero(st)
-            check(lib().spa_r2_encode(d.ptr, tb_d.ptr, sg_d.ptr, nseg, side_dev[0].ptr, side_dev[1].ptr, side_dev[2].ptr,
-                                      rm_d.ptr, remap_d.ptr, freq_d.ptr, cum_d.ptr, fc.ptr, out.ptr, CAP, out_len.ptr, st))
-            lens = out_len.to_host(stream=st)
+        nbat = min(max(nseg, 1), self.enc_batch)
+        fc = dev.DeviceArray(nbat * SEG * 3, np.uint32)
+        out = dev.DeviceArray(nbat * CAP, np.uint8)
+        out_len = dev.DeviceArray(nbat, np.uint32)
+        for s0 in range(0, nseg, nbat):
+            n = min(nbat, nseg - s0)
+            tm.mark("encode")
+            check(lib().spa_r2_encode(d.ptr, tb_d.ptr, sg_d.ptr + 16 * s0, n, side_dev[0].ptr, side_dev[1].ptr,
+                                      side_dev[2].ptr, rm_d.ptr, remap_d.ptr, freq_d.ptr, cum_d.ptr, fc.ptr, out.ptr, CAP,
+                                      out_len.ptr, st))
+            tm.mark(None)
+            lens = out_len.to_host(stream=st)[:n]
             if (lens == 0xFFFFFFFF).any():
                 raise RuntimeError("R2: rANS segment overflow")
-            offs = np.zeros(nseg + 1, np.uint64)
+            offs = np.zeros(n + 1, np.uint64)
             offs[1:] = np.cumsum(lens.astype(np.uint64))
             dst = dev.DeviceArray(max(1, int(offs[-1])), np.uint8)
             offs_d = dev.DeviceArray.from_host(offs, st)
-            check(lib().spa_qr_gather(out.ptr, CAP, out_len.ptr, offs_d.ptr, nseg, dst.ptr, st))
+            tm.mark("gather")
+            check(lib().spa_qr_gather(out.ptr, CAP, out_len.ptr, offs_d.ptr, n, dst.ptr, st))
+            tm.mark(None)
             streams.append(dst.to_host(stream=st)[:int(offs[-1])].tobytes())
             lens_all.append(lens)
+        self.last_timing = tm.result()
         lens = np.concatenate(lens_all).astype(np.uint32) if lens_all else np.zeros(0, np.uint32)
         dups = [[i, r, s] for i, ps in dup_pairs.items() for r, s in ps]
-        meta = dict(layout=layout, dups=dups, nrows_c=[nrows_c[i] for i in range(len(layout["t"]))])
+        meta = dict(layout=layout, dups=dups, nrows_c=[nrows_c[i] for i in range(nt)])
         stream = b"".join(streams)
         return {"meta": zstd.compress(json.dumps(meta).encode(), 19),
                 "side": zstd.compress(rfi.tobytes() + cfi.tobytes() + scl.tobytes(), 19),
                 "tables": store_tables(freq, used), "lens": zstd.compress(lens.tobytes(), 19), "stream": stream,
                 "arrays": dict(rfi=rfi, cfi=cfi, scl=scl, counts=counts_h, freq=freq, used=used, lens=lens,
                                nrows_c=np.array(meta["nrows_c"], np.int64),
-                               dups=np.array(dups, np.int64).reshape(-1, 3),
-                               rowmap=np.concatenate(rmap_all).astype(np.int32) if rmap_all else np.zeros(1, np.int32))}
+                               dups=np.array(dups, np.int64).reshape(-1, 3), rowmap=rowmap)}
 
-    def decompress(self, parts, out=None):
+    def decompress(self, parts, out=None, device=False):
         """parts (compress()'s byte parts) -> the file with its coded tensors written (bf16v2.py:422-476);
-        `out`: the file's other bytes already in place (a uint8 array of the file's size), else zeros"""
+        `out`: the file's other bytes already in place (a uint8 array of the file's size), else zeros.
+        device=True: the result stays in HBM, returned as a DeviceArray of the file's bytes up to the
+        end of its last coded tensor (only the coded tensors written; decompress_dev)."""
         st = self.stream
+        tm = _Timer(self.timing, st)
         meta = json.loads(zstd.decompress(bytes(parts["meta"])))
         layout = meta["layout"]
         nt = len(layout["t"])
@@ -277,59 +367,63 @@ class BF16v2:
         cum = cum_of(freq)
         remap = np.full(layout["nroles"] * TPT, -1, np.int32)
         remap[used] = np.arange(len(used), dtype=np.int32)
-        freq_d, cum_d, remap_d = (dev.DeviceArray.from_host(np.ascontiguousarray(x), st) for x in (freq, cum, remap))
-        lut = dev.DeviceArray((max(1, len(freq)), 1 << PB), np.uint8)
-        check(lib().spa_rans_build_lut_pb(cum_d.ptr, len(freq), PB, lut.ptr, st))
+        cum_d, remap_d = (dev.DeviceArray.from_host(np.ascontiguousarray(x), st) for x in (cum, remap))
+        dtab = dev.DeviceArray((max(1, len(freq)), lib().spa_r2_dec_table_bytes()), np.uint8)
+        tm.mark("tables")
+        check(lib().spa_r2_build_dec_tables(cum_d.ptr, len(freq), dtab.ptr, st))
+        tm.mark(None)
         lens = np.frombuffer(zstd.decompress(bytes(parts["lens"])), np.uint32)
         nrows_c = {i: n for i, n in enumerate(meta["nrows_c"])}
         dups = {}
         for i, r, s in meta["dups"]:
             dups.setdefault(i, []).append((r, s))
-        rmap_all, rmap_off_t = [], {}
+        rmap_all, rmap_off = [], {}
         for i in range(nt):
             if i in dups:
                 rl = layout["t"][i][2]
                 nr = layout["t"][i][1] // 2 // rl
                 isdup = np.zeros(nr, bool)
                 isdup[[r for r, _ in dups[i]]] = True
-                rmap_off_t[i] = sum(len(x) for x in rmap_all)
+                rmap_off[i] = sum(len(x) for x in rmap_all)
                 rmap_all.append(np.flatnonzero(~isdup).astype(np.int32))
         rowmap = np.concatenate(rmap_all) if rmap_all else np.zeros(1, np.int32)
+        if nt == 0:
+            return dev.DeviceArray(1, np.uint8) if device else (np.zeros(layout["size"], np.uint8) if out is None else out)
         rowmap_d = dev.DeviceArray.from_host(rowmap, st)
-        out = np.zeros(layout["size"], np.uint8) if out is None else out
+        tb, sg = plan(layout, list(range(nt)), nrows_c, rmap_off)
+        if len(lens) != len(sg):
+            raise ValueError(f"R2: {len(lens)} segment lengths for {len(sg)} segments")
+        offs = np.zeros(max(1, len(sg)), np.uint64)
+        offs[1:len(sg)] = np.cumsum(lens.astype(np.uint64))[:-1]
+        a = 0 if device else layout["t"][0][0]
+        b = max(off + nb for off, nb, _, _ in layout["t"])
+        d = dev.DeviceArray(b - a, np.uint8)
+        tb["doff"] += layout["t"][0][0] - a
         stream_h = np.frombuffer(bytes(parts["stream"]), np.uint8)
-        spos, lpos = 0, 0
-        for grp in groups(layout, self.group_bytes):
-            rmap_off = {i: rmap_off_t[i] for i in grp if i in rmap_off_t}
-            tb, sg = plan(layout, grp, nrows_c, rmap_off)
-            gl = lens[lpos:lpos + len(sg)]
-            lpos += len(sg)
-            nbytes = int(gl.sum(dtype=np.uint64))
-            offs = np.zeros(max(1, len(sg)), np.uint64)
-            offs[1:len(sg)] = np.cumsum(gl.astype(np.uint64))[:-1]
-            a = layout["t"][grp[0]][0]
-            b = layout["t"][grp[-1]][0] + layout["t"][grp[-1]][1]
-            d = dev.DeviceArray(b - a, np.uint8)
-            keep = []                   # device inputs of the launches, alive until the group is read back
-            if len(sg):
-                s_d = dev.DeviceArray.from_host(stream_h[spos:spos + nbytes] if nbytes else np.zeros(1, np.uint8), st)
-                offs_d = dev.DeviceArray.from_host(offs, st)
-                tb_d = dev.DeviceArray.from_host(tb.view(np.uint8), st)
-                sg_d = dev.DeviceArray.from_host(sg.view(np.uint8), st)
-                keep += [s_d, offs_d, tb_d, sg_d]
-                check(lib().spa_r2_decode(s_d.ptr, offs_d.ptr, d.ptr, tb_d.ptr, sg_d.ptr, len(sg),
-                                          side_dev[0].ptr, side_dev[1].ptr, side_dev[2].ptr, rowmap_d.ptr, remap_d.ptr,
-                                          freq_d.ptr, cum_d.ptr, lut.ptr, st))
-            spos += nbytes
-            for i in grp:
-                if i in dups:
-                    off, nb, rl, _ = layout["t"][i]
-                    pairs = dev.DeviceArray.from_host(np.array(dups[i], np.int64).reshape(-1), st)
-                    keep.append(pairs)
-                    check(lib().spa_r2_copy_rows(d.ptr + (off - a), rl, pairs.ptr, len(dups[i]), st))
-            g = d.to_host(stream=st)
-            del keep
-            for i in grp:
-                off, nb, _, _ = layout["t"][i]
-                out[off:off + nb] = g[off - a:off - a + nb]
+        s_d = dev.DeviceArray.from_host(stream_h if len(stream_h) else np.zeros(1, np.uint8), st)
+        offs_d = dev.DeviceArray.from_host(offs, st)
+        tb_d = dev.DeviceArray.from_host(tb.view(np.uint8), st)
+        sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if len(sg) else np.zeros(16, np.uint8), st)
+        keep = []                   # device inputs of the launches, alive until the result is read back
+        tm.mark("decode")
+        check(lib().spa_r2_decode(s_d.ptr, offs_d.ptr, d.ptr, tb_d.ptr, sg_d.ptr, len(sg), side_dev[0].ptr,
+                                  side_dev[1].ptr, side_dev[2].ptr, rowmap_d.ptr, remap_d.ptr, dtab.ptr, st))
+        tm.mark("copy_rows")
+        for i in range(nt):
+            if i in dups:
+                off, nb, rl, _ = layout["t"][i]
+                pairs = dev.DeviceArray.from_host(np.array(dups[i], np.int64).reshape(-1), st)
+                keep.append(pairs)
+                check(lib().spa_r2_copy_rows(d.ptr + (off - a), rl, pairs.ptr, len(dups[i]), st))
+        tm.mark(None)
+        if device:
+            dev.synchronize(st)
+            self.last_timing = tm.result()
+            return d
+        g = d.to_host(stream=st)
+        del keep
+        self.last_timing = tm.result()
+        out = np.zeros(layout["size"], np.uint8) if out is None else out
+        for off, nb, _, _ in layout["t"]:
+            out[off:off + nb] = g[off - a:off - a + nb]
         return out

@@ -42,20 +42,27 @@ def test_hip_r2_matches_reference(vectors, name):
         assert out[off:off + nb].tobytes() == host[off:off + nb].tobytes()
 
 
-def test_hip_r2_row_statistics_bit_exact():
-    """the float64 log2 row RMS (sums, division, sqrt, detmath log2) equals the oracle's bit for bit"""
+@pytest.mark.parametrize("shape", [(256, 1000), (200, 999), (130, 4096), (300, 131072)])
+def test_hip_r2_row_statistics_bit_exact(shape):
+    """the float64 log2 row RMS (sums, division, sqrt, detmath log2) equals the oracle's bit for bit,
+    and so do rfi, cfi and scl: rows read as vectors with a partial last tile (1000), rows not 16-byte
+    aligned (999), rows past the last full workgroup (130), and columns summed over three chunks of
+    rows (131072: 128-row chunks)"""
+    say("case r2 stats", shape)
     g = np.random.Generator(np.random.PCG64(11))
-    x = g.normal(0, 1, (256, 1000)) * np.exp(g.uniform(-40, 10, (256, 1)))
+    x = g.normal(0, 1, shape) * np.exp(g.uniform(-40, 10, (shape[0], 1)))
     x[3] = 0.0
     x[4, :7] = 1e-40
     u = synth.bf16_bits(x.astype(np.float32))
     d = dev.DeviceArray.from_host(u.reshape(-1))
     nr, rl = u.shape
     rfi, cfi, scl = dev.DeviceArray(nr, np.int16), dev.DeviceArray(rl, np.int16), dev.DeviceArray(rl, np.int8)
-    work, rf = dev.DeviceArray(nr, np.float32), dev.DeviceArray(nr, np.float64)
-    check(lib().spa_r2_stats(d.ptr, nr, rl, rfi.ptr, cfi.ptr, scl.ptr, None, work.ptr, rf.ptr, None))
+    wb = lib().spa_r2_stats_work_bytes(nr, rl)
+    work, rf, h = dev.DeviceArray(wb, np.uint8), dev.DeviceArray(nr, np.float64), dev.DeviceArray(nr, np.uint64)
+    check(lib().spa_r2_stats(d.ptr, nr, rl, rfi.ptr, cfi.ptr, scl.ptr, h.ptr, work.ptr, wb, rf.ptr, None))
     want_rf = or2.dm_log2(np.sqrt(or2.rows_sum(or2.bf16_f32(u), True) / rl) + 1e-30)
     assert rf.to_host().tobytes() == want_rf.tobytes()
+    assert np.array_equal(h.to_host(), or2.row_hash(u, rl))
     want = or2.stats(u, rl)
     assert np.array_equal(rfi.to_host(), want[0]) and np.array_equal(cfi.to_host(), want[1])
     assert np.array_equal(scl.to_host(), want[2])
@@ -91,3 +98,101 @@ def test_hip_r2_larger_file_round_trip_and_tables():
     host = np.frombuffer(data, np.uint8)
     for off, nb, _, _ in layout["t"]:
         assert out[off:off + nb].tobytes() == host[off:off + nb].tobytes()
+
+
+@pytest.mark.parametrize("pad", [None, 0, 448, -5, 9999])
+def test_hip_r2_hist_any_window(pad):
+    """the histogram's LDS window of exponent contexts (TB.pad) changes no count: a tensor whose rows
+    span ~12 octaves (contexts far outside any 64-wide window) counted with the window at the median,
+    at either end and clamped, against the oracle's symbols"""
+    say("case r2 hist pad", pad)
+    g = np.random.Generator(np.random.PCG64(31))
+    x = g.normal(0, 1, (700, 1536)) * np.exp2(g.uniform(-14, -2, (700, 1)))
+    w = synth.bf16_bits(x.astype(np.float32))
+    layout = r2.layout_of([("blk.0.attn_q.weight", 0, w.nbytes, 1536)], w.nbytes)
+    rfi, cfi, scl = or2.stats(w, 1536)
+    tb, sg = r2.plan(layout, [0], {0: 700}, {}, rfi, cfi)
+    if pad is not None:
+        tb["pad"] = pad
+    d = dev.DeviceArray.from_host(w.reshape(-1))
+    side = [dev.DeviceArray.from_host(np.ascontiguousarray(v)) for v in (rfi, cfi, scl)]
+    tb_d, sg_d = dev.DeviceArray.from_host(tb.view(np.uint8)), dev.DeviceArray.from_host(sg.view(np.uint8))
+    rm = dev.DeviceArray.from_host(np.zeros(1, np.int32))
+    counts = dev.DeviceArray((r2.TPT, 256), np.uint32).zero()
+    check(lib().spa_r2_hist(d.ptr, tb_d.ptr, sg_d.ptr, len(sg), side[0].ptr, side[1].ptr, side[2].ptr, rm.ptr, counts.ptr, None))
+    got = counts.to_host()
+    want = np.zeros_like(got)
+    t, s = or2.symbols(w, 1536, None, rfi, cfi, scl, 0)
+    np.add.at(want, (t, s), 1)
+    pe = np.flatnonzero(want[:512].sum(1))
+    assert pe.max() - pe.min() > 64
+    assert np.array_equal(got, want)
+
+
+def test_hip_r2_device_resident_matches_host():
+    """compress of the file already in HBM (duplicate rows fetched from the device) gives the same
+    parts as compress of host bytes, and decompress(device=True) leaves the tensors in HBM"""
+    say("case r2 device-resident roles")
+    data, layout, gb = case_file("embd_dups")
+    codec = r2.BF16v2(group_bytes=gb)
+    want = codec.compress(data, layout)
+    d = dev.DeviceArray.from_host(np.frombuffer(data, np.uint8))
+    got = codec.compress(d, layout)
+    for k in ("meta", "side", "tables", "lens", "stream"):
+        assert got[k] == want[k], k
+    back = codec.decompress(got, device=True).to_host()
+    host = np.frombuffer(data, np.uint8)
+    for off, nb, _, _ in layout["t"]:
+        assert back[off:off + nb].tobytes() == host[off:off + nb].tobytes()
+
+
+def test_hip_synth_normal_bf16():
+    """the device generator of benchmark inputs: deterministic per seed, N(0, std)-shaped"""
+    say("case synth normal bf16")
+    n = 1 << 20
+    a, b = dev.DeviceArray(n, np.uint16), dev.DeviceArray(n, np.uint16)
+    check(lib().spa_synth_normal_bf16(a.ptr, n, 7, 0.02, None))
+    check(lib().spa_synth_normal_bf16(b.ptr, n, 7, 0.02, None))
+    x, y = a.to_host(), b.to_host()
+    assert np.array_equal(x, y)
+    f = synth.bf16_to_f32(x)
+    assert abs(f.mean()) < 1e-4 and abs(f.std() - 0.02) < 2e-4
+    assert len(np.unique(x)) > 1000
+
+
+def test_hip_r2_dec_tables_give_lut_symbols():
+    """the compact decode tables (symbol at every 128th slot, cumulative frequencies) name the same
+    symbol for every one of the 2^15 slots as the full lookup table, on tables with zero-frequency
+    symbols, one symbol holding every slot, and long runs of frequency-1 symbols"""
+    say("case r2 decode tables")
+    g = np.random.Generator(np.random.PCG64(41))
+    freq = np.zeros((6, 256), np.int64)
+    freq[0, 7] = 1 << 15
+    freq[1] = 128
+    freq[2, :200] = 1; freq[2, 255] = (1 << 15) - 200
+    freq[3, ::3] = g.integers(1, 400, 86); freq[3, 0] += (1 << 15) - freq[3].sum()
+    p = g.dirichlet(np.full(256, 0.05)); f = np.floor(p * ((1 << 15) - 256)).astype(np.int64) + 1
+    f[np.argmax(f)] += (1 << 15) - f.sum(); freq[4] = f
+    freq[5, 100:228] = 256
+    assert (freq.sum(1) == 1 << 15).all()
+    cum = r2.cum_of(freq.astype(np.uint16))
+    cum_d = dev.DeviceArray.from_host(cum)
+    nb = lib().spa_r2_dec_table_bytes()
+    dt = dev.DeviceArray((6, nb), np.uint8)
+    lut = dev.DeviceArray((6, 1 << 15), np.uint8)
+    check(lib().spa_r2_build_dec_tables(cum_d.ptr, 6, dt.ptr, None))
+    check(lib().spa_rans_build_lut_pb(cum_d.ptr, 6, 15, lut.ptr, None))
+    dth, luth = dt.to_host(), lut.to_host()
+    slots = np.arange(1 << 15)
+    for t in range(6):
+        coarse = dth[t, :256].astype(np.int64)
+        c16 = dth[t, 256:256 + 514].view(np.uint16).astype(np.int64)
+        assert np.array_equal(c16, cum[t])
+        sym = coarse[slots >> 7]
+        for _ in range(256):                      # step forward while the next cumulative frequency <= slot
+            adv = (c16[np.minimum(sym + 1, 256)] <= slots) & (sym < 255)
+            if not adv.any():
+                break
+            sym = sym + adv
+        assert np.array_equal(sym, luth[t].astype(np.int64)), t
+        assert np.array_equal(np.repeat(np.arange(256), freq[t]), luth[t])
