@@ -18,6 +18,7 @@ import numpy as np
 
 from . import device as dev
 from . import zstd
+from .framing import pack, unpack  # noqa: F401  (the reference's codecs_gguf.pack/unpack)
 from ._lib import check, lib
 
 SELF_TYPES = {2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 20, 23, 42}
@@ -128,29 +129,6 @@ def load_tables(buf):
     used = np.cumsum(np.frombuffer(raw, np.uint32, n, 4).astype(np.int64))
     freq = np.frombuffer(raw, np.uint16, n * 256, 4 + 4 * n).reshape(n, 256)
     return freq, used
-
-
-def pack(chunks):
-    """u32 count, then per chunk: u16 name length, name, u64 length, data (codecs_gguf.py:33-56)"""
-    out = [struct.pack("<I", len(chunks))]
-    for name, data in chunks.items():
-        nb = name.encode()
-        out += [struct.pack("<H", len(nb)), nb, struct.pack("<Q", len(data)), bytes(data)]
-    return b"".join(out)
-
-
-def unpack(buf):
-    (n,), pos, chunks = struct.unpack_from("<I", buf), 4, {}
-    for _ in range(n):
-        (ln,) = struct.unpack_from("<H", buf, pos)
-        pos += 2
-        name = bytes(buf[pos:pos + ln]).decode()
-        pos += ln
-        (dl,) = struct.unpack_from("<Q", buf, pos)
-        pos += 8
-        chunks[name] = buf[pos:pos + dl]
-        pos += dl
-    return chunks
 
 
 def _gather(arrs, stream=None):

@@ -9,19 +9,24 @@ normalisation (gpu2.normalize_gpu, a loop over a few hundred rows) and the frami
 
 `layout` is BF16v2._layout's dict (bf16v2.py:182-188): {"size": file bytes, "t": [[offset, bytes,
 row length, "bf16"], ...] (2-D BF16 tensors by offset), "role": role index per tensor, "nroles"}.
-Outside this module: GGUF parsing and the header coder of the file's other bytes ("rest" part,
-gpu_bf16.py:421-428).
+R2Tensors (bf16v2.py:488-617) decodes chosen tensors alone. The file's other bytes travel in the
+"rest" part, coded on the host: both of its forms decode here and the lzma form is written here;
+the tokenizer-aware form (gpu2.header_pairs_c) needs the GGUF's key spans and stays with the
+caller's GGUF reader.
 """
 import ctypes
 import json
+import lzma
 import re
 import struct
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
 from . import device as dev
 from . import zstd
 from ._lib import check, lib
+from .framing import pack_parts, unpack
 
 PB = 15
 K = 8
@@ -347,83 +352,312 @@ class BF16v2:
                                nrows_c=np.array(meta["nrows_c"], np.int64),
                                dups=np.array(dups, np.int64).reshape(-1, 3), rowmap=rowmap)}
 
-    def decompress(self, parts, out=None, device=False):
-        """parts (compress()'s byte parts) -> the file with its coded tensors written (bf16v2.py:422-476);
-        `out`: the file's other bytes already in place (a uint8 array of the file's size), else zeros.
-        device=True: the result stays in HBM, returned as a DeviceArray of the file's bytes up to the
-        end of its last coded tensor (only the coded tensors written; decompress_dev)."""
+    def compress_parts(self, data, layout, rest=None):
+        """compress() as the reference's compress_parts chunk (bf16v2.py:276-291): pack_parts of
+        meta, side, tables, lens, stream, rest. `rest`: the header coder's output for the file's
+        other bytes; default the lzma form the reference falls back to without a tokenizer
+        (header_x of rest_of, gpu_bf16.py:421-424); needed when `data` is on the device"""
+        ch = self.compress(data, layout)
+        if rest is None:
+            if isinstance(data, dev.DeviceArray):
+                raise ValueError("R2: a device-resident file needs its `rest` part from the caller")
+            rest = header_x(rest_of(data, layout))
+        return pack_parts({"meta": ch["meta"], "side": ch["side"], "tables": ch["tables"], "lens": ch["lens"],
+                           "stream": ch["stream"], "rest": rest})
+
+    def decompress(self, parts, out=None, device=False, alloc=None):
+        """the file back (bf16v2.py:422-486): `parts` is compress()'s dict or a packed chunk
+        (compress_parts' bytes); the coded tensors are decoded on the device, the other bytes come
+        from `out` (already in place) or from the "rest" part when there is one, else zeros.
+        alloc(n) -> writable uint8 array for the output. device=True: the result stays in HBM, a
+        DeviceArray of the file's bytes up to the end of its last coded tensor, only the coded
+        tensors written (decompress_dev)."""
         st = self.stream
         tm = _Timer(self.timing, st)
-        meta = json.loads(zstd.decompress(bytes(parts["meta"])))
-        layout = meta["layout"]
-        nt = len(layout["t"])
-        rb, cb, nrow, ncol = bases(layout)
-        side = zstd.decompress(bytes(parts["side"]))
-        rfi = np.frombuffer(side, np.int16, nrow, 0)
-        cfi = np.frombuffer(side, np.int16, ncol, 2 * nrow)
-        scl = np.frombuffer(side, np.int8, ncol, 2 * nrow + 2 * ncol)
-        side_dev = [dev.DeviceArray.from_host(np.ascontiguousarray(x), st) for x in (rfi, cfi, scl)]
-        freq, used = load_tables(parts["tables"])
-        cum = cum_of(freq)
-        remap = np.full(layout["nroles"] * TPT, -1, np.int32)
-        remap[used] = np.arange(len(used), dtype=np.int32)
-        cum_d, remap_d = (dev.DeviceArray.from_host(np.ascontiguousarray(x), st) for x in (cum, remap))
-        dtab = dev.DeviceArray((max(1, len(freq)), lib().spa_r2_dec_table_bytes()), np.uint8)
-        tm.mark("tables")
-        check(lib().spa_r2_build_dec_tables(cum_d.ptr, len(freq), dtab.ptr, st))
-        tm.mark(None)
-        lens = np.frombuffer(zstd.decompress(bytes(parts["lens"])), np.uint32)
-        nrows_c = {i: n for i, n in enumerate(meta["nrows_c"])}
-        dups = {}
-        for i, r, s in meta["dups"]:
-            dups.setdefault(i, []).append((r, s))
-        rmap_all, rmap_off = [], {}
-        for i in range(nt):
-            if i in dups:
-                rl = layout["t"][i][2]
-                nr = layout["t"][i][1] // 2 // rl
-                isdup = np.zeros(nr, bool)
-                isdup[[r for r, _ in dups[i]]] = True
-                rmap_off[i] = sum(len(x) for x in rmap_all)
-                rmap_all.append(np.flatnonzero(~isdup).astype(np.int32))
-        rowmap = np.concatenate(rmap_all) if rmap_all else np.zeros(1, np.int32)
-        if nt == 0:
-            return dev.DeviceArray(1, np.uint8) if device else (np.zeros(layout["size"], np.uint8) if out is None else out)
-        rowmap_d = dev.DeviceArray.from_host(rowmap, st)
-        tb, sg = plan(layout, list(range(nt)), nrows_c, rmap_off)
-        if len(lens) != len(sg):
-            raise ValueError(f"R2: {len(lens)} segment lengths for {len(sg)} segments")
-        offs = np.zeros(max(1, len(sg)), np.uint64)
-        offs[1:len(sg)] = np.cumsum(lens.astype(np.uint64))[:-1]
-        a = 0 if device else layout["t"][0][0]
-        b = max(off + nb for off, nb, _, _ in layout["t"])
-        d = dev.DeviceArray(b - a, np.uint8)
-        tb["doff"] += layout["t"][0][0] - a
-        stream_h = np.frombuffer(bytes(parts["stream"]), np.uint8)
-        s_d = dev.DeviceArray.from_host(stream_h if len(stream_h) else np.zeros(1, np.uint8), st)
-        offs_d = dev.DeviceArray.from_host(offs, st)
-        tb_d = dev.DeviceArray.from_host(tb.view(np.uint8), st)
-        sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if len(sg) else np.zeros(16, np.uint8), st)
-        keep = []                   # device inputs of the launches, alive until the result is read back
-        tm.mark("decode")
-        check(lib().spa_r2_decode(s_d.ptr, offs_d.ptr, d.ptr, tb_d.ptr, sg_d.ptr, len(sg), side_dev[0].ptr,
-                                  side_dev[1].ptr, side_dev[2].ptr, rowmap_d.ptr, remap_d.ptr, dtab.ptr, st))
-        tm.mark("copy_rows")
-        for i in range(nt):
-            if i in dups:
-                off, nb, rl, _ = layout["t"][i]
-                pairs = dev.DeviceArray.from_host(np.array(dups[i], np.int64).reshape(-1), st)
-                keep.append(pairs)
-                check(lib().spa_r2_copy_rows(d.ptr + (off - a), rl, pairs.ptr, len(dups[i]), st))
-        tm.mark(None)
-        if device:
-            dev.synchronize(st)
+        if not isinstance(parts, dict):
+            parts = unpack(parts if isinstance(parts, memoryview) else memoryview(parts))
+        dec = _Decoder(parts.__getitem__, st, tm)
+        layout, nt = dec.layout, len(dec.layout["t"])
+        if nt == 0 and device:
+            return dev.DeviceArray(1, np.uint8)
+        if nt:
+            a = 0 if device else layout["t"][0][0]
+            b = max(off + nb for off, nb, _, _ in layout["t"])
+            d = dev.DeviceArray(b - a, np.uint8)
+            stream_h = np.frombuffer(parts["stream"], np.uint8)
+            s_d = dev.DeviceArray.from_host(stream_h if len(stream_h) else np.zeros(1, np.uint8), st)
+            idxs = list(range(nt))
+            dec.run(s_d, dec.soff[:-1], d, idxs, [layout["t"][i][0] - a for i in idxs], tm)
+            if device:
+                dev.synchronize(st)
+                self.last_timing = tm.result()
+                return d
+            g = d.to_host(stream=st)
             self.last_timing = tm.result()
-            return d
-        g = d.to_host(stream=st)
-        del keep
-        self.last_timing = tm.result()
-        out = np.zeros(layout["size"], np.uint8) if out is None else out
+        if out is None:
+            out = alloc(layout["size"]) if alloc else np.zeros(layout["size"], np.uint8)
         for off, nb, _, _ in layout["t"]:
             out[off:off + nb] = g[off - a:off - a + nb]
+        if "rest" in parts:
+            fill_rest(out, header_d(bytes(parts["rest"])), layout)
         return out
+
+
+class _Decoder:
+    """the decode side's tables and maps (bf16v2.py:425-451, :496-530): side information, compact
+    decode tables and remap on the device, segment lengths and stream offsets, duplicate rows"""
+
+    def __init__(self, part, st, tm=None):
+        self.st = st
+        meta = json.loads(zstd.decompress(bytes(part("meta"))))
+        self.layout = layout = meta["layout"]
+        t = layout["t"]
+        self.rb, self.cb, nrow, ncol = bases(layout)
+        side = zstd.decompress(bytes(part("side")))
+        host = (np.frombuffer(side, np.int16, nrow, 0), np.frombuffer(side, np.int16, ncol, 2 * nrow),
+                np.frombuffer(side, np.int8, ncol, 2 * nrow + 2 * ncol))
+        self.side = [dev.DeviceArray.from_host(np.ascontiguousarray(x) if len(x) else np.zeros(1, x.dtype), st) for x in host]
+        freq, used = load_tables(part("tables"))
+        remap = np.full(layout["nroles"] * TPT, -1, np.int32)
+        remap[used] = np.arange(len(used), dtype=np.int32)
+        cum_d = dev.DeviceArray.from_host(cum_of(freq) if len(freq) else np.zeros((1, 257), np.uint32), st)
+        self.remap = dev.DeviceArray.from_host(remap if len(remap) else np.full(1, -1, np.int32), st)
+        self.dtab = dev.DeviceArray((max(1, len(freq)), lib().spa_r2_dec_table_bytes()), np.uint8)
+        if tm:
+            tm.mark("tables")
+        check(lib().spa_r2_build_dec_tables(cum_d.ptr, len(freq), self.dtab.ptr, st))
+        if tm:
+            tm.mark(None)
+        self._keep = [cum_d]
+        lens = np.frombuffer(zstd.decompress(bytes(part("lens"))), np.uint32)
+        self.nrows_c = meta["nrows_c"]
+        nseg = [-(-self.nrows_c[i] * rl // SEG) for i, (_, _, rl, _) in enumerate(t)]
+        self.seg0 = np.zeros(len(t) + 1, np.int64)
+        self.seg0[1:] = np.cumsum(nseg)
+        if self.seg0[-1] != len(lens):
+            raise ValueError("R2: segment lengths do not match the layout")
+        self.soff = np.zeros(len(lens) + 1, np.uint64)
+        self.soff[1:] = np.cumsum(lens, dtype=np.uint64)
+        self.dups = {}
+        for i, r, s_ in meta["dups"]:
+            self.dups.setdefault(i, []).append((r, s_))
+        rmap_all, self.rmap_off = [], {}            # the encoder's construction order
+        for i in range(len(t)):
+            if i in self.dups:
+                rl = t[i][2]
+                isdup = np.zeros(t[i][1] // 2 // rl, bool)
+                isdup[[r for r, _ in self.dups[i]]] = True
+                self.rmap_off[i] = sum(len(x) for x in rmap_all)
+                rmap_all.append(np.flatnonzero(~isdup).astype(np.int32))
+        self.rowmap = dev.DeviceArray.from_host(np.concatenate(rmap_all) if rmap_all else np.zeros(1, np.int32), st)
+
+    def run(self, s_d, in_off, d, idxs, doffs, tm=None):
+        """decode tensors idxs from the device stream s_d (in_off: each of their segments' byte
+        offset in it, in order) into d at byte offsets doffs, duplicate rows restored"""
+        st, t = self.st, self.layout["t"]
+        tb = np.zeros(len(idxs), TB_DT)
+        segs = []
+        for k, i in enumerate(idxs):
+            off, nb, rl, _ = t[i]
+            tb[k] = (doffs[k], rl, self.rb[i], self.cb[i], self.layout["role"][i] * TPT, self.rmap_off.get(i, -1), 0)
+            n = self.nrows_c[i] * rl
+            sg = np.zeros(-(-n // SEG), SG_DT)
+            sg["t"] = k
+            sg["i0"] = np.arange(0, n, SEG)
+            sg["n"] = np.minimum(SEG, n - sg["i0"])
+            segs.append(sg)
+        sg = np.concatenate(segs) if segs else np.zeros(0, SG_DT)
+        if len(in_off) != len(sg):
+            raise ValueError("R2: segment offsets do not match the tensors")
+        keep = [dev.DeviceArray.from_host(np.ascontiguousarray(in_off, np.uint64) if len(sg) else np.zeros(1, np.uint64), st),
+                dev.DeviceArray.from_host(tb.view(np.uint8) if len(tb) else np.zeros(32, np.uint8), st),
+                dev.DeviceArray.from_host(sg.view(np.uint8) if len(sg) else np.zeros(16, np.uint8), st)]
+        if tm:
+            tm.mark("decode")
+        check(lib().spa_r2_decode(s_d.ptr, keep[0].ptr, d.ptr, keep[1].ptr, keep[2].ptr, len(sg), self.side[0].ptr,
+                                  self.side[1].ptr, self.side[2].ptr, self.rowmap.ptr, self.remap.ptr, self.dtab.ptr, st))
+        if tm:
+            tm.mark("copy_rows")
+        for k, i in enumerate(idxs):
+            if i in self.dups:
+                rl = t[i][2]
+                pairs = dev.DeviceArray.from_host(np.array(self.dups[i], np.int64).reshape(-1), st)
+                keep.append(pairs)
+                check(lib().spa_r2_copy_rows(d.ptr + doffs[k], rl, pairs.ptr, len(self.dups[i]), st))
+        if tm:
+            tm.mark(None)
+        dev.synchronize(st)              # the descriptors above are freed on return
+        return d
+
+
+class R2Tensors:
+    """random access to an R2-coded file on the device (bf16v2.py:488-617): any of its 2-D BF16
+    tensors decoded alone (its segments found from the segment lengths), the other bytes from the
+    "rest" part. part(name) -> bytes of a small part; read(offset, n, out) reads n bytes of the coded
+    stream (offset from its start) into the writable uint8 array `out`."""
+
+    def __init__(self, part, read, stream=None):
+        self.read, self.stream = read, stream
+        self.dec = _Decoder(part, stream)
+        self.layout = self.dec.layout
+        self.size = self.layout["size"]
+        t = self.layout["t"]
+        self.t_off = np.array([x[0] for x in t], np.int64)
+        self.before = np.zeros(len(t) + 1, np.int64)
+        self.before[1:] = np.cumsum([x[1] for x in t])
+        self.index = {x[0]: i for i, x in enumerate(t)}
+        self.rest = np.frombuffer(header_d(bytes(part("rest"))), np.uint8)
+
+    def coded_bytes(self, i):
+        """bytes of the coded stream of tensor i"""
+        return int(self.dec.soff[self.dec.seg0[i + 1]] - self.dec.soff[self.dec.seg0[i]])
+
+    def outside(self, a, b):
+        """bytes [a, b) of the file, a range outside the coded tensors"""
+        k = int(np.searchsorted(self.t_off, a, side="right"))
+        r = a - int(self.before[k])
+        return self.rest[r:r + b - a]
+
+    def fetch(self, idxs):
+        """the coded stream of tensors idxs read into host memory -> argument of decode()"""
+        soff, seg0 = self.dec.soff, self.dec.seg0
+        ranges = []                               # a tensor's range merged with its neighbour's
+        for i in sorted(idxs):
+            s0, s1 = int(soff[seg0[i]]), int(soff[seg0[i + 1]])
+            if ranges and ranges[-1][1] == s0:
+                ranges[-1][1] = s1
+            else:
+                ranges.append([s0, s1])
+        host = np.empty(max(1, sum(b - a for a, b in ranges)), np.uint8)
+        where, o = {}, 0
+        for a, b in ranges:
+            self.read(a, b - a, host[o:o + b - a])
+            where[a] = o
+            o += b - a
+        return list(idxs), host, where
+
+    def decode(self, idxs):
+        """coded tensors idxs (layout indices, or what fetch(idxs) returned) -> (DeviceArray, byte
+        offset of each tensor in it, 256-byte aligned)"""
+        t = self.layout["t"]
+        idxs, host, where = idxs if isinstance(idxs, tuple) else self.fetch(idxs)
+        soff, seg0 = self.dec.soff, self.dec.seg0
+        in_off, outs, doff = [], [], 0
+        for i in idxs:
+            s = soff[seg0[i]:seg0[i + 1]]
+            if len(s):
+                r0 = max(a for a in where if a <= int(s[0]))
+                in_off.append(s - np.uint64(r0) + np.uint64(where[r0]))
+            outs.append(doff)
+            doff += -(-t[i][1] // 256) * 256
+        d = dev.DeviceArray(max(doff, 1), np.uint8)
+        s_d = dev.DeviceArray.from_host(host, self.stream)
+        self.dec.run(s_d, np.concatenate(in_off) if in_off else np.zeros(0, np.uint64), d, list(idxs), outs)
+        return d, outs
+
+    def write_to(self, write, window=1 << 30):
+        """the whole file, in order, through write(bytes-like): a window of tensors decoded at a time"""
+        t = self.layout["t"]
+        pos, i = 0, 0
+        while i < len(t):
+            j, nb = i, 0
+            while j < len(t) and (j == i or nb + t[j][1] <= window):
+                nb += t[j][1]
+                j += 1
+            d, outs = self.decode(range(i, j))
+            h = d.to_host(stream=self.stream)
+            for k in range(i, j):
+                off, n = t[k][0], t[k][1]
+                if off > pos:
+                    write(self.outside(pos, off))
+                write(h[outs[k - i]:outs[k - i] + n])
+                pos = off + n
+            del d, h
+            i = j
+        if pos < self.size:
+            write(self.outside(pos, self.size))
+
+
+# ------------------------------------------------------------------ the file's other bytes
+# The header coder runs on the host (lzma); restated here so that a packed R2 chunk decodes whole.
+
+HEADER_CHUNKS = 4
+
+
+def rest_of(data, layout):
+    """the file's bytes outside its coded tensors, in order (gpu2.py:299-304)"""
+    parts, pos = [], 0
+    for off, nb, _, _ in layout["t"]:
+        parts.append(bytes(data[pos:off]))
+        pos = off + nb
+    parts.append(bytes(data[pos:]))
+    return b"".join(parts)
+
+
+def fill_rest(out, rest, layout):
+    """rest_of's bytes back around the coded tensors (gpu2.py:307-313)"""
+    pos = rpos = 0
+    for off, nb, _, _ in layout["t"]:
+        gap = off - pos
+        out[pos:off] = np.frombuffer(rest, np.uint8, gap, rpos)
+        rpos += gap
+        pos = off + nb
+    out[pos:] = np.frombuffer(rest, np.uint8, len(rest) - rpos, rpos)
+
+
+def xz_chunks_c(buf):
+    """lzma (preset 9 | extreme) of the bytes in HEADER_CHUNKS parts, lengths first (gpu2.py:316-321)"""
+    n = len(buf)
+    parts = [buf[i * n // HEADER_CHUNKS:(i + 1) * n // HEADER_CHUNKS] for i in range(HEADER_CHUNKS)]
+    with ThreadPoolExecutor(HEADER_CHUNKS) as ex:
+        out = list(ex.map(lambda p: lzma.compress(p, preset=9 | lzma.PRESET_EXTREME), parts))
+    return struct.pack(f"<{HEADER_CHUNKS}I", *map(len, out)) + b"".join(out)
+
+
+def xz_chunks_d(buf):
+    lens = struct.unpack_from(f"<{HEADER_CHUNKS}I", buf)
+    pos, parts = 4 * HEADER_CHUNKS, []
+    for ln in lens:
+        parts.append(buf[pos:pos + ln])
+        pos += ln
+    with ThreadPoolExecutor(HEADER_CHUNKS) as ex:
+        return b"".join(ex.map(lzma.decompress, parts))
+
+
+def header_pairs_d(buf):
+    """the tokenizer-aware header form (gpu2.py:434-457): GGUF token strings rebuilt from the 256
+    byte tokens and the BPE merge pairs, the merges array from the same pairs"""
+    t0, t1, m0, m1, ntok, nm = struct.unpack_from("<6Q", buf)
+    lens4 = struct.unpack_from("<4I", buf, 48)
+    pos, comp = 64, []
+    for ln in lens4:
+        comp.append(buf[pos:pos + ln])
+        pos += ln
+    with ThreadPoolExecutor(4) as ex:
+        stripped, lens, tb, planes = ex.map(lzma.decompress, comp)
+    lens = np.frombuffer(lens, np.uint16).astype(np.int64)
+    ends = np.cumsum(lens)
+    starts = ends - lens
+    raw = [tb[a:b] for a, b in zip(starts.tolist(), ends.tolist())]
+    pl = np.frombuffer(planes, np.uint8).reshape(3, 2, nm).astype(np.uint32)
+    pairs = (pl[0] | (pl[1] << 8) | (pl[2] << 16)).T.tolist()
+    toks = raw[:256]
+    merge_items = []
+    for a, b in pairs:
+        ta, tb_ = toks[a], toks[b]
+        toks.append(ta + tb_)
+        merge_items.append(struct.pack("<Q", len(ta) + len(tb_) + 1) + ta + b" " + tb_)
+    toks.extend(raw[256:])
+    tok_items = b"".join(struct.pack("<Q", len(x)) + x for x in toks)
+    b = t0 + (m0 - t1)
+    return stripped[:t0] + tok_items + stripped[t0:b] + b"".join(merge_items) + stripped[b:]
+
+
+def header_x(rest):
+    """the header part without a tokenizer: "X" + xz_chunks_c (gpu_bf16.py:421-424)"""
+    return b"X" + xz_chunks_c(rest)
+
+
+def header_d(buf):
+    """either header form back to rest_of's bytes (gpu_bf16.py:426-428)"""
+    return header_pairs_d(buf[1:]) if buf[:1] == b"P" else xz_chunks_d(buf[1:])

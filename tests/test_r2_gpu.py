@@ -196,3 +196,35 @@ def test_hip_r2_dec_tables_give_lut_symbols():
             sym = sym + adv
         assert np.array_equal(sym, luth[t].astype(np.int64)), t
         assert np.array_equal(np.repeat(np.arange(256), freq[t]), luth[t])
+
+
+def test_hip_r2_packed_chunk_and_random_access():
+    """compress_parts' packed chunk decodes to the whole file (the rest part included); R2Tensors
+    decodes chosen tensors alone (from reads of their stream ranges) and writes the file in order
+    through windows of tensors"""
+    say("case r2 packed + R2Tensors roles")
+    data, layout, gb = case_file("roles")
+    codec = r2.BF16v2(group_bytes=gb)
+    chunk = b"".join(bytes(p) for p in codec.compress_parts(data, layout))
+    out = codec.decompress(chunk)
+    assert out.tobytes() == data
+    parts = r2.unpack(memoryview(chunk))
+    stream = np.frombuffer(parts["stream"], np.uint8)
+    reads = []
+
+    def read(off, n, dst):
+        reads.append((off, n))
+        dst[:] = stream[off:off + n]
+
+    rt = r2.R2Tensors(lambda name: bytes(parts[name]), read)
+    host = np.frombuffer(data, np.uint8)
+    for idxs in ([2], [0, 3], [1, 2, 3]):
+        d, outs = rt.decode(idxs)
+        h = d.to_host()
+        for i, o in zip(idxs, outs):
+            off, nb, _, _ = layout["t"][i]
+            assert h[o:o + nb].tobytes() == host[off:off + nb].tobytes()
+    assert sum(n for _, n in reads[:1]) == rt.coded_bytes(2)
+    pieces = []
+    rt.write_to(lambda b: pieces.append(bytes(b)), window=40 << 10)
+    assert b"".join(pieces) == data
