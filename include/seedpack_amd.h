@@ -169,23 +169,28 @@ uint64_t spa_r2_stats_work_bytes(int64_t nrows, int rowlen);
 int spa_r2_hist(const void* dev, const void* tb, const void* sg, int nseg, const int16_t* rfi, const int16_t* cfi,
                 const int8_t* scl, const int32_t* rowmap, uint32_t* counts, void* stream);
 
-/* rANS encode of nseg segments (v2_enc, bf16v2.py:77-111): slot s of `out` (cap bytes) ends with the
- * segment's bytes, out_len[s] their count (0xFFFFFFFF: overflow). fc_work: nseg x 16384 x 3 u32 of
- * workspace. */
+/* rANS encode of nseg segments (v2_enc, bf16v2.py:77-111): slot s of `out` (16-byte aligned; cap
+ * bytes, a multiple of 16) ends with the segment's bytes, out_len[s] their count (0xFFFFFFFF: under
+ * 64 bytes left after some weight, the reference's overflow). fc_work: ceil(nseg / 64) x 64 x 16384 x 3
+ * u32 of workspace. */
 int spa_r2_encode(const void* dev, const void* tb, const void* sg, int nseg, const int16_t* rfi, const int16_t* cfi,
                   const int8_t* scl, const int32_t* rowmap, const int32_t* remap, const uint16_t* freq,
                   const uint32_t* cum, uint32_t* fc_work, void* out, uint64_t cap, uint32_t* out_len, void* stream);
 
-/* rANS decode of nseg segments into dev (v2_dec, bf16v2.py:113-137); dtab from
- * spa_r2_build_dec_tables (the reference decodes through build_lut's 2^15-entry tables,
- * bf16v2.py:139-145; these give the same symbols). */
-int spa_r2_decode(const void* in, const uint64_t* in_off, void* dev, const void* tb, const void* sg, int nseg,
-                  const int16_t* rfi, const int16_t* cfi, const int8_t* scl, const int32_t* rowmap,
-                  const int32_t* remap, const uint8_t* dtab, void* stream);
+/* rANS decode of nseg segments into dev (v2_dec, bf16v2.py:113-137): `in` (16-byte aligned) holds
+ * in_bytes of coded stream, segment s starting at in_off[s]; reads stop at in_bytes rounded up to 16
+ * (a damaged stream decodes to garbage, never past its buffer, which must span that rounding).
+ * dtab from spa_r2_build_dec_tables over all roles x 656 contexts (the reference decodes through
+ * build_lut's 2^15-entry tables and a remap, bf16v2.py:113-145; these give the same symbols). */
+int spa_r2_decode(const void* in, uint64_t in_bytes, const uint64_t* in_off, void* dev, const void* tb, const void* sg,
+                  int nseg, const int16_t* rfi, const int16_t* cfi, const int8_t* scl, const int32_t* rowmap,
+                  const uint8_t* dtab, void* stream);
 
-/* Compact decode tables of ntab PB-15 tables (cum: ntab x 257 u32): spa_r2_dec_table_bytes() bytes
- * each, the symbol at every 128th slot and the cumulative frequencies. */
-int spa_r2_build_dec_tables(const uint32_t* cum, int ntab, uint8_t* dtab, void* stream);
+/* Compact decode tables for nctx contexts (roles x 656): context c gets table remap[c] of cum
+ * (257 u32 per table), or a one-symbol table when remap[c] < 0; spa_r2_dec_table_bytes() bytes per
+ * context: per 128-slot bucket the u64 (symbol | cum << 8 | freq << 24) of its first slot's symbol,
+ * then every symbol's u32 (cum | freq << 16). */
+int spa_r2_build_dec_tables(const uint32_t* cum, const int32_t* remap, int nctx, uint8_t* dtab, void* stream);
 uint64_t spa_r2_dec_table_bytes(void);
 
 /* Duplicate rows restored from their sources: rows pairs[2i] = rows pairs[2i+1] of a tensor of rowlen

@@ -64,9 +64,9 @@ SIGNATURES = {
     "spa_r2_hist": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "spa_r2_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_uint64, c_void_p, c_void_p]),
-    "spa_r2_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
+    "spa_r2_decode": (c_int, [c_void_p, c_uint64, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
                               c_void_p, c_void_p, c_void_p, c_void_p]),
-    "spa_r2_build_dec_tables": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
+    "spa_r2_build_dec_tables": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "spa_r2_dec_table_bytes": (c_uint64, []),
     "spa_r2_copy_rows": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p]),
     "spa_rans_build_lut_pb": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),

@@ -330,128 +330,309 @@ __global__ __launch_bounds__(HT) void k_hist(const uint8_t* __restrict__ dev, co
     if (tab >= 0) hist_flush(hm, he, hs, tab, pe0, counts);
 }
 
-// the (freq << 16 | cum) word of each of a segment's symbols, in forward order, at fc + s * SEG * 3
+// The (freq << 16 | cum) word of every symbol, three per weight in forward order, for the coder.
+// Layout: word i of batch segment s at fc[((s / 64) * 3 * SEG + i) * 64 + s % 64], so that the 64
+// lanes of an encoding wave read one 256-byte row per step. A workgroup takes 64 segments x FCK
+// weights: each thread computes 16 weights' words of one segment into an LDS tile, which is then
+// written out row by row.
+constexpr int FCK = 64;
 __global__ __launch_bounds__(256) void k_fc(const uint8_t* __restrict__ dev, const TB* __restrict__ tb, const SG* __restrict__ sg,
-                                            const int16_t* __restrict__ rfi, const int16_t* __restrict__ cfi,
+                                            int nseg, const int16_t* __restrict__ rfi, const int16_t* __restrict__ cfi,
                                             const int8_t* __restrict__ scl, const int32_t* __restrict__ rowmap,
                                             const int32_t* __restrict__ remap, const uint16_t* __restrict__ freq,
                                             const uint32_t* __restrict__ cum, uint32_t* __restrict__ fc) {
-    const SG g = sg[blockIdx.x];
-    const TB T = tb[g.t];
-    const uint16_t* W = reinterpret_cast<const uint16_t*>(dev + T.doff);
-    uint32_t* o = fc + (int64_t)blockIdx.x * SEG * 3;
-    Cursor cur;
-    cur.start(g.i0 + threadIdx.x, T.rowlen);
-    for (int k = threadIdx.x; k < g.n; k += 256, cur.step(256, T.rowlen)) {
-        int ex, man, sgn, pe, rlc, sc;
-        const int64_t orow = orig_row(T, rowmap, cur.rc);
-        const int j = cur.j;
-        contexts(T, orow, j, W[orow * T.rowlen + j], rfi, cfi, scl, ex, man, sgn, pe, rlc, sc);
-        const int t0 = remap[T.tab + pe], t1 = remap[T.tab + 512 + rlc], t2 = remap[T.tab + 640 + sc];
-        o[3 * k + 0] = ((uint32_t)freq[t0 * 256 + ex] << 16) | cum[t0 * 257 + ex];
-        o[3 * k + 1] = ((uint32_t)freq[t1 * 256 + man] << 16) | cum[t1 * 257 + man];
-        o[3 * k + 2] = ((uint32_t)freq[t2 * 256 + sgn] << 16) | cum[t2 * 257 + sgn];
+    __shared__ uint32_t tile[3 * FCK][65];
+    const int t = threadIdx.x, ls = t >> 2, sub = t & 3;
+    const int s = blockIdx.x * 64 + ls;
+    const int k0 = blockIdx.y * FCK + sub * 16;
+    if (s < nseg) {
+        const SG g = sg[s];
+        if (k0 < g.n) {
+            const TB T = tb[g.t];
+            const uint16_t* W = reinterpret_cast<const uint16_t*>(dev + T.doff);
+            Cursor cur;
+            cur.start(g.i0 + k0, T.rowlen);
+            const int kn = g.n - k0 < 16 ? g.n - k0 : 16;
+            for (int q = 0; q < kn; ++q, cur.step(1, T.rowlen)) {
+                int ex, man, sgn, pe, rlc, sc;
+                const int64_t orow = orig_row(T, rowmap, cur.rc);
+                const int j = cur.j;
+                contexts(T, orow, j, W[orow * T.rowlen + j], rfi, cfi, scl, ex, man, sgn, pe, rlc, sc);
+                const int t0 = remap[T.tab + pe], t1 = remap[T.tab + 512 + rlc], t2 = remap[T.tab + 640 + sc];
+                const int r = (sub * 16 + q) * 3;
+                tile[r][ls] = ((uint32_t)freq[t0 * 256 + ex] << 16) | cum[t0 * 257 + ex];
+                tile[r + 1][ls] = ((uint32_t)freq[t1 * 256 + man] << 16) | cum[t1 * 257 + man];
+                tile[r + 2][ls] = ((uint32_t)freq[t2 * 256 + sgn] << 16) | cum[t2 * 257 + sgn];
+            }
+        }
     }
+    __syncthreads();
+    uint32_t* o = fc + ((int64_t)blockIdx.x * 3 * SEG + (int64_t)blockIdx.y * 3 * FCK) * 64;
+    for (int i = t; i < 3 * FCK * 64; i += 256) o[i] = tile[i >> 6][i & 63];
 }
 
-// one lane per segment: the words coded backwards (sign, mantissa, exponent of the last weight
-// first), 4-byte flush
+// One lane per segment, a wave per 64 segments: the words coded backwards (sign, mantissa, exponent
+// of the last weight first), the wave stepping down from its longest segment so that its lanes read
+// one fc row per step; a lane's output bytes are packed four to a dword and stored downwards from
+// the end of its slot (cap bytes, a multiple of 4); 4-byte flush.
 __global__ __launch_bounds__(64) void k_enc(const SG* __restrict__ sg, int nseg, const uint32_t* __restrict__ fc,
                                             uint8_t* __restrict__ out, uint64_t cap, uint32_t* __restrict__ out_len) {
-    const int s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= nseg) return;
-    const int n3 = 3 * sg[s].n;
-    const uint32_t* in = fc + (int64_t)s * SEG * 3;
-    uint8_t* const start = out + (uint64_t)s * cap;
-    uint8_t* const end = start + cap;
-    uint8_t* ptr = end;
-    uint32_t x = RANS_L;
-    for (int i = n3 - 1; i >= 0; --i) {
-        const uint32_t wd = in[i];
-        const uint32_t f = wd >> 16, c = wd & 0xffffu;
-        const uint32_t xm = ((RANS_L >> PB) << 8) * f;
-        while (x >= xm) { *--ptr = (uint8_t)(x & 0xff); x >>= 8; }
-        x = ((x / f) << PB) + (x % f) + c;
-        if (ptr - start < 64) { out_len[s] = 0xffffffffu; return; }
+    const int s = blockIdx.x * 64 + threadIdx.x;
+    const bool on = s < nseg;
+    const int n3 = on ? 3 * sg[s].n : 0;
+    int nmax = n3;
+    for (int o = 32; o; o >>= 1) nmax = max(nmax, __shfl_xor(nmax, o));
+    const uint32_t* in = fc + (int64_t)blockIdx.x * 3 * SEG * 64 + threadIdx.x;
+    uint32_t* const start = reinterpret_cast<uint32_t*>(out + (uint64_t)(on ? s : 0) * cap);
+    uint32_t* wp = start + cap / 4;
+    uint32_t acc = 0, x = RANS_L, nbytes = 0;
+    bool ovf = false;
+    auto emit = [&](uint32_t v) {
+        acc |= v << (8 * (3 - (nbytes & 3)));
+        if ((++nbytes & 3) == 0) {
+            *--wp = acc;
+            acc = 0;
+        }
+    };
+    // words loaded 8 at a time, one group ahead of the coding (their addresses do not depend on it)
+    constexpr int PF = 8;
+    uint32_t nxt[PF];
+#pragma unroll
+    for (int q = 0; q < PF; ++q) {
+        const int ii = nmax - 1 - q;
+        nxt[q] = (ii >= 0 && ii < n3) ? in[(int64_t)ii * 64] : 1u << 16;
     }
-    for (int i = 0; i < 4; ++i) { *--ptr = (uint8_t)(x & 0xff); x >>= 8; }
-    out_len[s] = (uint32_t)(end - ptr);
+    for (int i0 = nmax - 1; i0 >= 0; i0 -= PF) {
+        uint32_t cw[PF];
+#pragma unroll
+        for (int q = 0; q < PF; ++q) {
+            cw[q] = nxt[q];
+            const int ii = i0 - PF - q;
+            nxt[q] = (ii >= 0 && ii < n3) ? in[(int64_t)ii * 64] : 1u << 16;
+        }
+#pragma unroll
+        for (int q = 0; q < PF; ++q) {
+            const int i = i0 - q;
+            if (i >= 0 && i < n3 && !ovf) {
+                const uint32_t f = cw[q] >> 16, c = cw[q] & 0xffffu;
+                const uint32_t xm = ((RANS_L >> PB) << 8) * f;
+                while (x >= xm) {
+                    emit(x & 0xff);
+                    x >>= 8;
+                }
+                x = ((x / f) << PB) + (x % f) + c;
+                if (i % 3 == 0) ovf = nbytes > cap - 64;   // after each weight: under 64 bytes left (bf16v2.py:106)
+            }
+        }
+    }
+    if (!on) return;
+    if (ovf) {
+        out_len[s] = 0xffffffffu;
+        return;
+    }
+    for (int i = 0; i < 4; ++i) {
+        emit(x & 0xff);
+        x >>= 8;
+    }
+    if (nbytes & 3) *--wp = acc;                 // its top bytes are the stream's first
+    out_len[s] = nbytes;
 }
 
-// Decode tables, DT_BYTES per table: the symbol holding slot 128 b for b < 256 (u8), then the
-// cumulative frequencies (257 x u16). A slot's symbol is the coarse entry stepped forward while the
-// next cumulative frequency is still <= the slot: the same symbol as a full 2^15-entry lookup table,
-// from 770 bytes per table instead of 32 KB, so a role's tables stay in the caches.
-constexpr int DT_BYTES = 1024;
+// Decode tables, DT_BYTES per context (a role's 656 contexts side by side, so the decoder needs no
+// remap): for each of the 256 slot buckets of 128 slots, a u64 naming the first and last symbols
+// holding slots of the bucket, with the first one's cumulative frequency and frequency
+// (first | (last - first) << 8 | cum << 16 | freq << 32), then every symbol's (cum | freq << 16)
+// (u32). A slot's symbol is the bucket's first when the slot lies below its cum + freq, else found
+// by binary search over the bucket's other symbols: the same symbol as a full 2^15-entry lookup
+// table, from one 8-byte load for most slots and at most 8 more; 3 KB per table instead of 32 KB.
+// Contexts without a table (never coded) get a one-symbol table, reached only by damaged streams.
+constexpr int DT_BYTES = 3072;
 __device__ __forceinline__ int dec_sym(const uint8_t* dt, uint32_t slot, uint32_t& c0, uint32_t& f) {
-    const uint16_t* cum = reinterpret_cast<const uint16_t*>(dt + 256);
-    int s = dt[slot >> 7];
-    uint32_t lo = cum[s], hi = cum[s + 1];
-    while (hi <= slot && s < 255) {
-        ++s;
-        lo = hi;
-        hi = cum[s + 1];
+    const uint64_t e = reinterpret_cast<const uint64_t*>(dt)[slot >> 7];
+    int s = (int)(e & 255u);
+    c0 = (uint32_t)(e >> 16) & 0xFFFFu;
+    f = (uint32_t)(e >> 32) & 0xFFFFu;
+    const int span = (int)((e >> 8) & 255u);
+    if (c0 + f <= slot && span > 0) {             // (span 0 here: only a table not summing to 2^15)
+        // the last symbol in (first, last] whose cumulative frequency is <= slot
+        const uint32_t* ps = reinterpret_cast<const uint32_t*>(dt + 2048);
+        int lo = s + 1, hi = s + span;
+        uint32_t u = ps[hi];
+        if ((u & 0xFFFFu) > slot) {
+            while (hi - lo > 0) {                 // invariant: cum[lo] <= slot < cum[hi]
+                const int mid = (lo + hi + 1) >> 1;
+                const uint32_t um = ps[mid];
+                if ((um & 0xFFFFu) <= slot) lo = mid;
+                else hi = mid - 1;
+            }
+            hi = lo;
+            u = ps[lo];
+        }
+        s = hi;
+        c0 = u & 0xFFFFu;
+        f = u >> 16;
     }
-    c0 = lo;
-    f = hi - lo;
     return s;
 }
 
-__global__ __launch_bounds__(256) void k_dtab(const uint32_t* __restrict__ cum, uint8_t* __restrict__ dt) {
-    const uint32_t* c = cum + (size_t)blockIdx.x * 257;
+__global__ __launch_bounds__(256) void k_dtab(const uint32_t* __restrict__ cum, const int32_t* __restrict__ remap,
+                                              uint8_t* __restrict__ dt) {
+    __shared__ uint32_t ps[256];
+    __shared__ uint32_t cs[257];
+    const int t = remap[blockIdx.x];
+    const uint32_t* c = cum + (size_t)(t < 0 ? 0 : t) * 257;
     uint8_t* o = dt + (size_t)blockIdx.x * DT_BYTES;
-    uint16_t* oc = reinterpret_cast<uint16_t*>(o + 256);
-    for (int i = threadIdx.x; i < 257; i += 256) oc[i] = (uint16_t)(c[i] < 65535u ? c[i] : 65535u);
-    const uint32_t slot = (uint32_t)threadIdx.x << 7;
-    int lo = 0, hi = 256;                       // the last symbol s <= 255 with cum[s] <= slot
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (c[mid] <= slot) lo = mid;
-        else hi = mid;
-    }
-    o[threadIdx.x] = (uint8_t)lo;
+    const int i = threadIdx.x;
+    for (int k = i; k < 257; k += 256) cs[k] = t < 0 ? (k ? 32768u : 0u) : (c[k] < 65535u ? c[k] : 65535u);
+    __syncthreads();
+    const uint32_t fi = cs[i + 1] > cs[i] ? cs[i + 1] - cs[i] : 0u;
+    ps[i] = cs[i] | (fi << 16);
+    reinterpret_cast<uint32_t*>(o + 2048)[i] = ps[i];
+    // first / last symbol holding a slot of bucket i: the last s <= 255 with cum[s] <= slot
+    auto holder = [&](uint32_t slot) {
+        int lo = 0, hi = 256;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (cs[mid] <= slot) lo = mid;
+            else hi = mid;
+        }
+        return lo;
+    };
+    const int first = holder((uint32_t)i << 7), last = holder(((uint32_t)i << 7) + 127);
+    const uint32_t u = ps[first];
+    reinterpret_cast<uint64_t*>(o)[i] = (uint64_t)first | ((uint64_t)(last - first) << 8) | ((uint64_t)(u & 0xFFFFu) << 16) |
+                                        ((uint64_t)(u >> 16) << 32);
 }
 
-// one lane per segment (the format's unit of sequential decoding)
-__global__ __launch_bounds__(64) void k_dec(const uint8_t* __restrict__ in, const uint64_t* __restrict__ in_off,
-                                            uint8_t* __restrict__ dev, const TB* __restrict__ tb, const SG* __restrict__ sg,
-                                            int nseg, const int16_t* __restrict__ rfi, const int16_t* __restrict__ cfi,
-                                            const int8_t* __restrict__ scl, const int32_t* __restrict__ rowmap,
-                                            const int32_t* __restrict__ remap, const uint8_t* __restrict__ dtab) {
+// A lane's reader of its segment's bytes: a 16-byte window in registers refilled from the next
+// aligned 16-byte block, which is already loaded (its load issued when the window was last refilled),
+// so the coded stream is read once from HBM and its latency hides behind the decoding; blocks at or
+// past `lim` (the stream's length rounded up to 16 bytes) read as zeros.
+struct Reader {
+    const uint4* p;
+    const uint4* lim;
+    uint4 w, nx;                                 // w.x holds the current dword; consumed dwords shift out
+    int left, b;                                 // dwords left in the window, byte index in w.x
+    __device__ __forceinline__ uint4 fetch() {
+        const uint4 v = p < lim ? *p : make_uint4(0u, 0u, 0u, 0u);
+        ++p;
+        return v;
+    }
+    __device__ __forceinline__ void next_dword() {
+        w.x = w.y;
+        w.y = w.z;
+        w.z = w.w;
+        if (--left == 0) {
+            w = nx;
+            nx = fetch();
+            left = 4;
+        }
+    }
+    __device__ __forceinline__ void start(const uint8_t* base, uint64_t off, uint64_t nblocks) {
+        p = reinterpret_cast<const uint4*>(base) + (off >> 4);
+        lim = reinterpret_cast<const uint4*>(base) + nblocks;
+        w = fetch();
+        nx = fetch();
+        left = 4;
+        for (int q = (int)((off >> 2) & 3); q > 0; --q) next_dword();
+        b = (int)(off & 3);
+    }
+    __device__ __forceinline__ uint32_t byte() {
+        const uint32_t v = (w.x >> (8 * b)) & 0xFFu;
+        if (++b == 4) {
+            b = 0;
+            next_dword();
+        }
+        return v;
+    }
+};
+
+// One lane per segment (the format's unit of sequential decoding). Where rows and the column
+// side information are 16-byte aligned (row length a multiple of 8), a lane decodes its weights in
+// groups of 8: the group's cfi / scl read in one 16- and one 8-byte load, its 8 outputs written as
+// one 16-byte store; otherwise weight by weight.
+__global__ __launch_bounds__(256) void k_dec(const uint8_t* __restrict__ in, uint64_t in_blocks, const uint64_t* __restrict__ in_off,
+                                             uint8_t* __restrict__ dev, const TB* __restrict__ tb, const SG* __restrict__ sg,
+                                             int nseg, const int16_t* __restrict__ rfi, const int16_t* __restrict__ cfi,
+                                             const int8_t* __restrict__ scl, const int32_t* __restrict__ rowmap,
+                                             const uint8_t* __restrict__ dtab) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
     const SG g = sg[s];
     const TB T = tb[g.t];
     uint16_t* W = reinterpret_cast<uint16_t*>(dev + T.doff);
-    const uint8_t* ptr = in + in_off[s];
+    Reader rd;
+    rd.start(in, in_off[s], in_blocks);
     uint32_t x = 0;
-    for (int i = 0; i < 4; ++i) x = (x << 8) | *ptr++;
-    const int32_t* rm = remap + T.tab;
+    for (int i = 0; i < 4; ++i) x = (x << 8) | rd.byte();
+    const uint8_t* dt = dtab + (size_t)T.tab * DT_BYTES;
     const int16_t* cf = cfi + T.colbase;
     const int8_t* sc = scl + T.colbase;
     auto get = [&](int ctx) {
-        const int tt = rm[ctx] < 0 ? 0 : rm[ctx];            // unused contexts only on damaged streams
         const uint32_t slot = x & (PSCALE - 1);
         uint32_t c0, f;
-        const int v = dec_sym(dtab + (size_t)tt * DT_BYTES, slot, c0, f);
+        const int v = dec_sym(dt + (size_t)ctx * DT_BYTES, slot, c0, f);
         x = f * (x >> PB) + slot - c0;
         // a valid stream needs at most two bytes here; the cap ends the loop on a damaged one
 #pragma unroll
-        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | *ptr++;
+        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | rd.byte();
         return v;
+    };
+    auto weight = [&](int pred, int scv) {
+        const int ex = get(clampi(pred + 256, 0, 511));
+        const int man = get(512 + clampi(8 * ex - pred - 1016 + 64, 0, 127));
+        const int sgn = get(640 + scv);
+        return (uint32_t)((sgn << 15) | (ex << 7) | man);
     };
     Cursor cur;
     cur.start(g.i0, T.rowlen);
     int64_t orow = orig_row(T, rowmap, cur.rc);
     int rf = rfi[T.rowbase + orow];
     uint16_t* Wr = W + orow * T.rowlen;
+    const bool vec = (T.rowlen & 7) == 0 && (T.colbase & 7) == 0 && ((reinterpret_cast<uintptr_t>(W) & 15) == 0) &&
+                     ((reinterpret_cast<uintptr_t>(cfi) & 15) == 0) && ((reinterpret_cast<uintptr_t>(scl) & 7) == 0);
+    if (vec) {                                   // g.i0, g.n and the row length are multiples of 8
+        // the group's column side information (loaded one group ahead) and outputs move through
+        // 128-bit shift registers
+        uint4 c8n = *reinterpret_cast<const uint4*>(cf + cur.j);
+        uint2 s8n = *reinterpret_cast<const uint2*>(sc + cur.j);
+        for (int k = 0; k < g.n; k += 8) {
+            const int j = cur.j;
+            uint4 c8 = c8n;
+            uint64_t s64 = (uint64_t)s8n.x | ((uint64_t)s8n.y << 32);
+            const int jn = j + 8 < T.rowlen ? j + 8 : 0;
+            c8n = *reinterpret_cast<const uint4*>(cf + jn);
+            s8n = *reinterpret_cast<const uint2*>(sc + jn);
+            uint4 o = make_uint4(0u, 0u, 0u, 0u);
+            for (int t = 0; t < 8; ++t) {
+                const int cfv = (int)(int16_t)(uint16_t)c8.x;
+                c8.x = (c8.x >> 16) | (c8.y << 16);
+                c8.y = (c8.y >> 16) | (c8.z << 16);
+                c8.z = (c8.z >> 16) | (c8.w << 16);
+                c8.w >>= 16;
+                const int scv = (int)(int8_t)(uint8_t)s64;
+                s64 >>= 8;
+                const uint32_t v = weight(rf + cfv, scv);
+                o.x = (o.x >> 16) | (o.y << 16);
+                o.y = (o.y >> 16) | (o.z << 16);
+                o.z = (o.z >> 16) | (o.w << 16);
+                o.w = (o.w >> 16) | (v << 16);
+            }
+            *reinterpret_cast<uint4*>(Wr + j) = o;
+            cur.j += 8;
+            if (cur.j == T.rowlen && k + 8 < g.n) {
+                cur.j = 0;
+                ++cur.rc;
+                orow = orig_row(T, rowmap, cur.rc);
+                rf = rfi[T.rowbase + orow];
+                Wr = W + orow * T.rowlen;
+            }
+        }
+        return;
+    }
     for (int k = 0; k < g.n; ++k) {
         const int j = cur.j;
-        const int pred = rf + cf[j];
-        const int ex = get(clampi(pred + 256, 0, 511));
-        const int man = get(512 + clampi(8 * ex - pred - 1016 + 64, 0, 127));
-        const int sgn = get(640 + sc[j]);
-        Wr[j] = (uint16_t)((sgn << 15) | (ex << 7) | man);
+        Wr[j] = (uint16_t)weight(rf + cf[j], sc[j]);
         if (++cur.j == T.rowlen && k + 1 < g.n) {
             cur.j = 0;
             ++cur.rc;
@@ -528,34 +709,38 @@ int spa_r2_encode(const void* dev, const void* tb, const void* sg, int nseg, con
                   const int8_t* scl, const int32_t* rowmap, const int32_t* remap, const uint16_t* freq, const uint32_t* cum,
                   uint32_t* fc_work, void* out, uint64_t cap, uint32_t* out_len, void* stream) {
     if (nseg < 0) return fail(SPA_ERR_ARG, "spa_r2_encode: negative segment count");
-    if (cap < 1024) return fail(SPA_ERR_ARG, "spa_r2_encode: segment capacity %llu too small", (unsigned long long)cap);
+    if (cap < 1024 || cap % 16) return fail(SPA_ERR_ARG, "spa_r2_encode: segment capacity %llu (a multiple of 16, >= 1024)", (unsigned long long)cap);
+    if (reinterpret_cast<uintptr_t>(out) & 15) return fail(SPA_ERR_ARG, "spa_r2_encode: output not 16-byte aligned");
     if (nseg == 0) return SPA_OK;
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_fc, dim3((unsigned)nseg), dim3(256), 0, st, (const uint8_t*)dev, (const TB*)tb, (const SG*)sg, rfi, cfi,
-                       scl, rowmap, remap, freq, cum, fc_work);
-    hipLaunchKernelGGL(k_enc, dim3((unsigned)((nseg + 63) / 64)), dim3(64), 0, st, (const SG*)sg, nseg, (const uint32_t*)fc_work,
-                       (uint8_t*)out, cap, out_len);
+    const unsigned ngrp = (unsigned)((nseg + 63) / 64);
+    hipLaunchKernelGGL(k_fc, dim3(ngrp, SEG / FCK), dim3(256), 0, st, (const uint8_t*)dev, (const TB*)tb, (const SG*)sg, nseg, rfi,
+                       cfi, scl, rowmap, remap, freq, cum, fc_work);
+    hipLaunchKernelGGL(k_enc, dim3(ngrp), dim3(64), 0, st, (const SG*)sg, nseg, (const uint32_t*)fc_work, (uint8_t*)out, cap,
+                       out_len);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }
 
-int spa_r2_decode(const void* in, const uint64_t* in_off, void* dev, const void* tb, const void* sg, int nseg, const int16_t* rfi,
-                  const int16_t* cfi, const int8_t* scl, const int32_t* rowmap, const int32_t* remap, const uint8_t* dtab,
+int spa_r2_decode(const void* in, uint64_t in_bytes, const uint64_t* in_off, void* dev, const void* tb, const void* sg, int nseg,
+                  const int16_t* rfi, const int16_t* cfi, const int8_t* scl, const int32_t* rowmap, const uint8_t* dtab,
                   void* stream) {
     if (nseg < 0) return fail(SPA_ERR_ARG, "spa_r2_decode: negative segment count");
     if (nseg == 0) return SPA_OK;
-    hipLaunchKernelGGL(k_dec, dim3((unsigned)((nseg + 63) / 64)), dim3(64), 0, (hipStream_t)stream, (const uint8_t*)in, in_off,
-                       (uint8_t*)dev, (const TB*)tb, (const SG*)sg, nseg, rfi, cfi, scl, rowmap, remap, dtab);
+    if (reinterpret_cast<uintptr_t>(in) & 15) return fail(SPA_ERR_ARG, "spa_r2_decode: stream not 16-byte aligned");
+    hipLaunchKernelGGL(k_dec, dim3((unsigned)((nseg + 255) / 256)), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)in,
+                       (in_bytes + 15) / 16, in_off, (uint8_t*)dev, (const TB*)tb, (const SG*)sg, nseg, rfi, cfi, scl, rowmap,
+                       dtab);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }
 
 uint64_t spa_r2_dec_table_bytes(void) { return DT_BYTES; }
 
-int spa_r2_build_dec_tables(const uint32_t* cum, int ntab, uint8_t* dtab, void* stream) {
-    if (ntab < 0) return fail(SPA_ERR_ARG, "spa_r2_build_dec_tables: negative table count");
-    if (ntab == 0) return SPA_OK;
-    hipLaunchKernelGGL(k_dtab, dim3((unsigned)ntab), dim3(256), 0, (hipStream_t)stream, cum, dtab);
+int spa_r2_build_dec_tables(const uint32_t* cum, const int32_t* remap, int nctx, uint8_t* dtab, void* stream) {
+    if (nctx < 0) return fail(SPA_ERR_ARG, "spa_r2_build_dec_tables: negative context count");
+    if (nctx == 0) return SPA_OK;
+    hipLaunchKernelGGL(k_dtab, dim3((unsigned)nctx), dim3(256), 0, (hipStream_t)stream, cum, remap, dtab);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }

@@ -318,7 +318,7 @@ class BF16v2:
         remap_d, freq_d, cum_d = (dev.DeviceArray.from_host(x, st) for x in (remap, freq, cum_of(freq)))
         streams, lens_all = [], []
         nbat = min(max(nseg, 1), self.enc_batch)
-        fc = dev.DeviceArray(nbat * SEG * 3, np.uint32)
+        fc = dev.DeviceArray(-(-nbat // 64) * 64 * SEG * 3, np.uint32)
         out = dev.DeviceArray(nbat * CAP, np.uint8)
         out_len = dev.DeviceArray(nbat, np.uint32)
         for s0 in range(0, nseg, nbat):
@@ -384,8 +384,7 @@ class BF16v2:
             a = 0 if device else layout["t"][0][0]
             b = max(off + nb for off, nb, _, _ in layout["t"])
             d = dev.DeviceArray(b - a, np.uint8)
-            stream_h = np.frombuffer(parts["stream"], np.uint8)
-            s_d = dev.DeviceArray.from_host(stream_h if len(stream_h) else np.zeros(1, np.uint8), st)
+            s_d = _Decoder.upload(np.frombuffer(parts["stream"], np.uint8), st)
             idxs = list(range(nt))
             dec.run(s_d, dec.soff[:-1], d, idxs, [layout["t"][i][0] - a for i in idxs], tm)
             if device:
@@ -418,17 +417,18 @@ class _Decoder:
                 np.frombuffer(side, np.int8, ncol, 2 * nrow + 2 * ncol))
         self.side = [dev.DeviceArray.from_host(np.ascontiguousarray(x) if len(x) else np.zeros(1, x.dtype), st) for x in host]
         freq, used = load_tables(part("tables"))
-        remap = np.full(layout["nroles"] * TPT, -1, np.int32)
+        nctx = layout["nroles"] * TPT
+        remap = np.full(max(1, nctx), -1, np.int32)
         remap[used] = np.arange(len(used), dtype=np.int32)
         cum_d = dev.DeviceArray.from_host(cum_of(freq) if len(freq) else np.zeros((1, 257), np.uint32), st)
-        self.remap = dev.DeviceArray.from_host(remap if len(remap) else np.full(1, -1, np.int32), st)
-        self.dtab = dev.DeviceArray((max(1, len(freq)), lib().spa_r2_dec_table_bytes()), np.uint8)
+        remap_d = dev.DeviceArray.from_host(remap, st)
+        self.dtab = dev.DeviceArray((max(1, nctx), lib().spa_r2_dec_table_bytes()), np.uint8)
         if tm:
             tm.mark("tables")
-        check(lib().spa_r2_build_dec_tables(cum_d.ptr, len(freq), self.dtab.ptr, st))
+        check(lib().spa_r2_build_dec_tables(cum_d.ptr, remap_d.ptr, nctx, self.dtab.ptr, st))
         if tm:
             tm.mark(None)
-        self._keep = [cum_d]
+        self._keep = [cum_d, remap_d]
         lens = np.frombuffer(zstd.decompress(bytes(part("lens"))), np.uint32)
         self.nrows_c = meta["nrows_c"]
         nseg = [-(-self.nrows_c[i] * rl // SEG) for i, (_, _, rl, _) in enumerate(t)]
@@ -451,9 +451,19 @@ class _Decoder:
                 rmap_all.append(np.flatnonzero(~isdup).astype(np.int32))
         self.rowmap = dev.DeviceArray.from_host(np.concatenate(rmap_all) if rmap_all else np.zeros(1, np.int32), st)
 
+    @staticmethod
+    def upload(stream_h, st):
+        """coded stream bytes -> device, padded to a whole number of 16-byte blocks (the decoder's
+        reads)"""
+        n = len(stream_h)
+        d = dev.DeviceArray(max(16, -(-n // 16) * 16), np.uint8)
+        if n:
+            check(lib().spa_memcpy_h2d(d.ptr, np.ascontiguousarray(stream_h).ctypes.data, n, st))
+        return d
+
     def run(self, s_d, in_off, d, idxs, doffs, tm=None):
-        """decode tensors idxs from the device stream s_d (in_off: each of their segments' byte
-        offset in it, in order) into d at byte offsets doffs, duplicate rows restored"""
+        """decode tensors idxs from the device stream s_d (from upload(); in_off: each of their
+        segments' byte offset in it, in order) into d at byte offsets doffs, duplicate rows restored"""
         st, t = self.st, self.layout["t"]
         tb = np.zeros(len(idxs), TB_DT)
         segs = []
@@ -474,8 +484,8 @@ class _Decoder:
                 dev.DeviceArray.from_host(sg.view(np.uint8) if len(sg) else np.zeros(16, np.uint8), st)]
         if tm:
             tm.mark("decode")
-        check(lib().spa_r2_decode(s_d.ptr, keep[0].ptr, d.ptr, keep[1].ptr, keep[2].ptr, len(sg), self.side[0].ptr,
-                                  self.side[1].ptr, self.side[2].ptr, self.rowmap.ptr, self.remap.ptr, self.dtab.ptr, st))
+        check(lib().spa_r2_decode(s_d.ptr, s_d.nbytes, keep[0].ptr, d.ptr, keep[1].ptr, keep[2].ptr, len(sg),
+                                  self.side[0].ptr, self.side[1].ptr, self.side[2].ptr, self.rowmap.ptr, self.dtab.ptr, st))
         if tm:
             tm.mark("copy_rows")
         for k, i in enumerate(idxs):
@@ -551,7 +561,7 @@ class R2Tensors:
             outs.append(doff)
             doff += -(-t[i][1] // 256) * 256
         d = dev.DeviceArray(max(doff, 1), np.uint8)
-        s_d = dev.DeviceArray.from_host(host, self.stream)
+        s_d = _Decoder.upload(host, self.stream)
         self.dec.run(s_d, np.concatenate(in_off) if in_off else np.zeros(0, np.uint64), d, list(idxs), outs)
         return d, outs
 

@@ -178,23 +178,36 @@ def test_hip_r2_dec_tables_give_lut_symbols():
     cum = r2.cum_of(freq.astype(np.uint16))
     cum_d = dev.DeviceArray.from_host(cum)
     nb = lib().spa_r2_dec_table_bytes()
-    dt = dev.DeviceArray((6, nb), np.uint8)
+    remap = np.array([5, 4, 3, 2, 1, 0, -1], np.int32)          # contexts -> tables; the last has none
+    remap_d = dev.DeviceArray.from_host(remap)
+    dt = dev.DeviceArray((7, nb), np.uint8)
     lut = dev.DeviceArray((6, 1 << 15), np.uint8)
-    check(lib().spa_r2_build_dec_tables(cum_d.ptr, 6, dt.ptr, None))
+    check(lib().spa_r2_build_dec_tables(cum_d.ptr, remap_d.ptr, 7, dt.ptr, None))
     check(lib().spa_rans_build_lut_pb(cum_d.ptr, 6, 15, lut.ptr, None))
     dth, luth = dt.to_host(), lut.to_host()
     slots = np.arange(1 << 15)
+
+    def decode_all(tab):
+        """every slot's (symbol, cum, freq) from the compact table: the bucket's first symbol, or
+        the last of the bucket's other symbols whose cum <= slot"""
+        e = tab[:2048].view(np.uint64).astype(np.int64)[slots >> 7]
+        ps = tab[2048:3072].view(np.uint32).astype(np.int64)
+        first, span, c0, f = e & 255, (e >> 8) & 255, (e >> 16) & 0xFFFF, (e >> 32) & 0xFFFF
+        sym = first.copy()
+        for k in range(1, 256):                   # every candidate of the bucket, in order
+            cand = first + k
+            take = (k <= span) & ((ps[np.minimum(cand, 255)] & 0xFFFF) <= slots)
+            sym = np.where(take, cand, sym)
+        u = ps[sym]
+        moved = sym != first
+        return sym, np.where(moved, u & 0xFFFF, c0), np.where(moved, u >> 16, f)
+
+    sym, c0, f = decode_all(dth[6])                       # no table: one symbol with every slot
+    assert not sym.any() and not c0.any() and (f == 1 << 15).all()
     for t in range(6):
-        coarse = dth[t, :256].astype(np.int64)
-        c16 = dth[t, 256:256 + 514].view(np.uint16).astype(np.int64)
-        assert np.array_equal(c16, cum[t])
-        sym = coarse[slots >> 7]
-        for _ in range(256):                      # step forward while the next cumulative frequency <= slot
-            adv = (c16[np.minimum(sym + 1, 256)] <= slots) & (sym < 255)
-            if not adv.any():
-                break
-            sym = sym + adv
+        sym, c0, f = decode_all(dth[5 - t])
         assert np.array_equal(sym, luth[t].astype(np.int64)), t
+        assert np.array_equal(c0, cum[t][sym]) and np.array_equal(f, freq[t][sym])
         assert np.array_equal(np.repeat(np.arange(256), freq[t]), luth[t])
 
 
