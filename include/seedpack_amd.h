@@ -40,6 +40,10 @@ int spa_set_device(int device);
 int spa_get_device(int* device);
 int spa_malloc(void** ptr, size_t nbytes);
 int spa_free(void* ptr);
+/* Page-locked host memory (hipHostMalloc): copies to and from it run at the link's full rate, as the
+ * reference's pinned staging does (gpuquant.py:266-282). */
+int spa_host_alloc(void** ptr, size_t nbytes);
+int spa_host_free(void* ptr);
 int spa_memcpy_h2d(void* dst, const void* src, size_t nbytes, void* stream);
 int spa_memcpy_d2h(void* dst, const void* src, size_t nbytes, void* stream);
 int spa_memcpy_d2d(void* dst, const void* src, size_t nbytes, void* stream);
@@ -169,13 +173,19 @@ uint64_t spa_r2_stats_work_bytes(int64_t nrows, int rowlen);
 int spa_r2_hist(const void* dev, const void* tb, const void* sg, int nseg, const int16_t* rfi, const int16_t* cfi,
                 const int8_t* scl, const int32_t* rowmap, uint32_t* counts, void* stream);
 
-/* rANS encode of nseg segments (v2_enc, bf16v2.py:77-111): slot s of `out` (16-byte aligned; cap
- * bytes, a multiple of 16) ends with the segment's bytes, out_len[s] their count (0xFFFFFFFF: under
- * 64 bytes left after some weight, the reference's overflow). fc_work: ceil(nseg / 64) x 64 x 16384 x 3
- * u32 of workspace. */
+/* Coding words for nctx contexts (roles x 656): fcw[c][sym] = freq[remap[c]][sym] << 16 |
+ * cum[remap[c]][sym] (256 u32 per context; zeros where remap[c] < 0). The reference's v2_enc reads
+ * freq, cum and remap per symbol (bf16v2.py:84-111). */
+int spa_r2_encode_tables(const int32_t* remap, int nctx, const uint16_t* freq, const uint32_t* cum, uint32_t* fcw,
+                         void* stream);
+
+/* rANS encode of nseg segments (v2_enc, bf16v2.py:77-111) with spa_r2_encode_tables' words: slot s
+ * of `out` (16-byte aligned; cap bytes, a multiple of 16) ends with the segment's bytes, out_len[s]
+ * their count (0xFFFFFFFF: under 64 bytes left after some weight, the reference's overflow).
+ * fc_work: ceil(nseg / 64) x 64 x 16384 x 3 u32 of workspace. */
 int spa_r2_encode(const void* dev, const void* tb, const void* sg, int nseg, const int16_t* rfi, const int16_t* cfi,
-                  const int8_t* scl, const int32_t* rowmap, const int32_t* remap, const uint16_t* freq,
-                  const uint32_t* cum, uint32_t* fc_work, void* out, uint64_t cap, uint32_t* out_len, void* stream);
+                  const int8_t* scl, const int32_t* rowmap, const uint32_t* fcw, uint32_t* fc_work, void* out,
+                  uint64_t cap, uint32_t* out_len, void* stream);
 
 /* rANS decode of nseg segments into dev (v2_dec, bf16v2.py:113-137): `in` (16-byte aligned) holds
  * in_bytes of coded stream, segment s starting at in_off[s]; reads stop at in_bytes rounded up to 16

@@ -24,6 +24,8 @@ SIGNATURES = {
     "spa_get_device": (c_int, [ctypes.POINTER(c_int)]),
     "spa_malloc": (c_int, [ctypes.POINTER(c_void_p), c_size_t]),
     "spa_free": (c_int, [c_void_p]),
+    "spa_host_alloc": (c_int, [ctypes.POINTER(c_void_p), c_size_t]),
+    "spa_host_free": (c_int, [c_void_p]),
     "spa_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "spa_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "spa_memcpy_d2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
@@ -62,8 +64,9 @@ SIGNATURES = {
                              c_void_p]),
     "spa_r2_stats_work_bytes": (c_uint64, [c_int64, c_int]),
     "spa_r2_hist": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
-    "spa_r2_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                              c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_uint64, c_void_p, c_void_p]),
+    "spa_r2_encode_tables": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "spa_r2_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                              c_void_p, c_uint64, c_void_p, c_void_p]),
     "spa_r2_decode": (c_int, [c_void_p, c_uint64, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
                               c_void_p, c_void_p, c_void_p, c_void_p]),
     "spa_r2_build_dec_tables": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),

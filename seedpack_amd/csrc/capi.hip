@@ -60,6 +60,12 @@ int spa_malloc(void** ptr, size_t nbytes) {
     return SPA_OK;
 }
 int spa_free(void* ptr) { SPA_HIP_TRY(hipFree(ptr)); return SPA_OK; }
+int spa_host_alloc(void** ptr, size_t nbytes) {
+    if (!ptr) return fail(SPA_ERR_ARG, "spa_host_alloc: null out pointer");
+    SPA_HIP_TRY(hipHostMalloc(ptr, nbytes ? nbytes : 1, hipHostMallocDefault));
+    return SPA_OK;
+}
+int spa_host_free(void* ptr) { SPA_HIP_TRY(hipHostFree(ptr)); return SPA_OK; }
 int spa_memcpy_h2d(void* dst, const void* src, size_t n, void* s) {
     SPA_HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, (hipStream_t)s));
     SPA_HIP_TRY(hipStreamSynchronize((hipStream_t)s));

@@ -330,19 +330,28 @@ __global__ __launch_bounds__(HT) void k_hist(const uint8_t* __restrict__ dev, co
     if (tab >= 0) hist_flush(hm, he, hs, tab, pe0, counts);
 }
 
-// The (freq << 16 | cum) word of every symbol, three per weight in forward order, for the coder.
-// Layout: word i of batch segment s at fc[((s / 64) * 3 * SEG + i) * 64 + s % 64], so that the 64
-// lanes of an encoding wave read one 256-byte row per step. A workgroup takes 64 segments x FCK
-// weights: each thread computes 16 weights' words of one segment into an LDS tile, which is then
-// written out row by row.
+// Per-context coding words: fcw[c][sym] = freq << 16 | cum of symbol sym in context c's table
+// (c over roles x 656; contexts never coded hold zeros), so the symbol pass needs one load per
+// symbol and no remap.
+__global__ __launch_bounds__(256) void k_fcw(const int32_t* __restrict__ remap, const uint16_t* __restrict__ freq,
+                                             const uint32_t* __restrict__ cum, uint32_t* __restrict__ fcw) {
+    const int t = remap[blockIdx.x], i = threadIdx.x;
+    fcw[(size_t)blockIdx.x * 256 + i] = t < 0 ? 0u : (((uint32_t)freq[(size_t)t * 256 + i] << 16) | cum[(size_t)t * 257 + i]);
+}
+
+// The coding word of every symbol, three per weight in forward order, for the coder. Layout: word i
+// of batch segment s at fc[((s / 64) * 3 * SEG + i) * 64 + s % 64], so that the 64 lanes of an
+// encoding wave read one 256-byte row per step. A workgroup takes 64 segments x FCK weights; lane l
+// of wave v takes segment l's weights v*16 .. v*16+15 of the chunk (read as two 16-byte vectors, with
+// their column side information, where rows are 16-weight aligned), its 48 words go to an LDS tile
+// [word][segment] that is written out row by row.
 constexpr int FCK = 64;
 __global__ __launch_bounds__(256) void k_fc(const uint8_t* __restrict__ dev, const TB* __restrict__ tb, const SG* __restrict__ sg,
                                             int nseg, const int16_t* __restrict__ rfi, const int16_t* __restrict__ cfi,
                                             const int8_t* __restrict__ scl, const int32_t* __restrict__ rowmap,
-                                            const int32_t* __restrict__ remap, const uint16_t* __restrict__ freq,
-                                            const uint32_t* __restrict__ cum, uint32_t* __restrict__ fc) {
+                                            const uint32_t* __restrict__ fcw, uint32_t* __restrict__ fc) {
     __shared__ uint32_t tile[3 * FCK][65];
-    const int t = threadIdx.x, ls = t >> 2, sub = t & 3;
+    const int t = threadIdx.x, ls = t & 63, sub = t >> 6;
     const int s = blockIdx.x * 64 + ls;
     const int k0 = blockIdx.y * FCK + sub * 16;
     if (s < nseg) {
@@ -350,19 +359,44 @@ __global__ __launch_bounds__(256) void k_fc(const uint8_t* __restrict__ dev, con
         if (k0 < g.n) {
             const TB T = tb[g.t];
             const uint16_t* W = reinterpret_cast<const uint16_t*>(dev + T.doff);
+            const uint32_t* fw = fcw + (size_t)T.tab * 256;
             Cursor cur;
             cur.start(g.i0 + k0, T.rowlen);
             const int kn = g.n - k0 < 16 ? g.n - k0 : 16;
-            for (int q = 0; q < kn; ++q, cur.step(1, T.rowlen)) {
-                int ex, man, sgn, pe, rlc, sc;
-                const int64_t orow = orig_row(T, rowmap, cur.rc);
-                const int j = cur.j;
-                contexts(T, orow, j, W[orow * T.rowlen + j], rfi, cfi, scl, ex, man, sgn, pe, rlc, sc);
-                const int t0 = remap[T.tab + pe], t1 = remap[T.tab + 512 + rlc], t2 = remap[T.tab + 640 + sc];
+            auto words = [&](int q, uint32_t u, int pred, int scv) {
+                const int ex = (u >> 7) & 255, man = u & 127, sgn = u >> 15;
+                const int pe = clampi(pred + 256, 0, 511);
+                const int rlc = clampi(8 * ex - pred - 1016 + 64, 0, 127);
                 const int r = (sub * 16 + q) * 3;
-                tile[r][ls] = ((uint32_t)freq[t0 * 256 + ex] << 16) | cum[t0 * 257 + ex];
-                tile[r + 1][ls] = ((uint32_t)freq[t1 * 256 + man] << 16) | cum[t1 * 257 + man];
-                tile[r + 2][ls] = ((uint32_t)freq[t2 * 256 + sgn] << 16) | cum[t2 * 257 + sgn];
+                tile[r][ls] = fw[pe * 256 + ex];
+                tile[r + 1][ls] = fw[(512 + rlc) * 256 + man];
+                tile[r + 2][ls] = fw[(640 + scv) * 256 + sgn];
+            };
+            const bool vec = kn == 16 && (T.rowlen & 15) == 0 && (T.colbase & 15) == 0 && (cur.j & 15) == 0 &&
+                             ((reinterpret_cast<uintptr_t>(W) & 15) == 0);
+            if (vec) {                           // 16 weights of one row
+                const int64_t orow = orig_row(T, rowmap, cur.rc);
+                const int rf = rfi[T.rowbase + orow];
+                const uint4* wp = reinterpret_cast<const uint4*>(W + orow * T.rowlen + cur.j);
+                const uint4* cp = reinterpret_cast<const uint4*>(cfi + T.colbase + cur.j);
+                const uint4 w0 = wp[0], w1 = wp[1], c0 = cp[0], c1 = cp[1];
+                const uint4 s16 = *reinterpret_cast<const uint4*>(scl + T.colbase + cur.j);
+                const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                const uint32_t cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                const uint32_t sv[4] = {s16.x, s16.y, s16.z, s16.w};
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const uint32_t u = (wv[q >> 1] >> (16 * (q & 1))) & 0xFFFFu;
+                    const int cfv = (int)(int16_t)(uint16_t)(cv[q >> 1] >> (16 * (q & 1)));
+                    const int scv = (int)(int8_t)(uint8_t)(sv[q >> 2] >> (8 * (q & 3)));
+                    words(q, u, rf + cfv, scv);
+                }
+            } else {
+                for (int q = 0; q < kn; ++q, cur.step(1, T.rowlen)) {
+                    const int64_t orow = orig_row(T, rowmap, cur.rc);
+                    const int j = cur.j;
+                    words(q, W[orow * T.rowlen + j], rfi[T.rowbase + orow] + cfi[T.colbase + j], scl[T.colbase + j]);
+                }
             }
         }
     }
@@ -394,8 +428,8 @@ __global__ __launch_bounds__(64) void k_enc(const SG* __restrict__ sg, int nseg,
             acc = 0;
         }
     };
-    // words loaded 8 at a time, one group ahead of the coding (their addresses do not depend on it)
-    constexpr int PF = 8;
+    // words loaded 16 at a time, one group ahead of the coding (their addresses do not depend on it)
+    constexpr int PF = 16;
     uint32_t nxt[PF];
 #pragma unroll
     for (int q = 0; q < PF; ++q) {
@@ -705,9 +739,17 @@ int spa_r2_hist(const void* dev, const void* tb, const void* sg, int nseg, const
     return SPA_OK;
 }
 
+int spa_r2_encode_tables(const int32_t* remap, int nctx, const uint16_t* freq, const uint32_t* cum, uint32_t* fcw, void* stream) {
+    if (nctx < 0) return fail(SPA_ERR_ARG, "spa_r2_encode_tables: negative context count");
+    if (nctx == 0) return SPA_OK;
+    hipLaunchKernelGGL(k_fcw, dim3((unsigned)nctx), dim3(256), 0, (hipStream_t)stream, remap, freq, cum, fcw);
+    SPA_HIP_TRY(hipGetLastError());
+    return SPA_OK;
+}
+
 int spa_r2_encode(const void* dev, const void* tb, const void* sg, int nseg, const int16_t* rfi, const int16_t* cfi,
-                  const int8_t* scl, const int32_t* rowmap, const int32_t* remap, const uint16_t* freq, const uint32_t* cum,
-                  uint32_t* fc_work, void* out, uint64_t cap, uint32_t* out_len, void* stream) {
+                  const int8_t* scl, const int32_t* rowmap, const uint32_t* fcw, uint32_t* fc_work, void* out, uint64_t cap,
+                  uint32_t* out_len, void* stream) {
     if (nseg < 0) return fail(SPA_ERR_ARG, "spa_r2_encode: negative segment count");
     if (cap < 1024 || cap % 16) return fail(SPA_ERR_ARG, "spa_r2_encode: segment capacity %llu (a multiple of 16, >= 1024)", (unsigned long long)cap);
     if (reinterpret_cast<uintptr_t>(out) & 15) return fail(SPA_ERR_ARG, "spa_r2_encode: output not 16-byte aligned");
@@ -715,7 +757,7 @@ int spa_r2_encode(const void* dev, const void* tb, const void* sg, int nseg, con
     hipStream_t st = (hipStream_t)stream;
     const unsigned ngrp = (unsigned)((nseg + 63) / 64);
     hipLaunchKernelGGL(k_fc, dim3(ngrp, SEG / FCK), dim3(256), 0, st, (const uint8_t*)dev, (const TB*)tb, (const SG*)sg, nseg, rfi,
-                       cfi, scl, rowmap, remap, freq, cum, fc_work);
+                       cfi, scl, rowmap, fcw, fc_work);
     hipLaunchKernelGGL(k_enc, dim3(ngrp), dim3(64), 0, st, (const SG*)sg, nseg, (const uint32_t*)fc_work, (uint8_t*)out, cap,
                        out_len);
     SPA_HIP_TRY(hipGetLastError());

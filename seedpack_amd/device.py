@@ -65,6 +65,32 @@ def empty(shape, dtype):
     return DeviceArray(shape, dtype)
 
 
+class _Pinned:
+    """owner of a page-locked host allocation; freed with the last array that views it"""
+
+    def __init__(self, nbytes):
+        p = ctypes.c_void_p()
+        check(lib().spa_host_alloc(ctypes.byref(p), nbytes))
+        self.ptr = p.value
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            try:
+                lib().spa_host_free(self.ptr)
+            except Exception:
+                pass
+            self.ptr = None
+
+
+def pinned(n, dtype=np.uint8):
+    """a numpy array of n elements in page-locked host memory"""
+    dtype = np.dtype(dtype)
+    owner = _Pinned(max(1, n * dtype.itemsize))
+    buf = (ctypes.c_char * max(1, n * dtype.itemsize)).from_address(owner.ptr)
+    buf._owner = owner                                # the buffer keeps the allocation alive
+    return np.frombuffer(buf, dtype, n)
+
+
 def synchronize(stream=None):
     check(lib().spa_stream_synchronize(stream) if stream is not None else lib().spa_device_synchronize())
 

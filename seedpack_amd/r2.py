@@ -19,6 +19,7 @@ import json
 import lzma
 import re
 import struct
+import time
 from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
@@ -184,6 +185,13 @@ class _Timer:
 
     def __init__(self, on, stream):
         self.on, self.stream, self.marks = on, stream, []
+        self.host, self.t = {}, time.perf_counter()
+
+    def lap(self, name):
+        """host wall time since the previous lap, added to `name`"""
+        now = time.perf_counter()
+        self.host[name] = self.host.get(name, 0.0) + (now - self.t)
+        self.t = now
 
     def mark(self, name):
         if self.on:
@@ -192,10 +200,13 @@ class _Timer:
             self.marks.append((name, e))
 
     def result(self):
+        """device ms per phase (HIP events), and the host wall seconds per lap under "host_s" """
         out = {}
         for (name, e0), (_, e1) in zip(self.marks, self.marks[1:]):
             if name:
                 out[name] = out.get(name, 0.0) + e0.elapsed_ms(e1)
+        if self.on:
+            out["host_s"] = {k: round(v, 4) for k, v in self.host.items()}
         return out
 
 
@@ -209,7 +220,7 @@ class BF16v2:
     (encode in batches of `enc_batch` segments, for its 12-byte-per-weight symbol workspace).
     `group_bytes` is kept for the reference's interface."""
 
-    def __init__(self, group_bytes=400 << 20, dedup=True, stream=None, enc_batch=131072, timing=False):
+    def __init__(self, group_bytes=400 << 20, dedup=True, stream=None, enc_batch=262144, timing=False):
         self.group_bytes, self.dedup, self.stream = group_bytes, dedup, stream
         self.enc_batch, self.timing, self.last_timing = enc_batch, timing, {}
 
@@ -277,6 +288,7 @@ class BF16v2:
             a = layout["t"][0][0] if nt else 0
             b = max((off + nb for off, nb, _, _ in layout["t"]), default=0)
             d = dev.DeviceArray.from_host(host[a:b] if b > a else np.zeros(1, np.uint8), st)
+        tm.lap("upload")
 
         def rows_of(off, rl):
             """the BF16 bits of some rows of the tensor at file offset `off`"""
@@ -290,6 +302,7 @@ class BF16v2:
         else:
             side_dev, hh = [dev.DeviceArray(1, x.dtype) for x in (rfi, cfi, scl)], None
         tm.mark(None)
+        tm.lap("stats")
         for i in range(nt):
             off, nb, rl, _ = layout["t"][i]
             nr = nb // 2 // rl
@@ -311,11 +324,24 @@ class BF16v2:
         check(lib().spa_r2_hist(d.ptr, tb_d.ptr, sg_d.ptr, nseg, side_dev[0].ptr, side_dev[1].ptr, side_dev[2].ptr,
                                 rm_d.ptr, counts.ptr, st))
         tm.mark(None)
+        tm.lap("dups")
+        # the side information and the metadata are final here: their zstd-19 runs on the host
+        # while the device codes the stream
+        dups = [[i, r, s_] for i, ps in dup_pairs.items() for r, s_ in ps]
+        meta = dict(layout=layout, dups=dups, nrows_c=[nrows_c[i] for i in range(nt)])
+        pool = ThreadPoolExecutor(2)
+        meta_job = pool.submit(zstd.compress, json.dumps(meta).encode(), 19)
+        side_job = pool.submit(zstd.compress, rfi.tobytes() + cfi.tobytes() + scl.tobytes(), 19)
         counts_h = counts.to_host(stream=st)
+        tm.lap("hist")
         freq, used = normalize(counts_h)
+        tm.lap("normalize")
         remap = np.full(counts_h.shape[0], -1, np.int32)
         remap[used] = np.arange(len(used), dtype=np.int32)
-        remap_d, freq_d, cum_d = (dev.DeviceArray.from_host(x, st) for x in (remap, freq, cum_of(freq)))
+        remap_d, freq_d, cum_d = (dev.DeviceArray.from_host(x if len(x) else np.zeros((1,) + x.shape[1:], x.dtype), st)
+                                  for x in (remap, freq, cum_of(freq)))
+        fcw = dev.DeviceArray((max(1, len(remap)), 256), np.uint32)
+        check(lib().spa_r2_encode_tables(remap_d.ptr, len(remap), freq_d.ptr, cum_d.ptr, fcw.ptr, st))
         streams, lens_all = [], []
         nbat = min(max(nseg, 1), self.enc_batch)
         fc = dev.DeviceArray(-(-nbat // 64) * 64 * SEG * 3, np.uint32)
@@ -325,8 +351,7 @@ class BF16v2:
             n = min(nbat, nseg - s0)
             tm.mark("encode")
             check(lib().spa_r2_encode(d.ptr, tb_d.ptr, sg_d.ptr + 16 * s0, n, side_dev[0].ptr, side_dev[1].ptr,
-                                      side_dev[2].ptr, rm_d.ptr, remap_d.ptr, freq_d.ptr, cum_d.ptr, fc.ptr, out.ptr, CAP,
-                                      out_len.ptr, st))
+                                      side_dev[2].ptr, rm_d.ptr, fcw.ptr, fc.ptr, out.ptr, CAP, out_len.ptr, st))
             tm.mark(None)
             lens = out_len.to_host(stream=st)[:n]
             if (lens == 0xFFFFFFFF).any():
@@ -338,16 +363,21 @@ class BF16v2:
             tm.mark("gather")
             check(lib().spa_qr_gather(out.ptr, CAP, out_len.ptr, offs_d.ptr, n, dst.ptr, st))
             tm.mark(None)
-            streams.append(dst.to_host(stream=st)[:int(offs[-1])].tobytes())
+            piece = dev.pinned(int(offs[-1]))            # read back at the link's full rate
+            if len(piece):
+                check(lib().spa_memcpy_d2h(piece.ctypes.data, dst.ptr, len(piece), st))
+            streams.append(piece)
             lens_all.append(lens)
-        self.last_timing = tm.result()
+        tm.lap("encode")
         lens = np.concatenate(lens_all).astype(np.uint32) if lens_all else np.zeros(0, np.uint32)
-        dups = [[i, r, s] for i, ps in dup_pairs.items() for r, s in ps]
-        meta = dict(layout=layout, dups=dups, nrows_c=[nrows_c[i] for i in range(nt)])
-        stream = b"".join(streams)
-        return {"meta": zstd.compress(json.dumps(meta).encode(), 19),
-                "side": zstd.compress(rfi.tobytes() + cfi.tobytes() + scl.tobytes(), 19),
-                "tables": store_tables(freq, used), "lens": zstd.compress(lens.tobytes(), 19), "stream": stream,
+        # the coded stream: one piece per encoder batch, kept in pieces (pack_parts splices them)
+        stream = streams[0] if len(streams) == 1 else (streams or np.zeros(0, np.uint8))
+        small = {"meta": meta_job.result(), "side": side_job.result(), "tables": store_tables(freq, used),
+                 "lens": zstd.compress(lens.tobytes(), 19)}
+        pool.shutdown()
+        tm.lap("zstd")
+        self.last_timing = tm.result()
+        return {**small, "stream": stream,
                 "arrays": dict(rfi=rfi, cfi=cfi, scl=scl, counts=counts_h, freq=freq, used=used, lens=lens,
                                nrows_c=np.array(meta["nrows_c"], np.int64),
                                dups=np.array(dups, np.int64).reshape(-1, 3), rowmap=rowmap)}
@@ -377,6 +407,7 @@ class BF16v2:
         if not isinstance(parts, dict):
             parts = unpack(parts if isinstance(parts, memoryview) else memoryview(parts))
         dec = _Decoder(parts.__getitem__, st, tm)
+        tm.lap("tables")
         layout, nt = dec.layout, len(dec.layout["t"])
         if nt == 0 and device:
             return dev.DeviceArray(1, np.uint8)
@@ -384,14 +415,17 @@ class BF16v2:
             a = 0 if device else layout["t"][0][0]
             b = max(off + nb for off, nb, _, _ in layout["t"])
             d = dev.DeviceArray(b - a, np.uint8)
-            s_d = _Decoder.upload(np.frombuffer(parts["stream"], np.uint8), st)
+            s_d = _Decoder.upload(parts["stream"], st)
+            tm.lap("upload")
             idxs = list(range(nt))
             dec.run(s_d, dec.soff[:-1], d, idxs, [layout["t"][i][0] - a for i in idxs], tm)
+            tm.lap("decode")
             if device:
                 dev.synchronize(st)
                 self.last_timing = tm.result()
                 return d
             g = d.to_host(stream=st)
+            tm.lap("readback")
             self.last_timing = tm.result()
         if out is None:
             out = alloc(layout["size"]) if alloc else np.zeros(layout["size"], np.uint8)
@@ -453,12 +487,16 @@ class _Decoder:
 
     @staticmethod
     def upload(stream_h, st):
-        """coded stream bytes -> device, padded to a whole number of 16-byte blocks (the decoder's
-        reads)"""
-        n = len(stream_h)
+        """coded stream bytes (a bytes-like or a list of pieces) -> device, padded to a whole number
+        of 16-byte blocks (the decoder's reads)"""
+        pieces = [np.frombuffer(p, np.uint8) for p in (stream_h if isinstance(stream_h, list) else [stream_h])]
+        n = sum(len(p) for p in pieces)
         d = dev.DeviceArray(max(16, -(-n // 16) * 16), np.uint8)
-        if n:
-            check(lib().spa_memcpy_h2d(d.ptr, np.ascontiguousarray(stream_h).ctypes.data, n, st))
+        o = 0
+        for p in pieces:
+            if len(p):
+                check(lib().spa_memcpy_h2d(d.ptr + o, np.ascontiguousarray(p).ctypes.data, len(p), st))
+            o += len(p)
         return d
 
     def run(self, s_d, in_off, d, idxs, doffs, tm=None):
