@@ -3,7 +3,9 @@
 //
 // Mapping: a group of G lanes per super-block, one lane per sub-block (G = 8 sub-blocks of 32 for
 // Q4_K/Q5_K, G = 16 sub-blocks of 16 for Q2_K/Q3_K/Q6_K); a 256-lane workgroup handles 256/G
-// consecutive super-blocks. The per-sub-block searches (the bulk of the work) run in parallel.
+// consecutive super-blocks. The per-sub-block searches (the bulk of the work) run in parallel; with
+// an imatrix the super-block's own searches over its G sub-block results run once, one lane per
+// task (the scales, the mins) in the workgroup's first wave, while the other waves wait.
 // The super-block sum of squares must be one left-to-right float sum over 256 terms: lane g adds
 // its terms to the running sum it receives from lane g-1 (a shuffle per hand-off), so the order is
 // the reference's. Sub-block results reach every lane of the group by shuffles; each lane repeats
@@ -160,6 +162,42 @@ struct Q45K {
         }
         return h;
     }
+    // imatrix path split for the kernel's block-level phase: the sub-block search (every lane) ...
+    static constexpr int NT = 2;
+    __device__ __forceinline__ static void sub_imx(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB], float& a, float& b,
+                                                   float& wsum) {
+        const float sum_x2 = group_sumsq<G, SUB>(x, sub);
+        const float sigma2 = 2 * sum_x2 / 256;
+        float w[SUB];
+#pragma unroll
+        for (int l = 0; l < SUB; ++l) w[l] = qw[l] * sqrtf(sigma2 + x[l] * x[l]);
+        float sumw = 0;
+#pragma unroll
+        for (int l = 0; l < SUB; ++l) sumw += w[l];
+        float min;
+        a = make_qkx3_quants<SUB, NMAX>(x, w, L, min, -0.9f, 0.05f, 36);
+        b = min;
+        wsum = sumw;
+    }
+    // ... the super-block's scales (task 0) or mins (task 1) quantized (one lane each) ...
+    __device__ __forceinline__ static void task(int, const float (&v)[G], const float (&sw)[G], uint32_t& f16, uint8_t (&lv)[G]) {
+        int Lq[G];
+        f16 = f32_to_f16(make_qp_quants<G>(63, v, Lq, sw));
+#pragma unroll
+        for (int j = 0; j < G; ++j) lv[j] = (uint8_t)(NMAX == 31 ? tmin(63, Lq[j] & 0xff) : (Lq[j] & 0xff));
+    }
+    // ... and the header from the two
+    __device__ __forceinline__ static KHeader assemble(const uint32_t* f16, const uint8_t (*lv)[G]) {
+        KHeader h;
+        h.zero = false;
+        int Ls[G], Lm[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) { Ls[j] = lv[0][j]; Lm[j] = lv[1][j]; }
+        pack_k4_scales(Ls, Lm, h.sc);
+        h.d = f16[0];
+        h.dmin = f16[1];
+        return h;
+    }
     // decoded (scale, min) levels of sub-block j, as get_scale_min_k4 reads them back
     __device__ __forceinline__ static uint32_t info(const KHeader& h, int j) { return scale_min_k4(j, h.sc); }
     // requantize this sub-block with the stored scales (ggml-quants.c:1607-1616)
@@ -278,6 +316,38 @@ struct Q2K {
             mmf = f16_to_f32(h.dmin);
         }
         (void)dmf; (void)mmf;
+        return h;
+    }
+    // imatrix path split for the kernel's block-level phase (see Q45K)
+    static constexpr int NT = 2;
+    __device__ __forceinline__ static void sub_imx(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB], float& a, float& b,
+                                                   float& wsum) {
+        const float sumx2 = group_sumsq<G, SUB>(x, sub);
+        const float sigma2 = sumx2 / 256;
+        float w[SUB];
+#pragma unroll
+        for (int l = 0; l < SUB; ++l) w[l] = qw[l] * sqrtf(sigma2 + x[l] * x[l]);
+        float sumw = 0;
+#pragma unroll
+        for (int l = 0; l < SUB; ++l) sumw += w[l];
+        float min;
+        a = make_qkx3_quants<SUB, 3>(x, w, L, min, -0.9f, 0.05f, 36);
+        b = min;
+        wsum = sumw;
+    }
+    __device__ __forceinline__ static void task(int, const float (&v)[G], const float (&sw)[G], uint32_t& f16, uint8_t (&lv)[G]) {
+        int Lq[G];
+        f16 = f32_to_f16(make_qp_quants<G>(15, v, Lq, sw));
+#pragma unroll
+        for (int j = 0; j < G; ++j) lv[j] = (uint8_t)(Lq[j] & 0xff);
+    }
+    __device__ __forceinline__ static KHeader assemble(const uint32_t* f16, const uint8_t (*lv)[G]) {
+        KHeader h;
+        h.zero = false;
+        h.d = f16[0];
+        h.dmin = f16[1];
+#pragma unroll
+        for (int j = 0; j < G; ++j) h.sc[j] = ((uint32_t)lv[0][j] | ((uint32_t)lv[1][j] << 4)) & 0xff;
         return h;
     }
     __device__ __forceinline__ static uint32_t info(const KHeader& h, int j) { return h.sc[j]; }
@@ -422,6 +492,44 @@ struct Q3K {
         }
         return h;
     }
+    // imatrix path split for the kernel's block-level phase (see Q45K): one task, the scales' quantization
+    static constexpr int NT = 1;
+    __device__ __forceinline__ static void sub_imx(float (&x)[SUB], const float* qw, int sub, int (&L)[SUB], float& a, float& b,
+                                                   float& wsum) {
+        const float sumx2 = group_sumsq<G, SUB>(x, sub);
+        const float sigma2 = 2 * sumx2 / 256;
+        float w[SUB];
+#pragma unroll
+        for (int l = 0; l < SUB; ++l) w[l] = qw[l] * sqrtf(sigma2 + x[l] * x[l]);
+        float sumw = 0;
+#pragma unroll
+        for (int l = 0; l < SUB; ++l) sumw += w[l];
+        a = make_qx_quants<SUB, true>(4, x, w, L);
+        b = 0.f;
+        wsum = sumw;
+    }
+    __device__ __forceinline__ static void task(int, const float (&a)[G], const float (&sw)[G], uint32_t& f16, uint8_t (&lv)[G]) {
+        int Ls[G];
+        f16 = f32_to_f16(make_qx_quants<G, true>(32, a, sw, Ls));
+#pragma unroll
+        for (int j = 0; j < G; ++j) lv[j] = (uint8_t)Ls[j];
+    }
+    __device__ __forceinline__ static KHeader assemble(const uint32_t* f16, const uint8_t (*lv)[G]) {
+        KHeader h;
+        h.zero = false;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) h.sc[j] = 0;
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            int l = lv[0][j];
+            if (j < 8) h.sc[j] = (uint32_t)(l & 0xF);
+            else h.sc[j - 8] = (h.sc[j - 8] | ((uint32_t)(l & 0xF) << 4)) & 0xff;
+            l >>= 4;
+            h.sc[j % 4 + 8] = (h.sc[j % 4 + 8] | ((uint32_t)l << (2 * (j / 4)))) & 0xff;
+        }
+        h.d = f16[0];
+        return h;
+    }
     // the signed 6-bit scale of sub-block j as read back from the packed bytes (ggml-quants.c:1411-1413)
     __device__ __forceinline__ static uint32_t info(const KHeader& h, int j) {
         int sc = j < 8 ? (int)(h.sc[j] & 0xF) : (int)(h.sc[j - 8] >> 4);
@@ -469,6 +577,7 @@ struct Q3K {
 
 struct Q6K {
     static constexpr int G = 16, SUB = 16, BS = 210;
+    static constexpr int NT = 0;       // the block level is a max and a rounding: no split
     // quantize_row_q6_K_impl (ggml-quants.c:1971-2053) and quantize_row_q6_K_ref (:1870-1938): the
     // imatrix path weights by the raw imatrix, the NULL path by x*x.
     template <bool IMX>
@@ -568,7 +677,33 @@ __global__ __launch_bounds__(WG) void k_kquant(const void* __restrict__ src, int
         qw = imx + (sbc - row * sb_per_row) * 256 + sub * SUB;
     }
     int L[SUB];
-    const KHeader h = Op::template search<IMX>(x, qw, sub, L);
+    KHeader h;
+    if constexpr (IMX && Op::NT > 0) {
+        // The block-level searches (make_qp_quants / make_qx_quants over the G sub-block results) run
+        // once per super-block, one lane per task, instead of in every lane of the group: lanes
+        // publish their sub-block results, the first NT x SBW lanes of the workgroup run the tasks,
+        // every lane assembles its header from the tasks' outputs.
+        __shared__ float pa[SBW][G], pb[SBW][G], pw[SBW][G];
+        __shared__ uint32_t tf[SBW][Op::NT];
+        __shared__ uint8_t tl[SBW][Op::NT][G];
+        Op::sub_imx(x, qw, sub, L, pa[lsb][sub], pb[lsb][sub], pw[lsb][sub]);
+        __syncthreads();
+        if (threadIdx.x < SBW * Op::NT) {
+            const int tsb = threadIdx.x / Op::NT, which = threadIdx.x % Op::NT;
+            const float* src = which ? pb[tsb] : pa[tsb];     // the task's values: scales or mins
+            float v[G], w[G];
+#pragma unroll
+            for (int j = 0; j < G; ++j) { v[j] = src[j]; w[j] = pw[tsb][j]; }
+            uint8_t lv[G];
+            Op::task(which, v, w, tf[tsb][which], lv);
+#pragma unroll
+            for (int j = 0; j < G; ++j) tl[tsb][which][j] = lv[j];
+        }
+        __syncthreads();
+        h = Op::assemble(tf[lsb], tl[lsb]);
+    } else {
+        h = Op::template search<IMX>(x, qw, sub, L);
+    }
     // every lane of the group holds the same header; lane 0 publishes the per-sub-block decode
     if (sub == 0) {
 #pragma unroll
