@@ -147,8 +147,11 @@ __device__ __forceinline__ float make_qkx2_quants(const float (&x)[N], const flo
 // Note the running `min`: a step that wins changes the offset used by every later step.
 // The levels of a step are a pure function of (iscale, min), so only the winning pair is kept and
 // L is produced once at the end. Inside the step loop, nearest_int(MIN(v, nmax)) for 0 < v <= nmax
-// is computed as rintf(fminf(v, nmax)): both round half to even and return the same integer (the
-// magic-number form is exact for |v| < 2^22); v <= 0 and NaN give 0 as in the C code.
+// is computed as rintf(fminf(fmaxf(v, 0), nmax)): both round half to even and return the same integer
+// (the magic-number form is exact for |v| < 2^22); v <= 0 and NaN give a zero level as in the C code
+// (possibly -0.0, which changes nothing: every sum starts at +0.0 and adds non-negative terms or
+// w*l*x products, and an IEEE sum from +0.0 is never -0.0, so each sum and each squared difference
+// is the same number).
 template <int N, int NMAX>
 __device__ __forceinline__ float make_qkx3_quants(const float (&x)[N], const float (&w)[N], int (&L)[N], float& the_min,
                                                   float rmin, float rdelta, int nstep) {
@@ -189,7 +192,7 @@ __device__ __forceinline__ float make_qkx3_quants(const float (&x)[N], const flo
 #pragma unroll
         for (int i = 0; i < N; ++i) {
             const float v = iscale * (x[i] - min);
-            const float fl = v > 0.f ? rintf(fminf(v, (float)NMAX)) : 0.f;
+            const float fl = rintf(fminf(fmaxf(v, 0.f), (float)NMAX));
             Lf[i] = fl;
             const float wl = w[i] * fl;
             sum_l += wl;
