@@ -297,6 +297,34 @@ def r2_cfg4(stream, layers=36):
     return res
 
 
+def dequant_cfg2(stream, dsrc, dimx, reps=10):
+    """dequantizers (GPUQuant.dequantize) on the configuration-2 embedding quantized to each K-quant
+    and Q8_0 / Q4_0: float32 out; HBM-bound (4 bytes written per weight + the block bytes read)"""
+    from seedpack_amd import device as dev
+    from seedpack_amd._lib import check, lib
+    from seedpack_amd.gpuquant import quantize_into
+    from seedpack_amd.requant import NAMES, row_size
+    rows, npr = 151936, 1024
+    out = dev.DeviceArray(rows * npr, np.float32)
+    res = {}
+    for t in (8, 2) + tuple(KTYPES):
+        q = dev.DeviceArray(rows * row_size(t, npr), np.uint8)
+        quantize_into(t, dsrc, npr, q, None if t in (8, 2) else dimx, 0, stream.handle)
+        check(lib().spa_dequantize(t, q.ptr, rows, npr, out.ptr, stream.handle))
+        e0, e1 = dev.Event(), dev.Event()
+        e0.record(stream.handle)
+        for _ in range(reps):
+            check(lib().spa_dequantize(t, q.ptr, rows, npr, out.ptr, stream.handle))
+        e1.record(stream.handle)
+        ms = e0.elapsed_ms(e1) / reps
+        nb = q.nbytes + out.nbytes
+        res[NAMES[t]] = {"ms": round(ms, 4), "GB_s_f32_out": round(out.nbytes / ms / 1e6, 1),
+                         "hbm_frac": round(nb / ms / 1e6 / PEAK_HBM_GBS, 4)}
+        del q
+    log(f"bench: dequant token_embd {res}")
+    return res
+
+
 def qr_cfg1(stream, reps=3):
     """configuration 1 residual coding: Q8_0 / Q4_0 of the 3072x1024 tensor as the prediction, the file
     is that with 1% of its blocks perturbed (one byte each); QR encode (histogram, tables, coding, gather)
@@ -453,6 +481,7 @@ def main():
             legacy[f"{NAMES[t]}_{name}"] = {"GB_s_bf16_in": round(2 * nw / (ms / 1e3) / 1e9, 1), "ms": round(ms, 4),
                                            "hbm_frac": round(alg_bytes(t, nw, shape[1], False) / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
 
+    dqb = dequant_cfg2(stream, dsrc["token_embd"], dimx["token_embd"])
     iq = iquant_cfg3(stream)
     qrb = qr_cfg1(stream)
     qrg = qr_cfg3(stream)
@@ -465,7 +494,7 @@ def main():
             "data": "synthetic (seeded N(0,0.02) BF16, LogNormal(0,1) imatrix)",
             "config": {"workload": "cfg2: Q2_K,Q3_K,Q4_K,Q5_K,Q6_K (imatrix) on token_embd 151936x1024 + ffn_down 1024x3072",
                        "bf16_bytes_per_step": bf16_bytes, "launches_per_step": len(launches)},
-            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "qr_cfg1": qrb, "qr_cfg3": qrg, "r2_base": r2b, "r2_cfg4": r2c,
+            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "dequant_token_embd": dqb, "qr_cfg1": qrb, "qr_cfg3": qrg, "r2_base": r2b, "r2_cfg4": r2c,
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
 

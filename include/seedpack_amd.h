@@ -83,6 +83,13 @@ int spa_type_variants(int ggml_type);
 int spa_quantize(int ggml_type, int variant, const void* src, int src_kind, int64_t nrows, int64_t n_per_row,
                  const float* imatrix, void* dst, void* stream);
 
+/* Dequantizes nrows x n_per_row weights of a quantized row-major run of blocks (src) into dst
+ * (nrows * n_per_row floats, 16-byte aligned), bit-identical to llama.cpp's
+ * dequantize_row_<type> (ggml-quants.c:439-568, :961-1968, :2489-2764) for the 20 types
+ * spa_quantize supports. Replaces the k_dq_<type> launches of GPUQuant.dequantize
+ * (gpuquant.py:214-219, :413-421). */
+int spa_dequantize(int ggml_type, const void* src, int64_t nrows, int64_t n_per_row, float* dst, void* stream);
+
 /* Host view of IQ lattice table `index` (0 IQ2_XXS, 1 IQ2_XS, 2 IQ1_S/IQ1_M, 3 IQ2_S, 4 IQ3_XXS,
  * 5 IQ3_S), built by the library on first use: the codebook as coordinate bytes (8 or 4 per point),
  * the level-index map and the neighbour lists, equal to what llama.cpp's iq2xs_init_impl /

@@ -3,7 +3,8 @@ compiled from /root/reference/seedpack/ggml by oracle/Makefile into oracle/_ref/
 
 quantize() follows the reference's CPU entry (seedpack/requant.py:115-134): rows split into
 contiguous chunks over a thread pool, each chunk one quantize_<type>(src, dst, nrow, n_per_row,
-imatrix) call; IQ tables are initialised first (requant.py:28-29, :48-56).
+imatrix) call; IQ tables are initialised first (requant.py:28-29, :48-56). dequantize() runs
+dequantize_row_<type> (ggml-quants.c:439-2764) over the whole run of blocks.
 """
 import ctypes
 import os
@@ -94,4 +95,17 @@ def quantize(ttype, x, imatrix=None, variant=0, threads=None):
     else:
         with ThreadPoolExecutor(threads) as ex:
             list(ex.map(run, range(0, nrows, chunk)))
+    return out
+
+
+def dequantize(ttype, blocks, n):
+    """quantized bytes (a run of blocks holding n weights) -> float32[n], via the reference C build"""
+    b = np.ascontiguousarray(np.frombuffer(bytes(blocks), np.uint8))
+    assert n % QK[ttype] == 0 and len(b) >= n // QK[ttype] * BS[ttype]
+    L = lib(0)
+    f = getattr(L, "de" + QFUN[ttype].replace("quantize_", "quantize_row_"))
+    f.restype = None
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+    out = np.empty(n, np.float32)
+    f(b.ctypes.data, out.ctypes.data, n)
     return out

@@ -92,6 +92,23 @@ class GPUQuant:
                 out.append(res)
         return None if on_result else out
 
+    def dequantize(self, ttype, y, npr, out=None):
+        """quantized bytes of a tensor (DeviceArray or host uint8, rows of npr weights) -> float32
+        DeviceArray (or into `out`), llama.cpp's dequantize_row_<type> (gpuquant.py:413-421)"""
+        if ttype not in QFUN:
+            raise ValueError(f"unknown ggml type {ttype}")
+        _, qk, bs = QFUN[ttype]
+        y = self._dev(y)
+        rb = npr // qk * bs
+        nrows = y.nbytes // rb
+        if npr % qk or nrows * rb != y.nbytes:
+            raise ValueError(f"{y.nbytes} bytes are not whole rows of {npr} weights of type {ttype}")
+        x = dev.DeviceArray(nrows * npr, np.float32) if out is None else out
+        if x.nbytes < nrows * npr * 4:
+            raise ValueError("output too small")
+        check(lib().spa_dequantize(ttype, y.ptr, nrows, npr, x.ptr, self.stream))
+        return x
+
     def quantize_batch(self, ttype, xs, imatrices, variant=0):
         """xs: list of float32 arrays (nrows, n_per_row); returns device uint8 arrays (gpuquant.py:424-430)"""
         return self.quantize_tensors(ttype, [(x, x.shape[-1]) for x in xs], imatrices, variant, device=True)
