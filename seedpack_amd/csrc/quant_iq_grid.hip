@@ -132,6 +132,55 @@ __device__ __forceinline__ void sums_2l1(const float (&xval)[N], const float (&w
     }
 }
 
+// A lattice group's levels are kept as its level index (B bits per coordinate: the map's key), one
+// register per group instead of one per weight; the search states of the 32-weight sub-blocks
+// otherwise do not fit the register file twice over.
+template <int D>
+struct LIdx {
+    static constexpr int B = D == 8 ? 2 : 3, M = (1 << B) - 1;
+    __device__ __forceinline__ static int level(int u, int i) { return (u >> (B * i)) & M; }
+};
+
+// the group at `off` rounded at inverse scale id: nearest_int(0.5 (id x - 1)) clamped to the levels
+template <int D, int N, int KMAXQ>
+__device__ __forceinline__ int round_group(const float (&xval)[N], int off, float id) {
+    int u = 0;
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        const int l = nearest_int(0.5f * (id * xval[off + i] - 1));
+        u |= tmax(0, tmin(KMAXQ - 1, l)) << (LIdx<D>::B * i);
+    }
+    return u;
+}
+
+// best_neighbour, returning the chosen point's level index
+template <int D, int N>
+__device__ __forceinline__ int best_neighbour_idx(const uint16_t* __restrict__ nb, const uint8_t* grid, const float (&xval)[N],
+                                                  const float (&w)[N], int off, float scale) {
+    int L[N];
+    best_neighbour<D, N>(nb, grid, xval, w, off, scale, L);
+    int u = 0;
+#pragma unroll
+    for (int i = 0; i < D; ++i) u |= L[off + i] << (LIdx<D>::B * i);
+    return u;
+}
+
+// sums_2l1 over groups held as level indices (element order)
+template <int D, int N>
+__device__ __forceinline__ void sums_idx(const float (&xval)[N], const float (&w)[N], const int (&idx)[N / D], float& sumqx,
+                                         float& sumq2) {
+    sumqx = 0; sumq2 = 0;
+#pragma unroll
+    for (int k = 0; k < N / D; ++k) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const float q = (float)(2 * LIdx<D>::level(idx[k], i) + 1);
+            sumqx += w[D * k + i] * xval[D * k + i] * q;
+            sumq2 += w[D * k + i] * q * q;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- the lattice types (IQ2_*, IQ3_*)
 
 // Result of one sub-block. An empty sub-block (its early exit in the reference) writes no bytes:
@@ -153,7 +202,7 @@ struct SubOut {
 template <int N, int D, int KMAXQ, int IS_LO, int IS_HI, bool ONGRID_INIT, bool REFIT_ALL, bool SET_L_IN_REFIT>
 __device__ __forceinline__ float lattice_search(const float (&xval)[N], const float (&w)[N], const float (&waux)[N],
                                                 float max, float step, const IqDeviceTable& tab, const uint8_t* grid,
-                                                int (&L)[N]) {
+                                                int (&idx)[N / D]) {
     constexpr int NG = N / D;
     bool on[NG];
 #pragma unroll
@@ -163,28 +212,22 @@ __device__ __forceinline__ float lattice_search(const float (&xval)[N], const fl
     for (int is = IS_LO; is <= IS_HI; ++is) {
         const float id = ((float)(2 * KMAXQ - 1) + (float)is * step) / max;
         const float this_scale = 1 / id;
-        int La[N];
+        int ia[NG];
         bool ona[NG];
 #pragma unroll
         for (int k = 0; k < NG; ++k) {
-#pragma unroll
-            for (int i = 0; i < D; ++i) {
-                const int l = nearest_int(0.5f * (id * xval[D * k + i] - 1));
-                La[D * k + i] = tmax(0, tmin(KMAXQ - 1, l));
-            }
-            const int gi = tab.map[level_index<D, N>(La, D * k)];
+            ia[k] = round_group<D, N, KMAXQ>(xval, D * k, id);
+            const int gi = tab.map[ia[k]];
             ona[k] = gi >= 0;
-            if (gi < 0) best_neighbour<D, N>(tab.nb - gi - 1, grid, xval, waux, D * k, this_scale, La);
+            if (gi < 0) ia[k] = best_neighbour_idx<D, N>(tab.nb - gi - 1, grid, xval, waux, D * k, this_scale);
         }
         float sumqx, sumq2;
-        sums_2l1<N>(xval, w, La, sumqx, sumq2);
+        sums_idx<D, N>(xval, w, ia, sumqx, sumq2);
         if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
             scale = sumqx / sumq2;
             best = scale * sumqx;
 #pragma unroll
-            for (int i = 0; i < N; ++i) L[i] = La[i];
-#pragma unroll
-            for (int k = 0; k < NG; ++k) on[k] = ona[k];
+            for (int k = 0; k < NG; ++k) { idx[k] = ia[k]; on[k] = ona[k]; }
         }
     }
     int n_off = 0;
@@ -195,23 +238,14 @@ __device__ __forceinline__ float lattice_search(const float (&xval)[N], const fl
 #pragma unroll
         for (int k = 0; k < NG; ++k) {
             if (!REFIT_ALL && on[k]) continue;
-            int lv[N];
-#pragma unroll
-            for (int i = 0; i < D; ++i) {
-                const int l = nearest_int(0.5f * (id * xval[D * k + i] - 1));
-                lv[D * k + i] = tmax(0, tmin(KMAXQ - 1, l));
-                if (SET_L_IN_REFIT) L[D * k + i] = lv[D * k + i];
-            }
-            const int gi = tab.map[level_index<D, N>(lv, D * k)];
-            if (gi < 0) {
-                best_neighbour<D, N>(tab.nb - gi - 1, grid, xval, waux, D * k, scale, L);
-            } else if (!SET_L_IN_REFIT) {
-#pragma unroll
-                for (int i = 0; i < D; ++i) L[D * k + i] = lv[D * k + i];
-            }
+            // the rounded levels, or the best neighbour's when off the grid (SET_L_IN_REFIT only
+            // changes when the levels are written, not their values)
+            const int u = round_group<D, N, KMAXQ>(xval, D * k, id);
+            const int gi = tab.map[u];
+            idx[k] = gi < 0 ? best_neighbour_idx<D, N>(tab.nb - gi - 1, grid, xval, waux, D * k, scale) : u;
         }
         float sumqx, sumq2;
-        sums_2l1<N>(xval, w, L, sumqx, sumq2);
+        sums_idx<D, N>(xval, w, idx, sumqx, sumq2);
         if (sumq2 > 0) scale = sumqx / sumq2;
     }
     return scale;
@@ -232,33 +266,33 @@ __device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float 
     for (int i = 1; i < 32; ++i) max = tmax(max, xval[i]);
     o.empty = true;
     if (max < GROUP_MAX_EPS) return o;
-    int L[32];
-    float scale = make_qp_quants<32>(KMAXQ + 1, xval, L, w);
+    float scale;
+    {
+        int Lq[32];     // make_qp_quants' levels never reach the output: scale > 0 below refits every group
+        scale = make_qp_quants<32>(KMAXQ + 1, xval, Lq, w);
+    }
     const float eff_max = scale * KMAXQ;
     if (eff_max <= 0) return o;
     o.empty = false;
     float best = 0;
+    int idx[4] = {0, 0, 0, 0};
     for (int is = -6; is <= 6; ++is) {
         const float id = ((float)(2 * KMAXQ - 1) + (float)is * 0.1f) / eff_max;
         const float this_scale = 1 / id;
-        int La[32];
+        int ia[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int l = nearest_int(0.5f * (id * xval[8 * k + i] - 1));
-                La[8 * k + i] = tmax(0, tmin(KMAXQ - 1, l));
-            }
-            const int gi = tab.map[level_index<8, 32>(La, 8 * k)];
-            if (gi < 0) best_neighbour<8, 32>(tab.nb - gi - 1, grid, xval, waux, 8 * k, this_scale, La);
+            ia[k] = round_group<8, 32, KMAXQ>(xval, 8 * k, id);
+            const int gi = tab.map[ia[k]];
+            if (gi < 0) ia[k] = best_neighbour_idx<8, 32>(tab.nb - gi - 1, grid, xval, waux, 8 * k, this_scale);
         }
         float sumqx, sumq2;
-        sums_2l1<32>(xval, w, La, sumqx, sumq2);
+        sums_idx<8, 32>(xval, w, ia, sumqx, sumq2);
         if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
             scale = sumqx / sumq2;
             best = scale * sumqx;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) L[i] = La[i];
+            for (int k = 0; k < 4; ++k) idx[k] = ia[k];
         }
     }
     if (scale > 0) {
@@ -266,22 +300,12 @@ __device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float 
         const float id = 1 / scale;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            int lv[32];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int l = nearest_int(0.5f * (id * xval[8 * k + i] - 1));
-                lv[8 * k + i] = tmax(0, tmin(KMAXQ - 1, l));
-            }
-            const int gi = tab.map[level_index<8, 32>(lv, 8 * k)];
-            if (gi < 0) {
-                best_neighbour<8, 32>(tab.nb - gi - 1, grid, xval, waux, 8 * k, scale, L);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) L[8 * k + i] = lv[8 * k + i];
-            }
+            const int u = round_group<8, 32, KMAXQ>(xval, 8 * k, id);
+            const int gi = tab.map[u];
+            idx[k] = gi < 0 ? best_neighbour_idx<8, 32>(tab.nb - gi - 1, grid, xval, waux, 8 * k, scale) : u;
         }
         float sumqx, sumq2;
-        sums_2l1<32>(xval, w, L, sumqx, sumq2);
+        sums_idx<8, 32>(xval, w, idx, sumqx, sumq2);
         if (sumq2 > 0) scale = sumqx / sumq2;
     }
     if (scale < 0) {
@@ -290,7 +314,7 @@ __device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float 
         for (int k = 0; k < 4; ++k) sg[k] = (~sg[k]) & 127;
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) { o.gidx[k] = tab.map[level_index<8, 32>(L, 8 * k)]; o.signs[k] = sg[k]; }
+    for (int k = 0; k < 4; ++k) { o.gidx[k] = tab.map[idx[k]]; o.signs[k] = sg[k]; }
     o.scale = scale;
     return o;
 }
@@ -312,17 +336,15 @@ __device__ __forceinline__ SubOut iq2_16_sub(const float (&x)[16], const float (
     o.empty = true;
     if (max < (XS ? GROUP_MAX_EPS : 1e-8f)) return o;   // GROUP_MAX_EPS_IQ2_S = 1e-8f
     o.empty = false;
-    int L[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) L[i] = 0;
-    float scale = lattice_search<16, 8, 3, -9, 9, true, false, true>(xval, w, waux, max, 0.1f, tab, grid, L);
+    int idx[2] = {0, 0};
+    float scale = lattice_search<16, 8, 3, -9, 9, true, false, true>(xval, w, waux, max, 0.1f, tab, grid, idx);
     if (scale < 0) {
         scale = -scale;
 #pragma unroll
         for (int k = 0; k < 2; ++k) sg[k] = XS ? ((~sg[k]) & 127) : ((~sg[k]) & 255);
     }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) { o.gidx[k] = tab.map[level_index<8, 16>(L, 8 * k)]; o.signs[k] = sg[k]; }
+    for (int k = 0; k < 2; ++k) { o.gidx[k] = tab.map[idx[k]]; o.signs[k] = sg[k]; }
     o.scale = scale;
     return o;
 }
@@ -344,19 +366,17 @@ __device__ __forceinline__ SubOut iq3_sub(const float (&x)[32], const float (&w)
     o.empty = true;
     if (XXS ? (max < 1e-8f) : (max == 0.f)) return o;   // GROUP_MAX_EPS_IQ3_XXS = 1e-8f; IQ3_S: !max
     o.empty = false;
-    int L[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) L[i] = 0;
+    int idx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float scale;
-    if constexpr (XXS) scale = lattice_search<32, 4, 8, -15, 15, true, false, false>(xval, w, waux, max, 0.2f, tab, grid, L);
-    else scale = lattice_search<32, 4, 8, -9, 9, false, true, false>(xval, w, waux, max, 0.2f, tab, grid, L);
+    if constexpr (XXS) scale = lattice_search<32, 4, 8, -15, 15, true, false, false>(xval, w, waux, max, 0.2f, tab, grid, idx);
+    else scale = lattice_search<32, 4, 8, -9, 9, false, true, false>(xval, w, waux, max, 0.2f, tab, grid, idx);
     if (scale < 0) {
         scale = -scale;
 #pragma unroll
         for (int k = 0; k < 4; ++k) sg[k] = XXS ? ((~sg[k]) & 127) : ((~sg[k]) & 255);
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) o.gidx[k] = tab.map[level_index<4, 32>(L, 4 * k)];
+    for (int k = 0; k < 8; ++k) o.gidx[k] = tab.map[idx[k]];
 #pragma unroll
     for (int k = 0; k < 4; ++k) o.signs[k] = sg[k];
     o.scale = scale;
