@@ -175,8 +175,12 @@ __device__ __forceinline__ void sums_idx(const float (&xval)[N], const float (&w
 #pragma unroll
         for (int i = 0; i < D; ++i) {
             const float q = (float)(2 * LIdx<D>::level(idx[k], i) + 1);
-            sumqx += w[D * k + i] * xval[D * k + i] * q;
-            sumq2 += w[D * k + i] * q * q;
+            // w passes an empty asm so that w*xval is not hoisted out of the trial loop (N live
+            // registers more, one wave less per SIMD)
+            float wi = w[D * k + i];
+            asm volatile("" : "+v"(wi));
+            sumqx += wi * xval[D * k + i] * q;
+            sumq2 += wi * q * q;
         }
     }
 }
@@ -500,8 +504,9 @@ __device__ __forceinline__ float iq1_snap(const float (&x)[N], const float (&w)[
 }
 
 // IQ1_S sub-block of 32 -- quantize_row_iq1_s_impl (ggml-quants.c:4509-4671)
+template <class R>
 __device__ __forceinline__ SubOut iq1_s_sub(const float (&x)[32], const float (&w)[32], const IqDeviceTable& tab,
-                                            const uint8_t* grid) {
+                                            const uint8_t* grid, const R& reload) {
     constexpr float XP0 = -1 + IQ1S_DELTA, XP1 = IQ1S_DELTA, XP2 = 1 + IQ1S_DELTA;
     constexpr float XM0 = -1 - IQ1S_DELTA, XM1 = -IQ1S_DELTA, XM2 = 1 - IQ1S_DELTA;
     SubOut o{};
@@ -525,6 +530,13 @@ __device__ __forceinline__ SubOut iq1_s_sub(const float (&x)[32], const float (&
     // every split i1 <= i2 in the reference's order; i1 is the same in every lane, so the prefix
     // sums at i1 are picked once per i1 and the inner loop indexes registers by constants
     for (int i1 = 0; i1 <= 32; ++i1) {
+        // the prefix sums pass through an empty asm each step: otherwise the i1-invariant products of
+        // the unrolled i2 loop are hoisted out as ~130 extra live registers (half the occupancy)
+#pragma unroll
+        for (int t = 0; t <= 32; ++t) {
+            asm volatile("" : "+v"(sumx[t]));
+            asm volatile("" : "+v"(sumw[t]));
+        }
         float x1 = 0, w1 = 0;
 #pragma unroll
         for (int t = 0; t <= 32; ++t)
@@ -546,8 +558,10 @@ __device__ __forceinline__ SubOut iq1_s_sub(const float (&x)[32], const float (&
     }
     if (b1 < 0 || b2 < 0 || best_shift == 0) return o;
     o.empty = false;
+    float xr[32], wr[32];
+    reload(xr, wr);
     int L[32];
-    split_levels<32>(x, b1, b2, L);
+    split_levels<32>(xr, b1, b2, L);
     if (scale < 0) {
 #pragma unroll
         for (int j = 0; j < 32; ++j) L[j] = 2 - L[j];
@@ -556,16 +570,16 @@ __device__ __forceinline__ SubOut iq1_s_sub(const float (&x)[32], const float (&
     }
     const bool p = best_shift == 1;
     const bool pos[4] = {p, p, p, p};
-    o.scale = iq1_snap<32>(x, w, L, scale, pos, tab, grid, o.gidx);
+    o.scale = iq1_snap<32>(xr, wr, L, scale, pos, tab, grid, o.gidx);
     o.shift = best_shift;
     return o;
 }
 
 // IQ1_M sub-block of 16 -- quantize_row_iq1_m_impl (ggml-quants.c:4693-4916); VARIANT 1 is the
 // earlier search that sums every split directly (variants/ggml-quants.pre-f95b0d9539.c:4773-4860)
-template <int VARIANT>
+template <int VARIANT, class R>
 __device__ __forceinline__ SubOut iq1_m_sub(const float (&x)[16], const float (&w)[16], const IqDeviceTable& tab,
-                                            const uint8_t* grid) {
+                                            const uint8_t* grid, const R& reload) {
     constexpr float XP0 = -1 + IQ1M_DELTA, XP1 = IQ1M_DELTA, XP2 = 1 + IQ1M_DELTA;
     constexpr float XM0 = -1 - IQ1M_DELTA, XM1 = -IQ1M_DELTA, XM2 = 1 - IQ1M_DELTA;
     SubOut o{};
@@ -601,6 +615,14 @@ __device__ __forceinline__ SubOut iq1_m_sub(const float (&x)[16], const float (&
         const float cp1 = XP0 * XP0 - XP1 * XP1, cp2 = XP1 * XP1 - XP2 * XP2;
         const float cm1 = XM0 * XM0 - XM1 * XM1, cm2 = XM1 * XM1 - XM2 * XM2;
         for (int i1 = 0; i1 <= 16; ++i1) {
+            // (as in the IQ1_S search: no hoisting of the i1-invariant terms)
+#pragma unroll
+            for (int t = 0; t <= 16; ++t) {
+                asm volatile("" : "+v"(px0[t]));
+                asm volatile("" : "+v"(px1[t]));
+                asm volatile("" : "+v"(pw0[t]));
+                asm volatile("" : "+v"(pw1[t]));
+            }
             float a0 = 0, a1 = 0, c0 = 0, c1 = 0;
 #pragma unroll
             for (int t = 0; t <= 16; ++t)
@@ -659,8 +681,10 @@ __device__ __forceinline__ SubOut iq1_m_sub(const float (&x)[16], const float (&
     }
     if (b1 < 0 || b2 < 0 || best_k < 0) return o;
     o.empty = false;
+    float xr[16], wr[16];
+    reload(xr, wr);
     int L[16];
-    split_levels<16>(x, b1, b2, L);
+    split_levels<16>(xr, b1, b2, L);
     if (scale < 0) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) L[j] = 2 - L[j];
@@ -668,7 +692,7 @@ __device__ __forceinline__ SubOut iq1_m_sub(const float (&x)[16], const float (&
         best_k = 3 - best_k;
     }
     const bool pos[2] = {best_k < 2, best_k % 2 == 0};
-    o.scale = iq1_snap<16>(x, w, L, scale, pos, tab, grid, o.gidx);
+    o.scale = iq1_snap<16>(xr, wr, L, scale, pos, tab, grid, o.gidx);
     o.shift = best_k;
     return o;
 }
@@ -722,23 +746,32 @@ __global__ __launch_bounds__(WG) void k_iqgrid(const void* __restrict__ src, int
     for (int i = 0; i < N; ++i) sq[i] = x[i] * x[i];
     const float sumx2 = group_sum<G, N>(sq, sub);
     const float sigma2 = C::TWO ? 2 * sumx2 / 256 : sumx2 / 256;
+    auto weights = [&](const float (&xv)[N], float (&wv)[N]) {
+        if (imx) {
+            const float* qw = imx + (sbc % sbpr) * 256 + sub * N;
+#pragma unroll
+            for (int i = 0; i < N; ++i) wv[i] = qw[i] * sqrtf(sigma2 + xv[i] * xv[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < N; ++i) wv[i] = K == K_IQ2_S ? 0.25f * sigma2 + xv[i] * xv[i] : xv[i] * xv[i];
+        }
+    };
+    // the IQ1 searches hold sorted copies and prefix sums: x and w are read again afterwards (same
+    // values) rather than kept in registers through them
+    auto reload = [&](float (&xv)[N], float (&wv)[N]) {
+        load_weights<N>(src, kind, sbc * 256 + sub * N, xv);
+        weights(xv, wv);
+    };
     float w[N];
-    if (imx) {
-        const float* qw = imx + (sbc % sbpr) * 256 + sub * N;
-#pragma unroll
-        for (int i = 0; i < N; ++i) w[i] = qw[i] * sqrtf(sigma2 + x[i] * x[i]);
-    } else {
-#pragma unroll
-        for (int i = 0; i < N; ++i) w[i] = K == K_IQ2_S ? 0.25f * sigma2 + x[i] * x[i] : x[i] * x[i];
-    }
+    weights(x, w);
     SubOut r;
     if constexpr (K == K_IQ2_XXS) r = iq2_xxs_sub(x, w, tab, grid);
     else if constexpr (K == K_IQ2_XS) r = iq2_16_sub<true>(x, w, tab, grid);
     else if constexpr (K == K_IQ2_S) r = iq2_16_sub<false>(x, w, tab, grid);
     else if constexpr (K == K_IQ3_XXS) r = iq3_sub<true>(x, w, tab, grid);
     else if constexpr (K == K_IQ3_S) r = iq3_sub<false>(x, w, tab, grid);
-    else if constexpr (K == K_IQ1_S) r = iq1_s_sub(x, w, tab, grid);
-    else r = iq1_m_sub<K == K_IQ1_M1 ? 1 : 0>(x, w, tab, grid);
+    else if constexpr (K == K_IQ1_S) r = iq1_s_sub(x, w, tab, grid, reload);
+    else r = iq1_m_sub<K == K_IQ1_M1 ? 1 : 0>(x, w, tab, grid, reload);
     // super-block scale: MAX over the sub-block scales in sub-block order (empty ones count as 0)
     const float s_own = r.empty ? 0.f : r.scale;
     float max_scale = 0;
@@ -759,6 +792,8 @@ __global__ __launch_bounds__(WG) void k_iqgrid(const void* __restrict__ src, int
         // point 0 with signs (+, +) (ggml-quants.c:4884-4910)
         constexpr float XP0 = -1 + IQ1M_DELTA, XP1 = IQ1M_DELTA, XP2 = 1 + IQ1M_DELTA;
         constexpr float XM0 = -1 - IQ1M_DELTA, XM1 = -IQ1M_DELTA, XM2 = 1 - IQ1M_DELTA;
+        float xr[N], wr[N];
+        reload(xr, wr);
         float aqx[16], aq2[16];
         const int shift = r.empty ? 0 : r.shift;
 #pragma unroll
@@ -770,8 +805,8 @@ __global__ __launch_bounds__(WG) void k_iqgrid(const void* __restrict__ src, int
             for (int j = 0; j < 8; ++j) {
                 const int lv = (q[j] - 1) / 2;
                 const float qq = (p ? pick3(lv, XP0, XP1, XP2) : pick3(lv, XM0, XM1, XM2)) * (float)(2 * l + 1);
-                aqx[8 * k + j] = w[8 * k + j] * qq * x[8 * k + j];
-                aq2[8 * k + j] = w[8 * k + j] * qq * qq;
+                aqx[8 * k + j] = wr[8 * k + j] * qq * xr[8 * k + j];
+                aq2[8 * k + j] = wr[8 * k + j] * qq * qq;
             }
         }
         float sqx = 0.f, sq2 = 0.f;
