@@ -713,17 +713,22 @@ enum Kind { K_IQ2_XXS, K_IQ2_XS, K_IQ2_S, K_IQ3_XXS, K_IQ3_S, K_IQ1_S, K_IQ1_M0,
 
 // N: sub-block; BS: block bytes; GBYTES: codebook bytes; TWO: sigma2 = 2 sumx2 / 256 (else sumx2 / 256)
 template <int K> struct Cfg;
-template <> struct Cfg<K_IQ2_XXS> { static constexpr int N = 32, BS = 66, GBYTES = 256 * 8; static constexpr bool TWO = false; };
-template <> struct Cfg<K_IQ2_XS> { static constexpr int N = 16, BS = 74, GBYTES = 512 * 8; static constexpr bool TWO = false; };
-template <> struct Cfg<K_IQ2_S> { static constexpr int N = 16, BS = 82, GBYTES = 1024 * 8; static constexpr bool TWO = true; };
-template <> struct Cfg<K_IQ3_XXS> { static constexpr int N = 32, BS = 98, GBYTES = 256 * 4; static constexpr bool TWO = true; };
-template <> struct Cfg<K_IQ3_S> { static constexpr int N = 32, BS = 110, GBYTES = 512 * 4; static constexpr bool TWO = true; };
-template <> struct Cfg<K_IQ1_S> { static constexpr int N = 32, BS = 50, GBYTES = 2048 * 8; static constexpr bool TWO = true; };
-template <> struct Cfg<K_IQ1_M0> { static constexpr int N = 16, BS = 56, GBYTES = 2048 * 8; static constexpr bool TWO = true; };
-template <> struct Cfg<K_IQ1_M1> { static constexpr int N = 16, BS = 56, GBYTES = 2048 * 8; static constexpr bool TWO = true; };
+// WPE: the waves per SIMD the register allocation is held to. The 32-weight lattice searches need
+// ~200 registers; at 3 waves (168) a few spill, which costs less than the lost latency hiding at 2
+// (measured: IQ3_XXS 7.6 -> 9.4 GB/s, IQ2_XXS 8.5 -> 10.9); 4 spills them by the thousand. The
+// 16-weight and IQ1_S searches fit 128 with few spills (IQ1_S 21.5 -> 23.8 at 4); IQ1_M keeps 3
+// (23.1 at 4, 24.0 at 3).
+template <> struct Cfg<K_IQ2_XXS> { static constexpr int N = 32, BS = 66, GBYTES = 256 * 8, WPE = 3; static constexpr bool TWO = false; };
+template <> struct Cfg<K_IQ2_XS> { static constexpr int N = 16, BS = 74, GBYTES = 512 * 8, WPE = 4; static constexpr bool TWO = false; };
+template <> struct Cfg<K_IQ2_S> { static constexpr int N = 16, BS = 82, GBYTES = 1024 * 8, WPE = 4; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ3_XXS> { static constexpr int N = 32, BS = 98, GBYTES = 256 * 4, WPE = 3; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ3_S> { static constexpr int N = 32, BS = 110, GBYTES = 512 * 4, WPE = 3; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ1_S> { static constexpr int N = 32, BS = 50, GBYTES = 2048 * 8, WPE = 4; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ1_M0> { static constexpr int N = 16, BS = 56, GBYTES = 2048 * 8, WPE = 3; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ1_M1> { static constexpr int N = 16, BS = 56, GBYTES = 2048 * 8, WPE = 3; static constexpr bool TWO = true; };
 
 template <int K>
-__global__ __launch_bounds__(WG) void k_iqgrid(const void* __restrict__ src, int kind, uint8_t* __restrict__ dst, int64_t nsb,
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE))) void k_iqgrid(const void* __restrict__ src, int kind, uint8_t* __restrict__ dst, int64_t nsb,
                                                int64_t sbpr, const float* __restrict__ imx, IqDeviceTable tab) {
     using C = Cfg<K>;
     constexpr int N = C::N, G = 256 / N, SBW = WG / G;
