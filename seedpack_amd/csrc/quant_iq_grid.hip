@@ -38,6 +38,12 @@ __device__ __forceinline__ float group_sum(const float (&v)[N], int sub) {
     return s;
 }
 
+template <int D>
+struct LIdx {
+    static constexpr int B = D == 8 ? 2 : 3, M = (1 << B) - 1;
+    __device__ __forceinline__ static int level(int u, int i) { return (u >> (B * i)) & M; }
+};
+
 // grid point j's coordinate values (2l+1) from the LDS codebook
 template <int D>
 __device__ __forceinline__ void grid_point(const uint8_t* grid, int j, int (&q)[D]) {
@@ -52,12 +58,24 @@ __device__ __forceinline__ void grid_point(const uint8_t* grid, int j, int (&q)[
     }
 }
 
+// One lane's array of floats kept in LDS, element i at word i*WG of the lane's column: the lanes of a
+// wave touch consecutive words (no bank conflicts), and the values take no registers.
+struct LdsCol {
+    float* p;
+    __device__ __forceinline__ float operator[](int i) const { return p[i * WG]; }
+    __device__ __forceinline__ void set(int i, float v) const { p[i * WG] = v; }
+};
+
 // iq2_find_best_neighbour / iq3_find_best_neighbour (ggml-quants.c:3271-3293, :3915-3937): among the
-// listed neighbours, the first with the smallest weighted squared error at `scale`; its levels go to
-// L[off..off+D). The list always holds at least one point.
+// listed neighbours, the first with the smallest weighted squared error at `scale` (weights: the
+// group's sqrt(w), from LDS); returns that point's level index. The list always holds at least one
+// point.
 template <int D, int N>
-__device__ __forceinline__ int best_neighbour(const uint16_t* __restrict__ nb, const uint8_t* grid, const float (&xval)[N],
-                                              const float (&w)[N], int off, float scale, int (&L)[N]) {
+__device__ __forceinline__ int best_neighbour_idx(const uint16_t* __restrict__ nb, const uint8_t* grid, const float (&xval)[N],
+                                                  LdsCol wa, int off, float scale) {
+    float wv[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) wv[i] = wa[off + i];
     const int n = nb[0];
     float best_d2 = FLT_BIG;
     int gi = nb[1];
@@ -69,15 +87,16 @@ __device__ __forceinline__ int best_neighbour(const uint16_t* __restrict__ nb, c
 #pragma unroll
         for (int i = 0; i < D; ++i) {
             const float diff = scale * (float)q[i] - xval[off + i];
-            d2 += w[off + i] * diff * diff;
+            d2 += wv[i] * diff * diff;
         }
         if (d2 < best_d2) { best_d2 = d2; gi = j; }
     }
     int q[D];
     grid_point<D>(grid, gi, q);
+    int u = 0;
 #pragma unroll
-    for (int i = 0; i < D; ++i) L[off + i] = (q[i] - 1) / 2;
-    return gi;
+    for (int i = 0; i < D; ++i) u |= ((q[i] - 1) / 2) << (LIdx<D>::B * i);
+    return u;
 }
 
 // |x| per group of 8 and the sign bits; with PARITY (IQ2_XXS, IQ2_XS, IQ3_XXS) an odd count of
@@ -135,12 +154,6 @@ __device__ __forceinline__ void sums_2l1(const float (&xval)[N], const float (&w
 // A lattice group's levels are kept as its level index (B bits per coordinate: the map's key), one
 // register per group instead of one per weight; the search states of the 32-weight sub-blocks
 // otherwise do not fit the register file twice over.
-template <int D>
-struct LIdx {
-    static constexpr int B = D == 8 ? 2 : 3, M = (1 << B) - 1;
-    __device__ __forceinline__ static int level(int u, int i) { return (u >> (B * i)) & M; }
-};
-
 // the group at `off` rounded at inverse scale id: nearest_int(0.5 (id x - 1)) clamped to the levels
 template <int D, int N, int KMAXQ>
 __device__ __forceinline__ int round_group(const float (&xval)[N], int off, float id) {
@@ -150,18 +163,6 @@ __device__ __forceinline__ int round_group(const float (&xval)[N], int off, floa
         const int l = nearest_int(0.5f * (id * xval[off + i] - 1));
         u |= tmax(0, tmin(KMAXQ - 1, l)) << (LIdx<D>::B * i);
     }
-    return u;
-}
-
-// best_neighbour, returning the chosen point's level index
-template <int D, int N>
-__device__ __forceinline__ int best_neighbour_idx(const uint16_t* __restrict__ nb, const uint8_t* grid, const float (&xval)[N],
-                                                  const float (&w)[N], int off, float scale) {
-    int L[N];
-    best_neighbour<D, N>(nb, grid, xval, w, off, scale, L);
-    int u = 0;
-#pragma unroll
-    for (int i = 0; i < D; ++i) u |= L[off + i] << (LIdx<D>::B * i);
     return u;
 }
 
@@ -204,7 +205,7 @@ struct SubOut {
 // SET_L_IN_REFIT: the refit writes the rounded levels before the map lookup (IQ2_XS, IQ2_S);
 // otherwise the levels come from the grid point (IQ3_*): the same values either way.
 template <int N, int D, int KMAXQ, int IS_LO, int IS_HI, bool ONGRID_INIT, bool REFIT_ALL, bool SET_L_IN_REFIT>
-__device__ __forceinline__ float lattice_search(const float (&xval)[N], const float (&w)[N], const float (&waux)[N],
+__device__ __forceinline__ float lattice_search(const float (&xval)[N], const float (&w)[N], LdsCol waux,
                                                 float max, float step, const IqDeviceTable& tab, const uint8_t* grid,
                                                 int (&idx)[N / D]) {
     constexpr int NG = N / D;
@@ -257,12 +258,12 @@ __device__ __forceinline__ float lattice_search(const float (&xval)[N], const fl
 
 // IQ2_XXS -- quantize_row_iq2_xxs_impl (ggml-quants.c:3295-3471): 32-weight sub-blocks, 4 groups of 8
 __device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float (&w)[32], const IqDeviceTable& tab,
-                                              const uint8_t* grid) {
+                                              const uint8_t* grid, LdsCol waux) {
     constexpr int KMAXQ = 3;
     SubOut o{};
-    float waux[32], xval[32];
+    float xval[32];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) waux[i] = sqrtf(w[i]);
+    for (int i = 0; i < 32; ++i) waux.set(i, sqrtf(w[i]));
     uint32_t sg[4];
     make_signs<32, true>(x, w, xval, sg);
     float max = xval[0];
@@ -327,11 +328,11 @@ __device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float 
 // (:5114-5280): 16-weight sub-blocks, 2 lattice groups of 8
 template <bool XS>
 __device__ __forceinline__ SubOut iq2_16_sub(const float (&x)[16], const float (&w)[16], const IqDeviceTable& tab,
-                                             const uint8_t* grid) {
+                                             const uint8_t* grid, LdsCol waux) {
     SubOut o{};
-    float waux[16], xval[16];
+    float xval[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) waux[i] = sqrtf(w[i]);
+    for (int i = 0; i < 16; ++i) waux.set(i, sqrtf(w[i]));
     uint32_t sg[2];
     make_signs<16, XS>(x, w, xval, sg);
     float max = xval[0];
@@ -357,11 +358,11 @@ __device__ __forceinline__ SubOut iq2_16_sub(const float (&x)[16], const float (
 // (:4170-4353): 32-weight sub-blocks, 8 lattice groups of 4
 template <bool XXS>
 __device__ __forceinline__ SubOut iq3_sub(const float (&x)[32], const float (&w)[32], const IqDeviceTable& tab,
-                                          const uint8_t* grid) {
+                                          const uint8_t* grid, LdsCol waux) {
     SubOut o{};
-    float waux[32], xval[32];
+    float xval[32];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) waux[i] = sqrtf(w[i]);
+    for (int i = 0; i < 32; ++i) waux.set(i, sqrtf(w[i]));
     uint32_t sg[4];
     make_signs<32, XXS>(x, w, xval, sg);
     float max = xval[0];
@@ -735,7 +736,12 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
     constexpr bool IQ1 = K == K_IQ1_S || K == K_IQ1_M0 || K == K_IQ1_M1;
     __shared__ __align__(16) uint8_t grid[C::GBYTES];
     __shared__ __align__(16) uint16_t otile[SBW * C::BS / 2];
-    __shared__ Park park[SBW][G];
+    // sqrt(w) of the lattice types' neighbour searches in per-lane LDS columns (LdsCol); once the
+    // searches are done the same bytes hold the parked per-lane results
+    constexpr int WA_BYTES = IQ1 ? 0 : N * WG * 4, PARK_BYTES = SBW * G * (int)sizeof(Park);
+    __shared__ __align__(16) uint8_t wa_park[WA_BYTES > PARK_BYTES ? WA_BYTES : PARK_BYTES];
+    Park (*park)[G] = reinterpret_cast<Park (*)[G]>(wa_park);
+    const LdsCol waux{reinterpret_cast<float*>(wa_park) + threadIdx.x};
     for (int i = threadIdx.x; i < C::GBYTES / 16; i += WG)
         reinterpret_cast<uint4*>(grid)[i] = reinterpret_cast<const uint4*>(tab.grid)[i];
     __syncthreads();
@@ -770,11 +776,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
     float w[N];
     weights(x, w);
     SubOut r;
-    if constexpr (K == K_IQ2_XXS) r = iq2_xxs_sub(x, w, tab, grid);
-    else if constexpr (K == K_IQ2_XS) r = iq2_16_sub<true>(x, w, tab, grid);
-    else if constexpr (K == K_IQ2_S) r = iq2_16_sub<false>(x, w, tab, grid);
-    else if constexpr (K == K_IQ3_XXS) r = iq3_sub<true>(x, w, tab, grid);
-    else if constexpr (K == K_IQ3_S) r = iq3_sub<false>(x, w, tab, grid);
+    if constexpr (K == K_IQ2_XXS) r = iq2_xxs_sub(x, w, tab, grid, waux);
+    else if constexpr (K == K_IQ2_XS) r = iq2_16_sub<true>(x, w, tab, grid, waux);
+    else if constexpr (K == K_IQ2_S) r = iq2_16_sub<false>(x, w, tab, grid, waux);
+    else if constexpr (K == K_IQ3_XXS) r = iq3_sub<true>(x, w, tab, grid, waux);
+    else if constexpr (K == K_IQ3_S) r = iq3_sub<false>(x, w, tab, grid, waux);
     else if constexpr (K == K_IQ1_S) r = iq1_s_sub(x, w, tab, grid, reload);
     else r = iq1_m_sub<K == K_IQ1_M1 ? 1 : 0>(x, w, tab, grid, reload);
     // super-block scale: MAX over the sub-block scales in sub-block order (empty ones count as 0)
@@ -835,6 +841,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
     for (int k = 0; k < 8; ++k) pk.gidx[k] = r.empty ? 0 : r.gidx[k];
 #pragma unroll
     for (int k = 0; k < 4; ++k) pk.signs[k] = r.empty ? 0u : r.signs[k];
+    if constexpr (!IQ1) __syncthreads();   // every lane's search has read its sqrt(w) column
     park[lsb][sub] = pk;
     __syncthreads();
     if (active && sub == 0) {
