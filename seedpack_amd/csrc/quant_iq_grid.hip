@@ -58,44 +58,126 @@ __device__ __forceinline__ void grid_point(const uint8_t* grid, int j, int (&q)[
     }
 }
 
-// One lane's array of floats kept in LDS, element i at word i*WG of the lane's column: the lanes of a
-// wave touch consecutive words (no bank conflicts), and the values take no registers.
-struct LdsCol {
-    float* p;
-    __device__ __forceinline__ float operator[](int i) const { return p[i * WG]; }
-    __device__ __forceinline__ void set(int i, float v) const { p[i * WG] = v; }
+// ------------------------------------------------------- wave-balanced neighbour search
+//
+// A lattice group off the grid is snapped to the best point of its neighbour list
+// (iq2_find_best_neighbour / iq3_find_best_neighbour, ggml-quants.c:3271-3293, :3915-3937): among the
+// listed points, the first with the smallest weighted squared error sum_i sqrt(w_i) (s q_i - x_i)^2
+// at the trial scale s. The lists hold 1 to ~300 points; one lane per list would leave the wave
+// waiting for its longest list (3-4x the useful work on the configuration-3 tensors). Instead, for
+// one group index k at a time, the lists of all the wave's off-grid groups are cut into pieces of
+// NB_R consecutive entries and the pieces are dealt to the 64 lanes in rounds, so every lane evaluates
+// NB_R entries per round. A piece's owner (its group's |x|, scale, list) is read from the owner's LDS
+// record and its sqrt(w) from the owner's LDS row. Each list's winner is kept in an LDS slot as the
+// 64-bit key (d2 bits, position, point) lowered by atomic min: d2 >= +0 orders as its bit pattern, so
+// the least key is the smallest d2 at the smallest position -- the reference's first strict minimum.
+// Entries are kept only when d2 < FLT_MAX (the reference's initial best); a list with none keeps its
+// first point (the reference asserts there instead).
+constexpr int NB_R = 4;   // list entries per piece
+
+template <int D>
+struct NbWave {
+    __align__(16) float rec[64][D + 4];   // per owner lane: |x| of the group, scale, list offset, first piece, length
+    unsigned long long slot[64];          // per owner lane: least key so far
+    unsigned long long starts;            // pieces of the current round that begin a list (bit per lane)
+    int tl[64];                           // owner lanes in piece order
 };
 
-// iq2_find_best_neighbour / iq3_find_best_neighbour (ggml-quants.c:3271-3293, :3915-3937): among the
-// listed neighbours, the first with the smallest weighted squared error at `scale` (weights: the
-// group's sqrt(w), from LDS); returns that point's level index. The list always holds at least one
-// point.
+struct NbCtx {
+    void* w;               // this wave's NbWave
+    const float* wrows;    // per-lane rows of sqrt(w) (N floats each), the workgroup's
+    int wbase;             // the wave's first thread in the workgroup
+};
+
+// LDS writes of the wave's lanes complete before its later LDS reads, and no compiler reordering
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// The level index of the best neighbour of group k for the lanes with `off` set (gi: the map's
+// negative entry for the group's rounded point); called by all lanes of the wave together.
 template <int D, int N>
-__device__ __forceinline__ int best_neighbour_idx(const uint16_t* __restrict__ nb, const uint8_t* grid, const float (&xval)[N],
-                                                  LdsCol wa, int off, float scale) {
-    float wv[D];
+__device__ int wave_best_neighbour(const NbCtx& c, int k, bool off, int gi, const float (&xval)[N], float scale,
+                                   const uint16_t* __restrict__ nbt, const uint8_t* grid) {
+    NbWave<D>& W = *reinterpret_cast<NbWave<D>*>(c.w);
+    constexpr unsigned long long INIT = (unsigned long long)0x7f7fffffu << 32;   // (FLT_MAX, position 0)
+    const int lane = (int)__lane_id();
+    const int ptr = off ? -gi - 1 : 0;
+    const int len = off ? (int)nbt[ptr] : 0;
+    const int np = (len + NB_R - 1) / NB_R;
+    int incl = np;
 #pragma unroll
-    for (int i = 0; i < D; ++i) wv[i] = wa[off + i];
-    const int n = nb[0];
-    float best_d2 = FLT_BIG;
-    int gi = nb[1];
-    for (int jj = 1; jj <= n; ++jj) {
-        const int j = nb[jj];
-        int q[D];
-        grid_point<D>(grid, j, q);
-        float d2 = 0;
-#pragma unroll
-        for (int i = 0; i < D; ++i) {
-            const float diff = scale * (float)q[i] - xval[off + i];
-            d2 += wv[i] * diff * diff;
-        }
-        if (d2 < best_d2) { best_d2 = d2; gi = j; }
+    for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(incl, d);
+        if (lane >= d) incl += t;
     }
-    int q[D];
-    grid_point<D>(grid, gi, q);
-    int u = 0;
+    const int first = incl - np, total = __shfl(incl, 63);
+    const unsigned long long owners = __ballot(np > 0);
+    if (np > 0) {
+        float4* r = reinterpret_cast<float4*>(W.rec[lane]);
 #pragma unroll
-    for (int i = 0; i < D; ++i) u |= ((q[i] - 1) / 2) << (LIdx<D>::B * i);
+        for (int v = 0; v < D / 4; ++v)
+            r[v] = make_float4(xval[D * k + 4 * v], xval[D * k + 4 * v + 1], xval[D * k + 4 * v + 2], xval[D * k + 4 * v + 3]);
+        r[D / 4] = make_float4(scale, __int_as_float(ptr), __int_as_float(first), __int_as_float(len));
+        W.slot[lane] = INIT;
+        W.tl[__popcll(owners & ((1ull << lane) - 1))] = lane;
+    }
+    int carry = -1;   // piece-order index of the list holding the piece before this round's first
+    for (int base = 0; base < total; base += 64) {
+        if (lane == 0) W.starts = 0;
+        wave_lds_sync();
+        if (np > 0 && first >= base && first < base + 64) atomicOr(&W.starts, 1ull << (first - base));
+        wave_lds_sync();
+        const unsigned long long m = W.starts;
+        const unsigned long long upto = lane == 63 ? ~0ull : (2ull << lane) - 1;
+        const int seq = carry + __popcll(m & upto);
+        carry += __popcll(m);
+        const int q = base + lane;
+        if (q < total) {
+            const int o = W.tl[seq];
+            const float4* r = reinterpret_cast<const float4*>(W.rec[o]);
+            const float4* wr = reinterpret_cast<const float4*>(c.wrows + (c.wbase + o) * N + D * k);
+            float xg[D], wv[D];
+#pragma unroll
+            for (int v = 0; v < D / 4; ++v) {
+                const float4 a = r[v], b = wr[v];
+                xg[4 * v] = a.x; xg[4 * v + 1] = a.y; xg[4 * v + 2] = a.z; xg[4 * v + 3] = a.w;
+                wv[4 * v] = b.x; wv[4 * v + 1] = b.y; wv[4 * v + 2] = b.z; wv[4 * v + 3] = b.w;
+            }
+            const float4 meta = r[D / 4];
+            const float s = meta.x;
+            const int p = __float_as_int(meta.y), L = __float_as_int(meta.w);
+            const int pos0 = (q - __float_as_int(meta.z)) * NB_R;
+            float best = FLT_BIG;
+            uint32_t bj = 0;
+#pragma unroll
+            for (int e = 0; e < NB_R; ++e) {
+                const int pos = pos0 + e;
+                if (pos < L) {
+                    const int j = nbt[p + 1 + pos];
+                    int qg[D];
+                    grid_point<D>(grid, j, qg);
+                    float d2 = 0;
+#pragma unroll
+                    for (int i = 0; i < D; ++i) {
+                        const float diff = s * (float)qg[i] - xg[i];
+                        d2 += wv[i] * diff * diff;
+                    }
+                    if (d2 < best) { best = d2; bj = ((uint32_t)pos << 16) | (uint32_t)j; }
+                }
+            }
+            if (best < FLT_BIG) atomicMin(&W.slot[o], ((unsigned long long)__float_as_uint(best) << 32) | bj);
+        }
+        wave_lds_sync();
+    }
+    int u = 0;
+    if (np > 0) {
+        const unsigned long long key = W.slot[lane];
+        const int j = key == INIT ? (int)nbt[ptr + 1] : (int)(key & 0xffffu);
+        int qg[D];
+        grid_point<D>(grid, j, qg);
+#pragma unroll
+        for (int i = 0; i < D; ++i) u |= ((qg[i] - 1) / 2) << (LIdx<D>::B * i);
+    }
+    wave_lds_sync();
     return u;
 }
 
@@ -204,8 +286,10 @@ struct SubOut {
 // best scale and the scale refitted (ggml-quants.c:3540-3616, :5176-5252, :4014-4086, :4250-4322).
 // SET_L_IN_REFIT: the refit writes the rounded levels before the map lookup (IQ2_XS, IQ2_S);
 // otherwise the levels come from the grid point (IQ3_*): the same values either way.
+// All lanes of the wave run it (the neighbour searches are wave-wide); a lane whose sub-block is
+// empty (`live` false) searches nothing and its result is not used.
 template <int N, int D, int KMAXQ, int IS_LO, int IS_HI, bool ONGRID_INIT, bool REFIT_ALL, bool SET_L_IN_REFIT>
-__device__ __forceinline__ float lattice_search(const float (&xval)[N], const float (&w)[N], LdsCol waux,
+__device__ __forceinline__ float lattice_search(bool live, const float (&xval)[N], const float (&w)[N], const NbCtx& nc,
                                                 float max, float step, const IqDeviceTable& tab, const uint8_t* grid,
                                                 int (&idx)[N / D]) {
     constexpr int NG = N / D;
@@ -221,10 +305,11 @@ __device__ __forceinline__ float lattice_search(const float (&xval)[N], const fl
         bool ona[NG];
 #pragma unroll
         for (int k = 0; k < NG; ++k) {
-            ia[k] = round_group<D, N, KMAXQ>(xval, D * k, id);
-            const int gi = tab.map[ia[k]];
+            const int u = round_group<D, N, KMAXQ>(xval, D * k, id);
+            const int gi = tab.map[u];
             ona[k] = gi >= 0;
-            if (gi < 0) ia[k] = best_neighbour_idx<D, N>(tab.nb - gi - 1, grid, xval, waux, D * k, this_scale);
+            const int nu = wave_best_neighbour<D, N>(nc, k, live && gi < 0, gi, xval, this_scale, tab.nb, grid);
+            ia[k] = gi < 0 ? nu : u;
         }
         float sumqx, sumq2;
         sums_idx<D, N>(xval, w, ia, sumqx, sumq2);
@@ -238,17 +323,19 @@ __device__ __forceinline__ float lattice_search(const float (&xval)[N], const fl
     int n_off = 0;
 #pragma unroll
     for (int k = 0; k < NG; ++k) n_off += on[k] ? 0 : 1;
-    if (n_off > 0 && scale > 0) {
-        const float id = 1 / scale;
+    const bool refit = live && n_off > 0 && scale > 0;
+    const float id = 1 / scale;
 #pragma unroll
-        for (int k = 0; k < NG; ++k) {
-            if (!REFIT_ALL && on[k]) continue;
-            // the rounded levels, or the best neighbour's when off the grid (SET_L_IN_REFIT only
-            // changes when the levels are written, not their values)
-            const int u = round_group<D, N, KMAXQ>(xval, D * k, id);
-            const int gi = tab.map[u];
-            idx[k] = gi < 0 ? best_neighbour_idx<D, N>(tab.nb - gi - 1, grid, xval, waux, D * k, scale) : u;
-        }
+    for (int k = 0; k < NG; ++k) {
+        // the rounded levels, or the best neighbour's when off the grid (SET_L_IN_REFIT only
+        // changes when the levels are written, not their values)
+        const bool redo = refit && (REFIT_ALL || !on[k]);
+        const int u = round_group<D, N, KMAXQ>(xval, D * k, id);
+        const int gi = tab.map[u];
+        const int nu = wave_best_neighbour<D, N>(nc, k, redo && gi < 0, gi, xval, scale, tab.nb, grid);
+        if (redo) idx[k] = gi < 0 ? nu : u;
+    }
+    if (refit) {
         float sumqx, sumq2;
         sums_idx<D, N>(xval, w, idx, sumqx, sumq2);
         if (sumq2 > 0) scale = sumqx / sumq2;
@@ -256,29 +343,38 @@ __device__ __forceinline__ float lattice_search(const float (&xval)[N], const fl
     return scale;
 }
 
+// sqrt(w) of the sub-block into this lane's LDS row, read by the neighbour searches
+template <int N>
+__device__ __forceinline__ void put_sqrt_w(const NbCtx& nc, const float (&w)[N]) {
+    float4* row = reinterpret_cast<float4*>(const_cast<float*>(nc.wrows) + threadIdx.x * N);
+#pragma unroll
+    for (int v = 0; v < N / 4; ++v) row[v] = make_float4(sqrtf(w[4 * v]), sqrtf(w[4 * v + 1]), sqrtf(w[4 * v + 2]), sqrtf(w[4 * v + 3]));
+}
+
+// A lattice group's levels are kept as its level index (B bits per coordinate: the map's key), one
+// register per group instead of one per weight; the search states of the 32-weight sub-blocks
+// otherwise do not fit the register file twice over.
 // IQ2_XXS -- quantize_row_iq2_xxs_impl (ggml-quants.c:3295-3471): 32-weight sub-blocks, 4 groups of 8
 __device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float (&w)[32], const IqDeviceTable& tab,
-                                              const uint8_t* grid, LdsCol waux) {
+                                              const uint8_t* grid, const NbCtx& nc) {
     constexpr int KMAXQ = 3;
     SubOut o{};
     float xval[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) waux.set(i, sqrtf(w[i]));
+    put_sqrt_w<32>(nc, w);
     uint32_t sg[4];
     make_signs<32, true>(x, w, xval, sg);
     float max = xval[0];
 #pragma unroll
     for (int i = 1; i < 32; ++i) max = tmax(max, xval[i]);
-    o.empty = true;
-    if (max < GROUP_MAX_EPS) return o;
     float scale;
     {
         int Lq[32];     // make_qp_quants' levels never reach the output: scale > 0 below refits every group
         scale = make_qp_quants<32>(KMAXQ + 1, xval, Lq, w);
     }
     const float eff_max = scale * KMAXQ;
-    if (eff_max <= 0) return o;
-    o.empty = false;
+    // the reference's early exits (max < GROUP_MAX_EPS, eff_max <= 0) leave the sub-block empty
+    const bool live = !(max < GROUP_MAX_EPS) && eff_max > 0;
+    o.empty = !live;
     float best = 0;
     int idx[4] = {0, 0, 0, 0};
     for (int is = -6; is <= 6; ++is) {
@@ -287,9 +383,10 @@ __device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float 
         int ia[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            ia[k] = round_group<8, 32, KMAXQ>(xval, 8 * k, id);
-            const int gi = tab.map[ia[k]];
-            if (gi < 0) ia[k] = best_neighbour_idx<8, 32>(tab.nb - gi - 1, grid, xval, waux, 8 * k, this_scale);
+            const int u = round_group<8, 32, KMAXQ>(xval, 8 * k, id);
+            const int gi = tab.map[u];
+            const int nu = wave_best_neighbour<8, 32>(nc, k, live && gi < 0, gi, xval, this_scale, tab.nb, grid);
+            ia[k] = gi < 0 ? nu : u;
         }
         float sumqx, sumq2;
         sums_idx<8, 32>(xval, w, ia, sumqx, sumq2);
@@ -300,19 +397,22 @@ __device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float 
             for (int k = 0; k < 4; ++k) idx[k] = ia[k];
         }
     }
-    if (scale > 0) {
-        // every group requantized at the best scale (ggml-quants.c:3411-3432)
-        const float id = 1 / scale;
+    // every group requantized at the best scale (ggml-quants.c:3411-3432)
+    const bool refit = live && scale > 0;
+    const float id = 1 / scale;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int u = round_group<8, 32, KMAXQ>(xval, 8 * k, id);
-            const int gi = tab.map[u];
-            idx[k] = gi < 0 ? best_neighbour_idx<8, 32>(tab.nb - gi - 1, grid, xval, waux, 8 * k, scale) : u;
-        }
+    for (int k = 0; k < 4; ++k) {
+        const int u = round_group<8, 32, KMAXQ>(xval, 8 * k, id);
+        const int gi = tab.map[u];
+        const int nu = wave_best_neighbour<8, 32>(nc, k, refit && gi < 0, gi, xval, scale, tab.nb, grid);
+        if (refit) idx[k] = gi < 0 ? nu : u;
+    }
+    if (refit) {
         float sumqx, sumq2;
         sums_idx<8, 32>(xval, w, idx, sumqx, sumq2);
         if (sumq2 > 0) scale = sumqx / sumq2;
     }
+    if (!live) return o;
     if (scale < 0) {
         scale = -scale;
 #pragma unroll
@@ -328,21 +428,20 @@ __device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float 
 // (:5114-5280): 16-weight sub-blocks, 2 lattice groups of 8
 template <bool XS>
 __device__ __forceinline__ SubOut iq2_16_sub(const float (&x)[16], const float (&w)[16], const IqDeviceTable& tab,
-                                             const uint8_t* grid, LdsCol waux) {
+                                             const uint8_t* grid, const NbCtx& nc) {
     SubOut o{};
     float xval[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) waux.set(i, sqrtf(w[i]));
+    put_sqrt_w<16>(nc, w);
     uint32_t sg[2];
     make_signs<16, XS>(x, w, xval, sg);
     float max = xval[0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) max = tmax(max, xval[i]);
-    o.empty = true;
-    if (max < (XS ? GROUP_MAX_EPS : 1e-8f)) return o;   // GROUP_MAX_EPS_IQ2_S = 1e-8f
-    o.empty = false;
+    const bool live = !(max < (XS ? GROUP_MAX_EPS : 1e-8f));   // GROUP_MAX_EPS_IQ2_S = 1e-8f
+    o.empty = !live;
     int idx[2] = {0, 0};
-    float scale = lattice_search<16, 8, 3, -9, 9, true, false, true>(xval, w, waux, max, 0.1f, tab, grid, idx);
+    float scale = lattice_search<16, 8, 3, -9, 9, true, false, true>(live, xval, w, nc, max, 0.1f, tab, grid, idx);
+    if (!live) return o;
     if (scale < 0) {
         scale = -scale;
 #pragma unroll
@@ -358,23 +457,22 @@ __device__ __forceinline__ SubOut iq2_16_sub(const float (&x)[16], const float (
 // (:4170-4353): 32-weight sub-blocks, 8 lattice groups of 4
 template <bool XXS>
 __device__ __forceinline__ SubOut iq3_sub(const float (&x)[32], const float (&w)[32], const IqDeviceTable& tab,
-                                          const uint8_t* grid, LdsCol waux) {
+                                          const uint8_t* grid, const NbCtx& nc) {
     SubOut o{};
     float xval[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) waux.set(i, sqrtf(w[i]));
+    put_sqrt_w<32>(nc, w);
     uint32_t sg[4];
     make_signs<32, XXS>(x, w, xval, sg);
     float max = xval[0];
 #pragma unroll
     for (int i = 1; i < 32; ++i) max = tmax(max, xval[i]);
-    o.empty = true;
-    if (XXS ? (max < 1e-8f) : (max == 0.f)) return o;   // GROUP_MAX_EPS_IQ3_XXS = 1e-8f; IQ3_S: !max
-    o.empty = false;
+    const bool live = !(XXS ? (max < 1e-8f) : (max == 0.f));   // GROUP_MAX_EPS_IQ3_XXS = 1e-8f; IQ3_S: !max
+    o.empty = !live;
     int idx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float scale;
-    if constexpr (XXS) scale = lattice_search<32, 4, 8, -15, 15, true, false, false>(xval, w, waux, max, 0.2f, tab, grid, idx);
-    else scale = lattice_search<32, 4, 8, -9, 9, false, true, false>(xval, w, waux, max, 0.2f, tab, grid, idx);
+    if constexpr (XXS) scale = lattice_search<32, 4, 8, -15, 15, true, false, false>(live, xval, w, nc, max, 0.2f, tab, grid, idx);
+    else scale = lattice_search<32, 4, 8, -9, 9, false, true, false>(live, xval, w, nc, max, 0.2f, tab, grid, idx);
+    if (!live) return o;
     if (scale < 0) {
         scale = -scale;
 #pragma unroll
@@ -712,21 +810,22 @@ struct Park {
 
 enum Kind { K_IQ2_XXS, K_IQ2_XS, K_IQ2_S, K_IQ3_XXS, K_IQ3_S, K_IQ1_S, K_IQ1_M0, K_IQ1_M1 };
 
-// N: sub-block; BS: block bytes; GBYTES: codebook bytes; TWO: sigma2 = 2 sumx2 / 256 (else sumx2 / 256)
+// D: lattice group size; N: sub-block; BS: block bytes; GBYTES: codebook bytes; TWO: sigma2 = 2 sumx2 / 256
+// (else sumx2 / 256)
 template <int K> struct Cfg;
 // WPE: the waves per SIMD the register allocation is held to. The 32-weight lattice searches need
 // ~200 registers; at 3 waves (168) a few spill, which costs less than the lost latency hiding at 2
 // (measured: IQ3_XXS 7.6 -> 9.4 GB/s, IQ2_XXS 8.5 -> 10.9); 4 spills them by the thousand. The
 // 16-weight and IQ1_S searches fit 128 with few spills (IQ1_S 21.5 -> 23.8 at 4); IQ1_M keeps 3
 // (23.1 at 4, 24.0 at 3).
-template <> struct Cfg<K_IQ2_XXS> { static constexpr int N = 32, BS = 66, GBYTES = 256 * 8, WPE = 3; static constexpr bool TWO = false; };
-template <> struct Cfg<K_IQ2_XS> { static constexpr int N = 16, BS = 74, GBYTES = 512 * 8, WPE = 4; static constexpr bool TWO = false; };
-template <> struct Cfg<K_IQ2_S> { static constexpr int N = 16, BS = 82, GBYTES = 1024 * 8, WPE = 4; static constexpr bool TWO = true; };
-template <> struct Cfg<K_IQ3_XXS> { static constexpr int N = 32, BS = 98, GBYTES = 256 * 4, WPE = 3; static constexpr bool TWO = true; };
-template <> struct Cfg<K_IQ3_S> { static constexpr int N = 32, BS = 110, GBYTES = 512 * 4, WPE = 3; static constexpr bool TWO = true; };
-template <> struct Cfg<K_IQ1_S> { static constexpr int N = 32, BS = 50, GBYTES = 2048 * 8, WPE = 4; static constexpr bool TWO = true; };
-template <> struct Cfg<K_IQ1_M0> { static constexpr int N = 16, BS = 56, GBYTES = 2048 * 8, WPE = 3; static constexpr bool TWO = true; };
-template <> struct Cfg<K_IQ1_M1> { static constexpr int N = 16, BS = 56, GBYTES = 2048 * 8, WPE = 3; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ2_XXS> { static constexpr int D = 8, N = 32, BS = 66, GBYTES = 256 * 8, WPE = 3; static constexpr bool TWO = false; };
+template <> struct Cfg<K_IQ2_XS> { static constexpr int D = 8, N = 16, BS = 74, GBYTES = 512 * 8, WPE = 4; static constexpr bool TWO = false; };
+template <> struct Cfg<K_IQ2_S> { static constexpr int D = 8, N = 16, BS = 82, GBYTES = 1024 * 8, WPE = 3; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ3_XXS> { static constexpr int D = 4, N = 32, BS = 98, GBYTES = 256 * 4, WPE = 3; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ3_S> { static constexpr int D = 4, N = 32, BS = 110, GBYTES = 512 * 4, WPE = 3; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ1_S> { static constexpr int D = 8, N = 32, BS = 50, GBYTES = 2048 * 8, WPE = 4; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ1_M0> { static constexpr int D = 8, N = 16, BS = 56, GBYTES = 2048 * 8, WPE = 3; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ1_M1> { static constexpr int D = 8, N = 16, BS = 56, GBYTES = 2048 * 8, WPE = 3; static constexpr bool TWO = true; };
 
 template <int K>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE))) void k_iqgrid(const void* __restrict__ src, int kind, uint8_t* __restrict__ dst, int64_t nsb,
@@ -736,12 +835,13 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
     constexpr bool IQ1 = K == K_IQ1_S || K == K_IQ1_M0 || K == K_IQ1_M1;
     __shared__ __align__(16) uint8_t grid[C::GBYTES];
     __shared__ __align__(16) uint16_t otile[SBW * C::BS / 2];
-    // sqrt(w) of the lattice types' neighbour searches in per-lane LDS columns (LdsCol); once the
-    // searches are done the same bytes hold the parked per-lane results
+    // sqrt(w) of the lattice types' neighbour searches in per-lane LDS rows; once the searches are
+    // done the same bytes hold the parked per-lane results
     constexpr int WA_BYTES = IQ1 ? 0 : N * WG * 4, PARK_BYTES = SBW * G * (int)sizeof(Park);
     __shared__ __align__(16) uint8_t wa_park[WA_BYTES > PARK_BYTES ? WA_BYTES : PARK_BYTES];
+    __shared__ NbWave<C::D> nbw[IQ1 ? 1 : WG / 64];
     Park (*park)[G] = reinterpret_cast<Park (*)[G]>(wa_park);
-    const LdsCol waux{reinterpret_cast<float*>(wa_park) + threadIdx.x};
+    const NbCtx nc{&nbw[IQ1 ? 0 : threadIdx.x / 64], reinterpret_cast<const float*>(wa_park), (int)(threadIdx.x & ~63u)};
     for (int i = threadIdx.x; i < C::GBYTES / 16; i += WG)
         reinterpret_cast<uint4*>(grid)[i] = reinterpret_cast<const uint4*>(tab.grid)[i];
     __syncthreads();
@@ -776,11 +876,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
     float w[N];
     weights(x, w);
     SubOut r;
-    if constexpr (K == K_IQ2_XXS) r = iq2_xxs_sub(x, w, tab, grid, waux);
-    else if constexpr (K == K_IQ2_XS) r = iq2_16_sub<true>(x, w, tab, grid, waux);
-    else if constexpr (K == K_IQ2_S) r = iq2_16_sub<false>(x, w, tab, grid, waux);
-    else if constexpr (K == K_IQ3_XXS) r = iq3_sub<true>(x, w, tab, grid, waux);
-    else if constexpr (K == K_IQ3_S) r = iq3_sub<false>(x, w, tab, grid, waux);
+    if constexpr (K == K_IQ2_XXS) r = iq2_xxs_sub(x, w, tab, grid, nc);
+    else if constexpr (K == K_IQ2_XS) r = iq2_16_sub<true>(x, w, tab, grid, nc);
+    else if constexpr (K == K_IQ2_S) r = iq2_16_sub<false>(x, w, tab, grid, nc);
+    else if constexpr (K == K_IQ3_XXS) r = iq3_sub<true>(x, w, tab, grid, nc);
+    else if constexpr (K == K_IQ3_S) r = iq3_sub<false>(x, w, tab, grid, nc);
     else if constexpr (K == K_IQ1_S) r = iq1_s_sub(x, w, tab, grid, reload);
     else r = iq1_m_sub<K == K_IQ1_M1 ? 1 : 0>(x, w, tab, grid, reload);
     // super-block scale: MAX over the sub-block scales in sub-block order (empty ones count as 0)
