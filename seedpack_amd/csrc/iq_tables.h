@@ -7,7 +7,7 @@ namespace spa {
 
 struct IqDeviceTable {
     const uint8_t* grid;      // size x (8 or 4) coordinate values 2l+1
-    const int32_t* map;       // level index -> grid point, or -(offset+1) into nb
+    const int32_t* map;       // level index -> grid point, or -1 - (offset << 9 | length) of its list in nb
     const uint16_t* nb;       // neighbour lists: count, then grid point indices
     int size;
 };

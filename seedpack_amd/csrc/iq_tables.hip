@@ -124,12 +124,21 @@ int iq_device_table(int idx, IqDeviceTable* out) {
     std::lock_guard<std::mutex> lk(g_dev_mu);
     IqDeviceTable& t = g_dev[dev][idx];
     if (!t.grid) {
+        // off-grid entries carry their list's length beside its offset: one load gives both
+        std::vector<int32_t> dm(h.map.size());
+        for (size_t i = 0; i < h.map.size(); ++i) {
+            const int32_t v = h.map[i];
+            if (v >= 0) { dm[i] = v; continue; }
+            const uint32_t off = (uint32_t)(-v - 1), len = h.nb[off];
+            if (off >= (1u << 22) || len == 0 || len >= 512) return fail(SPA_ERR_ARG, "iq table %d: list %u of length %u", idx, off, len);
+            dm[i] = -1 - (int32_t)((off << 9) | len);
+        }
         void *g = nullptr, *m = nullptr, *nb = nullptr;
         SPA_HIP_TRY(hipMalloc(&g, h.grid.size()));
-        SPA_HIP_TRY(hipMalloc(&m, h.map.size() * sizeof(int32_t)));
+        SPA_HIP_TRY(hipMalloc(&m, dm.size() * sizeof(int32_t)));
         SPA_HIP_TRY(hipMalloc(&nb, h.nb.size() * sizeof(uint16_t)));
         SPA_HIP_TRY(hipMemcpy(g, h.grid.data(), h.grid.size(), hipMemcpyHostToDevice));
-        SPA_HIP_TRY(hipMemcpy(m, h.map.data(), h.map.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+        SPA_HIP_TRY(hipMemcpy(m, dm.data(), dm.size() * sizeof(int32_t), hipMemcpyHostToDevice));
         SPA_HIP_TRY(hipMemcpy(nb, h.nb.data(), h.nb.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
         t.grid = (const uint8_t*)g;
         t.map = (const int32_t*)m;

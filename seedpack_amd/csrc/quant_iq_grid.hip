@@ -66,21 +66,21 @@ __device__ __forceinline__ void grid_point(const uint8_t* grid, int j, int (&q)[
 // at the trial scale s. The lists hold 1 to ~300 points; one lane per list would leave the wave
 // waiting for its longest list (3-4x the useful work on the configuration-3 tensors). Instead, for
 // one group index k at a time, the lists of all the wave's off-grid groups are cut into pieces of
-// NB_R consecutive entries and the pieces are dealt to the 64 lanes in rounds, so every lane evaluates
-// NB_R entries per round. A piece's owner (its group's |x|, scale, list) is read from the owner's LDS
+// a few consecutive entries and the pieces are dealt to the 64 lanes in rounds, so every lane
+// evaluates the same number of entries per round. A piece's owner (its group's |x|, scale, list) is read from the owner's LDS
 // record and its sqrt(w) from the owner's LDS row. Each list's winner is kept in an LDS slot as the
 // 64-bit key (d2 bits, position, point) lowered by atomic min: d2 >= +0 orders as its bit pattern, so
 // the least key is the smallest d2 at the smallest position -- the reference's first strict minimum.
 // Entries are kept only when d2 < FLT_MAX (the reference's initial best); a list with none keeps its
 // first point (the reference asserts there instead).
-constexpr int NB_R = 4;   // list entries per piece
+// Entries per piece: long lists (the 8-dimensional lattices, 35 entries on average when off the grid)
+// take 8, the 4-dimensional ones (about 14) take 4.
+template <int D> constexpr int nb_piece() { return D == 8 ? 8 : 4; }
 
 template <int D>
 struct NbWave {
     __align__(16) float rec[64][D + 4];   // per owner lane: |x| of the group, scale, list offset, first piece, length
     unsigned long long slot[64];          // per owner lane: least key so far
-    unsigned long long starts;            // pieces of the current round that begin a list (bit per lane)
-    int tl[64];                           // owner lanes in piece order
 };
 
 struct NbCtx {
@@ -92,25 +92,32 @@ struct NbCtx {
 // LDS writes of the wave's lanes complete before its later LDS reads, and no compiler reordering
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// The device map holds, for a point off the grid, -1 - (list offset << 9 | list length)
+__device__ __forceinline__ int nb_offset(int gi) { return (-1 - gi) >> 9; }
+__device__ __forceinline__ int nb_length(int gi) { return (-1 - gi) & 511; }
+
 // The level index of the best neighbour of group k for the lanes with `off` set (gi: the map's
 // negative entry for the group's rounded point); called by all lanes of the wave together.
 template <int D, int N>
 __device__ int wave_best_neighbour(const NbCtx& c, int k, bool off, int gi, const float (&xval)[N], float scale,
                                    const uint16_t* __restrict__ nbt, const uint8_t* grid) {
+    constexpr int R = nb_piece<D>();
+    constexpr int NPB = R == 8 ? 7 : 8;   // bits of the piece count ceil(511 / R)
     NbWave<D>& W = *reinterpret_cast<NbWave<D>*>(c.w);
     constexpr unsigned long long INIT = (unsigned long long)0x7f7fffffu << 32;   // (FLT_MAX, position 0)
     const int lane = (int)__lane_id();
-    const int ptr = off ? -gi - 1 : 0;
-    const int len = off ? (int)nbt[ptr] : 0;
-    const int np = (len + NB_R - 1) / NB_R;
-    int incl = np;
+    const int ptr = off ? nb_offset(gi) : 0;
+    const int len = off ? nb_length(gi) : 0;
+    const int np = (len + R - 1) / R;
+    // exclusive prefix of the piece counts over the wave, one bit plane at a time
+    int first = 0, total = 0;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int t = __shfl_up(incl, d);
-        if (lane >= d) incl += t;
+    for (int b = 0; b < NPB; ++b) {
+        const unsigned long long m = __ballot((np >> b) & 1);
+        first += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) << b;
+        total += __popcll(m) << b;
     }
-    const int first = incl - np, total = __shfl(incl, 63);
-    const unsigned long long owners = __ballot(np > 0);
+    const int incl = first + np;
     if (np > 0) {
         float4* r = reinterpret_cast<float4*>(W.rec[lane]);
 #pragma unroll
@@ -118,21 +125,18 @@ __device__ int wave_best_neighbour(const NbCtx& c, int k, bool off, int gi, cons
             r[v] = make_float4(xval[D * k + 4 * v], xval[D * k + 4 * v + 1], xval[D * k + 4 * v + 2], xval[D * k + 4 * v + 3]);
         r[D / 4] = make_float4(scale, __int_as_float(ptr), __int_as_float(first), __int_as_float(len));
         W.slot[lane] = INIT;
-        W.tl[__popcll(owners & ((1ull << lane) - 1))] = lane;
     }
-    int carry = -1;   // piece-order index of the list holding the piece before this round's first
+    wave_lds_sync();
     for (int base = 0; base < total; base += 64) {
-        if (lane == 0) W.starts = 0;
-        wave_lds_sync();
-        if (np > 0 && first >= base && first < base + 64) atomicOr(&W.starts, 1ull << (first - base));
-        wave_lds_sync();
-        const unsigned long long m = W.starts;
-        const unsigned long long upto = lane == 63 ? ~0ull : (2ull << lane) - 1;
-        const int seq = carry + __popcll(m & upto);
-        carry += __popcll(m);
         const int q = base + lane;
+        // the owner of piece q: the number of lanes whose pieces end at or before q (incl rises with lane)
+        int o = 0;
+#pragma unroll
+        for (int st = 32; st >= 1; st >>= 1) {
+            const int probe = __shfl(incl, o + st - 1);
+            if (probe <= q) o += st;
+        }
         if (q < total) {
-            const int o = W.tl[seq];
             const float4* r = reinterpret_cast<const float4*>(W.rec[o]);
             const float4* wr = reinterpret_cast<const float4*>(c.wrows + (c.wbase + o) * N + D * k);
             float xg[D], wv[D];
@@ -145,11 +149,11 @@ __device__ int wave_best_neighbour(const NbCtx& c, int k, bool off, int gi, cons
             const float4 meta = r[D / 4];
             const float s = meta.x;
             const int p = __float_as_int(meta.y), L = __float_as_int(meta.w);
-            const int pos0 = (q - __float_as_int(meta.z)) * NB_R;
+            const int pos0 = (q - __float_as_int(meta.z)) * R;
             float best = FLT_BIG;
             uint32_t bj = 0;
 #pragma unroll
-            for (int e = 0; e < NB_R; ++e) {
+            for (int e = 0; e < R; ++e) {
                 const int pos = pos0 + e;
                 if (pos < L) {
                     const int j = nbt[p + 1 + pos];
@@ -166,8 +170,8 @@ __device__ int wave_best_neighbour(const NbCtx& c, int k, bool off, int gi, cons
             }
             if (best < FLT_BIG) atomicMin(&W.slot[o], ((unsigned long long)__float_as_uint(best) << 32) | bj);
         }
-        wave_lds_sync();
     }
+    wave_lds_sync();
     int u = 0;
     if (np > 0) {
         const unsigned long long key = W.slot[lane];
@@ -301,15 +305,18 @@ __device__ __forceinline__ float lattice_search(bool live, const float (&xval)[N
     for (int is = IS_LO; is <= IS_HI; ++is) {
         const float id = ((float)(2 * KMAXQ - 1) + (float)is * step) / max;
         const float this_scale = 1 / id;
-        int ia[NG];
+        int ia[NG], ga[NG];
         bool ona[NG];
 #pragma unroll
         for (int k = 0; k < NG; ++k) {
-            const int u = round_group<D, N, KMAXQ>(xval, D * k, id);
-            const int gi = tab.map[u];
-            ona[k] = gi >= 0;
-            const int nu = wave_best_neighbour<D, N>(nc, k, live && gi < 0, gi, xval, this_scale, tab.nb, grid);
-            ia[k] = gi < 0 ? nu : u;
+            ia[k] = round_group<D, N, KMAXQ>(xval, D * k, id);
+            ga[k] = tab.map[ia[k]];
+        }
+#pragma unroll
+        for (int k = 0; k < NG; ++k) {
+            ona[k] = ga[k] >= 0;
+            const int nu = wave_best_neighbour<D, N>(nc, k, live && ga[k] < 0, ga[k], xval, this_scale, tab.nb, grid);
+            if (ga[k] < 0) ia[k] = nu;
         }
         float sumqx, sumq2;
         sums_idx<D, N>(xval, w, ia, sumqx, sumq2);
@@ -380,13 +387,16 @@ __device__ __forceinline__ SubOut iq2_xxs_sub(const float (&x)[32], const float 
     for (int is = -6; is <= 6; ++is) {
         const float id = ((float)(2 * KMAXQ - 1) + (float)is * 0.1f) / eff_max;
         const float this_scale = 1 / id;
-        int ia[4];
+        int ia[4], ga[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const int u = round_group<8, 32, KMAXQ>(xval, 8 * k, id);
-            const int gi = tab.map[u];
-            const int nu = wave_best_neighbour<8, 32>(nc, k, live && gi < 0, gi, xval, this_scale, tab.nb, grid);
-            ia[k] = gi < 0 ? nu : u;
+            ia[k] = round_group<8, 32, KMAXQ>(xval, 8 * k, id);
+            ga[k] = tab.map[ia[k]];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int nu = wave_best_neighbour<8, 32>(nc, k, live && ga[k] < 0, ga[k], xval, this_scale, tab.nb, grid);
+            if (ga[k] < 0) ia[k] = nu;
         }
         float sumqx, sumq2;
         sums_idx<8, 32>(xval, w, ia, sumqx, sumq2);
@@ -576,8 +586,8 @@ __device__ __forceinline__ float iq1_snap(const float (&x)[N], const float (&w)[
             int Lg[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) { xv[i] = x[8 * k + i]; wv[i] = w[8 * k + i]; }
-            gi = pos[k] ? iq1_neighbour(tab.nb - gi - 1, grid, xv, wv, scale, XP0, XP1, XP2, Lg)
-                        : iq1_neighbour(tab.nb - gi - 1, grid, xv, wv, scale, XM0, XM1, XM2, Lg);
+            gi = pos[k] ? iq1_neighbour(tab.nb + nb_offset(gi), grid, xv, wv, scale, XP0, XP1, XP2, Lg)
+                        : iq1_neighbour(tab.nb + nb_offset(gi), grid, xv, wv, scale, XM0, XM1, XM2, Lg);
 #pragma unroll
             for (int i = 0; i < 8; ++i) L[8 * k + i] = Lg[i];
         }
@@ -820,7 +830,7 @@ template <int K> struct Cfg;
 // (23.1 at 4, 24.0 at 3).
 template <> struct Cfg<K_IQ2_XXS> { static constexpr int D = 8, N = 32, BS = 66, GBYTES = 256 * 8, WPE = 3; static constexpr bool TWO = false; };
 template <> struct Cfg<K_IQ2_XS> { static constexpr int D = 8, N = 16, BS = 74, GBYTES = 512 * 8, WPE = 4; static constexpr bool TWO = false; };
-template <> struct Cfg<K_IQ2_S> { static constexpr int D = 8, N = 16, BS = 82, GBYTES = 1024 * 8, WPE = 3; static constexpr bool TWO = true; };
+template <> struct Cfg<K_IQ2_S> { static constexpr int D = 8, N = 16, BS = 82, GBYTES = 1024 * 8, WPE = 4; static constexpr bool TWO = true; };
 template <> struct Cfg<K_IQ3_XXS> { static constexpr int D = 4, N = 32, BS = 98, GBYTES = 256 * 4, WPE = 3; static constexpr bool TWO = true; };
 template <> struct Cfg<K_IQ3_S> { static constexpr int D = 4, N = 32, BS = 110, GBYTES = 512 * 4, WPE = 3; static constexpr bool TWO = true; };
 template <> struct Cfg<K_IQ1_S> { static constexpr int D = 8, N = 32, BS = 50, GBYTES = 2048 * 8, WPE = 4; static constexpr bool TWO = true; };
