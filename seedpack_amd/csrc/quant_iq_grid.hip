@@ -79,13 +79,15 @@ template <int D> constexpr int nb_piece() { return D == 8 ? 8 : 4; }
 
 template <int D>
 struct NbWave {
-    __align__(16) float rec[64][D + 4];   // per owner lane: |x| of the group, scale, list offset, first piece, length
+    // per owner lane: |x| of the group, scale, list offset, first piece, length; rows of 12 words put
+    // the records of 8 consecutive owners on distinct banks
+    __align__(16) float rec[64][12];
     unsigned long long slot[64];          // per owner lane: least key so far
 };
 
 struct NbCtx {
     void* w;               // this wave's NbWave
-    const float* wrows;    // per-lane rows of sqrt(w) (N floats each), the workgroup's
+    const float* wrows;    // per-lane rows of sqrt(w) (N floats each, rotated: wrow_at), the workgroup's
     int wbase;             // the wave's first thread in the workgroup
 };
 
@@ -95,6 +97,11 @@ __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcn
 // The device map holds, for a point off the grid, -1 - (list offset << 9 | list length)
 __device__ __forceinline__ int nb_offset(int gi) { return (-1 - gi) >> 9; }
 __device__ __forceinline__ int nb_length(int gi) { return (-1 - gi) & 511; }
+
+// Thread t's row of sqrt(w) holds its 4-weight group v at float4 slot (v + t) mod N/4: the rows of
+// different owners read in one instruction start on different banks.
+template <int N>
+__device__ __forceinline__ int wrow_at(int t, int v) { return (v + t) % (N / 4); }
 
 // The level index of the best neighbour of group k for the lanes with `off` set (gi: the map's
 // negative entry for the group's rounded point); called by all lanes of the wave together.
@@ -138,11 +145,11 @@ __device__ int wave_best_neighbour(const NbCtx& c, int k, bool off, int gi, cons
         }
         if (q < total) {
             const float4* r = reinterpret_cast<const float4*>(W.rec[o]);
-            const float4* wr = reinterpret_cast<const float4*>(c.wrows + (c.wbase + o) * N + D * k);
+            const float4* wr = reinterpret_cast<const float4*>(c.wrows + (c.wbase + o) * N);
             float xg[D], wv[D];
 #pragma unroll
             for (int v = 0; v < D / 4; ++v) {
-                const float4 a = r[v], b = wr[v];
+                const float4 a = r[v], b = wr[wrow_at<N>(c.wbase + o, D * k / 4 + v)];
                 xg[4 * v] = a.x; xg[4 * v + 1] = a.y; xg[4 * v + 2] = a.z; xg[4 * v + 3] = a.w;
                 wv[4 * v] = b.x; wv[4 * v + 1] = b.y; wv[4 * v + 2] = b.z; wv[4 * v + 3] = b.w;
             }
@@ -355,7 +362,7 @@ template <int N>
 __device__ __forceinline__ void put_sqrt_w(const NbCtx& nc, const float (&w)[N]) {
     float4* row = reinterpret_cast<float4*>(const_cast<float*>(nc.wrows) + threadIdx.x * N);
 #pragma unroll
-    for (int v = 0; v < N / 4; ++v) row[v] = make_float4(sqrtf(w[4 * v]), sqrtf(w[4 * v + 1]), sqrtf(w[4 * v + 2]), sqrtf(w[4 * v + 3]));
+    for (int v = 0; v < N / 4; ++v) row[wrow_at<N>((int)threadIdx.x, v)] = make_float4(sqrtf(w[4 * v]), sqrtf(w[4 * v + 1]), sqrtf(w[4 * v + 2]), sqrtf(w[4 * v + 3]));
 }
 
 // A lattice group's levels are kept as its level index (B bits per coordinate: the map's key), one
