@@ -99,12 +99,14 @@ int spa_dequantize(int ggml_type, const void* src, int64_t nrows, int64_t n_per_
 int spa_iq_table_host(int index, const void** grid, int* grid_bytes, const int32_t** map, int* map_n,
                       const uint16_t** neighbours, int* nb_n);
 
-/* ---- QR residual coder (non-grid quant types; seedpack/qr.py) ----
+/* ---- QR residual coder (all 20 quant types; seedpack/qr.py) ----
  * Batch descriptors are device arrays with the reference's byte layout (qr.py:898-900):
  *   tm: one 32-byte record per tensor {i64 blk0, i64 seed_off, i32 seed_type, i32 cols, i64 imx_off}
  *   sg: one 16-byte record per segment {i32 t, i32 nb, i64 b0}
  * F, P: the batch's file and predicted blocks back to back; seed: the seed tensors (BF16 = type 30,
- * F32 = 0, F16 = 1) addressed by seed_off. gk / imx are for the grid types (not built yet; pass NULL).
+ * F32 = 0, F16 = 1) addressed by seed_off. gk (the grid keys, qr.py:935-948) and imx (the tensors'
+ * importance, addressed by imx_off) are read for the grid types (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS,
+ * IQ3_S, IQ1_S, IQ1_M) and may be NULL otherwise.
  * mv: the model version recorded with the batch (2 for new batches, 1 for archives before 0.3.0). */
 
 /* Blocks per rANS segment of a type: max(16, 16384 / QK) (qr.py:952-954); 0 if not a QR type. */
