@@ -18,23 +18,40 @@ constexpr float GROUP_MAX_EPS = 1e-15f;
 // kvalues_iq4nl (ggml-common.h:1120)
 __constant__ const int8_t KVALUES[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
 
-// best_index_int8(16, kvalues_iq4nl, x) -- ggml-quants.c:28-37: binary search, ties to the upper value
-__device__ __forceinline__ int best_index(float x) {
-    if (x <= (float)KVALUES[0]) return 0;
-    if (x >= (float)KVALUES[15]) return 15;
-    int ml = 0, mu = 15;
+// best_index_int8(16, kvalues_iq4nl, x) -- ggml-quants.c:28-37: binary search, ties to the upper value.
+// The four halvings run unconditionally (the reference skips a step only on its [0, 1] range, where
+// the step cannot move: x > kvalues[0] there) and carry the values at both ends, so the final
+// nearest-of-two test needs no lookup. Levels 1-2 compare against constants; levels 3-4 read the
+// codebook from LDS (16 words on distinct banks): no per-lane global loads.
+struct Near {
+    int idx;     // best_index_int8's result
+    float val;   // kvalues_iq4nl[idx]
+};
+__device__ __forceinline__ Near nearest_iq4(const float* __restrict__ kv, float x) {
+    int lo = 0, hi = 15;
+    float vlo = (float)KVALUES[0], vhi = (float)KVALUES[15];
+    // level 1: mid 7
+    const bool c1 = x < (float)KVALUES[7];
+    if (c1) { hi = 7; vhi = (float)KVALUES[7]; } else { lo = 7; vlo = (float)KVALUES[7]; }
+    // level 2: mid 3 or 11
+    const float v2 = c1 ? (float)KVALUES[3] : (float)KVALUES[11];
+    const int m2 = c1 ? 3 : 11;
+    if (x < v2) { hi = m2; vhi = v2; } else { lo = m2; vlo = v2; }
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {          // 16 entries: exactly 4 halvings
-        if (mu - ml > 1) {
-            const int mav = (ml + mu) / 2;
-            if (x < (float)KVALUES[mav]) mu = mav; else ml = mav;
-        }
+    for (int it = 0; it < 2; ++it) {
+        const int mid = (lo + hi) >> 1;
+        const float v = kv[mid];
+        if (x < v) { hi = mid; vhi = v; } else { lo = mid; vlo = v; }
     }
-    return x - (float)KVALUES[mu - 1] < (float)KVALUES[mu] - x ? mu - 1 : mu;
+    Near r = x - vlo < vhi - x ? Near{lo, vlo} : Near{hi, vhi};
+    if (x >= (float)KVALUES[15]) r = Near{15, (float)KVALUES[15]};
+    if (x <= (float)KVALUES[0]) r = Near{0, (float)KVALUES[0]};
+    return r;
 }
+__device__ __forceinline__ int best_index(const float* __restrict__ kv, float x) { return nearest_iq4(kv, x).idx; }
 
 // scale search of one 32-weight block (ggml-quants.c:4962-5010, ntry = 7); returns the block scale
-__device__ __forceinline__ float block_scale(const float (&x)[32], const float (&w)[32]) {
+__device__ __forceinline__ float block_scale(const float* __restrict__ kv, const float (&x)[32], const float (&w)[32]) {
     float amax = 0, max = 0;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
@@ -47,7 +64,7 @@ __device__ __forceinline__ float block_scale(const float (&x)[32], const float (
     float sumqx = 0, sumq2 = 0;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        const float q = (float)KVALUES[best_index(id * x[j])];
+        const float q = nearest_iq4(kv, id * x[j]).val;
         sumqx += w[j] * q * x[j];
         sumq2 += w[j] * q * q;
     }
@@ -58,7 +75,7 @@ __device__ __forceinline__ float block_scale(const float (&x)[32], const float (
         sumqx = sumq2 = 0;
 #pragma unroll
         for (int j = 0; j < 32; ++j) {
-            const float q = (float)KVALUES[best_index(id * x[j])];
+            const float q = nearest_iq4(kv, id * x[j]).val;
             sumqx += w[j] * q * x[j];
             sumq2 += w[j] * q * q;
         }
@@ -74,6 +91,9 @@ __device__ __forceinline__ float block_scale(const float (&x)[32], const float (
 __global__ __launch_bounds__(WG) void k_iq4_nl(const void* __restrict__ src, int kind, uint8_t* __restrict__ dst,
                                                int64_t nblocks, int64_t bpr, const float* __restrict__ imx) {
     __shared__ __align__(16) uint16_t tile[WG * 18 / 2];
+    __shared__ float kv[16];
+    if (threadIdx.x < 16) kv[threadIdx.x] = (float)KVALUES[threadIdx.x];
+    __syncthreads();
     const int64_t b0 = (int64_t)blockIdx.x * WG;
     const int64_t b = b0 + threadIdx.x;
     if (b < nblocks) {
@@ -92,14 +112,14 @@ __global__ __launch_bounds__(WG) void k_iq4_nl(const void* __restrict__ src, int
 #pragma unroll
             for (int j = 0; j < 32; ++j) w[j] = x[j] * x[j];
         }
-        const float d = block_scale(x, w);
+        const float d = block_scale(kv, x, w);
         const float id = d != 0.f ? 1 / d : 0.f;
         TileOut o{tile + threadIdx.x * 9};
         o.put16(0, f32_to_f16(d));
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
-            const uint32_t b0_ = best_index(id * x[j]) | (best_index(id * x[16 + j]) << 4);
-            const uint32_t b1_ = best_index(id * x[j + 1]) | (best_index(id * x[17 + j]) << 4);
+            const uint32_t b0_ = best_index(kv, id * x[j]) | (best_index(kv, id * x[16 + j]) << 4);
+            const uint32_t b1_ = best_index(kv, id * x[j + 1]) | (best_index(kv, id * x[17 + j]) << 4);
             o.put2(2 + j, b0_, b1_);
         }
     }
@@ -115,6 +135,9 @@ __global__ __launch_bounds__(WG) void k_iq4_xs(const void* __restrict__ src, int
     __shared__ __align__(16) uint8_t ltile[SBW * 256];
     __shared__ __align__(16) uint16_t otile[SBW * 136 / 2];
     __shared__ int lsc[SBW][G];
+    __shared__ float kv[16];
+    if (threadIdx.x < 16) kv[threadIdx.x] = (float)KVALUES[threadIdx.x];
+    __syncthreads();
     const int lsb = threadIdx.x / G, sub = threadIdx.x % G;
     const int64_t sb0 = (int64_t)blockIdx.x * SBW;
     const int64_t sb = sb0 + lsb;
@@ -145,7 +168,7 @@ __global__ __launch_bounds__(WG) void k_iq4_xs(const void* __restrict__ src, int
 #pragma unroll
         for (int j = 0; j < 32; ++j) w[j] = sq[j];
     }
-    const float scale = block_scale(x, w);
+    const float scale = block_scale(kv, x, w);
     // the scale with the largest magnitude (first one on ties), then the super-scale
     float max_scale = 0, amax_scale = 0;
 #pragma unroll
@@ -162,8 +185,8 @@ __global__ __launch_bounds__(WG) void k_iq4_xs(const void* __restrict__ src, int
     uint32_t* lt = reinterpret_cast<uint32_t*>(ltile + lsb * 256 + sub * 32);
 #pragma unroll
     for (int j = 0; j < 32; j += 4)
-        lt[j / 4] = (uint32_t)best_index(idl * x[j]) | ((uint32_t)best_index(idl * x[j + 1]) << 8) |
-                    ((uint32_t)best_index(idl * x[j + 2]) << 16) | ((uint32_t)best_index(idl * x[j + 3]) << 24);
+        lt[j / 4] = (uint32_t)best_index(kv, idl * x[j]) | ((uint32_t)best_index(kv, idl * x[j + 1]) << 8) |
+                    ((uint32_t)best_index(kv, idl * x[j + 2]) << 16) | ((uint32_t)best_index(kv, idl * x[j + 3]) << 24);
     lsc[lsb][sub] = l + 32;
     __syncthreads();
     if (active && sub == 0) {
