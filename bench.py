@@ -13,6 +13,7 @@ same JSON line.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
 import argparse
+import concurrent.futures
 import json
 import os
 import sys
@@ -243,6 +244,155 @@ def cfg4_matrices(layers=36):
     return [("token_embd.weight", 151936, 4096)] + t + [("output.weight", 151936, 4096)]
 
 
+def cfg4_base(stream, layers=36):
+    """configuration 4's BF16 file region in HBM: every 2-D matrix back to back (32-byte aligned after
+    a 4 KB header), N(0, 0.02) from a counter-based generator per tensor -> (array, [(name, offset,
+    bytes, row length)], file size)"""
+    from seedpack_amd import device as dev
+    from seedpack_amd._lib import check, lib
+    pos, ts = 4096, []
+    for name, rows, rl in cfg4_matrices(layers):
+        pos += (-pos) % 32
+        ts.append((name, pos, rows * rl * 2, rl))
+        pos += rows * rl * 2
+    d = dev.DeviceArray(pos, np.uint8).zero(stream.handle)
+    for k, (name, off, nb, rl) in enumerate(ts):
+        check(lib().spa_synth_normal_bf16(d.ptr + off, nb // 2, 0x5EED0040 + k, 0.02, stream.handle))
+    stream.synchronize()
+    return d, ts, pos
+
+
+# configuration 4's quant files: the 20 quantizers, and a Q4_K_M-like mix (Q6_K for attn_v, ffn_down
+# and output, Q4_K elsewhere)
+PACK_TYPES = [2, 3, 6, 7, 8, 42, 10, 11, 12, 13, 14, 16, 17, 18, 19, 20, 21, 22, 23, 29]
+
+
+def _q4km(name):
+    return 14 if any(k in name for k in ("attn_v", "ffn_down", "output.")) else 12
+
+
+def pack_cfg4(stream, layers=36, per_million=10000, files=None):
+    """configuration 4's pack on the device. The BF16 base and one LogNormal(0, 1) imatrix per tensor
+    are resident in HBM, and so are the quant files (every 2-D matrix in one type), made untimed by
+    this library's quantizer with per_million / 10^6 of their blocks perturbed (one byte each). Then,
+    timed as one run: per file, every tensor is regrown and compared (residual.residual_tensor:
+    prediction, differing-byte count, the candidate variants) and the QR tensors are coded in batches
+    of about 384 MB (qr.encode_parts on the device, its zstd-19 framing on 8 worker threads beside the
+    device work, as the reference's pool does); then the base codec compresses the base. pack GB/s =
+    (BF16 bytes + quant file bytes) / that run's wall time. Each file's first batch is decoded again and
+    compared afterwards, untimed."""
+    from seedpack_amd import device as dev
+    from seedpack_amd import qr, r2, residual
+    from seedpack_amd._lib import check, lib
+    from seedpack_amd.gpuquant import GPUQuant
+    from seedpack_amd.requant import NAMES, QFUN
+    d, ts, pos = cfg4_base(stream, layers)
+    nb_all = sum(t[2] for t in ts)
+    g = np.random.Generator(np.random.PCG64(0x1A7))
+    imx_h = [g.lognormal(0.0, 1.0, rl).astype(np.float32) for (_, _, _, rl) in ts]
+    imx_off = np.cumsum([0] + [a.size for a in imx_h])[:-1]
+    imx_all = dev.DeviceArray.from_host(np.concatenate(imx_h), stream.handle)
+    imx_k = [imx_all.view(int(o) * 4, (a.size,), np.float32) for o, a in zip(imx_off, imx_h)]
+    base_k = [d.view(off, (nb // 2,), np.uint16) for (_, off, nb, _) in ts]
+    gq = GPUQuant(stream=stream.handle)
+    plan = [(NAMES[t], (lambda name, t=t: t)) for t in PACK_TYPES] + [("Q4_K_M", _q4km)]
+    if files is not None:
+        plan = [p for p in plan if p[0] in files]
+    _, tot = dev.mem_info()
+    made = []
+    for fi, (fname, type_of) in enumerate(plan):
+        types = [type_of(name) for (name, _, _, _) in ts]
+        regions = []
+        for k, (name, off, nb, rl) in enumerate(ts):
+            T = types[k]
+            y = gq.quantize_tensors(T, [(base_k[k], rl)], [imx_k[k]], device=True)[0]
+            bs = QFUN[T][2]
+            check(lib().spa_perturb_blocks(y.ptr, y.nbytes // bs, bs, per_million, 0xF11E0000 + 1000 * fi + k,
+                                           stream.handle))
+            regions.append(y)
+        made.append((fname, types, regions))
+    stream.synchronize()
+    log(f"bench: pack cfg4: {len(made)} files made")
+    pool = concurrent.futures.ThreadPoolExecutor(8)
+    out, framed, file_bytes = {}, [], 0
+    t_all = time.perf_counter()
+    for fname, types, regions in made:
+        t0 = time.perf_counter()
+        pending, wbytes, nqr = {}, {}, 0
+        phase = {"residual_s": 0.0, "qr_s": 0.0}
+        mine = []
+
+        def flush(T):
+            tq = time.perf_counter()
+            parts = qr.encode_parts(T, pending[T], d, imx_all, stream=stream.handle)
+            tq = time.perf_counter() - tq
+            phase["qr_s"] += tq
+            if tq > phase.get("qr_max_s", 0.0):
+                phase["qr_max_s"] = tq
+                phase["qr_max_parts"] = {k: round(v, 3) for k, v in parts["seconds"].items()}
+                phase["qr_max_parts"]["tries"] = parts["tries"]
+            # only each file's first batch keeps its tensors (for the check after the run)
+            mine.append((T, pool.submit(qr.frame, parts), list(pending[T]) if not mine else None))
+            pending[T], wbytes[T] = [], 0
+
+        for k, (name, off, nb, rl) in enumerate(ts):
+            T = types[k]
+            t = residual.Tensor(name, T, rl, regions[k], base_k[k], imatrix=imx_k[k])
+            tr = time.perf_counter()
+            r = residual.residual_tensor(t, gq, stream=stream.handle)
+            phase["residual_s"] += time.perf_counter() - tr
+            if r["qr"]:
+                nqr += 1
+                pending.setdefault(T, []).append((regions[k], r["prediction"], off, 30, rl, int(imx_off[k])))
+                wbytes[T] = wbytes.get(T, 0) + regions[k].nbytes
+                if wbytes[T] >= qr.BATCH:
+                    flush(T)
+        for T in list(pending):
+            if pending[T]:
+                flush(T)
+        stream.synchronize()
+        dt = time.perf_counter() - t0
+        fb = sum(y.nbytes for y in regions)
+        file_bytes += fb
+        framed.append((fname, mine))
+        out[fname] = {"file_bytes": fb, "qr_tensors": nqr, "device_s": round(dt, 3),
+                      "residual_s": round(phase["residual_s"], 3), "qr_parts_s": round(phase["qr_s"], 3),
+                      "qr_batches": len(mine), "qr_batch_max_s": round(phase.get("qr_max_s", 0.0), 3),
+                      "qr_batch_max_phases": phase.get("qr_max_parts")}
+        log(f"bench: pack cfg4 {fname}: {out[fname]}")
+    tr2 = time.perf_counter()
+    codec = r2.BF16v2(stream=stream.handle)
+    codec.compress(d, r2.layout_of(ts, pos))
+    r2_s = time.perf_counter() - tr2
+    bufs = {fname: [(T, f.result(), items) for (T, f, items) in mine] for fname, mine in framed}
+    total_s = time.perf_counter() - t_all
+    free1, _ = dev.mem_info()
+    pool.shutdown()
+    for fname, bl in bufs.items():
+        out[fname]["coded_bytes"] = sum(len(b) for (_, b, _) in bl)
+        ok = None
+        if bl:
+            T, buf, items = bl[0]
+            back = qr.decode(T, buf, [(p, so, st, c, io) for (_, p, so, st, c, io) in items], d, imx_all,
+                             stream=stream.handle)
+            pos_b, ok = 0, True
+            for (f, _, _, _, _, _) in items:
+                ok &= residual.diff_count(back.view(pos_b, (f.nbytes,), np.uint8), f, stream.handle) == 0
+                pos_b += f.nbytes
+            del back
+        out[fname]["first_batch_round_trip_ok"] = ok
+    res = {"workload": f"cfg4: {len(ts)} matrices ({layers} blocks + token_embd + output), {len(plan)} quant files, "
+                       f"{per_million / 1e4:g}% of each file's blocks perturbed",
+           "bf16_bytes": nb_all, "quant_file_bytes": file_bytes, "base_compress_s": round(r2_s, 3),
+           "pack_s": round(total_s, 3), "pack_GB_s": round((nb_all + file_bytes) / total_s / 1e9, 2),
+           "hbm_used_GB": round((tot - free1) / 1e9, 1), "files": out,
+           "note": "device path with the reference's framing: file reading, hashing, zstd of XOR residuals and the "
+                   "container stay with the host pipeline; HBM in use after the run (base, every file, outputs)"}
+    log(f"bench: pack cfg4 total {res['pack_s']} s, {res['pack_GB_s']} GB/s")
+    del d, made, bufs
+    return res
+
+
 def r2_cfg4(stream, layers=36):
     """R2 BF16 base codec on configuration 4's whole base (every 2-D matrix, 16.4 GB), generated in
     HBM (N(0, 0.02), a counter-based generator per tensor): compress of the resident file and
@@ -252,17 +402,8 @@ def r2_cfg4(stream, layers=36):
     from seedpack_amd import device as dev
     from seedpack_amd import framing, r2, residual
     from seedpack_amd._lib import check, lib
-    mats = cfg4_matrices(layers)
-    pos, ts = 4096, []
-    for name, rows, rl in mats:
-        pos += (-pos) % 32
-        ts.append((name, pos, rows * rl * 2, rl))
-        pos += rows * rl * 2
+    d, ts, pos = cfg4_base(stream, layers)
     layout = r2.layout_of(ts, pos)
-    d = dev.DeviceArray(pos, np.uint8).zero(stream.handle)
-    for k, (name, off, nb, rl) in enumerate(ts):
-        check(lib().spa_synth_normal_bf16(d.ptr + off, nb // 2, 0x5EED0040 + k, 0.02, stream.handle))
-    stream.synchronize()
     nb_all = sum(t[2] for t in ts)
     codec = r2.BF16v2(stream=stream.handle, timing=True)
     warm = r2.layout_of(ts[1:8], ts[7][1] + ts[7][2])          # one block: loads the kernels
@@ -379,12 +520,21 @@ def main():
                     help="two launches of each kernel (K-quants and Q8_0/Q4_0 on token_embd, the configuration-3 "
                          "i-quants on its 4096x12288 tensor) plus a 512 MiB copy, "
                          "for rocprofv3 counter runs; prints the launch list, no JSON line")
+    ap.add_argument("--pack", action="store_true",
+                    help="only configuration 4's pack (all quant files, base codec); prints its result, no JSON line")
+    ap.add_argument("--pack-layers", type=int, default=36, help="transformer blocks of the --pack model")
+    ap.add_argument("--pack-files", default=None, help="comma-separated quant files of --pack (default: all 21)")
     ap.add_argument("--codecs", action="store_true",
                     help="only the coding stages (QR on configurations 1 and 3, the R2 base codec), for rocprofv3 "
                          "kernel-trace runs; prints their results, no JSON line")
     a = ap.parse_args()
     if a.profile_pass:
         return profile_pass()
+    if a.pack:
+        from seedpack_amd import device as dev
+        files = a.pack_files.split(",") if a.pack_files else None
+        print(json.dumps(pack_cfg4(dev.Stream(), layers=a.pack_layers, files=files)))
+        return None
     if a.codecs:
         from seedpack_amd import device as dev
         stream = dev.Stream()

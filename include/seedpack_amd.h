@@ -65,6 +65,12 @@ int spa_copy(void* dst, const void* src, size_t nbytes, void* stream);
 /* n synthetic BF16 weights N(0, std) written in place from a counter-based hash of (seed, index), for
  * benchmark inputs generated on the device. No reference counterpart. */
 int spa_synth_normal_bf16(void* dst, int64_t n, uint64_t seed, float std, void* stream);
+/* No counterpart in the reference: a synthetic "published" quant file for benchmarks. In about
+ * per_million / 10^6 of the nblocks blocks of block_bytes (a counter hash of (seed, block) picks
+ * them), one byte is XORed with a non-zero value, as the reference's configuration 1 perturbs 1% of
+ * its target's blocks. */
+int spa_perturb_blocks(void* dst, int64_t nblocks, int block_bytes, uint32_t per_million, uint64_t seed,
+                       void* stream);
 
 /* ---- quantizers ---- */
 

@@ -42,6 +42,7 @@ SIGNATURES = {
     "spa_mem_info": (c_int, [ctypes.POINTER(c_size_t), ctypes.POINTER(c_size_t)]),
     "spa_copy": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "spa_synth_normal_bf16": (c_int, [c_void_p, c_int64, c_uint64, c_float, c_void_p]),
+    "spa_perturb_blocks": (c_int, [c_void_p, c_int64, c_int, ctypes.c_uint32, c_uint64, c_void_p]),
     "spa_dequantize": (c_int, [c_int, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "spa_row_size": (c_size_t, [c_int, c_int64]),
     "spa_type_variants": (c_int, [c_int]),

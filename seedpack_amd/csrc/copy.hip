@@ -26,6 +26,20 @@ __global__ __launch_bounds__(256) void k_synth_normal_bf16(uint16_t* __restrict_
     }
 }
 
+// Synthetic "published" quant files for benchmarks: in about per_million / 10^6 of the blocks (chosen
+// by the same counter hash of (seed, block)), one byte XORed with a non-zero value.
+__global__ __launch_bounds__(256) void k_perturb_blocks(uint8_t* __restrict__ dst, int64_t nblocks, int bs,
+                                                        uint32_t per_million, uint64_t seed) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblocks; b += stride) {
+        const uint64_t h = splitmix64(seed * 0xD1342543DE82EF95ull + (uint64_t)b);
+        if ((uint32_t)(h % 1000000u) < per_million) {
+            const int64_t at = b * bs + (int64_t)((h >> 20) % (uint64_t)bs);
+            dst[at] ^= (uint8_t)(1 + (h >> 40) % 255u);
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
@@ -49,6 +63,18 @@ extern "C" int spa_synth_normal_bf16(void* dst, int64_t n, uint64_t seed, float 
     if (n == 0) return SPA_OK;
     const int64_t blocks = (n + 255) / 256 < 16384 ? (n + 255) / 256 : 16384;
     hipLaunchKernelGGL(k_synth_normal_bf16, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (uint16_t*)dst, n, seed, std);
+    SPA_HIP_TRY(hipGetLastError());
+    return SPA_OK;
+}
+
+extern "C" int spa_perturb_blocks(void* dst, int64_t nblocks, int block_bytes, uint32_t per_million, uint64_t seed,
+                                  void* stream) {
+    if (nblocks < 0 || block_bytes <= 0 || per_million > 1000000u || (nblocks > 0 && !dst))
+        return spa::fail(SPA_ERR_ARG, "spa_perturb_blocks: bad arguments");
+    if (nblocks == 0) return SPA_OK;
+    const int64_t blocks = (nblocks + 255) / 256 < 16384 ? (nblocks + 255) / 256 : 16384;
+    hipLaunchKernelGGL(k_perturb_blocks, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (uint8_t*)dst,
+                       nblocks, block_bytes, per_million, seed);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }

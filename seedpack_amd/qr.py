@@ -13,6 +13,8 @@ DeviceArrays; seeds are device arrays (BF16 = type 30, F32 = 0, F16 = 1).
 """
 import ctypes
 import struct
+import threading
+import time
 
 import numpy as np
 
@@ -131,12 +133,33 @@ def load_tables(buf):
     return freq, used
 
 
-def _gather(arrs, stream=None):
-    """host or device uint8 arrays -> one device array, each copied to its place"""
+_WS = threading.local()
+
+
+def _workspace(name, nbytes):
+    """a device buffer of at least nbytes kept for this thread and device between encode_parts calls
+    (each call has finished its device work when it returns: the stream is read back). Allocating and
+    freeing several hundred MB per batch instead stalled for seconds now and then when much of the
+    device memory was in use."""
+    cache = getattr(_WS, "bufs", None)
+    if cache is None:
+        cache = _WS.bufs = {}
+    key = (dev.current_device(), name)
+    a = cache.get(key)
+    if a is None or a.nbytes < nbytes:
+        cache.pop(key, None)
+        a = None
+        a = cache[key] = dev.DeviceArray(max(1, nbytes + nbytes // 4), np.uint8)
+    return a.view(0, (max(1, nbytes),), np.uint8)
+
+
+def _gather(arrs, stream=None, workspace=None):
+    """host or device uint8 arrays -> one device array, each copied to its place (into the named
+    workspace buffer when given)"""
     if len(arrs) == 1 and isinstance(arrs[0], dev.DeviceArray):
         return arrs[0]
     n = sum(a.nbytes if isinstance(a, dev.DeviceArray) else len(a) for a in arrs)
-    out = dev.DeviceArray(max(n, 1), np.uint8)
+    out = _workspace(workspace, n) if workspace else dev.DeviceArray(max(n, 1), np.uint8)
     o = 0
     for a in arrs:
         if isinstance(a, dev.DeviceArray):
@@ -185,25 +208,34 @@ def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
     _check_type(T)
     mv = MODEL if mv is None else mv
     bs = BS[T]
+    clock = [time.perf_counter()]
+
+    def lap():
+        clock.append(time.perf_counter())
     tm, sg, nb = _descriptors(T, [_nbytes(it[0]) // bs for it in items], [it[2:] for it in items])
-    F = _gather([it[0] for it in items], stream)
-    P = _gather([it[1] for it in items], stream)
+    F = _gather([it[0] for it in items], stream, "F")
+    P = _gather([it[1] for it in items], stream, "P")
     nseg = len(sg)
     tm_d = dev.DeviceArray.from_host(tm.view(np.uint8), stream)
     sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if nseg else np.zeros(16, np.uint8), stream)
     counts = dev.DeviceArray((NTAB2, 256), np.uint32).zero(stream)
     imx = None if imx_dev is None else imx_dev.ptr
     gk = _gk_ptr(T)
+    lap()
     check(lib().spa_qr_hist(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, counts.ptr, gk, imx, mv, stream))
     counts_h = counts.to_host(stream=stream)
+    lap()
     freq, used = normalize(counts_h)
     remap = np.full(NTAB2, -1, np.int32)
     remap[used] = np.arange(len(used), dtype=np.int32)
     cum = cum_of(freq)
     remap_d, freq_d, cum_d = (dev.DeviceArray.from_host(a, stream) for a in (remap, freq, cum))
     cap = seg_blocks(T) * (3 * BS[T] if T in GRID_TYPES else (QK[T] + NSB_MAX) * 2) + 1024
+    lap()
+    tries = 0
     for _ in range(3):
-        out = dev.DeviceArray(max(1, nseg * cap), np.uint8)
+        tries += 1
+        out = _workspace("out", nseg * cap)
         out_len = dev.DeviceArray(max(1, nseg), np.uint32).zero(stream)
         check(lib().spa_qr_encode(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr, freq_d.ptr,
                                   cum_d.ptr, out.ptr, cap, out_len.ptr, gk, imx, mv, stream))
@@ -213,6 +245,7 @@ def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
         cap *= 2                                 # an overflowing segment: retry with twice the room
     else:
         raise RuntimeError("QR segment overflow")
+    lap()
     offs = np.zeros(nseg + 1, np.uint64)
     offs[1:] = np.cumsum(lens.astype(np.uint64))
     total = int(offs[-1])
@@ -220,17 +253,28 @@ def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
     offs_d = dev.DeviceArray.from_host(offs, stream)
     check(lib().spa_qr_gather(out.ptr, cap, out_len.ptr, offs_d.ptr, nseg, dst.ptr, stream))
     data = dst.to_host(stream=stream)[:total]
-    return {"counts": counts_h, "freq": freq, "used": used, "lens": lens.astype(np.uint32), "stream": data, "mv": mv}
+    lap()
+    ph = np.diff(clock)
+    return {"counts": counts_h, "freq": freq, "used": used, "lens": lens.astype(np.uint32), "stream": data, "mv": mv,
+            "seconds": {"setup": ph[0], "hist": ph[1], "tables": ph[2], "encode": ph[3], "gather": ph[4]},
+            "tries": tries}
 
 
-def encode(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
-    """one coded batch (qr.py:1007-1061) -> bytes"""
-    p = encode_parts(T, items, seed_dev, imx_dev, mv, stream)
+def frame(p):
+    """the framed batch of encode_parts' result: zstd-19 tables and lengths, the stream, the model
+    version (qr.py:1055-1061). Host work only (zstd releases the interpreter), so callers may run it
+    on worker threads while the device codes the next batch, as the reference's pool does
+    (repo3.py:946-979)."""
     out = {"t": store_tables(p["freq"], p["used"]), "l": zstd.compress(p["lens"].astype(np.uint32).tobytes(), 19),
            "s": p["stream"].tobytes()}
     if p["mv"] != 1:
         out["v"] = bytes([p["mv"]])
     return pack(out)
+
+
+def encode(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
+    """one coded batch (qr.py:1007-1061) -> bytes"""
+    return frame(encode_parts(T, items, seed_dev, imx_dev, mv, stream))
 
 
 def decode_parts(T, freq, used, lens, stream_bytes, items, seed_dev, imx_dev=None, mv=MODEL, stream=None):
