@@ -118,18 +118,24 @@ int spa_iq_table_host(int index, const void** grid, int* grid_bytes, const int32
 /* Blocks per rANS segment of a type: max(16, 16384 / QK) (qr.py:952-954); 0 if not a QR type. */
 int spa_qr_seg_blocks(int ggml_type);
 
-/* Symbol histogram of the batch into counts[294][256] (u32, accumulated: zero it first).
- * Replaces the qr_hist kernel (qr.py:674-710). */
+/* Device workspace bytes spa_qr_hist and spa_qr_encode need for nseg segments of the type: per
+ * block slot its equality flag and a list entry (about 5 bytes per block). */
+size_t spa_qr_work_bytes(int ggml_type, int nseg);
+
+/* Symbol histogram of the batch into counts[294][256] (u32, accumulated: zero it first). work:
+ * spa_qr_work_bytes of device scratch, used by this call only. Replaces the qr_hist kernel
+ * (qr.py:674-710). */
 int spa_qr_hist(int ggml_type, const void* F, const void* P, const void* seed, const void* tm, const void* sg,
-                int nseg, uint32_t* counts, const uint16_t* gk, const float* imx, int mv, void* stream);
+                int nseg, uint32_t* counts, const uint16_t* gk, const float* imx, int mv, void* work, void* stream);
 
 /* rANS-encodes each segment backwards into its own `cap`-byte slot of out (nseg * cap bytes), the
  * stream ending at the slot's end; out_len[s] = bytes used, or 0xFFFFFFFF if the slot overflowed
  * (the caller retries with a larger cap). remap[294] maps a context to its table row (-1 unused),
- * freq[n][256] (u16, rows sum to 4096), cum[n][257]. Replaces qr_enc (qr.py:712-758). */
+ * freq[n][256] (u16, rows sum to 4096), cum[n][257]; work as for spa_qr_hist. Replaces qr_enc
+ * (qr.py:712-758). */
 int spa_qr_encode(int ggml_type, const void* F, const void* P, const void* seed, const void* tm, const void* sg,
                   int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap,
-                  uint32_t* out_len, const uint16_t* gk, const float* imx, int mv, void* stream);
+                  uint32_t* out_len, const uint16_t* gk, const float* imx, int mv, void* work, void* stream);
 
 /* Decodes every segment (stream bytes of segment s start at in + in_off[s]) into F (the batch's
  * blocks). lut[n][4096] from spa_rans_build_lut. Replaces qr_dec (qr.py:760-807). */

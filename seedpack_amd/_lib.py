@@ -50,10 +50,12 @@ SIGNATURES = {
     "spa_iq_table_host": (c_int, [c_int, ctypes.POINTER(c_void_p), ctypes.POINTER(c_int), ctypes.POINTER(c_void_p),
                                   ctypes.POINTER(c_int), ctypes.POINTER(c_void_p), ctypes.POINTER(c_int)]),
     "spa_qr_seg_blocks": (c_int, [c_int]),
+    "spa_qr_work_bytes": (c_size_t, [c_int, c_int]),
     "spa_qr_hist": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
-                            c_void_p, c_int, c_void_p]),
+                            c_void_p, c_int, c_void_p, c_void_p]),
     "spa_qr_encode": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
-                              c_void_p, c_void_p, ctypes.c_uint64, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+                              c_void_p, c_void_p, ctypes.c_uint64, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
+                              c_void_p]),
     "spa_qr_decode": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "spa_qr_gather": (c_int, [c_void_p, ctypes.c_uint64, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),

@@ -6,8 +6,9 @@
 // renormalisation) coded backwards, ending with the 4-byte state; decoding reads forward.
 //
 // Mapping on the MI355X:
-//   * histogram: one lane per block (not per segment), so every block of the batch is modelled in
-//     parallel; counts are integer sums (order-free), aggregated across the wave before each
+//   * histogram: block equality and the flag symbols of all blocks first (qr_flags.h), then one
+//     lane per differing block from the list, so every such block is modelled in parallel with all
+//     lanes busy; counts are integer sums (order-free), aggregated across the wave before each
 //     global atomic (one atomic per distinct counter per wave step);
 //   * encode / decode: one lane per segment -- the coder state is inherently serial within a
 //     segment; the decoder assembles each block in a per-lane LDS slot and stores it whole.
@@ -15,73 +16,59 @@
 
 #include "../../include/seedpack_amd.h"
 #include "launch.h"
+#include "qr_flags.h"
 #include "qr_model.h"
 
 namespace spa {
 namespace qr {
 namespace {
 
-__device__ __forceinline__ void hadd(uint32_t* counts, uint32_t key) {
-    uint64_t pending = __ballot(1);
-    const int lane = __lane_id();
-    while (pending) {
-        const int leader = __ffsll((unsigned long long)pending) - 1;
-        const uint32_t k = __shfl(key, leader);
-        const uint64_t same = __ballot(key == k) & pending;
-        if (lane == leader) atomicAdd(&counts[k], (uint32_t)__popcll(same));
-        pending &= ~same;
-    }
-}
-
-// one lane per block: thread i -> segment i / SEG_BLOCKS, block (i % SEG_BLOCKS) of that segment
+// one lane per differing block of the list (slot = segment * SEG_BLOCKS + block), all lanes of the
+// grid striding over it; the flag symbols were counted with the list
 template <int T>
 __global__ __launch_bounds__(256) void k_qr_hist(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
                                                  const uint8_t* __restrict__ seed, const TM* __restrict__ tm,
-                                                 const SG* __restrict__ sg, int nseg, uint32_t* __restrict__ counts, int mv) {
+                                                 const SG* __restrict__ sg, const uint32_t* __restrict__ list,
+                                                 const uint32_t* __restrict__ nlist, uint32_t* __restrict__ counts, int mv) {
     using Y = Ty<T>;
     constexpr int SEG = SEG_BLOCKS<T>;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t s = gid / SEG;
-    const int j = (int)(gid % SEG);
-    if (s >= nseg) return;
-    const SG g = sg[s];
-    if (j >= g.nb) return;
-    const TM m = tm[g.t];
-    const int64_t b = g.b0 + j;
-    const uint8_t* fb = F + b * Y::BS;
-    const uint8_t* pb = P + b * Y::BS;
-    const bool eq = same_block(fb, pb, Y::BS);
-    const int prev = j > 0 ? (int)same_block(fb - Y::BS, pb - Y::BS, Y::BS) : 1;
-    hadd(counts, (uint32_t)((FLAG + prev) * 256 + (eq ? 1 : 0)));
-    if (eq) return;
-    int tv[Y::NF];
+    const uint32_t n = *nlist;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const uint32_t slot = list[i];
+        const SG g = sg[slot / SEG];
+        const TM m = tm[g.t];
+        const int64_t b = g.b0 + (int)(slot % SEG);
+        const uint8_t* fb = F + b * Y::BS;
+        const uint8_t* pb = P + b * Y::BS;
+        int tv[Y::NF];
 #pragma unroll
-    for (int k = 0; k < Y::NF; ++k) tv[k] = get_field<T>(fb, k);
-    int any = 0;
+        for (int k = 0; k < Y::NF; ++k) tv[k] = get_field<T>(fb, k);
+        int any = 0;
 #pragma unroll
-    for (int k = 0; k < Y::NF; ++k) {
-        const int kd = fkind<T>(k);
-        const int pr = fpred<T>(mv, pb, k, tv[0], Y::NF > 1 ? tv[1] : 0), dlt = tv[k] - pr;
-        if (kd < 2 && (dlt < -127 || dlt > 127)) {
-            hadd(counts, (uint32_t)((kd * 2 + any) * 256 + 128));
-            hadd(counts, (uint32_t)(FESC_LO * 256 + (tv[k] & 255)));
-            hadd(counts, (uint32_t)(FESC_HI * 256 + (tv[k] >> 8)));
-        } else {
-            hadd(counts, (uint32_t)((kd * 2 + any) * 256 + (dlt & 255)));
+        for (int k = 0; k < Y::NF; ++k) {
+            const int kd = fkind<T>(k);
+            const int pr = fpred<T>(mv, pb, k, tv[0], Y::NF > 1 ? tv[1] : 0), dlt = tv[k] - pr;
+            if (kd < 2 && (dlt < -127 || dlt > 127)) {
+                hadd(counts, (uint32_t)((kd * 2 + any) * 256 + 128));
+                hadd(counts, (uint32_t)(FESC_LO * 256 + (tv[k] & 255)));
+                hadd(counts, (uint32_t)(FESC_HI * 256 + (tv[k] >> 8)));
+            } else {
+                hadd(counts, (uint32_t)((kd * 2 + any) * 256 + (dlt & 255)));
+            }
+            any |= dlt != 0;
         }
-        any |= dlt != 0;
-    }
-    const uint8_t* sbase = seed + m.seed_off;
-    const int64_t gw0 = (b - m.blk0) * Y::QK;
-    const int64_t col0 = m.cols > 0 ? gw0 % m.cols : 0;
-    float a = 0.f, c = 0.f;
-    for (int w = 0; w < Y::QK; ++w) {
-        if (w % Y::SUBLEN == 0) wscale<T>(fb, w, a, c);
-        float x, h;
-        seed_val(m.seed_type, sbase, gw0 + w, x, h);
-        int r, sg_, ctx;
-        predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
-        hadd(counts, (uint32_t)(ctx * 256 + ((sg_ * (get_code<T>(fb, w) - r)) & 255)));
+        const uint8_t* sbase = seed + m.seed_off;
+        const int64_t gw0 = (b - m.blk0) * Y::QK;
+        const int64_t col0 = m.cols > 0 ? gw0 % m.cols : 0;
+        float a = 0.f, c = 0.f;
+        for (int w = 0; w < Y::QK; ++w) {
+            if (w % Y::SUBLEN == 0) wscale<T>(fb, w, a, c);
+            float x, h;
+            seed_val(m.seed_type, sbase, gw0 + w, x, h);
+            int r, sg_, ctx;
+            predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
+            hadd(counts, (uint32_t)(ctx * 256 + ((sg_ * (get_code<T>(fb, w) - r)) & 255)));
+        }
     }
 }
 
@@ -109,7 +96,8 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
                                                const uint8_t* __restrict__ seed, const TM* __restrict__ tm,
                                                const SG* __restrict__ sg, int nseg, const int* __restrict__ remap,
                                                const uint16_t* __restrict__ freq, const uint32_t* __restrict__ cum,
-                                               uint8_t* __restrict__ out, uint64_t cap, uint32_t* __restrict__ out_len, int mv) {
+                                               uint8_t* __restrict__ out, uint64_t cap, uint32_t* __restrict__ out_len,
+                                               const uint8_t* __restrict__ neq, int mv) {
     using Y = Ty<T>;
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
@@ -122,8 +110,8 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
     for (int64_t b = g.b0 + g.nb - 1; b >= g.b0; --b) {
         const uint8_t* fb = F + b * Y::BS;
         const uint8_t* pb = P + b * Y::BS;
-        const bool eq = same_block(fb, pb, Y::BS);
-        const int prev = b > g.b0 ? (int)same_block(fb - Y::BS, pb - Y::BS, Y::BS) : 1;
+        const bool eq = !neq[b];
+        const int prev = b > g.b0 ? (neq[b - 1] ? 0 : 1) : 1;
         if (eq) {
             e.put(FLAG + prev, 1);
             if (e.ptr - base < 8) { out_len[s] = 0xffffffffu; return; }
@@ -296,20 +284,29 @@ int dispatch(int T, A&&... args) {
 
 template <int T> struct Hist {
     static int run(const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,
-                   uint32_t* counts, int mv, hipStream_t st) {
+                   uint32_t* counts, int mv, void* work, hipStream_t st) {
         const int64_t n = (int64_t)nseg * SEG_BLOCKS<T>;
-        hipLaunchKernelGGL(k_qr_hist<T>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const uint8_t*)F,
-                           (const uint8_t*)P, (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, counts, mv);
+        const QrWork w = qr_work(work, n);
+        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, counts, st)) return e;
+        // the differing blocks are a small share of the batch in practice: at most 2048 workgroups
+        // stride over the list
+        const int64_t wgs = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
+        hipLaunchKernelGGL(k_qr_hist<T>, dim3((unsigned)wgs), dim3(256), 0, st, (const uint8_t*)F, (const uint8_t*)P,
+                           (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, (const uint32_t*)w.list,
+                           (const uint32_t*)w.nlist, counts, mv);
         SPA_HIP_TRY(hipGetLastError());
         return 0;
     }
 };
 template <int T> struct Encode {
     static int run(const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, const int* remap,
-                   const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, int mv, hipStream_t st) {
+                   const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, int mv, void* work,
+                   hipStream_t st) {
+        const QrWork w = qr_work(work, (int64_t)nseg * SEG_BLOCKS<T>);
+        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, nullptr, st)) return e;
         hipLaunchKernelGGL(k_qr_enc<T>, dim3((unsigned)((nseg + 63) / 64)), dim3(64), 0, st, (const uint8_t*)F,
                            (const uint8_t*)P, (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, remap, freq, cum,
-                           (uint8_t*)out, cap, out_len, mv);
+                           (uint8_t*)out, cap, out_len, (const uint8_t*)w.neq, mv);
         SPA_HIP_TRY(hipGetLastError());
         return 0;
     }
@@ -339,10 +336,10 @@ int check_common(int T, int nseg, int mv, const void* gk) {
 
 // grid types (qr_grid.hip)
 int grid_hist(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, uint32_t* counts,
-              const uint16_t* gk, const float* imx, int mv, hipStream_t st);
+              const uint16_t* gk, const float* imx, int mv, void* work, hipStream_t st);
 int grid_encode(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, const int* remap,
                 const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, const uint16_t* gk,
-                const float* imx, int mv, hipStream_t st);
+                const float* imx, int mv, void* work, hipStream_t st);
 int grid_decode(int T, const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
                 int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F,
                 const uint16_t* gk, const float* imx, int mv, hipStream_t st);
@@ -364,23 +361,32 @@ int spa_qr_seg_blocks(int T) {
     return 0;
 }
 
+size_t spa_qr_work_bytes(int T, int nseg) {
+    const int seg = spa_qr_seg_blocks(T);
+    if (!seg || nseg < 0) return 0;
+    return qr_work_bytes((int64_t)nseg * seg);
+}
+
 int spa_qr_hist(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,
-                uint32_t* counts, const uint16_t* gk, const float* imx, int mv, void* stream) {
+                uint32_t* counts, const uint16_t* gk, const float* imx, int mv, void* work, void* stream) {
     if (int e = check_common(T, nseg, mv, gk)) return e;
     if (nseg == 0) return 0;
-    if (grid_type(T)) return grid_hist(T, F, P, seed, tm, sg, nseg, counts, gk, imx, mv, (hipStream_t)stream);
-    return dispatch<Hist>(T, F, P, seed, tm, sg, nseg, counts, mv, (hipStream_t)stream);
+    if (!work) return spa::fail(SPA_ERR_ARG, "QR: no workspace (spa_qr_work_bytes)");
+    if (grid_type(T)) return grid_hist(T, F, P, seed, tm, sg, nseg, counts, gk, imx, mv, work, (hipStream_t)stream);
+    return dispatch<Hist>(T, F, P, seed, tm, sg, nseg, counts, mv, work, (hipStream_t)stream);
 }
 
 int spa_qr_encode(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,
                   const int* remap, const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len,
-                  const uint16_t* gk, const float* imx, int mv, void* stream) {
+                  const uint16_t* gk, const float* imx, int mv, void* work, void* stream) {
     if (int e = check_common(T, nseg, mv, gk)) return e;
     if (cap < 1024) return spa::fail(SPA_ERR_ARG, "QR: segment capacity %llu too small", (unsigned long long)cap);
     if (nseg == 0) return 0;
+    if (!work) return spa::fail(SPA_ERR_ARG, "QR: no workspace (spa_qr_work_bytes)");
     if (grid_type(T))
-        return grid_encode(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, gk, imx, mv, (hipStream_t)stream);
-    return dispatch<Encode>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, mv, (hipStream_t)stream);
+        return grid_encode(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, gk, imx, mv, work,
+                           (hipStream_t)stream);
+    return dispatch<Encode>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, mv, work, (hipStream_t)stream);
 }
 
 int spa_qr_decode(int T, const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm,

@@ -1,0 +1,122 @@
+// Block equality of a QR batch and the block-flag symbols, shared by the grid and non-grid coders.
+//
+// Most blocks of a file equal their prediction (each costs one flag symbol). Both the histogram and
+// the encoder need, per block, whether it equals its prediction and whether the previous block of its
+// segment did. k_qr_neq computes neq[b] for every block of the batch once, reading F and P as 16-byte
+// words coalesced across the workgroup; k_qr_slots counts the flag symbols of all blocks with
+// wave-aggregated atomics and lists the differing blocks, so that the modelling kernels run only on
+// those (one lane or one wave each, all of them busy).
+#pragma once
+
+#include "launch.h"
+#include "qr_model.h"
+
+namespace spa {
+namespace qr {
+namespace {   // one copy per translation unit (the grid and non-grid coders both launch these)
+
+// counts[key]++ for every active lane: one atomic per distinct key of the wave
+__device__ __forceinline__ void hadd(uint32_t* counts, uint32_t key) {
+    uint64_t pending = __ballot(1);
+    const int lane = __lane_id();
+    while (pending) {
+        const int leader = __ffsll((unsigned long long)pending) - 1;
+        const uint32_t k = __shfl(key, leader);
+        const uint64_t same = __ballot(key == k) & pending;
+        if (lane == leader) atomicAdd(&counts[k], (uint32_t)__popcll(same));
+        pending &= ~same;
+    }
+}
+
+// workspace: neq flags (one byte per block slot), the list length, the list (one u32 slot per block)
+struct QrWork {
+    uint8_t* neq;
+    uint32_t* nlist;
+    uint32_t* list;
+};
+__host__ __device__ inline size_t qr_work_bytes(int64_t slots) {
+    return (size_t)((slots + 255) / 256 * 256) + 256 + (size_t)slots * 4;
+}
+__host__ __device__ inline QrWork qr_work(void* w, int64_t slots) {
+    uint8_t* p = (uint8_t*)w;
+    const size_t a = (size_t)((slots + 255) / 256 * 256);
+    return QrWork{p, (uint32_t*)(p + a), (uint32_t*)(p + a + 256)};
+}
+
+// neq[b] for the batch's blocks b < (last segment's b0 + nb): 256 blocks per workgroup
+__global__ __launch_bounds__(256) void k_qr_neq(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
+                                                const SG* __restrict__ sg, int nseg, int bs, uint8_t* __restrict__ neq) {
+    __shared__ uint8_t fl[256];
+    const SG last = sg[nseg - 1];
+    const int64_t nb = last.b0 + last.nb;
+    const int64_t b0 = (int64_t)blockIdx.x * 256;
+    if (b0 >= nb) return;
+    const int nblk = (int)(nb - b0 < 256 ? nb - b0 : 256);
+    fl[threadIdx.x] = 0;
+    __syncthreads();
+    const uint8_t* f = F + b0 * bs;
+    const uint8_t* p = P + b0 * bs;
+    const int nbytes = nblk * bs;
+    int done = 0;
+    if (((reinterpret_cast<uintptr_t>(f) | reinterpret_cast<uintptr_t>(p)) & 15) == 0) {
+        const int nv = nbytes / 16;
+        for (int i = threadIdx.x; i < nv; i += 256) {
+            const uint4 a = reinterpret_cast<const uint4*>(f)[i], c = reinterpret_cast<const uint4*>(p)[i];
+            const uint32_t x[4] = {a.x ^ c.x, a.y ^ c.y, a.z ^ c.z, a.w ^ c.w};
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                if (x[w])
+                    for (int k = 0; k < 4; ++k)
+                        if ((x[w] >> (8 * k)) & 0xffu) fl[(16 * i + 4 * w + k) / bs] = 1;
+        }
+        done = nv * 16;
+    }
+    for (int o = done + threadIdx.x; o < nbytes; o += 256)
+        if (f[o] != p[o]) fl[o / bs] = 1;
+    __syncthreads();
+    if (threadIdx.x < nblk) neq[b0 + threadIdx.x] = fl[threadIdx.x];
+}
+
+// the flag symbol of every slot (segment s, block j) into counts; differing slots s * seg + j into list
+__global__ __launch_bounds__(256) void k_qr_slots(const SG* __restrict__ sg, int nseg, int seg,
+                                                  const uint8_t* __restrict__ neq, uint32_t* __restrict__ counts,
+                                                  uint32_t* __restrict__ list, uint32_t* __restrict__ nlist) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t s = gid / seg;
+    const int j = (int)(gid % seg);
+    if (s >= nseg) return;
+    const SG g = sg[s];
+    if (j >= g.nb) return;
+    const int64_t b = g.b0 + j;
+    const int eq = neq[b] ? 0 : 1;
+    const int prev = j > 0 ? (neq[b - 1] ? 0 : 1) : 1;
+    hadd(counts, (uint32_t)((FLAG + prev) * 256 + eq));
+    const uint64_t m = __ballot(!eq);
+    if (m) {
+        const int lane = __lane_id();
+        const int leader = __ffsll((unsigned long long)m) - 1;
+        uint32_t at = 0;
+        if (lane == leader) at = atomicAdd(nlist, (uint32_t)__popcll(m));
+        at = __shfl(at, leader);
+        if (!eq) list[at + __popcll(m & ((1ull << lane) - 1))] = (uint32_t)gid;
+    }
+}
+
+// neq flags, then (hist only) the flag counts and the list of differing slots
+inline int qr_flags(const void* F, const void* P, const void* sg, int nseg, int seg, int bs, QrWork w, uint32_t* counts,
+                    hipStream_t st) {
+    const int64_t slots = (int64_t)nseg * seg;
+    hipLaunchKernelGGL(k_qr_neq, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, st, (const uint8_t*)F,
+                       (const uint8_t*)P, (const SG*)sg, nseg, bs, w.neq);
+    if (counts) {
+        SPA_HIP_TRY(hipMemsetAsync(w.nlist, 0, sizeof(uint32_t), st));
+        hipLaunchKernelGGL(k_qr_slots, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, st, (const SG*)sg, nseg, seg,
+                           (const uint8_t*)w.neq, counts, w.list, w.nlist);
+    }
+    SPA_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+}  // namespace
+}  // namespace qr
+}  // namespace spa

@@ -8,7 +8,8 @@
 // from the gap between the two nearest distances (rank >= 16 escapes to the index's two bytes);
 // then each sign against the seed's sign (context: level 0 or not, |u|); IQ1_M adds its shift bit.
 //
-// Mapping on the MI355X: one wavefront per rANS segment (encode, decode) or per block (histogram).
+// Mapping on the MI355X: one wavefront per rANS segment (encode, decode) or per differing block
+// (histogram; the flag symbols of all blocks and the list of differing ones come from qr_flags.h).
 // Every lane runs the same symbol sequence with the same coder state -- the coder is serial by
 // nature -- while the lattice scan, the only heavy part (256 to 2048 points per group), is split
 // over the 64 lanes: lane l owns points l, l+64, ...; their keys stay in registers for the whole
@@ -19,6 +20,7 @@
 // wavefront, so a workgroup barrier orders the pair table's writes and reads within the wave.
 #include "../../include/seedpack_amd.h"
 #include "launch.h"
+#include "qr_flags.h"
 #include "qr_model.h"
 
 namespace spa {
@@ -263,18 +265,6 @@ __device__ __forceinline__ int sign_ctx(const Unit& g, const uint16_t* gk, const
     return (lev == 0) * 8 + (m4 < 7.f ? (int)m4 : 7);
 }
 
-// the whole wave: is the block equal to its prediction
-template <int BS>
-__device__ __forceinline__ bool wave_same(const uint8_t* a, const uint8_t* b, int lane) {
-    bool eq = true;
-#pragma unroll
-    for (int i = 0; i < (BS + 63) / 64; ++i) {
-        const int j = lane + 64 * i;
-        if (j < BS) eq = eq && a[j] == b[j];
-    }
-    return __all(eq);
-}
-
 // symbol sinks of the encoder's model walk: count (histogram) or code (rANS, backwards)
 struct Count {
     uint32_t* counts;
@@ -365,51 +355,49 @@ __device__ __forceinline__ void load_keys(const uint16_t* gk, int lane, uint32_t
     for (int i = 0; i < G<T>::PER; ++i) keys[i] = gk[lane + 64 * i];
 }
 
-// one wavefront per block: thread group b -> segment b / 64, block b % 64 of it
+// one wavefront per differing block of the list (slot = segment * SEG_BLOCKS + block), the grid's
+// waves striding over it; the flag symbols were counted with the list
 template <int T>
 __global__ __launch_bounds__(64) void k_qrg_hist(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
                                                  const uint8_t* __restrict__ seed, const TM* __restrict__ tm,
-                                                 const SG* __restrict__ sg, int nseg, uint32_t* __restrict__ counts,
+                                                 const SG* __restrict__ sg, const uint32_t* __restrict__ list,
+                                                 const uint32_t* __restrict__ nlist, uint32_t* __restrict__ counts,
                                                  const uint16_t* __restrict__ gk, const float* __restrict__ imx, int mv) {
     using Y = Ty<T>;
     constexpr int SEG = SEG_BLOCKS<T>;
     const int lane = threadIdx.x;
-    const int64_t s = blockIdx.x / SEG;
-    const int j = (int)(blockIdx.x % SEG);
-    if (s >= nseg) return;
-    const SG g = sg[s];
-    if (j >= g.nb) return;
-    const TM m = tm[g.t];
-    const int64_t b = g.b0 + j;
-    const uint8_t* fb = F + b * Y::BS;
-    const uint8_t* pb = P + b * Y::BS;
-    Count out{counts, lane};
-    const bool eq = wave_same<Y::BS>(fb, pb, lane);
-    const int prev = j > 0 ? (int)wave_same<Y::BS>(fb - Y::BS, pb - Y::BS, lane) : 1;
-    out.put(FLAG + prev, eq ? 1u : 0u);
-    if (eq) return;
-    int tv[Y::NF];
-#pragma unroll
-    for (int k = 0; k < Y::NF; ++k) tv[k] = get_field<T>(fb, k);
-    int any = 0;
-#pragma unroll
-    for (int k = 0; k < Y::NF; ++k) {
-        const int kd = fkind<T>(k), dlt = tv[k] - fpred<T>(mv, pb, k, tv[0], tv[1]);
-        if (kd < 2 && (dlt < -127 || dlt > 127)) {
-            out.put(kd * 2 + any, 128);
-            out.put(FESC_LO, (uint32_t)(tv[k] & 255));
-            out.put(FESC_HI, (uint32_t)(tv[k] >> 8));
-        } else {
-            out.put(kd * 2 + any, (uint32_t)(dlt & 255));
-        }
-        any |= dlt != 0;
-    }
     __shared__ float tab[TAB_N<T>];
     uint32_t keys[G<T>::PER];
     load_keys<T>(gk, lane, keys);
-    const float* im = (m.imx_off >= 0 && m.cols > 0) ? imx + m.imx_off : nullptr;
-    grid_walk<T>(out, [](Count&) { return false; }, fb, pb, gk, keys, tab, lane, m.seed_type, seed + m.seed_off,
-                 (b - m.blk0) * Y::QK, m.cols, im, mv);
+    const uint32_t n = *nlist;
+    for (uint32_t i = blockIdx.x; i < n; i += gridDim.x) {
+        const uint32_t slot = list[i];
+        const SG g = sg[slot / SEG];
+        const TM m = tm[g.t];
+        const int64_t b = g.b0 + (int)(slot % SEG);
+        const uint8_t* fb = F + b * Y::BS;
+        const uint8_t* pb = P + b * Y::BS;
+        Count out{counts, lane};
+        int tv[Y::NF];
+#pragma unroll
+        for (int k = 0; k < Y::NF; ++k) tv[k] = get_field<T>(fb, k);
+        int any = 0;
+#pragma unroll
+        for (int k = 0; k < Y::NF; ++k) {
+            const int kd = fkind<T>(k), dlt = tv[k] - fpred<T>(mv, pb, k, tv[0], tv[1]);
+            if (kd < 2 && (dlt < -127 || dlt > 127)) {
+                out.put(kd * 2 + any, 128);
+                out.put(FESC_LO, (uint32_t)(tv[k] & 255));
+                out.put(FESC_HI, (uint32_t)(tv[k] >> 8));
+            } else {
+                out.put(kd * 2 + any, (uint32_t)(dlt & 255));
+            }
+            any |= dlt != 0;
+        }
+        const float* im = (m.imx_off >= 0 && m.cols > 0) ? imx + m.imx_off : nullptr;
+        grid_walk<T>(out, [](Count&) { return false; }, fb, pb, gk, keys, tab, lane, m.seed_type, seed + m.seed_off,
+                     (b - m.blk0) * Y::QK, m.cols, im, mv);
+    }
 }
 
 // room kept below the coder's write pointer for one more unit, the block's fields and its flag
@@ -421,7 +409,8 @@ __global__ __launch_bounds__(64) void k_qrg_enc(const uint8_t* __restrict__ F, c
                                                 const SG* __restrict__ sg, int nseg, const int* __restrict__ remap,
                                                 const uint16_t* __restrict__ freq, const uint32_t* __restrict__ cum,
                                                 uint8_t* __restrict__ out, uint64_t cap, uint32_t* __restrict__ out_len,
-                                                const uint16_t* __restrict__ gk, const float* __restrict__ imx, int mv) {
+                                                const uint16_t* __restrict__ gk, const float* __restrict__ imx,
+                                                const uint8_t* __restrict__ neq, int mv) {
     using Y = Ty<T>;
     const int lane = threadIdx.x;
     const int s = blockIdx.x;
@@ -440,8 +429,8 @@ __global__ __launch_bounds__(64) void k_qrg_enc(const uint8_t* __restrict__ F, c
     for (int64_t b = g.b0 + g.nb - 1; b >= g.b0; --b) {
         const uint8_t* fb = F + b * Y::BS;
         const uint8_t* pb = P + b * Y::BS;
-        const bool eq = wave_same<Y::BS>(fb, pb, lane);
-        const int prev = b > g.b0 ? (int)wave_same<Y::BS>(fb - Y::BS, pb - Y::BS, lane) : 1;
+        const bool eq = !neq[b];
+        const int prev = b > g.b0 ? (neq[b - 1] ? 0 : 1) : 1;
         if (eq) {
             e.put(FLAG + prev, 1);
             if (stop(e)) { if (lane == 0) out_len[s] = 0xffffffffu; return; }
@@ -654,10 +643,15 @@ int dispatch_grid(int T, A&&... args) {
 
 template <int T> struct GHist {
     static int run(const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, uint32_t* counts,
-                   const uint16_t* gk, const float* imx, int mv, hipStream_t st) {
+                   const uint16_t* gk, const float* imx, int mv, void* work, hipStream_t st) {
         const int64_t n = (int64_t)nseg * SEG_BLOCKS<T>;
-        hipLaunchKernelGGL(k_qrg_hist<T>, dim3((unsigned)n), dim3(64), 0, st, (const uint8_t*)F, (const uint8_t*)P,
-                           (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, counts, gk, imx, mv);
+        const QrWork w = qr_work(work, n);
+        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, counts, st)) return e;
+        // one wave per differing block; at most 16384 waves stride over the list
+        const int64_t waves = n < 16384 ? n : 16384;
+        hipLaunchKernelGGL(k_qrg_hist<T>, dim3((unsigned)waves), dim3(64), 0, st, (const uint8_t*)F, (const uint8_t*)P,
+                           (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, (const uint32_t*)w.list,
+                           (const uint32_t*)w.nlist, counts, gk, imx, mv);
         SPA_HIP_TRY(hipGetLastError());
         return 0;
     }
@@ -665,10 +659,12 @@ template <int T> struct GHist {
 template <int T> struct GEnc {
     static int run(const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, const int* remap,
                    const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, const uint16_t* gk,
-                   const float* imx, int mv, hipStream_t st) {
+                   const float* imx, int mv, void* work, hipStream_t st) {
+        const QrWork w = qr_work(work, (int64_t)nseg * SEG_BLOCKS<T>);
+        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, nullptr, st)) return e;
         hipLaunchKernelGGL(k_qrg_enc<T>, dim3((unsigned)nseg), dim3(64), 0, st, (const uint8_t*)F, (const uint8_t*)P,
                            (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, remap, freq, cum, (uint8_t*)out, cap,
-                           out_len, gk, imx, mv);
+                           out_len, gk, imx, (const uint8_t*)w.neq, mv);
         SPA_HIP_TRY(hipGetLastError());
         return 0;
     }
@@ -688,13 +684,13 @@ template <int T> struct GDec {
 }  // namespace
 
 int grid_hist(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, uint32_t* counts,
-              const uint16_t* gk, const float* imx, int mv, hipStream_t st) {
-    return dispatch_grid<GHist>(T, F, P, seed, tm, sg, nseg, counts, gk, imx, mv, st);
+              const uint16_t* gk, const float* imx, int mv, void* work, hipStream_t st) {
+    return dispatch_grid<GHist>(T, F, P, seed, tm, sg, nseg, counts, gk, imx, mv, work, st);
 }
 int grid_encode(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, const int* remap,
                 const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, const uint16_t* gk,
-                const float* imx, int mv, hipStream_t st) {
-    return dispatch_grid<GEnc>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, gk, imx, mv, st);
+                const float* imx, int mv, void* work, hipStream_t st) {
+    return dispatch_grid<GEnc>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, gk, imx, mv, work, st);
 }
 int grid_decode(int T, const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
                 int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F,

@@ -389,11 +389,5 @@ __device__ __forceinline__ void predict(float a, float c, const uint8_t* pb, int
     if (mv >= 2 && hu == 0.f) ctx = CODE2 + p8 * 16 + min(15, (int)(fabsf(fr) * 32.f));
 }
 
-__device__ __forceinline__ bool same_block(const uint8_t* a, const uint8_t* b, int n) {
-    for (int i = 0; i < n; ++i)
-        if (a[i] != b[i]) return false;
-    return true;
-}
-
 }  // namespace qr
 }  // namespace spa

@@ -222,7 +222,9 @@ def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
     imx = None if imx_dev is None else imx_dev.ptr
     gk = _gk_ptr(T)
     lap()
-    check(lib().spa_qr_hist(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, counts.ptr, gk, imx, mv, stream))
+    work = _workspace("work", lib().spa_qr_work_bytes(T, nseg))
+    check(lib().spa_qr_hist(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, counts.ptr, gk, imx, mv, work.ptr,
+                            stream))
     counts_h = counts.to_host(stream=stream)
     lap()
     freq, used = normalize(counts_h)
@@ -238,7 +240,7 @@ def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
         out = _workspace("out", nseg * cap)
         out_len = dev.DeviceArray(max(1, nseg), np.uint32).zero(stream)
         check(lib().spa_qr_encode(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr, freq_d.ptr,
-                                  cum_d.ptr, out.ptr, cap, out_len.ptr, gk, imx, mv, stream))
+                                  cum_d.ptr, out.ptr, cap, out_len.ptr, gk, imx, mv, work.ptr, stream))
         lens = out_len.to_host(stream=stream)[:nseg]
         if not (lens == 0xFFFFFFFF).any():
             break
