@@ -13,10 +13,12 @@ same JSON line.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
 import argparse
+import collections
 import concurrent.futures
 import json
 import os
 import sys
+import threading
 import time
 
 import numpy as np
@@ -275,11 +277,13 @@ def pack_cfg4(stream, layers=36, per_million=10000, files=None):
     """configuration 4's pack on the device. The BF16 base and one LogNormal(0, 1) imatrix per tensor
     are resident in HBM, and so are the quant files (every 2-D matrix in one type), made untimed by
     this library's quantizer with per_million / 10^6 of their blocks perturbed (one byte each). Then,
-    timed as one run: per file, every tensor is regrown and compared (residual.residual_tensor:
-    prediction, differing-byte count, the candidate variants) and the QR tensors are coded in batches
-    of about 384 MB (qr.encode_parts on the device, its zstd-19 framing on 8 worker threads beside the
-    device work, as the reference's pool does); then the base codec compresses the base. pack GB/s =
-    (BF16 bytes + quant file bytes) / that run's wall time. Each file's first batch is decoded again and
+    timed as one run: per file, every tensor is regrown and compared (residual.residual_window over
+    windows of about 384 MB: predictions, differing-byte counts read back once per window, the
+    candidate variants) on the main stream, while two coder threads code the QR tensors in batches of
+    about 384 MB, each on its own stream (qr.encode_parts; the zstd-19 framing on 8 more threads), as
+    the reference's pool codes batches beside the prediction (repo3.py:946-979), and one more thread
+    compresses the base with the base codec. pack GB/s = (BF16
+    bytes + quant file bytes) / that run's wall time. Each file's first batch is decoded again and
     compared afterwards, untimed."""
     from seedpack_amd import device as dev
     from seedpack_amd import qr, r2, residual
@@ -313,61 +317,84 @@ def pack_cfg4(stream, layers=36, per_million=10000, files=None):
         made.append((fname, types, regions))
     stream.synchronize()
     log(f"bench: pack cfg4: {len(made)} files made")
-    pool = concurrent.futures.ThreadPoolExecutor(8)
-    out, framed, file_bytes = {}, [], 0
+    pool = concurrent.futures.ThreadPoolExecutor(8)      # zstd-19 framing of the coded batches
+    coder = concurrent.futures.ThreadPoolExecutor(2)     # QR batches, each worker on its own stream
+    side = concurrent.futures.ThreadPoolExecutor(1)      # the base codec, on its own streams
+    tls = threading.local()
+
+    def qr_batch(T, items):
+        if not hasattr(tls, "stream"):
+            tls.stream = dev.Stream()
+        tq = time.perf_counter()
+        parts = qr.encode_parts(T, items, d, imx_all, stream=tls.stream.handle)
+        return pool.submit(qr.frame, parts), time.perf_counter() - tq
+
+    def base_codec():
+        s2 = dev.Stream()
+        tb = time.perf_counter()
+        r2.BF16v2(stream=s2.handle).compress(d, r2.layout_of(ts, pos))
+        s2.synchronize()
+        return time.perf_counter() - tb
+
+    out, framed, file_bytes, inflight = {}, [], 0, collections.deque()
     t_all = time.perf_counter()
+    r2_future = side.submit(base_codec)
     for fname, types, regions in made:
         t0 = time.perf_counter()
         pending, wbytes, nqr = {}, {}, 0
-        phase = {"residual_s": 0.0, "qr_s": 0.0}
+        phase = {"residual_s": 0.0}
         mine = []
 
         def flush(T):
-            tq = time.perf_counter()
-            parts = qr.encode_parts(T, pending[T], d, imx_all, stream=stream.handle)
-            tq = time.perf_counter() - tq
-            phase["qr_s"] += tq
-            if tq > phase.get("qr_max_s", 0.0):
-                phase["qr_max_s"] = tq
-                phase["qr_max_parts"] = {k: round(v, 3) for k, v in parts["seconds"].items()}
-                phase["qr_max_parts"]["tries"] = parts["tries"]
+            # at most 8 batches queued for the coder (their predictions stay alive until coded)
+            while len(inflight) >= 8:
+                inflight.popleft().result()
+            f = coder.submit(qr_batch, T, pending[T])
+            inflight.append(f)
             # only each file's first batch keeps its tensors (for the check after the run)
-            mine.append((T, pool.submit(qr.frame, parts), list(pending[T]) if not mine else None))
+            mine.append((T, f, list(pending[T]) if not mine else None))
             pending[T], wbytes[T] = [], 0
 
+        window, wb = [], 0
         for k, (name, off, nb, rl) in enumerate(ts):
-            T = types[k]
-            t = residual.Tensor(name, T, rl, regions[k], base_k[k], imatrix=imx_k[k])
+            window.append(k)
+            wb += regions[k].nbytes
+            if wb < qr.BATCH and k + 1 < len(ts):
+                continue
+            # a window of about one coding batch: first predictions and counts queued back to back
             tr = time.perf_counter()
-            r = residual.residual_tensor(t, gq, stream=stream.handle)
+            res = residual.residual_window([residual.Tensor(ts[i][0], types[i], ts[i][3], regions[i], base_k[i],
+                                                            imatrix=imx_k[i]) for i in window], gq, stream=stream.handle)
             phase["residual_s"] += time.perf_counter() - tr
-            if r["qr"]:
-                nqr += 1
-                pending.setdefault(T, []).append((regions[k], r["prediction"], off, 30, rl, int(imx_off[k])))
-                wbytes[T] = wbytes.get(T, 0) + regions[k].nbytes
-                if wbytes[T] >= qr.BATCH:
-                    flush(T)
+            for i, r in zip(window, res):
+                if r["qr"]:
+                    T = types[i]
+                    nqr += 1
+                    pending.setdefault(T, []).append((regions[i], r["prediction"], ts[i][1], 30, ts[i][3], int(imx_off[i])))
+                    wbytes[T] = wbytes.get(T, 0) + regions[i].nbytes
+                    if wbytes[T] >= qr.BATCH:
+                        flush(T)
+            window, wb = [], 0
         for T in list(pending):
             if pending[T]:
                 flush(T)
-        stream.synchronize()
         dt = time.perf_counter() - t0
         fb = sum(y.nbytes for y in regions)
         file_bytes += fb
         framed.append((fname, mine))
-        out[fname] = {"file_bytes": fb, "qr_tensors": nqr, "device_s": round(dt, 3),
-                      "residual_s": round(phase["residual_s"], 3), "qr_parts_s": round(phase["qr_s"], 3),
-                      "qr_batches": len(mine), "qr_batch_max_s": round(phase.get("qr_max_s", 0.0), 3),
-                      "qr_batch_max_phases": phase.get("qr_max_parts")}
+        out[fname] = {"file_bytes": fb, "qr_tensors": nqr, "qr_batches": len(mine), "regrow_s": round(dt, 3),
+                      "residual_s": round(phase["residual_s"], 3)}
         log(f"bench: pack cfg4 {fname}: {out[fname]}")
-    tr2 = time.perf_counter()
-    codec = r2.BF16v2(stream=stream.handle)
-    codec.compress(d, r2.layout_of(ts, pos))
-    r2_s = time.perf_counter() - tr2
-    bufs = {fname: [(T, f.result(), items) for (T, f, items) in mine] for fname, mine in framed}
+    bufs = {}
+    for fname, mine in framed:
+        coded = [(T, f.result(), items) for (T, f, items) in mine]
+        out[fname]["qr_parts_s"] = round(sum(dt for (_, (_, dt), _) in coded), 3)
+        bufs[fname] = [(T, ff.result(), items) for (T, (ff, _), items) in coded]
+    r2_s = r2_future.result()
     total_s = time.perf_counter() - t_all
     free1, _ = dev.mem_info()
-    pool.shutdown()
+    for ex in (pool, coder, side):
+        ex.shutdown()
     for fname, bl in bufs.items():
         out[fname]["coded_bytes"] = sum(len(b) for (_, b, _) in bl)
         ok = None

@@ -153,6 +153,15 @@ def _workspace(name, nbytes):
     return a.view(0, (max(1, nbytes),), np.uint8)
 
 
+def _put(name, a, stream=None):
+    """a host array copied into the named workspace buffer (typed view)"""
+    a = np.ascontiguousarray(a)
+    w = _workspace(name, a.nbytes)
+    if a.nbytes:
+        check(lib().spa_memcpy_h2d(w.ptr, a.ctypes.data, a.nbytes, stream))
+    return w.view(0, a.shape, a.dtype) if a.nbytes else w
+
+
 def _gather(arrs, stream=None, workspace=None):
     """host or device uint8 arrays -> one device array, each copied to its place (into the named
     workspace buffer when given)"""
@@ -216,9 +225,11 @@ def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
     F = _gather([it[0] for it in items], stream, "F")
     P = _gather([it[1] for it in items], stream, "P")
     nseg = len(sg)
-    tm_d = dev.DeviceArray.from_host(tm.view(np.uint8), stream)
-    sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if nseg else np.zeros(16, np.uint8), stream)
-    counts = dev.DeviceArray((NTAB2, 256), np.uint32).zero(stream)
+    # every device buffer of the call is a workspace kept for the thread: no frees, which would wait
+    # for the whole device (work other threads queued on other streams included)
+    tm_d = _put("tm", tm.view(np.uint8), stream)
+    sg_d = _put("sg", sg.view(np.uint8) if nseg else np.zeros(16, np.uint8), stream)
+    counts = _workspace("counts", NTAB2 * 256 * 4).view(0, (NTAB2, 256), np.uint32).zero(stream)
     imx = None if imx_dev is None else imx_dev.ptr
     gk = _gk_ptr(T)
     lap()
@@ -231,14 +242,14 @@ def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
     remap = np.full(NTAB2, -1, np.int32)
     remap[used] = np.arange(len(used), dtype=np.int32)
     cum = cum_of(freq)
-    remap_d, freq_d, cum_d = (dev.DeviceArray.from_host(a, stream) for a in (remap, freq, cum))
+    remap_d, freq_d, cum_d = (_put(n, a, stream) for n, a in (("remap", remap), ("freq", freq), ("cum", cum)))
     cap = seg_blocks(T) * (3 * BS[T] if T in GRID_TYPES else (QK[T] + NSB_MAX) * 2) + 1024
     lap()
     tries = 0
     for _ in range(3):
         tries += 1
         out = _workspace("out", nseg * cap)
-        out_len = dev.DeviceArray(max(1, nseg), np.uint32).zero(stream)
+        out_len = _workspace("out_len", 4 * max(1, nseg)).view(0, (max(1, nseg),), np.uint32).zero(stream)
         check(lib().spa_qr_encode(T, F.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr, freq_d.ptr,
                                   cum_d.ptr, out.ptr, cap, out_len.ptr, gk, imx, mv, work.ptr, stream))
         lens = out_len.to_host(stream=stream)[:nseg]
@@ -251,10 +262,10 @@ def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
     offs = np.zeros(nseg + 1, np.uint64)
     offs[1:] = np.cumsum(lens.astype(np.uint64))
     total = int(offs[-1])
-    dst = dev.DeviceArray(max(1, total), np.uint8)
-    offs_d = dev.DeviceArray.from_host(offs, stream)
+    dst = _workspace("dst", max(1, total))
+    offs_d = _put("offs", offs, stream)
     check(lib().spa_qr_gather(out.ptr, cap, out_len.ptr, offs_d.ptr, nseg, dst.ptr, stream))
-    data = dst.to_host(stream=stream)[:total]
+    data = dst.to_host(stream=stream)[:total].copy()
     lap()
     ph = np.diff(clock)
     return {"counts": counts_h, "freq": freq, "used": used, "lens": lens.astype(np.uint32), "stream": data, "mv": mv,

@@ -14,6 +14,8 @@ come back to the host, which makes the same decisions as the reference:
   * a QR-coded tensor keeps its file bytes and best prediction for the QR coder; an XOR tensor
     keeps file ^ prediction in place; an exact prediction leaves an all-zero XOR residual.
 """
+import threading
+
 import numpy as np
 
 from . import device as dev
@@ -70,11 +72,22 @@ def split_variant(v):
     return k, (k == 0 and u >= UNIT_W), u % UNIT_W
 
 
+_TLS = threading.local()
+
+
 class _Count:
-    """a device u64 counter and its read-back"""
+    """a device u64 counter and its read-back. One counter per thread and device, reused: each use
+    ends with the read-back, and freeing a device allocation waits for the whole device (work other
+    threads queued on other streams included)."""
 
     def __init__(self):
-        self.d = dev.DeviceArray(1, np.uint64)
+        cache = getattr(_TLS, "counters", None)
+        if cache is None:
+            cache = _TLS.counters = {}
+        key = dev.current_device()
+        if key not in cache:
+            cache[key] = dev.DeviceArray(1, np.uint64)
+        self.d = cache[key]
 
     def value(self, stream=None):
         return int(self.d.to_host(stream=stream)[0])
@@ -130,21 +143,24 @@ def predict(gq, t, v, stream=None):
     return gq.quantize_tensors(t.type, [(t.base, t.cols)], [imx], code_variant, device=True)[0]
 
 
-def residual_tensor(t, gq=None, fitted_set=0, use_qr=True, stream=None):
-    """the residual of one tensor (the per-tensor decisions of repo3.py:1071-1188) ->
-    dict(kind, variant, nonzero, qr, prediction). t.region ends as: the file bytes (QR tensors,
-    coded against `prediction`), file ^ prediction (XOR tensors) or zeros (exact predictions)."""
-    gq = gq or GPUQuant(stream=stream)
+def _first(t, gq, fitted_set, use_qr, stream, count_ptr):
+    """the tensor's kind and first prediction, its differing-byte count written to count_ptr
+    (device u64) without waiting -> (kind, first variant, QR?, prediction) or None if not predicted"""
     k = kind(t.base_type, t.base.size, t.type, t.numel, t.region.nbytes)
     if k is None:
-        return {"kind": None, "variant": None, "nonzero": True, "qr": False, "prediction": None}
+        return None
     first = v0(k, t.imatrix is not None, fitted_set, fitted_set in t.fitted)
     isqr = use_qr and k == "rq" and t.type in QR_TYPES and t.base_type in SEED_TYPES
     p0 = predict(gq, t, first, stream)
     if isqr:
-        n0 = diff_count(t.region, p0, stream)
+        check(lib().spa_diff_count(t.region.ptr, p0.ptr, t.region.nbytes, count_ptr, stream))
     else:
-        n0 = xor_into(t.region, t.region, p0, stream)
+        check(lib().spa_xor(t.region.ptr, t.region.ptr, p0.ptr, t.region.nbytes, count_ptr, stream))
+    return k, first, isqr, p0
+
+
+def _decide(t, gq, k, first, isqr, p0, n0, stream):
+    """the candidate variants after a first prediction leaving n0 differing bytes, and the result"""
     choice, best, best_p = first, n0, p0
     cands = candidates(t.type, first) if k == "rq" else []
     if n0 and cands:
@@ -170,3 +186,36 @@ def residual_tensor(t, gq=None, fitted_set=0, use_qr=True, stream=None):
         isqr = False
     return {"kind": "qr" if isqr else k, "variant": choice, "nonzero": nonzero, "qr": isqr,
             "prediction": best_p if isqr else None, "diff_bytes": best}
+
+
+_NONE = {"kind": None, "variant": None, "nonzero": True, "qr": False, "prediction": None}
+
+
+def residual_tensor(t, gq=None, fitted_set=0, use_qr=True, stream=None):
+    """the residual of one tensor (the per-tensor decisions of repo3.py:1071-1188) ->
+    dict(kind, variant, nonzero, qr, prediction). t.region ends as: the file bytes (QR tensors,
+    coded against `prediction`), file ^ prediction (XOR tensors) or zeros (exact predictions)."""
+    gq = gq or GPUQuant(stream=stream)
+    c = _Count()
+    f = _first(t, gq, fitted_set, use_qr, stream, c.d.ptr)
+    if f is None:
+        return dict(_NONE)
+    return _decide(t, gq, *f, c.value(stream), stream)
+
+
+def residual_window(ts, gq=None, fitted_set=0, use_qr=True, stream=None):
+    """residual_tensor for a window of tensors with the same decisions, their first predictions and
+    byte counts queued back to back and read back together (one wait per window instead of one per
+    tensor, as the reference's window pipeline defers its comparisons, repo3.py:456-510) -> results
+    in the order of ts"""
+    gq = gq or GPUQuant(stream=stream)
+    cache = getattr(_TLS, "windows", None)
+    if cache is None:
+        cache = _TLS.windows = {}
+    key = dev.current_device()
+    if key not in cache or cache[key].size < len(ts):
+        cache[key] = dev.DeviceArray(max(64, 2 * len(ts)), np.uint64)
+    counts = cache[key]
+    firsts = [_first(t, gq, fitted_set, use_qr, stream, counts.ptr + 8 * i) for i, t in enumerate(ts)]
+    n = counts.to_host(stream=stream)[:len(ts)] if ts else []
+    return [dict(_NONE) if f is None else _decide(t, gq, *f, int(n[i]), stream) for i, (t, f) in enumerate(zip(ts, firsts))]

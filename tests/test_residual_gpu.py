@@ -139,3 +139,35 @@ def test_float_tensor_xor():
     assert out["kind"] == "xor" and out["nonzero"]
     res = t.region.to_host()
     assert np.flatnonzero(res).tolist() == [7] and res[7] == 1
+
+
+def test_window_matches_per_tensor():
+    """residual_window (counts read back once) makes residual_tensor's decisions on a mixed window:
+    exact, perturbed (QR and XOR routes), the IQ1_M variant retry, no imatrix, a float tensor"""
+    say("case residual window")
+    gq = GPUQuant()
+    g, w12, imx12 = _case(12)
+    p12 = gq.quantize_tensors(12, [(w12.reshape(-1), 1024)], [imx12])[0]
+    f12 = p12.copy()
+    f12[g.choice(f12.size, 40, replace=False)] ^= 0x11
+    w29, imx29 = synth.tensor(3, 0, rows=64)
+    c29 = w29.shape[1]
+    f29 = gq.quantize_tensors(29, [(w29.reshape(-1), c29)], [imx29], variant=1)[0]
+    _, w14, _ = _case(14)
+    f14 = gq.quantize_tensors(14, [(w14.reshape(-1), 1024)], [np.ones(1024, np.float32)])[0]
+    _, w1, _ = _case(1)
+    f1 = synth.bf16_to_f32(w1).reshape(-1).astype(np.float16).view(np.uint8).copy()
+    f1[7] ^= 1
+    specs = [(12, p12, w12, imx12, 1024), (12, f12, w12, imx12, 1024), (29, f29, w29, imx29, c29),
+             (14, f14, w14, None, 1024), (r.F16, f1, w1, None, 1024)]
+    for use_qr in (True, False):
+        one = [_tensor(t, f, w, m, c) for (t, f, w, m, c) in specs]
+        many = [_tensor(t, f, w, m, c) for (t, f, w, m, c) in specs]
+        a = [r.residual_tensor(t, gq, use_qr=use_qr) for (t, _) in one]
+        b = r.residual_window([t for (t, _) in many], gq, use_qr=use_qr)
+        for (x, (_, ra)), (y, (_, rb)) in zip(zip(a, one), zip(b, many)):
+            for key in ("kind", "variant", "nonzero", "qr", "diff_bytes"):
+                assert x.get(key) == y.get(key), (key, x.get(key), y.get(key))
+            assert ra.to_host().tobytes() == rb.to_host().tobytes()
+            if x["qr"]:
+                assert x["prediction"].to_host().tobytes() == y["prediction"].to_host().tobytes()
