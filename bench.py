@@ -664,6 +664,7 @@ def main():
     qrg = qr_cfg3(stream)
     r2b = r2_layer(stream)
     r2c = r2_cfg4(stream)
+    pk = pack_cfg4(stream)
     cpu = None if a.no_cpu else cpu_baseline(tensors)
     line = {"metric": "requant GB/s (BF16 in), K-quant family Q2_K..Q6_K with imatrix", "value": round(value, 3),
             "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 3),
@@ -672,6 +673,7 @@ def main():
             "config": {"workload": "cfg2: Q2_K,Q3_K,Q4_K,Q5_K,Q6_K (imatrix) on token_embd 151936x1024 + ffn_down 1024x3072",
                        "bf16_bytes_per_step": bf16_bytes, "launches_per_step": len(launches)},
             "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "dequant_token_embd": dqb, "qr_cfg1": qrb, "qr_cfg3": qrg, "r2_base": r2b, "r2_cfg4": r2c,
+            "pack_cfg4": pk,
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
 
