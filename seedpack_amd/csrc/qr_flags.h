@@ -77,29 +77,50 @@ __global__ __launch_bounds__(256) void k_qr_neq(const uint8_t* __restrict__ F, c
     if (threadIdx.x < nblk) neq[b0 + threadIdx.x] = fl[threadIdx.x];
 }
 
-// the flag symbol of every slot (segment s, block j) into counts; differing slots s * seg + j into list
+// the flag symbol of every slot (segment s, block j) into counts; differing slots s * seg + j into list.
+// The four flag counters (previous block equal, this block equal) are summed per lane over a
+// grid-stride loop, then per wave and per workgroup: one global atomic per counter and workgroup
+// (one per wave and block on a few addresses serialised in L2).
 __global__ __launch_bounds__(256) void k_qr_slots(const SG* __restrict__ sg, int nseg, int seg,
                                                   const uint8_t* __restrict__ neq, uint32_t* __restrict__ counts,
                                                   uint32_t* __restrict__ list, uint32_t* __restrict__ nlist) {
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t s = gid / seg;
-    const int j = (int)(gid % seg);
-    if (s >= nseg) return;
-    const SG g = sg[s];
-    if (j >= g.nb) return;
-    const int64_t b = g.b0 + j;
-    const int eq = neq[b] ? 0 : 1;
-    const int prev = j > 0 ? (neq[b - 1] ? 0 : 1) : 1;
-    hadd(counts, (uint32_t)((FLAG + prev) * 256 + eq));
-    const uint64_t m = __ballot(!eq);
-    if (m) {
-        const int lane = __lane_id();
-        const int leader = __ffsll((unsigned long long)m) - 1;
-        uint32_t at = 0;
-        if (lane == leader) at = atomicAdd(nlist, (uint32_t)__popcll(m));
-        at = __shfl(at, leader);
-        if (!eq) list[at + __popcll(m & ((1ull << lane) - 1))] = (uint32_t)gid;
+    __shared__ uint32_t c4[4];
+    if (threadIdx.x < 4) c4[threadIdx.x] = 0;
+    __syncthreads();
+    const int lane = __lane_id();
+    uint32_t mine[4] = {0, 0, 0, 0};   // [prev * 2 + eq]
+    const int64_t nslot = (int64_t)nseg * seg;
+    for (int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gid < nslot; gid += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t s = gid / seg;
+        const int j = (int)(gid % seg);
+        const SG g = sg[s];
+        const bool valid = j < g.nb;
+        int eq = 1;
+        if (valid) {
+            const int64_t b = g.b0 + j;
+            eq = neq[b] ? 0 : 1;
+            const int prev = j > 0 ? (neq[b - 1] ? 0 : 1) : 1;
+            mine[prev * 2 + eq]++;
+        }
+        const uint64_t m = __ballot(valid && !eq);
+        if (m) {
+            const int leader = __ffsll((unsigned long long)m) - 1;
+            uint32_t at = 0;
+            if (lane == leader) at = atomicAdd(nlist, (uint32_t)__popcll(m));
+            at = __shfl(at, leader);
+            if (valid && !eq) list[at + __popcll(m & ((1ull << lane) - 1))] = (uint32_t)gid;
+        }
     }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        uint32_t v = mine[k];
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+        if (lane == 0 && v) atomicAdd(&c4[k], v);
+    }
+    __syncthreads();
+    if (threadIdx.x < 4 && c4[threadIdx.x])
+        atomicAdd(&counts[(FLAG + (threadIdx.x >> 1)) * 256 + (threadIdx.x & 1)], c4[threadIdx.x]);
 }
 
 // neq flags, then (hist only) the flag counts and the list of differing slots
@@ -110,7 +131,8 @@ inline int qr_flags(const void* F, const void* P, const void* sg, int nseg, int 
                        (const uint8_t*)P, (const SG*)sg, nseg, bs, w.neq);
     if (counts) {
         SPA_HIP_TRY(hipMemsetAsync(w.nlist, 0, sizeof(uint32_t), st));
-        hipLaunchKernelGGL(k_qr_slots, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, st, (const SG*)sg, nseg, seg,
+        const int64_t wgs = (slots + 255) / 256 < 1024 ? (slots + 255) / 256 : 1024;
+        hipLaunchKernelGGL(k_qr_slots, dim3((unsigned)wgs), dim3(256), 0, st, (const SG*)sg, nseg, seg,
                            (const uint8_t*)w.neq, counts, w.list, w.nlist);
     }
     SPA_HIP_TRY(hipGetLastError());
