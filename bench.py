@@ -420,6 +420,98 @@ def pack_cfg4(stream, layers=36, per_million=10000, files=None):
     return res
 
 
+def unpack_cfg5(stream, layers=36, per_million=10000):
+    """configuration 5: extract from the configuration-4 archive. Untimed: the base (as in
+    pack_cfg4), a Q4_K_M-like file (Q4_K / Q6_K per tensor) and an IQ2_XS file with per_million /
+    10^6 of their blocks perturbed, packed as pack_cfg4 packs them (base codec; residuals QR-coded
+    and framed in batches of about 384 MB), the coded bytes kept in host memory. Timed: the base
+    decoded into HBM, then per file, per coded batch: its tensors regrown from the decoded base,
+    the batch QR-decoded against them (the file's blocks rebuilt in HBM) and copied to page-locked
+    host memory. Byte identity with the originals is checked on the device afterwards, untimed.
+    GB/s written = rebuilt file bytes / time (the base decode included)."""
+    from seedpack_amd import device as dev
+    from seedpack_amd import qr, r2, residual
+    from seedpack_amd._lib import check, lib
+    from seedpack_amd.gpuquant import GPUQuant
+    from seedpack_amd.requant import QFUN
+    d, ts, pos = cfg4_base(stream, layers)
+    g = np.random.Generator(np.random.PCG64(0x1A7))
+    imx_h = [g.lognormal(0.0, 1.0, rl).astype(np.float32) for (_, _, _, rl) in ts]
+    imx_off = np.cumsum([0] + [a.size for a in imx_h])[:-1]
+    imx_all = dev.DeviceArray.from_host(np.concatenate(imx_h), stream.handle)
+    imx_k = [imx_all.view(int(o) * 4, (a.size,), np.float32) for o, a in zip(imx_off, imx_h)]
+    gq = GPUQuant(stream=stream.handle)
+    codec = r2.BF16v2(stream=stream.handle)
+    base_parts = codec.compress(d, r2.layout_of(ts, pos))
+    base_parts.pop("arrays", None)
+    plan = [("Q4_K_M", _q4km), ("IQ2_XS", lambda name: 17)]
+    archive = []
+    for fi, (fname, type_of) in enumerate(plan):
+        types = [type_of(name) for (name, _, _, _) in ts]
+        regions, batches, pending, wbytes = [], [], {}, {}
+        for k, (name, off, nb, rl) in enumerate(ts):
+            T = types[k]
+            y = gq.quantize_tensors(T, [(d.view(off, (nb // 2,), np.uint16), rl)], [imx_k[k]], device=True)[0]
+            bs = QFUN[T][2]
+            check(lib().spa_perturb_blocks(y.ptr, y.nbytes // bs, bs, per_million, 0xF11E5000 + 1000 * fi + k,
+                                           stream.handle))
+            regions.append(y)
+            r = residual.residual_tensor(residual.Tensor(name, T, rl, y, d.view(off, (nb // 2,), np.uint16),
+                                                         imatrix=imx_k[k]), gq, stream=stream.handle)
+            assert r["qr"] and r["variant"] == 0
+            pending.setdefault(T, []).append((k, y, r["prediction"]))
+            wbytes[T] = wbytes.get(T, 0) + y.nbytes
+            if wbytes[T] >= qr.BATCH or k + 1 == len(ts):
+                for TT in ([T] if k + 1 < len(ts) else list(pending)):
+                    if not pending.get(TT):
+                        continue
+                    it = pending[TT]
+                    buf = qr.encode(TT, [(y_, p_, ts[i][1], 30, ts[i][3], int(imx_off[i])) for (i, y_, p_) in it], d,
+                                    imx_all, stream=stream.handle)
+                    batches.append((TT, [i for (i, _, _) in it], buf))
+                    pending[TT], wbytes[TT] = [], 0
+        archive.append((fname, types, regions, batches))
+    stream.synchronize()
+    del d
+    outbufs = [dev.pinned(sum(r_.nbytes for r_ in a[2])) for a in archive]   # the files' host staging
+    log("bench: unpack cfg5: archive made")
+    t0 = time.perf_counter()
+    base = codec.decompress(base_parts, device=True)
+    t_base = time.perf_counter() - t0
+    out, rebuilt, written = {}, [], 0
+    for (fname, types, regions, batches), host in zip(archive, outbufs):
+        t1 = time.perf_counter()
+        nbytes = sum(r_.nbytes for r_ in regions)
+        at = 0
+        for (T, idx, buf) in batches:
+            preds = [gq.quantize_tensors(T, [(base.view(ts[i][1], (ts[i][2] // 2,), np.uint16), ts[i][3])], [imx_k[i]],
+                                         device=True)[0] for i in idx]
+            F = qr.decode(T, buf, [(p_, ts[i][1], 30, ts[i][3], int(imx_off[i])) for p_, i in zip(preds, idx)], base,
+                          imx_all, stream=stream.handle)
+            nb = sum(regions[i].nbytes for i in idx)
+            check(lib().spa_memcpy_d2h(host[at:].ctypes.data, F.ptr, nb, stream.handle))
+            rebuilt.append((F, idx))
+            at += nb
+        dt = time.perf_counter() - t1
+        written += nbytes
+        out[fname] = {"file_bytes": nbytes, "batches": len(batches), "extract_s": round(dt, 3),
+                      "GB_s": round(nbytes / dt / 1e9, 2)}
+        log(f"bench: unpack cfg5 {fname}: {out[fname]}")
+    total = time.perf_counter() - t0
+    bad = 0
+    for (_, _, regions, _), (F, idx) in zip([a for a in archive for _ in a[3]], rebuilt):
+        o = 0
+        for i in idx:
+            bad += residual.diff_count(F.view(o, (regions[i].nbytes,), np.uint8), regions[i], stream.handle)
+            o += regions[i].nbytes
+    res = {"workload": f"cfg5: extract Q4_K_M-like and IQ2_XS files of configuration 4 ({len(ts)} matrices), "
+                       f"{per_million / 1e4:g}% of blocks perturbed", "base_decode_s": round(t_base, 3),
+           "files": out, "written_bytes": written, "extract_s": round(total, 3),
+           "GB_s_written": round(written / total / 1e9, 2), "bytes_differing": int(bad)}
+    log(f"bench: unpack cfg5 total {res['extract_s']} s, {res['GB_s_written']} GB/s, {bad} bytes differing")
+    return res
+
+
 def r2_cfg4(stream, layers=36):
     """R2 BF16 base codec on configuration 4's whole base (every 2-D matrix, 16.4 GB), generated in
     HBM (N(0, 0.02), a counter-based generator per tensor): compress of the resident file and
@@ -550,6 +642,8 @@ def main():
     ap.add_argument("--pack", action="store_true",
                     help="only configuration 4's pack (all quant files, base codec); prints its result, no JSON line")
     ap.add_argument("--pack-layers", type=int, default=36, help="transformer blocks of the --pack model")
+    ap.add_argument("--unpack", action="store_true",
+                    help="only configuration 5's extract (Q4_K_M-like and IQ2_XS from the configuration-4 archive)")
     ap.add_argument("--pack-files", default=None, help="comma-separated quant files of --pack (default: all 21)")
     ap.add_argument("--codecs", action="store_true",
                     help="only the coding stages (QR on configurations 1 and 3, the R2 base codec), for rocprofv3 "
@@ -561,6 +655,10 @@ def main():
         from seedpack_amd import device as dev
         files = a.pack_files.split(",") if a.pack_files else None
         print(json.dumps(pack_cfg4(dev.Stream(), layers=a.pack_layers, files=files)))
+        return None
+    if a.unpack:
+        from seedpack_amd import device as dev
+        print(json.dumps(unpack_cfg5(dev.Stream(), layers=a.pack_layers)))
         return None
     if a.codecs:
         from seedpack_amd import device as dev
@@ -665,6 +763,7 @@ def main():
     r2b = r2_layer(stream)
     r2c = r2_cfg4(stream)
     pk = pack_cfg4(stream)
+    upk = unpack_cfg5(stream)
     cpu = None if a.no_cpu else cpu_baseline(tensors)
     line = {"metric": "requant GB/s (BF16 in), K-quant family Q2_K..Q6_K with imatrix", "value": round(value, 3),
             "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 3),
@@ -673,7 +772,7 @@ def main():
             "config": {"workload": "cfg2: Q2_K,Q3_K,Q4_K,Q5_K,Q6_K (imatrix) on token_embd 151936x1024 + ffn_down 1024x3072",
                        "bf16_bytes_per_step": bf16_bytes, "launches_per_step": len(launches)},
             "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "dequant_token_embd": dqb, "qr_cfg1": qrb, "qr_cfg3": qrg, "r2_base": r2b, "r2_cfg4": r2c,
-            "pack_cfg4": pk,
+            "pack_cfg4": pk, "unpack_cfg5": upk,
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
 
