@@ -279,7 +279,7 @@ def pack_cfg4(stream, layers=36, per_million=10000, files=None):
     this library's quantizer with per_million / 10^6 of their blocks perturbed (one byte each). Then,
     timed as one run: per file, every tensor is regrown and compared (residual.residual_window over
     windows of about 384 MB: predictions, differing-byte counts read back once per window, the
-    candidate variants) on the main stream, while two coder threads code the QR tensors in batches of
+    candidate variants) on the main stream, while four coder threads code the QR tensors in batches of
     about 384 MB, each on its own stream (qr.encode_parts; the zstd-19 framing on 8 more threads), as
     the reference's pool codes batches beside the prediction (repo3.py:946-979), and one more thread
     compresses the base with the base codec. pack GB/s = (BF16
@@ -318,7 +318,7 @@ def pack_cfg4(stream, layers=36, per_million=10000, files=None):
     stream.synchronize()
     log(f"bench: pack cfg4: {len(made)} files made")
     pool = concurrent.futures.ThreadPoolExecutor(8)      # zstd-19 framing of the coded batches
-    coder = concurrent.futures.ThreadPoolExecutor(2)     # QR batches, each worker on its own stream
+    coder = concurrent.futures.ThreadPoolExecutor(4)     # QR batches, each worker on its own stream
     side = concurrent.futures.ThreadPoolExecutor(1)      # the base codec, on its own streams
     tls = threading.local()
 
@@ -346,8 +346,8 @@ def pack_cfg4(stream, layers=36, per_million=10000, files=None):
         mine = []
 
         def flush(T):
-            # at most 8 batches queued for the coder (their predictions stay alive until coded)
-            while len(inflight) >= 8:
+            # at most 16 batches queued for the coders (their predictions stay alive until coded)
+            while len(inflight) >= 16:
                 inflight.popleft().result()
             f = coder.submit(qr_batch, T, pending[T])
             inflight.append(f)

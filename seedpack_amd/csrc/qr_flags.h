@@ -131,7 +131,7 @@ inline int qr_flags(const void* F, const void* P, const void* sg, int nseg, int 
                        (const uint8_t*)P, (const SG*)sg, nseg, bs, w.neq);
     if (counts) {
         SPA_HIP_TRY(hipMemsetAsync(w.nlist, 0, sizeof(uint32_t), st));
-        const int64_t wgs = (slots + 255) / 256 < 1024 ? (slots + 255) / 256 : 1024;
+        const int64_t wgs = (slots + 255) / 256 < 8192 ? (slots + 255) / 256 : 8192;
         hipLaunchKernelGGL(k_qr_slots, dim3((unsigned)wgs), dim3(256), 0, st, (const SG*)sg, nseg, seg,
                            (const uint8_t*)w.neq, counts, w.list, w.nlist);
     }
