@@ -266,6 +266,57 @@ __global__ __launch_bounds__(64) void k_row_mean_sq(const void* __restrict__ src
     sigma2[row] = s / (float)npr;
 }
 
+// The same for BF16 rows: 64 rows per workgroup, 64x64 tiles through LDS (read as 16-byte vectors,
+// 8 lanes per row: coalesced), the next tile's loads issued before the current tile's sums; each lane
+// adds its row's squares in index order. Rows of npr % 64 == 32 end with a half tile read per lane.
+constexpr int RS = 64;
+__global__ __launch_bounds__(RS) void k_row_mean_sq_bf16(const uint16_t* __restrict__ w, int64_t nrows, int64_t npr,
+                                                         float* __restrict__ sigma2) {
+    __shared__ uint32_t tile[RS][RS / 2 + 1];
+    const int lane = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * RS, row = r0 + lane;
+    const int64_t nt = npr / RS;
+    float s = 0;
+    uint4 v[8];
+    auto load = [&](int64_t c0) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int64_t r = r0 + (lane >> 3) + 8 * k;
+            v[k] = r < nrows ? *reinterpret_cast<const uint4*>(w + r * npr + c0 + (lane & 7) * 8) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    if (nt) load(0);
+    for (int64_t t = 0; t < nt; ++t) {
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            uint32_t* d = &tile[(lane >> 3) + 8 * k][(lane & 7) * 4];
+            d[0] = v[k].x; d[1] = v[k].y; d[2] = v[k].z; d[3] = v[k].w;
+        }
+        __syncthreads();
+        if (t + 1 < nt) load((t + 1) * RS);
+#pragma unroll 8
+        for (int j = 0; j < RS / 2; ++j) {
+            const uint32_t pr = tile[lane][j];
+            const float x0 = bf16_to_f32(pr & 0xffffu), x1 = bf16_to_f32(pr >> 16);
+            s += x0 * x0;
+            s += x1 * x1;
+        }
+    }
+    if (row >= nrows) return;
+    for (int64_t j = nt * RS; j < npr; j += 8) {
+        const uint4 u = *reinterpret_cast<const uint4*>(w + row * npr + j);
+        const uint32_t q[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float x0 = bf16_to_f32(q[k] & 0xffffu), x1 = bf16_to_f32(q[k] >> 16);
+            s += x0 * x0;
+            s += x1 * x1;
+        }
+    }
+    sigma2[row] = s / (float)npr;
+}
+
 template <class Op>
 int run_ref(const QuantArgs& a) {
     const int64_t nblocks = a.nrows * a.n_per_row / Op::QK;
@@ -283,8 +334,12 @@ int run_impl(const QuantArgs& a) {
     if (nblocks == 0) return 0;
     float* sigma2 = nullptr;
     SPA_HIP_TRY(hipMallocAsync((void**)&sigma2, (size_t)a.nrows * sizeof(float), a.stream));
-    hipLaunchKernelGGL(k_row_mean_sq, dim3((unsigned)((a.nrows + 63) / 64)), dim3(64), 0, a.stream, a.src, a.src_kind,
-                       a.nrows, a.n_per_row, sigma2);
+    if (a.src_kind == SRC_BF16)
+        hipLaunchKernelGGL(k_row_mean_sq_bf16, dim3((unsigned)((a.nrows + RS - 1) / RS)), dim3(RS), 0, a.stream,
+                           (const uint16_t*)a.src, a.nrows, a.n_per_row, sigma2);
+    else
+        hipLaunchKernelGGL(k_row_mean_sq, dim3((unsigned)((a.nrows + 63) / 64)), dim3(64), 0, a.stream, a.src, a.src_kind,
+                           a.nrows, a.n_per_row, sigma2);
     const int64_t grid = (nblocks + WG - 1) / WG;
     hipLaunchKernelGGL((k_legacy<Op, true>), dim3((unsigned)grid), dim3(WG), 0, a.stream, a.src, a.src_kind,
                        (uint8_t*)a.dst, nblocks, a.n_per_row / Op::QK, a.imatrix, sigma2);

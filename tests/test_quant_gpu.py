@@ -127,3 +127,20 @@ def test_zero_rows_is_a_no_op():
     quantize_into(12, dev.DeviceArray(0, np.uint16), 256, dst)
     dev.synchronize()
     del src
+
+
+@pytest.mark.parametrize("t", [2, 3, 6, 7])
+def test_legacy_imatrix_rows_with_half_tile(gq, t):
+    """the BF16 row pre-pass of the imatrix legacy quantizers: rows of n_per_row % 64 == 32 (a half
+    tile at the end) and a row count that leaves a partial workgroup, against the oracle; the F32 copy
+    (the per-lane pre-pass) gives the same bytes"""
+    g = np.random.Generator(np.random.PCG64(0xB0 + t))
+    b = synth.normal_bf16(g, (70, 1056), 0.02, outlier_frac=0.002)
+    imx = g.lognormal(0, 1, 1056).astype(np.float32)
+    x = synth.bf16_to_f32(b).reshape(b.shape)
+    say("case legacy half tile", t)
+    got = hip(gq, t, b, imx)
+    want = quants.quantize(t, x, imx)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"{bad.size} bytes differ, first at {bad[:8]}"
+    assert hip(gq, t, x, imx).tobytes() == got.tobytes()
