@@ -90,6 +90,77 @@ struct Enc {
 // bytes kept free below the coder's write pointer while coding codes: the block's fields (up to three
 // symbols each) and its flag, at most two bytes per symbol
 template <int T> constexpr int64_t FIELD_ROOM = 6 * Ty<T>::NF + 16;
+// symbols of a differing block besides its flag: its codes and up to three per field
+template <int T> constexpr int MAXSYM = Ty<T>::QK + 3 * Ty<T>::NF;
+
+// The symbols of a differing block in the encoder's order -- codes last to first, then the fields
+// last to first (an escaped field as HI, LO, mark) -- handed to put(table, symbol); put returns false
+// to stop (the coder's room check after each code). The flag symbol is not included.
+template <int T, class Put>
+__device__ __forceinline__ bool block_syms(Put&& put, const uint8_t* fb, const uint8_t* pb, const uint8_t* sbase,
+                                           const TM& m, int64_t b, int mv) {
+    using Y = Ty<T>;
+    const int64_t gw0 = (b - m.blk0) * Y::QK;
+    const int64_t col0 = m.cols > 0 ? gw0 % m.cols : 0;
+    float a = 0.f, c = 0.f;
+    int sub = -1;
+    for (int w = Y::QK - 1; w >= 0; --w) {
+        if (w / Y::SUBLEN != sub) { sub = w / Y::SUBLEN; wscale<T>(fb, w, a, c); }
+        float x, h;
+        seed_val(m.seed_type, sbase, gw0 + w, x, h);
+        int r, sg_, ctx;
+        predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
+        if (!put(ctx, (uint32_t)((sg_ * (get_code<T>(fb, w) - r)) & 255), true)) return false;
+    }
+    int tv[Y::NF], dl[Y::NF], anyk[Y::NF];
+#pragma unroll
+    for (int k = 0; k < Y::NF; ++k) tv[k] = get_field<T>(fb, k);
+    int any = 0;
+#pragma unroll
+    for (int k = 0; k < Y::NF; ++k) {
+        dl[k] = tv[k] - fpred<T>(mv, pb, k, tv[0], Y::NF > 1 ? tv[1] : 0);
+        anyk[k] = any;
+        any |= dl[k] != 0;
+    }
+#pragma unroll
+    for (int k = Y::NF - 1; k >= 0; --k) {
+        const int kd = fkind<T>(k);
+        if (kd < 2 && (dl[k] < -127 || dl[k] > 127)) {
+            put(FESC_HI, (uint32_t)(tv[k] >> 8), false);
+            put(FESC_LO, (uint32_t)(tv[k] & 255), false);
+            put(kd * 2 + anyk[k], 128, false);
+        } else {
+            put(kd * 2 + anyk[k], (uint32_t)(dl[k] & 255), false);
+        }
+    }
+    return true;
+}
+
+// The symbols of the listed differing blocks (the first `cap` of the list), one lane per block, all
+// lanes busy: words (table << 8 | symbol) in the encoder's order and their count. The serial coder
+// then only replays them (one lane per segment would otherwise model each of its blocks while the
+// wave's other lanes wait).
+template <int T>
+__global__ __launch_bounds__(256) void k_qr_syms(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
+                                                 const uint8_t* __restrict__ seed, const TM* __restrict__ tm,
+                                                 const SG* __restrict__ sg, const uint32_t* __restrict__ list,
+                                                 const uint32_t* __restrict__ nlist, uint32_t cap,
+                                                 uint16_t* __restrict__ nsym, uint32_t* __restrict__ syms, int mv) {
+    using Y = Ty<T>;
+    constexpr int SEG = SEG_BLOCKS<T>;
+    const uint32_t n = *nlist < cap ? *nlist : cap;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const uint32_t slot = list[i];
+        const SG g = sg[slot / SEG];
+        const TM m = tm[g.t];
+        const int64_t b = g.b0 + (int)(slot % SEG);
+        uint32_t* out = syms + (size_t)i * MAXSYM<T>;
+        int k = 0;
+        block_syms<T>([&](int tab, uint32_t sym, bool) { out[k++] = ((uint32_t)tab << 8) | sym; return true; },
+                      F + b * Y::BS, P + b * Y::BS, seed + m.seed_off, m, b, mv);
+        nsym[i] = (uint16_t)k;
+    }
+}
 
 template <int T>
 __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
@@ -97,7 +168,9 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
                                                const SG* __restrict__ sg, int nseg, const int* __restrict__ remap,
                                                const uint16_t* __restrict__ freq, const uint32_t* __restrict__ cum,
                                                uint8_t* __restrict__ out, uint64_t cap, uint32_t* __restrict__ out_len,
-                                               const uint8_t* __restrict__ neq, int mv) {
+                                               const uint8_t* __restrict__ neq, const uint32_t* __restrict__ idx_of,
+                                               const uint16_t* __restrict__ nsym, const uint32_t* __restrict__ syms,
+                                               int mv) {
     using Y = Ty<T>;
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
@@ -107,9 +180,11 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
     uint8_t* const base = out + (uint64_t)s * cap;
     uint8_t* const end = base + cap;
     Enc e{RANS_L, end, remap, freq, cum};
+    auto put = [&](int tab, uint32_t sym, bool code) {
+        e.put(tab, sym);
+        return !(code && e.ptr - base < FIELD_ROOM<T>);
+    };
     for (int64_t b = g.b0 + g.nb - 1; b >= g.b0; --b) {
-        const uint8_t* fb = F + b * Y::BS;
-        const uint8_t* pb = P + b * Y::BS;
         const bool eq = !neq[b];
         const int prev = b > g.b0 ? (neq[b - 1] ? 0 : 1) : 1;
         if (eq) {
@@ -117,39 +192,16 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
             if (e.ptr - base < 8) { out_len[s] = 0xffffffffu; return; }
             continue;
         }
-        const int64_t gw0 = (b - m.blk0) * Y::QK;
-        const int64_t col0 = m.cols > 0 ? gw0 % m.cols : 0;
-        float a = 0.f, c = 0.f;
-        int sub = -1;
-        for (int w = Y::QK - 1; w >= 0; --w) {
-            if (w / Y::SUBLEN != sub) { sub = w / Y::SUBLEN; wscale<T>(fb, w, a, c); }
-            float x, h;
-            seed_val(m.seed_type, sbase, gw0 + w, x, h);
-            int r, sg_, ctx;
-            predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
-            e.put(ctx, (uint32_t)((sg_ * (get_code<T>(fb, w) - r)) & 255));
-            if (e.ptr - base < FIELD_ROOM<T>) { out_len[s] = 0xffffffffu; return; }
-        }
-        int tv[Y::NF], dl[Y::NF], anyk[Y::NF];
-#pragma unroll
-        for (int k = 0; k < Y::NF; ++k) tv[k] = get_field<T>(fb, k);
-        int any = 0;
-#pragma unroll
-        for (int k = 0; k < Y::NF; ++k) {
-            dl[k] = tv[k] - fpred<T>(mv, pb, k, tv[0], Y::NF > 1 ? tv[1] : 0);
-            anyk[k] = any;
-            any |= dl[k] != 0;
-        }
-#pragma unroll
-        for (int k = Y::NF - 1; k >= 0; --k) {
-            const int kd = fkind<T>(k);
-            if (kd < 2 && (dl[k] < -127 || dl[k] > 127)) {
-                e.put(FESC_HI, (uint32_t)(tv[k] >> 8));
-                e.put(FESC_LO, (uint32_t)(tv[k] & 255));
-                e.put(kd * 2 + anyk[k], 128);
-            } else {
-                e.put(kd * 2 + anyk[k], (uint32_t)(dl[k] & 255));
-            }
+        const uint32_t i = idx_of[b];
+        if (i != 0xffffffffu) {
+            // the block's symbols from the parallel pass: the codes (checked for room) first
+            const uint32_t* q = syms + (size_t)i * MAXSYM<T>;
+            const int n = nsym[i];
+            for (int k = 0; k < n; ++k)
+                if (!put((int)(q[k] >> 8), q[k] & 255u, k < Y::QK)) { out_len[s] = 0xffffffffu; return; }
+        } else if (!block_syms<T>(put, F + b * Y::BS, P + b * Y::BS, sbase, m, b, mv)) {
+            out_len[s] = 0xffffffffu;
+            return;
         }
         e.put(FLAG + prev, 0);
     }
@@ -286,8 +338,8 @@ template <int T> struct Hist {
     static int run(const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,
                    uint32_t* counts, int mv, void* work, hipStream_t st) {
         const int64_t n = (int64_t)nseg * SEG_BLOCKS<T>;
-        const QrWork w = qr_work(work, n);
-        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, counts, st)) return e;
+        const QrWork w = qr_work(work, n, MAXSYM<T>);
+        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, counts, false, st)) return e;
         // the differing blocks are a small share of the batch in practice: at most 2048 workgroups
         // stride over the list
         const int64_t wgs = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
@@ -302,11 +354,17 @@ template <int T> struct Encode {
     static int run(const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, const int* remap,
                    const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, int mv, void* work,
                    hipStream_t st) {
-        const QrWork w = qr_work(work, (int64_t)nseg * SEG_BLOCKS<T>);
-        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, nullptr, st)) return e;
+        const int64_t n = (int64_t)nseg * SEG_BLOCKS<T>;
+        const QrWork w = qr_work(work, n, MAXSYM<T>);
+        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, nullptr, true, st)) return e;
+        const int64_t wgs = ((int64_t)w.cap + 255) / 256 < 2048 ? ((int64_t)w.cap + 255) / 256 : 2048;
+        hipLaunchKernelGGL(k_qr_syms<T>, dim3((unsigned)wgs), dim3(256), 0, st, (const uint8_t*)F, (const uint8_t*)P,
+                           (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, (const uint32_t*)w.list,
+                           (const uint32_t*)w.nlist, w.cap, w.nsym, w.syms, mv);
         hipLaunchKernelGGL(k_qr_enc<T>, dim3((unsigned)((nseg + 63) / 64)), dim3(64), 0, st, (const uint8_t*)F,
                            (const uint8_t*)P, (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, remap, freq, cum,
-                           (uint8_t*)out, cap, out_len, (const uint8_t*)w.neq, mv);
+                           (uint8_t*)out, cap, out_len, (const uint8_t*)w.neq, (const uint32_t*)w.idx_of,
+                           (const uint16_t*)w.nsym, (const uint32_t*)w.syms, mv);
         SPA_HIP_TRY(hipGetLastError());
         return 0;
     }
@@ -321,6 +379,10 @@ template <int T> struct Decode {
         SPA_HIP_TRY(hipGetLastError());
         return 0;
     }
+};
+
+template <int T> struct MaxSym {
+    static int run() { return MAXSYM<T>; }
 };
 
 bool grid_type(int T) { return T == 16 || T == 17 || T == 18 || T == 19 || T == 21 || T == 22 || T == 29; }
@@ -364,7 +426,7 @@ int spa_qr_seg_blocks(int T) {
 size_t spa_qr_work_bytes(int T, int nseg) {
     const int seg = spa_qr_seg_blocks(T);
     if (!seg || nseg < 0) return 0;
-    return qr_work_bytes((int64_t)nseg * seg);
+    return qr_work_bytes((int64_t)nseg * seg, grid_type(T) ? 0 : dispatch<MaxSym>(T));
 }
 
 int spa_qr_hist(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,

@@ -28,19 +28,36 @@ __device__ __forceinline__ void hadd(uint32_t* counts, uint32_t key) {
     }
 }
 
-// workspace: neq flags (one byte per block slot), the list length, the list (one u32 slot per block)
+// workspace: neq flags (one byte per block slot), the list length, the list (one u32 slot per block),
+// per block its place in the list (u32), and for the non-grid encoder the symbols of the first `cap`
+// listed blocks (maxsym u32 words and a u16 count each; cap = a sixteenth of the slots: blocks beyond
+// it are modelled by the coder itself)
 struct QrWork {
     uint8_t* neq;
     uint32_t* nlist;
     uint32_t* list;
+    uint32_t* idx_of;
+    uint16_t* nsym;
+    uint32_t* syms;
+    uint32_t cap;
 };
-__host__ __device__ inline size_t qr_work_bytes(int64_t slots) {
-    return (size_t)((slots + 255) / 256 * 256) + 256 + (size_t)slots * 4;
+__host__ __device__ inline int64_t qr_sym_cap(int64_t slots) { return slots / 16 > 1024 ? slots / 16 : 1024; }
+__host__ __device__ inline size_t qr_work_bytes(int64_t slots, int maxsym) {
+    const size_t a = (size_t)((slots + 255) / 256 * 256), cap = (size_t)qr_sym_cap(slots);
+    return a + 256 + (size_t)slots * 8 + (cap * 2 + 255) / 256 * 256 + (maxsym ? cap * (size_t)maxsym * 4 : 0);
 }
-__host__ __device__ inline QrWork qr_work(void* w, int64_t slots) {
+__host__ __device__ inline QrWork qr_work(void* w, int64_t slots, int maxsym) {
     uint8_t* p = (uint8_t*)w;
-    const size_t a = (size_t)((slots + 255) / 256 * 256);
-    return QrWork{p, (uint32_t*)(p + a), (uint32_t*)(p + a + 256)};
+    const size_t a = (size_t)((slots + 255) / 256 * 256), cap = (size_t)qr_sym_cap(slots);
+    QrWork q;
+    q.neq = p;
+    q.nlist = (uint32_t*)(p + a);
+    q.list = (uint32_t*)(p + a + 256);
+    q.idx_of = q.list + slots;
+    q.nsym = (uint16_t*)(q.idx_of + slots);
+    q.syms = maxsym ? (uint32_t*)((uint8_t*)q.nsym + (cap * 2 + 255) / 256 * 256) : nullptr;
+    q.cap = maxsym ? (uint32_t)cap : 0;
+    return q;
 }
 
 // neq[b] for the batch's blocks b < (last segment's b0 + nb): 256 blocks per workgroup
@@ -83,7 +100,8 @@ __global__ __launch_bounds__(256) void k_qr_neq(const uint8_t* __restrict__ F, c
 // (one per wave and block on a few addresses serialised in L2).
 __global__ __launch_bounds__(256) void k_qr_slots(const SG* __restrict__ sg, int nseg, int seg,
                                                   const uint8_t* __restrict__ neq, uint32_t* __restrict__ counts,
-                                                  uint32_t* __restrict__ list, uint32_t* __restrict__ nlist) {
+                                                  uint32_t* __restrict__ list, uint32_t* __restrict__ nlist,
+                                                  uint32_t* __restrict__ idx_of, uint32_t cap) {
     __shared__ uint32_t c4[4];
     if (threadIdx.x < 4) c4[threadIdx.x] = 0;
     __syncthreads();
@@ -108,7 +126,11 @@ __global__ __launch_bounds__(256) void k_qr_slots(const SG* __restrict__ sg, int
             uint32_t at = 0;
             if (lane == leader) at = atomicAdd(nlist, (uint32_t)__popcll(m));
             at = __shfl(at, leader);
-            if (valid && !eq) list[at + __popcll(m & ((1ull << lane) - 1))] = (uint32_t)gid;
+            if (valid && !eq) {
+                const uint32_t pos = at + (uint32_t)__popcll(m & ((1ull << lane) - 1));
+                list[pos] = (uint32_t)gid;
+                if (idx_of) idx_of[g.b0 + j] = pos < cap ? pos : 0xffffffffu;
+            }
         }
     }
 #pragma unroll
@@ -119,22 +141,25 @@ __global__ __launch_bounds__(256) void k_qr_slots(const SG* __restrict__ sg, int
         if (lane == 0 && v) atomicAdd(&c4[k], v);
     }
     __syncthreads();
-    if (threadIdx.x < 4 && c4[threadIdx.x])
+    if (counts && threadIdx.x < 4 && c4[threadIdx.x])
         atomicAdd(&counts[(FLAG + (threadIdx.x >> 1)) * 256 + (threadIdx.x & 1)], c4[threadIdx.x]);
 }
 
-// neq flags, then (hist only) the flag counts and the list of differing slots
-inline int qr_flags(const void* F, const void* P, const void* sg, int nseg, int seg, int bs, QrWork w, uint32_t* counts,
-                    hipStream_t st) {
+// neq flags, then the list of differing slots with (hist) the flag counts or (encode) each listed
+// block's place in the list
+inline int qr_flags(const void* F, const void* P, const void* sg, int nseg, int seg, int bs, const QrWork& w,
+                    uint32_t* counts, bool places, hipStream_t st) {
     const int64_t slots = (int64_t)nseg * seg;
     hipLaunchKernelGGL(k_qr_neq, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, st, (const uint8_t*)F,
                        (const uint8_t*)P, (const SG*)sg, nseg, bs, w.neq);
-    if (counts) {
-        SPA_HIP_TRY(hipMemsetAsync(w.nlist, 0, sizeof(uint32_t), st));
-        const int64_t wgs = (slots + 255) / 256 < 8192 ? (slots + 255) / 256 : 8192;
-        hipLaunchKernelGGL(k_qr_slots, dim3((unsigned)wgs), dim3(256), 0, st, (const SG*)sg, nseg, seg,
-                           (const uint8_t*)w.neq, counts, w.list, w.nlist);
+    if (!counts && !places) {
+        SPA_HIP_TRY(hipGetLastError());
+        return 0;
     }
+    SPA_HIP_TRY(hipMemsetAsync(w.nlist, 0, sizeof(uint32_t), st));
+    const int64_t wgs = (slots + 255) / 256 < 8192 ? (slots + 255) / 256 : 8192;
+    hipLaunchKernelGGL(k_qr_slots, dim3((unsigned)wgs), dim3(256), 0, st, (const SG*)sg, nseg, seg, (const uint8_t*)w.neq,
+                       counts, w.list, w.nlist, places ? w.idx_of : nullptr, w.cap);
     SPA_HIP_TRY(hipGetLastError());
     return 0;
 }

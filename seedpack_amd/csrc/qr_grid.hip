@@ -645,8 +645,8 @@ template <int T> struct GHist {
     static int run(const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, uint32_t* counts,
                    const uint16_t* gk, const float* imx, int mv, void* work, hipStream_t st) {
         const int64_t n = (int64_t)nseg * SEG_BLOCKS<T>;
-        const QrWork w = qr_work(work, n);
-        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, counts, st)) return e;
+        const QrWork w = qr_work(work, n, 0);
+        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, counts, false, st)) return e;
         // one wave per differing block; at most 16384 waves stride over the list
         const int64_t waves = n < 16384 ? n : 16384;
         hipLaunchKernelGGL(k_qrg_hist<T>, dim3((unsigned)waves), dim3(64), 0, st, (const uint8_t*)F, (const uint8_t*)P,
@@ -660,8 +660,8 @@ template <int T> struct GEnc {
     static int run(const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, const int* remap,
                    const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, const uint16_t* gk,
                    const float* imx, int mv, void* work, hipStream_t st) {
-        const QrWork w = qr_work(work, (int64_t)nseg * SEG_BLOCKS<T>);
-        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, nullptr, st)) return e;
+        const QrWork w = qr_work(work, (int64_t)nseg * SEG_BLOCKS<T>, 0);
+        if (int e = qr_flags(F, P, sg, nseg, SEG_BLOCKS<T>, Ty<T>::BS, w, nullptr, false, st)) return e;
         hipLaunchKernelGGL(k_qrg_enc<T>, dim3((unsigned)nseg), dim3(64), 0, st, (const uint8_t*)F, (const uint8_t*)P,
                            (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, remap, freq, cum, (uint8_t*)out, cap,
                            out_len, gk, imx, (const uint8_t*)w.neq, mv);
