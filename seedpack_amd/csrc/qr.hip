@@ -255,10 +255,7 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
         uint8_t* dst = F + b * Y::BS;
         const int eq = d.get(FLAG + prev);
         prev = eq;
-        if (eq) {
-            for (int i = 0; i < Y::BS; ++i) dst[i] = pb[i];
-            continue;
-        }
+        if (eq) continue;                         // F holds P's bytes already (qr_prefill)
         for (int i = 0; i < Y::BS; ++i) fb[i] = 0;
         int vals[Y::NF];
         int any = 0;
@@ -373,6 +370,7 @@ template <int T> struct Decode {
     static int run(const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
                    int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F, int mv,
                    hipStream_t st) {
+        if (int e = qr_prefill(F, P, sg, nseg, Ty<T>::BS, st)) return e;
         hipLaunchKernelGGL(k_qr_dec<T>, dim3((unsigned)((nseg + DEC_WG - 1) / DEC_WG)), dim3(DEC_WG), 0, st,
                            (const uint8_t*)in, in_off, (const uint8_t*)P, (const uint8_t*)seed, (const TM*)tm, (const SG*)sg,
                            nseg, remap, freq, cum, lut, (uint8_t*)F, mv);

@@ -145,6 +145,30 @@ __global__ __launch_bounds__(256) void k_qr_slots(const SG* __restrict__ sg, int
         atomicAdd(&counts[(FLAG + (threadIdx.x >> 1)) * 256 + (threadIdx.x & 1)], c4[threadIdx.x]);
 }
 
+// F = P over the batch's blocks (b < last segment's b0 + nb) before a decode: the decoders then write
+// only the blocks that differ, and the equal ones (most of a file) move as coalesced 16-byte words
+// instead of one lane's byte loop per block
+__global__ __launch_bounds__(256) void k_qr_prefill(uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
+                                                    const SG* __restrict__ sg, int nseg, int bs) {
+    const SG last = sg[nseg - 1];
+    const int64_t n = (last.b0 + last.nb) * bs;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t done = 0;
+    if (((reinterpret_cast<uintptr_t>(F) | reinterpret_cast<uintptr_t>(P)) & 15) == 0) {
+        const int64_t nv = n / 16;
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += stride)
+            reinterpret_cast<uint4*>(F)[i] = reinterpret_cast<const uint4*>(P)[i];
+        done = nv * 16;
+    }
+    for (int64_t i = done + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) F[i] = P[i];
+}
+
+inline int qr_prefill(void* F, const void* P, const void* sg, int nseg, int bs, hipStream_t st) {
+    hipLaunchKernelGGL(k_qr_prefill, dim3(4096), dim3(256), 0, st, (uint8_t*)F, (const uint8_t*)P, (const SG*)sg, nseg, bs);
+    SPA_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
 // neq flags, then the list of differing slots with (hist) the flag counts or (encode) each listed
 // block's place in the list
 inline int qr_flags(const void* F, const void* P, const void* sg, int nseg, int seg, int bs, const QrWork& w,

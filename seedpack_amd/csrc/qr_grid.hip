@@ -522,12 +522,7 @@ __global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, 
         uint8_t* dst = F + b * Y::BS;
         const int eq = d.get(FLAG + prev);
         prev = eq;
-        if (eq) {
-#pragma unroll
-            for (int i = 0; i < (Y::BS + 63) / 64; ++i)
-                if (lane + 64 * i < Y::BS) dst[lane + 64 * i] = pb[lane + 64 * i];
-            continue;
-        }
+        if (eq) continue;                         // F holds P's bytes already (qr_prefill)
         // every lane applies the same writes to the block in LDS, so each lane's reads see them
 #pragma unroll
         for (int i = 0; i < BSW; ++i) blk32[i] = 0;
@@ -673,6 +668,7 @@ template <int T> struct GDec {
     static int run(const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
                    int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F,
                    const uint16_t* gk, const float* imx, int mv, hipStream_t st) {
+        if (int e = qr_prefill(F, P, sg, nseg, Ty<T>::BS, st)) return e;
         hipLaunchKernelGGL(k_qrg_dec<T>, dim3((unsigned)nseg), dim3(64), 0, st, (const uint8_t*)in, in_off, (const uint8_t*)P,
                            (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, remap, freq, cum, lut, (uint8_t*)F, gk,
                            imx, mv);
