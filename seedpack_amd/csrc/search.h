@@ -185,13 +185,21 @@ __device__ __forceinline__ float make_qkx3_quants(const float (&x)[N], const flo
     const float min0 = min;
     float best_iscale = iscale0, best_min = min0;   // (iscale, min) that produced the kept levels
     bool from_step = false;
+    // x - min for the running min, kept for 16-weight sub-blocks (recomputed only when a step wins and
+    // moves the min); the 32-weight ones have no registers to spare for it (occupancy 3 -> 2)
+    constexpr bool KEEP = N <= 16;
+    float xm[KEEP ? N : 1];
+    if constexpr (KEEP) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) xm[i] = x[i] - min;
+    }
     for (int is = 0; is <= nstep; ++is) {
         const float iscale = (rmin + rdelta * (float)is + (float)NMAX) / (max - min);
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
         float Lf[N];
 #pragma unroll
         for (int i = 0; i < N; ++i) {
-            const float v = iscale * (x[i] - min);
+            const float v = iscale * (KEEP ? xm[i] : x[i] - min);
             const float fl = rintf(fminf(fmaxf(v, 0.f), (float)NMAX));
             Lf[i] = fl;
             const float wl = w[i] * fl;
@@ -221,6 +229,10 @@ __device__ __forceinline__ float make_qkx3_quants(const float (&x)[N], const flo
                 best_mad = mad;
                 scale = this_scale;
                 min = this_min;
+                if constexpr (KEEP) {
+#pragma unroll
+                    for (int i = 0; i < N; ++i) xm[i] = x[i] - min;
+                }
             }
         }
     }
