@@ -880,11 +880,16 @@ FUNCS = {
     10: q2_K, 11: q3_K, 12: lambda x, imx=None: q4_5_K(x, imx, 15), 13: lambda x, imx=None: q4_5_K(x, imx, 31),
     14: q6_K, 20: iq4_nl, 23: iq4_xs,
 }
+GRID_TYPES = (16, 17, 18, 19, 21, 22, 29)
 
 
 def quantize(ttype, x, imatrix=None, variant=0):
     """float32 (nrows, n_per_row) -> quantized bytes (uint8), as quantize_<type>(x, dst, nrows,
-    n_per_row, imatrix)"""
+    n_per_row, imatrix). The lattice types (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M)
+    are restated in C (oracle/iq_grid.c, bound by oracle/iq_grid.py)."""
+    if ttype in GRID_TYPES:
+        from oracle import iq_grid
+        return iq_grid.quantize(ttype, x, imatrix, variant)
     if ttype not in FUNCS or variant != 0:
         raise NotImplementedError(f"oracle: type {ttype} variant {variant}")
     x = np.ascontiguousarray(x, F)
