@@ -78,12 +78,32 @@ struct Enc {
     const int* remap;
     const uint16_t* freq;
     const uint32_t* cum;
-    __device__ __forceinline__ void put(int tab, uint32_t sym) {
-        const int tt = remap[tab];
-        const uint32_t f = freq[tt * 256 + sym], c = cum[tt * 257 + sym];
+    __device__ __forceinline__ void put_fc(uint32_t f, uint32_t c) {
         const uint32_t xm = ((RANS_L >> PB) << 8) * f;
         while (x >= xm) { *--ptr = (uint8_t)(x & 0xff); x >>= 8; }
         x = ((x / f) << PB) + (x % f) + c;
+    }
+    __device__ __forceinline__ void put(int tab, uint32_t sym) {
+        const int tt = remap[tab];
+        put_fc(freq[tt * 256 + sym], cum[tt * 257 + sym]);
+    }
+};
+
+// Frequencies and starts of the flag symbols 0 and 1 in the two flag contexts (previous block
+// differing / equal), held in registers: every block codes a flag, most blocks nothing else. A context
+// without symbols in the batch reads as 0 (a valid batch never codes it).
+struct FlagTab {
+    uint32_t f[2][2], c[2][2];
+    __device__ __forceinline__ void load(const int* remap, const uint16_t* freq, const uint32_t* cum) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int tt = remap[FLAG + p];
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+                f[p][v] = tt >= 0 ? freq[tt * 256 + v] : 0u;
+                c[p][v] = tt >= 0 ? cum[tt * 257 + v] : 0u;
+            }
+        }
     }
 };
 
@@ -162,6 +182,11 @@ __global__ __launch_bounds__(256) void k_qr_syms(const uint8_t* __restrict__ F, 
     }
 }
 
+// One lane per segment, blocks last to first. The lane's block flags come from the equality pass as a
+// bit mask in LDS. Work goes in rounds: each lane codes the flags of its run of equal blocks up to its
+// next differing block, then the lanes that stopped at one code its symbols together -- so the wave
+// runs the symbol loop once per round rather than once per block any of its lanes differs in. Each
+// lane codes its own symbols in the same order as a block-by-block walk: the stream is the same.
 template <int T>
 __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
                                                const uint8_t* __restrict__ seed, const TM* __restrict__ tm,
@@ -172,40 +197,60 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
                                                const uint16_t* __restrict__ nsym, const uint32_t* __restrict__ syms,
                                                int mv) {
     using Y = Ty<T>;
+    constexpr int NW = SEG_BLOCKS<T> / 32;
+    __shared__ uint32_t nbits[64][NW + 1];
+    const int lane = threadIdx.x;
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
     const SG g = sg[s];
     const TM m = tm[g.t];
+    const int nb = g.nb < SEG_BLOCKS<T> ? g.nb : SEG_BLOCKS<T>;
+    for (int w = 0; w < NW; ++w) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+            if (32 * w + j < nb) v |= (uint32_t)(neq[g.b0 + 32 * w + j] != 0) << j;
+        nbits[lane][w] = v;
+    }
+    auto differs = [&](int i) { return (nbits[lane][i >> 5] >> (i & 31)) & 1u; };
     const uint8_t* sbase = seed + m.seed_off;
     uint8_t* const base = out + (uint64_t)s * cap;
     uint8_t* const end = base + cap;
     Enc e{RANS_L, end, remap, freq, cum};
+    FlagTab ft;
+    ft.load(remap, freq, cum);
     auto put = [&](int tab, uint32_t sym, bool code) {
         e.put(tab, sym);
         return !(code && e.ptr - base < FIELD_ROOM<T>);
     };
-    for (int64_t b = g.b0 + g.nb - 1; b >= g.b0; --b) {
-        const bool eq = !neq[b];
-        const int prev = b > g.b0 ? (neq[b - 1] ? 0 : 1) : 1;
-        if (eq) {
-            e.put(FLAG + prev, 1);
+    int i = nb - 1;                              // block g.b0 + i
+    for (;;) {
+        bool pend = false;
+        for (; i >= 0; --i) {
+            const int prev = i > 0 ? (differs(i - 1) ? 0 : 1) : 1;
+            if (differs(i)) { pend = true; break; }
+            e.put_fc(ft.f[prev][1], ft.c[prev][1]);
             if (e.ptr - base < 8) { out_len[s] = 0xffffffffu; return; }
-            continue;
         }
-        const uint32_t i = idx_of[b];
-        if (i != 0xffffffffu) {
+        if (__ballot(pend) == 0) break;
+        if (!pend) continue;
+        const int64_t b = g.b0 + i;
+        const uint32_t k = idx_of[b];
+        if (k != 0xffffffffu) {
             // the block's symbols from the parallel pass: the codes (checked for room) first
-            const uint32_t* q = syms + (size_t)i * MAXSYM<T>;
-            const int n = nsym[i];
-            for (int k = 0; k < n; ++k)
-                if (!put((int)(q[k] >> 8), q[k] & 255u, k < Y::QK)) { out_len[s] = 0xffffffffu; return; }
+            const uint32_t* q = syms + (size_t)k * MAXSYM<T>;
+            const int n = nsym[k];
+            for (int j = 0; j < n; ++j)
+                if (!put((int)(q[j] >> 8), q[j] & 255u, j < Y::QK)) { out_len[s] = 0xffffffffu; return; }
         } else if (!block_syms<T>(put, F + b * Y::BS, P + b * Y::BS, sbase, m, b, mv)) {
             out_len[s] = 0xffffffffu;
             return;
         }
-        e.put(FLAG + prev, 0);
+        const int prev = i > 0 ? (differs(i - 1) ? 0 : 1) : 1;
+        e.put_fc(ft.f[prev][0], ft.c[prev][0]);
+        --i;
     }
-    for (int i = 0; i < 4; ++i) { *--e.ptr = (uint8_t)(e.x & 0xff); e.x >>= 8; }
+    for (int j = 0; j < 4; ++j) { *--e.ptr = (uint8_t)(e.x & 0xff); e.x >>= 8; }
     out_len[s] = (uint32_t)(end - e.ptr);
 }
 
@@ -216,21 +261,28 @@ struct Dec {
     const uint16_t* freq;
     const uint32_t* cum;
     const uint8_t* lut;
-    __device__ __forceinline__ int get(int tab) {
-        const int tt = remap[tab];
+    __device__ __forceinline__ int step(const uint8_t* tl, const uint16_t* tf, const uint32_t* tc) {
         const uint32_t slot = x & (PSCALE - 1);
-        const int v = lut[(size_t)tt * PSCALE + slot];
-        x = freq[tt * 256 + v] * (x >> PB) + slot - cum[tt * 257 + v];
+        const int v = tl[slot];
+        x = tf[v] * (x >> PB) + slot - tc[v];
         // a valid stream needs at most two bytes here (x >= 2^11 before them); the cap ends the
         // loop on a damaged stream instead of spinning on zero bytes
 #pragma unroll
         for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | *ptr++;
         return v;
     }
+    __device__ __forceinline__ int get(int tab) {
+        const int tt = remap[tab];
+        return step(lut + (size_t)tt * PSCALE, freq + tt * 256, cum + tt * 257);
+    }
 };
 
 constexpr int DEC_WG = 64;
 
+// One lane per segment. The two flag contexts' tables (slot -> symbol, frequencies, starts) are copied
+// to LDS: every block decodes a flag, most blocks nothing else. Work goes in rounds, as in the encoder:
+// each lane decodes flags up to its next differing block, then the lanes that stopped at one decode
+// and model it together, so one lane's differing block does not hold the other 63.
 template <int T>
 __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ in, const uint64_t* __restrict__ in_off,
                                                    const uint8_t* __restrict__ P, const uint8_t* __restrict__ seed,
@@ -241,6 +293,19 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
     using Y = Ty<T>;
     constexpr int BSP = (Y::BS + 3) & ~3;
     __shared__ __align__(4) uint8_t blk[DEC_WG * BSP];
+    __shared__ uint8_t flut[2][PSCALE];
+    __shared__ uint16_t ffreq[2][256];
+    __shared__ uint32_t fcum[2][256];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int tt = remap[FLAG + p];
+        for (int i = threadIdx.x; i < (int)PSCALE; i += DEC_WG) flut[p][i] = tt >= 0 ? lut[(size_t)tt * PSCALE + i] : 0;
+        for (int i = threadIdx.x; i < 256; i += DEC_WG) {
+            ffreq[p][i] = tt >= 0 ? freq[tt * 256 + i] : 0;
+            fcum[p][i] = tt >= 0 ? cum[tt * 257 + i] : 0u;
+        }
+    }
+    __syncthreads();
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
     uint8_t* fb = blk + threadIdx.x * BSP;
@@ -250,12 +315,18 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
     Dec d{0, in + in_off[s], remap, freq, cum, lut};
     for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | *d.ptr++;
     int prev = 1;
-    for (int64_t b = g.b0; b < g.b0 + g.nb; ++b) {
+    int64_t b = g.b0;
+    const int64_t bend = g.b0 + g.nb;
+    for (;;) {
+        bool pend = false;
+        for (; b < bend; ++b) {
+            prev = d.step(flut[prev], ffreq[prev], fcum[prev]) != 0;
+            if (!prev) { pend = true; break; }     // F holds P's bytes for the equal blocks (qr_prefill)
+        }
+        if (__ballot(pend) == 0) break;
+        if (!pend) continue;
         const uint8_t* pb = P + b * Y::BS;
         uint8_t* dst = F + b * Y::BS;
-        const int eq = d.get(FLAG + prev);
-        prev = eq;
-        if (eq) continue;                         // F holds P's bytes already (qr_prefill)
         for (int i = 0; i < Y::BS; ++i) fb[i] = 0;
         int vals[Y::NF];
         int any = 0;
@@ -292,6 +363,8 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
             put_code<T>(fb, w, q);
         }
         for (int i = 0; i < Y::BS; ++i) dst[i] = fb[i];
+        ++b;
+        prev = 0;
     }
 }
 
