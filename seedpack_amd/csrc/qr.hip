@@ -89,24 +89,6 @@ struct Enc {
     }
 };
 
-// Frequencies and starts of the flag symbols 0 and 1 in the two flag contexts (previous block
-// differing / equal), held in registers: every block codes a flag, most blocks nothing else. A context
-// without symbols in the batch reads as 0 (a valid batch never codes it).
-struct FlagTab {
-    uint32_t f[2][2], c[2][2];
-    __device__ __forceinline__ void load(const int* remap, const uint16_t* freq, const uint32_t* cum) {
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int tt = remap[FLAG + p];
-#pragma unroll
-            for (int v = 0; v < 2; ++v) {
-                f[p][v] = tt >= 0 ? freq[tt * 256 + v] : 0u;
-                c[p][v] = tt >= 0 ? cum[tt * 257 + v] : 0u;
-            }
-        }
-    }
-};
-
 // bytes kept free below the coder's write pointer while coding codes: the block's fields (up to three
 // symbols each) and its flag, at most two bytes per symbol
 template <int T> constexpr int64_t FIELD_ROOM = 6 * Ty<T>::NF + 16;
@@ -261,26 +243,23 @@ struct Dec {
     const uint16_t* freq;
     const uint32_t* cum;
     const uint8_t* lut;
-    __device__ __forceinline__ int step(const uint8_t* tl, const uint16_t* tf, const uint32_t* tc) {
+    __device__ __forceinline__ int get(int tab) {
+        const int tt = remap[tab];
         const uint32_t slot = x & (PSCALE - 1);
-        const int v = tl[slot];
-        x = tf[v] * (x >> PB) + slot - tc[v];
+        const int v = lut[(size_t)tt * PSCALE + slot];
+        x = freq[tt * 256 + v] * (x >> PB) + slot - cum[tt * 257 + v];
         // a valid stream needs at most two bytes here (x >= 2^11 before them); the cap ends the
         // loop on a damaged stream instead of spinning on zero bytes
 #pragma unroll
         for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | *ptr++;
         return v;
     }
-    __device__ __forceinline__ int get(int tab) {
-        const int tt = remap[tab];
-        return step(lut + (size_t)tt * PSCALE, freq + tt * 256, cum + tt * 257);
-    }
 };
 
 constexpr int DEC_WG = 64;
 
-// One lane per segment. The two flag contexts' tables (slot -> symbol, frequencies, starts) are copied
-// to LDS: every block decodes a flag, most blocks nothing else. Work goes in rounds, as in the encoder:
+// One lane per segment; the flags are decoded from the register flag table. Work goes in rounds, as in
+// the encoder:
 // each lane decodes flags up to its next differing block, then the lanes that stopped at one decode
 // and model it together, so one lane's differing block does not hold the other 63.
 template <int T>
@@ -293,21 +272,10 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
     using Y = Ty<T>;
     constexpr int BSP = (Y::BS + 3) & ~3;
     __shared__ __align__(4) uint8_t blk[DEC_WG * BSP];
-    __shared__ uint8_t flut[2][PSCALE];
-    __shared__ uint16_t ffreq[2][256];
-    __shared__ uint32_t fcum[2][256];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int tt = remap[FLAG + p];
-        for (int i = threadIdx.x; i < (int)PSCALE; i += DEC_WG) flut[p][i] = tt >= 0 ? lut[(size_t)tt * PSCALE + i] : 0;
-        for (int i = threadIdx.x; i < 256; i += DEC_WG) {
-            ffreq[p][i] = tt >= 0 ? freq[tt * 256 + i] : 0;
-            fcum[p][i] = tt >= 0 ? cum[tt * 257 + i] : 0u;
-        }
-    }
-    __syncthreads();
     const int s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= nseg) return;
+    FlagTab ft;
+    ft.load(remap, freq, cum);
     uint8_t* fb = blk + threadIdx.x * BSP;
     const SG g = sg[s];
     const TM m = tm[g.t];
@@ -320,7 +288,7 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
     for (;;) {
         bool pend = false;
         for (; b < bend; ++b) {
-            prev = d.step(flut[prev], ffreq[prev], fcum[prev]) != 0;
+            prev = ft.get(d.x, d.ptr, prev);
             if (!prev) { pend = true; break; }     // F holds P's bytes for the equal blocks (qr_prefill)
         }
         if (__ballot(pend) == 0) break;

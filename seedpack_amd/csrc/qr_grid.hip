@@ -280,9 +280,7 @@ struct Code {
     const uint16_t* freq;
     const uint32_t* cum;
     int lane;
-    __device__ __forceinline__ void put(int tab, uint32_t sym) {
-        const int tt = remap[tab];
-        const uint32_t f = freq[tt * 256 + sym], c = cum[tt * 257 + sym];
+    __device__ __forceinline__ void put_fc(uint32_t f, uint32_t c) {
         const uint32_t xm = ((RANS_L >> PB) << 8) * f;
         while (x >= xm) {
             --ptr;
@@ -290,6 +288,10 @@ struct Code {
             x >>= 8;
         }
         x = ((x / f) << PB) + (x % f) + c;
+    }
+    __device__ __forceinline__ void put(int tab, uint32_t sym) {
+        const int tt = remap[tab];
+        put_fc(freq[tt * 256 + sym], cum[tt * 257 + sym]);
     }
 };
 
@@ -426,13 +428,19 @@ __global__ __launch_bounds__(64) void k_qrg_enc(const uint8_t* __restrict__ F, c
     load_keys<T>(gk, lane, keys);
     Code e{RANS_L, end, remap, freq, cum, lane};
     auto stop = [base](Code& c) { return c.ptr - base < ROOM; };
+    // the segment's block flags as one mask (a segment has at most 64 blocks), the flag tables in registers
+    static_assert(SEG_BLOCKS<T> <= 64, "one mask bit per block of the segment");
+    const uint64_t nm = __ballot(lane < g.nb && neq[g.b0 + lane] != 0);
+    FlagTab ft;
+    ft.load(remap, freq, cum);
     for (int64_t b = g.b0 + g.nb - 1; b >= g.b0; --b) {
         const uint8_t* fb = F + b * Y::BS;
         const uint8_t* pb = P + b * Y::BS;
-        const bool eq = !neq[b];
-        const int prev = b > g.b0 ? (neq[b - 1] ? 0 : 1) : 1;
+        const int i = (int)(b - g.b0);
+        const bool eq = !((nm >> i) & 1u);
+        const int prev = i > 0 ? (((nm >> (i - 1)) & 1u) ? 0 : 1) : 1;
         if (eq) {
-            e.put(FLAG + prev, 1);
+            e.put_fc(ft.f[prev][1], ft.c[prev][1]);
             if (stop(e)) { if (lane == 0) out_len[s] = 0xffffffffu; return; }
             continue;
         }
@@ -461,7 +469,7 @@ __global__ __launch_bounds__(64) void k_qrg_enc(const uint8_t* __restrict__ F, c
                 e.put(kd * 2 + anyk[k], (uint32_t)(dl[k] & 255));
             }
         }
-        e.put(FLAG + prev, 0);
+        e.put_fc(ft.f[prev][0], ft.c[prev][0]);
     }
     for (int i = 0; i < 4; ++i) {
         --e.ptr;
@@ -516,11 +524,13 @@ __global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, 
     load_keys<T>(gk, lane, keys);
     Decoder d{0, in + in_off[s], remap, freq, cum, lut};
     for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | *d.ptr++;
+    FlagTab ft;
+    ft.load(remap, freq, cum);
     int prev = 1;
     for (int64_t b = g.b0; b < g.b0 + g.nb; ++b) {
         const uint8_t* pb = P + b * Y::BS;
         uint8_t* dst = F + b * Y::BS;
-        const int eq = d.get(FLAG + prev);
+        const int eq = ft.get(d.x, d.ptr, prev);
         prev = eq;
         if (eq) continue;                         // F holds P's bytes already (qr_prefill)
         // every lane applies the same writes to the block in LDS, so each lane's reads see them

@@ -28,6 +28,34 @@ constexpr int NTAB2 = NTAB + 208;
 constexpr int FESC_LO = 8, FESC_HI = 9;
 constexpr int MAXF = 34;
 
+// Frequencies and starts of the flag symbols 0 and 1 in the two flag contexts (previous block
+// differing / equal), held in registers: every block codes a flag, most blocks nothing else. A context
+// without symbols in the batch reads as 0 (a valid batch never codes it).
+struct FlagTab {
+    uint32_t f[2][2], c[2][2];
+    __device__ __forceinline__ void load(const int* remap, const uint16_t* freq, const uint32_t* cum) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int tt = remap[FLAG + p];
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+                f[p][v] = tt >= 0 ? freq[tt * 256 + v] : 0u;
+                c[p][v] = tt >= 0 ? cum[tt * 257 + v] : 0u;
+            }
+        }
+    }
+    // one flag decoded from state x in context p: symbol 1's slots start at c[p][1], symbol 0's at 0 (a
+    // valid stream's slot is in one of the two ranges); renormalised from ptr as the general step
+    __device__ __forceinline__ int get(uint32_t& x, const uint8_t*& ptr, int p) const {
+        const uint32_t slot = x & (PSCALE - 1);
+        const int v = slot >= c[p][1] ? 1 : 0;
+        x = f[p][v] * (x >> PB) + slot - c[p][v];
+#pragma unroll
+        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | *ptr++;
+        return v;
+    }
+};
+
 // kvalues_iq4nl (ggml-common.h:1120) as floats: the non-linear code values of IQ4_NL / IQ4_XS
 __constant__ const float KV[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
 
