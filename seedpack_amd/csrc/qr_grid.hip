@@ -134,20 +134,50 @@ struct Unit {
     float s, dl;
 };
 
+// A block's 256 seed values and the imatrix entries of their columns, staged in LDS by the wave (four
+// of each per lane) so the model reads neither from global memory one value at a time.
+struct BlockSeed {
+    float* x;
+    float* im;
+    bool has_im;
+};
+// stages block gw0's values into bs (all 64 lanes of the single-wave workgroup take part) and returns
+// the grid types' sigma2 from the in-order sum of squares of the 256 seed values (qr.py:557-560)
+template <int T>
+__device__ __forceinline__ float stage_block(const BlockSeed& bs, int lane, int st, const uint8_t* sbase, int64_t gw0,
+                                             const float* im, int cols) {
+    __syncthreads();                              // the previous block's readers are done
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = lane + 64 * k;
+        float x, h;
+        seed_val(st, sbase, gw0 + i, x, h);
+        bs.x[i] = x;
+        if (im) bs.im[i] = im[(gw0 + i) % cols];
+    }
+    __syncthreads();
+    float sx2 = 0.f;
+    for (int i = 0; i < 256; i += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(bs.x + i);
+        sx2 += q.x * q.x;
+        sx2 += q.y * q.y;
+        sx2 += q.z * q.z;
+        sx2 += q.w * q.w;
+    }
+    return (T == 16 || T == 17) ? sx2 * (1.0f / 256.f) : (2.f * sx2) * (1.0f / 256.f);
+}
+
 // targets, weights and seed signs of unit u (qr.py:569-593)
 template <int T>
-__device__ __forceinline__ void unit_model(const uint8_t* fb, int u, int st, const uint8_t* sbase, int64_t gw0, float sigma2,
-                                           const float* im, int cols, Unit& g) {
+__device__ __forceinline__ void unit_model(const uint8_t* fb, int u, const BlockSeed& bs, float sigma2, Unit& g) {
     using Gt = G<T>;
     gscale<T>(fb, u, g.s, g.dl);
     float x[8], v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int64_t gw = gw0 + 8 * u + i;
-        float h;
-        seed_val(st, sbase, gw, x[i], h);
+        x[i] = bs.x[8 * u + i];
         float wi = sqrtf(sigma2 + x[i] * x[i]);
-        if (im) wi = wi * im[gw % cols];
+        if (bs.has_im) wi = wi * bs.im[8 * u + i];
         g.w[i] = wi;
         g.pn[i] = x[i] < 0.f;
         v[i] = Gt::SGN ? fabsf(x[i]) : x[i];
@@ -237,18 +267,6 @@ __device__ __forceinline__ void wave_argmin(float& d, int& k) {
     }
 }
 
-// the in-order sum of squares of the block's 256 seed values and the grid types' sigma2 (qr.py:557-560)
-template <int T>
-__device__ __forceinline__ float block_sigma2(int st, const uint8_t* sbase, int64_t gw0) {
-    float sx2 = 0.f;
-    for (int i = 0; i < 256; ++i) {
-        float x, h;
-        seed_val(st, sbase, gw0 + i, x, h);
-        sx2 += x * x;
-    }
-    return (T == 16 || T == 17) ? sx2 * (1.0f / 256.f) : (2.f * sx2) * (1.0f / 256.f);
-}
-
 __device__ __forceinline__ int rank_ctx0(int mv, int64_t col, int cols) {
     return mv >= 2 ? GRANK2 + 4 * (cols <= 0 || col < 256 ? 0 : 1 + (int)min((int64_t)2, col * 3 / cols)) : GRID_RANK;
 }
@@ -300,14 +318,15 @@ struct Code {
 template <int T, class S, class Stop>
 __device__ __forceinline__ bool grid_walk(S& out, Stop stop, const uint8_t* fb, const uint8_t* pb, const uint16_t* gk,
                                           const uint32_t (&keys)[G<T>::PER], float* tab, int lane, int st,
-                                          const uint8_t* sbase, int64_t gw0, int cols, const float* im, int mv) {
+                                          const uint8_t* sbase, int64_t gw0, int cols, const float* im, int mv,
+                                          const BlockSeed& bs) {
     using Gt = G<T>;
-    const float sigma2 = block_sigma2<T>(st, sbase, gw0);
+    const float sigma2 = stage_block<T>(bs, lane, st, sbase, gw0, im, cols);
     const int64_t col0 = cols > 0 ? gw0 % cols : 0;
     for (int u = 31; u >= 0; --u) {
         const int rank0 = rank_ctx0(mv, col0 + 8 * u, cols), sign0 = sign_ctx0(mv, col0 + 8 * u, cols);
         Unit g;
-        unit_model<T>(fb, u, st, sbase, gw0, sigma2, im, cols, g);
+        unit_model<T>(fb, u, bs, sigma2, g);
         int tg[2] = {0, 0};
 #pragma unroll
         for (int gg = 0; gg < Gt::NG; ++gg) tg[gg] = get_gidx<T>(fb, u * Gt::NG + gg);
@@ -369,6 +388,7 @@ __global__ __launch_bounds__(64) void k_qrg_hist(const uint8_t* __restrict__ F, 
     constexpr int SEG = SEG_BLOCKS<T>;
     const int lane = threadIdx.x;
     __shared__ float tab[TAB_N<T>];
+    __shared__ __align__(16) float sx[256], sim[256];
     uint32_t keys[G<T>::PER];
     load_keys<T>(gk, lane, keys);
     const uint32_t n = *nlist;
@@ -398,7 +418,7 @@ __global__ __launch_bounds__(64) void k_qrg_hist(const uint8_t* __restrict__ F, 
         }
         const float* im = (m.imx_off >= 0 && m.cols > 0) ? imx + m.imx_off : nullptr;
         grid_walk<T>(out, [](Count&) { return false; }, fb, pb, gk, keys, tab, lane, m.seed_type, seed + m.seed_off,
-                     (b - m.blk0) * Y::QK, m.cols, im, mv);
+                     (b - m.blk0) * Y::QK, m.cols, im, mv, BlockSeed{sx, sim, im != nullptr});
     }
 }
 
@@ -424,6 +444,7 @@ __global__ __launch_bounds__(64) void k_qrg_enc(const uint8_t* __restrict__ F, c
     uint8_t* const base = out + (uint64_t)s * cap;
     uint8_t* const end = base + cap;
     __shared__ float tab[TAB_N<T>];
+    __shared__ __align__(16) float sx[256], sim[256];
     uint32_t keys[G<T>::PER];
     load_keys<T>(gk, lane, keys);
     Code e{RANS_L, end, remap, freq, cum, lane};
@@ -444,7 +465,8 @@ __global__ __launch_bounds__(64) void k_qrg_enc(const uint8_t* __restrict__ F, c
             if (stop(e)) { if (lane == 0) out_len[s] = 0xffffffffu; return; }
             continue;
         }
-        if (!grid_walk<T>(e, stop, fb, pb, gk, keys, tab, lane, m.seed_type, sbase, (b - m.blk0) * Y::QK, m.cols, im, mv)) {
+        if (!grid_walk<T>(e, stop, fb, pb, gk, keys, tab, lane, m.seed_type, sbase, (b - m.blk0) * Y::QK, m.cols, im, mv,
+                          BlockSeed{sx, sim, im != nullptr})) {
             if (lane == 0) out_len[s] = 0xffffffffu;
             return;
         }
@@ -512,6 +534,7 @@ __global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, 
     constexpr int BSW = (Y::BS + 3) / 4;
     __shared__ uint32_t blk32[BSW];
     __shared__ float tab[TAB_N<T>];
+    __shared__ __align__(16) float sx[256], sim[256];
     uint8_t* blk = reinterpret_cast<uint8_t*>(blk32);
     const int lane = threadIdx.x;
     const int s = blockIdx.x;
@@ -520,6 +543,7 @@ __global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, 
     const TM m = tm[g.t];
     const uint8_t* sbase = seed + m.seed_off;
     const float* im = (m.imx_off >= 0 && m.cols > 0) ? imx + m.imx_off : nullptr;
+    const BlockSeed bs{sx, sim, im != nullptr};
     uint32_t keys[Gt::PER];
     load_keys<T>(gk, lane, keys);
     Decoder d{0, in + in_off[s], remap, freq, cum, lut};
@@ -557,7 +581,7 @@ __global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, 
         set_fields<T>(blk, vals);
         const int64_t gw0 = (b - m.blk0) * Y::QK;
         const int64_t col0 = m.cols > 0 ? gw0 % m.cols : 0;
-        const float sigma2 = block_sigma2<T>(m.seed_type, sbase, gw0);
+        const float sigma2 = stage_block<T>(bs, lane, m.seed_type, sbase, gw0, im, m.cols);
         for (int u = 0; u < 32; ++u) {
             const int rank0 = rank_ctx0(mv, col0 + 8 * u, m.cols), sign0 = sign_ctx0(mv, col0 + 8 * u, m.cols);
             if constexpr (T == 29) {
@@ -565,7 +589,7 @@ __global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, 
                 if (sh ^ get_shift(pb, u)) put_shift(blk, u);
             }
             Unit gu;
-            unit_model<T>(blk, u, m.seed_type, sbase, gw0, sigma2, im, m.cols, gu);
+            unit_model<T>(blk, u, bs, sigma2, gu);
             int tg[2] = {0, 0};
 #pragma unroll
             for (int gg = 0; gg < Gt::NG; ++gg) {
