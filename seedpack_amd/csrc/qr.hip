@@ -187,11 +187,17 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
     const SG g = sg[s];
     const TM m = tm[g.t];
     const int nb = g.nb < SEG_BLOCKS<T> ? g.nb : SEG_BLOCKS<T>;
+    // 32 flags per word: unconditional loads (indices clamped into the segment), so each word's loads
+    // are in flight together instead of one branch and one wait per flag
     for (int w = 0; w < NW; ++w) {
         uint32_t v = 0;
+        if (32 * w < nb) {
+            uint8_t f[32];
 #pragma unroll
-        for (int j = 0; j < 32; ++j)
-            if (32 * w + j < nb) v |= (uint32_t)(neq[g.b0 + 32 * w + j] != 0) << j;
+            for (int j = 0; j < 32; ++j) f[j] = neq[g.b0 + min(32 * w + j, nb - 1)];
+#pragma unroll
+            for (int j = 0; j < 32; ++j) v |= (uint32_t)(f[j] != 0 && 32 * w + j < nb) << j;
+        }
         nbits[lane][w] = v;
     }
     auto differs = [&](int i) { return (nbits[lane][i >> 5] >> (i & 31)) & 1u; };
@@ -219,11 +225,31 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
         const int64_t b = g.b0 + i;
         const uint32_t k = idx_of[b];
         if (k != 0xffffffffu) {
-            // the block's symbols from the parallel pass: the codes (checked for room) first
+            // the block's symbols from the parallel pass: the codes (checked for room) first. Eight
+            // symbols' table entries are fetched together ahead of their coding steps, so the coder's
+            // chain waits on memory once per eight symbols
             const uint32_t* q = syms + (size_t)k * MAXSYM<T>;
             const int n = nsym[k];
-            for (int j = 0; j < n; ++j)
-                if (!put((int)(q[j] >> 8), q[j] & 255u, j < Y::QK)) { out_len[s] = 0xffffffffu; return; }
+            for (int j0 = 0; j0 < n; j0 += 8) {
+                uint32_t fq[8], cq[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    fq[t] = 1u;
+                    cq[t] = 0u;
+                    if (j0 + t < n) {
+                        const uint32_t wd = q[j0 + t];
+                        const int tt = remap[wd >> 8];
+                        fq[t] = freq[tt * 256 + (wd & 255u)];
+                        cq[t] = cum[tt * 257 + (wd & 255u)];
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    if (j0 + t >= n) break;
+                    e.put_fc(fq[t], cq[t]);
+                    if (j0 + t < Y::QK && e.ptr - base < FIELD_ROOM<T>) { out_len[s] = 0xffffffffu; return; }
+                }
+            }
         } else if (!block_syms<T>(put, F + b * Y::BS, P + b * Y::BS, sbase, m, b, mv)) {
             out_len[s] = 0xffffffffu;
             return;
@@ -243,8 +269,8 @@ struct Dec {
     const uint16_t* freq;
     const uint32_t* cum;
     const uint8_t* lut;
-    __device__ __forceinline__ int get(int tab) {
-        const int tt = remap[tab];
+    __device__ __forceinline__ int get(int tab) { return get_tt(remap[tab]); }
+    __device__ __forceinline__ int get_tt(int tt) {
         const uint32_t slot = x & (PSCALE - 1);
         const int v = lut[(size_t)tt * PSCALE + slot];
         x = freq[tt * 256 + v] * (x >> PB) + slot - cum[tt * 257 + v];
@@ -318,17 +344,29 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
         set_fields<T>(fb, vals);
         const int64_t gw0 = (b - m.blk0) * Y::QK;
         const int64_t col0 = m.cols > 0 ? gw0 % m.cols : 0;
+        // the codes' contexts depend on the decoded fields, the seed and P only: eight weights' contexts
+        // and table numbers are made ahead of their decoding steps, so the chain waits on the seed and
+        // the remap table once per eight weights
+        static_assert(Y::SUBLEN % 8 == 0, "weight groups of eight within a sub-block");
         float a = 0.f, c = 0.f;
-        for (int w = 0; w < Y::QK; ++w) {
-            if (w % Y::SUBLEN == 0) wscale<T>(fb, w, a, c);
-            float x, h;
-            seed_val(m.seed_type, sbase, gw0 + w, x, h);
-            int r, sg_, ctx;
-            predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
-            const int v = d.get(ctx);
-            int q = r + sg_ * s8((uint32_t)v);
-            if (T == 8) q = s8((uint32_t)q);
-            put_code<T>(fb, w, q);
+        for (int w0 = 0; w0 < Y::QK; w0 += 8) {
+            if (w0 % Y::SUBLEN == 0) wscale<T>(fb, w0, a, c);
+            int r8[8], sg8[8], tt8[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                float x, h;
+                seed_val(m.seed_type, sbase, gw0 + w0 + t, x, h);
+                int ctx;
+                predict<T>(a, c, pb, w0 + t, x, h, mv, pos8(col0 + w0 + t, m.cols), r8[t], sg8[t], ctx);
+                tt8[t] = remap[ctx];
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int v = d.get_tt(tt8[t]);
+                int q = r8[t] + sg8[t] * s8((uint32_t)v);
+                if (T == 8) q = s8((uint32_t)q);
+                put_code<T>(fb, w0 + t, q);
+            }
         }
         for (int i = 0; i < Y::BS; ++i) dst[i] = fb[i];
         ++b;
