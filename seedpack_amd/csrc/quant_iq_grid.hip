@@ -73,9 +73,12 @@ __device__ __forceinline__ void grid_point(const uint8_t* grid, int j, int (&q)[
 // the least key is the smallest d2 at the smallest position -- the reference's first strict minimum.
 // Entries are kept only when d2 < FLT_MAX (the reference's initial best); a list with none keeps its
 // first point (the reference asserts there instead).
-// Entries per piece: long lists (the 8-dimensional lattices, 35 entries on average when off the grid)
-// take 8, the 4-dimensional ones (about 14) take 4.
+// Entries per piece (measured per type on the configuration-3 tensors): long lists (the
+// 8-dimensional lattices, 35 entries on average when off the grid) take 8, the 4-dimensional ones
+// (about 14) take 4; IQ2_S takes 4 and IQ3_S 6.
 template <int D> constexpr int nb_piece() { return D == 8 ? 8 : 4; }
+// bits of the largest piece count per list, ceil(511 / R)
+constexpr int nb_count_bits(int r) { return 32 - __builtin_clz((unsigned)((511 + r - 1) / r)); }
 
 template <int D>
 struct NbWave {
@@ -105,11 +108,10 @@ __device__ __forceinline__ int wrow_at(int t, int v) { return (v + t) % (N / 4);
 
 // The level index of the best neighbour of group k for the lanes with `off` set (gi: the map's
 // negative entry for the group's rounded point); called by all lanes of the wave together.
-template <int D, int N>
+template <int D, int N, int R = nb_piece<D>()>
 __device__ int wave_best_neighbour(const NbCtx& c, int k, bool off, int gi, const float (&xval)[N], float scale,
                                    const uint16_t* __restrict__ nbt, const uint8_t* grid) {
-    constexpr int R = nb_piece<D>();
-    constexpr int NPB = R == 8 ? 7 : 8;   // bits of the piece count ceil(511 / R)
+    constexpr int NPB = nb_count_bits(R);
     NbWave<D>& W = *reinterpret_cast<NbWave<D>*>(c.w);
     constexpr unsigned long long INIT = (unsigned long long)0x7f7fffffu << 32;   // (FLT_MAX, position 0)
     const int lane = (int)__lane_id();
@@ -159,21 +161,25 @@ __device__ int wave_best_neighbour(const NbCtx& c, int k, bool off, int gi, cons
             const int pos0 = (q - __float_as_int(meta.z)) * R;
             float best = FLT_BIG;
             uint32_t bj = 0;
+            // the piece's list entries, then their codebook points, are all requested before the
+            // first distance is formed (one wait each instead of a load chain per entry); positions
+            // past the list end re-read its last entry and are left out of the minimum
+            int jj[R];
+#pragma unroll
+            for (int e = 0; e < R; ++e) jj[e] = nbt[p + 1 + min(pos0 + e, L - 1)];
+            int qg[R][D];
+#pragma unroll
+            for (int e = 0; e < R; ++e) grid_point<D>(grid, jj[e], qg[e]);
 #pragma unroll
             for (int e = 0; e < R; ++e) {
                 const int pos = pos0 + e;
-                if (pos < L) {
-                    const int j = nbt[p + 1 + pos];
-                    int qg[D];
-                    grid_point<D>(grid, j, qg);
-                    float d2 = 0;
+                float d2 = 0;
 #pragma unroll
-                    for (int i = 0; i < D; ++i) {
-                        const float diff = s * (float)qg[i] - xg[i];
-                        d2 += wv[i] * diff * diff;
-                    }
-                    if (d2 < best) { best = d2; bj = ((uint32_t)pos << 16) | (uint32_t)j; }
+                for (int i = 0; i < D; ++i) {
+                    const float diff = s * (float)qg[e][i] - xg[i];
+                    d2 += wv[i] * diff * diff;
                 }
+                if (pos < L && d2 < best) { best = d2; bj = ((uint32_t)pos << 16) | (uint32_t)jj[e]; }
             }
             if (best < FLT_BIG) atomicMin(&W.slot[o], ((unsigned long long)__float_as_uint(best) << 32) | bj);
         }
@@ -299,7 +305,8 @@ struct SubOut {
 // otherwise the levels come from the grid point (IQ3_*): the same values either way.
 // All lanes of the wave run it (the neighbour searches are wave-wide); a lane whose sub-block is
 // empty (`live` false) searches nothing and its result is not used.
-template <int N, int D, int KMAXQ, int IS_LO, int IS_HI, bool ONGRID_INIT, bool REFIT_ALL, bool SET_L_IN_REFIT>
+template <int N, int D, int KMAXQ, int IS_LO, int IS_HI, bool ONGRID_INIT, bool REFIT_ALL, bool SET_L_IN_REFIT,
+          int R = nb_piece<D>()>
 __device__ __forceinline__ float lattice_search(bool live, const float (&xval)[N], const float (&w)[N], const NbCtx& nc,
                                                 float max, float step, const IqDeviceTable& tab, const uint8_t* grid,
                                                 int (&idx)[N / D]) {
@@ -322,7 +329,7 @@ __device__ __forceinline__ float lattice_search(bool live, const float (&xval)[N
 #pragma unroll
         for (int k = 0; k < NG; ++k) {
             ona[k] = ga[k] >= 0;
-            const int nu = wave_best_neighbour<D, N>(nc, k, live && ga[k] < 0, ga[k], xval, this_scale, tab.nb, grid);
+            const int nu = wave_best_neighbour<D, N, R>(nc, k, live && ga[k] < 0, ga[k], xval, this_scale, tab.nb, grid);
             if (ga[k] < 0) ia[k] = nu;
         }
         float sumqx, sumq2;
@@ -346,7 +353,7 @@ __device__ __forceinline__ float lattice_search(bool live, const float (&xval)[N
         const bool redo = refit && (REFIT_ALL || !on[k]);
         const int u = round_group<D, N, KMAXQ>(xval, D * k, id);
         const int gi = tab.map[u];
-        const int nu = wave_best_neighbour<D, N>(nc, k, redo && gi < 0, gi, xval, scale, tab.nb, grid);
+        const int nu = wave_best_neighbour<D, N, R>(nc, k, redo && gi < 0, gi, xval, scale, tab.nb, grid);
         if (redo) idx[k] = gi < 0 ? nu : u;
     }
     if (refit) {
@@ -457,7 +464,7 @@ __device__ __forceinline__ SubOut iq2_16_sub(const float (&x)[16], const float (
     const bool live = !(max < (XS ? GROUP_MAX_EPS : 1e-8f));   // GROUP_MAX_EPS_IQ2_S = 1e-8f
     o.empty = !live;
     int idx[2] = {0, 0};
-    float scale = lattice_search<16, 8, 3, -9, 9, true, false, true>(live, xval, w, nc, max, 0.1f, tab, grid, idx);
+    float scale = lattice_search<16, 8, 3, -9, 9, true, false, true, XS ? 8 : 4>(live, xval, w, nc, max, 0.1f, tab, grid, idx);
     if (!live) return o;
     if (scale < 0) {
         scale = -scale;
@@ -488,7 +495,7 @@ __device__ __forceinline__ SubOut iq3_sub(const float (&x)[32], const float (&w)
     int idx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float scale;
     if constexpr (XXS) scale = lattice_search<32, 4, 8, -15, 15, true, false, false>(live, xval, w, nc, max, 0.2f, tab, grid, idx);
-    else scale = lattice_search<32, 4, 8, -9, 9, false, true, false>(live, xval, w, nc, max, 0.2f, tab, grid, idx);
+    else scale = lattice_search<32, 4, 8, -9, 9, false, true, false, 6>(live, xval, w, nc, max, 0.2f, tab, grid, idx);
     if (!live) return o;
     if (scale < 0) {
         scale = -scale;
