@@ -86,6 +86,7 @@ struct NbWave {
     // the records of 8 consecutive owners on distinct banks
     __align__(16) float rec[64][12];
     unsigned long long slot[64];          // per owner lane: least key so far
+    int mark[D == 4 ? 64 : 1];            // (D = 4) per round: the lane whose pieces start at this slot, else -1
 };
 
 struct NbCtx {
@@ -96,6 +97,18 @@ struct NbCtx {
 
 // LDS writes of the wave's lanes complete before its later LDS reads, and no compiler reordering
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// inclusive prefix maximum over the 64 lanes (-1 is the identity): shifts by 1, 2, 4, 8 inside each
+// row of 16 lanes, then lane 15 of rows 0 and 2 into rows 1 and 3, then lane 31 into rows 2 and 3
+__device__ __forceinline__ int wave_prefix_max(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x111, 0xf, 0xf, false));   // row_shr:1
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x112, 0xf, 0xf, false));   // row_shr:2
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x114, 0xf, 0xf, false));   // row_shr:4
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x118, 0xf, 0xf, false));   // row_shr:8
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x142, 0xa, 0xf, false));   // row_bcast:15
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x143, 0xc, 0xf, false));   // row_bcast:31
+    return v;
+}
 
 // The device map holds, for a point off the grid, -1 - (list offset << 9 | list length)
 __device__ __forceinline__ int nb_offset(int gi) { return (-1 - gi) >> 9; }
@@ -135,15 +148,30 @@ __device__ int wave_best_neighbour(const NbCtx& c, int k, bool off, int gi, cons
         r[D / 4] = make_float4(scale, __int_as_float(ptr), __int_as_float(first), __int_as_float(len));
         W.slot[lane] = INIT;
     }
+    if constexpr (D == 4) W.mark[lane] = -1;
     wave_lds_sync();
     for (int base = 0; base < total; base += 64) {
         const int q = base + lane;
-        // the owner of piece q: the number of lanes whose pieces end at or before q (incl rises with lane)
+        // the owner of piece q, the lane whose pieces [first, incl) hold q
         int o = 0;
+        if constexpr (D == 4) {
+            // short lists, many owners per round: each lane whose pieces meet this round marks the
+            // slot of its first one in it (distinct slots; slot 0 always has one, the owner of piece
+            // `base`), and the owner of q is the last mark at or before q; each lane resets its slot
+            // after reading it
+            if (np > 0 && first < base + 64 && incl > base) W.mark[(first > base ? first : base) - base] = lane;
+            wave_lds_sync();
+            const int m = W.mark[lane];
+            W.mark[lane] = -1;
+            o = max(wave_prefix_max(m), 0);
+        } else {
+            // long lists, few owners per round: the number of lanes whose pieces end at or before q
+            // (incl rises with lane), by binary search
 #pragma unroll
-        for (int st = 32; st >= 1; st >>= 1) {
-            const int probe = __shfl(incl, o + st - 1);
-            if (probe <= q) o += st;
+            for (int st = 32; st >= 1; st >>= 1) {
+                const int probe = __shfl(incl, o + st - 1);
+                if (probe <= q) o += st;
+            }
         }
         if (q < total) {
             const float4* r = reinterpret_cast<const float4*>(W.rec[o]);
@@ -868,6 +896,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
     const NbCtx nc{&nbw[IQ1 ? 0 : threadIdx.x / 64], reinterpret_cast<const float*>(wa_park), (int)(threadIdx.x & ~63u)};
     for (int i = threadIdx.x; i < C::GBYTES / 16; i += WG)
         reinterpret_cast<uint4*>(grid)[i] = reinterpret_cast<const uint4*>(tab.grid)[i];
+    if constexpr (!IQ1) {
+        // every owner record starts as an empty list at offset 0 (scale, offset, first piece, length
+        // all zero), so a record is never read before it names a list of the table
+        reinterpret_cast<float4*>(nbw[threadIdx.x / 64].rec[threadIdx.x % 64])[C::D / 4] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     __syncthreads();
     const int lsb = threadIdx.x / G, sub = threadIdx.x % G;
     const int64_t sb0 = (int64_t)blockIdx.x * SBW;
