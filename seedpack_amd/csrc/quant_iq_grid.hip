@@ -584,25 +584,41 @@ constexpr float IQ1M_DELTA = 0.125f;    // ggml-common.h IQ1M_DELTA
 
 __device__ __forceinline__ float pick3(int lv, float a, float b, float c) { return lv == 0 ? a : (lv == 1 ? b : c); }
 
-// iq1_find_best_neighbour2 (ggml-quants.c:4444-4499) over the listed neighbours, distance with the
-// level values g0, g1, g2. The reference scans the whole grid when no listed point gives a distance
-// below FLT_MAX and aborts if that scan finds none; with finite inputs a listed point always wins.
+// iq1_find_best_neighbour2 (ggml-quants.c:4444-4499) over the listed neighbours. A point's coordinate
+// value q (1, 3, 5 for levels 0, 1, 2) selects the level value g = -1 + d, d, 1 + d (d = +-delta);
+// here g is formed as 0.5 q + gc with gc = d - 1.5, which is exact (the values are small dyadic
+// rationals), so the distance sees the reference's constants. The reference scans the whole grid
+// when no listed point gives a distance below FLT_MAX and aborts if that scan finds none; with finite
+// inputs a listed point always wins.
+#ifndef IQ1_RUN
+#define IQ1_RUN 4
+#endif
 __device__ __forceinline__ int iq1_neighbour(const uint16_t* __restrict__ nb, const uint8_t* grid, const float (&xv)[8],
-                                             const float (&wv)[8], float scale, float g0, float g1, float g2, int (&Lg)[8]) {
+                                             const float (&wv)[8], float scale, float gc, int (&Lg)[8]) {
     const int n = nb[0];
     float best = FLT_BIG;
     int gi = nb[1];
-    for (int jj = 1; jj <= n; ++jj) {
-        const int j = nb[jj];
-        int q[8];
-        grid_point<8>(grid, j, q);
-        float d2 = 0;
+    // the list in runs of IQ1_RUN entries: a run's entries and codebook points are all requested
+    // before its distances are formed (the lists hold ~300 points); entries past the end re-read the
+    // last one and are left out, and the first strict minimum in list order wins as in the reference
+    for (int j0 = 1; j0 <= n; j0 += IQ1_RUN) {
+        int jj[IQ1_RUN];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float diff = scale * pick3((q[i] - 1) / 2, g0, g1, g2) - xv[i];
-            d2 += wv[i] * diff * diff;
+        for (int e = 0; e < IQ1_RUN; ++e) jj[e] = nb[min(j0 + e, n)];
+        uint2 gp[IQ1_RUN];   // the points stay packed (one byte per coordinate) until used
+#pragma unroll
+        for (int e = 0; e < IQ1_RUN; ++e) gp[e] = reinterpret_cast<const uint2*>(grid)[jj[e]];
+#pragma unroll
+        for (int e = 0; e < IQ1_RUN; ++e) {
+            float d2 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float q = (float)(((i < 4 ? gp[e].x : gp[e].y) >> (8 * (i & 3))) & 0xff);
+                const float diff = scale * (0.5f * q + gc) - xv[i];
+                d2 += wv[i] * diff * diff;
+            }
+            if (j0 + e <= n && d2 < best) { best = d2; gi = jj[e]; }
         }
-        if (d2 < best) { best = d2; gi = j; }
     }
     int q[8];
     grid_point<8>(grid, gi, q);
@@ -628,8 +644,7 @@ __device__ __forceinline__ float iq1_snap(const float (&x)[N], const float (&w)[
             int Lg[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) { xv[i] = x[8 * k + i]; wv[i] = w[8 * k + i]; }
-            gi = pos[k] ? iq1_neighbour(tab.nb + nb_offset(gi), grid, xv, wv, scale, XP0, XP1, XP2, Lg)
-                        : iq1_neighbour(tab.nb + nb_offset(gi), grid, xv, wv, scale, XM0, XM1, XM2, Lg);
+            gi = iq1_neighbour(tab.nb + nb_offset(gi), grid, xv, wv, scale, pos[k] ? IQ1S_DELTA - 1.5f : -IQ1S_DELTA - 1.5f, Lg);
 #pragma unroll
             for (int i = 0; i < 8; ++i) L[8 * k + i] = Lg[i];
         }
