@@ -77,8 +77,6 @@ __device__ __forceinline__ void grid_point(const uint8_t* grid, int j, int (&q)[
 // 8-dimensional lattices, 35 entries on average when off the grid) take 8, the 4-dimensional ones
 // (about 14) take 4; IQ2_S takes 4 and IQ3_S 6.
 template <int D> constexpr int nb_piece() { return D == 8 ? 8 : 4; }
-// bits of the largest piece count per list, ceil(511 / R)
-constexpr int nb_count_bits(int r) { return 32 - __builtin_clz((unsigned)((511 + r - 1) / r)); }
 
 template <int D>
 struct NbWave {
@@ -124,22 +122,22 @@ __device__ __forceinline__ int wrow_at(int t, int v) { return (v + t) % (N / 4);
 template <int D, int N, int R = nb_piece<D>()>
 __device__ int wave_best_neighbour(const NbCtx& c, int k, bool off, int gi, const float (&xval)[N], float scale,
                                    const uint16_t* __restrict__ nbt, const uint8_t* grid) {
-    constexpr int NPB = nb_count_bits(R);
     NbWave<D>& W = *reinterpret_cast<NbWave<D>*>(c.w);
     constexpr unsigned long long INIT = (unsigned long long)0x7f7fffffu << 32;   // (FLT_MAX, position 0)
     const int lane = (int)__lane_id();
     const int ptr = off ? nb_offset(gi) : 0;
     const int len = off ? nb_length(gi) : 0;
     const int np = (len + R - 1) / R;
-    // exclusive prefix of the piece counts over the wave, one bit plane at a time
-    int first = 0, total = 0;
-#pragma unroll
-    for (int b = 0; b < NPB; ++b) {
-        const unsigned long long m = __ballot((np >> b) & 1);
-        first += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) << b;
-        total += __popcll(m) << b;
-    }
-    const int incl = first + np;
+    // inclusive prefix of the piece counts over the wave (the scan of wave_prefix_max with +)
+    int incl = np;
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xf, 0xf, false);   // row_shr:1
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xf, 0xf, false);   // row_shr:2
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xf, 0xf, false);   // row_shr:4
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xf, 0xf, false);   // row_shr:8
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xa, 0xf, false);   // row_bcast:15
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xc, 0xf, false);   // row_bcast:31
+    const int first = incl - np;
+    const int total = __builtin_amdgcn_readlane(incl, 63);
     if (np > 0) {
         float4* r = reinterpret_cast<float4*>(W.rec[lane]);
 #pragma unroll
@@ -817,24 +815,36 @@ __device__ __forceinline__ SubOut iq1_m_sub(const float (&x)[16], const float (&
             }
         }
     } else {
+        // Every split's four sums run over the sorted weights j = 0..15 in order, level 0 below i1,
+        // 1 below i2, 2 from i2 on. The running sums after the level-0 run depend on i1 only (p0),
+        // and after the level-1 run on (i1, i2), growing by one term per i2 (p1); only the level-2
+        // tail is added per split. The additions and their order are those of the direct sums.
+        // term(j, l, k): the contribution of sorted weight j at level l to sum k (sums 0 and 3 take
+        // the +delta / -delta value in both halves, 1 and 2 swap them in the second half)
+        auto add_terms = [&](float (&qx)[4], float (&q2)[4], int j, float gp, float gm) {
+            const float ap = sw[j] * gp * sx[j], am = sw[j] * gm * sx[j];
+            const float bp = sw[j] * gp * gp, bm = sw[j] * gm * gm;
+            const bool h0 = si[j] < 8;
+            qx[0] += ap; q2[0] += bp;
+            qx[3] += am; q2[3] += bm;
+            if (h0) { qx[1] += ap; q2[1] += bp; qx[2] += am; q2[2] += bm; }
+            else    { qx[1] += am; q2[1] += bm; qx[2] += ap; q2[2] += bp; }
+        };
+        float p0x[4] = {0, 0, 0, 0}, p0q[4] = {0, 0, 0, 0};
         for (int i1 = 0; i1 <= 16; ++i1) {
+            float p1x[4], p1q[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) { p1x[k] = p0x[k]; p1q[k] = p0q[k]; }
             for (int i2 = i1; i2 <= 16; ++i2) {
+                // sw passes an empty asm each split: otherwise the split-invariant products of every
+                // weight and level are hoisted out of the loops and spill
 #pragma unroll
-                for (int k = 0; k < 4; ++k) { sumqx[k] = 0; sumq2[k] = 0; }
+                for (int j = 0; j < 16; ++j) asm volatile("" : "+v"(sw[j]));
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int lv = j < i1 ? 0 : (j < i2 ? 1 : 2);
-                    const float vp = pick3(lv, XP0, XP1, XP2), vm = pick3(lv, XM0, XM1, XM2);
-                    const float ap = sw[j] * vp * sx[j], am = sw[j] * vm * sx[j];
-                    const float bp = sw[j] * vp * vp, bm = sw[j] * vm * vm;
-                    if (si[j] < 8) {
-                        sumqx[0] += ap; sumqx[1] += ap; sumqx[2] += am; sumqx[3] += am;
-                        sumq2[0] += bp; sumq2[1] += bp; sumq2[2] += bm; sumq2[3] += bm;
-                    } else {
-                        sumqx[0] += ap; sumqx[2] += ap; sumqx[1] += am; sumqx[3] += am;
-                        sumq2[0] += bp; sumq2[2] += bp; sumq2[1] += bm; sumq2[3] += bm;
-                    }
-                }
+                for (int k = 0; k < 4; ++k) { sumqx[k] = p1x[k]; sumq2[k] = p1q[k]; }
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (j >= i2) add_terms(sumqx, sumq2, j, XP2, XM2);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     if (sumq2[k] > 0 && sumqx[k] * sumqx[k] > best_score * sumq2[k]) {
@@ -842,7 +852,13 @@ __device__ __forceinline__ SubOut iq1_m_sub(const float (&x)[16], const float (&
                         b1 = i1; b2 = i2; best_k = k;
                     }
                 }
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (j == i2) add_terms(p1x, p1q, j, XP1, XM1);
             }
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (j == i1) add_terms(p0x, p0q, j, XP0, XM0);
         }
     }
     if (b1 < 0 || b2 < 0 || best_k < 0) return o;
