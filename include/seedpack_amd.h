@@ -138,9 +138,11 @@ int spa_qr_encode(int ggml_type, const void* F, const void* P, const void* seed,
                   uint32_t* out_len, const uint16_t* gk, const float* imx, int mv, void* work, void* stream);
 
 /* Decodes every segment (stream bytes of segment s start at in + in_off[s]) into F (the batch's
- * blocks). lut[n][4096] from spa_rans_build_lut. Replaces qr_dec (qr.py:760-807). */
-int spa_qr_decode(int ggml_type, const void* in, const uint64_t* in_off, const void* P, const void* seed,
-                  const void* tm, const void* sg, int nseg, const int* remap, const uint16_t* freq,
+ * blocks). `in` holds in_bytes of stream: reads past them see zeros (a damaged stream decodes to
+ * garbage, never outside its buffer). lut[n][4096] from spa_rans_build_lut. Replaces qr_dec
+ * (qr.py:760-807). */
+int spa_qr_decode(int ggml_type, const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P,
+                  const void* seed, const void* tm, const void* sg, int nseg, const int* remap, const uint16_t* freq,
                   const uint32_t* cum, const uint8_t* lut, void* F, const uint16_t* gk, const float* imx, int mv,
                   void* stream);
 

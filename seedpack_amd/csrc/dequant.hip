@@ -219,7 +219,7 @@ int run(const void* src, int64_t n, float* dst, hipStream_t st) {
     const int ti = iq_table_index(T);
     if (ti >= 0) {
         IqDeviceTable tab;
-        const int rc = iq_device_table(ti, &tab);
+        const int rc = iq_device_table(ti, &tab, st);
         if (rc) return rc;
         t.grid = tab.grid;
     }

@@ -1,6 +1,7 @@
 // Device copies of the IQ lattice tables (built once per process, uploaded once per device).
 #pragma once
 
+#include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace spa {
@@ -14,7 +15,8 @@ struct IqDeviceTable {
 
 // 0 IQ2_XXS, 1 IQ2_XS, 2 IQ1_S/IQ1_M, 3 IQ2_S, 4 IQ3_XXS, 5 IQ3_S; -1 otherwise
 int iq_table_index(int ggml_type);
-// the tables of `idx` on the current device (uploads them on first use); 0 or an SPA_ERR_* code
-int iq_device_table(int idx, IqDeviceTable* out);
+// the tables of `idx` on the current device; 0 or an SPA_ERR_* code. The first call on a device
+// queues their upload on `stream`; work queued on `stream` after any call sees them complete.
+int iq_device_table(int idx, IqDeviceTable* out, hipStream_t stream);
 
 }  // namespace spa

@@ -100,7 +100,39 @@ const Host& host_table(int idx) {
 
 constexpr int MAXDEV = 16;
 std::mutex g_dev_mu;
-IqDeviceTable g_dev[MAXDEV][6];
+
+// One table on one device: a single allocation holding grid, map and neighbour lists, filled by
+// copies queued on the stream of the first call that needs it; `ready` is recorded after them and
+// every later user's stream waits for it, so nothing on any stream reads the table before it is
+// there, and no call blocks the host.
+struct DevTable {
+    IqDeviceTable t{};
+    hipEvent_t ready = nullptr;
+};
+DevTable g_dev[MAXDEV][6];
+// the device form of each table's map (list lengths packed beside their offsets), built once per
+// process and kept: queued copies read it after the call that queued them has returned
+std::once_flag g_dm_once[6];
+std::vector<int32_t> g_dm[6];
+int g_dm_err[6];
+
+const std::vector<int32_t>& device_map(int idx) {
+    std::call_once(g_dm_once[idx], [idx] {
+        const Host& h = host_table(idx);
+        std::vector<int32_t>& dm = g_dm[idx];
+        dm.resize(h.map.size());
+        for (size_t i = 0; i < h.map.size(); ++i) {
+            const int32_t v = h.map[i];
+            if (v >= 0) { dm[i] = v; continue; }
+            const uint32_t off = (uint32_t)(-v - 1), len = h.nb[off];
+            if (off >= (1u << 22) || len == 0 || len >= 512) { g_dm_err[idx] = 1; return; }
+            dm[i] = -1 - (int32_t)((off << 9) | len);
+        }
+    });
+    return g_dm[idx];
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 }  // namespace
 
@@ -116,36 +148,44 @@ int iq_table_index(int ggml_type) {
     return -1;
 }
 
-int iq_device_table(int idx, IqDeviceTable* out) {
+int iq_device_table(int idx, IqDeviceTable* out, hipStream_t stream) {
     int dev = 0;
     SPA_HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= MAXDEV || idx < 0 || idx > 5) return fail(SPA_ERR_ARG, "iq table %d on device %d", idx, dev);
     const Host& h = host_table(idx);
+    const std::vector<int32_t>& dm = device_map(idx);
+    if (g_dm_err[idx]) return fail(SPA_ERR_ARG, "iq table %d: a neighbour list does not fit the packed map", idx);
     std::lock_guard<std::mutex> lk(g_dev_mu);
-    IqDeviceTable& t = g_dev[dev][idx];
-    if (!t.grid) {
-        // off-grid entries carry their list's length beside its offset: one load gives both
-        std::vector<int32_t> dm(h.map.size());
-        for (size_t i = 0; i < h.map.size(); ++i) {
-            const int32_t v = h.map[i];
-            if (v >= 0) { dm[i] = v; continue; }
-            const uint32_t off = (uint32_t)(-v - 1), len = h.nb[off];
-            if (off >= (1u << 22) || len == 0 || len >= 512) return fail(SPA_ERR_ARG, "iq table %d: list %u of length %u", idx, off, len);
-            dm[i] = -1 - (int32_t)((off << 9) | len);
+    DevTable& d = g_dev[dev][idx];
+    if (!d.t.grid) {
+        const size_t og = 0, om = align256(h.grid.size()), on = om + align256(dm.size() * sizeof(int32_t));
+        const size_t total = on + h.nb.size() * sizeof(uint16_t);
+        uint8_t* base = nullptr;
+        hipEvent_t ev = nullptr;
+        hipError_t e = hipMalloc((void**)&base, total);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipMemcpyAsync(base + og, h.grid.data(), h.grid.size(), hipMemcpyHostToDevice, stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(base + om, dm.data(), dm.size() * sizeof(int32_t), hipMemcpyHostToDevice, stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(base + on, h.nb.data(), h.nb.size() * sizeof(uint16_t), hipMemcpyHostToDevice, stream);
+        if (e == hipSuccess) e = hipEventRecord(ev, stream);
+        if (e != hipSuccess) {
+            // nothing is published: wait for whatever was queued, then release it
+            (void)hipStreamSynchronize(stream);
+            if (ev) (void)hipEventDestroy(ev);
+            if (base) (void)hipFree(base);
+            return fail(SPA_ERR_HIP, "iq table %d upload: %s", idx, hipGetErrorString(e));
         }
-        void *g = nullptr, *m = nullptr, *nb = nullptr;
-        SPA_HIP_TRY(hipMalloc(&g, h.grid.size()));
-        SPA_HIP_TRY(hipMalloc(&m, dm.size() * sizeof(int32_t)));
-        SPA_HIP_TRY(hipMalloc(&nb, h.nb.size() * sizeof(uint16_t)));
-        SPA_HIP_TRY(hipMemcpy(g, h.grid.data(), h.grid.size(), hipMemcpyHostToDevice));
-        SPA_HIP_TRY(hipMemcpy(m, dm.data(), dm.size() * sizeof(int32_t), hipMemcpyHostToDevice));
-        SPA_HIP_TRY(hipMemcpy(nb, h.nb.data(), h.nb.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
-        t.grid = (const uint8_t*)g;
-        t.map = (const int32_t*)m;
-        t.nb = (const uint16_t*)nb;
-        t.size = kSpecs[idx].size;
+        d.t.grid = base + og;
+        d.t.map = (const int32_t*)(base + om);
+        d.t.nb = (const uint16_t*)(base + on);
+        d.t.size = kSpecs[idx].size;
+        d.ready = ev;
+    } else {
+        SPA_HIP_TRY(hipStreamWaitEvent(stream, d.ready, 0));
     }
-    *out = t;
+    *out = d.t;
     return 0;
 }
 

@@ -217,7 +217,7 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
         for (; i >= 0; --i) {
             const int prev = i > 0 ? (differs(i - 1) ? 0 : 1) : 1;
             if (differs(i)) { pend = true; break; }
-            e.put_fc(ft.f[prev][1], ft.c[prev][1]);
+            e.put_fc(ft.freq_of(prev, 1), ft.cum_of(prev, 1));
             if (e.ptr - base < 8) { out_len[s] = 0xffffffffu; return; }
         }
         if (__ballot(pend) == 0) break;
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
             return;
         }
         const int prev = i > 0 ? (differs(i - 1) ? 0 : 1) : 1;
-        e.put_fc(ft.f[prev][0], ft.c[prev][0]);
+        e.put_fc(ft.freq_of(prev, 0), ft.cum_of(prev, 0));
         --i;
     }
     for (int j = 0; j < 4; ++j) { *--e.ptr = (uint8_t)(e.x & 0xff); e.x >>= 8; }
@@ -265,6 +265,7 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
 struct Dec {
     uint32_t x;
     const uint8_t* ptr;
+    const uint8_t* end;
     const int* remap;
     const uint16_t* freq;
     const uint32_t* cum;
@@ -277,7 +278,7 @@ struct Dec {
         // a valid stream needs at most two bytes here (x >= 2^11 before them); the cap ends the
         // loop on a damaged stream instead of spinning on zero bytes
 #pragma unroll
-        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | *ptr++;
+        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | next_byte(ptr, end);
         return v;
     }
 };
@@ -289,7 +290,8 @@ constexpr int DEC_WG = 64;
 // each lane decodes flags up to its next differing block, then the lanes that stopped at one decode
 // and model it together, so one lane's differing block does not hold the other 63.
 template <int T>
-__global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ in, const uint64_t* __restrict__ in_off,
+__global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ in, uint64_t in_bytes,
+                                                   const uint64_t* __restrict__ in_off,
                                                    const uint8_t* __restrict__ P, const uint8_t* __restrict__ seed,
                                                    const TM* __restrict__ tm, const SG* __restrict__ sg, int nseg,
                                                    const int* __restrict__ remap, const uint16_t* __restrict__ freq,
@@ -306,15 +308,16 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
     const SG g = sg[s];
     const TM m = tm[g.t];
     const uint8_t* sbase = seed + m.seed_off;
-    Dec d{0, in + in_off[s], remap, freq, cum, lut};
-    for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | *d.ptr++;
+    const uint8_t* const in_end = in + in_bytes;
+    Dec d{0, in + (in_off[s] < in_bytes ? in_off[s] : in_bytes), in_end, remap, freq, cum, lut};
+    for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | next_byte(d.ptr, in_end);
     int prev = 1;
     int64_t b = g.b0;
     const int64_t bend = g.b0 + g.nb;
     for (;;) {
         bool pend = false;
         for (; b < bend; ++b) {
-            prev = ft.get(d.x, d.ptr, prev);
+            prev = ft.get(d.x, d.ptr, in_end, prev);
             if (!prev) { pend = true; break; }     // F holds P's bytes for the equal blocks (qr_prefill)
         }
         if (__ballot(pend) == 0) break;
@@ -446,13 +449,13 @@ template <int T> struct Encode {
     }
 };
 template <int T> struct Decode {
-    static int run(const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
+    static int run(const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
                    int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F, int mv,
                    hipStream_t st) {
         if (int e = qr_prefill(F, P, sg, nseg, Ty<T>::BS, st)) return e;
         hipLaunchKernelGGL(k_qr_dec<T>, dim3((unsigned)((nseg + DEC_WG - 1) / DEC_WG)), dim3(DEC_WG), 0, st,
-                           (const uint8_t*)in, in_off, (const uint8_t*)P, (const uint8_t*)seed, (const TM*)tm, (const SG*)sg,
-                           nseg, remap, freq, cum, lut, (uint8_t*)F, mv);
+                           (const uint8_t*)in, in_bytes, in_off, (const uint8_t*)P, (const uint8_t*)seed, (const TM*)tm,
+                           (const SG*)sg, nseg, remap, freq, cum, lut, (uint8_t*)F, mv);
         SPA_HIP_TRY(hipGetLastError());
         return 0;
     }
@@ -479,7 +482,7 @@ int grid_hist(int T, const void* F, const void* P, const void* seed, const void*
 int grid_encode(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, const int* remap,
                 const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, const uint16_t* gk,
                 const float* imx, int mv, void* work, hipStream_t st);
-int grid_decode(int T, const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
+int grid_decode(int T, const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
                 int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F,
                 const uint16_t* gk, const float* imx, int mv, hipStream_t st);
 
@@ -528,14 +531,15 @@ int spa_qr_encode(int T, const void* F, const void* P, const void* seed, const v
     return dispatch<Encode>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, mv, work, (hipStream_t)stream);
 }
 
-int spa_qr_decode(int T, const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm,
-                  const void* sg, int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut,
-                  void* F, const uint16_t* gk, const float* imx, int mv, void* stream) {
+int spa_qr_decode(int T, const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed,
+                  const void* tm, const void* sg, int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum,
+                  const uint8_t* lut, void* F, const uint16_t* gk, const float* imx, int mv, void* stream) {
     if (int e = check_common(T, nseg, mv, gk)) return e;
     if (nseg == 0) return 0;
     if (grid_type(T))
-        return grid_decode(T, in, in_off, P, seed, tm, sg, nseg, remap, freq, cum, lut, F, gk, imx, mv, (hipStream_t)stream);
-    return dispatch<Decode>(T, in, in_off, P, seed, tm, sg, nseg, remap, freq, cum, lut, F, mv, (hipStream_t)stream);
+        return grid_decode(T, in, in_bytes, in_off, P, seed, tm, sg, nseg, remap, freq, cum, lut, F, gk, imx, mv,
+                           (hipStream_t)stream);
+    return dispatch<Decode>(T, in, in_bytes, in_off, P, seed, tm, sg, nseg, remap, freq, cum, lut, F, mv, (hipStream_t)stream);
 }
 
 int spa_qr_gather(const void* src, uint64_t cap, const uint32_t* len, const uint64_t* off, int nseg, void* dst, void* stream) {
@@ -552,5 +556,6 @@ int spa_rans_build_lut(const uint32_t* cum, int ntab, uint8_t* lut, void* stream
     SPA_HIP_TRY(hipGetLastError());
     return 0;
 }
+
 
 }  // extern "C"

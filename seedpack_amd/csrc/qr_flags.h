@@ -60,10 +60,13 @@ __host__ __device__ inline QrWork qr_work(void* w, int64_t slots, int maxsym) {
     return q;
 }
 
-// neq[b] for the batch's blocks b < (last segment's b0 + nb): 256 blocks per workgroup
+// neq[b] for the batch's blocks b < (last segment's b0 + nb): 256 blocks per workgroup. nlist (when
+// given) is set to 0 for the k_qr_slots launch that follows on the stream.
 __global__ __launch_bounds__(256) void k_qr_neq(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P,
-                                                const SG* __restrict__ sg, int nseg, int bs, uint8_t* __restrict__ neq) {
+                                                const SG* __restrict__ sg, int nseg, int bs, uint8_t* __restrict__ neq,
+                                                uint32_t* __restrict__ nlist) {
     __shared__ uint8_t fl[256];
+    if (nlist && blockIdx.x == 0 && threadIdx.x == 0) *nlist = 0;
     const SG last = sg[nseg - 1];
     const int64_t nb = last.b0 + last.nb;
     const int64_t b0 = (int64_t)blockIdx.x * 256;
@@ -174,13 +177,13 @@ inline int qr_prefill(void* F, const void* P, const void* sg, int nseg, int bs, 
 inline int qr_flags(const void* F, const void* P, const void* sg, int nseg, int seg, int bs, const QrWork& w,
                     uint32_t* counts, bool places, hipStream_t st) {
     const int64_t slots = (int64_t)nseg * seg;
+    const bool list = counts || places;
     hipLaunchKernelGGL(k_qr_neq, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, st, (const uint8_t*)F,
-                       (const uint8_t*)P, (const SG*)sg, nseg, bs, w.neq);
-    if (!counts && !places) {
+                       (const uint8_t*)P, (const SG*)sg, nseg, bs, w.neq, list ? w.nlist : nullptr);
+    if (!list) {
         SPA_HIP_TRY(hipGetLastError());
         return 0;
     }
-    SPA_HIP_TRY(hipMemsetAsync(w.nlist, 0, sizeof(uint32_t), st));
     const int64_t wgs = (slots + 255) / 256 < 8192 ? (slots + 255) / 256 : 8192;
     hipLaunchKernelGGL(k_qr_slots, dim3((unsigned)wgs), dim3(256), 0, st, (const SG*)sg, nseg, seg, (const uint8_t*)w.neq,
                        counts, w.list, w.nlist, places ? w.idx_of : nullptr, w.cap);

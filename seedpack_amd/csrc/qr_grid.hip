@@ -461,7 +461,7 @@ __global__ __launch_bounds__(64) void k_qrg_enc(const uint8_t* __restrict__ F, c
         const bool eq = !((nm >> i) & 1u);
         const int prev = i > 0 ? (((nm >> (i - 1)) & 1u) ? 0 : 1) : 1;
         if (eq) {
-            e.put_fc(ft.f[prev][1], ft.c[prev][1]);
+            e.put_fc(ft.freq_of(prev, 1), ft.cum_of(prev, 1));
             if (stop(e)) { if (lane == 0) out_len[s] = 0xffffffffu; return; }
             continue;
         }
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(64) void k_qrg_enc(const uint8_t* __restrict__ F, c
                 e.put(kd * 2 + anyk[k], (uint32_t)(dl[k] & 255));
             }
         }
-        e.put_fc(ft.f[prev][0], ft.c[prev][0]);
+        e.put_fc(ft.freq_of(prev, 0), ft.cum_of(prev, 0));
     }
     for (int i = 0; i < 4; ++i) {
         --e.ptr;
@@ -504,6 +504,7 @@ __global__ __launch_bounds__(64) void k_qrg_enc(const uint8_t* __restrict__ F, c
 struct Decoder {
     uint32_t x;
     const uint8_t* ptr;
+    const uint8_t* end;
     const int* remap;
     const uint16_t* freq;
     const uint32_t* cum;
@@ -516,13 +517,14 @@ struct Decoder {
         // a valid stream needs at most two bytes here (x >= 2^11 before them); the cap ends the
         // loop on a damaged stream instead of spinning on zero bytes
 #pragma unroll
-        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | *ptr++;
+        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | next_byte(ptr, end);
         return v;
     }
 };
 
 template <int T>
-__global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, const uint64_t* __restrict__ in_off,
+__global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, uint64_t in_bytes,
+                                                const uint64_t* __restrict__ in_off,
                                                 const uint8_t* __restrict__ P, const uint8_t* __restrict__ seed,
                                                 const TM* __restrict__ tm, const SG* __restrict__ sg, int nseg,
                                                 const int* __restrict__ remap, const uint16_t* __restrict__ freq,
@@ -546,15 +548,16 @@ __global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, 
     const BlockSeed bs{sx, sim, im != nullptr};
     uint32_t keys[Gt::PER];
     load_keys<T>(gk, lane, keys);
-    Decoder d{0, in + in_off[s], remap, freq, cum, lut};
-    for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | *d.ptr++;
+    const uint8_t* const in_end = in + in_bytes;
+    Decoder d{0, in + (in_off[s] < in_bytes ? in_off[s] : in_bytes), in_end, remap, freq, cum, lut};
+    for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | next_byte(d.ptr, in_end);
     FlagTab ft;
     ft.load(remap, freq, cum);
     int prev = 1;
     for (int64_t b = g.b0; b < g.b0 + g.nb; ++b) {
         const uint8_t* pb = P + b * Y::BS;
         uint8_t* dst = F + b * Y::BS;
-        const int eq = ft.get(d.x, d.ptr, prev);
+        const int eq = ft.get(d.x, d.ptr, in_end, prev);
         prev = eq;
         if (eq) continue;                         // F holds P's bytes already (qr_prefill)
         // every lane applies the same writes to the block in LDS, so each lane's reads see them
@@ -699,11 +702,11 @@ template <int T> struct GEnc {
     }
 };
 template <int T> struct GDec {
-    static int run(const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
+    static int run(const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
                    int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F,
                    const uint16_t* gk, const float* imx, int mv, hipStream_t st) {
         if (int e = qr_prefill(F, P, sg, nseg, Ty<T>::BS, st)) return e;
-        hipLaunchKernelGGL(k_qrg_dec<T>, dim3((unsigned)nseg), dim3(64), 0, st, (const uint8_t*)in, in_off, (const uint8_t*)P,
+        hipLaunchKernelGGL(k_qrg_dec<T>, dim3((unsigned)nseg), dim3(64), 0, st, (const uint8_t*)in, in_bytes, in_off, (const uint8_t*)P,
                            (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, remap, freq, cum, lut, (uint8_t*)F, gk,
                            imx, mv);
         SPA_HIP_TRY(hipGetLastError());
@@ -722,10 +725,10 @@ int grid_encode(int T, const void* F, const void* P, const void* seed, const voi
                 const float* imx, int mv, void* work, hipStream_t st) {
     return dispatch_grid<GEnc>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, gk, imx, mv, work, st);
 }
-int grid_decode(int T, const void* in, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
-                int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F,
-                const uint16_t* gk, const float* imx, int mv, hipStream_t st) {
-    return dispatch_grid<GDec>(T, in, in_off, P, seed, tm, sg, nseg, remap, freq, cum, lut, F, gk, imx, mv, st);
+int grid_decode(int T, const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed,
+                const void* tm, const void* sg, int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum,
+                const uint8_t* lut, void* F, const uint16_t* gk, const float* imx, int mv, hipStream_t st) {
+    return dispatch_grid<GDec>(T, in, in_bytes, in_off, P, seed, tm, sg, nseg, remap, freq, cum, lut, F, gk, imx, mv, st);
 }
 
 }  // namespace qr

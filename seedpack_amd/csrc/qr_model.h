@@ -28,30 +28,46 @@ constexpr int NTAB2 = NTAB + 208;
 constexpr int FESC_LO = 8, FESC_HI = 9;
 constexpr int MAXF = 34;
 
-// Frequencies and starts of the flag symbols 0 and 1 in the two flag contexts (previous block
-// differing / equal), held in registers: every block codes a flag, most blocks nothing else. A context
-// without symbols in the batch reads as 0 (a valid batch never codes it).
+// Next stream byte for the decoders' renormalisation: reads stop at `end` (zeros past it), so a
+// damaged or truncated stream decodes to garbage without leaving its buffer.
+__device__ __forceinline__ uint32_t next_byte(const uint8_t*& ptr, const uint8_t* end) {
+    const uint32_t b = ptr < end ? *ptr : 0u;
+    ++ptr;
+    return b;
+}
+
+// Frequencies of the flag symbols 0 and 1 in the two flag contexts p (previous block differing /
+// equal): every block codes a flag, most blocks nothing else. A context's symbol 0 starts at 0 and
+// symbol 1 at freq(p, 0) (the tables' cumulative counts), so four 16-bit frequencies say everything;
+// they sit in one 64-bit register, context p in bits 32p.., symbol v in bits 16v.. of it, and are
+// picked by shifts: a pick between separate fields may be turned into an indexed load from a copy of
+// the structure in scratch memory. A context without symbols in the batch reads as 0 (a valid batch
+// never codes it).
 struct FlagTab {
-    uint32_t f[2][2], c[2][2];
+    uint64_t q;
     __device__ __forceinline__ void load(const int* remap, const uint16_t* freq, const uint32_t* cum) {
+        (void)cum;
+        q = 0;
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const int tt = remap[FLAG + p];
-#pragma unroll
-            for (int v = 0; v < 2; ++v) {
-                f[p][v] = tt >= 0 ? freq[tt * 256 + v] : 0u;
-                c[p][v] = tt >= 0 ? cum[tt * 257 + v] : 0u;
-            }
+            if (tt >= 0) q |= (uint64_t)(freq[tt * 256] | ((uint32_t)freq[tt * 256 + 1] << 16)) << (32 * p);
         }
     }
-    // one flag decoded from state x in context p: symbol 1's slots start at c[p][1], symbol 0's at 0 (a
-    // valid stream's slot is in one of the two ranges); renormalised from ptr as the general step
-    __device__ __forceinline__ int get(uint32_t& x, const uint8_t*& ptr, int p) const {
+    __device__ __forceinline__ uint32_t freq_of(int p, int v) const {
+        return (uint32_t)(q >> (32 * p + 16 * v)) & 0xffffu;
+    }
+    __device__ __forceinline__ uint32_t cum_of(int p, int v) const { return v ? freq_of(p, 0) : 0u; }
+    // one flag decoded from state x in context p: symbol 1's slots start at freq(p, 0), symbol 0's at 0
+    // (a valid stream's slot is in one of the two ranges); renormalised from ptr as the general step
+    __device__ __forceinline__ int get(uint32_t& x, const uint8_t*& ptr, const uint8_t* end, int p) const {
         const uint32_t slot = x & (PSCALE - 1);
-        const int v = slot >= c[p][1] ? 1 : 0;
-        x = f[p][v] * (x >> PB) + slot - c[p][v];
+        const uint32_t w = (uint32_t)(q >> (32 * p));
+        const uint32_t f0 = w & 0xffffu;
+        const int v = slot >= f0 ? 1 : 0;
+        x = (w >> (16 * v) & 0xffffu) * (x >> PB) + slot - (v ? f0 : 0u);
 #pragma unroll
-        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | *ptr++;
+        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | next_byte(ptr, end);
         return v;
     }
 };

@@ -1153,7 +1153,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
 template <int K>
 int run(const QuantArgs& a, int table) {
     IqDeviceTable tab;
-    if (int e = iq_device_table(table, &tab)) return e;
+    if (int e = iq_device_table(table, &tab, a.stream)) return e;
     constexpr int D = (K == K_IQ3_XXS || K == K_IQ3_S) ? 4 : 8;
     if ((int64_t)tab.size * D != Cfg<K>::GBYTES)
         return fail(SPA_ERR_ASSERT, "grid i-quant type %d: codebook of %d points does not fit the kernel", a.type, tab.size);

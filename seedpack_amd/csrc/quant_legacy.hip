@@ -4,8 +4,8 @@
 // Mapping: one lane per block. A workgroup of 256 lanes quantizes 256 consecutive blocks (the
 // tensor is one contiguous run of blocks, rows back to back), assembles their bytes in LDS and
 // writes them with coalesced dword stores. The imatrix paths need the row's mean square
-// (sum_x2 / n_per_row, summed left to right over the whole row, ggml-quants.c:2082-2084); it comes
-// from a one-lane-per-row pre-pass.
+// (sum_x2 / n_per_row, summed left to right over the whole row, ggml-quants.c:2082-2084); each
+// workgroup computes it for the rows its blocks belong to before quantizing them.
 #include "common.h"
 #include "launch.h"
 #include "search.h"
@@ -223,13 +223,43 @@ struct Q2_0 {
     }
 };
 
+// (sum over row `row` of x*x, added left to right) / n_per_row -- ggml-quants.c:2082-2084. One lane
+// walks the whole row; the next 32 weights are requested before the current 32 are added, so the
+// dependent adds, not the loads, set the pace.
+__device__ float row_mean_sq(const void* __restrict__ src, int kind, int64_t row, int64_t npr) {
+    float s = 0;
+    float x[32], nx[32];
+    load_weights<32>(src, kind, row * npr, nx);
+    for (int64_t j = 0; j < npr; j += 32) {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) x[k] = nx[k];
+        if (j + 32 < npr) load_weights<32>(src, kind, row * npr + j + 32, nx);
+#pragma unroll
+        for (int k = 0; k < 32; ++k) s += x[k] * x[k];
+    }
+    return s / (float)npr;
+}
+
+// One lane per block, 256 blocks per workgroup. With the imatrix (IMPL) each block's weights need
+// its row's mean square: the workgroup first computes it for every row its blocks touch (one lane
+// per row, at most 256 rows), so no buffer outside the launch holds it.
 template <class Op, bool IMPL>
 __global__ __launch_bounds__(WG) void k_legacy(const void* __restrict__ src, int kind, uint8_t* __restrict__ dst,
                                                int64_t nblocks, int64_t blocks_per_row,
-                                               const float* __restrict__ imx, const float* __restrict__ sigma2) {
+                                               const float* __restrict__ imx) {
     __shared__ __align__(16) uint16_t tile[WG * Op::BS / 2];
+    __shared__ float s2_rows[IMPL ? WG : 1];
     const int64_t b0 = (int64_t)blockIdx.x * WG;
     const int64_t b = b0 + threadIdx.x;
+    const int nb = (int)(nblocks - b0 < WG ? nblocks - b0 : WG);
+    const int64_t row_lo = b0 / blocks_per_row;
+    if constexpr (IMPL) {
+        // rows row_lo .. (b0 + nb - 1) / blocks_per_row: at most WG of them (blocks_per_row >= 1)
+        const int nrow = (int)((b0 + nb - 1) / blocks_per_row - row_lo + 1);
+        if ((int)threadIdx.x < nrow)
+            s2_rows[threadIdx.x] = row_mean_sq(src, kind, row_lo + threadIdx.x, blocks_per_row * Op::QK);
+        __syncthreads();
+    }
     if (b < nblocks) {
         float x[Op::QK];
         load_weights<Op::QK>(src, kind, b * Op::QK, x);
@@ -237,7 +267,7 @@ __global__ __launch_bounds__(WG) void k_legacy(const void* __restrict__ src, int
         if constexpr (IMPL) {
             const int64_t row = b / blocks_per_row;
             const int64_t col = (b - row * blocks_per_row) * Op::QK;
-            const float s2 = sigma2[row];
+            const float s2 = s2_rows[row - row_lo];
             float w[Op::QK];
 #pragma unroll
             for (int j = 0; j < Op::QK; ++j) w[j] = imx[col + j] * sqrtf(s2 + x[j] * x[j]);
@@ -247,105 +277,17 @@ __global__ __launch_bounds__(WG) void k_legacy(const void* __restrict__ src, int
         }
     }
     __syncthreads();
-    const int nb = (int)(nblocks - b0 < WG ? nblocks - b0 : WG);
     store_tile(tile, dst + b0 * Op::BS, nb * Op::BS);
 }
 
-// sigma2[row] = (sum over the row of x*x, left to right) / n_per_row -- ggml-quants.c:2082-2084.
-__global__ __launch_bounds__(64) void k_row_mean_sq(const void* __restrict__ src, int kind, int64_t nrows,
-                                                    int64_t npr, float* __restrict__ sigma2) {
-    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= nrows) return;
-    float s = 0;
-    for (int64_t j = 0; j < npr; j += 8) {
-        float x[8];
-        load_weights<8>(src, kind, row * npr + j, x);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) s += x[k] * x[k];
-    }
-    sigma2[row] = s / (float)npr;
-}
-
-// The same for BF16 rows: 64 rows per workgroup, 64x64 tiles through LDS (read as 16-byte vectors,
-// 8 lanes per row: coalesced), the next tile's loads issued before the current tile's sums; each lane
-// adds its row's squares in index order. Rows of npr % 64 == 32 end with a half tile read per lane.
-constexpr int RS = 64;
-__global__ __launch_bounds__(RS) void k_row_mean_sq_bf16(const uint16_t* __restrict__ w, int64_t nrows, int64_t npr,
-                                                         float* __restrict__ sigma2) {
-    __shared__ uint32_t tile[RS][RS / 2 + 1];
-    const int lane = threadIdx.x;
-    const int64_t r0 = (int64_t)blockIdx.x * RS, row = r0 + lane;
-    const int64_t nt = npr / RS;
-    float s = 0;
-    uint4 v[8];
-    auto load = [&](int64_t c0) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int64_t r = r0 + (lane >> 3) + 8 * k;
-            v[k] = r < nrows ? *reinterpret_cast<const uint4*>(w + r * npr + c0 + (lane & 7) * 8) : make_uint4(0u, 0u, 0u, 0u);
-        }
-    };
-    if (nt) load(0);
-    for (int64_t t = 0; t < nt; ++t) {
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            uint32_t* d = &tile[(lane >> 3) + 8 * k][(lane & 7) * 4];
-            d[0] = v[k].x; d[1] = v[k].y; d[2] = v[k].z; d[3] = v[k].w;
-        }
-        __syncthreads();
-        if (t + 1 < nt) load((t + 1) * RS);
-#pragma unroll 8
-        for (int j = 0; j < RS / 2; ++j) {
-            const uint32_t pr = tile[lane][j];
-            const float x0 = bf16_to_f32(pr & 0xffffu), x1 = bf16_to_f32(pr >> 16);
-            s += x0 * x0;
-            s += x1 * x1;
-        }
-    }
-    if (row >= nrows) return;
-    for (int64_t j = nt * RS; j < npr; j += 8) {
-        const uint4 u = *reinterpret_cast<const uint4*>(w + row * npr + j);
-        const uint32_t q[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float x0 = bf16_to_f32(q[k] & 0xffffu), x1 = bf16_to_f32(q[k] >> 16);
-            s += x0 * x0;
-            s += x1 * x1;
-        }
-    }
-    sigma2[row] = s / (float)npr;
-}
-
-template <class Op>
-int run_ref(const QuantArgs& a) {
+template <class Op, bool IMPL>
+int run(const QuantArgs& a) {
     const int64_t nblocks = a.nrows * a.n_per_row / Op::QK;
     if (nblocks == 0) return 0;
     const int64_t grid = (nblocks + WG - 1) / WG;
-    hipLaunchKernelGGL((k_legacy<Op, false>), dim3((unsigned)grid), dim3(WG), 0, a.stream, a.src, a.src_kind,
-                       (uint8_t*)a.dst, nblocks, a.n_per_row / Op::QK, nullptr, nullptr);
+    hipLaunchKernelGGL((k_legacy<Op, IMPL>), dim3((unsigned)grid), dim3(WG), 0, a.stream, a.src, a.src_kind,
+                       (uint8_t*)a.dst, nblocks, a.n_per_row / Op::QK, IMPL ? a.imatrix : nullptr);
     SPA_HIP_TRY(hipGetLastError());
-    return 0;
-}
-
-template <class Op>
-int run_impl(const QuantArgs& a) {
-    const int64_t nblocks = a.nrows * a.n_per_row / Op::QK;
-    if (nblocks == 0) return 0;
-    float* sigma2 = nullptr;
-    SPA_HIP_TRY(hipMallocAsync((void**)&sigma2, (size_t)a.nrows * sizeof(float), a.stream));
-    if (a.src_kind == SRC_BF16)
-        hipLaunchKernelGGL(k_row_mean_sq_bf16, dim3((unsigned)((a.nrows + RS - 1) / RS)), dim3(RS), 0, a.stream,
-                           (const uint16_t*)a.src, a.nrows, a.n_per_row, sigma2);
-    else
-        hipLaunchKernelGGL(k_row_mean_sq, dim3((unsigned)((a.nrows + 63) / 64)), dim3(64), 0, a.stream, a.src, a.src_kind,
-                           a.nrows, a.n_per_row, sigma2);
-    const int64_t grid = (nblocks + WG - 1) / WG;
-    hipLaunchKernelGGL((k_legacy<Op, true>), dim3((unsigned)grid), dim3(WG), 0, a.stream, a.src, a.src_kind,
-                       (uint8_t*)a.dst, nblocks, a.n_per_row / Op::QK, a.imatrix, sigma2);
-    const hipError_t le = hipGetLastError();
-    SPA_HIP_TRY(hipFreeAsync(sigma2, a.stream));
-    if (le != hipSuccess) return fail(-5, "k_legacy launch: %s", hipGetErrorString(le));
     return 0;
 }
 
@@ -354,12 +296,12 @@ int run_impl(const QuantArgs& a) {
 int launch_legacy(const QuantArgs& a) {
     const bool w = a.imatrix != nullptr;
     switch (a.type) {
-        case 8: return run_ref<Q8_0>(a);                                  // imatrix ignored (:2296-2301)
-        case 2: return w ? run_impl<Q4_0>(a) : run_ref<Q4_0>(a);
-        case 3: return w ? run_impl<Q4_1>(a) : run_ref<Q4_1>(a);
-        case 6: return w ? run_impl<Q5_0>(a) : run_ref<Q5_0>(a);
-        case 7: return w ? run_impl<Q5_1>(a) : run_ref<Q5_1>(a);
-        case 42: return run_ref<Q2_0>(a);                                 // imatrix ignored (:2114-2127)
+        case 8: return run<Q8_0, false>(a);                               // imatrix ignored (:2296-2301)
+        case 2: return w ? run<Q4_0, true>(a) : run<Q4_0, false>(a);
+        case 3: return w ? run<Q4_1, true>(a) : run<Q4_1, false>(a);
+        case 6: return w ? run<Q5_0, true>(a) : run<Q5_0, false>(a);
+        case 7: return w ? run<Q5_1, true>(a) : run<Q5_1, false>(a);
+        case 42: return run<Q2_0, false>(a);                              // imatrix ignored (:2114-2127)
         default: return fail(-2, "launch_legacy: type %d is not a legacy type", a.type);
     }
 }

@@ -200,16 +200,20 @@ def _check_type(T):
 
 
 _GK_DEV = {}
+_GK_LOCK = threading.Lock()
 
 
 def _gk_ptr(T):
-    """device grid keys of grid type T (uploaded once per device), or None for the other types"""
+    """device grid keys of grid type T (uploaded once per device, under a lock: coder threads share
+    them, and an entry once published is never replaced), or None for the other types"""
     if T not in GRID_TYPES:
         return None
-    dev_id = dev.current_device()
-    if (T, dev_id) not in _GK_DEV:
-        _GK_DEV[(T, dev_id)] = dev.DeviceArray.from_host(grid_keys(T))
-    return _GK_DEV[(T, dev_id)].ptr
+    key = (T, dev.current_device())
+    with _GK_LOCK:
+        a = _GK_DEV.get(key)
+        if a is None:
+            a = _GK_DEV[key] = dev.DeviceArray.from_host(grid_keys(T))
+    return a.ptr
 
 
 def encode_parts(T, items, seed_dev, imx_dev=None, mv=None, stream=None):
@@ -306,15 +310,18 @@ def decode_parts(T, freq, used, lens, stream_bytes, items, seed_dev, imx_dev=Non
     lut = dev.DeviceArray((max(1, len(freq)), 1 << PB), np.uint8)
     check(lib().spa_rans_build_lut(cum_d.ptr, len(freq), lut.ptr, stream))
     lens = np.asarray(lens, np.uint64)
+    s = np.frombuffer(bytes(stream_bytes), np.uint8)
+    if len(lens) != nseg or int(lens.sum()) > len(s):
+        raise ValueError(f"QR batch of type {T}: {len(lens)} segment lengths summing to {int(lens.sum())} bytes for "
+                         f"{nseg} segments and a {len(s)}-byte stream")
     offs = np.zeros(max(1, nseg), np.uint64)
     offs[1:nseg] = np.cumsum(lens)[:-1]
-    s = np.frombuffer(bytes(stream_bytes), np.uint8)
     s_d = dev.DeviceArray.from_host(s if len(s) else np.zeros(1, np.uint8), stream)
     tm_d = dev.DeviceArray.from_host(tm.view(np.uint8), stream)
     sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if nseg else np.zeros(16, np.uint8), stream)
     offs_d = dev.DeviceArray.from_host(offs, stream)
     imx = None if imx_dev is None else imx_dev.ptr
-    check(lib().spa_qr_decode(T, s_d.ptr, offs_d.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr,
+    check(lib().spa_qr_decode(T, s_d.ptr, len(s), offs_d.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr,
                               freq_d.ptr, cum_d.ptr, lut.ptr, F.ptr, _gk_ptr(T), imx, mv, stream))
     return F
 

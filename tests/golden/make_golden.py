@@ -71,9 +71,11 @@ def make_small(path):
     print(f"wrote {path} ({len(out)} arrays, {os.path.getsize(path)} bytes)")
 
 
-# full-size tensors whose reference bytes are pinned by digest: (config, tensor index, types)
+# full-size tensors whose reference bytes are pinned by digest: (config, tensor index, types); a
+# type listed as (type, variant) is quantized with that code variant (IQ1_M's pre-f95b0d9539 search
+# is variant 1, the one every IQ1_M tensor with a residual is predicted again with)
 FULL = [(1, 0, [8, 2]), (2, 1, [10, 11, 12, 13, 14]), (2, 0, [10, 11, 12, 13, 14]),
-        (3, 0, [23, 18, 17, 16, 19, 29]), (3, 1, [23, 18, 17, 16, 19, 29])]
+        (3, 0, [23, 18, 17, 16, 19, 29, (29, 1)]), (3, 1, [23, 18, 17, 16, 19, 29, (29, 1)])]
 
 
 def make_full(path):
@@ -84,10 +86,11 @@ def make_full(path):
         w, imx = synth.tensor(cfg, ti)
         x = synth.bf16_to_f32(w).reshape(w.shape)
         for t in types:
-            key = f"cfg{cfg}_t{ti}_{t}_0"
+            t, variant = t if isinstance(t, tuple) else (t, 0)
+            key = f"cfg{cfg}_t{ti}_{t}_{variant}"
             if key in man:
                 continue
-            y = ref.quantize(t, x, imx)
+            y = ref.quantize(t, x, imx, variant=variant)
             man[key] = {"sha256": hashlib.sha256(y.tobytes()).hexdigest(), "nbytes": int(y.size),
                         "shape": list(w.shape), "imatrix": imx is not None}
             print(key, man[key]["sha256"][:16], flush=True)

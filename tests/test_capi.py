@@ -47,3 +47,4 @@ def test_bad_arguments_fail_before_any_device_call():
     assert L.spa_quantize(12, 1, None, 0, 1, 256, None, None, None) == -2       # no variant 1 for Q4_K
     assert L.spa_quantize(16, 0, None, 0, 1, 256, None, None, None) == -4       # null src first
     assert L.spa_type_variants(29) == 2 and L.spa_type_variants(12) == 1 and L.spa_type_variants(99) == 0
+

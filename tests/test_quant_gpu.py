@@ -83,7 +83,7 @@ def test_hip_full_size_matches_reference_digest(gq, key):
         pytest.skip(f"type {t} not built")
     say("case full", key)
     w, imx = synth.tensor(cfg, ti)
-    got = hip(gq, t, w, imx)
+    got = hip(gq, t, w, imx, variant)
     assert got.size == ent["nbytes"]
     assert hashlib.sha256(got.tobytes()).hexdigest() == ent["sha256"]
 
