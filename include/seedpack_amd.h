@@ -146,6 +146,18 @@ int spa_qr_decode(int ggml_type, const void* in, uint64_t in_bytes, const uint64
                   const uint32_t* cum, const uint8_t* lut, void* F, const uint16_t* gk, const float* imx, int mv,
                   void* stream);
 
+/* No counterpart in the reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc). spa_qr_encode with its workspace
+ * taken from a static per-device scratch of spa_qr_noalloc_scratch_bytes() (64 MiB) instead of a
+ * `work` argument: no allocation, no hipMemset. Calls whose spa_qr_work_bytes(ggml_type, nseg) exceed
+ * it fail with SPA_ERR_ARG. All calls on one device share that scratch: calls that overlap in time on
+ * one device (other streams or threads) race and must be serialised by the caller. */
+int spa_qr_encode_noalloc(int ggml_type, const void* F, const void* P, const void* seed, const void* tm,
+                          const void* sg, int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum,
+                          void* out, uint64_t cap, uint32_t* out_len, const uint16_t* gk, const float* imx, int mv,
+                          void* stream);
+size_t spa_qr_noalloc_scratch_bytes(void);
+
 /* Compacts the segment slots into one stream: dst[off[s] ..] = the last len[s] bytes of slot s.
  * Replaces gather (qr.py:880-887, gpu2.py:264-271). */
 int spa_qr_gather(const void* src, uint64_t cap, const uint32_t* len, const uint64_t* off, int nseg, void* dst,

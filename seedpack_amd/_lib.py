@@ -58,6 +58,10 @@ SIGNATURES = {
                               c_void_p]),
     "spa_qr_decode": (c_int, [c_int, c_void_p, c_uint64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "spa_qr_encode_noalloc": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
+                                      c_void_p, c_void_p, c_void_p, ctypes.c_uint64, c_void_p, c_void_p, c_void_p,
+                                      c_int, c_void_p]),
+    "spa_qr_noalloc_scratch_bytes": (c_size_t, []),
     "spa_qr_gather": (c_int, [c_void_p, ctypes.c_uint64, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "spa_rans_build_lut": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
     "spa_xor": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),

@@ -14,6 +14,8 @@
 //     segment; the decoder assembles each block in a per-lane LDS slot and stores it whole.
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../../include/seedpack_amd.h"
 #include "launch.h"
 #include "qr_flags.h"
@@ -491,6 +493,35 @@ int grid_decode(int T, const void* in, uint64_t in_bytes, const uint64_t* in_off
 
 using namespace spa::qr;
 
+// Workspace of spa_qr_encode_noalloc: one copy per device, held until the process ends. Host code
+// never uses this name as an address: each device's copy is reached through the pointer
+// hipGetSymbolAddress returns on that device (scratch_on_device).
+#define SPA_QR_NOALLOC_SCRATCH (64u << 20)
+static __device__ __align__(256) uint8_t scratch[SPA_QR_NOALLOC_SCRATCH];
+
+namespace {
+constexpr int kMaxDev = 16;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDev];
+
+// the current device's copy of `scratch` (looked up once per device, with that device current)
+int scratch_on_device(void** out) {
+    int dev = 0;
+    SPA_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDev) return spa::fail(SPA_ERR_ARG, "QR: device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return spa::fail(SPA_ERR_HIP, "QR: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+}  // namespace
+
 extern "C" {
 
 int spa_qr_seg_blocks(int T) {
@@ -557,5 +588,26 @@ int spa_rans_build_lut(const uint32_t* cum, int ntab, uint8_t* lut, void* stream
     return 0;
 }
 
+int spa_qr_encode_noalloc(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg,
+                          const int* remap, const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap,
+                          uint32_t* out_len, const uint16_t* gk, const float* imx, int mv, void* stream) {
+    if (!spa_qr_seg_blocks(T)) return spa::fail(SPA_ERR_TYPE, "QR: type %d is not a QR type", T);
+    if (int e = check_common(T, nseg, mv, gk)) return e;
+    if (cap < 1024) return spa::fail(SPA_ERR_ARG, "QR: segment capacity %llu too small", (unsigned long long)cap);
+    const size_t need = spa_qr_work_bytes(T, nseg);
+    if (need > SPA_QR_NOALLOC_SCRATCH)
+        return spa::fail(SPA_ERR_ARG, "spa_qr_encode_noalloc: %d segments of type %d need %zu bytes of workspace, "
+                         "more than the %u of its static scratch (split the batch or use spa_qr_encode)",
+                         nseg, T, need, SPA_QR_NOALLOC_SCRATCH);
+    if (nseg == 0) return 0;
+    void* work = nullptr;
+    if (int e = scratch_on_device(&work)) return e;
+    if (grid_type(T))
+        return grid_encode(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, gk, imx, mv, work,
+                           (hipStream_t)stream);
+    return dispatch<Encode>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, mv, work, (hipStream_t)stream);
+}
+
+size_t spa_qr_noalloc_scratch_bytes(void) { return SPA_QR_NOALLOC_SCRATCH; }
 
 }  // extern "C"

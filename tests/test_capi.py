@@ -48,3 +48,17 @@ def test_bad_arguments_fail_before_any_device_call():
     assert L.spa_quantize(16, 0, None, 0, 1, 256, None, None, None) == -4       # null src first
     assert L.spa_type_variants(29) == 2 and L.spa_type_variants(12) == 1 and L.spa_type_variants(99) == 0
 
+
+def test_noalloc_encoder_rejects_before_any_device_call():
+    """a batch whose workspace exceeds the static scratch is refused from its sizes alone"""
+    L = _lib.lib()
+    scratch = L.spa_qr_noalloc_scratch_bytes()
+    assert scratch == 64 << 20
+    nseg = 1
+    while L.spa_qr_work_bytes(8, nseg) <= scratch:
+        nseg *= 2
+    assert L.spa_qr_encode_noalloc(8, None, None, None, None, None, nseg, None, None, None, None, 1 << 16, None, None,
+                                   None, 2, None) == -4
+    assert b"static scratch" in L.spa_last_error()
+    assert L.spa_qr_encode_noalloc(99, None, None, None, None, None, 1, None, None, None, None, 1 << 16, None, None,
+                                   None, 2, None) == -2
