@@ -3,20 +3,18 @@
 compress(data, layout) -> parts and decompress(parts) -> the tensors' bytes keep BF16v2's
 algorithm and stream format (bf16v2.py:185-486): side information per tensor (rfi, cfi, scl),
 exact duplicate rows coded once, per-role frequency tables (656 per role: 512 exponent, 128
-mantissa, 16 sign contexts) normalised to 2^15, and rANS segments of 16384 weights. The statistics, fingerprints, histogram, symbol
-lookups, coding, gather and decoding run as HIP kernels; the duplicate-row check, the table
-normalisation (gpu2.normalize_gpu, a loop over a few hundred rows) and the framing run on the host.
+mantissa, 16 sign contexts) normalised to 2^15, and rANS segments of 16384 weights. The statistics,
+fingerprints, histogram, symbol lookups, coding, gather and decoding run as HIP kernels; the
+duplicate-row check, the table normalisation (gpu2.normalize_gpu, a loop over a few hundred rows)
+and the framing run on the host.
 
 `layout` is BF16v2._layout's dict (bf16v2.py:182-188): {"size": file bytes, "t": [[offset, bytes,
 row length, "bf16"], ...] (2-D BF16 tensors by offset), "role": role index per tensor, "nroles"}.
 R2Tensors (bf16v2.py:488-617) decodes chosen tensors alone. The file's other bytes travel in the
-"rest" part, coded on the host: both of its forms decode here and the lzma form is written here;
-the tokenizer-aware form (gpu2.header_pairs_c) needs the GGUF's key spans and stays with the
-caller's GGUF reader.
+"rest" part, coded on the host by seedpack_amd.header.
 """
 import ctypes
 import json
-import lzma
 import re
 import struct
 import time
@@ -28,6 +26,7 @@ from . import device as dev
 from . import zstd
 from ._lib import check, lib
 from .framing import pack_parts, unpack
+from .header import fill_rest, header_d, header_x, rest_of
 
 PB = 15
 K = 8
@@ -56,41 +55,30 @@ def layout_of(tensors, size):
             "role": [roles.index(role(t[0])) for t in ts], "nroles": len(roles)}
 
 
-def groups(layout, group_bytes):
-    gs, cur, cb = [], [], 0
-    for i, (off, nb, rl, _) in enumerate(layout["t"]):
-        if cur and cb + nb > group_bytes:
-            gs.append(cur)
-            cur, cb = [], 0
-        cur.append(i)
-        cb += nb
-    if cur:
-        gs.append(cur)
-    return gs
-
-
 def bases(layout):
-    rb, cb, rowbase, colbase = [], [], 0, 0
-    for off, nb, rl, _ in layout["t"]:
-        rb.append(rowbase)
-        cb.append(colbase)
-        rowbase += nb // 2 // rl
-        colbase += rl
-    return rb, cb, rowbase, colbase
+    """per tensor its first row and first column in the file-wide side information arrays, and the
+    totals: (row bases, column bases, rows, columns) -- rows and columns of the tensors in order"""
+    t = layout["t"]
+    rl = np.array([x[2] for x in t], np.int64)
+    rows = np.array([x[1] for x in t], np.int64) // 2 // np.maximum(rl, 1)
+    rb = np.concatenate([[0], np.cumsum(rows)]).astype(np.int64)
+    cb = np.concatenate([[0], np.cumsum(rl)]).astype(np.int64)
+    return rb[:-1].tolist(), cb[:-1].tolist(), int(rb[-1]), int(cb[-1])
 
 
 HEW = 64                           # exponent contexts the histogram kernel counts in LDS
 
 
 def plan(layout, grp, nrows_c, rmap_off, rfi=None, cfi=None):
-    """(TB, SG) descriptors of one group, device offsets relative to the group's first tensor
-    (bf16v2.py:208-220). With the side information given, TB.pad holds the base of the histogram
-    kernel's LDS window of exponent contexts, centred on the tensor's median context (the counts
-    do not depend on it)."""
+    """(TB, SG) descriptors of the tensors grp: device offsets relative to the first one, and the
+    segments -- each tensor's coded rows cut into SEG-weight runs (the last one shorter), tensors in
+    order (the stream format, bf16v2.py:208-220). With the side information given, TB.pad holds the
+    base of the histogram kernel's LDS window of exponent contexts, centred on the tensor's median
+    context (the counts do not depend on it)."""
     rb, cb, _, _ = bases(layout)
     tb = np.zeros(len(grp), TB_DT)
-    segs = []
     a = layout["t"][grp[0]][0]
+    sgs = []
     for k, i in enumerate(grp):
         off, nb, rl, _ = layout["t"][i]
         pe0 = 0
@@ -99,9 +87,12 @@ def plan(layout, grp, nrows_c, rmap_off, rfi=None, cfi=None):
             pe0 = min(max(mid - HEW // 2, 0), NE - HEW)
         tb[k] = (off - a, rl, rb[i], cb[i], layout["role"][i] * TPT, rmap_off.get(i, -1), pe0)
         n = nrows_c[i] * rl
-        for i0 in range(0, n, SEG):
-            segs.append((k, min(SEG, n - i0), i0))
-    return tb, (np.array(segs, SG_DT) if segs else np.zeros(0, SG_DT))
+        sg = np.zeros(-(-n // SEG), SG_DT)
+        sg["t"] = k
+        sg["i0"] = np.arange(0, n, SEG)
+        sg["n"] = np.minimum(SEG, n - sg["i0"])
+        sgs.append(sg)
+    return tb, (np.concatenate(sgs) if sgs else np.zeros(0, SG_DT))
 
 
 def normalize(counts, scale=1 << PB):
@@ -151,28 +142,25 @@ def load_tables(buf):
 
 
 def _dups(hashes, rows, rl):
-    """(rows kept (sorted) or None, [(duplicate row, source row)]) from the row fingerprints and a
-    byte check of every candidate (bf16v2.py:246-271); `rows(ids)` returns those rows' BF16 bits"""
-    nr = len(hashes)
-    order = np.argsort(hashes, kind="stable")
-    hs = hashes[order]
-    same = np.flatnonzero(hs[1:] == hs[:-1])
-    if len(same) == 0:
+    """duplicate rows of a tensor: every row equal to a row with a lower index is coded once and
+    copied from the lowest such row (bf16v2.py:246-271). Rows whose 64-bit fingerprints collide are
+    compared byte for byte (`rows(ids)` -> those rows' BF16 bits). -> (the rows kept, sorted, or
+    None when there is no duplicate; sorted [(duplicate row, source row)])"""
+    _, inv, cnt = np.unique(hashes, return_inverse=True, return_counts=True)
+    cand = np.flatnonzero(cnt[inv] > 1)            # rows that share a fingerprint with another
+    if len(cand) == 0:
         return None, []
-    ks = np.unique(np.concatenate([same, same + 1]))
-    hu = dict(zip(order[ks].tolist(), rows(order[ks])))
-    pairs, isdup, first = [], np.zeros(nr, bool), {}
-    for k in ks:
-        r = int(order[k])
-        cands = first.setdefault(int(hs[k]), [])
-        src = next((c for c in cands if np.array_equal(hu[c], hu[r])), None)
-        if src is None:
-            cands.append(r)
-        else:
+    content = dict(zip(cand.tolist(), (np.asarray(r).tobytes() for r in rows(cand))))
+    first, pairs = {}, []
+    for r in cand.tolist():                        # increasing row index
+        key = (int(inv[r]), content[r])
+        src = first.setdefault(key, r)
+        if src != r:
             pairs.append((r, src))
-            isdup[r] = True
     if not pairs:
         return None, []
+    isdup = np.zeros(len(hashes), bool)
+    isdup[[r for r, _ in pairs]] = True
     return np.flatnonzero(~isdup).astype(np.int32), sorted(pairs)
 
 
@@ -382,18 +370,23 @@ class BF16v2:
                                nrows_c=np.array(meta["nrows_c"], np.int64),
                                dups=np.array(dups, np.int64).reshape(-1, 3), rowmap=rowmap)}
 
-    def compress_parts(self, data, layout, rest=None):
-        """compress() as the reference's compress_parts chunk (bf16v2.py:276-291): pack_parts of
-        meta, side, tables, lens, stream, rest. `rest`: the header coder's output for the file's
-        other bytes; default the lzma form the reference falls back to without a tokenizer
-        (header_x of rest_of, gpu_bf16.py:421-424); needed when `data` is on the device"""
+    # the parts' order in a chunk: compress_parts' (bf16v2.py:276-291) and, for a base the reference
+    # writes while coding it, compress_stream's (bf16v2.py:293-321); unpack() finds parts by name
+    ORDER = {"parts": ("meta", "side", "tables", "lens", "stream", "rest"),
+             "stream": ("meta", "side", "tables", "stream", "lens", "rest")}
+
+    def compress_parts(self, data, layout, rest=None, order="parts"):
+        """compress() as a chunk, pack_parts' list of buffers: meta, side, tables, lens, stream, rest
+        (order="stream": meta, side, tables, stream, lens, rest). `rest`: the header coder's output
+        for the file's other bytes (seedpack_amd.header.header_c); default its lzma form; needed when
+        `data` is on the device"""
         ch = self.compress(data, layout)
         if rest is None:
             if isinstance(data, dev.DeviceArray):
                 raise ValueError("R2: a device-resident file needs its `rest` part from the caller")
             rest = header_x(rest_of(data, layout))
-        return pack_parts({"meta": ch["meta"], "side": ch["side"], "tables": ch["tables"], "lens": ch["lens"],
-                           "stream": ch["stream"], "rest": rest})
+        ch["rest"] = rest
+        return pack_parts({k: ch[k] for k in self.ORDER[order]})
 
     def decompress(self, parts, out=None, device=False, alloc=None):
         """the file back (bf16v2.py:422-486): `parts` is compress()'s dict or a packed chunk
@@ -401,7 +394,8 @@ class BF16v2:
         from `out` (already in place) or from the "rest" part when there is one, else zeros.
         alloc(n) -> writable uint8 array for the output. device=True: the result stays in HBM, a
         DeviceArray of the file's bytes up to the end of its last coded tensor, only the coded
-        tensors written (decompress_dev)."""
+        tensors written (decompress_dev); device="full": the whole file in HBM, the other bytes
+        uploaded from the "rest" part (-> (DeviceArray, rest_of bytes))."""
         st = self.stream
         tm = _Timer(self.timing, st)
         if not isinstance(parts, dict):
@@ -409,6 +403,8 @@ class BF16v2:
         dec = _Decoder(parts.__getitem__, st, tm)
         tm.lap("tables")
         layout, nt = dec.layout, len(dec.layout["t"])
+        if device == "full":
+            return self._decompress_full(parts, dec, tm)
         if nt == 0 and device:
             return dev.DeviceArray(1, np.uint8)
         if nt:
@@ -434,6 +430,27 @@ class BF16v2:
         if "rest" in parts:
             fill_rest(out, header_d(bytes(parts["rest"])), layout)
         return out
+
+    def _decompress_full(self, parts, dec, tm):
+        st, layout = self.stream, dec.layout
+        d = dev.DeviceArray(max(1, layout["size"]), np.uint8)
+        t = layout["t"]
+        if t:
+            s_d = _Decoder.upload(parts["stream"], st)
+            idxs = list(range(len(t)))
+            dec.run(s_d, dec.soff[:-1], d, idxs, [x[0] for x in t], tm)
+        rest = np.frombuffer(header_d(bytes(parts["rest"])), np.uint8)
+        staged = dev.pinned(max(1, rest.size))
+        staged[:] = rest
+        pos = taken = 0
+        for off, nb, *_ in t + [[layout["size"], 0]]:
+            if off > pos:                             # the bytes between coded tensors
+                check(lib().spa_memcpy_h2d(d.ptr + pos, staged[taken:].ctypes.data, off - pos, st))
+                taken += off - pos
+            pos = off + nb
+        dev.synchronize(st)
+        self.last_timing = tm.result()
+        return d, rest
 
 
 class _Decoder:
@@ -539,10 +556,14 @@ class _Decoder:
 
 
 class R2Tensors:
-    """random access to an R2-coded file on the device (bf16v2.py:488-617): any of its 2-D BF16
-    tensors decoded alone (its segments found from the segment lengths), the other bytes from the
-    "rest" part. part(name) -> bytes of a small part; read(offset, n, out) reads n bytes of the coded
-    stream (offset from its start) into the writable uint8 array `out`."""
+    """random access to an R2-coded file (bf16v2.py:488-617): any of its 2-D BF16 tensors decoded
+    alone on the device, the file's other bytes from the "rest" part. part(name) -> bytes of a small
+    part; read(offset, n, out) reads n bytes of the coded stream (offset from its start) into the
+    writable uint8 array `out`.
+
+    Per tensor i: its segments are seg0[i]..seg0[i+1] of the stream, their bytes soff[seg0[i]] ..
+    soff[seg0[i+1]]. A file position outside the coded tensors maps to position - (coded bytes
+    before it) of the rest."""
 
     def __init__(self, part, read, stream=None):
         self.read, self.stream = read, stream
@@ -550,67 +571,73 @@ class R2Tensors:
         self.layout = self.dec.layout
         self.size = self.layout["size"]
         t = self.layout["t"]
-        self.t_off = np.array([x[0] for x in t], np.int64)
-        self.before = np.zeros(len(t) + 1, np.int64)
-        self.before[1:] = np.cumsum([x[1] for x in t])
-        self.index = {x[0]: i for i, x in enumerate(t)}
+        self.index = {x[0]: i for i, x in enumerate(t)}           # file offset -> tensor index
+        self._starts = np.array([x[0] for x in t], np.int64)
+        self._coded_before = np.concatenate([[0], np.cumsum([x[1] for x in t])]).astype(np.int64)
+        seg_off = self.dec.soff[self.dec.seg0].astype(np.int64)       # stream offset of each tensor's first segment
+        self._span = np.stack([seg_off[:-1], seg_off[1:]], 1)        # [tensor] -> stream bytes [a, b)
         self.rest = np.frombuffer(header_d(bytes(part("rest"))), np.uint8)
 
     def coded_bytes(self, i):
         """bytes of the coded stream of tensor i"""
-        return int(self.dec.soff[self.dec.seg0[i + 1]] - self.dec.soff[self.dec.seg0[i]])
+        a, b = self._span[i]
+        return int(b - a)
 
     def outside(self, a, b):
-        """bytes [a, b) of the file, a range outside the coded tensors"""
-        k = int(np.searchsorted(self.t_off, a, side="right"))
-        r = a - int(self.before[k])
-        return self.rest[r:r + b - a]
+        """bytes [a, b) of the file, a range that no coded tensor overlaps"""
+        k = int(np.searchsorted(self._starts, a, side="right"))      # coded tensors starting at or before a
+        r = a - int(self._coded_before[k])
+        return self.rest[r:r + (b - a)]
 
     def fetch(self, idxs):
-        """the coded stream of tensors idxs read into host memory -> argument of decode()"""
-        soff, seg0 = self.dec.soff, self.dec.seg0
-        ranges = []                               # a tensor's range merged with its neighbour's
-        for i in sorted(idxs):
-            s0, s1 = int(soff[seg0[i]]), int(soff[seg0[i + 1]])
-            if ranges and ranges[-1][1] == s0:
-                ranges[-1][1] = s1
+        """the coded streams of tensors idxs read into one host buffer (neighbouring ranges in one
+        read) -> argument of decode(): (tensor indices, buffer, each tensor's offset in it)"""
+        idxs = list(idxs)
+        order = sorted(idxs, key=lambda i: self._span[i][0])
+        runs = []                                   # [stream start, stream end, tensors]
+        for i in order:
+            a, b = (int(v) for v in self._span[i])
+            if runs and runs[-1][1] == a:
+                runs[-1][1] = b
+                runs[-1][2].append(i)
             else:
-                ranges.append([s0, s1])
-        host = np.empty(max(1, sum(b - a for a, b in ranges)), np.uint8)
-        where, o = {}, 0
-        for a, b in ranges:
+                runs.append([a, b, [i]])
+        host = np.empty(max(1, sum(b - a for a, b, _ in runs)), np.uint8)
+        at, o = {}, 0
+        for a, b, members in runs:
             self.read(a, b - a, host[o:o + b - a])
-            where[a] = o
+            for i in members:
+                at[i] = o + int(self._span[i][0]) - a
             o += b - a
-        return list(idxs), host, where
+        return idxs, host, at
 
     def decode(self, idxs):
-        """coded tensors idxs (layout indices, or what fetch(idxs) returned) -> (DeviceArray, byte
-        offset of each tensor in it, 256-byte aligned)"""
+        """coded tensors idxs (layout indices, or what fetch() returned) -> (DeviceArray, byte offset
+        of each tensor in it, 256-byte aligned)"""
         t = self.layout["t"]
-        idxs, host, where = idxs if isinstance(idxs, tuple) else self.fetch(idxs)
+        idxs, host, at = idxs if isinstance(idxs, tuple) else self.fetch(idxs)
         soff, seg0 = self.dec.soff, self.dec.seg0
         in_off, outs, doff = [], [], 0
         for i in idxs:
-            s = soff[seg0[i]:seg0[i + 1]]
-            if len(s):
-                r0 = max(a for a in where if a <= int(s[0]))
-                in_off.append(s - np.uint64(r0) + np.uint64(where[r0]))
+            segs = soff[seg0[i]:seg0[i + 1]].astype(np.int64)
+            in_off.append((segs - segs[0] + at[i]).astype(np.uint64) if len(segs) else np.zeros(0, np.uint64))
             outs.append(doff)
             doff += -(-t[i][1] // 256) * 256
         d = dev.DeviceArray(max(doff, 1), np.uint8)
         s_d = _Decoder.upload(host, self.stream)
-        self.dec.run(s_d, np.concatenate(in_off) if in_off else np.zeros(0, np.uint64), d, list(idxs), outs)
+        self.dec.run(s_d, np.concatenate(in_off) if in_off else np.zeros(0, np.uint64), d, idxs, outs)
         return d, outs
 
     def write_to(self, write, window=1 << 30):
-        """the whole file, in order, through write(bytes-like): a window of tensors decoded at a time"""
+        """the whole file in order through write(bytes-like), decoding about `window` bytes of tensors
+        at a time"""
         t = self.layout["t"]
         pos, i = 0, 0
         while i < len(t):
-            j, nb = i, 0
-            while j < len(t) and (j == i or nb + t[j][1] <= window):
-                nb += t[j][1]
+            j = i + 1
+            total = t[i][1]
+            while j < len(t) and total + t[j][1] <= window:
+                total += t[j][1]
                 j += 1
             d, outs = self.decode(range(i, j))
             h = d.to_host(stream=self.stream)
@@ -624,88 +651,3 @@ class R2Tensors:
             i = j
         if pos < self.size:
             write(self.outside(pos, self.size))
-
-
-# ------------------------------------------------------------------ the file's other bytes
-# The header coder runs on the host (lzma); restated here so that a packed R2 chunk decodes whole.
-
-HEADER_CHUNKS = 4
-
-
-def rest_of(data, layout):
-    """the file's bytes outside its coded tensors, in order (gpu2.py:299-304)"""
-    parts, pos = [], 0
-    for off, nb, _, _ in layout["t"]:
-        parts.append(bytes(data[pos:off]))
-        pos = off + nb
-    parts.append(bytes(data[pos:]))
-    return b"".join(parts)
-
-
-def fill_rest(out, rest, layout):
-    """rest_of's bytes back around the coded tensors (gpu2.py:307-313)"""
-    pos = rpos = 0
-    for off, nb, _, _ in layout["t"]:
-        gap = off - pos
-        out[pos:off] = np.frombuffer(rest, np.uint8, gap, rpos)
-        rpos += gap
-        pos = off + nb
-    out[pos:] = np.frombuffer(rest, np.uint8, len(rest) - rpos, rpos)
-
-
-def xz_chunks_c(buf):
-    """lzma (preset 9 | extreme) of the bytes in HEADER_CHUNKS parts, lengths first (gpu2.py:316-321)"""
-    n = len(buf)
-    parts = [buf[i * n // HEADER_CHUNKS:(i + 1) * n // HEADER_CHUNKS] for i in range(HEADER_CHUNKS)]
-    with ThreadPoolExecutor(HEADER_CHUNKS) as ex:
-        out = list(ex.map(lambda p: lzma.compress(p, preset=9 | lzma.PRESET_EXTREME), parts))
-    return struct.pack(f"<{HEADER_CHUNKS}I", *map(len, out)) + b"".join(out)
-
-
-def xz_chunks_d(buf):
-    lens = struct.unpack_from(f"<{HEADER_CHUNKS}I", buf)
-    pos, parts = 4 * HEADER_CHUNKS, []
-    for ln in lens:
-        parts.append(buf[pos:pos + ln])
-        pos += ln
-    with ThreadPoolExecutor(HEADER_CHUNKS) as ex:
-        return b"".join(ex.map(lzma.decompress, parts))
-
-
-def header_pairs_d(buf):
-    """the tokenizer-aware header form (gpu2.py:434-457): GGUF token strings rebuilt from the 256
-    byte tokens and the BPE merge pairs, the merges array from the same pairs"""
-    t0, t1, m0, m1, ntok, nm = struct.unpack_from("<6Q", buf)
-    lens4 = struct.unpack_from("<4I", buf, 48)
-    pos, comp = 64, []
-    for ln in lens4:
-        comp.append(buf[pos:pos + ln])
-        pos += ln
-    with ThreadPoolExecutor(4) as ex:
-        stripped, lens, tb, planes = ex.map(lzma.decompress, comp)
-    lens = np.frombuffer(lens, np.uint16).astype(np.int64)
-    ends = np.cumsum(lens)
-    starts = ends - lens
-    raw = [tb[a:b] for a, b in zip(starts.tolist(), ends.tolist())]
-    pl = np.frombuffer(planes, np.uint8).reshape(3, 2, nm).astype(np.uint32)
-    pairs = (pl[0] | (pl[1] << 8) | (pl[2] << 16)).T.tolist()
-    toks = raw[:256]
-    merge_items = []
-    for a, b in pairs:
-        ta, tb_ = toks[a], toks[b]
-        toks.append(ta + tb_)
-        merge_items.append(struct.pack("<Q", len(ta) + len(tb_) + 1) + ta + b" " + tb_)
-    toks.extend(raw[256:])
-    tok_items = b"".join(struct.pack("<Q", len(x)) + x for x in toks)
-    b = t0 + (m0 - t1)
-    return stripped[:t0] + tok_items + stripped[t0:b] + b"".join(merge_items) + stripped[b:]
-
-
-def header_x(rest):
-    """the header part without a tokenizer: "X" + xz_chunks_c (gpu_bf16.py:421-424)"""
-    return b"X" + xz_chunks_c(rest)
-
-
-def header_d(buf):
-    """either header form back to rest_of's bytes (gpu_bf16.py:426-428)"""
-    return header_pairs_d(buf[1:]) if buf[:1] == b"P" else xz_chunks_d(buf[1:])

@@ -1,0 +1,720 @@
+"""Whole-repository archives on the MI355X: SeedPack's M29 method (seedpack/repo3.py M29RepoGPU and
+the pack / unpack / test steps of seedpack/cli.py) with this library's kernels.
+
+An archive holds the BF16 model (the "base", R2-coded) and the repository's other files; every
+quantized GGUF is stored as its difference from what the quantizers regrow from the base with the
+repository's imatrix: tensors the regrowth reproduces cost nothing, the rest are QR-coded against
+their prediction (or XORed, for float tensors).
+
+MI355X design. The reference bounds GPU memory: it streams the base in 1 GB windows and feeds each
+file to the GPU a window at a time (repo3.py:1869-2094). Here the whole base stays in HBM (a 9B
+model is 16-18 GB of 288 GB) and each quantized file is uploaded whole: its tensors are regrown,
+compared, XORed, QR-coded and zeroed on the device, and only the coded residual returns to the host.
+The reference's windows still decide bytes of the archive, so they are computed and applied where
+they do: a file's QR batches are cut per window and type (repo3.py:1956-1966, :946-979), a tensor
+equal to one an earlier file of the same window left a residual becomes a reference
+(repo3.py:2006-2030), and the zstd level of a file's residual is judged from its first span
+(repo3.py:1935-1944).
+
+Archive layout (the reference's, so that archives are interchangeable): chunks "extras" (lzma-9 of
+the packed small files), "x<j>" (zstd of a big extra file), "b<i>" (base i: pack({"r2": R2 chunk})),
+"f<i>" (file i's residual: zstd against the base header as raw-content dictionary), "q<i>" (its QR
+batches: pack({"meta": zstd(json [[type, names], ...]), "0": batch, ...})), "manifest" (zstd-19 of
+its JSON); the container index carries the catalog (names, sizes, SHA-256, roles).
+
+Not built here (they raise): base-less quant files (the reference's seed codec and M21), split
+GGUF models, quants made with another imatrix (imxfit), the M28 / M30 methods.
+"""
+import collections
+import fnmatch
+import hashlib
+import json
+import lzma
+import os
+import re
+import threading
+import time
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+
+from . import container, device as dev, gguf, header, imatrix as imx_mod, qr, r2, residual, zstd
+from ._lib import check, lib
+from .framing import nbytes, pack, pack_parts, unpack
+from .gpuquant import GPUQuant
+from .requant import QFUN
+
+METHOD = "M29 model repo: M28 with the BF16 v2 base codec (R2)"     # repo3.py:2539
+TOOL = "seedpack 0.5.0"              # the program whose archives these are byte-for-byte (cli.py:31)
+WINDOW = 1 << 30                     # base bytes per window (repo3.py:1672)
+PRED_WINDOW = 3 << 30                # first predictions per window, bytes (repo3.py:1677)
+DUP_MIN = 64 << 10                   # smaller tensors are not made references (repo3.py:1024)
+REF_KEEP = 3 << 30                   # bytes of referenced tensors per window (repo3.py:1887)
+BUNDLE_MAX = 64 << 20                # other files up to this size go into the lzma bundle (repo3.py:1364)
+SPARSE = 0.02                        # residuals with fewer non-zero bytes: zstd level >= 9 (repo3.py:45)
+SKIP_DIRS = {".git", ".cache", "__pycache__"}
+F32, F16, BF16 = 0, 1, 30
+
+
+def log(verbose, *a):
+    if verbose:
+        print(*a, flush=True)
+
+
+# ------------------------------------------------------------------ inputs
+
+def collect(inputs):
+    """input paths -> {name in the archive: path}: files by their base name, directories walked (sorted,
+    version-control and cache folders skipped) with names relative to them (cli.py:158-175)"""
+    out = {}
+    for inp in inputs:
+        if os.path.isdir(inp):
+            for root, dirs, fs in os.walk(inp):
+                dirs[:] = sorted(d for d in dirs if d not in SKIP_DIRS)
+                for f in sorted(fs):
+                    p = os.path.join(root, f)
+                    out.setdefault(os.path.relpath(p, inp).replace(os.sep, "/"), []).append(p)
+        elif os.path.isfile(inp):
+            out.setdefault(os.path.basename(inp), []).append(inp)
+        else:
+            raise FileNotFoundError(inp)
+    dup = [n for n, ps in out.items() if len(ps) > 1]
+    if dup:
+        raise ValueError(f"several inputs map to the same name in the archive: {', '.join(dup[:5])}")
+    return {n: ps[0] for n, ps in out.items()}
+
+
+def file_role(path):
+    """'base' for a GGUF whose tensor bytes are at least half BF16, 'derived' for another GGUF, None for
+    any other file or an imatrix GGUF (cli.py:181-205)"""
+    if not path.lower().endswith(".gguf"):
+        return None
+    meta, ts = gguf.meta_of(path), gguf.tensors_of(path)
+    if not meta and not ts:
+        return None
+    if meta.get("general.type") == "imatrix":
+        return None
+    total = sum(t.nbytes for t in ts) or 1
+    return "base" if sum(t.nbytes for t in ts if t.type == BF16) / total >= 0.5 else "derived"
+
+
+def order_groups(orders):
+    """the files' tensor orders (tuples of names) -> {a group's order: [its files' indices]}: longest
+    orders first, a file whose order is a subsequence of a group's joins it (repo3.py:277-291)"""
+    groups = {}
+    for k in sorted(range(len(orders)), key=lambda k: -len(orders[k])):
+        for g in groups:
+            it = iter(g)
+            if all(n in it for n in orders[k]):
+                groups[g].append(k)
+                break
+        else:
+            groups[orders[k]] = [k]
+    return {g: sorted(ks) for g, ks in groups.items()}
+
+
+def windows(nbytes_, window=WINDOW, pred=None, pred_window=PRED_WINDOW):
+    """positions 0..n-1 (tensors in order, their base bytes) -> [(start, end)]: a window closes before a
+    tensor that would take it past `window` base bytes or `pred_window` prediction bytes
+    (repo3.py:1689-1706)"""
+    pred = pred or [0] * len(nbytes_)
+    out, s, acc, accp = [], 0, 0, 0
+    for p in range(len(nbytes_)):
+        if p > s and (acc + nbytes_[p] > window or accp + pred[p] > pred_window):
+            out.append((s, p))
+            s, acc, accp = p, 0, 0
+        acc += nbytes_[p]
+        accp += pred[p]
+    if nbytes_:
+        out.append((s, len(nbytes_)))
+    return out
+
+
+def _read_into(path, out, off=0, pool=None):
+    """bytes [off, off + len(out)) of a file into the writable uint8 array `out`, in parallel pieces"""
+    n = out.size
+    step = 64 << 20
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        def piece(o):
+            mv = memoryview(out[o:o + step])
+            got = 0
+            while got < len(mv):
+                k = os.preadv(fd, [mv[got:]], off + o + got)
+                if k <= 0:
+                    raise IOError(f"{path}: file shrank while being read")
+                got += k
+        if pool is None or n <= step:
+            for o in range(0, n, step):
+                piece(o)
+        else:
+            for f in [pool.submit(piece, o) for o in range(0, n, step)]:
+                f.result()
+    finally:
+        os.close(fd)
+    return out
+
+
+class _Staging:
+    """reusable page-locked host buffers (copies to and from HBM at the link's full rate), grown on demand"""
+
+    def __init__(self):
+        self.bufs = {}
+
+    def get(self, key, n):
+        b = self.bufs.get(key)
+        if b is None or b.size < n:
+            self.bufs.pop(key, None)
+            b = self.bufs[key] = dev.pinned(max(n, 1 << 20))
+        return b[:n]
+
+
+class _DevBuf:
+    """a reusable device buffer (freeing HBM waits for the whole device), grown on demand"""
+
+    def __init__(self):
+        self.a = None
+
+    def get(self, n):
+        if self.a is None or self.a.nbytes < n:
+            self.a = None
+            self.a = dev.DeviceArray(max(n, 1 << 20), np.uint8)
+        return self.a.view(0, (n,), np.uint8)
+
+
+class _Base:
+    """a base model resident in HBM: the whole file (header included) at its file offsets"""
+
+    def __init__(self, index, name, host, d, g):
+        self.index, self.name, self.d, self.g = index, name, d, g
+        self.header = bytes(host[:g.data_start])
+        self.by_name = {t.name: t for t in g.tensors}
+
+    def view(self, t):
+        """base tensor t as the quantizers take it (bf16 bits / f16 / f32)"""
+        dt = np.uint16 if t.type == BF16 else np.float16 if t.type == F16 else np.float32
+        return self.d.view(t.offset, (t.numel,), dt)
+
+
+def _ws(n):
+    """sha256 of a buffer"""
+    return hashlib.sha256(memoryview(n).cast("B")).hexdigest()
+
+
+# ------------------------------------------------------------------ packing
+
+class Packer:
+    """pack(inputs, output) -> stats; the M29 pipeline of repo3.M28RepoGPU.compress (repo3.py:1374-1662)
+    for a repository with BF16 base model(s), quantized GGUFs derived from them, an imatrix and other
+    files"""
+
+    def __init__(self, level=7, verbose=False, coders=4):
+        self.level, self.verbose = level, verbose
+        self.stream = dev.Stream()
+        self.gq = GPUQuant(stream=self.stream.handle)
+        self.io = ThreadPoolExecutor(8)          # file reads (pieces), tensor hashes
+        self.hasher = ThreadPoolExecutor(4)      # file checksums
+        self.zpool = ThreadPoolExecutor(4)       # residual zstd, QR framing
+        self.coders = ThreadPoolExecutor(coders)
+        self.tls = threading.local()
+        self.staging = _Staging()
+        self.fbuf = _DevBuf()
+        self.stats = collections.Counter()
+        self.sizes = {}
+
+    # ---------------------------------------------------------------- bases
+    def _load_base(self, i, name, path):
+        """the base file read into page-locked memory and uploaded whole"""
+        size = os.path.getsize(path)
+        host = dev.pinned(size)
+        _read_into(path, host, pool=self.io)
+        d = dev.DeviceArray(size, np.uint8)
+        check(lib().spa_memcpy_h2d(d.ptr, host.ctypes.data, size, self.stream.handle))
+        return host, _Base(i, name, host, d, gguf.GGUF(host))
+
+    def _code_base(self, b, host, order):
+        """the base's chunk: pack({"r2": R2 chunk}) with the reference's part order, coded on its own
+        stream from the resident copy"""
+        s = dev.Stream()
+        g = b.g
+        lay = r2.layout_of([(t.name, t.offset, t.nbytes, t.shape[0]) for t in g.tensors
+                            if t.type == BF16 and len(t.shape) == 2], len(host))
+        with ThreadPoolExecutor(1) as hp:
+            rest = hp.submit(header.header_c, host, g, lay)
+            codec = r2.BF16v2(stream=s.handle)
+            inner = codec.compress_parts(b.d, lay, rest=rest.result(), order=order) if lay["t"] else \
+                pack_parts({"meta": zstd.compress(json.dumps({"layout": lay, "dups": [], "nrows_c": []}).encode(), 19),
+                            "side": zstd.compress(b"", 19), "tables": r2.store_tables(np.zeros((0, 256), np.uint16), []),
+                            "lens": zstd.compress(b"", 19), "stream": b"", "rest": rest.result()})
+        s.synchronize()
+        return pack_parts({"r2": inner})
+
+    # ---------------------------------------------------------------- QR coding on worker streams
+    def _qr_job(self, T, items, seed, imx):
+        if not hasattr(self.tls, "stream"):
+            self.tls.stream = dev.Stream()
+        parts = qr.encode_parts(T, items, seed, imx, stream=self.tls.stream.handle)
+        return qr.frame(parts)
+
+    # ---------------------------------------------------------------- one derived file
+    def _residual_file(self, fi, name, path, b, tens, wins_of, wstate, imx_dev, imx_off, imx_map, last_window):
+        """file fi against base b: its bytes read and hashed, uploaded, regrown and compared, QR-coded and
+        zeroed on the device -> (manifest entry, residual chunk, QR chunk or None, checksum)"""
+        size = os.path.getsize(path)
+        host = self.staging.get(("in", fi % 2), size)
+        _read_into(path, host, pool=self.io)
+        hjob = self.hasher.submit(_ws, host)
+        pred = [(t, k) for t, k in tens if k]
+        by_name = {t.name: t for t, _ in tens}
+        thash = {t.name: f for t, f in ((t, self.io.submit(lambda a: hashlib.blake2b(a, digest_size=16).digest(),
+                                                                  host[t.offset:t.offset + t.nbytes]))
+                                        for t, _ in pred)}
+        F = self.fbuf.get(size)
+        st = self.stream.handle
+        check(lib().spa_memcpy_h2d(F.ptr, host.ctypes.data, size, st))
+        thash = {n: f.result() for n, f in thash.items()}
+        # references: equal to a tensor an earlier file of the same window left a residual in
+        refs, mine = {}, []
+        for t, k in pred:
+            w = wins_of[t.name]
+            ws = wstate[w]
+            key = (t.name, t.type, thash[t.name])
+            src = ws["first"].get(key)
+            if src is not None and ws["memo"].get(key, False) and t.nbytes >= DUP_MIN:
+                if (src, t.name) not in ws["kept"]:
+                    if ws["kept_bytes"] + t.nbytes > REF_KEEP:
+                        mine.append((t, k))
+                        continue
+                    ws["kept"].add((src, t.name))
+                    ws["kept_bytes"] += t.nbytes
+                refs[t.name] = [src, t.name]
+                check(lib().spa_memset(F.ptr + t.offset, 0, t.nbytes, st))
+                continue
+            mine.append((t, k))
+        self.stats["ref"] += len(refs)
+        rts = [residual.Tensor(t.name, t.type, t.shape[0], F.view(t.offset, (t.nbytes,), np.uint8),
+                               b.view(b.by_name[t.name]), imatrix=imx_map.get(t.name), base_type=b.by_name[t.name].type,
+                               numel=t.numel) for t, _ in mine]
+        res = residual.residual_window(rts, self.gq, stream=st) if rts else []
+        out = {t.name: r for (t, _), r in zip(mine, res)}
+        for t, _ in mine:
+            ws = wstate[wins_of[t.name]]
+            key = (t.name, t.type, thash[t.name])
+            ws["first"].setdefault(key, fi)
+            ws["memo"][key] = bool(out[t.name]["nonzero"])
+        # plan entries and QR batches, window by window (the reference's order)
+        plan, qmeta, qjobs = [], [], []
+        by_w = collections.defaultdict(list)
+        for t, _ in pred:
+            by_w[wins_of[t.name]].append(t)
+        for w in sorted(by_w):
+            qitems = collections.defaultdict(list)
+            for t in by_w[w]:
+                if t.name in refs:
+                    continue
+                r = out[t.name]
+                plan.append([t.name, "qr" if r["qr"] else r["kind"], r["variant"], t.type])
+                if r["qr"]:
+                    qitems[t.type].append(t)
+            plan += [[n, "ref", refs[n], by_name[n].type] for n in refs if wins_of[n] == w]
+            for T, ts in qitems.items():
+                for batch in qr.batches(T, [t.nbytes for t in ts]):
+                    its = [ts[i] for i in batch]
+                    items = [(F.view(t.offset, (t.nbytes,), np.uint8), out[t.name]["prediction"], b.by_name[t.name].offset,
+                              b.by_name[t.name].type, b.by_name[t.name].shape[0],
+                              imx_off.get(t.name, -1) if T in qr.GRID_TYPES else -1) for t in its]
+                    if T in qr.GRID_TYPES:
+                        self.stats["qr_grid"] += len(its)
+                    qmeta.append([T, [t.name for t in its]])
+                    qjobs.append(self.coders.submit(self._qr_job, T, items, b.d, imx_dev if T in qr.GRID_TYPES else None))
+            for t in by_w[w]:
+                if t.name in out:
+                    self.stats["xor" if out[t.name]["kind"] == "xor" else
+                               "requant_diff" if out[t.name]["nonzero"] else "requant_exact"] += 1
+        self.stats["qr"] += sum(len(m[1]) for m in qmeta)
+        self.stream.synchronize()
+        qparts = [f.result() for f in qjobs]             # the coders read the QR tensors' file bytes
+        qr_regions = [(t.offset, t.nbytes) for t, _ in mine if out[t.name]["qr"]]
+        for off, nb in qr_regions:
+            check(lib().spa_memset(F.ptr + off, 0, nb, st))
+        resid = self.staging.get(("out", fi % 2), size)
+        check(lib().spa_memcpy_d2h(resid.ctypes.data, F.ptr, size, st))
+        # the zstd level, judged as the reference judges it: from the file's first span that holds a
+        # predicted tensor, from that tensor on, before the QR jobs zero their tensors (repo3.py:1935-1944)
+        prm = self._zparams(resid, host, pred, wins_of, qr_regions, last_window)
+        digest = hjob.result()
+        zjob = self.zpool.submit(zstd.compress_with, resid, prm, b.header)
+        qchunk = None
+        if qmeta:
+            qchunk = pack_parts({"meta": zstd.compress(json.dumps(qmeta).encode(), 19),
+                                 **{str(k): p for k, p in enumerate(qparts)}})
+        entry = {"name": name, "size": size, "base": b.index, "plan": plan}
+        return entry, zjob.result(), qchunk, digest
+
+    def _zparams(self, resid, host, pred, wins_of, qr_regions, last_window):
+        """zstd parameters of a file's residual: the sparse level when under SPARSE of every 61st byte of
+        its first span, from its first predicted tensor on, is non-zero (QR tensors still holding their
+        file bytes)"""
+        pred = [t for t, _ in pred]
+        start = min(t.offset for t in pred)
+        first_w = min(wins_of[t.name] for t in pred)
+        end = max(t.offset + t.nbytes for t in pred if wins_of[t.name] == first_w)
+        if first_w == last_window:
+            end = len(resid)                        # the last window's span runs to the end of the file
+        pos = np.arange(start, end, 61, dtype=np.int64)
+        v = resid[pos]                              # (fancy indexing: a copy)
+        for off, nb in qr_regions:
+            m = (pos >= off) & (pos < off + nb)
+            if m.any():
+                v[m] = host[pos[m]]
+        sparse = np.count_nonzero(v) * 61 < SPARSE * (end - start)
+        return zstd.Params(max(self.level, 9) if sparse else self.level, window_log=25)
+
+    # ---------------------------------------------------------------- the repository
+    def pack(self, inputs, output, tool=TOOL, created=None, force=False):
+        t0 = time.perf_counter()
+        files = collect(inputs)
+        if not files:
+            raise ValueError("nothing to archive")
+        if os.path.exists(output) and not force:
+            raise FileExistsError(output)
+        roles = {n: file_role(p) for n, p in files.items()}
+        bases = {n: p for n, p in files.items() if roles[n] == "base"}
+        derived = {n: p for n, p in files.items() if roles[n] == "derived"}
+        extras = {n: p for n, p in files.items() if roles[n] is None}
+        if any(re.match(r"^.*-\d{5}-of-\d{5}\.gguf$", n) for n in bases):
+            raise NotImplementedError("split GGUF models (joined bases) are not built")
+        base_names = [{t.name for t in gguf.tensors_of(p)} for p in bases.values()]
+        orphans = [n for n, p in derived.items() if not any({t.name for t in gguf.tensors_of(p)} & s for s in base_names)]
+        if orphans:
+            raise NotImplementedError(f"quantized files without a base ({orphans[0]}): the seed codec is not built")
+        total = sum(os.path.getsize(p) for p in files.values())
+        hashes = {}
+        w = container.Writer(output)
+        try:
+            # other files: the small ones in one lzma bundle, the big ones zstd'd one by one
+            small = {n: p for n, p in extras.items() if os.path.getsize(p) <= BUNDLE_MAX}
+            ex = {n: open(p, "rb").read() for n, p in small.items()}
+            for n, data in ex.items():
+                hashes[n] = self.hasher.submit(_ws, data)
+            bundle = lzma.compress(pack(ex), preset=9)
+            w.put("extras", bundle)
+            self.sizes["other files"] = len(bundle)
+            big = {}
+            for j, (n, p) in enumerate((n, p) for n, p in extras.items() if n not in small):
+                data = open(p, "rb").read()
+                hashes[n] = self.hasher.submit(_ws, data)
+                c = zstd.compress_with(data, zstd.Params(self.level, threads=8, ldm=True))
+                w.put(f"x{j}", c)
+                self.sizes[n] = len(c)
+                big[n] = [f"x{j}", len(data)]
+            imx_name = next((n for n in ex if n.startswith("imatrix")), None)
+            imx_all = imx_mod.load(ex[imx_name]) if imx_name else {}
+            # bases: read, uploaded, their checksums and codecs started (one stream each)
+            loaded = []
+            side = ThreadPoolExecutor(1)
+            base_jobs = []
+            for i, (n, p) in enumerate(bases.items()):
+                host, b = self._load_base(i, n, p)
+                hashes[n] = self.hasher.submit(_ws, host)
+                loaded.append((host, b))
+                base_jobs.append(side.submit(self._code_base, b, host, "stream" if i == 0 else "parts"))
+            self.stream.synchronize()
+            log(self.verbose, f"  {len(bases)} base(s) resident in HBM, {time.perf_counter() - t0:.1f} s")
+            # the repository's importance per tensor on the device (the grid QR types read it)
+            imx_vecs = {k: np.asarray(v, np.float32) for k, v in imx_all.items()}
+            flat = np.concatenate(list(imx_vecs.values())) if imx_vecs else np.zeros(1, np.float32)
+            imx_dev = dev.DeviceArray.from_host(flat, self.stream.handle)
+            imx_off, o = {}, 0
+            for k, v in imx_vecs.items():
+                imx_off[k] = o
+                o += v.size
+            imx_map = {k: imx_dev.view(4 * imx_off[k], (v.size,), np.float32) for k, v in imx_vecs.items()}
+            # derived files, per base, grouped by tensor order; windows over the base's tensor order
+            names = list(derived)
+            entries, chunks = [None] * len(names), {}
+            per_base = collections.defaultdict(list)
+            for fi, n in enumerate(names):
+                ts = gguf.tensors_of(derived[n])
+                common = [len({t.name for t in ts} & s) for s in base_names]
+                best = [k for k, c in enumerate(common) if c == max(common)][0]
+                per_base[best].append((fi, n, ts))
+            order_done = []
+            for bi, items in per_base.items():
+                host_b, b = loaded[bi]
+                found, plain = [], []
+                for fi, n, ts in items:
+                    tk = [(t, self._kind(b, t, imx_all)) for t in ts]
+                    self.stats["raw"] += sum(k is None for _, k in tk)
+                    order = tuple(t.name for t, k in sorted(tk, key=lambda x: x[0].offset) if k)
+                    (found if order else plain).append((order, fi, n, tk))
+                for order, ks in order_groups([f[0] for f in found]).items():
+                    sts = [found[k] for k in ks]
+                    # the windows' prediction bytes: per tensor, its distinct first predictions over the files
+                    pred = [sum({(t.type, residual.v0(k_, imx_all.get(t.name) is not None)): t.nbytes
+                                 for _, _, _, tk in sts for t, k_ in tk if t.name == nm and k_}.values()) for nm in order]
+                    wins = windows([b.by_name[nm].nbytes for nm in order], WINDOW, pred)
+                    wins_of = {nm: w_ for w_, (a, z) in enumerate(wins) for nm in order[a:z]}
+                    wstate = [{"first": {}, "memo": {}, "kept": set(), "kept_bytes": 0} for _ in wins]
+                    for _, fi, n, tk in sts:
+                        tf = time.perf_counter()
+                        entry, fchunk, qchunk, digest = self._residual_file(fi, n, derived[n], b, tk, wins_of, wstate,
+                                                                            imx_dev, imx_off, imx_map, len(wins) - 1)
+                        entries[fi], chunks[fi], hashes[n] = entry, (fchunk, qchunk), digest
+                        order_done.append(fi)
+                        log(self.verbose, f"  {n}: {entry['size']:,} B -> {len(fchunk):,} + "
+                                          f"{nbytes(qchunk) if qchunk else 0:,} B in {time.perf_counter() - tf:.2f} s")
+                for _, fi, n, tk in plain:
+                    # nothing to predict: the file zstd'd against the base header (repo3.py:2062-2076)
+                    data = open(derived[n], "rb").read()
+                    hashes[n] = self.hasher.submit(_ws, data)
+                    entries[fi] = {"name": n, "size": len(data), "base": b.index, "plan": []}
+                    chunks[fi] = (zstd.compress_with(data, zstd.Params(self.level, window_log=25, threads=4), b.header), None)
+                    order_done.append(fi)
+            coded = [j.result() for j in base_jobs]
+            side.shutdown()
+            # chunk order of the reference: the first base (written while it is coded), the files
+            # derived from the bases, then the other bases
+            w.put("b0", coded[0]) if coded else None
+            for fi in order_done:
+                fchunk, qchunk = chunks[fi]
+                w.put(f"f{fi}", fchunk)
+                self.sizes[names[fi]] = len(fchunk)
+                if qchunk is not None:
+                    w.put(f"q{fi}", qchunk)
+                    self.sizes[names[fi] + " (QR)"] = nbytes(qchunk)
+            for i in range(1, len(coded)):
+                w.put(f"b{i}", coded[i])
+            for n, c in zip(bases, coded):
+                self.sizes[n] = nbytes(c)
+            manifest = {"method": METHOD, "bases": list(bases), "seeds": [], "files": entries,
+                        "extras": {"bundle": list(ex), "single": big}}
+            if self.stats["qr_grid"] or self.stats["ref"]:
+                manifest["needs"] = "0.3.0"
+            w.put("manifest", zstd.compress(json.dumps(manifest).encode(), 19))
+            hashes = {n: (h.result() if hasattr(h, "result") else h) for n, h in hashes.items()}
+            catalog = [{"name": n, "size": os.path.getsize(p), "hash": hashes[n], "role": roles[n] or "file",
+                        "stored": self.sizes.get(n)} for n, p in files.items()]
+            w.close({"tool": tool, "method": METHOD, "created": created or _created(), "hash": "sha256",
+                     "files": catalog, "total": total})
+        except BaseException:
+            w.abort()
+            raise
+        dt = time.perf_counter() - t0
+        size = os.path.getsize(output)
+        log(self.verbose, f"{output}: {total:,} B -> {size:,} B in {dt:.1f} s ({total / dt / 1e9:.2f} GB/s)")
+        return {"input_bytes": total, "archive_bytes": size, "seconds": dt, "GB_s": total / dt / 1e9,
+                "stats": dict(self.stats)}
+
+    @staticmethod
+    def _kind(b, t, imx_all):
+        """how tensor t of a quantized file is predicted from base b: 'rq', 'xor' or None (repo3.py:691-700)"""
+        bt = b.by_name.get(t.name)
+        if bt is None:
+            return None
+        k = residual.kind(bt.type, bt.numel, t.type, t.numel, t.nbytes)
+        e = imx_all.get(t.name)
+        if k == "rq" and e is not None and len(e) != bt.shape[0]:
+            raise NotImplementedError(f"{t.name}: an importance vector of {len(e)} values for rows of {bt.shape[0]}")
+        return k
+
+
+def _created():
+    """the archive's creation time: now, or $SOURCE_DATE_EPOCH (UTC) for reproducible archives (cli.py:209-215)"""
+    epoch = os.environ.get("SOURCE_DATE_EPOCH")
+    if epoch:
+        return time.strftime("%Y-%m-%dT%H:%M:%S", time.gmtime(int(epoch)))
+    return time.strftime("%Y-%m-%dT%H:%M:%S")
+
+
+def pack_repo(inputs, output, **kw):
+    """pack the files / directories `inputs` into the archive `output` -> stats"""
+    return Packer(level=kw.pop("level", 7), verbose=kw.pop("verbose", False)).pack(inputs, output, **kw)
+
+
+# ------------------------------------------------------------------ unpacking / testing
+
+def select_names(catalog, patterns):
+    """the catalog's names matching the patterns (exact, glob or base name), in catalog order
+    (cli.py:296-306); all of them without patterns"""
+    names = [f["name"] for f in catalog]
+    if not patterns:
+        return names
+    chosen = []
+    for pat in patterns:
+        hit = [n for n in names if fnmatch.fnmatchcase(n, pat) or n == pat or os.path.basename(n) == pat]
+        if not hit:
+            raise KeyError(f"{pat}: no such file in the archive")
+        chosen += [n for n in hit if n not in chosen]
+    return chosen
+
+
+class Unpacker:
+    """the files of an archive rebuilt and checked against their SHA-256 (repo3.py:2277-2509,
+    cli.py:309-441): each base decoded into HBM once; each quantized file's residual decompressed on
+    the host, uploaded, its predictions regrown and XORed in and its QR batches decoded on the device,
+    then read back, checked and written"""
+
+    def __init__(self, verbose=False):
+        self.verbose = verbose
+        self.stream = dev.Stream()
+        self.gq = GPUQuant(stream=self.stream.handle)
+        self.staging = _Staging()
+        self.rbuf = _DevBuf()
+        self.io = ThreadPoolExecutor(4)           # checksums and writes
+
+    def run(self, archive, outdir=None, patterns=None):
+        t0 = time.perf_counter()
+        r = container.Reader(archive)
+        meta = r.meta
+        manifest = json.loads(zstd.decompress(r.get("manifest")))
+        if not manifest["method"].startswith("M29"):
+            raise NotImplementedError(f"archive method {manifest['method']!r}: only M29 archives are read here")
+        if manifest.get("seeds") or manifest.get("joined") or manifest.get("imx_fit"):
+            raise NotImplementedError("seeds, split models and fitted importance are not built")
+        cat = {f["name"]: f for f in meta["files"]}
+        want = set(select_names(meta["files"], patterns))
+        mf = manifest["files"]
+        sel = {i for i, m in enumerate(mf) if m["name"] in want}
+        todo = list(sel)
+        while todo:                                # files holding the sources of references
+            for e in mf[todo.pop()]["plan"]:
+                if e[1] in ("ref", "dup") and e[2][0] not in sel:
+                    sel.add(e[2][0])
+                    todo.append(e[2][0])
+        last_use = {}
+        for i in sorted(sel):
+            for e in mf[i]["plan"]:
+                if e[1] in ("ref", "dup"):
+                    last_use[tuple(e[2])] = max(last_use.get(tuple(e[2]), -1), i)
+        need_b = {i for i, n in enumerate(manifest["bases"]) if n in want} | \
+                 {mf[i]["base"] for i in sel if mf[i]["base"] is not None}
+        results, jobs = {}, []
+
+        def check_write(name, buf):
+            ok = hashlib.sha256(memoryview(buf).cast("B")).hexdigest() == cat[name]["hash"] and \
+                memoryview(buf).nbytes == cat[name]["size"]
+            if ok and outdir is not None:
+                path = os.path.join(outdir, *name.split("/"))
+                os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
+                with open(path + ".part", "wb") as f:
+                    f.write(memoryview(buf).cast("B"))
+                os.replace(path + ".part", path)
+            results[name] = ok
+            return ok
+
+        # other files
+        exm = manifest["extras"]
+        if any(n in want for n in exm["bundle"]) or sel:
+            ex = {k: bytes(v) for k, v in unpack(lzma.decompress(bytes(r.get("extras")))).items()}
+            for n in exm["bundle"]:
+                if n in want:
+                    jobs.append(self.io.submit(check_write, n, ex[n]))
+        else:
+            ex = {}
+        for n, (c, size) in exm["single"].items():
+            if n in want:
+                out = np.empty(size, np.uint8)
+                jobs.append(self.io.submit(check_write, n, zstd.decompress_into(r.get(c), out)))
+        imx_name = next((n for n in ex if n.startswith("imatrix")), None)
+        imx_all = {k: np.asarray(v, np.float32) for k, v in (imx_mod.load(ex[imx_name]) if imx_name else {}).items()}
+        flat = np.concatenate(list(imx_all.values())) if imx_all else np.zeros(1, np.float32)
+        imx_dev = dev.DeviceArray.from_host(flat, self.stream.handle)
+        imx_off, o = {}, 0
+        for k, v in imx_all.items():
+            imx_off[k] = o
+            o += v.size
+        imx_map = {k: imx_dev.view(4 * imx_off[k], (v.size,), np.float32) for k, v in imx_all.items()}
+        # bases, decoded into HBM
+        bases = {}
+        for i in sorted(need_b):
+            name = manifest["bases"][i]
+            ch = unpack(memoryview(r.get(f"b{i}")))
+            if "r2" not in ch:
+                raise NotImplementedError(f"base {name}: only R2-coded bases are read here")
+            d, rest = r2.BF16v2(stream=self.stream.handle).decompress(unpack(ch["r2"]), device="full")
+            g = gguf.GGUF(rest.tobytes(), light=True)     # the header is the start of the rest part
+            b = _Base(i, name, rest, d, g)
+            bases[i] = b
+            if name in want:
+                host = self.staging.get(("base", i), d.nbytes)
+                check(lib().spa_memcpy_d2h(host.ctypes.data, d.ptr, d.nbytes, self.stream.handle))
+                jobs.append(self.io.submit(check_write, name, host))
+            log(self.verbose, f"  base {name}: decoded, {time.perf_counter() - t0:.1f} s")
+        # quantized files, in archive order; tensors that later files copy are kept on the device
+        kept = {}
+        for i in sorted(sel):
+            m = mf[i]
+            tf = time.perf_counter()
+            b = bases.get(m["base"]) if m["base"] is not None else None
+            resid = self.staging.get(("file", i % 2), m["size"])
+            zstd.decompress_into(r.get(f"f{i}"), resid, b.header if b is not None else None)
+            if m["plan"]:
+                self._rebuild(r, i, m, b, resid, kept, last_use, imx_dev, imx_off, imx_map)
+            if m["name"] in want:
+                jobs.append(self.io.submit(check_write, m["name"], resid))
+                jobs[-1].result()                 # (its staging buffer is reused two files on)
+            log(self.verbose, f"  {m['name']}: {m['size']:,} B in {time.perf_counter() - tf:.2f} s")
+        for j in jobs:
+            j.result()
+        r.close()
+        dt = time.perf_counter() - t0
+        nbytes_ = sum(cat[n]["size"] for n in results)
+        return {"files": results, "bad": [n for n, ok in results.items() if not ok],
+                "missing": [n for n in want if n not in results], "bytes": nbytes_, "seconds": dt,
+                "GB_s": nbytes_ / dt / 1e9}
+
+    def _rebuild(self, r, i, m, b, resid, kept, last_use, imx_dev, imx_off, imx_map):
+        """file i's bytes from its residual (in `resid`, rebuilt in place) on the device"""
+        st = self.stream.handle
+        size = m["size"]
+        R = self.rbuf.get(size)
+        check(lib().spa_memcpy_h2d(R.ptr, resid.ctypes.data, size, st))
+        tens = {t.name: t for t in gguf.GGUF(resid, light=True).tensors}
+        plan = m["plan"]
+        ttype = {e[0]: (e[3] if len(e) > 3 else tens[e[0]].type) for e in plan}
+
+        def tensor(name):
+            bt = b.by_name[name]
+            return residual.Tensor(name, ttype[name], bt.shape[0], R.view(tens[name].offset, (tens[name].nbytes,), np.uint8),
+                                   b.view(bt), imatrix=imx_map.get(name), base_type=bt.type, numel=tens[name].numel)
+
+        for e in plan:
+            name, kind, v = e[0], e[1], e[2]
+            if kind in ("rq", "xor"):
+                t = tensor(name)
+                p = residual.predict(self.gq, t, v, stream=st)
+                check(lib().spa_xor(t.region.ptr, t.region.ptr, p.ptr, t.region.nbytes, None, st))
+        if any(e[1] == "qr" for e in plan):
+            ch = unpack(memoryview(r.get(f"q{i}")))
+            var = {e[0]: e[2] for e in plan}
+            for k, (T, names) in enumerate(json.loads(zstd.decompress(ch["meta"]))):
+                ts = [tensor(n) for n in names]
+                preds = [residual.predict(self.gq, t, var[t.name], stream=st) for t in ts]
+                items = [(p, b.by_name[t.name].offset, b.by_name[t.name].type, b.by_name[t.name].shape[0],
+                          imx_off.get(t.name, -1) if T in qr.GRID_TYPES else -1) for t, p in zip(ts, preds)]
+                F = qr.decode(T, bytes(ch[str(k)]), items, b.d, imx_dev if T in qr.GRID_TYPES else None, stream=st)
+                o = 0
+                for t in ts:
+                    check(lib().spa_memcpy_d2d(t.region.ptr, F.ptr + o, t.region.nbytes, st))
+                    o += t.region.nbytes
+                del F, preds
+        for e in plan:
+            if e[1] in ("ref", "dup"):
+                src = kept[tuple(e[2])]
+                t = tens[e[0]]
+                check(lib().spa_memcpy_d2d(R.ptr + t.offset, src.ptr, t.nbytes, st))
+        for key in [key for key, last in last_use.items() if last <= i and key in kept]:
+            del kept[key]
+        for (fi, name), last in last_use.items():
+            if fi == i and last > i:
+                t = tens[name]
+                a = dev.DeviceArray(t.nbytes, np.uint8)
+                check(lib().spa_memcpy_d2d(a.ptr, R.ptr + t.offset, t.nbytes, st))
+                kept[(fi, name)] = a
+        check(lib().spa_memcpy_d2h(resid.ctypes.data, R.ptr, size, st))
+
+
+def unpack_repo(archive, outdir=None, patterns=None, verbose=False):
+    """extract (outdir given) or test the archive's files -> stats (the checksum result per file)"""
+    return Unpacker(verbose=verbose).run(archive, outdir, patterns)

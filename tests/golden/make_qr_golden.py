@@ -16,6 +16,7 @@ BASELINE.json configs[0].
 import ast
 import os
 import sys
+import tempfile
 
 import numpy as np
 
@@ -25,7 +26,9 @@ REF = "/root/reference"
 sys.path.insert(0, ROOT)
 
 os.environ["SEEDPACK_CPU"] = "1"
-os.environ.setdefault("SEEDPACK_CACHE", os.path.join(ROOT, "_work", "refcache"))
+# the reference's --cpu backend caches its compiled kernels; a temporary directory keeps them out of
+# the repository
+os.environ.setdefault("SEEDPACK_CACHE", tempfile.mkdtemp(prefix="seedpack_refcache_"))
 sys.path.insert(0, REF)
 
 from oracle import ref as qref  # noqa: E402

@@ -4,7 +4,8 @@ row_hash), table normalisation (gpu2.normalize_gpu) and its v2_hist / v2_enc / v
 through the reference's --cpu backend (seedpack/cpu.py, seedpack/cpukernels.py). Run in the build
 container only:
 
-    python tests/golden/make_r2_golden.py
+    python tests/golden/make_r2_golden.py            # r2_vectors.npz
+    python tests/golden/make_r2_golden.py --header   # header_vectors.npz: the "rest" part's two forms
 
 bf16v2.py and gpu2.py import numba / zstandard (absent here), so the functions and the kernel text
 are read with `ast` and executed against the --cpu backend; the driver steps of
@@ -12,9 +13,12 @@ BF16v2._analyse / _encode (bf16v2.py:323-411: per group of tensors, statistics, 
 normalisation; encode, gather) are restated below without the GGUF parsing and header coding.
 Nothing here runs on the GPU box or at test time: the output is data (r2_vectors.npz).
 """
+import argparse
 import ast
+import hashlib
 import os
 import sys
+import tempfile
 
 import numpy as np
 
@@ -24,7 +28,9 @@ REF = "/root/reference"
 sys.path.insert(0, ROOT)
 
 os.environ["SEEDPACK_CPU"] = "1"
-os.environ.setdefault("SEEDPACK_CACHE", os.path.join(ROOT, "_work", "refcache"))
+# the reference's --cpu backend caches its compiled kernels; a temporary directory keeps them out of
+# the repository
+os.environ.setdefault("SEEDPACK_CACHE", tempfile.mkdtemp(prefix="seedpack_refcache_"))
 sys.path.insert(0, REF)
 
 from tests.golden.r2_cases import CASES, case_file  # noqa: E402
@@ -166,6 +172,48 @@ def decode(ns, data, layout, res, aux):
     return out.tobytes()
 
 
+def load_header_coder():
+    """the reference's header coder (gpu2.py:299-431, gpu_bf16.py:421-424), read with `ast`:
+    rest_of, xz_chunks_c, _items, _xz, header_pairs_c and M24BF16GPU._header_c"""
+    import lzma
+    import struct
+    from concurrent.futures import ThreadPoolExecutor
+    ns = {"np": np, "lzma": lzma, "struct": struct, "ThreadPoolExecutor": ThreadPoolExecutor}
+    src, tree = _source(os.path.join(REF, "seedpack", "gpu2.py"))
+    for node in tree.body:
+        if isinstance(node, ast.Assign) and any(getattr(t, "id", None) == "HEADER_CHUNKS" for t in node.targets):
+            exec(ast.get_source_segment(src, node), ns)
+        if isinstance(node, ast.FunctionDef) and node.name in ("rest_of", "xz_chunks_c", "_items", "_xz",
+                                                              "header_pairs_c"):
+            exec(ast.get_source_segment(src, node), ns)
+    bsrc, btree = _source(os.path.join(REF, "seedpack", "gpu_bf16.py"))
+    for node in btree.body:
+        if isinstance(node, ast.ClassDef) and node.name == "M24BF16GPU":
+            for fn in node.body:
+                if isinstance(fn, ast.FunctionDef) and fn.name == "_header_c":
+                    code = ast.get_source_segment(bsrc, fn)
+                    code = "\n".join(line[4:] if line.startswith("    ") else line for line in code.splitlines())
+                    exec(code.replace("@staticmethod\n", ""), ns)
+    return ns
+
+
+def main_header():
+    """header_vectors.npz: per case of header_cases.py, the SHA-256 of the input file and the
+    reference's "rest" part for it (P or X form)"""
+    from seedpack_amd import gguf
+    from tests.golden.header_cases import NAMES, case_file
+    ns = load_header_coder()
+    out = {}
+    for name in NAMES:
+        data, layout = case_file(name)
+        g = gguf.GGUF(data)                 # spans / data_start: the reference reader's meaning
+        part = ns["_header_c"](data, g, layout)
+        out[f"{name}/input_sha256"] = np.frombuffer(hashlib.sha256(data).digest(), np.uint8)
+        out[f"{name}/rest"] = np.frombuffer(part, np.uint8)
+        print(f"{name}: {len(data)} B file, {part[:1].decode()} form, {len(part)} B", flush=True)
+    np.savez_compressed(os.path.join(HERE, "header_vectors.npz"), **out)
+
+
 def main():
     ns, cp = load()
     out = {}
@@ -182,4 +230,9 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--header", action="store_true", help="write header_vectors.npz only")
+    if ap.parse_args().header:
+        main_header()
+    else:
+        main()

@@ -1,0 +1,193 @@
+"""Host parts of the archive path (no GPU): GGUF reader/writer, the .seedpack container, the imatrix
+reader, zstd with parameters and dictionaries, and the base codec's header ("rest") coder against the
+reference's own output (tests/golden/header_vectors.npz, written by make_r2_golden.py --header)."""
+import hashlib
+import os
+import struct
+import zlib
+
+import numpy as np
+import pytest
+
+from seedpack_amd import container, gguf, header, imatrix, qr, repo, zstd
+from tests.golden.header_cases import NAMES, case_file
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def header_vectors():
+    return np.load(os.path.join(ROOT, "tests", "golden", "header_vectors.npz"))
+
+
+# ------------------------------------------------------------------ header coder vs the reference
+
+@pytest.mark.parametrize("name", NAMES)
+def test_header_part_equals_reference(header_vectors, name):
+    data, layout = case_file(name)
+    assert hashlib.sha256(data).digest() == header_vectors[f"{name}/input_sha256"].tobytes(), "case input drifted"
+    part = header.header_c(data, gguf.GGUF(data), layout)
+    want = header_vectors[f"{name}/rest"].tobytes()
+    assert part[:1] == want[:1], "form (P / X)"
+    assert part == want
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_header_part_decodes_back(header_vectors, name):
+    data, layout = case_file(name)
+    rest = header.rest_of(data, layout)
+    assert header.header_d(header_vectors[f"{name}/rest"].tobytes()) == rest     # the reference's bytes
+    out = np.zeros(len(data), np.uint8)
+    for off, nb, *_ in layout["t"]:
+        out[off:off + nb] = np.frombuffer(data, np.uint8, nb, off)
+    header.fill_rest(out, header.header_d(header.header_c(data, gguf.GGUF(data), layout)), layout)
+    assert out.tobytes() == data
+
+
+def test_pairs_form_needs_the_merge_structure():
+    """a planted mistake in the fixture's input (a merged token that is not its pair's concatenation)
+    must turn the P form down"""
+    data, layout = case_file("bpe")
+    g = gguf.GGUF(data)
+    assert header.pairs_c(data, g, layout) is not None
+    bad, _ = case_file("bpe_bad_token")
+    assert header.pairs_c(bad, gguf.GGUF(bad), layout) is None
+
+
+# ------------------------------------------------------------------ GGUF
+
+def test_gguf_round_trip_and_light_mode():
+    kv = {"general.architecture": "qwen35", "general.alignment": 64, "a.u32": 7, "a.i64": -5, "a.f32": 0.25,
+          "a.bool": True, "a.ints": [1, -2, 3], "a.floats": [0.5, 1.5], "tokenizer.ggml.tokens": [f"t{i}" for i in range(100)],
+          "a.typed": (gguf.T_ARRAY, (10, [1, 2 ** 40]))}
+    tensors = [("x", (128, 3), gguf.BF16), ("y", (256, 2), 12), ("z", (5,), gguf.F32), ("w", (64, 4), 42)]
+    head, where, size = gguf.header_bytes(kv, tensors, align=64)
+    data = head + bytes(size - len(head))
+    g = gguf.GGUF(data)
+    assert g.version == 3 and g.data_start == len(head) and g.data_start % 64 == 0
+    assert g.meta["a.i64"] == -5 and g.meta["a.ints"] == [1, -2, 3] and g.meta["a.typed"] == [1, 2 ** 40]
+    assert g.meta["tokenizer.ggml.tokens"][99] == "t99"
+    assert [(t.name, t.shape, t.type, t.offset, t.nbytes) for t in g.tensors] == \
+        [(n, s, ty, o, nb) for (n, s, ty), (o, nb) in zip(tensors, where)]
+    assert [t.nbytes for t in g.tensors] == [768, 288, 20, 72]
+    assert all(t.offset % 64 == 0 for t in g.tensors)
+    light = gguf.GGUF(data, light=True)
+    assert light.meta["tokenizer.ggml.tokens"] is None and light.tensors == g.tensors
+    a, b = g.spans["a.u32"]
+    assert struct.unpack_from("<I", data, a)[0] == 7 and b - a == 4
+    with pytest.raises(ValueError):
+        gguf.GGUF(b"GGUX" + data[4:])
+
+
+# ------------------------------------------------------------------ container
+
+def test_crc32_combine_matches_zlib():
+    g = np.random.default_rng(5)
+    for la, lb in [(0, 1), (3, 0), (1000, 77777), (5, 1 << 20), (1 << 16, 12345678)]:
+        a, b = g.bytes(la), g.bytes(lb)
+        assert container.crc32_combine(zlib.crc32(a), zlib.crc32(b), lb) == zlib.crc32(a + b)
+    big = g.bytes(70 << 20)
+    assert container.crc32_parallel(big) == zlib.crc32(big)
+
+
+def test_container_round_trip_streams_and_damage(tmp_path):
+    p = str(tmp_path / "a.seedpack")
+    g = np.random.default_rng(6)
+    blob = g.integers(0, 256, 3 << 20, dtype=np.uint8)
+    w = container.Writer(p)
+    w.put("first", b"hello")
+    s = w.put_stream("streamed")
+    s.head(bytes(16))
+    s.write(blob[:1000])
+    s.write(blob[1000:])
+    s.close(b"0123456789abcdef")
+    w.put("pieces", [b"ab", memoryview(b"cd"), np.arange(3, dtype=np.uint8)])
+    w.close({"tool": "test", "files": [1, 2]})
+    assert not os.path.exists(p + ".part")
+    r = container.Reader(p)
+    assert r.meta == {"tool": "test", "files": [1, 2]}
+    assert list(r.chunks) == ["first", "streamed", "pieces"]
+    assert bytes(r.get("first")) == b"hello"
+    got = r.get("streamed")
+    assert bytes(got[:16]) == b"0123456789abcdef" and np.array_equal(got[16:], blob)
+    assert bytes(r.get("pieces")) == b"abcd\0\1\2"
+    assert bytes(r.read_at("streamed", 16 + 5, 4)) == blob[5:9].tobytes()
+    with open(p, "rb") as f:
+        raw = f.read()
+    assert raw[:12] == b"SEEDPACK" + struct.pack("<I", 1) and raw[-8:] == b"SEEDEND\0"
+    off, n, _ = struct.unpack("<QQ8s", raw[-24:])
+    assert zstd.decompress(raw[off:off + n]).startswith(b'{"chunks": {"first": [12, 5, ')
+    r.close()
+    bad = bytearray(raw)
+    bad[12 + 5 + 20] ^= 1                   # a byte inside "streamed"
+    open(p, "wb").write(bytes(bad))
+    with pytest.raises(container.FormatError):
+        container.Reader(p).get("streamed")
+    open(p, "wb").write(raw[:-30])
+    with pytest.raises(container.FormatError):
+        container.Reader(p)
+
+
+def test_container_abort_leaves_nothing(tmp_path):
+    p = str(tmp_path / "b.seedpack")
+    w = container.Writer(p)
+    w.put("x", b"1")
+    s = w.put_stream("y")
+    s.head(b"h")
+    w.abort()
+    assert not os.path.exists(p) and not os.path.exists(p + ".part")
+
+
+# ------------------------------------------------------------------ imatrix, zstd
+
+def test_imatrix_legacy_and_gguf():
+    g = np.random.default_rng(7)
+    e = {"blk.0.attn_q.weight": g.lognormal(0, 1, 64).astype(np.float32), "output.weight": np.ones(32, np.float32)}
+    buf = imatrix.write_dat(e, ncall=3, chunk_count=125, dataset="calib.txt")
+    got = imatrix.load(buf)
+    for k in e:
+        np.testing.assert_array_equal(got[k], (e[k] * np.float32(3)) / np.float32(3))
+    assert imatrix.chunks(buf) == 125 and imatrix.chunks(imatrix.write_dat(e)) is None
+    sums = g.random((2, 16)).astype(np.float32)
+    counts = np.array([4, 0], np.float32)
+    kv = {"general.type": "imatrix", "imatrix.chunk_count": 9}
+    head, where, size = gguf.header_bytes(kv, [("t.in_sum2", (16, 2), gguf.F32), ("t.counts", (2,), gguf.F32)])
+    data = bytearray(size)
+    data[:len(head)] = head
+    data[where[0][0]:where[0][0] + 128] = sums.tobytes()
+    data[where[1][0]:where[1][0] + 8] = counts.tobytes()
+    v = imatrix.load(bytes(data))["t"]
+    np.testing.assert_array_equal(v[:16], sums[0] / np.float32(4))
+    np.testing.assert_array_equal(v[16:], np.ones(16, np.float32))
+    assert imatrix.chunks(bytes(data)) == 9
+
+
+def test_zstd_params_dictionary_and_pieces():
+    g = np.random.default_rng(8)
+    d = (g.integers(0, 8, 4 << 20) == 0).astype(np.uint8) * g.integers(0, 256, 4 << 20).astype(np.uint8)
+    dic = g.bytes(50000)
+    d[:50000] = np.frombuffer(dic, np.uint8)        # the frame's matches refer to the dictionary
+    for p in (zstd.Params(7, 25), zstd.Params(9, 25, threads=4), zstd.Params(7, threads=2, ldm=True)):
+        c = zstd.Compressor(p, dic, size=d.size)
+        frame = c.compress(d[:1234567]) + c.compress(d[1234567:]) + c.finish()
+        assert frame == zstd.compress_with(d, p, dic)          # the split into pieces does not matter
+        assert np.array_equal(zstd.decompress_into(frame, np.empty(d.size, np.uint8), dic), d)
+        with pytest.raises((ValueError, RuntimeError)):
+            zstd.decompress_into(frame, np.empty(d.size, np.uint8))      # the dictionary is needed
+    with pytest.raises(ValueError):
+        zstd.decompress_into(frame[:len(frame) // 2], np.empty(d.size, np.uint8), dic)
+    assert zstd.decompress(zstd.compress(b"abc" * 1000, 19)) == b"abc" * 1000
+
+
+# ------------------------------------------------------------------ archive rules
+
+def test_window_and_batch_rules():
+    """the reference's window rule, its prediction-bytes bound, and the QR batch split"""
+    gb = 1 << 30
+    assert repo.windows([gb + 5, 100, 200, gb]) == [(0, 1), (1, 3), (3, 4)]
+    assert repo.windows([10] * 5, window=25) == [(0, 2), (2, 4), (4, 5)]
+    assert repo.windows([1] * 4, pred=[2, 2, 2, 2], pred_window=4) == [(0, 2), (2, 4)]
+    assert repo.windows([]) == []
+    assert repo.order_groups([("a", "b", "c"), ("a", "c"), ("d",), ("a", "b", "c")]) == \
+        {("a", "b", "c"): [0, 1, 3], ("d",): [2]}
+    assert qr.batches(12, [300 << 20, 100 << 20, 10]) == [[0], [1, 2]]

@@ -1,11 +1,12 @@
 """Host side of the R2 codec that runs without a GPU: the chunk framing, the file's other bytes
-(rest_of / fill_rest) and both header forms."""
+(rest_of / fill_rest) and both header forms (the P form also against the reference's own output in
+tests/test_archive_host.py)."""
 import lzma
 import struct
 
 import numpy as np
 
-from seedpack_amd import framing, r2
+from seedpack_amd import framing, header
 
 
 def _gguf_strings(items):
@@ -27,10 +28,10 @@ def test_rest_of_and_fill_rest():
     g = np.random.default_rng(3)
     data = g.integers(0, 256, 1000, dtype=np.uint8).tobytes()
     layout = {"size": 1000, "t": [[96, 200, 10, "bf16"], [320, 100, 10, "bf16"], [900, 100, 10, "bf16"]]}
-    rest = r2.rest_of(data, layout)
+    rest = header.rest_of(data, layout)
     assert rest == data[:96] + data[296:320] + data[420:900]
     out = np.zeros(1000, np.uint8)
-    r2.fill_rest(out, rest, layout)
+    header.fill_rest(out, rest, layout)
     want = np.frombuffer(data, np.uint8).copy()
     for off, nb, _, _ in layout["t"]:
         want[off:off + nb] = 0
@@ -41,8 +42,8 @@ def test_header_x_round_trip():
     g = np.random.default_rng(4)
     for n in (0, 3, 4097):
         b = g.integers(0, 4, n, dtype=np.uint8).tobytes()
-        h = r2.header_x(b)
-        assert h[:1] == b"X" and r2.header_d(h) == b
+        h = header.header_x(b)
+        assert h[:1] == b"X" and header.header_d(h) == b
         lens = struct.unpack_from("<4I", h, 1)
         assert lzma.decompress(h[17:17 + lens[0]]) == b[:n // 4]
 
@@ -79,4 +80,4 @@ def test_header_pairs_form_rebuilds_the_token_arrays():
     planes = np.concatenate([(pr >> (8 * i)).astype(np.uint8).T.ravel() for i in range(3)])
     comp = [lzma.compress(x) for x in (stripped, lens.tobytes(), b"".join(raw), planes.tobytes())]
     buf = b"P" + struct.pack("<6Q", t0, t1, m0, m1, len(toks), len(pairs)) + struct.pack("<4I", *map(len, comp)) + b"".join(comp)
-    assert r2.header_d(buf) == rest
+    assert header.header_d(buf) == rest

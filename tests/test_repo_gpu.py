@@ -1,0 +1,149 @@
+"""Whole-repository archives on the GPU (configurations 4 and 5 at reduced sizes): a synthetic
+Qwen-shaped repository (BF16 base with a BPE tokenizer, imatrix, 21 quantized GGUFs made from the
+base with 1% of their blocks changed, a small extra file) packed into a .seedpack archive and
+extracted again.
+
+Checked: every file extracts byte-identical and passes its SHA-256 (so every QR batch of every file
+decodes back); the container, manifest and chunks follow the reference's layout; the base's header
+part takes the tokenizer-aware form; for every QR type, one batch of the archive equals the oracle's
+stream for the same tensors (oracle/qr.py's per-tensor histograms summed into the batch's tables,
+each tensor's segments coded with them); windows, references and QR batch cuts follow the
+reference's rules (repo3.py:1689-1706, :2006-2030, :946-979)."""
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import qr as oqr
+from seedpack_amd import container, device as dev, gguf, qr, repo, synth, zstd
+from seedpack_amd.framing import unpack
+from seedpack_amd.requant import NAMES
+
+pytestmark = pytest.mark.gpu
+TYPES = [2, 3, 6, 7, 8, 42, 10, 11, 12, 13, 14, 16, 17, 18, 19, 20, 21, 22, 23, 29]
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _files():
+    f = {f"model-{NAMES[t]}.gguf": (lambda name, t=t: t) for t in TYPES}
+    f["model-Q4_K_M.gguf"] = synth.q4_k_m
+    return f
+
+
+@pytest.fixture(scope="module")
+def small_repo(tmp_path_factory):
+    root = str(tmp_path_factory.mktemp("repo"))
+    say("case repo small: writing the synthetic repository")
+    tensors = synth.qwen_tensors(layers=2, hidden=256, ffn=512, kv=256, vocab=512)
+    sizes = synth.write_repo(root, tensors, _files(), per_million=20000, nmerge=3000)
+    arc = os.path.join(str(tmp_path_factory.mktemp("arc")), "small.seedpack")
+    say("case repo small: pack")
+    stats = repo.pack_repo([root], arc)
+    return root, arc, sizes, stats
+
+
+def test_small_repo_extracts_byte_identical(small_repo, tmp_path):
+    root, arc, sizes, stats = small_repo
+    say("case repo small: unpack", stats)
+    out = str(tmp_path / "out")
+    res = repo.unpack_repo(arc, out)
+    assert not res["bad"] and not res["missing"], res
+    names = sorted(os.listdir(root))
+    assert sorted(res["files"]) == names
+    for n in names:
+        a, b = open(os.path.join(root, n), "rb").read(), open(os.path.join(out, n), "rb").read()
+        assert a == b, n
+    # selective extraction: one quant file alone
+    res = repo.unpack_repo(arc, None, ["model-IQ2_XS.gguf"])
+    assert res["files"] == {"model-IQ2_XS.gguf": True}
+    assert stats["stats"]["qr"] > 0 and stats["stats"]["requant_diff"] > 0
+
+
+def test_small_repo_archive_layout(small_repo):
+    root, arc, sizes, stats = small_repo
+    r = container.Reader(arc)
+    man = json.loads(zstd.decompress(r.get("manifest")))
+    assert man["method"] == repo.METHOD and man["bases"] == ["model-BF16.gguf"] and man["seeds"] == []
+    assert man["extras"]["bundle"] == ["README.md", "imatrix.dat"] and man["extras"]["single"] == {}
+    assert man.get("needs") == "0.3.0"                        # QR-coded grid types
+    chunks = list(r.chunks)
+    assert chunks[:2] == ["extras", "b0"] and chunks[-1] == "manifest"
+    files = [m["name"] for m in man["files"]]
+    fchunks = [c for c in chunks if c[0] in "fq"]
+    assert fchunks == [c for i in range(len(files)) for c in (f"f{i}", f"q{i}")]
+    # the base chunk: pack({"r2": meta, side, tables, stream, lens, rest}), its rest in the P form
+    b0 = unpack(memoryview(r.get("b0")))
+    inner = unpack(b0["r2"])
+    assert list(inner) == ["meta", "side", "tables", "stream", "lens", "rest"]
+    assert bytes(inner["rest"][:1]) == b"P"
+    # plan entries: [name, kind, variant, type]; 2-D tensors QR-coded, norms predicted by conversion
+    for m in man["files"]:
+        kinds = {e[1] for e in m["plan"]}
+        assert kinds <= {"qr", "rq", "xor"} and "qr" in kinds and "xor" in kinds, (m["name"], kinds)
+        assert all(len(e) == 4 for e in m["plan"])
+    cat = {f["name"]: f for f in r.meta["files"]}
+    assert cat["model-BF16.gguf"]["role"] == "base" and cat["imatrix.dat"]["role"] == "file"
+    assert cat["model-Q8_0.gguf"]["role"] == "derived" and r.meta["hash"] == "sha256"
+    assert r.meta["total"] == sum(os.path.getsize(os.path.join(root, n)) for n in os.listdir(root))
+
+
+def _oracle_batch(T, tens, mv, gk):
+    """the oracle's coded batch of several tensors [(F, P, seed, seed_type, cols, imx)]: per-tensor
+    symbol histograms summed, one normalisation, each tensor's segments coded with those tables"""
+    counts, blocks = None, []
+    for F, P, seed, st, cols, imx in tens:
+        c, b = oqr.histogram(T, F, P, seed, st, cols, mv, imx, gk)
+        counts = c if counts is None else counts + c
+        blocks.append(b)
+    freq, used = oqr.normalize(counts)
+    remap = np.full(oqr.NTAB2, -1, np.int32)
+    remap[used] = np.arange(len(used), dtype=np.int32)
+    cum = oqr.cum_of(freq)
+    parts = [oqr.rans_encode(oqr.segment_sequence(T, b, b0, n), remap, freq, cum) for b in blocks
+             for b0, n in oqr.segments(T, len(b))]
+    return freq, used, np.array([len(p) for p in parts], np.uint32), b"".join(parts)
+
+
+def test_small_repo_one_batch_per_type_equals_oracle(small_repo):
+    root, arc, sizes, stats = small_repo
+    r = container.Reader(arc)
+    man = json.loads(zstd.decompress(r.get("manifest")))
+    base = open(os.path.join(root, "model-BF16.gguf"), "rb").read()
+    bt = {t.name: t for t in gguf.GGUF(base).tensors}
+    from seedpack_amd import imatrix
+    imx = imatrix.load(open(os.path.join(root, "imatrix.dat"), "rb").read())
+    seen = set()
+    for i, m in enumerate(man["files"]):
+        data = open(os.path.join(root, m["name"]), "rb").read()
+        ft = {t.name: t for t in gguf.GGUF(data).tensors}
+        q = unpack(memoryview(r.get(f"q{i}")))
+        var = {e[0]: e[2] for e in m["plan"]}
+        for k, (T, names) in enumerate(json.loads(zstd.decompress(q["meta"]))):
+            if T in seen:
+                continue
+            seen.add(T)
+            say(f"case repo oracle batch: {m['name']} type {T}, {len(names)} tensors")
+            assert all(var[n] == 0 for n in names)
+            from seedpack_amd.gpuquant import GPUQuant
+            gq = GPUQuant()
+            tens = []
+            for n in names:
+                b = bt[n]
+                w = np.frombuffer(base, np.uint16, b.numel, b.offset)
+                P = gq.quantize_tensors(T, [(w, b.shape[0])], [imx[n]])[0]
+                F = np.frombuffer(data, np.uint8, ft[n].nbytes, ft[n].offset)
+                seed = np.frombuffer(base, np.uint8, b.nbytes, b.offset)
+                tens.append((F.tobytes(), P.tobytes(), seed.tobytes(), 30, b.shape[0],
+                             imx[n] if T in qr.GRID_TYPES else None))
+            freq, used, lens, stream = _oracle_batch(T, tens, qr.MODEL, qr.grid_keys(T) if T in qr.GRID_TYPES else None)
+            ch = unpack(q[str(k)])
+            f2, u2 = qr.load_tables(ch["t"])
+            assert np.array_equal(u2, used) and np.array_equal(f2, freq), "tables"
+            assert np.array_equal(np.frombuffer(zstd.decompress(ch["l"]), np.uint32), lens), "segment lengths"
+            assert bytes(ch["s"]) == stream, "stream"
+    assert seen == set(TYPES)
