@@ -237,13 +237,8 @@ def r2_layer(stream):
 def cfg4_matrices(layers=36):
     """configuration 4's 2-D BF16 matrices (name, rows, row length): 36 Qwen3.5-9B-shaped blocks and
     the 151936-row embedding and output, 8,190,427,136 weights"""
-    t = []
-    for b in range(layers):
-        for name, rows, rl in (("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 4096),
-                               ("attn_output", 4096, 4096), ("ffn_gate", 12288, 4096), ("ffn_up", 12288, 4096),
-                               ("ffn_down", 4096, 12288)):
-            t.append((f"blk.{b}.{name}.weight", rows, rl))
-    return [("token_embd.weight", 151936, 4096)] + t + [("output.weight", 151936, 4096)]
+    from seedpack_amd import synth
+    return [(n, s[1], s[0]) for n, s, t in synth.qwen_tensors(layers, norms=False)]
 
 
 def cfg4_base(stream, layers=36):
@@ -269,247 +264,97 @@ def cfg4_base(stream, layers=36):
 PACK_TYPES = [2, 3, 6, 7, 8, 42, 10, 11, 12, 13, 14, 16, 17, 18, 19, 20, 21, 22, 23, 29]
 
 
-def _q4km(name):
-    return 14 if any(k in name for k in ("attn_v", "ffn_down", "output.")) else 12
+class HbmPeak:
+    """peak device memory in use (hipMemGetInfo polled every 20 ms on a thread) between start() and stop()"""
+
+    def __init__(self):
+        from seedpack_amd import device as dev
+        self.dev, self.peak, self.run = dev, 0, False
+
+    def _poll(self):
+        while self.run:
+            free, total = self.dev.mem_info()
+            self.peak = max(self.peak, total - free)
+            time.sleep(0.02)
+
+    def start(self):
+        free, total = self.dev.mem_info()
+        self.base, self.peak, self.run = total - free, total - free, True
+        self.t = threading.Thread(target=self._poll, daemon=True)
+        self.t.start()
+        return self
+
+    def stop(self):
+        self.run = False
+        self.t.join()
+        return self.peak
 
 
-def pack_cfg4(stream, layers=36, per_million=10000, files=None):
-    """configuration 4's pack on the device. The BF16 base and one LogNormal(0, 1) imatrix per tensor
-    are resident in HBM, and so are the quant files (every 2-D matrix in one type), made untimed by
-    this library's quantizer with per_million / 10^6 of their blocks perturbed (one byte each). Then,
-    timed as one run: per file, every tensor is regrown and compared (residual.residual_window over
-    windows of about 384 MB: predictions, differing-byte counts read back once per window, the
-    candidate variants) on the main stream, while four coder threads code the QR tensors in batches of
-    about 384 MB, each on its own stream (qr.encode_parts; the zstd-19 framing on 8 more threads), as
-    the reference's pool codes batches beside the prediction (repo3.py:946-979), and one more thread
-    compresses the base with the base codec. pack GB/s = (BF16
-    bytes + quant file bytes) / that run's wall time. Each file's first batch is decoded again and
-    compared afterwards, untimed."""
+def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False):
+    """configurations 4 and 5 from host files, as the reference's CLI measures them (cli.py:288-292,
+    :441): a synthetic Qwen3.5-9B-shaped repository (BF16 GGUF with a 151,936-token BPE tokenizer,
+    imatrix.dat, README.md, 21 quantized GGUFs made by this library's quantizers with 1% of their
+    blocks changed) written to host files (untimed); then, timed, seedpack_amd.repo's pack of the
+    directory into a .seedpack archive (file reads, SHA-256 of every file, regrowth / comparison /
+    QR coding on the device, the R2 base codec, zstd of the residuals, the container), and the
+    extract of the Q4_K_M-like and IQ2_XS files from that archive (residual zstd, regrowth, QR decode,
+    SHA-256 check, files written). Peak HBM by hipMemGetInfo polling. The extracted files are
+    compared byte for byte with the originals."""
+    import shutil
     from seedpack_amd import device as dev
-    from seedpack_amd import qr, r2, residual
-    from seedpack_amd._lib import check, lib
-    from seedpack_amd.gpuquant import GPUQuant
-    from seedpack_amd.requant import NAMES, QFUN
-    d, ts, pos = cfg4_base(stream, layers)
-    nb_all = sum(t[2] for t in ts)
-    g = np.random.Generator(np.random.PCG64(0x1A7))
-    imx_h = [g.lognormal(0.0, 1.0, rl).astype(np.float32) for (_, _, _, rl) in ts]
-    imx_off = np.cumsum([0] + [a.size for a in imx_h])[:-1]
-    imx_all = dev.DeviceArray.from_host(np.concatenate(imx_h), stream.handle)
-    imx_k = [imx_all.view(int(o) * 4, (a.size,), np.float32) for o, a in zip(imx_off, imx_h)]
-    base_k = [d.view(off, (nb // 2,), np.uint16) for (_, off, nb, _) in ts]
-    gq = GPUQuant(stream=stream.handle)
-    plan = [(NAMES[t], (lambda name, t=t: t)) for t in PACK_TYPES] + [("Q4_K_M", _q4km)]
+    from seedpack_amd import repo, synth
+    from seedpack_amd.requant import NAMES
+    qf = {f"model-{NAMES[t]}.gguf": (lambda name, t=t: t) for t in PACK_TYPES}
+    qf["model-Q4_K_M.gguf"] = synth.q4_k_m
     if files is not None:
-        plan = [p for p in plan if p[0] in files]
-    _, tot = dev.mem_info()
-    made = []
-    for fi, (fname, type_of) in enumerate(plan):
-        types = [type_of(name) for (name, _, _, _) in ts]
-        regions = []
-        for k, (name, off, nb, rl) in enumerate(ts):
-            T = types[k]
-            y = gq.quantize_tensors(T, [(base_k[k], rl)], [imx_k[k]], device=True)[0]
-            bs = QFUN[T][2]
-            check(lib().spa_perturb_blocks(y.ptr, y.nbytes // bs, bs, per_million, 0xF11E0000 + 1000 * fi + k,
-                                           stream.handle))
-            regions.append(y)
-        made.append((fname, types, regions))
-    stream.synchronize()
-    log(f"bench: pack cfg4: {len(made)} files made")
-    pool = concurrent.futures.ThreadPoolExecutor(8)      # zstd-19 framing of the coded batches
-    coder = concurrent.futures.ThreadPoolExecutor(4)     # QR batches, each worker on its own stream
-    side = concurrent.futures.ThreadPoolExecutor(1)      # the base codec, on its own streams
-    tls = threading.local()
-
-    def qr_batch(T, items):
-        if not hasattr(tls, "stream"):
-            tls.stream = dev.Stream()
-        tq = time.perf_counter()
-        parts = qr.encode_parts(T, items, d, imx_all, stream=tls.stream.handle)
-        return pool.submit(qr.frame, parts), time.perf_counter() - tq
-
-    def base_codec():
-        s2 = dev.Stream()
-        tb = time.perf_counter()
-        r2.BF16v2(stream=s2.handle).compress(d, r2.layout_of(ts, pos))
-        s2.synchronize()
-        return time.perf_counter() - tb
-
-    out, framed, file_bytes, inflight = {}, [], 0, collections.deque()
-    t_all = time.perf_counter()
-    r2_future = side.submit(base_codec)
-    for fname, types, regions in made:
+        qf = {k: v for k, v in qf.items() if k in files}
+    src, arc_dir, out = os.path.join(root, "repo"), os.path.join(root, "arc"), os.path.join(root, "out")
+    for d in (src, arc_dir, out):
+        shutil.rmtree(d, ignore_errors=True)
+        os.makedirs(d)
+    try:
         t0 = time.perf_counter()
-        pending, wbytes, nqr = {}, {}, 0
-        phase = {"residual_s": 0.0}
-        mine = []
-
-        def flush(T):
-            # at most 16 batches queued for the coders (their predictions stay alive until coded)
-            while len(inflight) >= 16:
-                inflight.popleft().result()
-            f = coder.submit(qr_batch, T, pending[T])
-            inflight.append(f)
-            # only each file's first batch keeps its tensors (for the check after the run)
-            mine.append((T, f, list(pending[T]) if not mine else None))
-            pending[T], wbytes[T] = [], 0
-
-        window, wb = [], 0
-        for k, (name, off, nb, rl) in enumerate(ts):
-            window.append(k)
-            wb += regions[k].nbytes
-            if wb < qr.BATCH and k + 1 < len(ts):
-                continue
-            # a window of about one coding batch: first predictions and counts queued back to back
-            tr = time.perf_counter()
-            res = residual.residual_window([residual.Tensor(ts[i][0], types[i], ts[i][3], regions[i], base_k[i],
-                                                            imatrix=imx_k[i]) for i in window], gq, stream=stream.handle)
-            phase["residual_s"] += time.perf_counter() - tr
-            for i, r in zip(window, res):
-                if r["qr"]:
-                    T = types[i]
-                    nqr += 1
-                    pending.setdefault(T, []).append((regions[i], r["prediction"], ts[i][1], 30, ts[i][3], int(imx_off[i])))
-                    wbytes[T] = wbytes.get(T, 0) + regions[i].nbytes
-                    if wbytes[T] >= qr.BATCH:
-                        flush(T)
-            window, wb = [], 0
-        for T in list(pending):
-            if pending[T]:
-                flush(T)
-        dt = time.perf_counter() - t0
-        fb = sum(y.nbytes for y in regions)
-        file_bytes += fb
-        framed.append((fname, mine))
-        out[fname] = {"file_bytes": fb, "qr_tensors": nqr, "qr_batches": len(mine), "regrow_s": round(dt, 3),
-                      "residual_s": round(phase["residual_s"], 3)}
-        log(f"bench: pack cfg4 {fname}: {out[fname]}")
-    bufs = {}
-    for fname, mine in framed:
-        coded = [(T, f.result(), items) for (T, f, items) in mine]
-        out[fname]["qr_parts_s"] = round(sum(dt for (_, (_, dt), _) in coded), 3)
-        bufs[fname] = [(T, ff.result(), items) for (T, (ff, _), items) in coded]
-    r2_s = r2_future.result()
-    total_s = time.perf_counter() - t_all
-    free1, _ = dev.mem_info()
-    for ex in (pool, coder, side):
-        ex.shutdown()
-    for fname, bl in bufs.items():
-        out[fname]["coded_bytes"] = sum(len(b) for (_, b, _) in bl)
-        ok = None
-        if bl:
-            T, buf, items = bl[0]
-            back = qr.decode(T, buf, [(p, so, st, c, io) for (_, p, so, st, c, io) in items], d, imx_all,
-                             stream=stream.handle)
-            pos_b, ok = 0, True
-            for (f, _, _, _, _, _) in items:
-                ok &= residual.diff_count(back.view(pos_b, (f.nbytes,), np.uint8), f, stream.handle) == 0
-                pos_b += f.nbytes
-            del back
-        out[fname]["first_batch_round_trip_ok"] = ok
-    res = {"workload": f"cfg4: {len(ts)} matrices ({layers} blocks + token_embd + output), {len(plan)} quant files, "
-                       f"{per_million / 1e4:g}% of each file's blocks perturbed",
-           "bf16_bytes": nb_all, "quant_file_bytes": file_bytes, "base_compress_s": round(r2_s, 3),
-           "pack_s": round(total_s, 3), "pack_GB_s": round((nb_all + file_bytes) / total_s / 1e9, 2),
-           "hbm_used_GB": round((tot - free1) / 1e9, 1), "files": out,
-           "note": "device path with the reference's framing: file reading, hashing, zstd of XOR residuals and the "
-                   "container stay with the host pipeline; HBM in use after the run (base, every file, outputs)"}
-    log(f"bench: pack cfg4 total {res['pack_s']} s, {res['pack_GB_s']} GB/s")
-    del d, made, bufs
-    return res
+        s = dev.Stream()
+        sizes = synth.write_repo(src, synth.qwen_tensors(layers), qf, per_million=10000, nmerge=151936 - 256 - 8,
+                                 stream=s, log=log)
+        dev.synchronize()
+        log(f"bench: repo written: {len(sizes)} files, {sum(sizes.values()) / 1e9:.1f} GB in {time.perf_counter() - t0:.1f} s")
+        arc = os.path.join(arc_dir, "model.seedpack")
+        peak = HbmPeak().start()
+        st = repo.Packer(verbose=True, staging_bytes=32 << 30).pack([src], arc)
+        pk_peak = peak.stop()
+        log(f"bench: pack {st['input_bytes'] / 1e9:.1f} GB -> {st['archive_bytes'] / 1e9:.2f} GB in {st['seconds']:.1f} s "
+            f"= {st['GB_s']:.2f} GB/s, peak HBM {pk_peak / 1e9:.1f} GB")
+        want = [n for n in ("model-Q4_K_M.gguf", "model-IQ2_XS.gguf") if n in qf]
+        peak = HbmPeak().start()
+        ex = repo.Unpacker(verbose=True).run(arc, out, want)
+        up_peak = peak.stop()
+        same = all(_same_file(os.path.join(src, n), os.path.join(out, n)) for n in want)
+        log(f"bench: extract {ex['bytes'] / 1e9:.2f} GB in {ex['seconds']:.2f} s = {ex['GB_s']:.2f} GB/s, "
+            f"byte-identical {same}")
+        pack = {"workload": f"cfg4: {len(sizes)} files from host files ({layers} blocks, 21 quant files, 1% of each "
+                            "file's blocks changed) -> .seedpack", "input_bytes": st["input_bytes"],
+                "archive_bytes": st["archive_bytes"], "ratio": round(st["archive_bytes"] / st["input_bytes"], 4),
+                "pack_s": round(st["seconds"], 2), "pack_GB_s": round(st["GB_s"], 3), "peak_hbm_GB": round(pk_peak / 1e9, 1),
+                "stats": st["stats"], "phases_s": st.get("phases")}
+        unpack = {"workload": "cfg5: Q4_K_M-like and IQ2_XS extracted from the cfg4 archive (files written, SHA-256 checked)",
+                  "written_bytes": ex["bytes"], "extract_s": round(ex["seconds"], 2), "GB_s_written": round(ex["GB_s"], 3),
+                  "checksums_ok": not ex["bad"] and not ex["missing"], "byte_identical": same,
+                  "peak_hbm_GB": round(up_peak / 1e9, 1)}
+        return pack, unpack
+    finally:
+        if not keep:
+            shutil.rmtree(root, ignore_errors=True)
 
 
-def unpack_cfg5(stream, layers=36, per_million=10000):
-    """configuration 5: extract from the configuration-4 archive. Untimed: the base (as in
-    pack_cfg4), a Q4_K_M-like file (Q4_K / Q6_K per tensor) and an IQ2_XS file with per_million /
-    10^6 of their blocks perturbed, packed as pack_cfg4 packs them (base codec; residuals QR-coded
-    and framed in batches of about 384 MB), the coded bytes kept in host memory. Timed: the base
-    decoded into HBM, then per file, per coded batch: its tensors regrown from the decoded base,
-    the batch QR-decoded against them (the file's blocks rebuilt in HBM) and copied to page-locked
-    host memory. Byte identity with the originals is checked on the device afterwards, untimed.
-    GB/s written = rebuilt file bytes / time (the base decode included)."""
-    from seedpack_amd import device as dev
-    from seedpack_amd import qr, r2, residual
-    from seedpack_amd._lib import check, lib
-    from seedpack_amd.gpuquant import GPUQuant
-    from seedpack_amd.requant import QFUN
-    d, ts, pos = cfg4_base(stream, layers)
-    g = np.random.Generator(np.random.PCG64(0x1A7))
-    imx_h = [g.lognormal(0.0, 1.0, rl).astype(np.float32) for (_, _, _, rl) in ts]
-    imx_off = np.cumsum([0] + [a.size for a in imx_h])[:-1]
-    imx_all = dev.DeviceArray.from_host(np.concatenate(imx_h), stream.handle)
-    imx_k = [imx_all.view(int(o) * 4, (a.size,), np.float32) for o, a in zip(imx_off, imx_h)]
-    gq = GPUQuant(stream=stream.handle)
-    codec = r2.BF16v2(stream=stream.handle)
-    base_parts = codec.compress(d, r2.layout_of(ts, pos))
-    base_parts.pop("arrays", None)
-    plan = [("Q4_K_M", _q4km), ("IQ2_XS", lambda name: 17)]
-    archive = []
-    for fi, (fname, type_of) in enumerate(plan):
-        types = [type_of(name) for (name, _, _, _) in ts]
-        regions, batches, pending, wbytes = [], [], {}, {}
-        for k, (name, off, nb, rl) in enumerate(ts):
-            T = types[k]
-            y = gq.quantize_tensors(T, [(d.view(off, (nb // 2,), np.uint16), rl)], [imx_k[k]], device=True)[0]
-            bs = QFUN[T][2]
-            check(lib().spa_perturb_blocks(y.ptr, y.nbytes // bs, bs, per_million, 0xF11E5000 + 1000 * fi + k,
-                                           stream.handle))
-            regions.append(y)
-            r = residual.residual_tensor(residual.Tensor(name, T, rl, y, d.view(off, (nb // 2,), np.uint16),
-                                                         imatrix=imx_k[k]), gq, stream=stream.handle)
-            assert r["qr"] and r["variant"] == 0
-            pending.setdefault(T, []).append((k, y, r["prediction"]))
-            wbytes[T] = wbytes.get(T, 0) + y.nbytes
-            if wbytes[T] >= qr.BATCH or k + 1 == len(ts):
-                for TT in ([T] if k + 1 < len(ts) else list(pending)):
-                    if not pending.get(TT):
-                        continue
-                    it = pending[TT]
-                    buf = qr.encode(TT, [(y_, p_, ts[i][1], 30, ts[i][3], int(imx_off[i])) for (i, y_, p_) in it], d,
-                                    imx_all, stream=stream.handle)
-                    batches.append((TT, [i for (i, _, _) in it], buf))
-                    pending[TT], wbytes[TT] = [], 0
-        archive.append((fname, types, regions, batches))
-    stream.synchronize()
-    del d
-    outbufs = [dev.pinned(sum(r_.nbytes for r_ in a[2])) for a in archive]   # the files' host staging
-    log("bench: unpack cfg5: archive made")
-    t0 = time.perf_counter()
-    base = codec.decompress(base_parts, device=True)
-    t_base = time.perf_counter() - t0
-    out, rebuilt, written = {}, [], 0
-    for (fname, types, regions, batches), host in zip(archive, outbufs):
-        t1 = time.perf_counter()
-        nbytes = sum(r_.nbytes for r_ in regions)
-        at = 0
-        for (T, idx, buf) in batches:
-            preds = [gq.quantize_tensors(T, [(base.view(ts[i][1], (ts[i][2] // 2,), np.uint16), ts[i][3])], [imx_k[i]],
-                                         device=True)[0] for i in idx]
-            F = qr.decode(T, buf, [(p_, ts[i][1], 30, ts[i][3], int(imx_off[i])) for p_, i in zip(preds, idx)], base,
-                          imx_all, stream=stream.handle)
-            nb = sum(regions[i].nbytes for i in idx)
-            check(lib().spa_memcpy_d2h(host[at:].ctypes.data, F.ptr, nb, stream.handle))
-            rebuilt.append((F, idx))
-            at += nb
-        dt = time.perf_counter() - t1
-        written += nbytes
-        out[fname] = {"file_bytes": nbytes, "batches": len(batches), "extract_s": round(dt, 3),
-                      "GB_s": round(nbytes / dt / 1e9, 2)}
-        log(f"bench: unpack cfg5 {fname}: {out[fname]}")
-    total = time.perf_counter() - t0
-    bad = 0
-    for (_, _, regions, _), (F, idx) in zip([a for a in archive for _ in a[3]], rebuilt):
-        o = 0
-        for i in idx:
-            bad += residual.diff_count(F.view(o, (regions[i].nbytes,), np.uint8), regions[i], stream.handle)
-            o += regions[i].nbytes
-    res = {"workload": f"cfg5: extract Q4_K_M-like and IQ2_XS files of configuration 4 ({len(ts)} matrices), "
-                       f"{per_million / 1e4:g}% of blocks perturbed", "base_decode_s": round(t_base, 3),
-           "files": out, "written_bytes": written, "extract_s": round(total, 3),
-           "GB_s_written": round(written / total / 1e9, 2), "bytes_differing": int(bad)}
-    log(f"bench: unpack cfg5 total {res['extract_s']} s, {res['GB_s_written']} GB/s, {bad} bytes differing")
-    return res
+def _same_file(a, b, chunk=1 << 28):
+    with open(a, "rb") as fa, open(b, "rb") as fb:
+        while True:
+            x, y = fa.read(chunk), fb.read(chunk)
+            if x != y:
+                return False
+            if not x:
+                return True
 
 
 def r2_cfg4(stream, layers=36):
@@ -640,10 +485,11 @@ def main():
                          "i-quants on its 4096x12288 tensor) plus a 512 MiB copy, "
                          "for rocprofv3 counter runs; prints the launch list, no JSON line")
     ap.add_argument("--pack", action="store_true",
-                    help="only configuration 4's pack (all quant files, base codec); prints its result, no JSON line")
+                    help="only configurations 4 and 5 (repository pack from host files, extract of two files); prints "
+                         "their result, no JSON line")
     ap.add_argument("--pack-layers", type=int, default=36, help="transformer blocks of the --pack model")
-    ap.add_argument("--unpack", action="store_true",
-                    help="only configuration 5's extract (Q4_K_M-like and IQ2_XS from the configuration-4 archive)")
+    ap.add_argument("--unpack", action="store_true", help="the same as --pack")
+    ap.add_argument("--no-repo", action="store_true", help="leave configurations 4 and 5 out of the JSON line")
     ap.add_argument("--pack-files", default=None, help="comma-separated quant files of --pack (default: all 21)")
     ap.add_argument("--codecs", action="store_true",
                     help="only the coding stages (QR on configurations 1 and 3, the R2 base codec), for rocprofv3 "
@@ -651,14 +497,10 @@ def main():
     a = ap.parse_args()
     if a.profile_pass:
         return profile_pass()
-    if a.pack:
-        from seedpack_amd import device as dev
+    if a.pack or a.unpack:
         files = a.pack_files.split(",") if a.pack_files else None
-        print(json.dumps(pack_cfg4(dev.Stream(), layers=a.pack_layers, files=files)))
-        return None
-    if a.unpack:
-        from seedpack_amd import device as dev
-        print(json.dumps(unpack_cfg5(dev.Stream(), layers=a.pack_layers)))
+        pk, upk = repo_cfg45(layers=a.pack_layers, files=files)
+        print(json.dumps({"pack_cfg4": pk, "unpack_cfg5": upk}))
         return None
     if a.codecs:
         from seedpack_amd import device as dev
@@ -762,8 +604,7 @@ def main():
     qrg = qr_cfg3(stream)
     r2b = r2_layer(stream)
     r2c = r2_cfg4(stream)
-    pk = pack_cfg4(stream)
-    upk = unpack_cfg5(stream)
+    pk, upk = (None, None) if a.no_repo else repo_cfg45()
     cpu = None if a.no_cpu else cpu_baseline(tensors)
     line = {"metric": "requant GB/s (BF16 in), K-quant family Q2_K..Q6_K with imatrix", "value": round(value, 3),
             "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 3),

@@ -1,26 +1,115 @@
 """Device memory, streams and events over the library's own HIP runtime (no framework needed).
 
 DeviceArray is the minimal device array the host layer passes around: a HIP allocation with a
-dtype and a shape. It plays the role CuPy arrays play in the reference (seedpack/xp.py:6-18).
+dtype and a shape. It plays the role CuPy arrays play in the reference (seedpack/xp.py:6-18). Freed
+allocations go to a per-size cache and are reused (as CuPy's memory pool does), so that short-lived
+arrays never reach hipFree, which waits for the whole device.
 """
+import collections
 import ctypes
+import threading
 
 import numpy as np
 
 from ._lib import check, lib
 
 
+class _Cache:
+    """freed device allocations kept for reuse, by device and size class: hipFree waits for every
+    stream of the device, so freeing a short-lived array (a prediction, a batch's buffers) would stall
+    the work other threads have queued. A freed block goes back to the thread that allocated it and
+    is reused only there: every thread here queues its work on one stream of its own, so work still
+    queued on a block precedes, in stream order, whatever reuses it (a block dropped by another
+    thread is dropped after that thread waited for its own work on it). At most `limit` bytes are held
+    in all; beyond it memory is freed."""
+
+    def __init__(self, limit=48 << 30):
+        self.limit, self.bytes, self.lock = limit, 0, threading.Lock()
+        self.tls = threading.local()
+        self.owners = {}
+
+    @staticmethod
+    def size_class(n):
+        n = max(int(n), 1)
+        step = 4096 if n <= (1 << 20) else 1 << 20
+        return -(-n // step) * step
+
+    def mine(self):
+        """this thread's free lists"""
+        f = getattr(self.tls, "free", None)
+        if f is None:
+            f = self.tls.free = collections.defaultdict(list)
+        return f
+
+    def take(self, dev_id, n):
+        f = self.mine()
+        with self.lock:
+            lst = f.get((dev_id, n))
+            if lst:
+                self.bytes -= n
+                return lst.pop()
+        return None
+
+    def give(self, owner, dev_id, ptr, n):
+        with self.lock:
+            if self.bytes + n > self.limit:
+                return False
+            self.bytes += n
+            owner[(dev_id, n)].append(ptr)
+            self.owners[id(owner)] = owner
+            return True
+
+    def drain(self, lists):
+        """free the blocks of the given free lists"""
+        with self.lock:
+            blocks = [(k[1], p) for f in lists for k, ps in f.items() for p in ps]
+            for f in lists:
+                f.clear()
+            self.bytes -= sum(n for n, _ in blocks)
+        for _, p in blocks:
+            lib().spa_free(p)
+
+    def alloc(self, n):
+        """a new device block of n bytes; when the device is full, this thread's cached blocks are
+        freed and, if that is not enough, every thread's after waiting for the whole device"""
+        p = ctypes.c_void_p()
+        for attempt in range(3):
+            if lib().spa_malloc(ctypes.byref(p), n) == 0:
+                return p.value
+            if attempt == 0:
+                self.drain([self.mine()])
+            else:
+                check(lib().spa_device_synchronize())
+                with self.lock:
+                    lists = list(self.owners.values())
+                self.drain(lists)
+        check(lib().spa_malloc(ctypes.byref(p), n))
+        return p.value
+
+
+CACHE = _Cache()
+
+
+def _device_id():
+    d = ctypes.c_int()
+    check(lib().spa_get_device(ctypes.byref(d)))
+    return d.value
+
+
 class DeviceArray:
-    __slots__ = ("ptr", "nbytes", "dtype", "shape", "_owner")
+    __slots__ = ("ptr", "nbytes", "dtype", "shape", "_owner", "_alloc")
 
     def __init__(self, shape, dtype, ptr=None, owner=None):
         self.dtype = np.dtype(dtype)
         self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
         self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        self._alloc = None
         if ptr is None:
-            p = ctypes.c_void_p()
-            check(lib().spa_malloc(ctypes.byref(p), self.nbytes))
-            self.ptr, self._owner = p.value, None
+            dev_id, n = _device_id(), _Cache.size_class(self.nbytes)
+            q = CACHE.take(dev_id, n)
+            if q is None:
+                q = CACHE.alloc(n)
+            self.ptr, self._owner, self._alloc = q, None, (CACHE.mine(), dev_id, n)
         else:
             self.ptr, self._owner = ptr, owner if owner is not None else self
 
@@ -55,7 +144,9 @@ class DeviceArray:
     def __del__(self):
         if getattr(self, "_owner", 1) is None and getattr(self, "ptr", None):
             try:
-                lib().spa_free(self.ptr)
+                owner, dev_id, n = self._alloc
+                if not CACHE.give(owner, dev_id, self.ptr, n):
+                    lib().spa_free(self.ptr)
             except Exception:
                 pass
             self.ptr = None

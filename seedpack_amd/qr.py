@@ -323,6 +323,7 @@ def decode_parts(T, freq, used, lens, stream_bytes, items, seed_dev, imx_dev=Non
     imx = None if imx_dev is None else imx_dev.ptr
     check(lib().spa_qr_decode(T, s_d.ptr, len(s), offs_d.ptr, P.ptr, seed_dev.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr,
                               freq_d.ptr, cum_d.ptr, lut.ptr, F.ptr, _gk_ptr(T), imx, mv, stream))
+    dev.synchronize(stream)          # the batch's descriptors and tables go out of scope here
     return F
 
 

@@ -34,9 +34,10 @@ import os
 import re
 import threading
 import time
-from concurrent.futures import ThreadPoolExecutor
+from concurrent.futures import Future, ThreadPoolExecutor
 
 import numpy as np
+import xxhash
 
 from . import container, device as dev, gguf, header, imatrix as imx_mod, qr, r2, residual, zstd
 from ._lib import check, lib
@@ -155,20 +156,6 @@ def _read_into(path, out, off=0, pool=None):
     return out
 
 
-class _Staging:
-    """reusable page-locked host buffers (copies to and from HBM at the link's full rate), grown on demand"""
-
-    def __init__(self):
-        self.bufs = {}
-
-    def get(self, key, n):
-        b = self.bufs.get(key)
-        if b is None or b.size < n:
-            self.bufs.pop(key, None)
-            b = self.bufs[key] = dev.pinned(max(n, 1 << 20))
-        return b[:n]
-
-
 class _DevBuf:
     """a reusable device buffer (freeing HBM waits for the whole device), grown on demand"""
 
@@ -180,6 +167,112 @@ class _DevBuf:
             self.a = None
             self.a = dev.DeviceArray(max(n, 1 << 20), np.uint8)
         return self.a.view(0, (n,), np.uint8)
+
+
+class _DevPool:
+    """a few reusable device buffers (the files in flight), grown on demand: acquire(n) -> a view of n
+    bytes (waits while all are out), release(view)"""
+
+    def __init__(self, count):
+        self.free, self.cv = [None] * count, threading.Condition()
+
+    def acquire(self, n):
+        with self.cv:
+            while not self.free:
+                self.cv.wait()
+            a = self.free.pop()
+        if a is None or a.nbytes < n:
+            a = dev.DeviceArray(max(n, 1 << 20), np.uint8)
+        v = a.view(0, (n,), np.uint8)
+        return v
+
+    def release(self, v):
+        with self.cv:
+            self.free.append(v._owner)
+            self.cv.notify_all()
+
+
+class _PinnedPool:
+    """page-locked host buffers handed out under a byte budget and reused: acquire(n) -> a buffer of at
+    least n bytes (waits while the budget is spent), release(buffer) hands it back"""
+
+    def __init__(self, budget):
+        self.budget, self.total, self.free = budget, 0, []
+        self.cv = threading.Condition()
+
+    def acquire(self, n):
+        with self.cv:
+            while True:
+                fit = [k for k, b in enumerate(self.free) if b.size >= n]
+                if fit:
+                    return self.free.pop(min(fit, key=lambda k: self.free[k].size))
+                if self.free and self.total + n > self.budget:
+                    # free buffers too small: the largest is dropped
+                    big = self.free.pop(max(range(len(self.free)), key=lambda k: self.free[k].size))
+                    self.total -= big.size
+                    continue
+                if self.total + n <= self.budget or self.total == 0:
+                    self.total += n
+                    break
+                self.cv.wait()
+        return dev.pinned(n)
+
+    def release(self, b):
+        base = b.base if b.base is not None and isinstance(b.base, np.ndarray) else b
+        while isinstance(base.base, np.ndarray):
+            base = base.base
+        with self.cv:
+            self.free.append(base)
+            self.cv.notify_all()
+
+
+def file_sha256(path, chunk=64 << 20):
+    """SHA-256 of a file, read in pieces into a buffer of its own"""
+    h = hashlib.sha256()
+    buf = np.empty(chunk, np.uint8)
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        off = 0
+        while True:
+            k = os.preadv(fd, [memoryview(buf)], off)
+            if k <= 0:
+                break
+            h.update(memoryview(buf)[:k])
+            off += k
+    finally:
+        os.close(fd)
+    return h.hexdigest()
+
+
+def process_order(files, groups):
+    """the order the derived files are processed in: largest first, except that two files of one group
+    sharing a (tensor name, type) pair keep their archive order -- a reference can only point to an
+    earlier file with the same tensor (repo3.py:2006-2030), so processing them in any such order makes
+    the same archive. A group whose potential references could exceed a window's REF_KEEP budget (then
+    the decisions depend on the order of all its files) keeps its archive order throughout.
+    files: {index: (bytes, {(name, type)}, group, {window: potential reference bytes})}"""
+    ks = sorted(files)
+    strict = set()
+    for g in set(v[2] for v in files.values()):
+        pot = collections.Counter()
+        for i in ks:
+            if files[i][2] == g:
+                for w, nb in files[i][3].items():
+                    pot[w] += nb
+        if any(v > REF_KEEP for v in pot.values()):
+            strict.add(g)
+
+    def before(j, i):                       # must j (archive order j < i) be processed before i?
+        gj, gi = files[j][2], files[i][2]
+        return gj == gi and (gi in strict or files[j][1] & files[i][1])
+
+    todo, out = list(ks), []
+    while todo:
+        ready = [i for i in todo if not any(j < i and before(j, i) for j in todo)]
+        pick = max(ready, key=lambda i: (files[i][0], -i))
+        out.append(pick)
+        todo.remove(pick)
+    return out
 
 
 class _Base:
@@ -208,28 +301,40 @@ class Packer:
     for a repository with BF16 base model(s), quantized GGUFs derived from them, an imatrix and other
     files"""
 
-    def __init__(self, level=7, verbose=False, coders=4):
+    def __init__(self, level=7, verbose=False, coders=4, zstd_lanes=12, staging_bytes=32 << 30):
         self.level, self.verbose = level, verbose
         self.stream = dev.Stream()
         self.gq = GPUQuant(stream=self.stream.handle)
-        self.io = ThreadPoolExecutor(8)          # file reads (pieces), tensor hashes
-        self.hasher = ThreadPoolExecutor(4)      # file checksums
-        self.zpool = ThreadPoolExecutor(4)       # residual zstd, QR framing
+        self.io = ThreadPoolExecutor(8)          # file reads (pieces)
+        self.hasher = ThreadPoolExecutor(8)      # file checksums
+        self.zpool = ThreadPoolExecutor(zstd_lanes)   # residual frames (one thread each, as the reference's)
+        self.reader = ThreadPoolExecutor(1)      # the next file read ahead
         self.coders = ThreadPoolExecutor(coders)
+        self.pool = _PinnedPool(staging_bytes)
+        self.fpool = _DevPool(3)                 # device copies of the files in flight
+        self.finisher = ThreadPoolExecutor(1)    # stage 2 of each file
         self.tls = threading.local()
-        self.staging = _Staging()
-        self.fbuf = _DevBuf()
+        self.timing = []
         self.stats = collections.Counter()
         self.sizes = {}
 
     # ---------------------------------------------------------------- bases
-    def _load_base(self, i, name, path):
-        """the base file read into page-locked memory and uploaded whole"""
+    def _load_base(self, i, name, path, piece=256 << 20):
+        """the base file uploaded whole, read through two page-locked pieces (the next piece is read
+        while the current one is copied); its bytes stay mapped for the header coder"""
         size = os.path.getsize(path)
-        host = dev.pinned(size)
-        _read_into(path, host, pool=self.io)
         d = dev.DeviceArray(size, np.uint8)
-        check(lib().spa_memcpy_h2d(d.ptr, host.ctypes.data, size, self.stream.handle))
+        bufs = [dev.pinned(min(piece, max(size, 1))) for _ in range(2)]
+        offs = list(range(0, size, piece))
+        nxt = self.reader.submit(_read_into, path, bufs[0][:min(piece, size)], 0, self.io) if offs else None
+        for k, o in enumerate(offs):
+            n = min(piece, size - o)
+            nxt.result()
+            if k + 1 < len(offs):
+                o2 = offs[k + 1]
+                nxt = self.reader.submit(_read_into, path, bufs[(k + 1) % 2][:min(piece, size - o2)], o2, self.io)
+            check(lib().spa_memcpy_h2d(d.ptr + o, bufs[k % 2].ctypes.data, n, self.stream.handle))
+        host = np.memmap(path, np.uint8, "r") if size else np.zeros(0, np.uint8)
         return host, _Base(i, name, host, d, gguf.GGUF(host))
 
     def _code_base(self, b, host, order):
@@ -257,27 +362,34 @@ class Packer:
         return qr.frame(parts)
 
     # ---------------------------------------------------------------- one derived file
-    def _residual_file(self, fi, name, path, b, tens, wins_of, wstate, imx_dev, imx_off, imx_map, last_window):
-        """file fi against base b: its bytes read and hashed, uploaded, regrown and compared, QR-coded and
-        zeroed on the device -> (manifest entry, residual chunk, QR chunk or None, checksum)"""
-        size = os.path.getsize(path)
-        host = self.staging.get(("in", fi % 2), size)
-        _read_into(path, host, pool=self.io)
-        hjob = self.hasher.submit(_ws, host)
+    def _read_file(self, job):
+        """(reader thread) the file's bytes into a page-locked buffer and its tensors' content hashes
+        (the keys of references); its checksum is computed from a read of its own"""
+        size = os.path.getsize(job["path"])
+        host = self.pool.acquire(size)[:size]
+        _read_into(job["path"], host, pool=self.io)
+        job["host"] = host
+        job["thash"] = {t.name: xxhash.xxh3_128_digest(memoryview(host[t.offset:t.offset + t.nbytes]))
+                        for t, k in job["tens"] if k}
+        return job
+
+    def _device_file(self, job, b, imx_dev, imx_off, imx_map):
+        """(device thread, stage 1) file job["fi"] against base b: uploaded, regrown and compared, its QR
+        batches handed to the coders -> the state stage 2 finishes"""
+        fi, host, tens = job["fi"], job["host"], job["tens"]
+        wins_of, wstate, thash = job["wins_of"], job["wstate"], job["thash"]
+        tm = {"t0": time.perf_counter()}
+        size = host.size
         pred = [(t, k) for t, k in tens if k]
         by_name = {t.name: t for t, _ in tens}
-        thash = {t.name: f for t, f in ((t, self.io.submit(lambda a: hashlib.blake2b(a, digest_size=16).digest(),
-                                                                  host[t.offset:t.offset + t.nbytes]))
-                                        for t, _ in pred)}
-        F = self.fbuf.get(size)
+        F = self.fpool.acquire(size)
         st = self.stream.handle
         check(lib().spa_memcpy_h2d(F.ptr, host.ctypes.data, size, st))
-        thash = {n: f.result() for n, f in thash.items()}
+        tm["upload"] = time.perf_counter()
         # references: equal to a tensor an earlier file of the same window left a residual in
         refs, mine = {}, []
         for t, k in pred:
-            w = wins_of[t.name]
-            ws = wstate[w]
+            ws = wstate[wins_of[t.name]]
             key = (t.name, t.type, thash[t.name])
             src = ws["first"].get(key)
             if src is not None and ws["memo"].get(key, False) and t.nbytes >= DUP_MIN:
@@ -296,13 +408,15 @@ class Packer:
                                b.view(b.by_name[t.name]), imatrix=imx_map.get(t.name), base_type=b.by_name[t.name].type,
                                numel=t.numel) for t, _ in mine]
         res = residual.residual_window(rts, self.gq, stream=st) if rts else []
+        tm["regrow"] = time.perf_counter()
         out = {t.name: r for (t, _), r in zip(mine, res)}
         for t, _ in mine:
             ws = wstate[wins_of[t.name]]
             key = (t.name, t.type, thash[t.name])
             ws["first"].setdefault(key, fi)
             ws["memo"][key] = bool(out[t.name]["nonzero"])
-        # plan entries and QR batches, window by window (the reference's order)
+        # plan entries and QR batches, window by window, each window's QR tensors by type in order of
+        # appearance (repo3.py:946-979)
         plan, qmeta, qjobs = [], [], []
         by_w = collections.defaultdict(list)
         for t, _ in pred:
@@ -314,65 +428,91 @@ class Packer:
                     continue
                 r = out[t.name]
                 plan.append([t.name, "qr" if r["qr"] else r["kind"], r["variant"], t.type])
+                self.stats["xor" if r["kind"] == "xor" else "requant_diff" if r["nonzero"] else "requant_exact"] += 1
                 if r["qr"]:
                     qitems[t.type].append(t)
             plan += [[n, "ref", refs[n], by_name[n].type] for n in refs if wins_of[n] == w]
             for T, ts in qitems.items():
                 for batch in qr.batches(T, [t.nbytes for t in ts]):
                     its = [ts[i] for i in batch]
+                    grid = T in qr.GRID_TYPES
                     items = [(F.view(t.offset, (t.nbytes,), np.uint8), out[t.name]["prediction"], b.by_name[t.name].offset,
-                              b.by_name[t.name].type, b.by_name[t.name].shape[0],
-                              imx_off.get(t.name, -1) if T in qr.GRID_TYPES else -1) for t in its]
-                    if T in qr.GRID_TYPES:
-                        self.stats["qr_grid"] += len(its)
+                              b.by_name[t.name].type, b.by_name[t.name].shape[0], imx_off.get(t.name, -1) if grid else -1)
+                             for t in its]
+                    self.stats["qr_grid"] += len(its) if grid else 0
                     qmeta.append([T, [t.name for t in its]])
-                    qjobs.append(self.coders.submit(self._qr_job, T, items, b.d, imx_dev if T in qr.GRID_TYPES else None))
-            for t in by_w[w]:
-                if t.name in out:
-                    self.stats["xor" if out[t.name]["kind"] == "xor" else
-                               "requant_diff" if out[t.name]["nonzero"] else "requant_exact"] += 1
+                    qjobs.append(self.coders.submit(self._qr_job, T, items, b.d, imx_dev if grid else None))
         self.stats["qr"] += sum(len(m[1]) for m in qmeta)
-        self.stream.synchronize()
-        qparts = [f.result() for f in qjobs]             # the coders read the QR tensors' file bytes
         qr_regions = [(t.offset, t.nbytes) for t, _ in mine if out[t.name]["qr"]]
-        for off, nb in qr_regions:
-            check(lib().spa_memset(F.ptr + off, 0, nb, st))
-        resid = self.staging.get(("out", fi % 2), size)
-        check(lib().spa_memcpy_d2h(resid.ctypes.data, F.ptr, size, st))
-        # the zstd level, judged as the reference judges it: from the file's first span that holds a
-        # predicted tensor, from that tensor on, before the QR jobs zero their tensors (repo3.py:1935-1944)
-        prm = self._zparams(resid, host, pred, wins_of, qr_regions, last_window)
-        digest = hjob.result()
-        zjob = self.zpool.submit(zstd.compress_with, resid, prm, b.header)
-        qchunk = None
-        if qmeta:
-            qchunk = pack_parts({"meta": zstd.compress(json.dumps(qmeta).encode(), 19),
-                                 **{str(k): p for k, p in enumerate(qparts)}})
-        entry = {"name": name, "size": size, "base": b.index, "plan": plan}
-        return entry, zjob.result(), qchunk, digest
+        # the bytes the residual's zstd level is judged from (the file's, in the QR tensors)
+        sample = self._zsample(host, pred, wins_of, qr_regions, job["last_window"])
+        self.stream.synchronize()
+        self.pool.release(job.pop("host"))
+        entry = {"name": job["name"], "size": size, "base": b.index, "plan": plan}
+        return {"fi": fi, "F": F, "qjobs": qjobs, "qmeta": qmeta, "qr_regions": qr_regions, "sample": sample,
+                "entry": entry, "zdict": b.header, "tm": tm}
 
-    def _zparams(self, resid, host, pred, wins_of, qr_regions, last_window):
-        """zstd parameters of a file's residual: the sparse level when under SPARSE of every 61st byte of
-        its first span, from its first predicted tensor on, is non-zero (QR tensors still holding their
-        file bytes)"""
+    def _finish_file(self, state):
+        """(finisher thread, stage 2) the QR batches awaited, their tensors zeroed, the residual read back
+        and handed to a zstd lane -> (manifest entry, QR chunk or None, future of the residual frame)"""
+        if not hasattr(self.tls, "stream"):
+            self.tls.stream = dev.Stream()
+        st = self.tls.stream.handle
+        F, size = state["F"], state["entry"]["size"]
+        qparts = [f.result() for f in state["qjobs"]]     # the coders read the QR tensors' file bytes
+        tm = state["tm"]
+        tm["qr"] = time.perf_counter()
+        for off, nb in state["qr_regions"]:
+            check(lib().spa_memset(F.ptr + off, 0, nb, st))
+        resid = self.pool.acquire(size)[:size]
+        check(lib().spa_memcpy_d2h(resid.ctypes.data, F.ptr, size, st))
+        self.fpool.release(F)
+        tm["readback"] = time.perf_counter()
+        pos, in_qr, qr_vals, span = state["sample"]
+        v = resid[pos]                              # (fancy indexing: a copy)
+        v[in_qr] = qr_vals
+        sparse = np.count_nonzero(v) * 61 < SPARSE * span
+        prm = zstd.Params(max(self.level, 9) if sparse else self.level, window_log=25)
+        qchunk = None
+        if state["qmeta"]:
+            qchunk = pack_parts({"meta": zstd.compress(json.dumps(state["qmeta"]).encode(), 19),
+                                 **{str(k): p for k, p in enumerate(qparts)}})
+        t0 = tm.pop("t0")
+        self.timing.append({"file": state["entry"]["name"], "level": prm.level,
+                            **{k: round(v - t0, 3) for k, v in tm.items()}})
+        return state["entry"], qchunk, self.zpool.submit(self._compress, resid, prm, state["zdict"])
+
+    def _compress(self, resid, prm, zdict):
+        """(zstd lanes) the residual's frame; its buffer back to the pool"""
+        try:
+            return zstd.compress_with(resid, prm, zdict)
+        finally:
+            self.pool.release(resid)
+
+    @staticmethod
+    def _zsample(host, pred, wins_of, qr_regions, last_window):
+        """the bytes the zstd level is judged from: every 61st byte of the file's first span that holds a
+        predicted tensor, from that tensor on -> (positions, which of them lie in QR tensors, the file's
+        bytes there, the span's length)"""
         pred = [t for t, _ in pred]
         start = min(t.offset for t in pred)
         first_w = min(wins_of[t.name] for t in pred)
         end = max(t.offset + t.nbytes for t in pred if wins_of[t.name] == first_w)
         if first_w == last_window:
-            end = len(resid)                        # the last window's span runs to the end of the file
+            end = host.size                         # the last window's span runs to the end of the file
         pos = np.arange(start, end, 61, dtype=np.int64)
-        v = resid[pos]                              # (fancy indexing: a copy)
+        in_qr = np.zeros(pos.size, bool)
         for off, nb in qr_regions:
-            m = (pos >= off) & (pos < off + nb)
-            if m.any():
-                v[m] = host[pos[m]]
-        sparse = np.count_nonzero(v) * 61 < SPARSE * (end - start)
-        return zstd.Params(max(self.level, 9) if sparse else self.level, window_log=25)
+            in_qr |= (pos >= off) & (pos < off + nb)
+        return pos, in_qr, host[pos[in_qr]], end - start
 
     # ---------------------------------------------------------------- the repository
     def pack(self, inputs, output, tool=TOOL, created=None, force=False):
         t0 = time.perf_counter()
+        phases = {}
+
+        def phase(name):
+            phases[name] = round(time.perf_counter() - t0, 3)
         files = collect(inputs)
         if not files:
             raise ValueError("nothing to archive")
@@ -415,11 +555,12 @@ class Packer:
             side = ThreadPoolExecutor(1)
             base_jobs = []
             for i, (n, p) in enumerate(bases.items()):
+                hashes[n] = self.hasher.submit(file_sha256, p)
                 host, b = self._load_base(i, n, p)
-                hashes[n] = self.hasher.submit(_ws, host)
                 loaded.append((host, b))
                 base_jobs.append(side.submit(self._code_base, b, host, "stream" if i == 0 else "parts"))
             self.stream.synchronize()
+            phase("bases resident")
             log(self.verbose, f"  {len(bases)} base(s) resident in HBM, {time.perf_counter() - t0:.1f} s")
             # the repository's importance per tensor on the device (the grid QR types read it)
             imx_vecs = {k: np.asarray(v, np.float32) for k, v in imx_all.items()}
@@ -439,50 +580,86 @@ class Packer:
                 common = [len({t.name for t in ts} & s) for s in base_names]
                 best = [k for k, c in enumerate(common) if c == max(common)][0]
                 per_base[best].append((fi, n, ts))
-            order_done = []
+            # derived files: per base, grouped by tensor order; windows over each group's order
+            jobs, plain, order_done = {}, [], []
             for bi, items in per_base.items():
-                host_b, b = loaded[bi]
-                found, plain = [], []
+                b = loaded[bi][1]
+                found = []
                 for fi, n, ts in items:
                     tk = [(t, self._kind(b, t, imx_all)) for t in ts]
                     self.stats["raw"] += sum(k is None for _, k in tk)
                     order = tuple(t.name for t, k in sorted(tk, key=lambda x: x[0].offset) if k)
-                    (found if order else plain).append((order, fi, n, tk))
-                for order, ks in order_groups([f[0] for f in found]).items():
+                    if order:
+                        found.append((order, fi, n, tk))
+                    else:
+                        plain.append((bi, fi, n))
+                for gk, (order, ks) in enumerate(order_groups([f[0] for f in found]).items()):
                     sts = [found[k] for k in ks]
                     # the windows' prediction bytes: per tensor, its distinct first predictions over the files
                     pred = [sum({(t.type, residual.v0(k_, imx_all.get(t.name) is not None)): t.nbytes
                                  for _, _, _, tk in sts for t, k_ in tk if t.name == nm and k_}.values()) for nm in order]
                     wins = windows([b.by_name[nm].nbytes for nm in order], WINDOW, pred)
-                    wins_of = {nm: w_ for w_, (a, z) in enumerate(wins) for nm in order[a:z]}
+                    wins_of = {nm: w_ for w_, (a_, z_) in enumerate(wins) for nm in order[a_:z_]}
                     wstate = [{"first": {}, "memo": {}, "kept": set(), "kept_bytes": 0} for _ in wins]
                     for _, fi, n, tk in sts:
-                        tf = time.perf_counter()
-                        entry, fchunk, qchunk, digest = self._residual_file(fi, n, derived[n], b, tk, wins_of, wstate,
-                                                                            imx_dev, imx_off, imx_map, len(wins) - 1)
-                        entries[fi], chunks[fi], hashes[n] = entry, (fchunk, qchunk), digest
+                        jobs[fi] = {"fi": fi, "name": n, "path": derived[n], "tens": tk, "wins_of": wins_of,
+                                    "wstate": wstate, "last_window": len(wins) - 1, "base": bi, "group": (bi, gk)}
                         order_done.append(fi)
-                        log(self.verbose, f"  {n}: {entry['size']:,} B -> {len(fchunk):,} + "
-                                          f"{nbytes(qchunk) if qchunk else 0:,} B in {time.perf_counter() - tf:.2f} s")
-                for _, fi, n, tk in plain:
-                    # nothing to predict: the file zstd'd against the base header (repo3.py:2062-2076)
-                    data = open(derived[n], "rb").read()
-                    hashes[n] = self.hasher.submit(_ws, data)
-                    entries[fi] = {"name": n, "size": len(data), "base": b.index, "plan": []}
-                    chunks[fi] = (zstd.compress_with(data, zstd.Params(self.level, window_log=25, threads=4), b.header), None)
-                    order_done.append(fi)
+            # processing order: largest first where that cannot change the archive (process_order)
+            info, seen_keys = {}, {}
+            for fi in sorted(jobs):
+                j = jobs[fi]
+                keys = {(t.name, t.type) for t, k in j["tens"] if k and t.nbytes >= DUP_MIN}
+                prev = seen_keys.setdefault(j["group"], set())
+                pot = collections.Counter()
+                for t, k in j["tens"]:
+                    if k and (t.name, t.type) in prev and t.nbytes >= DUP_MIN:
+                        pot[j["wins_of"][t.name]] += t.nbytes
+                prev |= keys
+                info[fi] = (os.path.getsize(j["path"]), keys, j["group"], pot)
+            porder = process_order(info, None)
+            for fi in porder:
+                hashes[names[fi]] = self.hasher.submit(file_sha256, jobs[fi]["path"])
+            # the pipeline: the next file read ahead, one file at a time on the device, the residual
+            # frames on the zstd lanes
+            zjobs = {}
+            ahead = self.reader.submit(self._read_file, jobs[porder[0]]) if porder else None
+            for k, fi in enumerate(porder):
+                job = ahead.result()
+                ahead = self.reader.submit(self._read_file, jobs[porder[k + 1]]) if k + 1 < len(porder) else None
+                b = loaded[job["base"]][1]
+                state = self._device_file(job, b, imx_dev, imx_off, imx_map)
+                zjobs[fi] = self.finisher.submit(self._finish_file, state)
+                log(self.verbose, f"  {state['entry']['name']}: {state['entry']['size']:,} B regrown and compared in "
+                                  f"{state['tm']['regrow'] - state['tm']['t0']:.2f} s")
+            phase("derived files on the device")
+            for bi, fi, n in plain:
+                # nothing to predict: the file zstd'd against the base header (repo3.py:2062-2076)
+                b = loaded[bi][1]
+                data = open(derived[n], "rb").read()
+                hashes[n] = self.hasher.submit(_ws, data)
+                entries[fi] = {"name": n, "size": len(data), "base": b.index, "plan": []}
+                done = Future()
+                done.set_result((entries[fi], None, self.zpool.submit(
+                    zstd.compress_with, data, zstd.Params(self.level, window_log=25, threads=4), b.header)))
+                zjobs[fi] = done
+                order_done.append(fi)
             coded = [j.result() for j in base_jobs]
             side.shutdown()
+            phase("base coded")
             # chunk order of the reference: the first base (written while it is coded), the files
-            # derived from the bases, then the other bases
-            w.put("b0", coded[0]) if coded else None
+            # derived from the bases (streamed ones, then the others), then the other bases
+            if coded:
+                w.put("b0", coded[0])
             for fi in order_done:
-                fchunk, qchunk = chunks[fi]
+                entries[fi], qchunk, zf = zjobs[fi].result()
+                fchunk = zf.result()
                 w.put(f"f{fi}", fchunk)
                 self.sizes[names[fi]] = len(fchunk)
                 if qchunk is not None:
                     w.put(f"q{fi}", qchunk)
                     self.sizes[names[fi] + " (QR)"] = nbytes(qchunk)
+            phase("residual frames")
             for i in range(1, len(coded)):
                 w.put(f"b{i}", coded[i])
             for n, c in zip(bases, coded):
@@ -493,6 +670,7 @@ class Packer:
                 manifest["needs"] = "0.3.0"
             w.put("manifest", zstd.compress(json.dumps(manifest).encode(), 19))
             hashes = {n: (h.result() if hasattr(h, "result") else h) for n, h in hashes.items()}
+            phase("checksums")
             catalog = [{"name": n, "size": os.path.getsize(p), "hash": hashes[n], "role": roles[n] or "file",
                         "stored": self.sizes.get(n)} for n, p in files.items()]
             w.close({"tool": tool, "method": METHOD, "created": created or _created(), "hash": "sha256",
@@ -503,8 +681,9 @@ class Packer:
         dt = time.perf_counter() - t0
         size = os.path.getsize(output)
         log(self.verbose, f"{output}: {total:,} B -> {size:,} B in {dt:.1f} s ({total / dt / 1e9:.2f} GB/s)")
+        phase("closed")
         return {"input_bytes": total, "archive_bytes": size, "seconds": dt, "GB_s": total / dt / 1e9,
-                "stats": dict(self.stats)}
+                "stats": dict(self.stats), "phases": phases, "files": self.timing}
 
     @staticmethod
     def _kind(b, t, imx_all):
@@ -555,13 +734,14 @@ class Unpacker:
     the host, uploaded, its predictions regrown and XORed in and its QR batches decoded on the device,
     then read back, checked and written"""
 
-    def __init__(self, verbose=False):
+    def __init__(self, verbose=False, staging_bytes=64 << 30):
         self.verbose = verbose
         self.stream = dev.Stream()
         self.gq = GPUQuant(stream=self.stream.handle)
-        self.staging = _Staging()
+        self.pool = _PinnedPool(staging_bytes)
         self.rbuf = _DevBuf()
-        self.io = ThreadPoolExecutor(4)           # checksums and writes
+        self.io = ThreadPoolExecutor(8)           # checksums and writes
+        self.ahead = ThreadPoolExecutor(1)        # the next file's residual decompressed ahead
 
     def run(self, archive, outdir=None, patterns=None):
         t0 = time.perf_counter()
@@ -591,17 +771,21 @@ class Unpacker:
                  {mf[i]["base"] for i in sel if mf[i]["base"] is not None}
         results, jobs = {}, []
 
-        def check_write(name, buf):
-            ok = hashlib.sha256(memoryview(buf).cast("B")).hexdigest() == cat[name]["hash"] and \
-                memoryview(buf).nbytes == cat[name]["size"]
-            if ok and outdir is not None:
-                path = os.path.join(outdir, *name.split("/"))
-                os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
-                with open(path + ".part", "wb") as f:
-                    f.write(memoryview(buf).cast("B"))
-                os.replace(path + ".part", path)
-            results[name] = ok
-            return ok
+        def check_write(name, buf, release=False):
+            try:
+                ok = hashlib.sha256(memoryview(buf).cast("B")).hexdigest() == cat[name]["hash"] and \
+                    memoryview(buf).nbytes == cat[name]["size"]
+                if ok and outdir is not None:
+                    path = os.path.join(outdir, *name.split("/"))
+                    os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
+                    with open(path + ".part", "wb") as f:
+                        f.write(memoryview(buf).cast("B"))
+                    os.replace(path + ".part", path)
+                results[name] = ok
+                return ok
+            finally:
+                if release:
+                    self.pool.release(buf)
 
         # other files
         exm = manifest["extras"]
@@ -637,23 +821,32 @@ class Unpacker:
             b = _Base(i, name, rest, d, g)
             bases[i] = b
             if name in want:
-                host = self.staging.get(("base", i), d.nbytes)
+                host = self.pool.acquire(d.nbytes)[:d.nbytes]
                 check(lib().spa_memcpy_d2h(host.ctypes.data, d.ptr, d.nbytes, self.stream.handle))
-                jobs.append(self.io.submit(check_write, name, host))
+                jobs.append(self.io.submit(check_write, name, host, True))
             log(self.verbose, f"  base {name}: decoded, {time.perf_counter() - t0:.1f} s")
         # quantized files, in archive order; tensors that later files copy are kept on the device
         kept = {}
-        for i in sorted(sel):
+        order = sorted(sel)
+
+        def residual_of(i):
+            m = mf[i]
+            b = bases.get(m["base"]) if m["base"] is not None else None
+            resid = self.pool.acquire(m["size"])[:m["size"]]
+            return zstd.decompress_into(r.get(f"f{i}"), resid, b.header if b is not None else None)
+
+        nxt = self.ahead.submit(residual_of, order[0]) if order else None
+        for k, i in enumerate(order):
             m = mf[i]
             tf = time.perf_counter()
-            b = bases.get(m["base"]) if m["base"] is not None else None
-            resid = self.staging.get(("file", i % 2), m["size"])
-            zstd.decompress_into(r.get(f"f{i}"), resid, b.header if b is not None else None)
+            resid = nxt.result()
+            nxt = self.ahead.submit(residual_of, order[k + 1]) if k + 1 < len(order) else None
             if m["plan"]:
-                self._rebuild(r, i, m, b, resid, kept, last_use, imx_dev, imx_off, imx_map)
+                self._rebuild(r, i, m, bases[m["base"]], resid, kept, last_use, imx_dev, imx_off, imx_map)
             if m["name"] in want:
-                jobs.append(self.io.submit(check_write, m["name"], resid))
-                jobs[-1].result()                 # (its staging buffer is reused two files on)
+                jobs.append(self.io.submit(check_write, m["name"], resid, True))
+            else:
+                self.pool.release(resid)
             log(self.verbose, f"  {m['name']}: {m['size']:,} B in {time.perf_counter() - tf:.2f} s")
         for j in jobs:
             j.result()

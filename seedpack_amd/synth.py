@@ -165,11 +165,14 @@ def write_repo(root, tensors, files, per_million=10000, nmerge=20000, seed=0x5EE
     del host
     imx_d = {n: dev.DeviceArray.from_host(v, st) for n, v in imx_h.items()}
     gq = GPUQuant(stream=st)
-    for fi, (fname, type_of) in enumerate(files.items()):
+    specs = []
+    for fname, type_of in files.items():
         qt = [(n, s, type_of(n) if len(s) == 2 else t) for n, s, t in tensors]
-        qhead, qwhere, qsize = gguf.header_bytes({**kv, "general.file_type": 15, "quantize.imatrix.file": "imatrix.dat",
-                                                  "quantize.imatrix.chunks_count": 125}, qt)
-        out = dev.pinned(qsize)
+        specs.append((fname, qt) + gguf.header_bytes({**kv, "general.file_type": 15, "quantize.imatrix.file": "imatrix.dat",
+                                                      "quantize.imatrix.chunks_count": 125}, qt))
+    staging = dev.pinned(max((sp[4] for sp in specs), default=1))      # one page-locked buffer for every file
+    for fi, (fname, qt, qhead, qwhere, qsize) in enumerate(specs):
+        out = staging[:qsize]
         out[:] = 0
         out[:len(qhead)] = np.frombuffer(qhead, np.uint8)
         for k, ((n, s, t), (off, nb)) in enumerate(zip(qt, qwhere)):
@@ -187,5 +190,4 @@ def write_repo(root, tensors, files, per_million=10000, nmerge=20000, seed=0x5EE
         sizes[fname] = qsize
         if log:
             log(f"synthetic repo: {fname} {qsize:,} B")
-        del out
     return sizes

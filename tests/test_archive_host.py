@@ -191,3 +191,28 @@ def test_window_and_batch_rules():
     assert repo.order_groups([("a", "b", "c"), ("a", "c"), ("d",), ("a", "b", "c")]) == \
         {("a", "b", "c"): [0, 1, 3], ("d",): [2]}
     assert qr.batches(12, [300 << 20, 100 << 20, 10]) == [[0], [1, 2]]
+
+
+def test_pinned_pool_reuses_and_bounds(monkeypatch):
+    """the packer's page-locked staging: buffers reused smallest-fitting first, never above the budget
+    (a free buffer too small for a request is dropped to make room)"""
+    monkeypatch.setattr(repo.dev, "pinned", lambda n: np.empty(n, np.uint8))
+    p = repo._PinnedPool(100)
+    a = p.acquire(40)[:30]
+    b = p.acquire(50)
+    p.release(a)                          # a view: its whole buffer comes back
+    c = p.acquire(35)
+    assert c.size == 40 and p.total == 90
+    p.release(b)
+    p.release(c)
+    d = p.acquire(60)
+    assert d.size == 60 and p.total == 100 and [x.size for x in p.free] == [40]
+
+
+def test_process_order_keeps_dependent_files_in_order():
+    # files 0 and 2 share a tensor key: 0 before 2; the rest largest first
+    files = {0: (5, {("a", 1)}, 0, {}), 1: (9, {("b", 1)}, 0, {}), 2: (7, {("a", 1)}, 0, {}), 3: (8, {("c", 2)}, 1, {})}
+    assert repo.process_order(files, None) == [1, 3, 0, 2]
+    # a group whose potential references could exceed a window's budget keeps archive order
+    files[2] = (7, {("a", 1)}, 0, {0: repo.REF_KEEP + 1})
+    assert repo.process_order(files, None) == [3, 0, 1, 2]

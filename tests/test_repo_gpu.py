@@ -147,3 +147,59 @@ def test_small_repo_one_batch_per_type_equals_oracle(small_repo):
             assert np.array_equal(np.frombuffer(zstd.decompress(ch["l"]), np.uint32), lens), "segment lengths"
             assert bytes(ch["s"]) == stream, "stream"
     assert seen == set(TYPES)
+
+
+def _scratch_dir(tmp_path_factory, name):
+    """a directory on tmpfs when the box has room there (the files are tens of GB), else under /tmp"""
+    import shutil
+    if os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > (80 << 30):
+        d = os.path.join("/dev/shm", f"spa_test_{os.getpid()}_{name}")
+        os.makedirs(d, exist_ok=True)
+        return d
+    return str(tmp_path_factory.mktemp(name))
+
+
+def test_cfg4_reduced_full_shapes(tmp_path_factory):
+    """configuration 4 at full tensor shapes: token_embd and output 151936x4096 and two Qwen3.5-9B
+    blocks (4096 / 12288 / 1024 shapes, F32 norms), a 151,936-token tokenizer, all 21 quant files with
+    1% of their blocks changed; packed and extracted byte-identical (configuration 5 is a selection of
+    that extract). Every QR batch holds tensors of one window and one type, at most BATCH bytes."""
+    import shutil
+    root = _scratch_dir(tmp_path_factory, "cfg4")
+    try:
+        src, out = os.path.join(root, "repo"), os.path.join(root, "out")
+        say("case repo cfg4 reduced: writing the synthetic repository")
+        tensors = synth.qwen_tensors(layers=2)
+        sizes = synth.write_repo(src, tensors, _files(), per_million=10000, nmerge=151936 - 256 - 8)
+        arc = os.path.join(root, "cfg4.seedpack")
+        say(f"case repo cfg4 reduced: pack {sum(sizes.values()) / 1e9:.1f} GB")
+        st = repo.pack_repo([src], arc)
+        say(f"case repo cfg4 reduced: packed in {st['seconds']:.1f} s ({st['GB_s']:.2f} GB/s), {st['phases']}")
+        res = repo.unpack_repo(arc, out)
+        say(f"case repo cfg4 reduced: extracted in {res['seconds']:.1f} s ({res['GB_s']:.2f} GB/s)")
+        assert not res["bad"] and not res["missing"], res
+        for n in sorted(os.listdir(src)):
+            with open(os.path.join(src, n), "rb") as fa, open(os.path.join(out, n), "rb") as fb:
+                while True:
+                    x, y = fa.read(1 << 28), fb.read(1 << 28)
+                    assert x == y, n
+                    if not x:
+                        break
+        # QR batches: one window, one type, within the batch size
+        r = container.Reader(arc)
+        man = json.loads(zstd.decompress(r.get("manifest")))
+        base = {t.name: t for t in gguf.tensors_of(os.path.join(src, "model-BF16.gguf"))}
+        order = [n for n, s, t in tensors]
+        wins = repo.windows([base[n].nbytes for n in order], repo.WINDOW, None)
+        win_of = {n: w for w, (a, z) in enumerate(wins) for n in order[a:z]}
+        assert len(wins) >= 3                     # the embedding alone, the blocks, the output
+        for i, m in enumerate(man["files"]):
+            ft = {t.name: t for t in gguf.tensors_of(os.path.join(src, m["name"]))}
+            q = unpack(memoryview(r.get(f"q{i}")))
+            for T, names in json.loads(zstd.decompress(q["meta"])):
+                assert len({win_of[n] for n in names}) == 1, (m["name"], names)
+                assert all(ft[n].type == T for n in names)
+                assert len(names) == 1 or sum(ft[n].nbytes for n in names) <= qr.BATCH
+    finally:
+        if root.startswith("/dev/shm"):
+            shutil.rmtree(root, ignore_errors=True)
