@@ -290,7 +290,7 @@ class HbmPeak:
         return self.peak
 
 
-def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False):
+def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False, reuse=False, write_only=False):
     """configurations 4 and 5 from host files, as the reference's CLI measures them (cli.py:288-292,
     :441): a synthetic Qwen3.5-9B-shaped repository (BF16 GGUF with a 151,936-token BPE tokenizer,
     imatrix.dat, README.md, 21 quantized GGUFs made by this library's quantizers with 1% of their
@@ -299,7 +299,8 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
     QR coding on the device, the R2 base codec, zstd of the residuals, the container), and the
     extract of the Q4_K_M-like and IQ2_XS files from that archive (residual zstd, regrowth, QR decode,
     SHA-256 check, files written). Peak HBM by hipMemGetInfo polling. The extracted files are
-    compared byte for byte with the originals."""
+    compared byte for byte with the originals. reuse: the repository a previous write_only call left
+    in root is packed (a kernel-trace run then sees the pack and the extract only)."""
     import shutil
     from seedpack_amd import device as dev
     from seedpack_amd import repo, synth
@@ -309,22 +310,37 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
     if files is not None:
         qf = {k: v for k, v in qf.items() if k in files}
     src, arc_dir, out = os.path.join(root, "repo"), os.path.join(root, "arc"), os.path.join(root, "out")
-    for d in (src, arc_dir, out):
+    done = os.path.join(root, "written.json")
+    reuse = reuse and os.path.exists(done)
+    keep = keep or reuse
+    for d in ((arc_dir, out) if reuse else (src, arc_dir, out)):
         shutil.rmtree(d, ignore_errors=True)
         os.makedirs(d)
     try:
-        t0 = time.perf_counter()
-        s = dev.Stream()
-        sizes = synth.write_repo(src, synth.qwen_tensors(layers), qf, per_million=10000, nmerge=151936 - 256 - 8,
-                                 stream=s, log=log)
-        dev.synchronize()
-        log(f"bench: repo written: {len(sizes)} files, {sum(sizes.values()) / 1e9:.1f} GB in {time.perf_counter() - t0:.1f} s")
+        if reuse:
+            sizes = json.load(open(done))
+            log(f"bench: repo reused: {len(sizes)} files, {sum(sizes.values()) / 1e9:.1f} GB")
+        else:
+            t0 = time.perf_counter()
+            s = dev.Stream()
+            sizes = synth.write_repo(src, synth.qwen_tensors(layers), qf, per_million=10000, nmerge=151936 - 256 - 8,
+                                     stream=s, log=log)
+            dev.synchronize()
+            json.dump(sizes, open(done, "w"))
+            log(f"bench: repo written: {len(sizes)} files, {sum(sizes.values()) / 1e9:.1f} GB in {time.perf_counter() - t0:.1f} s")
+        if write_only:
+            keep = True
+            return None, None
         arc = os.path.join(arc_dir, "model.seedpack")
         peak = HbmPeak().start()
-        st = repo.Packer(verbose=True, staging_bytes=32 << 30).pack([src], arc)
+        st = repo.Packer(verbose=True).pack([src], arc)
         pk_peak = peak.stop()
         log(f"bench: pack {st['input_bytes'] / 1e9:.1f} GB -> {st['archive_bytes'] / 1e9:.2f} GB in {st['seconds']:.1f} s "
-            f"= {st['GB_s']:.2f} GB/s, peak HBM {pk_peak / 1e9:.1f} GB")
+            f"= {st['GB_s']:.2f} GB/s, peak HBM {pk_peak / 1e9:.1f} GB (residuals waiting in HBM: at most "
+            f"{st['residuals_in_hbm_peak'] / 1e9:.1f} GB)")
+        for f in st["files"]:
+            log(f"bench:   {f}")
+        log(f"bench: pack cpu {st['cpu']}")
         want = [n for n in ("model-Q4_K_M.gguf", "model-IQ2_XS.gguf") if n in qf]
         peak = HbmPeak().start()
         ex = repo.Unpacker(verbose=True).run(arc, out, want)
@@ -336,7 +352,7 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
                             "file's blocks changed) -> .seedpack", "input_bytes": st["input_bytes"],
                 "archive_bytes": st["archive_bytes"], "ratio": round(st["archive_bytes"] / st["input_bytes"], 4),
                 "pack_s": round(st["seconds"], 2), "pack_GB_s": round(st["GB_s"], 3), "peak_hbm_GB": round(pk_peak / 1e9, 1),
-                "stats": st["stats"], "phases_s": st.get("phases")}
+                "stats": st["stats"], "phases_s": st.get("phases"), "host_cpu_s": st.get("cpu")}
         unpack = {"workload": "cfg5: Q4_K_M-like and IQ2_XS extracted from the cfg4 archive (files written, SHA-256 checked)",
                   "written_bytes": ex["bytes"], "extract_s": round(ex["seconds"], 2), "GB_s_written": round(ex["GB_s"], 3),
                   "checksums_ok": not ex["bad"] and not ex["missing"], "byte_identical": same,
@@ -491,16 +507,23 @@ def main():
     ap.add_argument("--unpack", action="store_true", help="the same as --pack")
     ap.add_argument("--no-repo", action="store_true", help="leave configurations 4 and 5 out of the JSON line")
     ap.add_argument("--pack-files", default=None, help="comma-separated quant files of --pack (default: all 21)")
+    ap.add_argument("--repo-dir", default="/dev/shm/spa_bench_repo", help="where --pack writes its repository")
+    ap.add_argument("--write-repo", action="store_true",
+                    help="only write the --pack repository into --repo-dir and keep it (for a later --reuse-repo run)")
+    ap.add_argument("--reuse-repo", action="store_true",
+                    help="--pack on the repository a --write-repo run left in --repo-dir (kept)")
     ap.add_argument("--codecs", action="store_true",
                     help="only the coding stages (QR on configurations 1 and 3, the R2 base codec), for rocprofv3 "
                          "kernel-trace runs; prints their results, no JSON line")
     a = ap.parse_args()
     if a.profile_pass:
         return profile_pass()
-    if a.pack or a.unpack:
+    if a.pack or a.unpack or a.write_repo:
         files = a.pack_files.split(",") if a.pack_files else None
-        pk, upk = repo_cfg45(layers=a.pack_layers, files=files)
-        print(json.dumps({"pack_cfg4": pk, "unpack_cfg5": upk}))
+        pk, upk = repo_cfg45(layers=a.pack_layers, files=files, root=a.repo_dir, reuse=a.reuse_repo,
+                             write_only=a.write_repo)
+        if not a.write_repo:
+            print(json.dumps({"pack_cfg4": pk, "unpack_cfg5": upk}))
         return None
     if a.codecs:
         from seedpack_amd import device as dev

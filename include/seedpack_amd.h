@@ -182,6 +182,19 @@ int spa_xor3(void* dst, const void* a, const void* b, const void* c, size_t n, u
  * Replaces _count_diff / _diff_async (repo3.py:476-491). */
 int spa_diff_count(const void* a, const void* b, size_t n, unsigned long long* count, void* stream);
 
+/* *count (device u64) = number of non-zero bytes among a[0], a[stride], a[2 stride], ... below n: the
+ * sample the residual frame's zstd level is judged from, np.count_nonzero(v[::61]) (repo3.py:1537,
+ * :1940), taken on the device-resident residual. */
+int spa_count_every(const void* a, size_t n, size_t stride, unsigned long long* count, void* stream);
+
+/* 128-bit content hashes of nregions byte regions of `base` (the keys by which a tensor is found equal
+ * to one of an earlier file; they replace the blake3 digests of repo3.py:1029 / :2018-2022 as those
+ * keys). desc (device, u64): offset and length of each region; out (device, u64): two words per region,
+ * sum over the region's 8-byte little-endian words w_p (the last zero-padded) of
+ * fmix64(w_p ^ fmix64(p * 0x9e3779b97f4a7c15 + s)) for s = 0x243f6a8885a308d3 and 0x13198a2e03707344
+ * (fmix64: MurmurHash3's 64-bit finaliser); equal keys also need equal lengths. */
+int spa_content_hash(const void* base, const uint64_t* desc, int nregions, unsigned long long* out, void* stream);
+
 /* Float-tensor prediction from the base weights (src_kind SPA_SRC_*): n values written as the file's
  * type dst_type = 0 (F32), 1 (F16, round to nearest even) or 30 (BF16, (u + 0x7FFF + ((u >> 16) & 1))
  * >> 16). Replaces _float_dev (repo3.py:673-689). */

@@ -141,11 +141,17 @@ class Writer:
         parts = data if isinstance(data, list) else [data]
         self.jobs.put(lambda: self._write(name, parts))
 
+    def put_later(self, name, fut):
+        """chunk `name` = the result of the future `fut` (bytes-like or a list of them), written in put
+        order once it is ready: the chunks put after it wait for it"""
+        self._claim(name)
+        self.jobs.put(lambda: self._write(name, (lambda d: d if isinstance(d, list) else [d])(fut.result())))
+
     def _write(self, name, parts):
         off, n, crc = self.f.tell(), 0, 0
         for p in parts:
             b = _bytes_of(p)
-            crc = zlib.crc32(b, crc)
+            crc = crc32_combine(crc, crc32_parallel(b), len(b)) if len(b) > 2 * PIECE else zlib.crc32(b, crc)
             self.f.write(b)
             n += len(b)
         self.chunks[name] = [off, n, crc]

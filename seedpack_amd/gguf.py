@@ -121,6 +121,18 @@ def tensors_of(path):
         return []
 
 
+def header_of(path):
+    """(metadata, tensor table) of the GGUF file at `path` (({}, []) if it is not one), from its
+    header only, in one pass"""
+    import mmap
+    try:
+        with open(path, "rb") as f, mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ) as mm:
+            g = GGUF(mm, light=True)
+            return g.meta, g.tensors
+    except (ValueError, OSError, struct.error, KeyError):
+        return {}, []
+
+
 def meta_of(path):
     """the key/value metadata of a GGUF file ({} if it is not one), from its header only"""
     import mmap

@@ -32,12 +32,12 @@ import json
 import lzma
 import os
 import re
+import resource
 import threading
 import time
-from concurrent.futures import Future, ThreadPoolExecutor
+from concurrent.futures import ThreadPoolExecutor, wait as futures_wait
 
 import numpy as np
-import xxhash
 
 from . import container, device as dev, gguf, header, imatrix as imx_mod, qr, r2, residual, zstd
 from ._lib import check, lib
@@ -85,12 +85,12 @@ def collect(inputs):
     return {n: ps[0] for n, ps in out.items()}
 
 
-def file_role(path):
+def file_role(path, header=None):
     """'base' for a GGUF whose tensor bytes are at least half BF16, 'derived' for another GGUF, None for
-    any other file or an imatrix GGUF (cli.py:181-205)"""
+    any other file or an imatrix GGUF (cli.py:181-205); header: its (metadata, tensors) if known"""
     if not path.lower().endswith(".gguf"):
         return None
-    meta, ts = gguf.meta_of(path), gguf.tensors_of(path)
+    meta, ts = header if header is not None else gguf.header_of(path)
     if not meta and not ts:
         return None
     if meta.get("general.type") == "imatrix":
@@ -170,26 +170,53 @@ class _DevBuf:
 
 
 class _DevPool:
-    """a few reusable device buffers (the files in flight), grown on demand: acquire(n) -> a view of n
-    bytes (waits while all are out), release(view)"""
+    """device buffers of the files in flight, under a byte budget and reused (freeing HBM waits for the
+    whole device): acquire(n) -> a view of n bytes of the smallest free buffer that holds it, else of a
+    new buffer while the budget allows (free buffers too small are freed to make room), else it waits;
+    release(view); close() frees every buffer"""
 
-    def __init__(self, count):
-        self.free, self.cv = [None] * count, threading.Condition()
+    def __init__(self, budget):
+        self.budget, self.total, self.peak, self.free = budget, 0, 0, []
+        self.cv = threading.Condition()
 
     def acquire(self, n):
+        n = max(int(n), 1)
         with self.cv:
-            while not self.free:
+            while True:
+                fit = [k for k, a in enumerate(self.free) if a.nbytes >= n]
+                if fit:
+                    a = self.free.pop(min(fit, key=lambda k: self.free[k].nbytes))
+                    return a.view(0, (n,), np.uint8)
+                if self.total + n <= self.budget or self.total == 0:
+                    self.total += n
+                    self.peak = max(self.peak, self.total)
+                    break
+                if self.free:
+                    a = self.free.pop(max(range(len(self.free)), key=lambda k: self.free[k].nbytes))
+                    self.total -= a.nbytes
+                    check(lib().spa_free(a.ptr))
+                    continue
                 self.cv.wait()
-            a = self.free.pop()
-        if a is None or a.nbytes < n:
-            a = dev.DeviceArray(max(n, 1 << 20), np.uint8)
-        v = a.view(0, (n,), np.uint8)
-        return v
+        try:
+            p = dev.CACHE.alloc(n)
+        except BaseException:
+            with self.cv:
+                self.total -= n
+                self.cv.notify_all()
+            raise
+        return dev.DeviceArray((n,), np.uint8, ptr=p, owner=self).view(0, (n,), np.uint8)
 
     def release(self, v):
         with self.cv:
             self.free.append(v._owner)
             self.cv.notify_all()
+
+    def close(self):
+        with self.cv:
+            free, self.free = self.free, []
+            self.total -= sum(a.nbytes for a in free)
+        for a in free:
+            lib().spa_free(a.ptr)
 
 
 class _PinnedPool:
@@ -226,6 +253,24 @@ class _PinnedPool:
             self.cv.notify_all()
 
 
+def _write_file(path, mv, pool, step=64 << 20):
+    """the bytes mv as the file `path`, written in parallel pieces"""
+    fd = os.open(path, os.O_WRONLY | os.O_CREAT | os.O_TRUNC, 0o644)
+    try:
+        def piece(o):
+            v = mv[o:o + step]
+            done = 0
+            while done < len(v):
+                done += os.pwrite(fd, v[done:], o + done)
+        if len(mv) <= step:
+            piece(0)
+        else:
+            for f in [pool.submit(piece, o) for o in range(0, len(mv), step)]:
+                f.result()
+    finally:
+        os.close(fd)
+
+
 def file_sha256(path, chunk=64 << 20):
     """SHA-256 of a file, read in pieces into a buffer of its own"""
     h = hashlib.sha256()
@@ -245,7 +290,8 @@ def file_sha256(path, chunk=64 << 20):
 
 
 def process_order(files, groups):
-    """the order the derived files are processed in: largest first, except that two files of one group
+    """the order the derived files are processed in: largest first (a file that a larger one must wait
+    for goes with that larger one), except that two files of one group
     sharing a (tensor name, type) pair keep their archive order -- a reference can only point to an
     earlier file with the same tensor (repo3.py:2006-2030), so processing them in any such order makes
     the same archive. A group whose potential references could exceed a window's REF_KEEP budget (then
@@ -266,10 +312,17 @@ def process_order(files, groups):
         gj, gi = files[j][2], files[i][2]
         return gj == gi and (gi in strict or files[j][1] & files[i][1])
 
+    # a file's priority: the largest file that waits for it (itself included), so that a small file
+    # holding back a big one goes early
+    prio = {i: files[i][0] for i in ks}
+    for i in reversed(ks):
+        for j in ks:
+            if j < i and before(j, i):
+                prio[j] = max(prio[j], prio[i])
     todo, out = list(ks), []
     while todo:
         ready = [i for i in todo if not any(j < i and before(j, i) for j in todo)]
-        pick = max(ready, key=lambda i: (files[i][0], -i))
+        pick = max(ready, key=lambda i: (prio[i], files[i][0], -i))
         out.append(pick)
         todo.remove(pick)
     return out
@@ -301,41 +354,48 @@ class Packer:
     for a repository with BF16 base model(s), quantized GGUFs derived from them, an imatrix and other
     files"""
 
-    def __init__(self, level=7, verbose=False, coders=4, zstd_lanes=12, staging_bytes=32 << 30):
+    def __init__(self, level=7, verbose=False, coders=8, zstd_lanes=14, staging_bytes=24 << 30, device_bytes=None):
         self.level, self.verbose = level, verbose
         self.stream = dev.Stream()
         self.gq = GPUQuant(stream=self.stream.handle)
         self.io = ThreadPoolExecutor(8)          # file reads (pieces)
         self.hasher = ThreadPoolExecutor(8)      # file checksums
-        self.zpool = ThreadPoolExecutor(zstd_lanes)   # residual frames (one thread each, as the reference's)
+        self.zpool = ThreadPoolExecutor(zstd_lanes)   # stage 2 of a file: its residual frame (one thread each)
         self.reader = ThreadPoolExecutor(1)      # the next file read ahead
         self.coders = ThreadPoolExecutor(coders)
-        self.pool = _PinnedPool(staging_bytes)
-        self.fpool = _DevPool(3)                 # device copies of the files in flight
-        self.finisher = ThreadPoolExecutor(1)    # stage 2 of each file
+        self.pool = _PinnedPool(staging_bytes)   # page-locked: file reads
+        if device_bytes is None:                 # residuals wait in HBM for their zstd lane
+            free, total = dev.mem_info()
+            device_bytes = max(free - (48 << 30), 8 << 30)
+        self.fpool = _DevPool(device_bytes)
         self.tls = threading.local()
+        self.cpu, self.cpu_lock = collections.Counter(), threading.Lock()
         self.timing = []
         self.stats = collections.Counter()
         self.sizes = {}
 
     # ---------------------------------------------------------------- bases
-    def _load_base(self, i, name, path, piece=256 << 20):
-        """the base file uploaded whole, read through two page-locked pieces (the next piece is read
-        while the current one is copied); its bytes stay mapped for the header coder"""
+    def _load_base(self, path, piece=1 << 30):
+        """the base file uploaded whole into HBM, read through two page-locked pieces (the next piece is
+        read, on a thread of its own, while the current one is copied)"""
         size = os.path.getsize(path)
         d = dev.DeviceArray(size, np.uint8)
-        bufs = [dev.pinned(min(piece, max(size, 1))) for _ in range(2)]
-        offs = list(range(0, size, piece))
-        nxt = self.reader.submit(_read_into, path, bufs[0][:min(piece, size)], 0, self.io) if offs else None
-        for k, o in enumerate(offs):
-            n = min(piece, size - o)
-            nxt.result()
-            if k + 1 < len(offs):
-                o2 = offs[k + 1]
-                nxt = self.reader.submit(_read_into, path, bufs[(k + 1) % 2][:min(piece, size - o2)], o2, self.io)
-            check(lib().spa_memcpy_h2d(d.ptr + o, bufs[k % 2].ctypes.data, n, self.stream.handle))
-        host = np.memmap(path, np.uint8, "r") if size else np.zeros(0, np.uint8)
-        return host, _Base(i, name, host, d, gguf.GGUF(host))
+        bufs = [self.pool.acquire(min(piece, max(size, 1))) for _ in range(2)]
+        try:
+            with ThreadPoolExecutor(1) as rd:
+                offs = list(range(0, size, piece))
+                nxt = rd.submit(_read_into, path, bufs[0][:min(piece, size)], 0, self.io) if offs else None
+                for k, o in enumerate(offs):
+                    n = min(piece, size - o)
+                    nxt.result()
+                    if k + 1 < len(offs):
+                        o2 = offs[k + 1]
+                        nxt = rd.submit(_read_into, path, bufs[(k + 1) % 2][:min(piece, size - o2)], o2, self.io)
+                    check(lib().spa_memcpy_h2d(d.ptr + o, bufs[k % 2].ctypes.data, n, self.stream.handle))
+        finally:
+            for x in bufs:
+                self.pool.release(x)
+        return d
 
     def _code_base(self, b, host, order):
         """the base's chunk: pack({"r2": R2 chunk}) with the reference's part order, coded on its own
@@ -358,27 +418,46 @@ class Packer:
     def _qr_job(self, T, items, seed, imx):
         if not hasattr(self.tls, "stream"):
             self.tls.stream = dev.Stream()
+        c0 = time.thread_time()
         parts = qr.encode_parts(T, items, seed, imx, stream=self.tls.stream.handle)
-        return qr.frame(parts)
+        c1 = time.thread_time()
+        out = qr.frame(parts)
+        self._cpu(("qr batches", 1), ("qr coder cpu_s", c1 - c0), ("qr tables+lens zstd-19 cpu_s", time.thread_time() - c1))
+        return out
+
+    def _sha256(self, buf):
+        c0 = time.thread_time()
+        h = _ws(buf)
+        self._cpu(("sha256 cpu_s", time.thread_time() - c0))
+        return h
+
+    def _cpu(self, *items):
+        with self.cpu_lock:
+            for k, v in items:
+                self.cpu[k] += v
 
     # ---------------------------------------------------------------- one derived file
     def _read_file(self, job):
-        """(reader thread) the file's bytes into a page-locked buffer and its tensors' content hashes
-        (the keys of references); its checksum is computed from a read of its own"""
+        """(reader thread) the file's bytes into a page-locked buffer and its checksum started on them"""
+        t0 = time.perf_counter()
         size = os.path.getsize(job["path"])
         host = self.pool.acquire(size)[:size]
+        t1 = time.perf_counter()
         _read_into(job["path"], host, pool=self.io)
+        t2 = time.perf_counter()
+        self._cpu(("file reads wall_s", t2 - t1))
         job["host"] = host
-        job["thash"] = {t.name: xxhash.xxh3_128_digest(memoryview(host[t.offset:t.offset + t.nbytes]))
-                        for t, k in job["tens"] if k}
+        job["sha256"] = self.hasher.submit(self._sha256, host)
+        job["read"] = {"staging": round(t1 - t0, 3), "read": round(t2 - t1, 3)}
         return job
 
     def _device_file(self, job, b, imx_dev, imx_off, imx_map):
         """(device thread, stage 1) file job["fi"] against base b: uploaded, regrown and compared, its QR
         batches handed to the coders -> the state stage 2 finishes"""
         fi, host, tens = job["fi"], job["host"], job["tens"]
-        wins_of, wstate, thash = job["wins_of"], job["wstate"], job["thash"]
+        wins_of, wstate = job["wins_of"], job["wstate"]
         tm = {"t0": time.perf_counter()}
+        tm.update(job["read"])
         size = host.size
         pred = [(t, k) for t, k in tens if k]
         by_name = {t.name: t for t, _ in tens}
@@ -386,6 +465,9 @@ class Packer:
         st = self.stream.handle
         check(lib().spa_memcpy_h2d(F.ptr, host.ctypes.data, size, st))
         tm["upload"] = time.perf_counter()
+        # the predicted tensors' content keys, hashed on the device before anything changes them
+        thash = dict(zip([t.name for t, _ in pred],
+                         residual.content_hashes(F, [(t.offset, t.nbytes) for t, _ in pred], st)))
         # references: equal to a tensor an earlier file of the same window left a residual in
         refs, mine = {}, []
         for t, k in pred:
@@ -417,7 +499,7 @@ class Packer:
             ws["memo"][key] = bool(out[t.name]["nonzero"])
         # plan entries and QR batches, window by window, each window's QR tensors by type in order of
         # appearance (repo3.py:946-979)
-        plan, qmeta, qjobs = [], [], []
+        plan, qmeta, qjobs, qregs = [], [], [], []
         by_w = collections.defaultdict(list)
         for t, _ in pred:
             by_w[wins_of[t.name]].append(t)
@@ -441,74 +523,94 @@ class Packer:
                              for t in its]
                     self.stats["qr_grid"] += len(its) if grid else 0
                     qmeta.append([T, [t.name for t in its]])
+                    qregs.append([(t.offset, t.nbytes) for t in its])
                     qjobs.append(self.coders.submit(self._qr_job, T, items, b.d, imx_dev if grid else None))
         self.stats["qr"] += sum(len(m[1]) for m in qmeta)
-        qr_regions = [(t.offset, t.nbytes) for t, _ in mine if out[t.name]["qr"]]
-        # the bytes the residual's zstd level is judged from (the file's, in the QR tensors)
-        sample = self._zsample(host, pred, wins_of, qr_regions, job["last_window"])
         self.stream.synchronize()
-        self.pool.release(job.pop("host"))
+        # the staged bytes go back once the checksum has read them too
+        job["sha256"].add_done_callback(lambda _, h=job.pop("host"): self.pool.release(h))
         entry = {"name": job["name"], "size": size, "base": b.index, "plan": plan}
-        return {"fi": fi, "F": F, "qjobs": qjobs, "qmeta": qmeta, "qr_regions": qr_regions, "sample": sample,
-                "entry": entry, "zdict": b.header, "tm": tm}
+        return {"fi": fi, "F": F, "qjobs": qjobs, "qmeta": qmeta, "qregs": qregs,
+                "span": self._zspan(pred, wins_of, job["last_window"], size), "entry": entry, "zdict": b.header,
+                "tm": tm}
 
-    def _finish_file(self, state):
-        """(finisher thread, stage 2) the QR batches awaited, their tensors zeroed, the residual read back
-        and handed to a zstd lane -> (manifest entry, QR chunk or None, future of the residual frame)"""
+    def _lane(self):
+        """this zstd lane's stream, page-locked piece and device counter"""
         if not hasattr(self.tls, "stream"):
             self.tls.stream = dev.Stream()
-        st = self.tls.stream.handle
+            self.tls.piece = dev.pinned(self.PIECE)
+            self.tls.count = dev.DeviceArray(1, np.uint64)
+        return self.tls.stream, self.tls.piece, self.tls.count
+
+    PIECE = 64 << 20
+
+    def _finish_file(self, state):
+        """(a zstd lane, stage 2) the zstd level judged on the device, then the residual streamed out of
+        HBM into its zstd frame piece by piece, each piece once the QR batches whose tensors start in
+        it or before are coded and their tensors zeroed -> (manifest entry, QR chunk or None,
+        residual frame)"""
+        s, piece, count = self._lane()
+        st = s.handle
         F, size = state["F"], state["entry"]["size"]
-        qparts = [f.result() for f in state["qjobs"]]     # the coders read the QR tensors' file bytes
         tm = state["tm"]
-        tm["qr"] = time.perf_counter()
-        for off, nb in state["qr_regions"]:
-            check(lib().spa_memset(F.ptr + off, 0, nb, st))
-        resid = self.pool.acquire(size)[:size]
-        check(lib().spa_memcpy_d2h(resid.ctypes.data, F.ptr, size, st))
-        self.fpool.release(F)
-        tm["readback"] = time.perf_counter()
-        pos, in_qr, qr_vals, span = state["sample"]
-        v = resid[pos]                              # (fancy indexing: a copy)
-        v[in_qr] = qr_vals
-        sparse = np.count_nonzero(v) * 61 < SPARSE * span
-        prm = zstd.Params(max(self.level, 9) if sparse else self.level, window_log=25)
+        try:
+            # the level rule on the residual with the QR tensors still holding the file's bytes (the
+            # coders only read them)
+            start, span = state["span"]
+            check(lib().spa_count_every(F.ptr + start, span, 61, count.ptr, st))
+            nz = int(count.to_host(stream=st)[0])
+            sparse = nz * 61 < SPARSE * span
+            prm = zstd.Params(max(self.level, 9) if sparse else self.level, window_log=25)
+            z = zstd.Compressor(prm, state["zdict"], size=size)
+            qjobs, qregs = state["qjobs"], state["qregs"]
+            first = [min(o for o, _ in r) for r in qregs]
+            pending = sorted(range(len(qjobs)), key=lambda k: first[k])
+            qparts, pi, frame = [None] * len(qjobs), 0, []
+            c0, waited = time.thread_time(), 0.0
+            for o in range(0, size, self.PIECE):
+                m = min(self.PIECE, size - o)
+                while pi < len(pending) and first[pending[pi]] < o + m:
+                    k = pending[pi]
+                    w0 = time.perf_counter()
+                    qparts[k] = qjobs[k].result()
+                    waited += time.perf_counter() - w0
+                    for off, nb in qregs[k]:
+                        check(lib().spa_memset(F.ptr + off, 0, nb, st))
+                    pi += 1
+                check(lib().spa_memcpy_d2h(piece.ctypes.data, F.ptr + o, m, st))
+                frame.append(z.compress(piece[:m]))
+            frame.append(z.finish())
+            self._cpu(("residual zstd cpu_s", time.thread_time() - c0))
+            tm["qr wait"] = waited
+        finally:
+            futures_wait(state["qjobs"])          # (after an error too: no coder still reads F)
+            self.fpool.release(F)
+        tm["zstd"] = time.perf_counter()
         qchunk = None
         if state["qmeta"]:
             qchunk = pack_parts({"meta": zstd.compress(json.dumps(state["qmeta"]).encode(), 19),
                                  **{str(k): p for k, p in enumerate(qparts)}})
         t0 = tm.pop("t0")
         self.timing.append({"file": state["entry"]["name"], "level": prm.level,
-                            **{k: round(v - t0, 3) for k, v in tm.items()}})
-        return state["entry"], qchunk, self.zpool.submit(self._compress, resid, prm, state["zdict"])
-
-    def _compress(self, resid, prm, zdict):
-        """(zstd lanes) the residual's frame; its buffer back to the pool"""
-        try:
-            return zstd.compress_with(resid, prm, zdict)
-        finally:
-            self.pool.release(resid)
+                            **{k: (round(v, 3) if k in ("staging", "read", "qr wait") else round(v - t0, 3)) for k, v in tm.items()}})
+        return state["entry"], qchunk, b"".join(frame)
 
     @staticmethod
-    def _zsample(host, pred, wins_of, qr_regions, last_window):
-        """the bytes the zstd level is judged from: every 61st byte of the file's first span that holds a
-        predicted tensor, from that tensor on -> (positions, which of them lie in QR tensors, the file's
-        bytes there, the span's length)"""
+    def _zspan(pred, wins_of, last_window, size):
+        """the bytes the zstd level is judged from: the file's first span that holds a predicted tensor,
+        from that tensor on (the last window's span runs to the end of the file) -> (start, length)"""
         pred = [t for t, _ in pred]
         start = min(t.offset for t in pred)
         first_w = min(wins_of[t.name] for t in pred)
         end = max(t.offset + t.nbytes for t in pred if wins_of[t.name] == first_w)
         if first_w == last_window:
-            end = host.size                         # the last window's span runs to the end of the file
-        pos = np.arange(start, end, 61, dtype=np.int64)
-        in_qr = np.zeros(pos.size, bool)
-        for off, nb in qr_regions:
-            in_qr |= (pos >= off) & (pos < off + nb)
-        return pos, in_qr, host[pos[in_qr]], end - start
+            end = size
+        return start, end - start
 
     # ---------------------------------------------------------------- the repository
     def pack(self, inputs, output, tool=TOOL, created=None, force=False):
         t0 = time.perf_counter()
+        ru0 = resource.getrusage(resource.RUSAGE_SELF)
         phases = {}
 
         def phase(name):
@@ -518,14 +620,15 @@ class Packer:
             raise ValueError("nothing to archive")
         if os.path.exists(output) and not force:
             raise FileExistsError(output)
-        roles = {n: file_role(p) for n, p in files.items()}
+        heads = {n: gguf.header_of(p) for n, p in files.items() if p.lower().endswith(".gguf")}
+        roles = {n: file_role(p, heads.get(n)) for n, p in files.items()}
         bases = {n: p for n, p in files.items() if roles[n] == "base"}
         derived = {n: p for n, p in files.items() if roles[n] == "derived"}
         extras = {n: p for n, p in files.items() if roles[n] is None}
         if any(re.match(r"^.*-\d{5}-of-\d{5}\.gguf$", n) for n in bases):
             raise NotImplementedError("split GGUF models (joined bases) are not built")
-        base_names = [{t.name for t in gguf.tensors_of(p)} for p in bases.values()]
-        orphans = [n for n, p in derived.items() if not any({t.name for t in gguf.tensors_of(p)} & s for s in base_names)]
+        base_names = [{t.name for t in heads[n][1]} for n in bases]
+        orphans = [n for n in derived if not any({t.name for t in heads[n][1]} & s for s in base_names)]
         if orphans:
             raise NotImplementedError(f"quantized files without a base ({orphans[0]}): the seed codec is not built")
         total = sum(os.path.getsize(p) for p in files.values())
@@ -534,34 +637,28 @@ class Packer:
         try:
             # other files: the small ones in one lzma bundle, the big ones zstd'd one by one
             small = {n: p for n, p in extras.items() if os.path.getsize(p) <= BUNDLE_MAX}
+            # (coded on a side thread; the writer takes them in chunk order when they are ready)
+            aux = ThreadPoolExecutor(1)
             ex = {n: open(p, "rb").read() for n, p in small.items()}
             for n, data in ex.items():
                 hashes[n] = self.hasher.submit(_ws, data)
-            bundle = lzma.compress(pack(ex), preset=9)
-            w.put("extras", bundle)
-            self.sizes["other files"] = len(bundle)
+            later = {"other files": aux.submit(lambda: lzma.compress(pack(ex), preset=9))}
+            w.put_later("extras", later["other files"])
             big = {}
             for j, (n, p) in enumerate((n, p) for n, p in extras.items() if n not in small):
                 data = open(p, "rb").read()
                 hashes[n] = self.hasher.submit(_ws, data)
-                c = zstd.compress_with(data, zstd.Params(self.level, threads=8, ldm=True))
-                w.put(f"x{j}", c)
-                self.sizes[n] = len(c)
+                later[n] = aux.submit(zstd.compress_with, data, zstd.Params(self.level, threads=8, ldm=True))
+                w.put_later(f"x{j}", later[n])
                 big[n] = [f"x{j}", len(data)]
+            phase("other files")
             imx_name = next((n for n in ex if n.startswith("imatrix")), None)
             imx_all = imx_mod.load(ex[imx_name]) if imx_name else {}
-            # bases: read, uploaded, their checksums and codecs started (one stream each)
+            # bases: their headers now (the files' plans need them), their bytes uploaded below
             loaded = []
-            side = ThreadPoolExecutor(1)
-            base_jobs = []
             for i, (n, p) in enumerate(bases.items()):
-                hashes[n] = self.hasher.submit(file_sha256, p)
-                host, b = self._load_base(i, n, p)
-                loaded.append((host, b))
-                base_jobs.append(side.submit(self._code_base, b, host, "stream" if i == 0 else "parts"))
-            self.stream.synchronize()
-            phase("bases resident")
-            log(self.verbose, f"  {len(bases)} base(s) resident in HBM, {time.perf_counter() - t0:.1f} s")
+                host = np.memmap(p, np.uint8, "r") if os.path.getsize(p) else np.zeros(0, np.uint8)
+                loaded.append((host, _Base(i, n, host, None, gguf.GGUF(host))))
             # the repository's importance per tensor on the device (the grid QR types read it)
             imx_vecs = {k: np.asarray(v, np.float32) for k, v in imx_all.items()}
             flat = np.concatenate(list(imx_vecs.values())) if imx_vecs else np.zeros(1, np.float32)
@@ -576,7 +673,7 @@ class Packer:
             entries, chunks = [None] * len(names), {}
             per_base = collections.defaultdict(list)
             for fi, n in enumerate(names):
-                ts = gguf.tensors_of(derived[n])
+                ts = heads[n][1]
                 common = [len({t.name for t in ts} & s) for s in base_names]
                 best = [k for k, c in enumerate(common) if c == max(common)][0]
                 per_base[best].append((fi, n, ts))
@@ -618,18 +715,33 @@ class Packer:
                 prev |= keys
                 info[fi] = (os.path.getsize(j["path"]), keys, j["group"], pot)
             porder = process_order(info, None)
-            for fi in porder:
-                hashes[names[fi]] = self.hasher.submit(file_sha256, jobs[fi]["path"])
+            # the first file read while the bases are uploaded, their checksums and codecs started
+            # (one stream each)
+            ahead = self.reader.submit(self._read_file, jobs[porder[0]]) if porder else None
+            side = ThreadPoolExecutor(1)
+            base_jobs = []
+            for (host, b), (n, p) in zip(loaded, bases.items()):
+                hashes[n] = self.hasher.submit(file_sha256, p)
+                b.d = self._load_base(p)
+                base_jobs.append(side.submit(self._code_base, b, host, "stream" if b.index == 0 else "parts"))
+                later[n] = base_jobs[-1]
+            if base_jobs:
+                # chunk order of the reference: the first base (written while the files are coded),
+                # the files derived from the bases, then the other bases
+                w.put_later("b0", base_jobs[0])
+            self.stream.synchronize()
+            phase("bases resident")
+            log(self.verbose, f"  {len(bases)} base(s) resident in HBM, {time.perf_counter() - t0:.1f} s")
             # the pipeline: the next file read ahead, one file at a time on the device, the residual
             # frames on the zstd lanes
             zjobs = {}
-            ahead = self.reader.submit(self._read_file, jobs[porder[0]]) if porder else None
             for k, fi in enumerate(porder):
                 job = ahead.result()
                 ahead = self.reader.submit(self._read_file, jobs[porder[k + 1]]) if k + 1 < len(porder) else None
                 b = loaded[job["base"]][1]
+                hashes[names[fi]] = job["sha256"]
                 state = self._device_file(job, b, imx_dev, imx_off, imx_map)
-                zjobs[fi] = self.finisher.submit(self._finish_file, state)
+                zjobs[fi] = self.zpool.submit(self._finish_file, state)
                 log(self.verbose, f"  {state['entry']['name']}: {state['entry']['size']:,} B regrown and compared in "
                                   f"{state['tm']['regrow'] - state['tm']['t0']:.2f} s")
             phase("derived files on the device")
@@ -639,31 +751,24 @@ class Packer:
                 data = open(derived[n], "rb").read()
                 hashes[n] = self.hasher.submit(_ws, data)
                 entries[fi] = {"name": n, "size": len(data), "base": b.index, "plan": []}
-                done = Future()
-                done.set_result((entries[fi], None, self.zpool.submit(
-                    zstd.compress_with, data, zstd.Params(self.level, window_log=25, threads=4), b.header)))
-                zjobs[fi] = done
+                zjobs[fi] = self.zpool.submit(lambda e, d, h: (e, None, zstd.compress_with(
+                    d, zstd.Params(self.level, window_log=25, threads=4), h)), entries[fi], data, b.header)
                 order_done.append(fi)
-            coded = [j.result() for j in base_jobs]
-            side.shutdown()
-            phase("base coded")
-            # chunk order of the reference: the first base (written while it is coded), the files
-            # derived from the bases (streamed ones, then the others), then the other bases
-            if coded:
-                w.put("b0", coded[0])
             for fi in order_done:
-                entries[fi], qchunk, zf = zjobs[fi].result()
-                fchunk = zf.result()
+                entries[fi], qchunk, fchunk = zjobs[fi].result()
                 w.put(f"f{fi}", fchunk)
                 self.sizes[names[fi]] = len(fchunk)
                 if qchunk is not None:
                     w.put(f"q{fi}", qchunk)
                     self.sizes[names[fi] + " (QR)"] = nbytes(qchunk)
             phase("residual frames")
-            for i in range(1, len(coded)):
-                w.put(f"b{i}", coded[i])
-            for n, c in zip(bases, coded):
-                self.sizes[n] = nbytes(c)
+            for i in range(1, len(base_jobs)):
+                w.put_later(f"b{i}", base_jobs[i])
+            for n, f in later.items():
+                self.sizes[n] = nbytes(f.result())
+            side.shutdown()
+            aux.shutdown()
+            phase("bases and other files coded")
             manifest = {"method": METHOD, "bases": list(bases), "seeds": [], "files": entries,
                         "extras": {"bundle": list(ex), "single": big}}
             if self.stats["qr_grid"] or self.stats["ref"]:
@@ -678,12 +783,18 @@ class Packer:
         except BaseException:
             w.abort()
             raise
+        finally:
+            self.fpool.close()
         dt = time.perf_counter() - t0
+        ru1 = resource.getrusage(resource.RUSAGE_SELF)
+        cpu_s = ru1.ru_utime + ru1.ru_stime - ru0.ru_utime - ru0.ru_stime
         size = os.path.getsize(output)
         log(self.verbose, f"{output}: {total:,} B -> {size:,} B in {dt:.1f} s ({total / dt / 1e9:.2f} GB/s)")
         phase("closed")
         return {"input_bytes": total, "archive_bytes": size, "seconds": dt, "GB_s": total / dt / 1e9,
-                "stats": dict(self.stats), "phases": phases, "files": self.timing}
+                "stats": dict(self.stats), "phases": phases, "files": self.timing,
+                "cpu": {"process cpu_s": round(cpu_s, 1), **{k: round(v, 1) for k, v in self.cpu.items()}},
+                "residuals_in_hbm_peak": self.fpool.peak}
 
     @staticmethod
     def _kind(b, t, imx_all):
@@ -740,7 +851,9 @@ class Unpacker:
         self.gq = GPUQuant(stream=self.stream.handle)
         self.pool = _PinnedPool(staging_bytes)
         self.rbuf = _DevBuf()
-        self.io = ThreadPoolExecutor(8)           # checksums and writes
+        self.files = ThreadPoolExecutor(4)        # a finished file: checked and written
+        self.io = ThreadPoolExecutor(8)           # its write, in pieces
+        self.hasher = ThreadPoolExecutor(4)       # its checksum, beside the write
         self.ahead = ThreadPoolExecutor(1)        # the next file's residual decompressed ahead
 
     def run(self, archive, outdir=None, patterns=None):
@@ -762,25 +875,32 @@ class Unpacker:
                 if e[1] in ("ref", "dup") and e[2][0] not in sel:
                     sel.add(e[2][0])
                     todo.append(e[2][0])
-        last_use = {}
+        users = collections.defaultdict(set)      # (source file, tensor) -> the files copying it
         for i in sorted(sel):
             for e in mf[i]["plan"]:
                 if e[1] in ("ref", "dup"):
-                    last_use[tuple(e[2])] = max(last_use.get(tuple(e[2]), -1), i)
+                    users[tuple(e[2])].add(i)
         need_b = {i for i, n in enumerate(manifest["bases"]) if n in want} | \
                  {mf[i]["base"] for i in sel if mf[i]["base"] is not None}
         results, jobs = {}, []
 
         def check_write(name, buf, release=False):
+            """the file's checksum and its write side by side; a file that fails its checksum is
+            not left behind"""
             try:
-                ok = hashlib.sha256(memoryview(buf).cast("B")).hexdigest() == cat[name]["hash"] and \
-                    memoryview(buf).nbytes == cat[name]["size"]
-                if ok and outdir is not None:
+                mv = memoryview(buf).cast("B")
+                h = self.hasher.submit(_ws, mv)
+                path = None
+                if outdir is not None:
                     path = os.path.join(outdir, *name.split("/"))
                     os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
-                    with open(path + ".part", "wb") as f:
-                        f.write(memoryview(buf).cast("B"))
-                    os.replace(path + ".part", path)
+                    _write_file(path + ".part", mv, self.io)
+                ok = h.result() == cat[name]["hash"] and mv.nbytes == cat[name]["size"]
+                if path is not None:
+                    if ok:
+                        os.replace(path + ".part", path)
+                    else:
+                        os.remove(path + ".part")
                 results[name] = ok
                 return ok
             finally:
@@ -793,13 +913,13 @@ class Unpacker:
             ex = {k: bytes(v) for k, v in unpack(lzma.decompress(bytes(r.get("extras")))).items()}
             for n in exm["bundle"]:
                 if n in want:
-                    jobs.append(self.io.submit(check_write, n, ex[n]))
+                    jobs.append(self.files.submit(check_write, n, ex[n]))
         else:
             ex = {}
         for n, (c, size) in exm["single"].items():
             if n in want:
                 out = np.empty(size, np.uint8)
-                jobs.append(self.io.submit(check_write, n, zstd.decompress_into(r.get(c), out)))
+                jobs.append(self.files.submit(check_write, n, zstd.decompress_into(r.get(c), out)))
         imx_name = next((n for n in ex if n.startswith("imatrix")), None)
         imx_all = {k: np.asarray(v, np.float32) for k, v in (imx_mod.load(ex[imx_name]) if imx_name else {}).items()}
         flat = np.concatenate(list(imx_all.values())) if imx_all else np.zeros(1, np.float32)
@@ -823,11 +943,18 @@ class Unpacker:
             if name in want:
                 host = self.pool.acquire(d.nbytes)[:d.nbytes]
                 check(lib().spa_memcpy_d2h(host.ctypes.data, d.ptr, d.nbytes, self.stream.handle))
-                jobs.append(self.io.submit(check_write, name, host, True))
+                jobs.append(self.files.submit(check_write, name, host, True))
             log(self.verbose, f"  base {name}: decoded, {time.perf_counter() - t0:.1f} s")
         # quantized files, in archive order; tensors that later files copy are kept on the device
-        kept = {}
-        order = sorted(sel)
+        kept, done = {}, set()
+        # largest first, a file after the files it copies tensors from (so the checksum of a big
+        # file overlaps the rebuild of the smaller ones)
+        srcs = {i: {k[0] for k, us in users.items() if i in us} for i in sel}
+        order, todo = [], set(sel)
+        while todo:
+            i = max((i for i in todo if not srcs[i] & todo), key=lambda i: (mf[i]["size"], -i))
+            order.append(i)
+            todo.remove(i)
 
         def residual_of(i):
             m = mf[i]
@@ -842,9 +969,10 @@ class Unpacker:
             resid = nxt.result()
             nxt = self.ahead.submit(residual_of, order[k + 1]) if k + 1 < len(order) else None
             if m["plan"]:
-                self._rebuild(r, i, m, bases[m["base"]], resid, kept, last_use, imx_dev, imx_off, imx_map)
+                self._rebuild(r, i, m, bases[m["base"]], resid, kept, users, done, imx_dev, imx_off, imx_map)
+            done.add(i)
             if m["name"] in want:
-                jobs.append(self.io.submit(check_write, m["name"], resid, True))
+                jobs.append(self.files.submit(check_write, m["name"], resid, True))
             else:
                 self.pool.release(resid)
             log(self.verbose, f"  {m['name']}: {m['size']:,} B in {time.perf_counter() - tf:.2f} s")
@@ -857,7 +985,7 @@ class Unpacker:
                 "missing": [n for n in want if n not in results], "bytes": nbytes_, "seconds": dt,
                 "GB_s": nbytes_ / dt / 1e9}
 
-    def _rebuild(self, r, i, m, b, resid, kept, last_use, imx_dev, imx_off, imx_map):
+    def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map):
         """file i's bytes from its residual (in `resid`, rebuilt in place) on the device"""
         st = self.stream.handle
         size = m["size"]
@@ -897,10 +1025,10 @@ class Unpacker:
                 src = kept[tuple(e[2])]
                 t = tens[e[0]]
                 check(lib().spa_memcpy_d2d(R.ptr + t.offset, src.ptr, t.nbytes, st))
-        for key in [key for key, last in last_use.items() if last <= i and key in kept]:
+        for key in [key for key in kept if users[key] <= done | {i}]:
             del kept[key]
-        for (fi, name), last in last_use.items():
-            if fi == i and last > i:
+        for (fi, name), us in users.items():
+            if fi == i and not us <= done | {i}:
                 t = tens[name]
                 a = dev.DeviceArray(t.nbytes, np.uint8)
                 check(lib().spa_memcpy_d2d(a.ptr, R.ptr + t.offset, t.nbytes, st))

@@ -14,6 +14,7 @@ come back to the host, which makes the same decisions as the reference:
   * a QR-coded tensor keeps its file bytes and best prediction for the QR coder; an XOR tensor
     keeps file ^ prediction in place; an exact prediction leaves an all-zero XOR residual.
 """
+import collections
 import threading
 
 import numpy as np
@@ -111,6 +112,18 @@ def diff_count(a, b=None, stream=None):
     c = _Count()
     check(lib().spa_diff_count(a.ptr, None if b is None else b.ptr, a.nbytes, c.d.ptr, stream))
     return c.value(stream)
+
+
+def content_hashes(base, regions, stream=None):
+    """128-bit content hashes (spa_content_hash) of the byte regions [(offset, length)] of the device
+    array `base` -> [(h0, h1)]"""
+    if not regions:
+        return []
+    desc = dev.DeviceArray.from_host(np.array(regions, np.uint64).reshape(-1), stream)
+    out = dev.DeviceArray(2 * len(regions), np.uint64)
+    check(lib().spa_content_hash(base.ptr, desc.ptr, len(regions), out.ptr, stream))
+    h = out.to_host(stream=stream).reshape(-1, 2)
+    return [(int(a), int(b)) for a, b in h]
 
 
 def float_prediction(src, t_type, stream=None):
@@ -218,4 +231,40 @@ def residual_window(ts, gq=None, fitted_set=0, use_qr=True, stream=None):
     counts = cache[key]
     firsts = [_first(t, gq, fitted_set, use_qr, stream, counts.ptr + 8 * i) for i, t in enumerate(ts)]
     n = counts.to_host(stream=stream)[:len(ts)] if ts else []
-    return [dict(_NONE) if f is None else _decide(t, gq, *f, int(n[i]), stream) for i, (t, f) in enumerate(zip(ts, firsts))]
+    # the QR tensors' other candidates, all predicted and counted before one wait
+    tried = collections.defaultdict(list)
+    for i, (t, f) in enumerate(zip(ts, firsts)):
+        if f is not None and f[2] and n[i]:
+            tried[i] = [(v, predict(gq, t, v, stream)) for v in sorted(set(candidates(t.type, f[1])))]
+    slots = [(i, v, p) for i, vs in tried.items() for v, p in vs]
+    if slots:
+        if counts.size < len(slots):
+            counts = cache[key] = dev.DeviceArray(2 * len(slots), np.uint64)
+        for s_, (i, v, p) in enumerate(slots):
+            check(lib().spa_diff_count(ts[i].region.ptr, p.ptr, ts[i].region.nbytes, counts.ptr + 8 * s_, stream))
+        e = counts.to_host(stream=stream)[:len(slots)]
+        tried = collections.defaultdict(list)
+        for s_, (i, v, p) in enumerate(slots):
+            tried[i].append((v, p, int(e[s_])))
+    out = []
+    for i, (t, f) in enumerate(zip(ts, firsts)):
+        if f is None:
+            out.append(dict(_NONE))
+        elif f[2]:
+            out.append(_decide_qr(t, f[1], f[3], int(n[i]), tried.get(i, []), stream))
+        else:
+            out.append(_decide(t, gq, *f, int(n[i]), stream))
+    return out
+
+
+def _decide_qr(t, first, p0, n0, tried, stream):
+    """_decide for a QR tensor whose candidates' differing-byte counts are known: tried [(variant,
+    prediction, count)] in variant order"""
+    choice, best, best_p = first, n0, p0
+    for v, pv, e in tried:
+        if e < best:                              # the first of the fewest differing bytes wins
+            choice, best, best_p = v, e, pv
+    if not best:                                  # exact: the XOR residual, all zero
+        check(lib().spa_memset(t.region.ptr, 0, t.region.nbytes, stream))
+        return {"kind": "rq", "variant": choice, "nonzero": False, "qr": False, "prediction": None, "diff_bytes": 0}
+    return {"kind": "qr", "variant": choice, "nonzero": True, "qr": True, "prediction": best_p, "diff_bytes": best}

@@ -210,9 +210,15 @@ def test_pinned_pool_reuses_and_bounds(monkeypatch):
 
 
 def test_process_order_keeps_dependent_files_in_order():
-    # files 0 and 2 share a tensor key: 0 before 2; the rest largest first
+    # files 0 and 2 share a tensor key: 0 before 2; the rest largest first (0 with the priority of 2)
     files = {0: (5, {("a", 1)}, 0, {}), 1: (9, {("b", 1)}, 0, {}), 2: (7, {("a", 1)}, 0, {}), 3: (8, {("c", 2)}, 1, {})}
     assert repo.process_order(files, None) == [1, 3, 0, 2]
-    # a group whose potential references could exceed a window's budget keeps archive order
+    # a small file that a large one must wait for goes first
+    files[0] = (2, {("a", 1)}, 0, {})
+    files[2] = (10, {("a", 1)}, 0, {})
+    assert repo.process_order(files, None) == [0, 2, 1, 3]
+    # a group whose potential references could exceed a window's budget keeps archive order (0 and 1
+    # go as early as the largest file waiting for them)
+    files[0] = (5, {("a", 1)}, 0, {})
     files[2] = (7, {("a", 1)}, 0, {0: repo.REF_KEEP + 1})
-    assert repo.process_order(files, None) == [3, 0, 1, 2]
+    assert repo.process_order(files, None) == [0, 1, 3, 2]

@@ -64,6 +64,16 @@ def test_small_repo_extracts_byte_identical(small_repo, tmp_path):
     assert stats["stats"]["qr"] > 0 and stats["stats"]["requant_diff"] > 0
 
 
+def test_small_repo_pack_is_deterministic(small_repo, tmp_path):
+    """two packs of the same files with the same creation time give the same archive bytes (the
+    pipeline's threads and processing order do not show in the archive)"""
+    root, arc, sizes, stats = small_repo
+    a, b = str(tmp_path / "a.seedpack"), str(tmp_path / "b.seedpack")
+    repo.Packer(zstd_lanes=3, coders=1).pack([root], a, created="2026-01-01T00:00:00")
+    repo.Packer().pack([root], b, created="2026-01-01T00:00:00")
+    assert open(a, "rb").read() == open(b, "rb").read()
+
+
 def test_small_repo_archive_layout(small_repo):
     root, arc, sizes, stats = small_repo
     r = container.Reader(arc)
