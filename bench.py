@@ -77,6 +77,20 @@ def _profiled_traffic(kernel):
     return json.load(open(p))["bytes_per_launch"].get(kernel)
 
 
+PEAK_VALU_T = 78.6       # wave64 FP32 VALU lane-ops/s: 256 CUs x 4 SIMDs x 32 lanes x 2.4 GHz (= 157.3 TFLOP/s / 2)
+
+
+def _profiled_valu(kernel):
+    """VALU lane-ops per launch of a kernel on the embedding: SQ_INSTS_VALU x 64 from the rocprofv3
+    counter pass summarised in profiles/"""
+    p = os.path.join(ROOT, "profiles", "valu.json")
+    if not os.path.exists(p):
+        return None
+    d = json.load(open(p))
+    n = d["insts_valu_per_launch"].get(kernel)
+    return None if n is None else n * d["lane_ops_per_instruction"]
+
+
 def _cpu_model():
     try:
         for ln in open("/proc/cpuinfo"):
@@ -594,12 +608,23 @@ def main():
     dom_ms = per[dom] / a.steps
     ab = alg_bytes(t, w.size, w.shape[1], True)
     achieved = ab / (dom_ms / 1e3) / 1e9
-    traffic = _profiled_traffic(NAMES[t].replace("_", "")) if n == "token_embd" else None
-    roofline = {"bound": "hbm", "kernel": f"k_kquant<{NAMES[t]}> on {n} {w.shape[0]}x{w.shape[1]}",
-                "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 5), "traffic": traffic,
-                "algorithmic_bytes": ab, "avg_launch_ms": round(dom_ms, 4),
-                "note": "search-bound K-quant (VALU); HBM fraction reported as the contract asks"}
+    kname = NAMES[t].replace("_", "")
+    traffic = _profiled_traffic(kname) if n == "token_embd" else None
+    ops = _profiled_valu(kname) if n == "token_embd" else None
+    hbm = {"achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 5),
+           "algorithmic_bytes": ab}
+    kdesc = f"k_kquant<{NAMES[t]}> on {n} {w.shape[0]}x{w.shape[1]}"
+    if ops:
+        # the K-quant searches are VALU-bound: the roof is the VALU issue rate; HBM beside it
+        va = ops / (dom_ms / 1e3) / 1e12
+        roofline = {"bound": "valu", "kernel": kdesc, "achieved": round(va, 2), "peak": PEAK_VALU_T,
+                    "unit": "T lane-ops/s", "frac": round(va / PEAK_VALU_T, 4), "traffic": traffic,
+                    "valu_lane_ops_per_launch": ops, "avg_launch_ms": round(dom_ms, 4), "hbm": hbm,
+                    "note": "lane-ops = SQ_INSTS_VALU x 64 per launch (profiles/valu.json) over the live launch time; "
+                            "peak = 1024 SIMDs x 32 lanes x 2.4 GHz (a wave64 FP32 VALU instruction every 2 cycles)"}
+    else:
+        roofline = {"bound": "hbm", "kernel": kdesc, **hbm, "traffic": traffic, "avg_launch_ms": round(dom_ms, 4),
+                    "note": "no VALU count profiled for this launch: HBM fraction only"}
 
     # HBM-bound legacy types: configuration 1 tensor and the embedding, Q8_0 / Q4_0 without imatrix
     legacy = {}

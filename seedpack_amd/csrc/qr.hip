@@ -74,20 +74,41 @@ __global__ __launch_bounds__(256) void k_qr_hist(const uint8_t* __restrict__ F, 
     }
 }
 
+// The encoder's step x -> (x / f) * 2^PB + x % f + c without a division (Giesen's rans_byte
+// reciprocal form): for f >= 2 with s = ceil(log2 f), r = ceil(2^(31+s) / f) and
+// q = (x * r) >> (31 + s) equal floor(x / f) for every x < 2^31 (the error term x * (r - 2^(31+s)/f)
+// / 2^(31+s) stays below 2^-s <= 1/f); then x' = x + c + q * (2^PB - f). For f = 1, r = 2^32 - 1 gives
+// q = x - 1 and the bias 2^PB - 1 makes up the difference. The state before a step is below
+// ((RANS_L >> PB) << 8) * f <= 2^31.
+__device__ __forceinline__ uint32_t enc_rcp(uint32_t f) {
+    if (f < 2) return 0xffffffffu;
+    const uint32_t sh = 32 - __clz(f - 1);
+    return (uint32_t)(((1ull << (31 + sh)) + f - 1) / f);
+}
+
+__global__ __launch_bounds__(256) void k_qr_rcp(const int* __restrict__ remap, const uint16_t* __restrict__ freq,
+                                                uint32_t* __restrict__ rcp) {
+    const int tt = remap[blockIdx.x];
+    if (tt >= 0) rcp[tt * 256 + threadIdx.x] = enc_rcp(freq[tt * 256 + threadIdx.x]);
+}
+
 struct Enc {
     uint32_t x;
     uint8_t* ptr;
     const int* remap;
     const uint16_t* freq;
     const uint32_t* cum;
-    __device__ __forceinline__ void put_fc(uint32_t f, uint32_t c) {
+    const uint32_t* rcp;
+    __device__ __forceinline__ void put_fc(uint32_t f, uint32_t c, uint32_t r) {
         const uint32_t xm = ((RANS_L >> PB) << 8) * f;
         while (x >= xm) { *--ptr = (uint8_t)(x & 0xff); x >>= 8; }
-        x = ((x / f) << PB) + (x % f) + c;
+        const uint32_t sh = f < 2 ? 0u : 31u - __clz(f - 1);
+        const uint32_t q = __umulhi(x, r) >> sh;
+        x = x + c + (f < 2 ? PSCALE - 1 : 0u) + q * (PSCALE - f);
     }
     __device__ __forceinline__ void put(int tab, uint32_t sym) {
         const int tt = remap[tab];
-        put_fc(freq[tt * 256 + sym], cum[tt * 257 + sym]);
+        put_fc(freq[tt * 256 + sym], cum[tt * 257 + sym], rcp[tt * 256 + sym]);
     }
 };
 
@@ -176,6 +197,7 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
                                                const uint8_t* __restrict__ seed, const TM* __restrict__ tm,
                                                const SG* __restrict__ sg, int nseg, const int* __restrict__ remap,
                                                const uint16_t* __restrict__ freq, const uint32_t* __restrict__ cum,
+                                               const uint32_t* __restrict__ rcp,
                                                uint8_t* __restrict__ out, uint64_t cap, uint32_t* __restrict__ out_len,
                                                const uint8_t* __restrict__ neq, const uint32_t* __restrict__ idx_of,
                                                const uint16_t* __restrict__ nsym, const uint32_t* __restrict__ syms,
@@ -206,9 +228,10 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
     const uint8_t* sbase = seed + m.seed_off;
     uint8_t* const base = out + (uint64_t)s * cap;
     uint8_t* const end = base + cap;
-    Enc e{RANS_L, end, remap, freq, cum};
+    Enc e{RANS_L, end, remap, freq, cum, rcp};
     FlagTab ft;
     ft.load(remap, freq, cum);
+    ft.load_rcp(remap, rcp);
     auto put = [&](int tab, uint32_t sym, bool code) {
         e.put(tab, sym);
         return !(code && e.ptr - base < FIELD_ROOM<T>);
@@ -219,7 +242,7 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
         for (; i >= 0; --i) {
             const int prev = i > 0 ? (differs(i - 1) ? 0 : 1) : 1;
             if (differs(i)) { pend = true; break; }
-            e.put_fc(ft.freq_of(prev, 1), ft.cum_of(prev, 1));
+            e.put_fc(ft.freq_of(prev, 1), ft.cum_of(prev, 1), ft.rcp_of(prev, 1));
             if (e.ptr - base < 8) { out_len[s] = 0xffffffffu; return; }
         }
         if (__ballot(pend) == 0) break;
@@ -233,22 +256,24 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
             const uint32_t* q = syms + (size_t)k * MAXSYM<T>;
             const int n = nsym[k];
             for (int j0 = 0; j0 < n; j0 += 8) {
-                uint32_t fq[8], cq[8];
+                uint32_t fq[8], cq[8], rq[8];
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
                     fq[t] = 1u;
                     cq[t] = 0u;
+                    rq[t] = 0xffffffffu;
                     if (j0 + t < n) {
                         const uint32_t wd = q[j0 + t];
                         const int tt = remap[wd >> 8];
                         fq[t] = freq[tt * 256 + (wd & 255u)];
                         cq[t] = cum[tt * 257 + (wd & 255u)];
+                        rq[t] = rcp[tt * 256 + (wd & 255u)];
                     }
                 }
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
                     if (j0 + t >= n) break;
-                    e.put_fc(fq[t], cq[t]);
+                    e.put_fc(fq[t], cq[t], rq[t]);
                     if (j0 + t < Y::QK && e.ptr - base < FIELD_ROOM<T>) { out_len[s] = 0xffffffffu; return; }
                 }
             }
@@ -257,7 +282,7 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
             return;
         }
         const int prev = i > 0 ? (differs(i - 1) ? 0 : 1) : 1;
-        e.put_fc(ft.freq_of(prev, 0), ft.cum_of(prev, 0));
+        e.put_fc(ft.freq_of(prev, 0), ft.cum_of(prev, 0), ft.rcp_of(prev, 0));
         --i;
     }
     for (int j = 0; j < 4; ++j) { *--e.ptr = (uint8_t)(e.x & 0xff); e.x >>= 8; }
@@ -442,9 +467,10 @@ template <int T> struct Encode {
         hipLaunchKernelGGL(k_qr_syms<T>, dim3((unsigned)wgs), dim3(256), 0, st, (const uint8_t*)F, (const uint8_t*)P,
                            (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, (const uint32_t*)w.list,
                            (const uint32_t*)w.nlist, w.cap, w.nsym, w.syms, mv);
+        hipLaunchKernelGGL(k_qr_rcp, dim3(NTAB2), dim3(256), 0, st, remap, freq, w.rcp);
         hipLaunchKernelGGL(k_qr_enc<T>, dim3((unsigned)((nseg + 63) / 64)), dim3(64), 0, st, (const uint8_t*)F,
                            (const uint8_t*)P, (const uint8_t*)seed, (const TM*)tm, (const SG*)sg, nseg, remap, freq, cum,
-                           (uint8_t*)out, cap, out_len, (const uint8_t*)w.neq, (const uint32_t*)w.idx_of,
+                           (const uint32_t*)w.rcp, (uint8_t*)out, cap, out_len, (const uint8_t*)w.neq, (const uint32_t*)w.idx_of,
                            (const uint16_t*)w.nsym, (const uint32_t*)w.syms, mv);
         SPA_HIP_TRY(hipGetLastError());
         return 0;

@@ -39,12 +39,14 @@ struct QrWork {
     uint32_t* idx_of;
     uint16_t* nsym;
     uint32_t* syms;
+    uint32_t* rcp;                     // (non-grid) the encoder's reciprocal per (table, symbol)
     uint32_t cap;
 };
 __host__ __device__ inline int64_t qr_sym_cap(int64_t slots) { return slots / 16 > 1024 ? slots / 16 : 1024; }
 __host__ __device__ inline size_t qr_work_bytes(int64_t slots, int maxsym) {
     const size_t a = (size_t)((slots + 255) / 256 * 256), cap = (size_t)qr_sym_cap(slots);
-    return a + 256 + (size_t)slots * 8 + (cap * 2 + 255) / 256 * 256 + (maxsym ? cap * (size_t)maxsym * 4 : 0);
+    return a + 256 + (size_t)slots * 8 + (cap * 2 + 255) / 256 * 256 +
+           (maxsym ? cap * (size_t)maxsym * 4 + (size_t)NTAB2 * 256 * 4 : 0);
 }
 __host__ __device__ inline QrWork qr_work(void* w, int64_t slots, int maxsym) {
     uint8_t* p = (uint8_t*)w;
@@ -56,6 +58,7 @@ __host__ __device__ inline QrWork qr_work(void* w, int64_t slots, int maxsym) {
     q.idx_of = q.list + slots;
     q.nsym = (uint16_t*)(q.idx_of + slots);
     q.syms = maxsym ? (uint32_t*)((uint8_t*)q.nsym + (cap * 2 + 255) / 256 * 256) : nullptr;
+    q.rcp = maxsym ? q.syms + cap * (size_t)maxsym : nullptr;
     q.cap = maxsym ? (uint32_t)cap : 0;
     return q;
 }

@@ -58,6 +58,15 @@ struct FlagTab {
         return (uint32_t)(q >> (32 * p + 16 * v)) & 0xffffu;
     }
     __device__ __forceinline__ uint32_t cum_of(int p, int v) const { return v ? freq_of(p, 0) : 0u; }
+    // the encoder's reciprocals of the four flag frequencies (enc_rcp), held as (v = 0, v = 1) pairs
+    uint64_t r0, r1;
+    __device__ __forceinline__ void load_rcp(const int* remap, const uint32_t* rcp) {
+        r0 = r1 = 0;
+        const int t0 = remap[FLAG], t1 = remap[FLAG + 1];
+        if (t0 >= 0) r0 = rcp[t0 * 256] | ((uint64_t)rcp[t0 * 256 + 1] << 32);
+        if (t1 >= 0) r1 = rcp[t1 * 256] | ((uint64_t)rcp[t1 * 256 + 1] << 32);
+    }
+    __device__ __forceinline__ uint32_t rcp_of(int p, int v) const { return (uint32_t)((p ? r1 : r0) >> (32 * v)); }
     // one flag decoded from state x in context p: symbol 1's slots start at freq(p, 0), symbol 0's at 0
     // (a valid stream's slot is in one of the two ranges); renormalised from ptr as the general step
     __device__ __forceinline__ int get(uint32_t& x, const uint8_t*& ptr, const uint8_t* end, int p) const {

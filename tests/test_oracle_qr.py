@@ -80,3 +80,31 @@ def test_rans_round_trip_textbook():
             x = (x << 8) | data[p]; p += 1
         assert oqr.RANS_L <= x < oqr.RANS_L << 8
     assert p == len(data) and x == oqr.RANS_L
+
+
+def test_encoder_reciprocal_step_equals_division():
+    """the device encoder's division-free step (qr.hip enc_rcp / Enc::put_fc): for every frequency
+    1..4096 and states 1 .. ((RANS_L >> PB) << 8) * f - 1 (the bound renormalisation leaves), with 32-bit
+    wrap-around, it equals (x // f) * 2^PB + x % f + c"""
+    M, L = 1 << 12, 1 << 23
+    g = np.random.default_rng(11)
+
+    def rcp(f):
+        if f < 2:
+            return 0xFFFFFFFF
+        sh = (f - 1).bit_length()
+        return ((1 << (31 + sh)) + f - 1) // f
+
+    def step(x, f, c):
+        sh = 0 if f < 2 else 31 - (32 - (f - 1).bit_length())
+        q = ((x * rcp(f)) >> 32) >> sh
+        return (x + c + (M - 1 if f < 2 else 0) + q * (M - f)) & 0xFFFFFFFF
+
+    for f in range(1, M + 1):
+        xm = ((L >> 12) << 8) * f                # the state after renormalisation is below this
+        xs = [1, 2, f, f + 1, xm - 1, xm - 2, xm - f, xm - f - 1] + [int(v) for v in g.integers(1, xm, 24)]
+        xs += [k * f + r for k in (1, xm // f - 1) for r in (0, f - 1)]
+        c = int(g.integers(0, M - f + 1))
+        for x in xs:
+            if 1 <= x < xm:
+                assert step(x, f, c) == ((x // f) << 12) + x % f + c, (f, x)
