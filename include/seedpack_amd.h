@@ -200,6 +200,44 @@ int spa_content_hash(const void* base, const uint64_t* desc, int nregions, unsig
  * >> 16). Replaces _float_dev (repo3.py:673-689). */
 int spa_float_pred(const void* src, int src_kind, int64_t n, int dst_type, void* dst, void* stream);
 
+/* ---- deterministic arithmetic (replaces detmath.py's kernels dm_rows / dm_rows_d / dm_cols / dm_gram /
+ * dm_bdot / dm_solve / dm_log2 / dm_exp2, detmath.py:60-259): float64 sums term by term in index order,
+ * products of floats exact in float64, nothing contracted. All launch on `stream` and return. */
+
+/* out[r] = sum_j x[r][j] (sq: x[r][j]^2) over the nr x nc row-major array x (f64 = 0: float32, 1:
+ * float64). detmath.rows (detmath.py:185-192). */
+int spa_dm_rows(const void* x, int f64, int64_t nr, int64_t nc, int sq, double* out, void* stream);
+/* out[c] = sum_r x[r][c] (sq: squares) over the rows r with mask[r] != 0 (mask NULL: all).
+ * detmath.cols (detmath.py:195-202). */
+int spa_dm_cols(const float* x, int64_t nr, int64_t nc, int sq, const uint8_t* mask, double* out, void* stream);
+/* X: n x k x d float32 (k <= 32) -> out[c] = X[c] X[c]^T (n x k x k float32 of float64 sums).
+ * detmath.gram (detmath.py:210-216). */
+int spa_dm_gram(const float* X, int64_t n, int k, int64_t d, float* out, void* stream);
+/* X: n x k x d, y: n x d (k <= 32) -> out[c] = X[c] y[c] (n x k). detmath.bdot (detmath.py:219-225). */
+int spa_dm_bdot(const float* X, const float* y, int64_t n, int k, int64_t d, float* out, void* stream);
+/* n systems A[c] x = b[c] (k <= 16), Gaussian elimination with partial pivoting in float64.
+ * detmath.solve (detmath.py:228-235). */
+int spa_dm_solve(const float* A, const float* b, int64_t n, int k, float* x, void* stream);
+/* float64 log2 / exp2 elementwise (detmath.py:20-58, :171-182). */
+int spa_dm_log2(const double* x, int64_t n, double* y, void* stream);
+int spa_dm_exp2(const double* x, int64_t n, double* y, void* stream);
+
+/* ---- estimating what a quant was made from ---- */
+
+/* The importance fit's conditions of rows X (R x cols float32) quantized as F (type T = Q4_0, Q4_1,
+ * Q5_0 or Q5_1; V its dequantized values, rowsq detmath's row sums of squares of X): per weight
+ * sqrt(rowsq/cols + x^2) (x - v) l, with l the weight's code (Q4_1 / Q5_1 also times [min != 0]),
+ * normalised per block, written as (block of columns, position, row) float32 into e1 (and e2).
+ * Replaces the body of imxfit.ls_gram before its Gram sums (imxfit.py:37-58). */
+int spa_imx_conditions(int T, const float* X, const void* F, const float* V, const double* rowsq, int64_t R, int64_t cols,
+                       float* e1, float* e2, void* stream);
+/* The sibling estimate (siblings.py:51-77 half_step / est_add / est_seed): half the interval of a
+ * weight's code from its bounds (-1: none); the running precision-weighted sums; the explicit seed
+ * (x, h) per weight, or (x0, 0) where no version told anything. */
+int spa_est_half_step(const float* x, const float* lo, const float* hi, int64_t n, float* h, void* stream);
+int spa_est_add(const float* x, const float* h, int64_t n, float* ws, float* wx, void* stream);
+int spa_est_seed(const float* ws, const float* wx, const float* x0, int64_t n, float* out, void* stream);
+
 /* ---- R2 BF16 base codec (replaces the kernels and statistics of bf16v2.py:24-155, :225-271) ----
  * TB descriptors are 32 bytes {i64 doff, i32 rowlen, rowbase, colbase, tab, rmap, pad} and SG 16 bytes
  * {i32 t, n, i64 i0}, the layout of bf16v2.py:157-158 TB_DT / SG_DT; segments of 16384 weights.

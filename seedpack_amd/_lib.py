@@ -68,6 +68,18 @@ SIGNATURES = {
     "spa_xor3": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_diff_count": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_count_every": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "spa_dm_rows": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int, c_void_p, c_void_p]),
+    "spa_dm_cols": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p]),
+    "spa_dm_gram": (c_int, [c_void_p, c_int64, c_int, c_int64, c_void_p, c_void_p]),
+    "spa_dm_bdot": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int64, c_void_p, c_void_p]),
+    "spa_dm_solve": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p]),
+    "spa_dm_log2": (c_int, [c_void_p, c_int64, c_void_p, c_void_p]),
+    "spa_dm_exp2": (c_int, [c_void_p, c_int64, c_void_p, c_void_p]),
+    "spa_imx_conditions": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
+                                   c_void_p]),
+    "spa_est_half_step": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "spa_est_add": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
+    "spa_est_seed": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "spa_content_hash": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "spa_float_pred": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p]),
     "spa_r2_stats": (c_int, [c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p,
