@@ -158,6 +158,27 @@ int spa_qr_encode_noalloc(int ggml_type, const void* F, const void* P, const voi
                           void* stream);
 size_t spa_qr_noalloc_scratch_bytes(void);
 
+/* ---- per-weight side information of the seed-less and sibling coders (qr.py:811-878) ----
+ * seed types of the TM records besides 0 / 1 / 30 (float seeds) and the non-grid QR types (a
+ * quantized seed, dequantized per weight with half its code step as the uncertainty): 98 = no seed,
+ * the seed buffer holds the tensor's per-column RMS (float32) and the codes are coded against zero;
+ * 99 = explicit, the seed buffer holds float32 (value, uncertainty) pairs per weight. */
+
+/* lo/hi[i] = the interval of values that rounds to weight i's code in blocks F of non-grid type T
+ * (qr.intervals, qr.py:819-844). */
+int spa_qr_intervals(int T, const void* F, int64_t nw, float* lo, float* hi, void* stream);
+/* h[i] = half the step between the grid levels around weight i of grid-type blocks F (qr.explicit_seed's
+ * grid_h, qr.py:811-817). */
+int spa_qr_grid_h(int T, const void* F, int64_t nw, float* h, void* stream);
+/* out[i] = 1 where weight i's code and its sub-block's integer scale (and min) are the same in F and P
+ * (qr.weight_equal, qr.py:846-863). */
+int spa_qr_weight_equal(int T, const void* F, const void* P, int64_t nw, uint8_t* out, void* stream);
+/* the scale fields of every block (spa_qr_nfields(T) ints per block) and blocks made of given fields with
+ * zero codes (qr.self_side's block_fields / blocks_from_fields, qr.py:865-878). */
+int spa_qr_block_fields(int T, const void* F, int64_t nblk, int* out, void* stream);
+int spa_qr_blocks_from_fields(int T, const int* v, int n, void* out, void* stream);
+int spa_qr_nfields(int T);
+
 /* Compacts the segment slots into one stream: dst[off[s] ..] = the last len[s] bytes of slot s.
  * Replaces gather (qr.py:880-887, gpu2.py:264-271). */
 int spa_qr_gather(const void* src, uint64_t cap, const uint32_t* len, const uint64_t* off, int nseg, void* dst,

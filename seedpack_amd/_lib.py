@@ -68,6 +68,12 @@ SIGNATURES = {
     "spa_xor3": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_diff_count": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_count_every": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "spa_qr_intervals": (c_int, [c_int, c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
+    "spa_qr_grid_h": (c_int, [c_int, c_void_p, c_int64, c_void_p, c_void_p]),
+    "spa_qr_weight_equal": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "spa_qr_block_fields": (c_int, [c_int, c_void_p, c_int64, c_void_p, c_void_p]),
+    "spa_qr_blocks_from_fields": (c_int, [c_int, c_void_p, c_int, c_void_p, c_void_p]),
+    "spa_qr_nfields": (c_int, [c_int]),
     "spa_dm_rows": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "spa_dm_cols": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p, c_void_p]),
     "spa_dm_gram": (c_int, [c_void_p, c_int64, c_int, c_int64, c_void_p, c_void_p]),

@@ -66,9 +66,9 @@ __global__ __launch_bounds__(256) void k_qr_hist(const uint8_t* __restrict__ F, 
         for (int w = 0; w < Y::QK; ++w) {
             if (w % Y::SUBLEN == 0) wscale<T>(fb, w, a, c);
             float x, h;
-            seed_val(m.seed_type, sbase, gw0 + w, x, h);
+            seed_val(m.seed_type, sbase, gw0 + w, m.cols, x, h);
             int r, sg_, ctx;
-            predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
+            predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), hboff_of(m), r, sg_, ctx);
             hadd(counts, (uint32_t)(ctx * 256 + ((sg_ * (get_code<T>(fb, w) - r)) & 255)));
         }
     }
@@ -132,9 +132,9 @@ __device__ __forceinline__ bool block_syms(Put&& put, const uint8_t* fb, const u
     for (int w = Y::QK - 1; w >= 0; --w) {
         if (w / Y::SUBLEN != sub) { sub = w / Y::SUBLEN; wscale<T>(fb, w, a, c); }
         float x, h;
-        seed_val(m.seed_type, sbase, gw0 + w, x, h);
+        seed_val(m.seed_type, sbase, gw0 + w, m.cols, x, h);
         int r, sg_, ctx;
-        predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), r, sg_, ctx);
+        predict<T>(a, c, pb, w, x, h, mv, pos8(col0 + w, m.cols), hboff_of(m), r, sg_, ctx);
         if (!put(ctx, (uint32_t)((sg_ * (get_code<T>(fb, w) - r)) & 255), true)) return false;
     }
     int tv[Y::NF], dl[Y::NF], anyk[Y::NF];
@@ -385,9 +385,9 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 float x, h;
-                seed_val(m.seed_type, sbase, gw0 + w0 + t, x, h);
+                seed_val(m.seed_type, sbase, gw0 + w0 + t, m.cols, x, h);
                 int ctx;
-                predict<T>(a, c, pb, w0 + t, x, h, mv, pos8(col0 + w0 + t, m.cols), r8[t], sg8[t], ctx);
+                predict<T>(a, c, pb, w0 + t, x, h, mv, pos8(col0 + w0 + t, m.cols), hboff_of(m), r8[t], sg8[t], ctx);
                 tt8[t] = remap[ctx];
             }
 #pragma unroll
@@ -495,6 +495,121 @@ template <int T> struct MaxSym {
 
 bool grid_type(int T) { return T == 16 || T == 17 || T == 18 || T == 19 || T == 21 || T == 22 || T == 29; }
 
+// ---- per-weight side kernels of the seed-less and sibling coders (qr.py:811-878)
+
+// the interval of original values that rounds to each weight's code (one infinite side at the end of
+// the code range; both for a zero scale)
+template <int T>
+__global__ __launch_bounds__(256) void k_intervals(const uint8_t* __restrict__ F, int64_t nw, float* __restrict__ lo,
+                                                   float* __restrict__ hi) {
+    using Y = Ty<T>;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nw) return;
+    const uint8_t* b = F + (i / Y::QK) * Y::BS;
+    const int w = (int)(i % Y::QK), q = get_code<T>(b, w);
+    float a, c;
+    wscale<T>(b, w, a, c);
+    float l, h;
+    if constexpr (NONLIN<T>) {
+        l = q > 0 ? a * (0.5f * (KV[q - 1] + KV[q])) : -INFINITY;
+        h = q < 15 ? a * (0.5f * (KV[q] + KV[q + 1])) : INFINITY;
+        if (a < 0.f) { const float t = l; l = q < 15 ? h : -INFINITY; h = q > 0 ? t : INFINITY; }
+        if (a == 0.f) { l = -INFINITY; h = INFINITY; }
+    } else {
+        const float v = a * (float)q + c, e = fabsf(a) * 0.5f;
+        l = v - e;
+        h = v + e;
+        const bool lowend = q == Y::QMIN, highend = q == Y::QMAX;
+        if (a > 0.f) { if (lowend) l = -INFINITY; if (highend) h = INFINITY; }
+        else if (a < 0.f) { if (highend) l = -INFINITY; if (lowend) h = INFINITY; }
+        else { l = -INFINITY; h = INFINITY; }
+    }
+    lo[i] = l;
+    hi[i] = h;
+}
+
+// 1 where a weight's code and its sub-block's integer scale (and min) equal the other block's
+template <int T>
+__global__ __launch_bounds__(256) void k_weq(const uint8_t* __restrict__ F, const uint8_t* __restrict__ P, int64_t nw,
+                                             uint8_t* __restrict__ out) {
+    using Y = Ty<T>;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nw) return;
+    const uint8_t* f = F + (i / Y::QK) * Y::BS;
+    const uint8_t* p = P + (i / Y::QK) * Y::BS;
+    const int w = (int)(i % Y::QK);
+    bool eq = get_code<T>(f, w) == get_code<T>(p, w);
+    const int sub = w / Y::SUBLEN;
+    if constexpr (T == 10) eq = eq && f[sub] == p[sub];
+    if constexpr (T == 11) eq = eq && q3k_scale(f + 96, sub) == q3k_scale(p + 96, sub);
+    if constexpr (T == 12 || T == 13) {
+        int s1, m1, s2, m2;
+        k4_scale_min(sub, f + 4, s1, m1);
+        k4_scale_min(sub, p + 4, s2, m2);
+        eq = eq && s1 == s2 && m1 == m2;
+    }
+    if constexpr (T == 14) eq = eq && f[192 + sub] == p[192 + sub];
+    if constexpr (T == 23) eq = eq && get_field<T>(f, 1 + sub) == get_field<T>(p, 1 + sub);
+    out[i] = (uint8_t)eq;
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void k_block_fields(const uint8_t* __restrict__ F, int64_t nblk, int* __restrict__ out) {
+    using Y = Ty<T>;
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+#pragma unroll
+    for (int k = 0; k < Y::NF; ++k) out[b * Y::NF + k] = get_field<T>(F + b * Y::BS, k);
+}
+
+// blocks with the given field values and zero codes
+template <int T>
+__global__ __launch_bounds__(256) void k_blocks_from_fields(const int* __restrict__ v, int n, uint8_t* __restrict__ out) {
+    using Y = Ty<T>;
+    const int k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= n) return;
+    uint8_t o[Y::BS];
+#pragma unroll
+    for (int i = 0; i < Y::BS; ++i) o[i] = 0;
+    int f[Y::NF];
+#pragma unroll
+    for (int j = 0; j < Y::NF; ++j) f[j] = v[(int64_t)k * Y::NF + j];
+    set_fields<T>(o, f);
+#pragma unroll
+    for (int i = 0; i < Y::BS; ++i) out[(int64_t)k * Y::BS + i] = o[i];
+}
+
+unsigned wgs_for(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+template <int T> struct Intervals {
+    static int run(const void* F, int64_t nw, float* lo, float* hi, hipStream_t st) {
+        hipLaunchKernelGGL(k_intervals<T>, dim3(wgs_for(nw)), dim3(256), 0, st, (const uint8_t*)F, nw, lo, hi);
+        SPA_HIP_TRY(hipGetLastError());
+        return 0;
+    }
+};
+template <int T> struct Weq {
+    static int run(const void* F, const void* P, int64_t nw, uint8_t* out, hipStream_t st) {
+        hipLaunchKernelGGL(k_weq<T>, dim3(wgs_for(nw)), dim3(256), 0, st, (const uint8_t*)F, (const uint8_t*)P, nw, out);
+        SPA_HIP_TRY(hipGetLastError());
+        return 0;
+    }
+};
+template <int T> struct Fields {
+    static int run(const void* F, int64_t nblk, int* out, hipStream_t st) {
+        hipLaunchKernelGGL(k_block_fields<T>, dim3(wgs_for(nblk)), dim3(256), 0, st, (const uint8_t*)F, nblk, out);
+        SPA_HIP_TRY(hipGetLastError());
+        return 0;
+    }
+};
+template <int T> struct FromFields {
+    static int run(const int* v, int n, void* out, hipStream_t st) {
+        hipLaunchKernelGGL(k_blocks_from_fields<T>, dim3(wgs_for(n)), dim3(256), 0, st, v, n, (uint8_t*)out);
+        SPA_HIP_TRY(hipGetLastError());
+        return 0;
+    }
+};
+
 int check_common(int T, int nseg, int mv, const void* gk) {
     if (nseg < 0) return fail(SPA_ERR_ARG, "QR: negative segment count");
     if (mv != 1 && mv != 2) return fail(SPA_ERR_ARG, "QR: unknown model %d", mv);
@@ -513,6 +628,7 @@ int grid_encode(int T, const void* F, const void* P, const void* seed, const voi
 int grid_decode(int T, const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
                 int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F,
                 const uint16_t* gk, const float* imx, int mv, hipStream_t st);
+int grid_half_steps(int T, const void* F, int64_t nw, float* h, hipStream_t st);
 
 }  // namespace qr
 }  // namespace spa
@@ -549,6 +665,53 @@ int scratch_on_device(void** out) {
 }  // namespace
 
 extern "C" {
+
+int spa_qr_grid_h(int T, const void* F, int64_t nw, float* h, void* stream) {
+    if (nw < 0) return spa::fail(SPA_ERR_ARG, "spa_qr_grid_h: negative count");
+    if (!nw) return 0;
+    if (!F || !h) return spa::fail(SPA_ERR_ARG, "spa_qr_grid_h: null pointer");
+    return grid_half_steps(T, F, nw, h, (hipStream_t)stream);
+}
+
+int spa_qr_intervals(int T, const void* F, int64_t nw, float* lo, float* hi, void* stream) {
+    if (nw < 0) return spa::fail(SPA_ERR_ARG, "spa_qr_intervals: negative count");
+    if (!nw) return 0;
+    if (!F || !lo || !hi) return spa::fail(SPA_ERR_ARG, "spa_qr_intervals: null pointer");
+    return dispatch<Intervals>(T, F, nw, lo, hi, (hipStream_t)stream);
+}
+
+int spa_qr_weight_equal(int T, const void* F, const void* P, int64_t nw, uint8_t* out, void* stream) {
+    if (nw < 0) return spa::fail(SPA_ERR_ARG, "spa_qr_weight_equal: negative count");
+    if (!nw) return 0;
+    if (!F || !P || !out) return spa::fail(SPA_ERR_ARG, "spa_qr_weight_equal: null pointer");
+    return dispatch<Weq>(T, F, P, nw, out, (hipStream_t)stream);
+}
+
+int spa_qr_block_fields(int T, const void* F, int64_t nblk, int* out, void* stream) {
+    if (nblk < 0) return spa::fail(SPA_ERR_ARG, "spa_qr_block_fields: negative count");
+    if (!nblk) return 0;
+    if (!F || !out) return spa::fail(SPA_ERR_ARG, "spa_qr_block_fields: null pointer");
+    return dispatch<Fields>(T, F, nblk, out, (hipStream_t)stream);
+}
+
+int spa_qr_blocks_from_fields(int T, const int* v, int n, void* out, void* stream) {
+    if (n < 0) return spa::fail(SPA_ERR_ARG, "spa_qr_blocks_from_fields: negative count");
+    if (!n) return 0;
+    if (!v || !out) return spa::fail(SPA_ERR_ARG, "spa_qr_blocks_from_fields: null pointer");
+    return dispatch<FromFields>(T, v, n, out, (hipStream_t)stream);
+}
+
+int spa_qr_nfields(int T) {
+    switch (T) {
+        case 2: case 6: case 8: case 20: case 42: return 1;
+        case 3: case 7: return 2;
+        case 10: return 34;
+        case 11: case 14: case 17: case 22: case 29: return 17;
+        case 12: case 13: return 18;
+        case 23: case 16: case 18: case 19: case 21: return 9;
+    }
+    return 0;
+}
 
 int spa_qr_seg_blocks(int T) {
     switch (T) {

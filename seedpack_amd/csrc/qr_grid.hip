@@ -151,7 +151,7 @@ __device__ __forceinline__ float stage_block(const BlockSeed& bs, int lane, int 
     for (int k = 0; k < 4; ++k) {
         const int i = lane + 64 * k;
         float x, h;
-        seed_val(st, sbase, gw0 + i, x, h);
+        seed_val(st, sbase, gw0 + i, cols, x, h);
         bs.x[i] = x;
         if (im) bs.im[i] = im[(gw0 + i) % cols];
     }
@@ -715,6 +715,29 @@ template <int T> struct GDec {
 };
 
 }  // namespace
+
+namespace {
+// per weight of grid-type blocks: half the step between the grid's levels around it (qr.py:811-817)
+template <int T>
+__global__ __launch_bounds__(256) void k_grid_h(const uint8_t* __restrict__ F, int64_t nw, float* __restrict__ h) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nw) return;
+    float s, dl;
+    gscale<T>(F + (i / 256) * Ty<T>::BS, (int)(i % 256) / 8, s, dl);
+    h[i] = (T == 19 || T == 29) ? 0.5f * fabsf(s) : fabsf(s);
+}
+template <int T> struct GridH {
+    static int run(const void* F, int64_t nw, float* h, hipStream_t st) {
+        hipLaunchKernelGGL(k_grid_h<T>, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, st, (const uint8_t*)F, nw, h);
+        SPA_HIP_TRY(hipGetLastError());
+        return 0;
+    }
+};
+}  // namespace
+
+int grid_half_steps(int T, const void* F, int64_t nw, float* h, hipStream_t st) {
+    return dispatch_grid<GridH>(T, F, nw, h, st);
+}
 
 int grid_hist(int T, const void* F, const void* P, const void* seed, const void* tm, const void* sg, int nseg, uint32_t* counts,
               const uint16_t* gk, const float* imx, int mv, void* work, hipStream_t st) {

@@ -399,12 +399,61 @@ __device__ __forceinline__ void wscale(const uint8_t* b, int w, float& a, float&
     }
 }
 
-// seed value of global weight gw and its half uncertainty, for float seeds: F32 (0), F16 (1), BF16 (30)
-__device__ __forceinline__ void seed_val(int st, const uint8_t* sb, int64_t gw, float& x, float& h) {
+// seed types besides the float ones: no seed (the tensor's per-column RMS is the uncertainty, the
+// value 0), and an explicit (value, uncertainty) pair of float32 per weight
+constexpr int SEED_COLRMS = 98, SEED_EXPLICIT = 99;
+// the uncertainty context's offset: 8, or 3 when the seed is only the column RMS
+constexpr int HBOFF = 8, HBOFF_COL = 3;
+
+// a quantized seed's value of weight w of its block and half its code's step
+template <int S>
+__device__ __forceinline__ void quant_seed(const uint8_t* blk, int w, float& x, float& h) {
+    float a, c;
+    wscale<S>(blk, w, a, c);
+    const int q = get_code<S>(blk, w);
+    if constexpr (NONLIN<S>) {
+        x = a * KV[q];
+        const float g = q < 15 ? KV[q + 1] - KV[q] : KV[15] - KV[14];
+        h = fabsf(a) * (0.5f * g);
+    } else {
+        x = a * (float)q + c;
+        h = fabsf(a) * 0.5f;
+    }
+}
+template <int S>
+__device__ __forceinline__ void quant_seed_at(const uint8_t* sb, int64_t gw, float& x, float& h) {
+    quant_seed<S>(sb + (gw / Ty<S>::QK) * Ty<S>::BS, (int)(gw % Ty<S>::QK), x, h);
+}
+
+// seed value of global weight gw and its half uncertainty (qr.py seed_val): F32 (0), F16 (1), BF16 (30),
+// a quantized tensor of a QR type without a grid, the column RMS (98), an explicit pair (99)
+__device__ __forceinline__ void seed_val_any(int st, const uint8_t* sb, int64_t gw, int cols, float& x, float& h) {
+    h = 0.f;
+    switch (st) {
+        case SEED_COLRMS: x = 0.f; h = reinterpret_cast<const float*>(sb)[gw % cols]; return;
+        case SEED_EXPLICIT: x = reinterpret_cast<const float*>(sb)[2 * gw]; h = reinterpret_cast<const float*>(sb)[2 * gw + 1]; return;
+        case 2: quant_seed_at<2>(sb, gw, x, h); return;
+        case 3: quant_seed_at<3>(sb, gw, x, h); return;
+        case 6: quant_seed_at<6>(sb, gw, x, h); return;
+        case 7: quant_seed_at<7>(sb, gw, x, h); return;
+        case 8: quant_seed_at<8>(sb, gw, x, h); return;
+        case 10: quant_seed_at<10>(sb, gw, x, h); return;
+        case 11: quant_seed_at<11>(sb, gw, x, h); return;
+        case 12: quant_seed_at<12>(sb, gw, x, h); return;
+        case 13: quant_seed_at<13>(sb, gw, x, h); return;
+        case 14: quant_seed_at<14>(sb, gw, x, h); return;
+        case 20: quant_seed_at<20>(sb, gw, x, h); return;
+        case 23: quant_seed_at<23>(sb, gw, x, h); return;
+        case 42: quant_seed_at<42>(sb, gw, x, h); return;
+    }
+    x = 0.f;
+}
+__device__ __forceinline__ void seed_val(int st, const uint8_t* sb, int64_t gw, int cols, float& x, float& h) {
     h = 0.f;
     if (st == 30) x = __uint_as_float((uint32_t)(sb[2 * gw] | (sb[2 * gw + 1] << 8)) << 16);
     else if (st == 0) x = reinterpret_cast<const float*>(sb)[gw];
-    else x = h2f((uint32_t)(sb[2 * gw] | (sb[2 * gw + 1] << 8)));
+    else if (st == 1) x = h2f((uint32_t)(sb[2 * gw] | (sb[2 * gw + 1] << 8)));
+    else seed_val_any(st, sb, gw, cols, x, h);
 }
 
 // position of a weight's column in its row: the first 256 columns, then 7 parts
@@ -412,10 +461,12 @@ __device__ __forceinline__ int pos8(int64_t col, int cols) {
     return cols <= 0 || col < 256 ? 0 : 1 + (int)min((int64_t)6, col * 7 / cols);
 }
 
+__device__ __forceinline__ int hboff_of(const TM& m) { return m.seed_type == SEED_COLRMS ? HBOFF_COL : HBOFF; }
+
 // predicted code r, mirror sign s and context of weight w from F's own scales (a, c)
 template <int T>
 __device__ __forceinline__ void predict(float a, float c, const uint8_t* pb, int w, float x, float h, int mv, int p8,
-                                        int& r, int& s, int& ctx) {
+                                        int hboff, int& r, int& s, int& ctx) {
     float u, hu;
     if constexpr (NONLIN<T>) {
         const float t = x / a;
@@ -435,11 +486,15 @@ __device__ __forceinline__ void predict(float a, float c, const uint8_t* pb, int
     const float ru = rintf(u), fr = u - ru;
     r = (int)fmaxf(fminf(ru, (float)Ty<T>::QMAX), (float)Ty<T>::QMIN);
     s = fr >= 0.f ? 1 : -1;
-    const int mb = min(7, (int)(fabsf(fr) * 16.f));
+    int mb = min(7, (int)(fabsf(fr) * 16.f));
+    if (hboff == HBOFF_COL) {                     // no seed: r is the zero point; its place in the range
+        s = 1;
+        mb = min(7, max(0, (r - Ty<T>::QMIN) * 8 / (Ty<T>::QMAX - Ty<T>::QMIN + 1)));
+    }
     int hb = 0;
-    if (hu > 0.f) hb = max(1, min(7, ilogbf(hu) + 8));
+    if (hu > 0.f) hb = max(1, min(7, ilogbf(hu) + hboff));
     ctx = NSB_MAX + hb * 8 + mb;
-    if (mv >= 2 && hu == 0.f) ctx = CODE2 + p8 * 16 + min(15, (int)(fabsf(fr) * 32.f));
+    if (mv >= 2 && hu == 0.f && hboff != HBOFF_COL) ctx = CODE2 + p8 * 16 + min(15, (int)(fabsf(fr) * 32.f));
 }
 
 }  // namespace qr

@@ -12,6 +12,7 @@ imatrix offset]); (decode): the same without the file bytes. Bytes are numpy uin
 DeviceArrays; seeds are device arrays (BF16 = type 30, F32 = 0, F16 = 1).
 """
 import ctypes
+import json
 import struct
 import threading
 import time
@@ -23,9 +24,14 @@ from . import zstd
 from .framing import pack, unpack  # noqa: F401  (the reference's codecs_gguf.pack/unpack)
 from ._lib import check, lib
 
-SELF_TYPES = {2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 20, 23, 42}
+SELF_TYPES = {2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 20, 23, 42}     # also coded without a seed, and seeds
 GRID_TYPES = {16, 17, 18, 19, 21, 22, 29}
 QR_TYPES = SELF_TYPES | GRID_TYPES
+SEED_TYPES = SELF_TYPES | {0, 1, 30}
+COLRMS = 98                                  # no seed: the seed buffer holds the per-column RMS (float32)
+EXPLICIT = 99                                # the seed buffer holds float32 (value, uncertainty) per weight
+NFIELDS = {2: 1, 6: 1, 8: 1, 20: 1, 42: 1, 3: 2, 7: 2, 10: 34, 11: 17, 14: 17, 12: 18, 13: 18, 23: 9,
+           16: 9, 18: 9, 19: 9, 21: 9, 17: 17, 22: 17, 29: 17}
 BS = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 20: 18, 23: 136, 42: 18,
       16: 66, 17: 74, 18: 98, 19: 50, 21: 110, 22: 82, 29: 56}
 QK = {t: (32 if t in (2, 3, 6, 7, 8, 20) else 64 if t == 42 else 256) for t in QR_TYPES}
@@ -334,3 +340,115 @@ def decode(T, buf, items, seed_dev, imx_dev=None, stream=None):
     freq, used = load_tables(ch["t"])
     lens = np.frombuffer(zstd.decompress(ch["l"]), np.uint32)
     return decode_parts(T, freq, used, lens, ch["s"], items, seed_dev, imx_dev, mv, stream)
+
+
+# ------------------------------------------------------------------ seeds other than a BF16 base
+
+def intervals(T, blocks, nw, stream=None):
+    """device uint8 blocks of non-grid type T -> (lo, hi) float32 DeviceArrays: the interval of values
+    each weight's code stands for (qr.py:1093-1098)"""
+    blocks = blocks if isinstance(blocks, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(blocks, np.uint8))
+    lo, hi = dev.DeviceArray(nw, np.float32), dev.DeviceArray(nw, np.float32)
+    check(lib().spa_qr_intervals(T, blocks.ptr, nw, lo.ptr, hi.ptr, stream))
+    return lo, hi
+
+
+def grid_half_steps(T, blocks, nw, stream=None):
+    """half the step between grid levels around each weight of grid-type blocks (float32 DeviceArray)"""
+    h = dev.DeviceArray(nw, np.float32)
+    check(lib().spa_qr_grid_h(T, blocks.ptr, nw, h.ptr, stream))
+    return h
+
+
+def explicit_seed(T, blocks, x, stream=None):
+    """an EXPLICIT seed (99) from a grid-type tensor: float32 (x, h) per weight, x its dequantized values,
+    h half the step between its grid's levels (qr.py:1100-1106) -> DeviceArray of 2 nw float32"""
+    nw = x.size
+    h = grid_half_steps(T, blocks, nw, stream)
+    xh = np.stack([x.to_host(stream=stream).reshape(-1), h.to_host(stream=stream)], axis=1).reshape(-1)
+    return dev.DeviceArray.from_host(np.ascontiguousarray(xh, np.float32), stream)
+
+
+def weight_equal(T, F, P, nw, stream=None):
+    """device uint8 per weight: code and sub-block integer scale equal in blocks F and P (qr.py:1109-1113)"""
+    out = dev.DeviceArray(nw, np.uint8)
+    check(lib().spa_qr_weight_equal(T, F.ptr, P.ptr, nw, out.ptr, stream))
+    return out
+
+
+def self_side(T, blocks, cols, gq=None, stream=None):
+    """no-seed coding of one tensor (device uint8 blocks, `cols` weights per row) -> (column RMS as fp16,
+    template blocks, rows): the RMS of each column of the dequantized tensor (detmath's in-order sums)
+    and one row of blocks holding the rounded mean of every block field (qr.py:1116-1136)"""
+    from . import detmath
+    from .gpuquant import GPUQuant
+    gq = gq or GPUQuant(stream=stream)
+    x = gq.dequantize(T, blocks, cols)
+    rows = x.size // cols
+    xs = x.view(0, (rows, cols), np.float32)
+    rms = np.sqrt((detmath.cols(xs, True, stream=stream).to_host(stream=stream) / rows).astype(np.float32)).astype(np.float16)
+    del x, xs
+    nb_row = cols // QK[T]
+    nblk = rows * nb_row
+    nf = NFIELDS[T]
+    fl = dev.DeviceArray(max(1, nblk * nf), np.int32)
+    check(lib().spa_qr_block_fields(T, blocks.ptr, nblk, fl.ptr, stream))
+    f = fl.to_host(stream=stream)[:nblk * nf].reshape(rows, nb_row, nf)
+    # (integer fields: the float64 sum over rows is exact, the mean one rounding)
+    v = np.rint(f.astype(np.float64).mean(0)).astype(np.int32)
+    vd = dev.DeviceArray.from_host(np.ascontiguousarray(v), stream)
+    tpl = dev.DeviceArray(nb_row * BS[T], np.uint8)
+    check(lib().spa_qr_blocks_from_fields(T, vd.ptr, nb_row, tpl.ptr, stream))
+    return rms, tpl.to_host(stream=stream), rows
+
+
+def self_encode(T, tensors, stream=None):
+    """tensors: [(host or device uint8 blocks, cols)] of non-grid type T, coded without a seed: each
+    batch QR-coded against template blocks with the column RMS as the seed (qr.py:1147-1163) -> bytes"""
+    from .gpuquant import GPUQuant
+    gq = GPUQuant(stream=stream)
+    parts, side = {}, []
+    for bi in batches(T, [_nbytes(b) for b, _ in tensors]):
+        items, seeds, rms_l, tpl_l, o = [], [], [], [], 0
+        for i in bi:
+            b, cols = tensors[i]
+            bd = b if isinstance(b, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(b, np.uint8).reshape(-1), stream)
+            rms, tpl, rows = self_side(T, bd, cols, gq, stream)
+            rms_l.append(rms)
+            tpl_l.append(tpl)
+            seeds.append(rms.astype(np.float32))
+            items.append((bd, dev.DeviceArray.from_host(np.tile(tpl, rows), stream), o, COLRMS, cols))
+            o += cols * 4
+        seed = dev.DeviceArray.from_host(np.concatenate(seeds).view(np.uint8), stream)
+        parts[str(len(side))] = encode(T, items, seed, stream=stream)
+        side.append([[_nbytes(tensors[i][0]), tensors[i][1]] for i in bi])
+        parts[f"r{len(side) - 1}"] = zstd.zstd_c(b"".join(r.tobytes() for r in rms_l), 19)
+        parts[f"t{len(side) - 1}"] = zstd.zstd_c(b"".join(t.tobytes() for t in tpl_l), 19)
+    return pack({"meta": zstd.zstd_c(json.dumps(side).encode()), **parts})
+
+
+def self_decode(T, buf, stream=None):
+    """-> list of device uint8 arrays, in self_encode's order (qr.py:1166-1186)"""
+    ch = unpack(memoryview(buf))
+    out = []
+    for k, sizes in enumerate(json.loads(zstd.decompress(ch["meta"]))):
+        rms_all = np.frombuffer(zstd.decompress(ch[f"r{k}"]), np.float16)
+        tpl_all = np.frombuffer(zstd.decompress(ch[f"t{k}"]), np.uint8)
+        items, seeds, ro, to, o = [], [], 0, 0, 0
+        for nbytes_, cols in sizes:
+            nb_row = cols // QK[T]
+            rows = nbytes_ // BS[T] // nb_row
+            rms = rms_all[ro:ro + cols]
+            ro += cols
+            tpl = tpl_all[to:to + nb_row * BS[T]]
+            to += nb_row * BS[T]
+            seeds.append(rms.astype(np.float32))
+            items.append((dev.DeviceArray.from_host(np.tile(tpl, rows), stream), o, COLRMS, cols))
+            o += cols * 4
+        seed = dev.DeviceArray.from_host(np.concatenate(seeds).view(np.uint8), stream)
+        F = decode(T, ch[str(k)], items, seed, stream=stream)
+        p = 0
+        for nbytes_, _ in sizes:
+            out.append(F.view(p, (nbytes_,), np.uint8))
+            p += nbytes_
+    return out

@@ -204,6 +204,14 @@ class Compressor:
             lib().ZSTD_freeCCtx(self.cctx)
 
 
+def zstd_c(data, level=19):
+    """the reference's codecs_gguf.zstd_c (codecs_gguf.py:72-79): small data with the level's
+    parameters; above 8 MiB a 2^27 window, long-distance matching and worker threads"""
+    if memoryview(data).nbytes <= (8 << 20):
+        return compress(data, level)
+    return compress_with(data, Params(level, window_log=27, threads=max(1, os.cpu_count() or 1), ldm=True))
+
+
 def compress_with(data, params, dict_data=None):
     """one frame of `data` with explicit parameters (and dictionary)"""
     c = Compressor(params, dict_data, size=memoryview(data).nbytes)

@@ -1,0 +1,27 @@
+"""Cases of the QR coder's other seeds (shared by make_qr_seed_golden.py and the tests): inputs are
+regenerated from their seeds."""
+import numpy as np
+
+from seedpack_amd import synth
+
+SELF_CASES = [("q4_0", 2, 32, 1024), ("q8_0", 8, 16, 1024), ("q4_1", 3, 16, 512), ("q2_k", 10, 8, 1024),
+              ("q3_k", 11, 8, 1024), ("q4_k", 12, 8, 1024), ("q5_k", 13, 8, 1024), ("q6_k", 14, 8, 1024),
+              ("iq4_nl", 20, 16, 512), ("iq4_xs", 23, 8, 1024), ("q2_0", 42, 16, 512), ("q5_0", 6, 16, 512),
+              ("q5_1", 7, 16, 512)]
+EXPLICIT_CASES = [("q4_k", 12, 8, 1024), ("q8_0", 8, 8, 1024), ("iq4_xs", 23, 8, 1024), ("iq2_xs", 17, 16, 512),
+                  ("iq3_xxs", 18, 16, 512), ("iq1_m", 29, 16, 512)]
+QSEED_CASES = [("q4_k_from_q8_0", 12, 8, 8, 1024), ("q2_k_from_q6_k", 10, 14, 8, 1024),
+               ("q4_0_from_q4_k", 2, 12, 16, 1024), ("q6_k_from_iq4_xs", 14, 23, 8, 1024),
+               ("iq2_xs_from_q8_0", 17, 8, 16, 512), ("q3_k_from_q5_1", 11, 7, 8, 1024),
+               ("q5_0_from_q2_0", 6, 42, 16, 512), ("q4_1_from_iq4_nl", 3, 20, 16, 512)]
+AUX_TYPES = [2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 20, 23, 42]
+GRID_AUX_TYPES = [16, 17, 18, 19, 21, 22, 29]
+NEED_IMX = {16, 17, 19, 29}
+
+
+def inputs(kind, k, rows, cols):
+    """float32 weights (rows, cols) and an imatrix"""
+    g = np.random.Generator(np.random.PCG64({"self": 0x5E1F, "explicit": 0xE4B1, "qseed": 0x05EE, "aux": 0xA0C5}[kind] + k))
+    x = synth.bf16_to_f32(synth.student_t_bf16(g, (rows, cols))).reshape(rows, cols)
+    imx = g.lognormal(0, 1, cols).astype(np.float32)
+    return x, imx
