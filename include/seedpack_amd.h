@@ -226,7 +226,7 @@ int spa_float_pred(const void* src, int src_kind, int64_t n, int dst_type, void*
  * products of floats exact in float64, nothing contracted. All launch on `stream` and return. */
 
 /* out[r] = sum_j x[r][j] (sq: x[r][j]^2) over the nr x nc row-major array x (f64 = 0: float32, 1:
- * float64). detmath.rows (detmath.py:185-192). */
+ * float64, 2: BF16 bits widened to float32). detmath.rows (detmath.py:185-192). */
 int spa_dm_rows(const void* x, int f64, int64_t nr, int64_t nc, int sq, double* out, void* stream);
 /* out[c] = sum_r x[r][c] (sq: squares) over the rows r with mask[r] != 0 (mask NULL: all).
  * detmath.cols (detmath.py:195-202). */
@@ -242,6 +242,29 @@ int spa_dm_solve(const float* A, const float* b, int64_t n, int k, float* x, voi
 /* float64 log2 / exp2 elementwise (detmath.py:20-58, :171-182). */
 int spa_dm_log2(const double* x, int64_t n, double* y, void* stream);
 int spa_dm_exp2(const double* x, int64_t n, double* y, void* stream);
+
+/* ---- M24 BF16 codec (method m28's base codec; replaces gpu_bf16.py's bf_hist / bf_enc / bf_dec and the
+ * column statistics of M24BF16GPU.compress_dev, gpu_bf16.py:36-132, :340-371). TB descriptors are 24
+ * bytes {i64 off, i32 rowlen, rowbase, colbase, tab}, SG 16 bytes {i32 t, n, i64 i0} (gpu_bf16.py:271-272);
+ * segments of 16384 weights, 160 tables per tensor, PB 12. */
+
+/* s1[c] / s2[c] = float64 sums in row order of w[r][c] / rfa[r] (and its square), w BF16 bits nr x rowlen,
+ * the quotient in float32. */
+int spa_m24_cols(const void* w, const float* rfa, int64_t nr, int rowlen, double* s1, double* s2, void* stream);
+/* counts[(tab + ctx) * 256 + symbol] += the segments' exponent, mantissa and sign symbols. */
+int spa_m24_hist(const void* file, const void* tb, const void* sg, int nseg, const int16_t* rfi, const int16_t* cfi,
+                 const int8_t* scl, uint32_t* counts, void* stream);
+/* encode: each segment into its slot of cap bytes (>= 2 * 16384 + 1024), written downwards, out_len[s] its
+ * length (0xffffffff on overflow); rcp: a workspace of spa_m24_rcp_bytes(ntab) bytes. */
+size_t spa_m24_rcp_bytes(int ntab);
+int spa_m24_encode(const void* file, const void* tb, const void* sg, int nseg, const int16_t* rfi, const int16_t* cfi,
+                   const int8_t* scl, const int* remap, int ntab, const uint16_t* freq, const uint32_t* cum, uint32_t* rcp,
+                   void* out, uint64_t cap, uint32_t* out_len, void* stream);
+/* decode segment s from in + in_off[s] (reads past in_bytes see zeros) into the tensors of file;
+ * lut from spa_rans_build_lut. */
+int spa_m24_decode(const void* in, uint64_t in_bytes, const uint64_t* in_off, void* file, const void* tb, const void* sg,
+                   int nseg, const int16_t* rfi, const int16_t* cfi, const int8_t* scl, const int* remap,
+                   const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* stream);
 
 /* ---- estimating what a quant was made from ---- */
 

@@ -68,6 +68,13 @@ SIGNATURES = {
     "spa_xor3": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_diff_count": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_count_every": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "spa_m24_cols": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p]),
+    "spa_m24_hist": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "spa_m24_rcp_bytes": (c_size_t, [c_int]),
+    "spa_m24_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                               c_void_p, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p, c_void_p]),
+    "spa_m24_decode": (c_int, [c_void_p, c_uint64, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "spa_qr_intervals": (c_int, [c_int, c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
     "spa_qr_grid_h": (c_int, [c_int, c_void_p, c_int64, c_void_p, c_void_p]),
     "spa_qr_weight_equal": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),

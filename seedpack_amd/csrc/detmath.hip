@@ -19,6 +19,11 @@ namespace {
 
 constexpr int TILE = 64;
 
+// an element as float64: float32 / float64 as they are, uint16 as BF16 bits
+__device__ __forceinline__ double as_f64(float v) { return (double)v; }
+__device__ __forceinline__ double as_f64(double v) { return v; }
+__device__ __forceinline__ double as_f64(uint16_t u) { return (double)__uint_as_float((uint32_t)u << 16); }
+
 template <typename T>
 __global__ __launch_bounds__(TILE) void k_rows(const T* __restrict__ x, int64_t nr, int64_t nc, int sq,
                                                double* __restrict__ out) {
@@ -36,9 +41,9 @@ __global__ __launch_bounds__(TILE) void k_rows(const T* __restrict__ x, int64_t 
         const int n = nc - c0 < TILE ? (int)(nc - c0) : TILE;
         if (row < nr) {
             if (sq)
-                for (int j = 0; j < n; ++j) { const double v = (double)tile[lane][j]; s = s + v * v; }
+                for (int j = 0; j < n; ++j) { const double v = as_f64(tile[lane][j]); s = s + v * v; }
             else
-                for (int j = 0; j < n; ++j) s = s + (double)tile[lane][j];
+                for (int j = 0; j < n; ++j) s = s + as_f64(tile[lane][j]);
         }
         __syncthreads();
     }
@@ -217,7 +222,10 @@ int spa_dm_rows(const void* x, int f64, int64_t nr, int64_t nc, int sq, double* 
     if (!nr) return SPA_OK;
     if (!out || (nc && !x)) return fail(SPA_ERR_ARG, "spa_dm_rows: null pointer");
     hipStream_t st = (hipStream_t)stream;
-    if (f64)
+    if (f64 == 2)
+        hipLaunchKernelGGL(spa::k_rows<uint16_t>, dim3(spa::blocks_for(nr, spa::TILE)), dim3(spa::TILE), 0, st,
+                           (const uint16_t*)x, nr, nc, sq, out);
+    else if (f64)
         hipLaunchKernelGGL(spa::k_rows<double>, dim3(spa::blocks_for(nr, spa::TILE)), dim3(spa::TILE), 0, st,
                            (const double*)x, nr, nc, sq, out);
     else

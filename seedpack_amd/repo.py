@@ -43,9 +43,12 @@ from . import container, device as dev, gguf, header, imatrix as imx_mod, qr, r2
 from ._lib import check, lib
 from .framing import nbytes, pack, pack_parts, unpack
 from .gpuquant import GPUQuant
+from .m24 import M24BF16
 from .requant import QFUN
 
 METHOD = "M29 model repo: M28 with the BF16 v2 base codec (R2)"     # repo3.py:2539
+METHODS = {"m29": METHOD,                                            # the archive methods built here
+           "m28": "M28 model repo: BF16 + quants re-derived on the GPU with llama.cpp quantisers + imatrix"}   # repo3.py:585-586
 TOOL = "seedpack 0.5.0"              # the program whose archives these are byte-for-byte (cli.py:31)
 WINDOW = 1 << 30                     # base bytes per window (repo3.py:1672)
 PRED_WINDOW = 3 << 30                # first predictions per window, bytes (repo3.py:1677)
@@ -354,8 +357,11 @@ class Packer:
     for a repository with BF16 base model(s), quantized GGUFs derived from them, an imatrix and other
     files"""
 
-    def __init__(self, level=7, verbose=False, coders=8, zstd_lanes=14, staging_bytes=24 << 30, device_bytes=None):
-        self.level, self.verbose = level, verbose
+    def __init__(self, level=7, verbose=False, coders=8, zstd_lanes=14, staging_bytes=24 << 30, device_bytes=None,
+                 method="m29"):
+        if method not in METHODS:
+            raise NotImplementedError(f"archive method {method!r} (built: {', '.join(METHODS)})")
+        self.level, self.verbose, self.method = level, verbose, method
         self.stream = dev.Stream()
         self.gq = GPUQuant(stream=self.stream.handle)
         self.io = ThreadPoolExecutor(8)          # file reads (pieces)
@@ -398,10 +404,14 @@ class Packer:
         return d
 
     def _code_base(self, b, host, order):
-        """the base's chunk: pack({"r2": R2 chunk}) with the reference's part order, coded on its own
-        stream from the resident copy"""
+        """the base's chunk: pack({"r2": R2 chunk}) with the reference's part order (m29), or the M24
+        chunk's parts (m28, repo3.py:1470-1475), coded on its own stream from the resident copy"""
         s = dev.Stream()
         g = b.g
+        if self.method == "m28":
+            parts = M24BF16(stream=s.handle).compress_dev(host, d=b.d, g=g)
+            s.synchronize()
+            return pack_parts(parts)
         lay = r2.layout_of([(t.name, t.offset, t.nbytes, t.shape[0]) for t in g.tensors
                             if t.type == BF16 and len(t.shape) == 2], len(host))
         with ThreadPoolExecutor(1) as hp:
@@ -769,7 +779,7 @@ class Packer:
             side.shutdown()
             aux.shutdown()
             phase("bases and other files coded")
-            manifest = {"method": METHOD, "bases": list(bases), "seeds": [], "files": entries,
+            manifest = {"method": METHODS[self.method], "bases": list(bases), "seeds": [], "files": entries,
                         "extras": {"bundle": list(ex), "single": big}}
             if self.stats["qr_grid"] or self.stats["ref"]:
                 manifest["needs"] = "0.3.0"
@@ -778,7 +788,7 @@ class Packer:
             phase("checksums")
             catalog = [{"name": n, "size": os.path.getsize(p), "hash": hashes[n], "role": roles[n] or "file",
                         "stored": self.sizes.get(n)} for n, p in files.items()]
-            w.close({"tool": tool, "method": METHOD, "created": created or _created(), "hash": "sha256",
+            w.close({"tool": tool, "method": METHODS[self.method], "created": created or _created(), "hash": "sha256",
                      "files": catalog, "total": total})
         except BaseException:
             w.abort()
@@ -818,8 +828,10 @@ def _created():
 
 
 def pack_repo(inputs, output, **kw):
-    """pack the files / directories `inputs` into the archive `output` -> stats"""
-    return Packer(level=kw.pop("level", 7), verbose=kw.pop("verbose", False)).pack(inputs, output, **kw)
+    """pack the files / directories `inputs` into the archive `output` -> stats (method "m29", the
+    reference's default, or "m28")"""
+    return Packer(level=kw.pop("level", 7), verbose=kw.pop("verbose", False), method=kw.pop("method", "m29")).pack(
+        inputs, output, **kw)
 
 
 # ------------------------------------------------------------------ unpacking / testing
@@ -861,8 +873,8 @@ class Unpacker:
         r = container.Reader(archive)
         meta = r.meta
         manifest = json.loads(zstd.decompress(r.get("manifest")))
-        if not manifest["method"].startswith("M29"):
-            raise NotImplementedError(f"archive method {manifest['method']!r}: only M29 archives are read here")
+        if not manifest["method"].startswith(("M29", "M28")):
+            raise NotImplementedError(f"archive method {manifest['method']!r}: only M28 / M29 archives are read here")
         if manifest.get("seeds") or manifest.get("joined") or manifest.get("imx_fit"):
             raise NotImplementedError("seeds, split models and fitted importance are not built")
         cat = {f["name"]: f for f in meta["files"]}
@@ -934,9 +946,15 @@ class Unpacker:
         for i in sorted(need_b):
             name = manifest["bases"][i]
             ch = unpack(memoryview(r.get(f"b{i}")))
-            if "r2" not in ch:
-                raise NotImplementedError(f"base {name}: only R2-coded bases are read here")
-            d, rest = r2.BF16v2(stream=self.stream.handle).decompress(unpack(ch["r2"]), device="full")
+            if "r2" in ch:
+                d, rest = r2.BF16v2(stream=self.stream.handle).decompress(unpack(ch["r2"]), device="full")
+            elif "side" in ch and "stream" in ch:          # an M24 chunk (method m28)
+                d = M24BF16(stream=self.stream.handle).decompress_dev(ch)
+                lay = json.loads(zstd.decompress(ch["layout"]))
+                first = min([t[0] for t in lay["t"]] + [lay["size"]])
+                rest = d.view(0, (first,), np.uint8).to_host(stream=self.stream.handle)
+            else:
+                raise NotImplementedError(f"base {name}: a base chunk of a kind not built here (the seed codec)")
             g = gguf.GGUF(rest.tobytes(), light=True)     # the header is the start of the rest part
             b = _Base(i, name, rest, d, g)
             bases[i] = b

@@ -74,6 +74,23 @@ def test_small_repo_pack_is_deterministic(small_repo, tmp_path):
     assert open(a, "rb").read() == open(b, "rb").read()
 
 
+def test_small_repo_method_m28(small_repo, tmp_path):
+    """method m28: the base chunk is M24's parts (layout, side, tables, lens, stream, rest); every file
+    extracts byte-identical"""
+    root, arc, sizes, stats = small_repo
+    a = str(tmp_path / "m28.seedpack")
+    repo.pack_repo([root], a, method="m28")
+    r = container.Reader(a)
+    man = json.loads(zstd.decompress(r.get("manifest")))
+    assert man["method"] == repo.METHODS["m28"]
+    assert list(unpack(memoryview(r.get("b0")))) == ["layout", "side", "tables", "lens", "stream", "rest"]
+    out = str(tmp_path / "out28")
+    res = repo.unpack_repo(a, out)
+    assert not res["bad"] and not res["missing"], res
+    for n in sorted(os.listdir(root)):
+        assert open(os.path.join(root, n), "rb").read() == open(os.path.join(out, n), "rb").read(), n
+
+
 def test_small_repo_archive_layout(small_repo):
     root, arc, sizes, stats = small_repo
     r = container.Reader(arc)
