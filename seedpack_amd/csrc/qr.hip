@@ -581,6 +581,21 @@ __global__ __launch_bounds__(256) void k_blocks_from_fields(const int* __restric
 
 unsigned wgs_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
+// every QR type, grid types included
+template <template <int> class K, class... A>
+int dispatch_any(int T, A&&... args) {
+    switch (T) {
+        case 16: return K<16>::run(args...);
+        case 17: return K<17>::run(args...);
+        case 18: return K<18>::run(args...);
+        case 19: return K<19>::run(args...);
+        case 21: return K<21>::run(args...);
+        case 22: return K<22>::run(args...);
+        case 29: return K<29>::run(args...);
+    }
+    return dispatch<K>(T, args...);
+}
+
 template <int T> struct Intervals {
     static int run(const void* F, int64_t nw, float* lo, float* hi, hipStream_t st) {
         hipLaunchKernelGGL(k_intervals<T>, dim3(wgs_for(nw)), dim3(256), 0, st, (const uint8_t*)F, nw, lo, hi);
@@ -691,14 +706,14 @@ int spa_qr_block_fields(int T, const void* F, int64_t nblk, int* out, void* stre
     if (nblk < 0) return spa::fail(SPA_ERR_ARG, "spa_qr_block_fields: negative count");
     if (!nblk) return 0;
     if (!F || !out) return spa::fail(SPA_ERR_ARG, "spa_qr_block_fields: null pointer");
-    return dispatch<Fields>(T, F, nblk, out, (hipStream_t)stream);
+    return dispatch_any<Fields>(T, F, nblk, out, (hipStream_t)stream);
 }
 
 int spa_qr_blocks_from_fields(int T, const int* v, int n, void* out, void* stream) {
     if (n < 0) return spa::fail(SPA_ERR_ARG, "spa_qr_blocks_from_fields: negative count");
     if (!n) return 0;
     if (!v || !out) return spa::fail(SPA_ERR_ARG, "spa_qr_blocks_from_fields: null pointer");
-    return dispatch<FromFields>(T, v, n, out, (hipStream_t)stream);
+    return dispatch_any<FromFields>(T, v, n, out, (hipStream_t)stream);
 }
 
 int spa_qr_nfields(int T) {

@@ -48,7 +48,8 @@ from .requant import QFUN
 
 METHOD = "M29 model repo: M28 with the BF16 v2 base codec (R2)"     # repo3.py:2539
 METHODS = {"m29": METHOD,                                            # the archive methods built here
-           "m28": "M28 model repo: BF16 + quants re-derived on the GPU with llama.cpp quantisers + imatrix"}   # repo3.py:585-586
+           "m28": "M28 model repo: BF16 + quants re-derived on the GPU with llama.cpp quantisers + imatrix",   # repo3.py:585-586
+           "m30": "M30 sibling quants: tensor versions coded in chains, no base"}                           # siblings.py:168
 TOOL = "seedpack 0.5.0"              # the program whose archives these are byte-for-byte (cli.py:31)
 WINDOW = 1 << 30                     # base bytes per window (repo3.py:1672)
 PRED_WINDOW = 3 << 30                # first predictions per window, bytes (repo3.py:1677)
@@ -358,7 +359,8 @@ class Packer:
     files"""
 
     def __init__(self, level=7, verbose=False, coders=8, zstd_lanes=14, staging_bytes=24 << 30, device_bytes=None,
-                 method="m29"):
+                 method="m29", m30_slice=None):
+        self.m30_slice = m30_slice
         if method not in METHODS:
             raise NotImplementedError(f"archive method {method!r} (built: {', '.join(METHODS)})")
         self.level, self.verbose, self.method = level, verbose, method
@@ -635,11 +637,11 @@ class Packer:
         bases = {n: p for n, p in files.items() if roles[n] == "base"}
         derived = {n: p for n, p in files.items() if roles[n] == "derived"}
         extras = {n: p for n, p in files.items() if roles[n] is None}
-        if any(re.match(r"^.*-\d{5}-of-\d{5}\.gguf$", n) for n in bases):
+        if self.method != "m30" and any(re.match(r"^.*-\d{5}-of-\d{5}\.gguf$", n) for n in bases):
             raise NotImplementedError("split GGUF models (joined bases) are not built")
         base_names = [{t.name for t in heads[n][1]} for n in bases]
         orphans = [n for n in derived if not any({t.name for t in heads[n][1]} & s for s in base_names)]
-        if orphans:
+        if orphans and self.method != "m30":
             raise NotImplementedError(f"quantized files without a base ({orphans[0]}): the seed codec is not built")
         total = sum(os.path.getsize(p) for p in files.values())
         hashes = {}
@@ -662,6 +664,14 @@ class Packer:
                 w.put_later(f"x{j}", later[n])
                 big[n] = [f"x{j}", len(data)]
             phase("other files")
+            if self.method == "m30":
+                self._pack_m30({**bases, **derived}, w, later, hashes, {"bundle": list(ex), "single": big})
+                phase("tensor chains")
+                self._close(w, files, roles, hashes, later, total, tool, created)
+                aux.shutdown()
+                dt = time.perf_counter() - t0
+                return {"input_bytes": total, "archive_bytes": os.path.getsize(output), "seconds": dt,
+                        "GB_s": total / dt / 1e9, "phases": phases}
             imx_name = next((n for n in ex if n.startswith("imatrix")), None)
             imx_all = imx_mod.load(ex[imx_name]) if imx_name else {}
             # bases: their headers now (the files' plans need them), their bytes uploaded below
@@ -806,6 +816,27 @@ class Packer:
                 "cpu": {"process cpu_s": round(cpu_s, 1), **{k: round(v, 1) for k, v in self.cpu.items()}},
                 "residuals_in_hbm_peak": self.fpool.peak}
 
+    def _pack_m30(self, ggufs, w, later, hashes, exm):
+        """method m30 (siblings.M30Siblings): every GGUF's tensors as version chains"""
+        from .siblings import M30Siblings
+        for n, p in ggufs.items():
+            hashes[n] = self.hasher.submit(file_sha256, p)
+        from .siblings import SLICE
+        m = M30Siblings(slice_weights=self.m30_slice or SLICE, stream=self.stream.handle, verbose=self.verbose)
+        man = m.compress(ggufs, w.put)
+        man["extras"] = exm
+        w.put("manifest", zstd.compress(json.dumps(man).encode(), 19))
+        self.sizes.update(m.sizes)
+
+    def _close(self, w, files, roles, hashes, later, total, tool, created):
+        for n, f in later.items():
+            self.sizes[n] = nbytes(f.result())
+        hashes = {n: (h.result() if hasattr(h, "result") else h) for n, h in hashes.items()}
+        catalog = [{"name": n, "size": os.path.getsize(p), "hash": hashes[n], "role": roles[n] or "file",
+                    "stored": self.sizes.get(n)} for n, p in files.items()]
+        w.close({"tool": tool, "method": METHODS[self.method], "created": created or _created(), "hash": "sha256",
+                 "files": catalog, "total": total})
+
     @staticmethod
     def _kind(b, t, imx_all):
         """how tensor t of a quantized file is predicted from base b: 'rq', 'xor' or None (repo3.py:691-700)"""
@@ -830,8 +861,8 @@ def _created():
 def pack_repo(inputs, output, **kw):
     """pack the files / directories `inputs` into the archive `output` -> stats (method "m29", the
     reference's default, or "m28")"""
-    return Packer(level=kw.pop("level", 7), verbose=kw.pop("verbose", False), method=kw.pop("method", "m29")).pack(
-        inputs, output, **kw)
+    return Packer(level=kw.pop("level", 7), verbose=kw.pop("verbose", False), method=kw.pop("method", "m29"),
+                  m30_slice=kw.pop("m30_slice", None)).pack(inputs, output, **kw)
 
 
 # ------------------------------------------------------------------ unpacking / testing
@@ -873,8 +904,10 @@ class Unpacker:
         r = container.Reader(archive)
         meta = r.meta
         manifest = json.loads(zstd.decompress(r.get("manifest")))
+        if manifest["method"].startswith("M30"):
+            return self._run_m30(r, meta, manifest, outdir, patterns, t0)
         if not manifest["method"].startswith(("M29", "M28")):
-            raise NotImplementedError(f"archive method {manifest['method']!r}: only M28 / M29 archives are read here")
+            raise NotImplementedError(f"archive method {manifest['method']!r}: only M28 / M29 / M30 archives are read here")
         if manifest.get("seeds") or manifest.get("joined") or manifest.get("imx_fit"):
             raise NotImplementedError("seeds, split models and fitted importance are not built")
         cat = {f["name"]: f for f in meta["files"]}
@@ -996,6 +1029,37 @@ class Unpacker:
             log(self.verbose, f"  {m['name']}: {m['size']:,} B in {time.perf_counter() - tf:.2f} s")
         for j in jobs:
             j.result()
+        r.close()
+        dt = time.perf_counter() - t0
+        nbytes_ = sum(cat[n]["size"] for n in results)
+        return {"files": results, "bad": [n for n, ok in results.items() if not ok],
+                "missing": [n for n in want if n not in results], "bytes": nbytes_, "seconds": dt,
+                "GB_s": nbytes_ / dt / 1e9}
+
+    def _run_m30(self, r, meta, manifest, outdir, patterns, t0):
+        """an M30 archive: the extras, then the GGUF files rebuilt from their tensor chains"""
+        from .siblings import M30Siblings
+        cat = {f["name"]: f for f in meta["files"]}
+        want = set(select_names(meta["files"], patterns))
+        results = {}
+
+        def sink(name, buf):
+            ok = _ws(buf) == cat[name]["hash"] and len(buf) == cat[name]["size"]
+            if ok and outdir is not None:
+                path = os.path.join(outdir, *name.split("/"))
+                os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
+                _write_file(path, memoryview(np.ascontiguousarray(buf)).cast("B"), self.io)
+            results[name] = ok
+
+        exm = manifest["extras"]
+        if any(n in want for n in exm["bundle"]):
+            for n, b in unpack(lzma.decompress(bytes(r.get("extras")))).items():
+                if n in want:
+                    sink(n, bytes(b))
+        for n, (c, size) in exm["single"].items():
+            if n in want:
+                sink(n, zstd.decompress_into(r.get(c), np.empty(size, np.uint8)))
+        M30Siblings(stream=self.stream.handle).decompress(manifest, r.get, want, sink)
         r.close()
         dt = time.perf_counter() - t0
         nbytes_ = sum(cat[n]["size"] for n in results)

@@ -7,7 +7,8 @@ from seedpack_amd import synth
 SELF_CASES = [("q4_0", 2, 32, 1024), ("q8_0", 8, 16, 1024), ("q4_1", 3, 16, 512), ("q2_k", 10, 8, 1024),
               ("q3_k", 11, 8, 1024), ("q4_k", 12, 8, 1024), ("q5_k", 13, 8, 1024), ("q6_k", 14, 8, 1024),
               ("iq4_nl", 20, 16, 512), ("iq4_xs", 23, 8, 1024), ("q2_0", 42, 16, 512), ("q5_0", 6, 16, 512),
-              ("q5_1", 7, 16, 512)]
+              ("q5_1", 7, 16, 512), ("iq2_xs", 17, 16, 512), ("iq3_xxs", 18, 16, 512), ("iq1_m", 29, 16, 512),
+              ("iq2_s", 22, 16, 512), ("iq1_s", 19, 16, 512)]
 EXPLICIT_CASES = [("q4_k", 12, 8, 1024), ("q8_0", 8, 8, 1024), ("iq4_xs", 23, 8, 1024), ("iq2_xs", 17, 16, 512),
                   ("iq3_xxs", 18, 16, 512), ("iq1_m", 29, 16, 512)]
 QSEED_CASES = [("q4_k_from_q8_0", 12, 8, 8, 1024), ("q2_k_from_q6_k", 10, 14, 8, 1024),

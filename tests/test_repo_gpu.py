@@ -91,6 +91,52 @@ def test_small_repo_method_m28(small_repo, tmp_path):
         assert open(os.path.join(root, n), "rb").read() == open(os.path.join(out, n), "rb").read(), n
 
 
+@pytest.fixture(scope="module")
+def sibling_repo(tmp_path_factory):
+    """a BF16 model of 1 MiB+ tensors and five quantizations of it"""
+    root = str(tmp_path_factory.mktemp("siblings"))
+    say("case m30: writing the synthetic repository")
+    tensors = synth.qwen_tensors(layers=1, hidden=1024, ffn=1024, kv=256, vocab=1024)
+    files = {f"model-{NAMES[t]}.gguf": (lambda name, t=t: t) for t in (8, 14, 12, 17, 2)}
+    synth.write_repo(root, tensors, files, per_million=20000, nmerge=1000)
+    return root
+
+
+@pytest.mark.parametrize("with_base", [True, False])
+def test_method_m30(sibling_repo, tmp_path, with_base):
+    """method m30 (sibling quants, no base): the repository's GGUFs coded as tensor version chains in
+    slices (a slice of 256K weights here, so the 1M-weight tensors take several), identical files
+    stored once; every file extracts byte-identical. Without the BF16 file the chains start at the
+    Q8_0 versions."""
+    import shutil
+    root = sibling_repo
+    src = str(tmp_path / "src")
+    os.makedirs(src)
+    for n in os.listdir(root):
+        if with_base or n != "model-BF16.gguf":
+            shutil.copy(os.path.join(root, n), src)
+    shutil.copy(os.path.join(root, "model-Q4_K.gguf"), os.path.join(src, "copy-Q4_K.gguf"))   # identical file
+    a = str(tmp_path / "m30.seedpack")
+    say(f"case m30: pack (with the BF16 file: {with_base})")
+    repo.pack_repo([src], a, method="m30", m30_slice=1 << 18)
+    r = container.Reader(a)
+    man = json.loads(zstd.decompress(r.get("manifest")))
+    assert man["method"] == repo.METHODS["m30"] and man["slice"] == 1 << 18 and man["needs"] == "0.4.0"
+    chunks = list(r.chunks)
+    assert chunks[:2] == ["extras", "heads"] and chunks[-2:] == ["small", "manifest"]
+    same = {m["name"]: m["same"] for m in man["files"]}
+    names = [m["name"] for m in man["files"]]
+    assert names[same["model-Q4_K.gguf"]] == "copy-Q4_K.gguf" or names[same["copy-Q4_K.gguf"]] == "model-Q4_K.gguf"
+    kinds = {k for g in man["groups"] for v in g["vers"] for k in v.get("kinds", [])}
+    assert "qr" in kinds and max(len(g["vers"]) for g in man["groups"]) >= 5
+    assert any(len(v.get("kinds", [])) > 1 for g in man["groups"] for v in g["vers"])     # several slices
+    out = str(tmp_path / "out30")
+    res = repo.unpack_repo(a, out)
+    assert not res["bad"] and not res["missing"], res
+    for n in sorted(os.listdir(src)):
+        assert open(os.path.join(src, n), "rb").read() == open(os.path.join(out, n), "rb").read(), n
+
+
 def test_small_repo_archive_layout(small_repo):
     root, arc, sizes, stats = small_repo
     r = container.Reader(arc)
