@@ -266,6 +266,94 @@ int spa_m24_decode(const void* in, uint64_t in_bytes, const uint64_t* in_off, vo
                    int nseg, const int16_t* rfi, const int16_t* cfi, const int8_t* scl, const int* remap,
                    const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* stream);
 
+/* ---- M22 Q8_0 codec (gpu3.M22Fast: the codec of Q8Parts and of a seed's Q8_0 tensors). Replaces the
+ * kernels of gpu2.py:37-297 (hist_a / enc_a / dec_a, hist_b / enc_b / dec_b) and gpu3.py:26-230 (predict,
+ * predict_multi, hist_c / enc_c / dec_c) and the array steps of GPU2.compress / GPU3._plan_tensor
+ * (gpu2.py:554-616, gpu3.py:272-353) with detmath.sim8 (detmath.py:250-259). blocks: the coded tensors'
+ * Q8_0 blocks back to back (34 bytes each); meta: 32-byte records {first, nblocks, nb_row, grp, colbase,
+ * rowbase, off, qset} per tensor (gpu2.py:278 META_DT); skip: per block, bit 0 a duplicate row (not
+ * coded), bit 1 coded by phase C, bit 2 position and maximum coded by phase C. Tables: PB 12, phase A
+ * 4384 per group, phase B 1088 per group from qbase, phase C 88 per predicted tensor. */
+
+/* pos[b]: the first position of the largest |weight| of block b. */
+int spa_q8_pos(const void* blocks, int64_t n, uint8_t* pos, void* stream);
+/* row_m[r] = (sum of the row's fp16 scale bits) / blocks per row, rows of all tensors in meta order. */
+int spa_q8_row_means(const void* blocks, const void* meta, int ntens, int64_t nrows, int* row_m, void* stream);
+/* A tensor's column sums for the context statistics: rel[block] = float(exp2(float(bits - row mean) / 1024))
+ * (workspace, nrows * nbr floats), then per slice s of rows_per_slice rows and column c the float64 sums in
+ * row order of w and w^2, w = float(q) * rel: part1 / part2 [nslices][nbr * 32] (gpu2.py:588-597). */
+int spa_q8_col_stats(const void* blocks, int first, int nbr, int64_t nrows, const int* row_m, float* rel,
+                     int64_t rows_per_slice, double* part1, double* part2, void* stream);
+/* Duplicate rows: h[r] = sum over the row's 64-bit words of word * mult[word] mod 2^64 (nbr * 34 a multiple
+ * of 8), and eq[i] = rows ra[i] and rb[i] are byte-equal (gpu2.py:693-716). */
+int spa_q8_row_hash(const void* blocks, int first, int nbr, int64_t nrows, const uint64_t* mult, uint64_t* h, void* stream);
+int spa_q8_rows_equal(const void* blocks, int first, int nbr, const int* ra, const int* rb, int n, uint8_t* eq, void* stream);
+/* The encoder's reciprocals rcp[t][s] of freq[t][s] for ntab used tables. */
+int spa_q8_rcp(const uint16_t* freq, int ntab, uint32_t* rcp, void* stream);
+/* Phase A (scale bytes, maximum's rank and value; 4096 blocks per segment): histogram, encode (slots of cap
+ * bytes written downwards, out_len[s] = length or 0xffffffff on overflow), decode (reads past in_bytes see
+ * zeros). bcf / spread per block-column, perm / rankof [block-column][32], scls per column. */
+int spa_q8_hist_a(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, int ntens, int nblocks,
+                  const uint8_t* bcf, const uint8_t* spread, const uint8_t* rankof, const uint8_t* scls, uint32_t* counts,
+                  void* stream);
+int spa_q8_enc_a(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, int ntens, int nblocks,
+                 const uint8_t* bcf, const uint8_t* spread, const uint8_t* rankof, const uint8_t* scls, const int* remap,
+                 const uint16_t* freq, const uint32_t* cum, const uint32_t* rcp, void* out, uint64_t cap, uint32_t* out_len,
+                 void* stream);
+int spa_q8_dec_a(const void* in, uint64_t in_bytes, const uint64_t* in_off, const uint8_t* skip, const void* meta, int ntens,
+                 int nblocks, const uint8_t* bcf, const uint8_t* spread, const uint8_t* perm, const uint8_t* scls,
+                 const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* blocks, uint8_t* pos,
+                 void* stream);
+/* Phase B (the other 31 weights, 1024 blocks per segment). The histogram takes work items of 12 bytes
+ * {tensor, first block, blocks} (blocks of one tensor, a workgroup each) and counts into the tensor's qset. */
+int spa_q8_hist_b(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, int ntens, int nblocks,
+                  const void* items, int nitems, const int16_t* cfi, const uint8_t* scls, const int* row_m, int qbase,
+                  uint32_t* counts, void* stream);
+int spa_q8_enc_b(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, int ntens, int nblocks,
+                 const int16_t* cfi, const uint8_t* scls, const int* row_m, int qbase, const int* remap, const uint16_t* freq,
+                 const uint32_t* cum, const uint32_t* rcp, void* out, uint64_t cap, uint32_t* out_len, void* stream);
+int spa_q8_dec_b(const void* in, uint64_t in_bytes, const uint64_t* in_off, const uint8_t* skip, const void* meta, int ntens,
+                 int nblocks, const int16_t* cfi, const uint8_t* scls, const int* row_m, int qbase, const int* remap,
+                 const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* blocks, const uint8_t* pos,
+                 void* stream);
+/* Phase C. Row prediction pint[r][j] (int8) from up to 4 parents per row (par / coef [rows][4], mu per
+ * column): all rows of one tensor (encoder), or the entries (slot, row) of one wave of every predicted
+ * tensor (decoder; slots: 32-byte records {i64 rbase, i64 pbase, i32 first, nbr, mubase, pad}). Segments:
+ * 16-byte records {tensor, first row, rows, slot}. fbin per row, cfi with the residual column adjustment. */
+int spa_q8_predict(const void* blocks, int first, int nbr, int64_t nrows, const int* par, const float* coef, const float* mu,
+                   int8_t* pint, void* stream);
+int spa_q8_predict_multi(const void* blocks, const int* ent_slot, const int* ent_row, int nent, int cmax, const void* slots,
+                         const int* par, const float* coef, const float* mu, int8_t* pint, void* stream);
+int spa_q8_hist_c(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, const void* segs, int nseg,
+                  const void* slots, const int16_t* cfi, const int* row_m, const int8_t* fbin, const int8_t* pint,
+                  uint32_t* counts, void* stream);
+int spa_q8_enc_c(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, const void* segs, int nseg,
+                 const void* slots, const int16_t* cfi, const int* row_m, const int8_t* fbin, const int8_t* pint,
+                 const int* remap, const uint16_t* freq, const uint32_t* cum, const uint32_t* rcp, void* out, uint64_t cap,
+                 uint32_t* out_len, void* stream);
+/* decodes segments [seg0, seg1) (one wave) */
+int spa_q8_dec_c(const void* in, uint64_t in_bytes, const uint64_t* in_off, int seg0, int seg1, const uint8_t* skip,
+                 const void* meta, const void* segs, int nseg, const void* slots, const int16_t* cfi, const int* row_m,
+                 const int8_t* fbin, const int8_t* pint, const int* remap, const uint16_t* freq, const uint32_t* cum,
+                 const uint8_t* lut, void* blocks, uint8_t* pos, void* stream);
+/* The row-prediction planner (gpu3.py:272-353). W[r][c] = q * d (float32, exact); W -= mu per column; Wq =
+ * clip(rint(W / nrm[r] * 127), -127, 127) in float64, 0 for rows that are not valid. */
+int spa_q8_row_matrix(const void* blocks, int first, int nbr, int64_t nrows, float* W, void* stream);
+int spa_q8_center(float* W, const float* mu, int64_t nrows, int C, void* stream);
+int spa_q8_norm_i8(const float* W, const double* nrm, const uint8_t* valid, int64_t nrows, int C, int8_t* Wq, void* stream);
+/* S[ra][rb] = A B^T exactly in int32 for int8 rows of C columns (C a multiple of 32, 16-byte aligned rows):
+ * detmath.sim8. */
+int spa_q8_sim8(const int8_t* A, int64_t ra, const int8_t* B, int64_t rb, int C, int32_t* S, void* stream);
+/* cand[r][0..3]: the rows c < wstart[r] with valid[c] of largest Wq[r].Wq[c], ties to the lower row, -1 where
+ * fewer exist (the reference's sim8 + masked argmax rounds, gpu3.py:296-310). */
+int spa_q8_neighbours(const int8_t* Wq, int64_t n, int C, const int* wstart, const uint8_t* valid, int* cand, void* stream);
+/* Per row: least squares on its first k = 1..4 candidates (Gram + 1e-3 I, detmath.solve, coefficients in
+ * 1/64 steps), the k of lowest estimated bits: frac (residual energy fraction), kuse, coefs [n][4]. */
+int spa_q8_fit_rows(const float* W, const int* cand, int64_t n, int C, float* frac, int* kuse, float* coefs, void* stream);
+/* part[ch][c]: float64 sums in row order of the chosen residual^2 over the valid rows of each chunk of rows. */
+int spa_q8_col_res(const float* W, const int* cand, const float* coefs, const int* kuse, const uint8_t* valid, int64_t n,
+                   int C, int64_t chunk, double* part, void* stream);
+
 /* ---- estimating what a quant was made from ---- */
 
 /* The importance fit's conditions of rows X (R x cols float32) quantized as F (type T = Q4_0, Q4_1,

@@ -1,6 +1,6 @@
 """The base codec's "rest" part: a BF16 GGUF's bytes outside its coded tensors (header, metadata,
 1-D tensors, padding), coded on the host with lzma, in one of the two forms the reference writes
-(seedpack/gpu_bf16.py:421-428, seedpack/gpu2.py:299-457):
+(seedpack/gpu_bf16.py:421-428, seedpack/gpu2.py:299-457, gpu2.py:636-649):
 
   "P" form, for a GGUF with a BPE tokenizer: token k >= 256 made by merge rule k - 256 is the two
       tokens that rule joins, so the merged tokens and the merge strings are dropped and rebuilt from
@@ -8,6 +8,8 @@
       tokens no merge makes (the 256 byte tokens, the trailing special tokens) and the pair ids as
       three byte planes. Layout: u64 t0, t1, m0, m1 (the token and merge item spans), u64 token
       count, u64 merge count, u32 x 4 compressed part sizes, then the four lzma parts;
+  "T" form (the Q8_0 codec only, when the P form does not apply): merge rule k is token 256 + k split
+      at one position, so the tokens are stored with each rule's split position;
   "X" form otherwise: the bytes in four equal parts, each lzma'd, sizes first.
 
 Every lzma stream is preset 9 | extreme (xz container, CRC64). The byte layouts are the format; the
@@ -141,13 +143,64 @@ def pairs_d(buf):
     return stripped[:t0] + tok_items + stripped[t0:gap] + b"".join(merge_items) + stripped[gap:]
 
 
+# ------------------------------------------------------------------ "T": BPE tokenizer by split positions
+
+def tok_c(data, g, layout):
+    """the T form's body (the Q8_0 codec's fallback when the P form does not apply), or None: merge
+    rule k is token 256 + k with a space inserted, so only the split position of each rule is kept.
+    Layout: u64 t0, t1, m0, m1, u64 token count, u32 x 4 compressed part sizes, then the lzma parts of
+    the stripped header, the u16 token lengths, the token bytes and the u16 split positions."""
+    if "tokenizer.ggml.tokens" not in g.spans or "tokenizer.ggml.merges" not in g.spans:
+        return None
+    toks, t0, t1 = _string_array(data, g.spans["tokenizer.ggml.tokens"][0])
+    merges, m0, m1 = _string_array(data, g.spans["tokenizer.ggml.merges"][0])
+    if not (t1 <= m0 and m1 <= g.data_start and len(toks) >= 256 + len(merges)):
+        return None
+    split = np.empty(len(merges), np.uint16)
+    for k, m in enumerate(merges):
+        tok = toks[256 + k]
+        at = m.find(b" ")
+        if at < 0 or len(m) != len(tok) + 1 or m[:at] != tok[:at] or m[at + 1:] != tok[at:]:
+            return None
+        split[k] = at
+    lens = np.fromiter((len(t) for t in toks), np.int64, len(toks))
+    if lens.max() > 0xFFFF:
+        return None
+    rest = rest_of(data, layout)
+    stripped = rest[:t0] + rest[t1:m0] + rest[m1:]
+    comp = list(_POOL.map(_xz, [stripped, lens.astype("<u2").tobytes(), b"".join(toks), split.astype("<u2").tobytes()]))
+    return (struct.pack("<5Q", t0, t1, m0, m1, len(toks)) + struct.pack("<4I", *(len(c) for c in comp))
+            + b"".join(comp))
+
+
+def tok_d(buf):
+    """the T form's body back to rest_of's bytes"""
+    t0, t1, m0, m1, ntok = struct.unpack_from("<5Q", buf)
+    sizes = struct.unpack_from("<4I", buf, 40)
+    at = np.cumsum((56,) + sizes).tolist()
+    stripped, lens, raw, split = _POOL.map(_unxz, [buf[at[k]:at[k + 1]] for k in range(4)])
+    lens = np.frombuffer(lens, "<u2").astype(np.int64)
+    ends = np.cumsum(lens)
+    toks = [raw[e - n:e] for e, n in zip(ends.tolist(), lens.tolist())]
+    assert len(toks) == ntok, "T form: token count"
+    tok_items = b"".join(struct.pack("<Q", len(t)) + t for t in toks)
+    merge_items = b"".join(struct.pack("<Q", len(toks[256 + k]) + 1) + toks[256 + k][:p] + b" " + toks[256 + k][p:]
+                           for k, p in enumerate(np.frombuffer(split, "<u2").tolist()))
+    gap = t0 + (m0 - t1)
+    return stripped[:t0] + tok_items + stripped[t0:gap] + merge_items + stripped[gap:]
+
+
 # ------------------------------------------------------------------ the part
 
-def header_c(data, g, layout):
+def header_c(data, g, layout, tokz=False):
     """the "rest" part of a base: the P form when the GGUF's tokenizer allows it, else the X form
-    (gpu_bf16.py:421-424). g: the file's parsed header (spans, data_start)"""
+    (gpu_bf16.py:421-424); tokz (the Q8_0 codec's header coder, gpu2.py:636-645): the T form before
+    the X form. g: the file's parsed header (spans, data_start)"""
     p = pairs_c(data, g, layout)
-    return b"P" + p if p is not None else b"X" + parts_c(rest_of(data, layout))
+    if p is not None:
+        return b"P" + p
+    t = tok_c(data, g, layout) if tokz else None
+    return b"T" + t if t is not None else b"X" + parts_c(rest_of(data, layout))
 
 
 def header_x(rest):
@@ -158,4 +211,5 @@ def header_x(rest):
 def header_d(buf):
     """either form back to rest_of's bytes (gpu_bf16.py:426-428)"""
     buf = bytes(buf)
-    return pairs_d(buf[1:]) if buf[:1] == b"P" else parts_d(buf[1:])
+    form = buf[:1]
+    return pairs_d(buf[1:]) if form == b"P" else tok_d(buf[1:]) if form == b"T" else parts_d(buf[1:])

@@ -130,7 +130,7 @@ def store_tables(freq, used):
     """zstd-19 of (u32 n, u32 used deltas, u16 freq[n][256]) (gpu2.py:489-492)"""
     u = np.asarray(used, np.int64)
     du = np.diff(u, prepend=0).astype(np.uint32)
-    return zstd.compress(struct.pack("<I", len(u)) + du.tobytes() + np.asarray(freq, np.uint16).tobytes(), 19)
+    return zstd.zstd_c(struct.pack("<I", len(u)) + du.tobytes() + np.asarray(freq, np.uint16).tobytes(), 19)
 
 
 def load_tables(buf):

@@ -1,13 +1,14 @@
 """Constructed BF16 GGUF files for the base codec's header ("rest") coder: a BPE tokenizer whose merge
 rules build tokens 256.. from earlier ones (the tokenizer-aware form applies), the same with one
 malformed merge and with a merged token that is not its pair's concatenation (both fall back to the
-lzma form), and a file without a tokenizer. Deterministic from their seeds; used by the fixture
+lzma form), one rule whose halves are not tokens (the Q8_0 codec's split-position form applies, the
+pair form does not), and a file without a tokenizer. Deterministic from their seeds; used by the fixture
 writer (make_r2_golden.py --header) and by the tests."""
 import numpy as np
 
 from seedpack_amd import gguf
 
-NAMES = ["bpe", "bpe_bad_merge", "bpe_bad_token", "plain"]
+NAMES = ["bpe", "bpe_bad_merge", "bpe_bad_token", "plain", "bpe_split"]
 
 
 def _bpe(g, nmerge):
@@ -34,6 +35,10 @@ def case_file(name):
             merges[1234] = merges[1234] + b" x"
         if name == "bpe_bad_token":
             toks[256 + 777] = toks[256 + 777] + b"!"
+        if name == "bpe_split":             # a rule whose halves are not tokens: the split-position form only
+            vocab = set(toks)
+            k = next(k for k in range(1000, len(merges)) if len(toks[256 + k]) >= 3 and toks[256 + k][1:] not in vocab)
+            merges[k] = toks[256 + k][:1] + b" " + toks[256 + k][1:]
         kv["tokenizer.ggml.model"] = "gpt2"
         kv["tokenizer.ggml.tokens"] = toks
         kv["tokenizer.ggml.token_type"] = [1] * len(toks)

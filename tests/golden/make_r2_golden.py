@@ -5,7 +5,7 @@ through the reference's --cpu backend (seedpack/cpu.py, seedpack/cpukernels.py).
 container only:
 
     python tests/golden/make_r2_golden.py            # r2_vectors.npz
-    python tests/golden/make_r2_golden.py --header   # header_vectors.npz: the "rest" part's two forms
+    python tests/golden/make_r2_golden.py --header   # header_vectors.npz: the "rest" part's forms
 
 bf16v2.py and gpu2.py import numba / zstandard (absent here), so the functions and the kernel text
 are read with `ast` and executed against the --cpu backend; the driver steps of
@@ -184,8 +184,14 @@ def load_header_coder():
         if isinstance(node, ast.Assign) and any(getattr(t, "id", None) == "HEADER_CHUNKS" for t in node.targets):
             exec(ast.get_source_segment(src, node), ns)
         if isinstance(node, ast.FunctionDef) and node.name in ("rest_of", "xz_chunks_c", "_items", "_xz",
-                                                              "header_pairs_c"):
+                                                              "header_pairs_c", "header_tok_c"):
             exec(ast.get_source_segment(src, node), ns)
+        if isinstance(node, ast.ClassDef) and node.name == "GPU2":          # the Q8_0 codec's header coder
+            for fn in node.body:
+                if isinstance(fn, ast.FunctionDef) and fn.name == "_header_c":
+                    code = ast.get_source_segment(src, fn)
+                    code = "\n".join(line[4:] if line.startswith("    ") else line for line in code.splitlines())
+                    exec(code.replace("def _header_c", "def q8_header_c"), ns)
     bsrc, btree = _source(os.path.join(REF, "seedpack", "gpu_bf16.py"))
     for node in btree.body:
         if isinstance(node, ast.ClassDef) and node.name == "M24BF16GPU":
@@ -199,7 +205,7 @@ def load_header_coder():
 
 def main_header():
     """header_vectors.npz: per case of header_cases.py, the SHA-256 of the input file and the
-    reference's "rest" part for it (P or X form)"""
+    reference's "rest" part for it (P or X form), and the Q8_0 codec's (P, T or X form)"""
     from seedpack_amd import gguf
     from tests.golden.header_cases import NAMES, case_file
     ns = load_header_coder()
@@ -210,6 +216,10 @@ def main_header():
         part = ns["_header_c"](data, g, layout)
         out[f"{name}/input_sha256"] = np.frombuffer(hashlib.sha256(data).digest(), np.uint8)
         out[f"{name}/rest"] = np.frombuffer(part, np.uint8)
+        # the Q8_0 codec's (M22: TOKPAIRS and TOKZ set, gpu3.py:248, :583-584) on the same file
+        q8 = ns["q8_header_c"](type("M22", (), {"TOKPAIRS": True, "TOKZ": True})(), data, g, layout)
+        out[f"{name}/rest_q8"] = np.frombuffer(q8, np.uint8)
+        print(f"{name}: Q8_0 codec header {q8[:1].decode()} form, {len(q8)} B", flush=True)
         print(f"{name}: {len(data)} B file, {part[:1].decode()} form, {len(part)} B", flush=True)
     np.savez_compressed(os.path.join(HERE, "header_vectors.npz"), **out)
 

@@ -44,6 +44,26 @@ def test_header_part_decodes_back(header_vectors, name):
     assert out.tobytes() == data
 
 
+@pytest.mark.parametrize("name", NAMES)
+def test_q8_header_part_equals_reference(header_vectors, name):
+    """the Q8_0 codec's header coder (P, then the split-position T form, then X) against the reference's"""
+    data, layout = case_file(name)
+    part = header.header_c(data, gguf.GGUF(data), layout, tokz=True)
+    want = header_vectors[f"{name}/rest_q8"].tobytes()
+    assert part[:1] == want[:1], "form (P / T / X)"
+    assert part == want
+    assert header.header_d(want) == header.rest_of(data, layout)
+
+
+def test_split_form_needs_its_structure():
+    """the T form applies to bpe_split (whose P form does not) and not to a merge with a second space"""
+    data, layout = case_file("bpe_split")
+    assert header.pairs_c(data, gguf.GGUF(data), layout) is None
+    assert header.tok_c(data, gguf.GGUF(data), layout) is not None
+    bad, _ = case_file("bpe_bad_merge")
+    assert header.tok_c(bad, gguf.GGUF(bad), layout) is None
+
+
 def test_pairs_form_needs_the_merge_structure():
     """a planted mistake in the fixture's input (a merged token that is not its pair's concatenation)
     must turn the P form down"""
