@@ -22,8 +22,13 @@ the packed small files), "x<j>" (zstd of a big extra file), "b<i>" (base i: pack
 batches: pack({"meta": zstd(json [[type, names], ...]), "0": batch, ...})), "manifest" (zstd-19 of
 its JSON); the container index carries the catalog (names, sizes, SHA-256, roles).
 
-Not built here (they raise): base-less quant files (the reference's seed codec and M21), split
-GGUF models, quants made with another imatrix (imxfit), the M28 / M30 methods.
+Quantized files without their BF16 model: the senior quant of each group of such files (most bits
+per weight) becomes their base, a "seed" (repo3.py:1359-1372), coded by the seed codec (seed.py);
+its quantized tensors are dequantized for the others' requantization and seed their QR coding
+directly. A file that no base shares a tensor with is coded alone: the Q8_0 codec M22 (q8.Q8Parts)
+when at least half of its bytes are Q8_0 tensors (repo3.py:1190-1215), else zstd.
+
+Not built here (they raise): split GGUF models, quants made with another imatrix (imxfit).
 """
 import collections
 import fnmatch
@@ -44,7 +49,9 @@ from ._lib import check, lib
 from .framing import nbytes, pack, pack_parts, unpack
 from .gpuquant import GPUQuant
 from .m24 import M24BF16
+from .q8 import Q8Parts
 from .requant import QFUN
+from .seed import SeedCodec, bits_per_weight
 
 METHOD = "M29 model repo: M28 with the BF16 v2 base codec (R2)"     # repo3.py:2539
 METHODS = {"m29": METHOD,                                            # the archive methods built here
@@ -56,6 +63,8 @@ PRED_WINDOW = 3 << 30                # first predictions per window, bytes (repo
 DUP_MIN = 64 << 10                   # smaller tensors are not made references (repo3.py:1024)
 REF_KEEP = 3 << 30                   # bytes of referenced tensors per window (repo3.py:1887)
 BUNDLE_MAX = 64 << 20                # other files up to this size go into the lzma bundle (repo3.py:1364)
+Q8_MIN = 0.5                         # a base-less file with this share of Q8_0 bytes: the Q8_0 codec (repo3.py:1191)
+DQ_CACHE = 32 << 30                  # dequantized seed tensors kept in HBM (float32 bytes)
 SPARSE = 0.02                        # residuals with fewer non-zero bytes: zstd level >= 9 (repo3.py:45)
 SKIP_DIRS = {".git", ".cache", "__pycache__"}
 F32, F16, BF16 = 0, 1, 30
@@ -333,17 +342,57 @@ def process_order(files, groups):
 
 
 class _Base:
-    """a base model resident in HBM: the whole file (header included) at its file offsets"""
+    """a base model resident in HBM: the whole file (header included) at its file offsets. A seed's
+    quantized tensors are dequantized (llama.cpp's dequantize_row_*) when first used and kept, the
+    least recently used dropped beyond DQ_CACHE bytes"""
 
-    def __init__(self, index, name, host, d, g):
-        self.index, self.name, self.d, self.g = index, name, d, g
+    def __init__(self, index, name, host, d, g, seed=False):
+        self.index, self.name, self.d, self.g, self.seed = index, name, d, g, seed
         self.header = bytes(host[:g.data_start])
         self.by_name = {t.name: t for t in g.tensors}
+        self.dq, self.dq_bytes = collections.OrderedDict(), 0
 
-    def view(self, t):
-        """base tensor t as the quantizers take it (bf16 bits / f16 / f32)"""
+    def view(self, t, stream=None):
+        """base tensor t as the quantizers take it (bf16 bits / f16 / f32; a quantized tensor as f32)"""
+        if t.type in QFUN:
+            a = self.dq.get(t.name)
+            if a is not None:
+                self.dq.move_to_end(t.name)
+                return a
+            cols = t.shape[0]
+            a = dev.DeviceArray(t.numel, np.float32)
+            check(lib().spa_dequantize(t.type, self.d.ptr + t.offset, t.numel // cols, cols, a.ptr, stream))
+            self.dq[t.name] = a
+            self.dq_bytes += a.nbytes
+            while self.dq_bytes > DQ_CACHE and len(self.dq) > 1:
+                _, old = self.dq.popitem(last=False)
+                self.dq_bytes -= old.nbytes
+            return a
         dt = np.uint16 if t.type == BF16 else np.float16 if t.type == F16 else np.float32
         return self.d.view(t.offset, (t.numel,), dt)
+
+
+def pick_seeds(base_tensors, derived_tensors):
+    """derived files that share no tensor name with a base, grouped by model: the senior quant of each
+    group (most bits per weight, then the larger name) becomes its seed (repo3.py:1359-1372).
+    base_tensors: [tensor lists]; derived_tensors: {name: tensor list} in input order"""
+    base_names = [{t.name for t in ts} for ts in base_tensors]
+    names = {n: {t.name for t in ts} for n, ts in derived_tensors.items()}
+    rest = [n for n in derived_tensors if names[n] and not any(names[n] & b for b in base_names)]
+    seeds = []
+    while rest:
+        s_ = max(rest, key=lambda n: (bits_per_weight(derived_tensors[n]), n))
+        group = {n for n in rest if 2 * len(names[n] & names[s_]) >= len(names[n])}
+        seeds.append(s_)
+        rest = [n for n in rest if n not in group]
+    return seeds
+
+
+def _zc_params(level, data):
+    """the zstd parameters of a file stored alone: level >= 9 for an almost all-zero one (repo3.py:1533-1544)"""
+    v = np.frombuffer(data, np.uint8)
+    sparse = np.count_nonzero(v[::61]) * 61 < SPARSE * len(v)
+    return zstd.Params(max(level, 9) if sparse else level, window_log=25, threads=4)
 
 
 def _ws(n):
@@ -405,11 +454,28 @@ class Packer:
                 self.pool.release(x)
         return d
 
+    def _code_alone(self, entry, data, ts):
+        """(a zstd lane) a file no base predicts: the Q8_0 codec when at least half its bytes are Q8_0
+        tensors, else zstd alone (repo3.py:1199-1215, :1633-1638)"""
+        if data and sum(t.nbytes for t in ts if t.type == 8) >= Q8_MIN * len(data):
+            s = dev.Stream()
+            c = Q8Parts(stream=s.handle).compress(data)
+            s.synchronize()
+            entry["codec"] = "q8"
+            self.stats["q8 files"] += 1
+            return entry, None, c
+        return entry, None, zstd.compress_with(data, _zc_params(self.level, data))
+
     def _code_base(self, b, host, order):
         """the base's chunk: pack({"r2": R2 chunk}) with the reference's part order (m29), or the M24
-        chunk's parts (m28, repo3.py:1470-1475), coded on its own stream from the resident copy"""
+        chunk's parts (m28, repo3.py:1470-1475), or a seed's chunk (seed.py), coded on its own stream
+        from the resident copy"""
         s = dev.Stream()
         g = b.g
+        if b.seed:
+            c = SeedCodec(stream=s.handle).compress(host, g=g, d=b.d)
+            s.synchronize()
+            return c
         if self.method == "m28":
             parts = M24BF16(stream=s.handle).compress_dev(host, d=b.d, g=g)
             s.synchronize()
@@ -499,7 +565,7 @@ class Packer:
             mine.append((t, k))
         self.stats["ref"] += len(refs)
         rts = [residual.Tensor(t.name, t.type, t.shape[0], F.view(t.offset, (t.nbytes,), np.uint8),
-                               b.view(b.by_name[t.name]), imatrix=imx_map.get(t.name), base_type=b.by_name[t.name].type,
+                               b.view(b.by_name[t.name], st), imatrix=imx_map.get(t.name), base_type=b.by_name[t.name].type,
                                numel=t.numel) for t, _ in mine]
         res = residual.residual_window(rts, self.gq, stream=st) if rts else []
         tm["regrow"] = time.perf_counter()
@@ -639,10 +705,14 @@ class Packer:
         extras = {n: p for n, p in files.items() if roles[n] is None}
         if self.method != "m30" and any(re.match(r"^.*-\d{5}-of-\d{5}\.gguf$", n) for n in bases):
             raise NotImplementedError("split GGUF models (joined bases) are not built")
+        seeds = []
+        if self.method != "m30":
+            # quants without their BF16 model: the senior quant of each group is coded like a base and
+            # the others are derived from it (repo3.py:1388-1394)
+            seeds = pick_seeds([heads[n][1] for n in bases], {n: heads[n][1] for n in derived})
+            bases = {**bases, **{n: derived[n] for n in seeds}}
+            derived = {n: p for n, p in derived.items() if n not in seeds}
         base_names = [{t.name for t in heads[n][1]} for n in bases]
-        orphans = [n for n in derived if not any({t.name for t in heads[n][1]} & s for s in base_names)]
-        if orphans and self.method != "m30":
-            raise NotImplementedError(f"quantized files without a base ({orphans[0]}): the seed codec is not built")
         total = sum(os.path.getsize(p) for p in files.values())
         hashes = {}
         w = container.Writer(output)
@@ -678,7 +748,7 @@ class Packer:
             loaded = []
             for i, (n, p) in enumerate(bases.items()):
                 host = np.memmap(p, np.uint8, "r") if os.path.getsize(p) else np.zeros(0, np.uint8)
-                loaded.append((host, _Base(i, n, host, None, gguf.GGUF(host))))
+                loaded.append((host, _Base(i, n, host, None, gguf.GGUF(host), seed=n in seeds)))
             # the repository's importance per tensor on the device (the grid QR types read it)
             imx_vecs = {k: np.asarray(v, np.float32) for k, v in imx_all.items()}
             flat = np.concatenate(list(imx_vecs.values())) if imx_vecs else np.zeros(1, np.float32)
@@ -692,9 +762,13 @@ class Packer:
             names = list(derived)
             entries, chunks = [None] * len(names), {}
             per_base = collections.defaultdict(list)
+            alone = []                                 # files no base shares a tensor with
             for fi, n in enumerate(names):
                 ts = heads[n][1]
                 common = [len({t.name for t in ts} & s) for s in base_names]
+                if not common or max(common) == 0:
+                    alone.append((fi, n, ts))
+                    continue
                 best = [k for k, c in enumerate(common) if c == max(common)][0]
                 per_base[best].append((fi, n, ts))
             # derived files: per base, grouped by tensor order; windows over each group's order
@@ -772,7 +846,13 @@ class Packer:
                 hashes[n] = self.hasher.submit(_ws, data)
                 entries[fi] = {"name": n, "size": len(data), "base": b.index, "plan": []}
                 zjobs[fi] = self.zpool.submit(lambda e, d, h: (e, None, zstd.compress_with(
-                    d, zstd.Params(self.level, window_log=25, threads=4), h)), entries[fi], data, b.header)
+                    d, _zc_params(self.level, d), h)), entries[fi], data, b.header)
+                order_done.append(fi)
+            for fi, n, ts in alone:
+                data = open(derived[n], "rb").read()
+                hashes[n] = self.hasher.submit(_ws, data)
+                entries[fi] = {"name": n, "size": len(data), "base": None, "plan": []}
+                zjobs[fi] = self.zpool.submit(self._code_alone, entries[fi], data, ts)
                 order_done.append(fi)
             for fi in order_done:
                 entries[fi], qchunk, fchunk = zjobs[fi].result()
@@ -789,14 +869,16 @@ class Packer:
             side.shutdown()
             aux.shutdown()
             phase("bases and other files coded")
-            manifest = {"method": METHODS[self.method], "bases": list(bases), "seeds": [], "files": entries,
+            manifest = {"method": METHODS[self.method], "bases": list(bases), "seeds": seeds, "files": entries,
                         "extras": {"bundle": list(ex), "single": big}}
             if self.stats["qr_grid"] or self.stats["ref"]:
                 manifest["needs"] = "0.3.0"
             w.put("manifest", zstd.compress(json.dumps(manifest).encode(), 19))
             hashes = {n: (h.result() if hasattr(h, "result") else h) for n, h in hashes.items()}
             phase("checksums")
-            catalog = [{"name": n, "size": os.path.getsize(p), "hash": hashes[n], "role": roles[n] or "file",
+            q8_files = {e["name"] for e in entries if e and e.get("codec") == "q8"}
+            catalog = [{"name": n, "size": os.path.getsize(p), "hash": hashes[n],
+                        "role": "derived, M21" if n in q8_files else roles[n] or "file",
                         "stored": self.sizes.get(n)} for n, p in files.items()]
             w.close({"tool": tool, "method": METHODS[self.method], "created": created or _created(), "hash": "sha256",
                      "files": catalog, "total": total})
@@ -908,8 +990,9 @@ class Unpacker:
             return self._run_m30(r, meta, manifest, outdir, patterns, t0)
         if not manifest["method"].startswith(("M29", "M28")):
             raise NotImplementedError(f"archive method {manifest['method']!r}: only M28 / M29 / M30 archives are read here")
-        if manifest.get("seeds") or manifest.get("joined") or manifest.get("imx_fit"):
-            raise NotImplementedError("seeds, split models and fitted importance are not built")
+        if manifest.get("joined") or manifest.get("imx_fit"):
+            raise NotImplementedError("split models and fitted importance are not built")
+        seeds = set(manifest.get("seeds", []))
         cat = {f["name"]: f for f in meta["files"]}
         want = set(select_names(meta["files"], patterns))
         mf = manifest["files"]
@@ -978,6 +1061,14 @@ class Unpacker:
         bases = {}
         for i in sorted(need_b):
             name = manifest["bases"][i]
+            if name in seeds:                               # a seed: its file decoded by parts (seed.py)
+                data = SeedCodec(stream=self.stream.handle).decompress(r.get(f"b{i}"))
+                d = dev.DeviceArray.from_host(data, self.stream.handle)
+                bases[i] = _Base(i, name, data, d, gguf.GGUF(data, light=True), seed=True)
+                if name in want:
+                    jobs.append(self.files.submit(check_write, name, data))
+                log(self.verbose, f"  seed {name}: decoded, {time.perf_counter() - t0:.1f} s")
+                continue
             ch = unpack(memoryview(r.get(f"b{i}")))
             if "r2" in ch:
                 d, rest = r2.BF16v2(stream=self.stream.handle).decompress(unpack(ch["r2"]), device="full")
@@ -987,7 +1078,7 @@ class Unpacker:
                 first = min([t[0] for t in lay["t"]] + [lay["size"]])
                 rest = d.view(0, (first,), np.uint8).to_host(stream=self.stream.handle)
             else:
-                raise NotImplementedError(f"base {name}: a base chunk of a kind not built here (the seed codec)")
+                raise ValueError(f"base {name}: a base chunk of an unknown kind")
             g = gguf.GGUF(rest.tobytes(), light=True)     # the header is the start of the rest part
             b = _Base(i, name, rest, d, g)
             bases[i] = b
@@ -1011,6 +1102,11 @@ class Unpacker:
             m = mf[i]
             b = bases.get(m["base"]) if m["base"] is not None else None
             resid = self.pool.acquire(m["size"])[:m["size"]]
+            if m.get("codec") == "q8":                      # a base-less file coded by the Q8_0 codec
+                s_ = dev.Stream()
+                Q8Parts(stream=s_.handle).decompress(r.get(f"f{i}"), out=resid)
+                s_.synchronize()
+                return resid
             return zstd.decompress_into(r.get(f"f{i}"), resid, b.header if b is not None else None)
 
         nxt = self.ahead.submit(residual_of, order[0]) if order else None
@@ -1080,7 +1176,7 @@ class Unpacker:
         def tensor(name):
             bt = b.by_name[name]
             return residual.Tensor(name, ttype[name], bt.shape[0], R.view(tens[name].offset, (tens[name].nbytes,), np.uint8),
-                                   b.view(bt), imatrix=imx_map.get(name), base_type=bt.type, numel=tens[name].numel)
+                                   b.view(bt, st), imatrix=imx_map.get(name), base_type=bt.type, numel=tens[name].numel)
 
         for e in plan:
             name, kind, v = e[0], e[1], e[2]

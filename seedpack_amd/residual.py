@@ -22,12 +22,12 @@ import numpy as np
 from . import device as dev
 from ._lib import check, lib
 from .gpuquant import GPUQuant
-from .qr import QR_TYPES
+from .qr import QR_TYPES, SELF_TYPES as QR_SELF_TYPES
 from .requant import QFUN, VARIANTS
 
 F32, F16, BF16 = 0, 1, 30
 FLOAT_TYPES = (F32, F16, BF16)
-SEED_TYPES = set(QFUN) | {F32, F16, BF16}       # base tensor types the QR coder takes as seeds (qr.py:41)
+SEED_TYPES = QR_SELF_TYPES | {F32, F16, BF16}   # base tensor types the QR coder takes as seeds (qr.py:41)
 UNIT_W = 100                                     # variant offset: unit importance weights (repo3.py:540)
 RECOV = 1000                                     # variant k * RECOV + v: fitted importance set k (repo3.py:541)
 

@@ -137,6 +137,57 @@ def test_method_m30(sibling_repo, tmp_path, with_base):
         assert open(os.path.join(src, n), "rb").read() == open(os.path.join(out, n), "rb").read(), n
 
 
+def _gguf_file(path, kv, tensors):
+    """a GGUF of [(name, shape, type, payload bytes)]"""
+    head, where, size = gguf.header_bytes(kv, [(n, sh, t) for n, sh, t, _ in tensors])
+    out = np.zeros(size, np.uint8)
+    out[:len(head)] = np.frombuffer(head, np.uint8)
+    for (_, _, _, payload), (off, nb) in zip(tensors, where):
+        out[off:off + nb] = np.frombuffer(payload, np.uint8)
+    with open(path, "wb") as f:
+        f.write(out.tobytes())
+
+
+def test_seed_repo_without_base(sibling_repo, tmp_path):
+    """quantized files without their BF16 model (method m29): the senior quant (Q8_0) becomes the seed,
+    coded by the seed codec (its token_embd row-predicted by the Q8_0 codec); the other quants are
+    derived from its dequantized tensors and QR-coded with its quantized tensors as seeds. A second
+    model's lone quant is a seed of its own; a GGUF without tensors is stored alone. Every file
+    extracts byte-identical."""
+    import shutil
+    from tests.golden.q8_cases import q8_blocks
+    src = str(tmp_path / "src")
+    os.makedirs(src)
+    for n in os.listdir(sibling_repo):
+        if n != "model-BF16.gguf":
+            shutil.copy(os.path.join(sibling_repo, n), src)
+    g = np.random.Generator(np.random.PCG64(77))
+    _gguf_file(os.path.join(src, "mmproj-Q8_0.gguf"), {"general.architecture": "clip"},
+               [("v.blk.0.attn_q.weight", (256, 64), 8, q8_blocks(g.normal(0, 0.02, (64, 256)).astype(np.float32)).tobytes()),
+                ("v.post_ln.weight", (256,), 0, np.ones(256, np.float32).tobytes())])
+    _gguf_file(os.path.join(src, "vocab.gguf"), {"general.architecture": "qwen35", "tokenizer.ggml.model": "gpt2"}, [])
+    a = str(tmp_path / "seed.seedpack")
+    say("case seed repo: pack")
+    stats = repo.pack_repo([src], a)
+    r = container.Reader(a)
+    man = json.loads(zstd.decompress(r.get("manifest")))
+    assert sorted(man["seeds"]) == ["mmproj-Q8_0.gguf", "model-Q8_0.gguf"] and man["bases"] == man["seeds"]
+    bi = man["bases"].index("model-Q8_0.gguf")
+    assert list(unpack(memoryview(r.get(f"b{bi}"))))[:2] == ["layout", "q8"]
+    files = {m["name"]: m for m in man["files"]}
+    assert files["vocab.gguf"]["base"] is None and files["vocab.gguf"]["plan"] == []
+    assert all(files[n]["base"] == bi for n in files if n.startswith("model-"))
+    kinds = {e[1] for n in files for e in files[n]["plan"]}
+    assert "qr" in kinds, kinds
+    assert stats["stats"]["qr"] > 0
+    say("case seed repo: unpack", stats["stats"])
+    out = str(tmp_path / "out")
+    res = repo.unpack_repo(a, out)
+    assert not res["bad"] and not res["missing"], res
+    for n in sorted(os.listdir(src)):
+        assert open(os.path.join(src, n), "rb").read() == open(os.path.join(out, n), "rb").read(), n
+
+
 def test_small_repo_archive_layout(small_repo):
     root, arc, sizes, stats = small_repo
     r = container.Reader(arc)
