@@ -504,6 +504,55 @@ def qr_cfg1(stream, reps=3):
     return res
 
 
+def q8_codec(stream, layers=4):
+    """the Q8_0 codec (q8.Q8Parts over M22: a seed's Q8_0 part) on a Qwen3.5-9B-shaped Q8_0 file:
+    token_embd and output 151936 x 4096 and `layers` transformer blocks, Q8_0 of N(0, 0.02) weights;
+    compress (row planner on token_embd) and decompress timed from a host file to a host file, the
+    result byte-identical; per-phase times with the stream drained between phases"""
+    from seedpack_amd import device as dev
+    from seedpack_amd import gguf, q8
+    from seedpack_amd._lib import check, lib
+    from seedpack_amd.gpuquant import quantize_into
+    st = stream.handle
+    shapes = [("token_embd.weight", (4096, 151936))]
+    for i in range(layers):
+        shapes += [(f"blk.{i}.attn_q.weight", (4096, 4096)), (f"blk.{i}.attn_k.weight", (4096, 1024)),
+                   (f"blk.{i}.attn_v.weight", (4096, 1024)), (f"blk.{i}.attn_output.weight", (4096, 4096)),
+                   (f"blk.{i}.ffn_gate.weight", (4096, 12288)), (f"blk.{i}.ffn_up.weight", (4096, 12288)),
+                   (f"blk.{i}.ffn_down.weight", (12288, 4096))]
+    shapes.append(("output.weight", (4096, 151936)))
+    head, where, size = gguf.header_bytes({"general.architecture": "qwen35", "general.alignment": 32},
+                                          [(n, sh, 8) for n, sh in shapes])
+    log(f"bench q8: building a {size / 1e9:.2f} GB Q8_0 file")
+    host = dev.pinned(size)
+    host[:] = 0
+    host[:len(head)] = np.frombuffer(head, np.uint8)
+    for k, ((n, sh), (off, nb)) in enumerate(zip(shapes, where)):
+        nw = sh[0] * sh[1]
+        w = dev.DeviceArray(nw, np.uint16)
+        check(lib().spa_synth_normal_bf16(w.ptr, nw, 0x0880 + 7 * k, 0.02, st))
+        y = dev.DeviceArray(nb, np.uint8)
+        quantize_into(8, w, sh[0], y, None, 0, st)
+        check(lib().spa_memcpy_d2h(host[off:].ctypes.data, y.ptr, nb, st))
+        del w, y
+    stream.synchronize()
+    g = gguf.GGUF(host)
+    parts = q8.Q8Parts(stream=st, timing=True)
+    t0 = time.perf_counter()
+    buf = parts.compress(host, g=g)
+    t1 = time.perf_counter()
+    dec = q8.Q8Parts(stream=st, timing=True)
+    out = dec.decompress(buf)
+    t2 = time.perf_counter()
+    ok = bool(np.array_equal(out, host))
+    res = {"file_bytes": size, "coded_bytes": len(buf), "ratio": round(len(buf) / size, 4), "parts": parts.parts,
+           "compress_s": round(t1 - t0, 3), "compress_GB_s": round(size / (t1 - t0) / 1e9, 3),
+           "decompress_s": round(t2 - t1, 3), "decompress_GB_s": round(size / (t2 - t1) / 1e9, 3),
+           "identical": ok, "compress_phases_s": parts.c.timing, "decompress_phases_s": dec.c.timing}
+    log(f"bench q8: {res}")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -526,6 +575,10 @@ def main():
                     help="only write the --pack repository into --repo-dir and keep it (for a later --reuse-repo run)")
     ap.add_argument("--reuse-repo", action="store_true",
                     help="--pack on the repository a --write-repo run left in --repo-dir (kept)")
+    ap.add_argument("--q8", action="store_true",
+                    help="only the Q8_0 codec (a seed's Q8_0 part) on a Qwen3.5-9B-shaped Q8_0 file; prints its "
+                         "result, no JSON line")
+    ap.add_argument("--q8-layers", type=int, default=4, help="transformer blocks of the --q8 file")
     ap.add_argument("--codecs", action="store_true",
                     help="only the coding stages (QR on configurations 1 and 3, the R2 base codec), for rocprofv3 "
                          "kernel-trace runs; prints their results, no JSON line")
@@ -538,6 +591,10 @@ def main():
                              write_only=a.write_repo)
         if not a.write_repo:
             print(json.dumps({"pack_cfg4": pk, "unpack_cfg5": upk}))
+        return None
+    if a.q8:
+        from seedpack_amd import device as dev
+        print(json.dumps({"q8_codec": q8_codec(dev.Stream(), a.q8_layers)}))
         return None
     if a.codecs:
         from seedpack_amd import device as dev

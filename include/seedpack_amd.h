@@ -288,11 +288,14 @@ int spa_q8_col_stats(const void* blocks, int first, int nbr, int64_t nrows, cons
  * of 8), and eq[i] = rows ra[i] and rb[i] are byte-equal (gpu2.py:693-716). */
 int spa_q8_row_hash(const void* blocks, int first, int nbr, int64_t nrows, const uint64_t* mult, uint64_t* h, void* stream);
 int spa_q8_rows_equal(const void* blocks, int first, int nbr, const int* ra, const int* rb, int n, uint8_t* eq, void* stream);
-/* The encoder's reciprocals rcp[t][s] of freq[t][s] for ntab used tables. */
+/* The encoder's reciprocals rcp[t][s] of freq[t][s] for ntab used tables; the decoders' tables lut[t][slot] =
+ * symbol | (freq - 1) << 8 | (slot - cum[symbol]) << 20 (4096 words per table). */
 int spa_q8_rcp(const uint16_t* freq, int ntab, uint32_t* rcp, void* stream);
+int spa_q8_lut32(const uint16_t* freq, const uint32_t* cum, int ntab, uint32_t* lut, void* stream);
 /* Phase A (scale bytes, maximum's rank and value; 4096 blocks per segment): histogram, encode (slots of cap
  * bytes written downwards, out_len[s] = length or 0xffffffff on overflow), decode (reads past in_bytes see
- * zeros). bcf / spread per block-column, perm / rankof [block-column][32], scls per column. */
+ * zeros; lut from spa_q8_lut32). bcf / spread per block-column, perm / rankof [block-column][32], scls per
+ * column. */
 int spa_q8_hist_a(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, int ntens, int nblocks,
                   const uint8_t* bcf, const uint8_t* spread, const uint8_t* rankof, const uint8_t* scls, uint32_t* counts,
                   void* stream);
@@ -302,8 +305,7 @@ int spa_q8_enc_a(const void* blocks, const uint8_t* pos, const uint8_t* skip, co
                  void* stream);
 int spa_q8_dec_a(const void* in, uint64_t in_bytes, const uint64_t* in_off, const uint8_t* skip, const void* meta, int ntens,
                  int nblocks, const uint8_t* bcf, const uint8_t* spread, const uint8_t* perm, const uint8_t* scls,
-                 const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* blocks, uint8_t* pos,
-                 void* stream);
+                 const int* remap, const uint32_t* lut, void* blocks, uint8_t* pos, void* stream);
 /* Phase B (the other 31 weights, 1024 blocks per segment). The histogram takes work items of 12 bytes
  * {tensor, first block, blocks} (blocks of one tensor, a workgroup each) and counts into the tensor's qset. */
 int spa_q8_hist_b(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, int ntens, int nblocks,
@@ -314,8 +316,7 @@ int spa_q8_enc_b(const void* blocks, const uint8_t* pos, const uint8_t* skip, co
                  const uint32_t* cum, const uint32_t* rcp, void* out, uint64_t cap, uint32_t* out_len, void* stream);
 int spa_q8_dec_b(const void* in, uint64_t in_bytes, const uint64_t* in_off, const uint8_t* skip, const void* meta, int ntens,
                  int nblocks, const int16_t* cfi, const uint8_t* scls, const int* row_m, int qbase, const int* remap,
-                 const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* blocks, const uint8_t* pos,
-                 void* stream);
+                 const uint32_t* lut, void* blocks, const uint8_t* pos, void* stream);
 /* Phase C. Row prediction pint[r][j] (int8) from up to 4 parents per row (par / coef [rows][4], mu per
  * column): all rows of one tensor (encoder), or the entries (slot, row) of one wave of every predicted
  * tensor (decoder; slots: 32-byte records {i64 rbase, i64 pbase, i32 first, nbr, mubase, pad}). Segments:
@@ -324,18 +325,22 @@ int spa_q8_predict(const void* blocks, int first, int nbr, int64_t nrows, const 
                    int8_t* pint, void* stream);
 int spa_q8_predict_multi(const void* blocks, const int* ent_slot, const int* ent_row, int nent, int cmax, const void* slots,
                          const int* par, const float* coef, const float* mu, int8_t* pint, void* stream);
+/* Per block of 32 predictions (nblk blocks of pint): prk[j] the rank of position j by |prediction|
+ * descending (ties by position), pinv[rank] its position, rctx the rank context min(max |p| / 16, 7)
+ * (gpu3.py:48-60); the phase C coders read these (prk / pinv laid out as pint, rctx one per block). */
+int spa_q8_ranks(const int8_t* pint, int64_t nblk, int8_t* prk, int8_t* pinv, int8_t* rctx, void* stream);
 int spa_q8_hist_c(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, const void* segs, int nseg,
                   const void* slots, const int16_t* cfi, const int* row_m, const int8_t* fbin, const int8_t* pint,
-                  uint32_t* counts, void* stream);
+                  const int8_t* prk, const int8_t* pinv, const int8_t* rctx, uint32_t* counts, void* stream);
 int spa_q8_enc_c(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, const void* segs, int nseg,
                  const void* slots, const int16_t* cfi, const int* row_m, const int8_t* fbin, const int8_t* pint,
-                 const int* remap, const uint16_t* freq, const uint32_t* cum, const uint32_t* rcp, void* out, uint64_t cap,
-                 uint32_t* out_len, void* stream);
+                 const int8_t* prk, const int8_t* pinv, const int8_t* rctx, const int* remap, const uint16_t* freq,
+                 const uint32_t* cum, const uint32_t* rcp, void* out, uint64_t cap, uint32_t* out_len, void* stream);
 /* decodes segments [seg0, seg1) (one wave) */
 int spa_q8_dec_c(const void* in, uint64_t in_bytes, const uint64_t* in_off, int seg0, int seg1, const uint8_t* skip,
                  const void* meta, const void* segs, int nseg, const void* slots, const int16_t* cfi, const int* row_m,
-                 const int8_t* fbin, const int8_t* pint, const int* remap, const uint16_t* freq, const uint32_t* cum,
-                 const uint8_t* lut, void* blocks, uint8_t* pos, void* stream);
+                 const int8_t* fbin, const int8_t* pint, const int8_t* prk, const int8_t* pinv, const int8_t* rctx,
+                 const int* remap, const uint32_t* lut, void* blocks, uint8_t* pos, void* stream);
 /* The row-prediction planner (gpu3.py:272-353). W[r][c] = q * d (float32, exact); W -= mu per column; Wq =
  * clip(rint(W / nrm[r] * 127), -127, 127) in float64, 0 for rows that are not valid. */
 int spa_q8_row_matrix(const void* blocks, int first, int nbr, int64_t nrows, float* W, void* stream);

@@ -50,26 +50,45 @@ __global__ __launch_bounds__(TILE) void k_rows(const T* __restrict__ x, int64_t 
     if (row < nr) out[row] = s;
 }
 
+// Column sums in row order, 64 columns per workgroup: the 256 lanes load a tile of CT_ROWS rows x 64
+// columns (coalesced 256-byte row pieces, the next tile's values held in registers while the current
+// one is summed), lanes 0..63 add their column's values from LDS in row order (one float64 chain per
+// column, as the reference's lane per column).
+constexpr int CT_ROWS = 128;
 __global__ __launch_bounds__(256) void k_cols(const float* __restrict__ x, int64_t nr, int64_t nc, int sq,
                                               const uint8_t* __restrict__ mask, double* __restrict__ out) {
-    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= nc) return;
-    double s = 0.0;
-    constexpr int AHEAD = 8;
-    for (int64_t r0 = 0; r0 < nr; r0 += AHEAD) {
-        float v[AHEAD];
-        bool on[AHEAD];
+    __shared__ float tile[CT_ROWS][64 + 1];
+    __shared__ uint8_t on[CT_ROWS];
+    const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;          // grp: rows grp, grp + 4, ...
+    const int64_t c0 = (int64_t)blockIdx.x * 64, c = c0 + lane;
+    constexpr int PER = CT_ROWS / 4;
+    float v[PER];
+    auto fetch = [&](int64_t r0) {
 #pragma unroll
-        for (int k = 0; k < AHEAD; ++k) {
-            const int64_t r = r0 + k;
-            on[k] = r < nr && (!mask || mask[r]);
-            v[k] = r < nr ? x[r * nc + c] : 0.f;
+        for (int k = 0; k < PER; ++k) {
+            const int64_t r = r0 + grp + 4 * k;
+            v[k] = (r < nr && c < nc) ? x[r * nc + c] : 0.f;
         }
+    };
+    double s = 0.0;
+    fetch(0);
+    for (int64_t r0 = 0; r0 < nr; r0 += CT_ROWS) {
 #pragma unroll
-        for (int k = 0; k < AHEAD; ++k)
-            if (on[k]) { const double d = (double)v[k]; s = s + (sq ? d * d : d); }
+        for (int k = 0; k < PER; ++k) tile[grp + 4 * k][lane] = v[k];
+        if (threadIdx.x < CT_ROWS) {
+            const int64_t r = r0 + threadIdx.x;
+            on[threadIdx.x] = r < nr && (!mask || mask[r]);
+        }
+        __syncthreads();
+        if (r0 + CT_ROWS < nr) fetch(r0 + CT_ROWS);          // in flight while this tile is summed
+        if (threadIdx.x < 64 && c < nc) {
+            const int n = nr - r0 < CT_ROWS ? (int)(nr - r0) : CT_ROWS;
+            for (int r = 0; r < n; ++r)
+                if (on[r]) { const double d = (double)tile[r][lane]; s = s + (sq ? d * d : d); }
+        }
+        __syncthreads();
     }
-    out[c] = s;
+    if (threadIdx.x < 64 && c < nc) out[c] = s;
 }
 
 // X: n x k x d; out[c][a][b] = sum_t X[c][a][t] X[c][b][t] (a workgroup per batch element c)
@@ -239,7 +258,7 @@ int spa_dm_cols(const float* x, int64_t nr, int64_t nc, int sq, const uint8_t* m
     if (nr < 0 || nc < 0) return fail(SPA_ERR_ARG, "spa_dm_cols: negative shape");
     if (!nc) return SPA_OK;
     if (!out || (nr && !x)) return fail(SPA_ERR_ARG, "spa_dm_cols: null pointer");
-    hipLaunchKernelGGL(spa::k_cols, dim3(spa::blocks_for(nc, 256)), dim3(256), 0, (hipStream_t)stream, x, nr, nc, sq,
+    hipLaunchKernelGGL(spa::k_cols, dim3(spa::blocks_for(nc, 64)), dim3(256), 0, (hipStream_t)stream, x, nr, nc, sq,
                        mask, out);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;

@@ -98,15 +98,25 @@ struct Enc {
     }
 };
 
+// The decoder's table: per (table, slot) one 32-bit word, symbol | (freq - 1) << 8 | (slot - cum) << 20,
+// so that a step is one dependent load (the word) instead of two (symbol, then its freq and cum).
+__global__ __launch_bounds__(256) void k_lut32(const uint16_t* __restrict__ freq, const uint32_t* __restrict__ cum, int ntab,
+                                               uint32_t* __restrict__ lut) {
+    const int tt = blockIdx.x;
+    if (tt >= ntab) return;
+    for (int s = threadIdx.x; s < 256; s += blockDim.x) {
+        const uint32_t f = freq[tt * 256 + s], c = cum[tt * 257 + s];
+        for (uint32_t k = 0; k < f; ++k) lut[(size_t)tt * PSCALE + c + k] = (uint32_t)s | ((f - 1) << 8) | (k << 20);
+    }
+}
+
 // reads past the stream's end give zeros (a corrupt stream decodes to garbage inside the buffers)
 struct Dec {
     uint32_t x;
     const uint8_t* ptr;
     const uint8_t* endp;
     const int* remap;
-    const uint16_t* freq;
-    const uint32_t* cum;
-    const uint8_t* lut;
+    const uint32_t* lut;
     __device__ __forceinline__ uint32_t byte() { const uint32_t b = ptr < endp ? *ptr : 0u; ++ptr; return b; }
     __device__ __forceinline__ void start(const uint8_t* in, uint64_t in_bytes, uint64_t off) {
         ptr = in + (off < in_bytes ? off : in_bytes);
@@ -114,13 +124,13 @@ struct Dec {
         x = 0;
         for (int i = 0; i < 4; ++i) x = (x << 8) | byte();
     }
-    __device__ __forceinline__ int get(int tab) {
-        const int tt = max(remap[tab], 0);            // a table the encoder never used: only in a corrupt stream
-        const uint32_t slot = x & (PSCALE - 1);
-        const int s = lut[(size_t)tt * PSCALE + slot];
-        x = freq[tt * 256 + s] * (x >> PB) + slot - cum[tt * 257 + s];
+    __device__ __forceinline__ int row(int tab) const { return max(remap[tab], 0); }   // < 0: only in a corrupt stream
+    __device__ __forceinline__ int get(int tab) { return get_row(row(tab)); }
+    __device__ __forceinline__ int get_row(int tt) {
+        const uint32_t e = lut[(size_t)tt * PSCALE + (x & (PSCALE - 1))];
+        x = ((e >> 8) & 4095u) * (x >> PB) + (x >> PB) + (e >> 20);     // freq * (x >> PB) + slot - cum
         while (x < RANS_L) x = (x << 8) | byte();
-        return s;
+        return (int)(e & 255u);
     }
 };
 
@@ -292,14 +302,13 @@ __global__ __launch_bounds__(64) void k_enc_a(const uint8_t* __restrict__ blocks
 
 __global__ __launch_bounds__(64) void k_dec_a(const uint8_t* __restrict__ in, uint64_t in_bytes,
                                               const uint64_t* __restrict__ in_off, AArgs A, const int* __restrict__ remap,
-                                              const uint16_t* __restrict__ freq, const uint32_t* __restrict__ cum,
-                                              const uint8_t* __restrict__ lut, uint8_t* __restrict__ blocks,
+                                              const uint32_t* __restrict__ lut, uint8_t* __restrict__ blocks,
                                               uint8_t* __restrict__ pos) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x, b0 = s * SEGA;
     if (b0 >= A.nblocks) return;
     const int b1 = min(b0 + SEGA, A.nblocks);
     int t = tensor_of(A.M, A.ntens, b0);
-    Dec d{0, nullptr, nullptr, remap, freq, cum, lut};
+    Dec d{0, nullptr, nullptr, remap, lut};
     d.start(in, in_bytes, in_off[s]);
     int prev = 0;
     for (int b = b0; b < b1; ++b) {
@@ -401,14 +410,15 @@ __global__ __launch_bounds__(64) void k_enc_b(const uint8_t* __restrict__ blocks
 
 __global__ __launch_bounds__(64) void k_dec_b(const uint8_t* __restrict__ in, uint64_t in_bytes,
                                               const uint64_t* __restrict__ in_off, BArgs B, const int* __restrict__ remap,
-                                              const uint16_t* __restrict__ freq, const uint32_t* __restrict__ cum,
-                                              const uint8_t* __restrict__ lut, uint8_t* __restrict__ blocks,
+                                              const uint32_t* __restrict__ lut, uint8_t* __restrict__ blocks,
                                               const uint8_t* __restrict__ pos) {
     const int s = blockIdx.x * blockDim.x + threadIdx.x, b0 = s * SEGB;
     if (b0 >= B.nblocks) return;
     const int b1 = min(b0 + SEGB, B.nblocks);
     int t = tensor_of(B.M, B.ntens, b0);
-    Dec d{0, nullptr, nullptr, remap, freq, cum, lut};
+    const int16_t* __restrict__ cfi = B.cfi;
+    const uint8_t* __restrict__ scls = B.scls;
+    Dec d{0, nullptr, nullptr, remap, lut};
     d.start(in, in_bytes, in_off[s]);
     for (int b = b0; b < b1; ++b) {
         while (t + 1 < B.ntens && b >= B.M[t + 1].first) ++t;
@@ -417,11 +427,20 @@ __global__ __launch_bounds__(64) void k_dec_b(const uint8_t* __restrict__ in, ui
         int c0;
         const int sh = b_shift(B, B.M[t], b, blk, c0), p = pos[b];
         const int qb = B.qbase + B.M[t].qset * TQ;
+        // the block's 31 magnitude and sign tables do not depend on the stream: looked up before the
+        // serial steps, which then wait on one table load each
+        int tm[32], ts[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const int c = c0 + j, pb = pbin(cfi[c], sh);
+            tm[j] = d.row(qb + pb);
+            ts[j] = d.row(qb + Q_SG + pb * 16 + scls[c]);
+        }
+#pragma unroll
         for (int j = 0; j < 32; ++j) {
             if (j == p) continue;
-            const int c = c0 + j, pb = pbin(B.cfi[c], sh);
-            const int mag = d.get(qb + pb);
-            const int sg = mag ? d.get(qb + Q_SG + pb * 16 + B.scls[c]) : 0;
+            const int mag = d.get_row(tm[j]);
+            const int sg = mag ? d.get_row(ts[j]) : 0;
             blk[2 + j] = (uint8_t)((sg ? -mag : mag) & 0xff);
         }
     }
@@ -479,30 +498,39 @@ __global__ __launch_bounds__(256) void k_predict_multi(const uint8_t* __restrict
                                                mu + S.mubase);
 }
 
-__device__ __forceinline__ int rank_of(const int8_t* pr, int p) {          // gpu3.py:48-52
-    const int ap = abs((int)pr[p]);
-    int r = 0;
+// The maximum's rank among the block's 32 predictions (|prediction| descending, ties by position) and
+// the rank context min(max |prediction| / 16, 7) (gpu3.py:48-60), per block before the serial coders:
+// prk[b][j] = rank of position j, pinv[b][rank] = position, rctx[b]. A workgroup per 8 blocks, a lane
+// per (block, position) over the block's predictions in LDS.
+__global__ __launch_bounds__(256) void k_ranks(const int8_t* __restrict__ pint, int64_t nblk, int8_t* __restrict__ prk,
+                                               int8_t* __restrict__ pinv, int8_t* __restrict__ rctx) {
+    __shared__ int a[256];
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int j = threadIdx.x & 31, base = threadIdx.x & ~31;
+    const bool in = i < nblk * 32;
+    const int v = in ? pint[i] : 0;
+    a[threadIdx.x] = v < 0 ? -v : v;
+    __syncthreads();
+    if (!in) return;
+    const int aj = a[threadIdx.x];
+    int r = 0, m = 0;
+#pragma unroll
     for (int k = 0; k < 32; ++k) {
-        const int a = abs((int)pr[k]);
-        r += (a > ap) || (a == ap && k < p);
+        const int ak = a[base + k];
+        r += (ak > aj) || (ak == aj && k < j);
+        m = ak > m ? ak : m;
     }
-    return r;
+    prk[i] = (int8_t)r;
+    pinv[(i & ~(int64_t)31) + r] = (int8_t)j;
+    if (j == 0) rctx[i >> 5] = (int8_t)min(m / 16, 7);
 }
-__device__ __forceinline__ int pos_of_rank(const int8_t* pr, int rk) {
-    for (int j = 0; j < 32; ++j)
-        if (rank_of(pr, j) == rk) return j;
-    return 0;
-}
-__device__ __forceinline__ int rank_ctx(const int8_t* pr) {
-    int m = 0;
-    for (int k = 0; k < 32; ++k) m = max(m, abs((int)pr[k]));
-    return min(m / 16, 7);
-}
+
 __device__ __forceinline__ int mx_ctx(const int8_t* pr, int p) { const int v = pr[p]; return (v < 0) * 8 + min(abs(v) / 16, 7); }
 
 struct CArgs {
     const uint8_t* skip; const Meta* M; const CSeg* seg; int nseg; const Slot* slots;
     const int16_t* cfi; const int* row_m; const int8_t* fbin; const int8_t* pint;
+    const int8_t* prk; const int8_t* pinv; const int8_t* rctx;       // k_ranks' tables, laid out as pint
 };
 
 __device__ __forceinline__ int c_ctx(int cf, int sh, int fb) { return clampi(pbin(cf, sh) + fb, 0, 63); }
@@ -529,9 +557,10 @@ __global__ __launch_bounds__(256) void k_hist_c(const uint8_t* __restrict__ bloc
             if (A.skip[b] & 1) continue;
             const uint8_t* blk = blocks + b * 34;
             const int sh = A.row_m[T.rowbase + r] - bits_of(blk) - T.off, p = pos[b];
-            const int8_t* pr = A.pint + S.pbase + (size_t)r * C + kk * 32;
+            const size_t q0 = S.pbase + (size_t)r * C + kk * 32;
+            const int8_t* pr = A.pint + q0;
             const int fb = A.fbin[S.rbase + r];
-            int idx = (64 + rank_ctx(pr)) * 256 + rank_of(pr, p);
+            int idx = (64 + A.rctx[q0 >> 5]) * 256 + A.prk[q0 + p];
             if (local) atomicAdd(&h[idx], 1u); else atomicAdd(&gl[idx], 1u);
             idx = (72 + mx_ctx(pr, p)) * 256 + blk[2 + p];
             if (local) atomicAdd(&h[idx], 1u); else atomicAdd(&gl[idx], 1u);
@@ -569,14 +598,15 @@ __global__ __launch_bounds__(64) void k_enc_c(const uint8_t* __restrict__ blocks
             if (A.skip[b] & 1) continue;
             const uint8_t* blk = blocks + b * 34;
             const int sh = A.row_m[T.rowbase + r] - bits_of(blk) - T.off, p = pos[b];
-            const int8_t* pr = A.pint + S.pbase + (size_t)r * C + kk * 32;
+            const size_t q0 = S.pbase + (size_t)r * C + kk * 32;
+            const int8_t* pr = A.pint + q0;
             for (int j = 31; j >= 0; --j) {
                 if (j == p) continue;
                 const int ctx = c_ctx(A.cfi[T.colbase + kk * 32 + j], sh, fb);
                 e.put(tb + ctx, (uint32_t)(((int8_t)blk[2 + j] - pr[j]) & 255));
             }
             e.put(tb + 72 + mx_ctx(pr, p), blk[2 + p]);
-            e.put(tb + 64 + rank_ctx(pr), (uint32_t)rank_of(pr, p));
+            e.put(tb + 64 + A.rctx[q0 >> 5], (uint32_t)A.prk[q0 + p]);
             if (e.ptr - start < 160) { out_len[s] = 0xffffffffu; return; }
         }
     }
@@ -585,8 +615,7 @@ __global__ __launch_bounds__(64) void k_enc_c(const uint8_t* __restrict__ blocks
 
 __global__ __launch_bounds__(64) void k_dec_c(const uint8_t* __restrict__ in, uint64_t in_bytes,
                                               const uint64_t* __restrict__ in_off, int seg0, int seg1, CArgs A,
-                                              const int* __restrict__ remap, const uint16_t* __restrict__ freq,
-                                              const uint32_t* __restrict__ cum, const uint8_t* __restrict__ lut,
+                                              const int* __restrict__ remap, const uint32_t* __restrict__ lut,
                                               uint8_t* __restrict__ blocks, uint8_t* __restrict__ pos) {
     const int s = seg0 + blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= seg1) return;
@@ -594,7 +623,9 @@ __global__ __launch_bounds__(64) void k_dec_c(const uint8_t* __restrict__ in, ui
     const Meta T = A.M[g.t];
     const Slot S = A.slots[g.slot];
     const int nbr = T.nb_row, C = nbr * 32, tb = g.slot * TPC;
-    Dec d{0, nullptr, nullptr, remap, freq, cum, lut};
+    const int16_t* __restrict__ cfi = A.cfi;
+    const int8_t* __restrict__ pint = A.pint;
+    Dec d{0, nullptr, nullptr, remap, lut};
     d.start(in, in_bytes, in_off[s]);
     for (int r = g.r0; r < g.r0 + g.nr; ++r) {
         const int fb = A.fbin[S.rbase + r];
@@ -603,17 +634,26 @@ __global__ __launch_bounds__(64) void k_dec_c(const uint8_t* __restrict__ in, ui
             if (A.skip[b] & 1) continue;
             uint8_t* blk = blocks + b * 34;
             const int sh = A.row_m[T.rowbase + r] - bits_of(blk) - T.off;
-            const int8_t* pr = A.pint + S.pbase + (size_t)r * C + kk * 32;
-            const int rk = d.get(tb + 64 + rank_ctx(pr));
-            const int p = pos_of_rank(pr, rk);
-            const int mx = d.get(tb + 72 + mx_ctx(pr, p));
+            const size_t q0 = S.pbase + (size_t)r * C + kk * 32;
+            // the block's predictions and its 31 residual tables, before the serial steps
+            int4 pw[2];
+            pw[0] = *reinterpret_cast<const int4*>(pint + q0);
+            pw[1] = *reinterpret_cast<const int4*>(pint + q0 + 16);
+            int tt[32];
+#pragma unroll
+            for (int j = 0; j < 32; ++j) tt[j] = d.row(tb + c_ctx(cfi[T.colbase + kk * 32 + j], sh, fb));
+            const int rk = d.get(tb + 64 + A.rctx[q0 >> 5]);
+            const int p = rk < 32 ? A.pinv[q0 + rk] : 0;          // a rank past 31: only in a corrupt stream
+            const int mx = d.get(tb + 72 + mx_ctx(pint + q0, p));
             blk[2 + p] = (uint8_t)mx;
             pos[b] = (uint8_t)p;
+#pragma unroll
             for (int j = 0; j < 32; ++j) {
                 if (j == p) continue;
-                const int ctx = c_ctx(A.cfi[T.colbase + kk * 32 + j], sh, fb);
-                const int sym = d.get(tb + ctx);
-                blk[2 + j] = (uint8_t)((pr[j] + sym) & 255);
+                const int w = (j < 16 ? (&pw[0].x)[(j & 15) >> 2] : (&pw[1].x)[(j & 15) >> 2]);
+                const int prj = (int)(int8_t)(w >> (8 * (j & 3)));
+                const int sym = d.get_row(tt[j]);
+                blk[2 + j] = (uint8_t)((prj + sym) & 255);
             }
         }
     }
@@ -1041,17 +1081,25 @@ int spa_q8_enc_a(const void* blocks, const uint8_t* pos, const uint8_t* skip, co
     return SPA_OK;
 }
 
+int spa_q8_lut32(const uint16_t* freq, const uint32_t* cum, int ntab, uint32_t* lut, void* stream) {
+    if (ntab < 0) return fail(SPA_ERR_ARG, "spa_q8_lut32: %d tables", ntab);
+    if (!ntab) return SPA_OK;
+    Q8_NONNULL(freq, cum, lut);
+    hipLaunchKernelGGL(k_lut32, dim3((unsigned)ntab), dim3(256), 0, (hipStream_t)stream, freq, cum, ntab, lut);
+    SPA_HIP_TRY(hipGetLastError());
+    return SPA_OK;
+}
+
 int spa_q8_dec_a(const void* in, uint64_t in_bytes, const uint64_t* in_off, const uint8_t* skip, const void* meta, int ntens,
                  int nblocks, const uint8_t* bcf, const uint8_t* spread, const uint8_t* perm, const uint8_t* scls,
-                 const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* blocks, uint8_t* pos,
-                 void* stream) {
+                 const int* remap, const uint32_t* lut, void* blocks, uint8_t* pos, void* stream) {
     if (int e = check_a(__func__, ntens, nblocks)) return e;
     if (!nblocks) return SPA_OK;
-    Q8_NONNULL(in, in_off, skip, meta, bcf, spread, perm, scls, remap, freq, cum, lut, blocks, pos);
+    Q8_NONNULL(in, in_off, skip, meta, bcf, spread, perm, scls, remap, lut, blocks, pos);
     AArgs A{skip, (const Meta*)meta, ntens, nblocks, bcf, spread, perm, nullptr, scls};
     const int nseg = (nblocks + SEGA - 1) / SEGA;
     hipLaunchKernelGGL(k_dec_a, dim3(nblk(nseg, 64)), dim3(64), 0, (hipStream_t)stream, (const uint8_t*)in, in_bytes, in_off,
-                       A, remap, freq, cum, lut, (uint8_t*)blocks, pos);
+                       A, remap, lut, (uint8_t*)blocks, pos);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }
@@ -1087,15 +1135,14 @@ int spa_q8_enc_b(const void* blocks, const uint8_t* pos, const uint8_t* skip, co
 
 int spa_q8_dec_b(const void* in, uint64_t in_bytes, const uint64_t* in_off, const uint8_t* skip, const void* meta, int ntens,
                  int nblocks, const int16_t* cfi, const uint8_t* scls, const int* row_m, int qbase, const int* remap,
-                 const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* blocks, const uint8_t* pos,
-                 void* stream) {
+                 const uint32_t* lut, void* blocks, const uint8_t* pos, void* stream) {
     if (int e = check_a(__func__, ntens, nblocks)) return e;
     if (!nblocks) return SPA_OK;
-    Q8_NONNULL(in, in_off, skip, meta, cfi, scls, row_m, remap, freq, cum, lut, blocks, pos);
+    Q8_NONNULL(in, in_off, skip, meta, cfi, scls, row_m, remap, lut, blocks, pos);
     BArgs B{skip, (const Meta*)meta, ntens, nblocks, cfi, scls, row_m, qbase};
     const int nseg = (nblocks + SEGB - 1) / SEGB;
     hipLaunchKernelGGL(k_dec_b, dim3(nblk(nseg, 64)), dim3(64), 0, (hipStream_t)stream, (const uint8_t*)in, in_bytes, in_off,
-                       B, remap, freq, cum, lut, (uint8_t*)blocks, pos);
+                       B, remap, lut, (uint8_t*)blocks, pos);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }
@@ -1122,13 +1169,22 @@ int spa_q8_predict_multi(const void* blocks, const int* ent_slot, const int* ent
     return SPA_OK;
 }
 
+int spa_q8_ranks(const int8_t* pint, int64_t nb, int8_t* prk, int8_t* pinv, int8_t* rctx, void* stream) {
+    if (nb < 0) return fail(SPA_ERR_ARG, "spa_q8_ranks: %lld blocks", (long long)nb);
+    if (!nb) return SPA_OK;
+    Q8_NONNULL(pint, prk, pinv, rctx);
+    hipLaunchKernelGGL(k_ranks, dim3(nblk(nb * 32, 256)), dim3(256), 0, (hipStream_t)stream, pint, nb, prk, pinv, rctx);
+    SPA_HIP_TRY(hipGetLastError());
+    return SPA_OK;
+}
+
 int spa_q8_hist_c(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, const void* segs, int nseg,
                   const void* slots, const int16_t* cfi, const int* row_m, const int8_t* fbin, const int8_t* pint,
-                  uint32_t* counts, void* stream) {
+                  const int8_t* prk, const int8_t* pinv, const int8_t* rctx, uint32_t* counts, void* stream) {
     if (nseg < 0) return fail(SPA_ERR_ARG, "spa_q8_hist_c: %d segments", nseg);
     if (!nseg) return SPA_OK;
-    Q8_NONNULL(blocks, pos, skip, meta, segs, slots, cfi, row_m, fbin, pint, counts);
-    CArgs A{skip, (const Meta*)meta, (const CSeg*)segs, nseg, (const Slot*)slots, cfi, row_m, fbin, pint};
+    Q8_NONNULL(blocks, pos, skip, meta, segs, slots, cfi, row_m, fbin, pint, prk, pinv, rctx, counts);
+    CArgs A{skip, (const Meta*)meta, (const CSeg*)segs, nseg, (const Slot*)slots, cfi, row_m, fbin, pint, prk, pinv, rctx};
     hipLaunchKernelGGL(k_hist_c, dim3(nblk(nseg, HC_SEGS)), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)blocks, pos, A,
                        counts);
     SPA_HIP_TRY(hipGetLastError());
@@ -1137,12 +1193,13 @@ int spa_q8_hist_c(const void* blocks, const uint8_t* pos, const uint8_t* skip, c
 
 int spa_q8_enc_c(const void* blocks, const uint8_t* pos, const uint8_t* skip, const void* meta, const void* segs, int nseg,
                  const void* slots, const int16_t* cfi, const int* row_m, const int8_t* fbin, const int8_t* pint,
-                 const int* remap, const uint16_t* freq, const uint32_t* cum, const uint32_t* rcp, void* out, uint64_t cap,
-                 uint32_t* out_len, void* stream) {
+                 const int8_t* prk, const int8_t* pinv, const int8_t* rctx, const int* remap, const uint16_t* freq,
+                 const uint32_t* cum, const uint32_t* rcp, void* out, uint64_t cap, uint32_t* out_len, void* stream) {
     if (nseg < 0 || cap < 256) return fail(SPA_ERR_ARG, "spa_q8_enc_c: %d segments, slot capacity %llu", nseg, (unsigned long long)cap);
     if (!nseg) return SPA_OK;
-    Q8_NONNULL(blocks, pos, skip, meta, segs, slots, cfi, row_m, fbin, pint, remap, freq, cum, rcp, out, out_len);
-    CArgs A{skip, (const Meta*)meta, (const CSeg*)segs, nseg, (const Slot*)slots, cfi, row_m, fbin, pint};
+    Q8_NONNULL(blocks, pos, skip, meta, segs, slots, cfi, row_m, fbin, pint, prk, pinv, rctx, remap, freq, cum, rcp, out,
+               out_len);
+    CArgs A{skip, (const Meta*)meta, (const CSeg*)segs, nseg, (const Slot*)slots, cfi, row_m, fbin, pint, prk, pinv, rctx};
     hipLaunchKernelGGL(k_enc_c, dim3(nblk(nseg, 64)), dim3(64), 0, (hipStream_t)stream, (const uint8_t*)blocks, pos, A, remap,
                        freq, cum, rcp, (uint8_t*)out, cap, out_len);
     SPA_HIP_TRY(hipGetLastError());
@@ -1151,14 +1208,14 @@ int spa_q8_enc_c(const void* blocks, const uint8_t* pos, const uint8_t* skip, co
 
 int spa_q8_dec_c(const void* in, uint64_t in_bytes, const uint64_t* in_off, int seg0, int seg1, const uint8_t* skip,
                  const void* meta, const void* segs, int nseg, const void* slots, const int16_t* cfi, const int* row_m,
-                 const int8_t* fbin, const int8_t* pint, const int* remap, const uint16_t* freq, const uint32_t* cum,
-                 const uint8_t* lut, void* blocks, uint8_t* pos, void* stream) {
+                 const int8_t* fbin, const int8_t* pint, const int8_t* prk, const int8_t* pinv, const int8_t* rctx,
+                 const int* remap, const uint32_t* lut, void* blocks, uint8_t* pos, void* stream) {
     if (seg0 < 0 || seg1 > nseg || seg0 > seg1) return fail(SPA_ERR_ARG, "spa_q8_dec_c: segments [%d, %d) of %d", seg0, seg1, nseg);
     if (seg0 == seg1) return SPA_OK;
-    Q8_NONNULL(in, in_off, skip, meta, segs, slots, cfi, row_m, fbin, pint, remap, freq, cum, lut, blocks, pos);
-    CArgs A{skip, (const Meta*)meta, (const CSeg*)segs, nseg, (const Slot*)slots, cfi, row_m, fbin, pint};
+    Q8_NONNULL(in, in_off, skip, meta, segs, slots, cfi, row_m, fbin, pint, prk, pinv, rctx, remap, lut, blocks, pos);
+    CArgs A{skip, (const Meta*)meta, (const CSeg*)segs, nseg, (const Slot*)slots, cfi, row_m, fbin, pint, prk, pinv, rctx};
     hipLaunchKernelGGL(k_dec_c, dim3(nblk(seg1 - seg0, 64)), dim3(64), 0, (hipStream_t)stream, (const uint8_t*)in, in_bytes,
-                       in_off, seg0, seg1, A, remap, freq, cum, lut, (uint8_t*)blocks, pos);
+                       in_off, seg0, seg1, A, remap, lut, (uint8_t*)blocks, pos);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }

@@ -23,7 +23,9 @@ def pack_parts(chunks):
 
 
 def pack(chunks):
-    return b"".join(bytes(p) if not isinstance(p, bytes) else p for p in pack_parts(chunks))
+    """the chunks in one bytes object (bytes-like parts joined without an intermediate copy)"""
+    return b"".join(p if isinstance(p, (bytes, bytearray, memoryview)) else memoryview(p).cast("B")
+                    for p in pack_parts(chunks))
 
 
 def unpack(buf):

@@ -18,6 +18,7 @@ Ccoef, Cfbin, Cmu, Ccadj], [rest]}) with the reference's names, orders and zstd 
 673-688, gpu3.py:405-418); "rest" (the bytes around the tensors) is header.py's P, T or X form.
 """
 import json
+import time
 from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
@@ -26,7 +27,7 @@ from . import detmath
 from . import device as dev
 from . import gguf, header, zstd
 from ._lib import check, lib
-from .framing import pack, unpack
+from .framing import pack, pack_parts, unpack
 from .r2 import cum_of, load_tables, normalize, store_tables
 
 PB = 12
@@ -165,9 +166,9 @@ def _decoder_tables(buf, ntab, st):
     if (cum[:, 256] != (1 << PB)).any():
         raise ValueError("Q8_0 codec: a stored table does not sum to 4096")
     freq_d, cum_d, remap_d = (dev.DeviceArray.from_host(a, st) for a in (freq, cum, remap))
-    lut = dev.DeviceArray((n, 1 << PB), np.uint8)
-    check(lib().spa_rans_build_lut(cum_d.ptr, n, lut.ptr, st))
-    return freq_d, cum_d, remap_d, lut
+    lut = dev.DeviceArray((n, 1 << PB), np.uint32)
+    check(lib().spa_q8_lut32(freq_d.ptr, cum_d.ptr, n, lut.ptr, st))
+    return remap_d, lut
 
 
 def _gather(out, cap, out_len, nseg, st, what):
@@ -182,7 +183,7 @@ def _gather(out, cap, out_len, nseg, st, what):
     dst = dev.DeviceArray(max(1, int(offs[-1])), np.uint8)
     offs_d = dev.DeviceArray.from_host(offs, st)
     check(lib().spa_qr_gather(out.ptr, cap, out_len.ptr, offs_d.ptr, nseg, dst.ptr, st))
-    return dst.to_host(stream=st)[:int(offs[-1])].tobytes(), lens.astype(np.uint16)
+    return dst.to_host(stream=st)[:int(offs[-1])], lens.astype(np.uint16)
 
 
 def _log2(x, st):
@@ -196,13 +197,29 @@ class M22:
     def __init__(self, stream=None, stat_elems=STAT_ELEMS, timing=False):
         self.stream = stream
         self.stat_elems = stat_elems
-        self.timing = {}
+        self.timing_on, self.timing = timing, {}
+        self._t = time.perf_counter()
+
+    def _lap(self, name):
+        """with timing on: the stream drained, the wall seconds since the previous lap added to `name`"""
+        if self.timing_on:
+            dev.synchronize(self.stream)
+            now = time.perf_counter()
+            self.timing[name] = round(self.timing.get(name, 0.0) + now - self._t, 4)
+            self._t = now
 
     # ---------------------------------------------------------- encoder
     def compress(self, data, tensors=None, header=True, parsed=None, d=None):
         """data: the file (bytes-like, host); tensors: indices of the Q8_0 tensors to code (default all);
         header=False leaves the other bytes out (the caller stores them); parsed: (layout, GGUF) when the
         caller has them; d: the file already in HBM (DeviceArray), else its tensors are uploaded"""
+        return pack(self.compress_dict(data, tensors, header, parsed, d))
+
+    def compress_parts(self, data, tensors=None, header=True, parsed=None, d=None):
+        """compress() as pack_parts' list of buffers (the streams are not joined)"""
+        return pack_parts(self.compress_dict(data, tensors, header, parsed, d))
+
+    def compress_dict(self, data, tensors=None, header=True, parsed=None, d=None):
         st = self.stream
         host = np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray) else data.reshape(-1)
         if parsed is None:
@@ -216,7 +233,7 @@ class M22:
             ch = self._compress(host, layout, d)
             if rest is not None:
                 ch["rest"] = rest.result()
-        return pack(ch)
+        return ch
 
     @staticmethod
     def _header_c(host, g, layout):
@@ -233,6 +250,7 @@ class M22:
         n = sum(nb for _, nb, _, _ in layout["t"]) // 34
         if n >= 1 << 31:
             raise ValueError(f"Q8_0 codec: {n} blocks in one part")
+        self._t = time.perf_counter()
         allb = dev.DeviceArray(n * 34, np.uint8)
         pos_b = 0
         for o, nb, _, _ in layout["t"]:
@@ -249,10 +267,13 @@ class M22:
         row_m = dev.DeviceArray(nrows_all, np.int32)
         check(lib().spa_q8_row_means(allb.ptr, meta_d.ptr, T, nrows_all, row_m.ptr, st))
         cfi, scls, off = self._column_side(allb, layout, meta0, row_m)
+        self._lap("column statistics")
         perm, rankof, spread = colblock_side(cfi)
         bcf = block_factor_bins(cfi, layout)
         skip, dups = self._dedup(allb, layout, meta0)
+        self._lap("duplicate rows")
         plans = self._plans(allb, layout, meta0, skip)
+        self._lap("row planner")
         for p in plans:
             sl = skip[p["first"]:p["first"] + p["nrows"] * p["nbr"]]
             sl[...] = np.where(sl == 1, 1, 6).astype(np.uint8)
@@ -276,6 +297,7 @@ class M22:
                                   side_d["cfi"].ptr, side_d["scls"].ptr, row_m.ptr, qbase, counts.ptr, st))
         tabs = _Tables(counts, nalloc, st)
         del counts
+        self._lap("histograms + tables A/B")
         tab_args = (tabs.remap_d.ptr, tabs.freq_d.ptr, tabs.cum_d.ptr, tabs.rcp_d.ptr)
         streams = []
         nsa, nsb = (n + SEGA - 1) // SEGA, (n + SEGB - 1) // SEGB
@@ -291,7 +313,9 @@ class M22:
                                          side_d["scls"].ptr, row_m.ptr, qbase, *tab_args, out.ptr, cap, out_len.ptr, st))
             streams.append(_gather(out, cap, out_len, nseg, st, what))
             del out
+            self._lap(f"phase {what}")
         extra = self._encode_extra(allb, pos, plans, meta, meta_d, side_d, cfi, row_m) if plans else {}
+        self._lap("phase C")
 
         side = {"off": [int(v) for v in off], "qset": [int(v) for v in meta["qset"]],
                 "dups": [[int(a) for a in r] for r in dups]}
@@ -395,6 +419,7 @@ class M22:
         col_w = detmath.cols(W, True, mask=valid_d, stream=st).to_host(stream=st)
         mu_d = dev.DeviceArray.from_host(mu, st)
         check(lib().spa_q8_center(W.ptr, mu_d.ptr, n, C, st))
+        self._lap("planner: row matrix, column means")
         nrm = np.maximum(np.sqrt(detmath.rows(W, True, stream=st).to_host(stream=st)), 1e-12)
         nrm_d = dev.DeviceArray.from_host(nrm, st)
         Wq = dev.DeviceArray((n, C), np.int8)
@@ -402,14 +427,17 @@ class M22:
         cand = dev.DeviceArray((n, KPAR), np.int32)
         wstart_d = dev.DeviceArray.from_host(wstart, st)
         check(lib().spa_q8_neighbours(Wq.ptr, n, C, wstart_d.ptr, valid_d.ptr, cand.ptr, st))
+        self._lap("planner: norms, int8 rows, neighbours")
         del Wq
         frac_d, kuse_d = dev.DeviceArray(n, np.float32), dev.DeviceArray(n, np.int32)
         coefs_d = dev.DeviceArray((n, KPAR), np.float32)
         check(lib().spa_q8_fit_rows(W.ptr, cand.ptr, n, C, frac_d.ptr, kuse_d.ptr, coefs_d.ptr, st))
+        self._lap("planner: least squares")
         nch = (n + LS_CHUNK - 1) // LS_CHUNK
         part = dev.DeviceArray((nch, C), np.float64)
         check(lib().spa_q8_col_res(W.ptr, cand.ptr, coefs_d.ptr, kuse_d.ptr, valid_d.ptr, n, C, LS_CHUNK, part.ptr, st))
         col_res = _in_order(part.to_host(stream=st))
+        self._lap("planner: residual columns")
         par, kuse = cand.to_host(stream=st), kuse_d.to_host(stream=st)
         coefs, frac = coefs_d.to_host(stream=st), frac_d.to_host(stream=st)
         valid_par = (np.arange(KPAR)[None, :] < kuse[:, None]) & valid[:, None]
@@ -440,6 +468,8 @@ class M22:
             ro, mo = int(rbase[slot]), int(mubase[slot])
             check(lib().spa_q8_predict(allb.ptr, p["first"], p["nbr"], p["nrows"], par_d.ptr + 4 * KPAR * ro,
                                        coef_d.ptr + 4 * KPAR * ro, mu_d.ptr + 4 * mo, pint.ptr + int(pbase[slot]), st))
+        prk, pinv, rctx = dev.DeviceArray(total, np.int8), dev.DeviceArray(total, np.int8), dev.DeviceArray(total // 32, np.int8)
+        check(lib().spa_q8_ranks(pint.ptr, total // 32, prk.ptr, pinv.ptr, rctx.ptr, st))
         segs, _ = segments(plans, WAVES, RPT)
         nseg = len(segs)
         slots = np.zeros(len(plans), SLOT_DT)
@@ -452,7 +482,8 @@ class M22:
             cfi_c[cb:cb + C] = (cfi_c[cb:cb + C].astype(np.int32) + p["cadj"].astype(np.int32)).astype(np.int16)
         segs_d, slots_d, cfi_d, fbin_d = (dev.DeviceArray.from_host(a, st) for a in
                                           (segs.view(np.uint8), slots.view(np.uint8), cfi_c, fbin_all))
-        c_args = (side_d["skip"].ptr, meta_d.ptr, segs_d.ptr, nseg, slots_d.ptr, cfi_d.ptr, row_m.ptr, fbin_d.ptr, pint.ptr)
+        c_args = (side_d["skip"].ptr, meta_d.ptr, segs_d.ptr, nseg, slots_d.ptr, cfi_d.ptr, row_m.ptr, fbin_d.ptr, pint.ptr,
+                  prk.ptr, pinv.ptr, rctx.ptr)
         ntab = len(plans) * TPC
         counts = dev.DeviceArray((ntab, 256), np.uint32).zero(st)
         check(lib().spa_q8_hist_c(allb.ptr, pos.ptr, *c_args, counts.ptr, st))
@@ -505,6 +536,7 @@ class M22:
 
     def _decode(self, buf):
         st = self.stream
+        self._t = time.perf_counter()
         ch = unpack(memoryview(buf) if not isinstance(buf, memoryview) else buf)
         pool = ThreadPoolExecutor(1)
         rest = pool.submit(header.header_d, bytes(ch["rest"])) if "rest" in ch else None
@@ -526,7 +558,7 @@ class M22:
         ncol = sum(rl for _, _, rl, _ in layout["t"])
         if len(cfi) != ncol or len(scls) != ncol:
             raise ValueError("Q8_0 codec: column side information does not match the layout")
-        freq_d, cum_d, remap_d, lut = _decoder_tables(ch["tables"], ntab, st)
+        remap_d, lut = _decoder_tables(ch["tables"], ntab, st)
         perm, rankof, spread = colblock_side(cfi)
         bcf = block_factor_bins(cfi, layout)
         skip = np.zeros(n, np.uint8)
@@ -545,12 +577,12 @@ class M22:
                   (("skip", skip), ("bcf", bcf), ("spread", spread), ("perm", perm), ("scls", scls), ("cfi", cfi))}
         allb = dev.DeviceArray(n * 34, np.uint8).zero(st)
         pos = dev.DeviceArray(n, np.uint8).zero(st)
-        tab_args = (remap_d.ptr, freq_d.ptr, cum_d.ptr, lut.ptr)
+        tab_args = (remap_d.ptr, lut.ptr)
         for what, ns, lo in (("A", nsa, 0), ("B", nsb, nsa)):
             ln = lens[lo:lo + ns]
             offs = np.zeros(ns, np.uint64)
             offs[1:] = np.cumsum(ln)[:-1]
-            s = np.frombuffer(bytes(ch[what]), np.uint8)
+            s = np.frombuffer(ch[what], np.uint8)
             if int(ln.sum()) > len(s):
                 raise ValueError(f"Q8_0 codec: phase {what} stream shorter than its segment lengths")
             s_d = dev.DeviceArray.from_host(s if len(s) else np.zeros(1, np.uint8), st)
@@ -567,8 +599,10 @@ class M22:
                                          side_d["cfi"].ptr, side_d["scls"].ptr, row_m.ptr, qbase, *tab_args, allb.ptr,
                                          pos.ptr, st))
             dev.synchronize(st)
+            self._lap(f"decode phase {what}")
         if cside is not None:
             self._decode_extra(ch, cside, allb, pos, meta, meta_d, side_d, cfi, row_m)
+            self._lap("decode phase C")
         if len(dups):
             for i, r, s_ in dups:
                 nbr, f = int(meta["nb_row"][i]), int(meta["first"][i])
@@ -601,7 +635,9 @@ class M22:
         if len(par_all) and (par_all.max() >= max(p["nrows"] for p in plans)):
             raise ValueError("Q8_0 codec: a parent row outside its tensor")
         pbase = np.cumsum([0] + [p["nrows"] * p["nbr"] * 32 for p in plans])[:-1].astype(np.int64)
-        pint = dev.DeviceArray(int(pbase[-1] + plans[-1]["nrows"] * plans[-1]["nbr"] * 32), np.int8).zero(st)
+        total = int(pbase[-1] + plans[-1]["nrows"] * plans[-1]["nbr"] * 32)
+        pint = dev.DeviceArray(total, np.int8).zero(st)
+        prk, pinv, rctx = dev.DeviceArray(total, np.int8), dev.DeviceArray(total, np.int8), dev.DeviceArray(total // 32, np.int8)
         segs, wave_start = segments(plans, waves, rpt)
         nseg = len(segs)
         slots = np.zeros(len(plans), SLOT_DT)
@@ -612,13 +648,13 @@ class M22:
             cb = int(meta["colbase"][p["t"]])
             C = p["nbr"] * 32
             cfi_c[cb:cb + C] = (cfi_c[cb:cb + C].astype(np.int32) + p["cadj"].astype(np.int32)).astype(np.int16)
-        freq_d, cum_d, remap_d, lut = _decoder_tables(ch["Ctables"], len(plans) * TPC, st)
+        remap_d, lut = _decoder_tables(ch["Ctables"], len(plans) * TPC, st)
         lens = np.frombuffer(zstd.decompress(ch["Clens"]), np.uint16).astype(np.uint64)
         if len(lens) != nseg:
             raise ValueError(f"Q8_0 codec: {len(lens)} phase C lengths for {nseg} segments")
         offs = np.zeros(nseg, np.uint64)
         offs[1:] = np.cumsum(lens)[:-1]
-        s = np.frombuffer(bytes(ch["C"]), np.uint8)
+        s = np.frombuffer(ch["C"], np.uint8)
         if int(lens.sum()) > len(s):
             raise ValueError("Q8_0 codec: phase C stream shorter than its segment lengths")
         s_d = dev.DeviceArray.from_host(s if len(s) else np.zeros(1, np.uint8), st)
@@ -643,9 +679,15 @@ class M22:
             e0, e1 = ent_start[w], ent_start[w + 1]
             check(lib().spa_q8_predict_multi(allb.ptr, ent_slot_d.ptr + 4 * e0, ent_row_d.ptr + 4 * e0, e1 - e0, cmax,
                                              slots_d.ptr, par_d.ptr, coef_d.ptr, mu_d.ptr, pint.ptr, st))
+            for slot, p in enumerate(plans):           # the wave's rows of each tensor: one run of pint
+                a, b = int(se[slot][0][w]), int(se[slot][1][w])
+                if b > a:
+                    q0 = int(pbase[slot]) + a * p["nbr"] * 32
+                    check(lib().spa_q8_ranks(pint.ptr + q0, (b - a) * p["nbr"], prk.ptr + q0, pinv.ptr + q0,
+                                             rctx.ptr + q0 // 32, st))
             check(lib().spa_q8_dec_c(s_d.ptr, len(s), offs_d.ptr, wave_start[w], wave_start[w + 1], side_d["skip"].ptr,
                                      meta_d.ptr, segs_d.ptr, nseg, slots_d.ptr, cfi_d.ptr, row_m.ptr, fbin_d.ptr, pint.ptr,
-                                     remap_d.ptr, freq_d.ptr, cum_d.ptr, lut.ptr, allb.ptr, pos.ptr, st))
+                                     prk.ptr, pinv.ptr, rctx.ptr, remap_d.ptr, lut.ptr, allb.ptr, pos.ptr, st))
         dev.synchronize(st)
 
 
@@ -655,8 +697,8 @@ class Q8Parts:
     The default budget is a fixed size, so the archive does not depend on the device."""
     PART = 1 << 30
 
-    def __init__(self, budget=None, stream=None):
-        self.c = M22(stream)
+    def __init__(self, budget=None, stream=None, timing=False):
+        self.c = M22(stream, timing=timing)
         self.budget = budget or self.PART
         self.parts = 0
 
@@ -682,7 +724,7 @@ class Q8Parts:
             groups = self.groups(layout)
             ch = {"layout": zstd.zstd_c(json.dumps(layout).encode())}
             for k, idx in enumerate(groups):
-                ch[f"p{k}"] = self.c.compress(host, tensors=idx, header=False, parsed=(layout, g), d=d)
+                ch[f"p{k}"] = self.c.compress_parts(host, tensors=idx, header=False, parsed=(layout, g), d=d)
             if hdr is not None:
                 ch["rest"] = hdr.result()
         self.parts = len(groups)
