@@ -38,7 +38,6 @@ constexpr int A_HI = 0, A_LO = 256 * 16, A_POS = A_LO + 256, A_MX = A_POS + 16, 
 constexpr int Q_SG = 64, TQ = 64 + 1024;                       // gpu2.py:52-53
 constexpr int TPC = 64 + 24;                                   // gpu3.py:31 with PREDA
 constexpr int KP = 4;                                          // parents per row (M21, gpu3.py:573)
-constexpr int NT = 64;                                         // kNN tile rows
 
 struct Meta { int first, nblocks, nb_row, grp, colbase, rowbase, off, qset; };     // gpu2.py:278 META_DT
 struct Item { int t, b0, nb; };                                 // histogram work: blocks [b0, b0+nb) of tensor t
@@ -732,34 +731,84 @@ __global__ __launch_bounds__(64) void k_sim8(const int8_t* __restrict__ A, int64
 }
 
 // per row r: the 4 rows c < wstart[r] with valid[c] of largest similarity Wq[r].Wq[c], ties to the
-// lower index, -1 where fewer exist (gpu3.py:296-310). A workgroup per 64 rows: four waves compute
-// a 64 x 64 block of similarities per candidate tile into LDS, then lane i of the first wave
-// merges row i's 64 values (ascending column) into its running top 4.
+// lower index, -1 where fewer exist (gpu3.py:296-310). An LDS-staged int8 GEMM fused with the top-4
+// merge: a workgroup takes 128 query rows and walks the candidate rows 128 at a time; per 64-column
+// chunk the 256 lanes stage the query and candidate tiles in LDS (double-buffered, the next chunk's
+// loads in flight during the MFMAs), each wave computes 32 query rows x 128 candidates as four
+// v_mfma_i32_32x32x32_i8 tiles; the 128 x 128 similarities then go through LDS to lanes 0..127,
+// which merge their row's values in ascending column order into a running top 4.
+constexpr int NQ = 128, NCAND = 128, KC = 64, KPITCH = KC + 16;
 __global__ __launch_bounds__(256) void k_neighbours(const int8_t* __restrict__ Wq, int64_t n, int C,
                                                     const int* __restrict__ wstart, const uint8_t* __restrict__ valid,
                                                     int* __restrict__ cand) {
-    __shared__ int32_t S[NT][NT + 1];
-    const int64_t q0 = (int64_t)blockIdx.x * NT;
-    const int w = threadIdx.x >> 6;
-    const int qm = (w >> 1) * 32, cn = (w & 1) * 32;
-    const int64_t qlast = q0 + NT - 1 < n ? q0 + NT - 1 : n - 1;
+    __shared__ __align__(16) int8_t As[2][NQ][KPITCH];
+    __shared__ __align__(16) int8_t Bs[2][NCAND][KPITCH];
+    __shared__ int32_t S[NQ][NCAND + 1];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int64_t q0 = (int64_t)blockIdx.x * NQ;
+    const int64_t qlast = q0 + NQ - 1 < n ? q0 + NQ - 1 : n - 1;
     // candidates are earlier rows: wstart[r] <= r is the contract, and no read goes past row n - 1
     const int64_t cmax = min(max((int64_t)wstart[qlast], (int64_t)0), n);
-    const int64_t q = q0 + threadIdx.x;
-    const int ws = (threadIdx.x < NT && q < n) ? (int)min(max((int64_t)wstart[q], (int64_t)0), cmax) : 0;
+    const int64_t q = q0 + tid;
+    const int ws = (tid < NQ && q < n) ? (int)min(max((int64_t)wstart[q], (int64_t)0), cmax) : 0;
     int v0 = -2147483647 - 1, v1 = v0, v2 = v0, v3 = v0, i0 = -1, i1 = -1, i2 = -1, i3 = -1;
-    for (int64_t j0 = 0; j0 < cmax; j0 += NT) {
-        const v16i acc = tile_dot(Wq, n, q0 + qm, Wq, cmax, j0 + cn, C);
-        const int col = cn + (threadIdx.x & 31);
+    const int nk = (C + KC - 1) / KC;
+    // this lane's two 16-byte pieces of a 128-row x 64-byte chunk: row p / 4, bytes 16 (p % 4)
+    const int pr0 = tid >> 2, pc0 = (tid & 3) * 16, pr1 = (tid + 256) >> 2, pc1 = ((tid + 256) & 3) * 16;
+    auto piece = [&](int64_t row, int64_t lim, int k) -> v4i {
+        if (row >= lim || k >= C) return v4i{0, 0, 0, 0};
+        return *reinterpret_cast<const v4i*>(Wq + row * C + k);
+    };
+    for (int64_t j0 = 0; j0 < cmax; j0 += NCAND) {
+        v16i acc[4];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) S[qm + tile_row(v)][col] = acc[v];
+        for (int t = 0; t < 4; ++t) acc[t] = v16i{};
+        v4i ra0 = piece(q0 + pr0, n, pc0), ra1 = piece(q0 + pr1, n, pc1);
+        v4i rb0 = piece(j0 + pr0, cmax, pc0), rb1 = piece(j0 + pr1, cmax, pc1);
+        *reinterpret_cast<v4i*>(&As[0][pr0][pc0]) = ra0;
+        *reinterpret_cast<v4i*>(&As[0][pr1][pc1]) = ra1;
+        *reinterpret_cast<v4i*>(&Bs[0][pr0][pc0]) = rb0;
+        *reinterpret_cast<v4i*>(&Bs[0][pr1][pc1]) = rb1;
         __syncthreads();
-        if (threadIdx.x < NT) {
-            const int lim = (int)((int64_t)ws - j0 < NT ? (int64_t)ws - j0 : NT);
+        for (int kc = 0; kc < nk; ++kc) {
+            const int cur = kc & 1;
+            const bool more = kc + 1 < nk;
+            if (more) {
+                const int k = (kc + 1) * KC;
+                ra0 = piece(q0 + pr0, n, k + pc0);
+                ra1 = piece(q0 + pr1, n, k + pc1);
+                rb0 = piece(j0 + pr0, cmax, k + pc0);
+                rb1 = piece(j0 + pr1, cmax, k + pc1);
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int kk = ks * 32 + (lane >> 5) * 16;
+                const v4i a = *reinterpret_cast<const v4i*>(&As[cur][32 * w + (lane & 31)][kk]);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const v4i b = *reinterpret_cast<const v4i*>(&Bs[cur][32 * t + (lane & 31)][kk]);
+                    acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[t], 0, 0, 0);
+                }
+            }
+            if (more) {
+                *reinterpret_cast<v4i*>(&As[cur ^ 1][pr0][pc0]) = ra0;
+                *reinterpret_cast<v4i*>(&As[cur ^ 1][pr1][pc1]) = ra1;
+                *reinterpret_cast<v4i*>(&Bs[cur ^ 1][pr0][pc0]) = rb0;
+                *reinterpret_cast<v4i*>(&Bs[cur ^ 1][pr1][pc1]) = rb1;
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) S[32 * w + tile_row(v)][32 * t + (lane & 31)] = acc[t][v];
+        __syncthreads();
+        if (tid < NQ) {
+            const int lim = (int)((int64_t)ws - j0 < NCAND ? (int64_t)ws - j0 : NCAND);
             for (int c = 0; c < lim; ++c) {
                 const int cj = (int)j0 + c;
                 if (!valid[cj]) continue;
-                const int val = S[threadIdx.x][c];
+                const int val = S[tid][c];
                 if (val > v3) {
                     if (val > v2) {
                         v3 = v2; i3 = i2;
@@ -774,7 +823,7 @@ __global__ __launch_bounds__(256) void k_neighbours(const int8_t* __restrict__ W
         }
         __syncthreads();
     }
-    if (threadIdx.x < NT && q < n) {
+    if (tid < NQ && q < n) {
         int* o = cand + q * KP;
         o[0] = i0; o[1] = i1; o[2] = i2; o[3] = i3;
     }
@@ -1266,7 +1315,7 @@ int spa_q8_neighbours(const int8_t* Wq, int64_t n, int C, const int* wstart, con
     if (!n) return SPA_OK;
     Q8_NONNULL(Wq, wstart, valid, cand);
     if ((uintptr_t)Wq & 15) return fail(SPA_ERR_ARG, "spa_q8_neighbours: rows must be 16-byte aligned");
-    hipLaunchKernelGGL(k_neighbours, dim3(nblk(n, NT)), dim3(256), 0, (hipStream_t)stream, Wq, n, C, wstart, valid, cand);
+    hipLaunchKernelGGL(k_neighbours, dim3(nblk(n, NQ)), dim3(256), 0, (hipStream_t)stream, Wq, n, C, wstart, valid, cand);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }
