@@ -10,18 +10,18 @@ from . import device as dev
 from ._lib import check, lib
 
 
-def _dev(a, dtype):
+def _dev(a, dtype, stream):
     if isinstance(a, dev.DeviceArray):
         if a.dtype != np.dtype(dtype):
             raise TypeError(f"{a.dtype} array where {np.dtype(dtype)} is expected")
         return a
-    return dev.DeviceArray.from_host(np.ascontiguousarray(a, dtype))
+    return dev.DeviceArray.from_host(np.ascontiguousarray(a, dtype), stream)
 
 
 def rows(x, square=False, stream=None):
     """float64 sums (of squares) along the rows of a 2-D float32 / float64 array (detmath.py:185-192)"""
     f64 = (x.dtype == np.float64)
-    x = _dev(x, np.float64 if f64 else np.float32)
+    x = _dev(x, np.float64 if f64 else np.float32, stream)
     nr, nc = x.shape
     out = dev.DeviceArray(nr, np.float64)
     check(lib().spa_dm_rows(x.ptr, int(f64), nr, nc, int(square), out.ptr, stream))
@@ -31,10 +31,10 @@ def rows(x, square=False, stream=None):
 def cols(x, square=False, mask=None, stream=None):
     """float64 sums (of squares) down the columns of a 2-D float32 array, rows with mask False left out
     (detmath.py:195-202)"""
-    x = _dev(x, np.float32)
+    x = _dev(x, np.float32, stream)
     nr, nc = x.shape
     m = None if mask is None else _dev(np.asarray(mask).astype(np.uint8) if not isinstance(mask, dev.DeviceArray) else mask,
-                                        np.uint8)
+                                        np.uint8, stream)
     out = dev.DeviceArray(nc, np.float64)
     check(lib().spa_dm_cols(x.ptr, nr, nc, int(square), None if m is None else m.ptr, out.ptr, stream))
     return out
@@ -49,7 +49,7 @@ def total(x, square=False, stream=None):
 
 def gram(X, stream=None):
     """X (n, k, d) float32 -> X X^T per batch element (n, k, k) float32 (detmath.py:210-216)"""
-    X = _dev(X, np.float32)
+    X = _dev(X, np.float32, stream)
     n, k, d = X.shape
     out = dev.DeviceArray((n, k, k), np.float32)
     check(lib().spa_dm_gram(X.ptr, n, k, d, out.ptr, stream))
@@ -58,7 +58,7 @@ def gram(X, stream=None):
 
 def bdot(X, y, stream=None):
     """X (n, k, d), y (n, d) float32 -> X y per batch element (n, k) float32 (detmath.py:219-225)"""
-    X, y = _dev(X, np.float32), _dev(y, np.float32)
+    X, y = _dev(X, np.float32, stream), _dev(y, np.float32, stream)
     n, k, d = X.shape
     out = dev.DeviceArray((n, k), np.float32)
     check(lib().spa_dm_bdot(X.ptr, y.ptr, n, k, d, out.ptr, stream))
@@ -67,7 +67,7 @@ def bdot(X, y, stream=None):
 
 def solve(A, b, stream=None):
     """batched small systems A (n, k, k) x = b (n, k), k <= 16 -> x (n, k) float32 (detmath.py:228-235)"""
-    A, b = _dev(A, np.float32), _dev(b, np.float32)
+    A, b = _dev(A, np.float32, stream), _dev(b, np.float32, stream)
     n, k = b.shape
     x = dev.DeviceArray((n, k), np.float32)
     check(lib().spa_dm_solve(A.ptr, b.ptr, n, k, x.ptr, stream))
@@ -76,7 +76,7 @@ def solve(A, b, stream=None):
 
 def log2(x, stream=None):
     """float64 log2 elementwise (detmath.py:171-175)"""
-    x = _dev(x, np.float64)
+    x = _dev(x, np.float64, stream)
     y = dev.DeviceArray(x.shape, np.float64)
     check(lib().spa_dm_log2(x.ptr, x.size, y.ptr, stream))
     return y
@@ -84,7 +84,7 @@ def log2(x, stream=None):
 
 def exp2(x, stream=None):
     """float64 2 ** x elementwise (detmath.py:178-182)"""
-    x = _dev(x, np.float64)
+    x = _dev(x, np.float64, stream)
     y = dev.DeviceArray(x.shape, np.float64)
     check(lib().spa_dm_exp2(x.ptr, x.size, y.ptr, stream))
     return y

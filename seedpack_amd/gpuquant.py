@@ -50,9 +50,11 @@ class GPUQuant:
         lib()
         self.stream = stream
 
-    @staticmethod
-    def _dev(a):
-        return a if isinstance(a, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(a))
+    def _dev(self, a):
+        # uploads go on this quantizer's stream: the library's streams do not wait for the null
+        # stream, and a block freed here is reused by the next upload while earlier launches on the
+        # stream may still read it
+        return a if isinstance(a, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(a), self.stream)
 
     def _imx(self, imx, npr):
         if imx is None:
@@ -61,7 +63,7 @@ class GPUQuant:
             return imx
         imx = np.ascontiguousarray(imx, np.float32).reshape(-1)
         assert imx.size == npr, (imx.size, npr)
-        return dev.DeviceArray.from_host(imx)
+        return dev.DeviceArray.from_host(imx, self.stream)
 
     def quantize_tensors(self, ttype, srcs, imatrices, variant=0, max_weights=1 << 28, on_result=None, device=False):
         """srcs: list of (weights as bf16 bits (uint16) / f16 / f32, device or host array, n_per_row).

@@ -23,10 +23,10 @@ def ls_gram(gq, T, X, F, stream=None):
     if T not in LS_TYPES:
         raise ValueError(f"type {T} is not a least-squares legacy type")
     _, qk, bs = QFUN[T]
-    X = X if isinstance(X, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(X, np.float32))
+    X = X if isinstance(X, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(X, np.float32), stream)
     R, cols = X.shape
     nb = cols // qk
-    F = F if isinstance(F, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(F, np.uint8).reshape(-1))
+    F = F if isinstance(F, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(F, np.uint8).reshape(-1), stream)
     if F.nbytes != R * nb * bs:
         raise ValueError(f"{F.nbytes} bytes of blocks for {R} rows of {cols} weights")
     V = gq.dequantize(T, F, cols)
@@ -59,7 +59,7 @@ def equal_blocks(gq, T, X, F, e):
     """share of the blocks of rows X (float32, rows x cols) that importance e reproduces; F: the
     file's blocks of those rows (imxfit.py:74-79)"""
     _, qk, bs = QFUN[T]
-    X = X if isinstance(X, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(X, np.float32))
+    X = X if isinstance(X, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(X, np.float32), gq.stream)
     Y = gq.quantize_batch(T, [X], [np.asarray(e, np.float32)])[0].to_host(stream=gq.stream)
-    Fh = F.to_host() if isinstance(F, dev.DeviceArray) else np.asarray(F, np.uint8)
+    Fh = F.to_host(stream=gq.stream) if isinstance(F, dev.DeviceArray) else np.asarray(F, np.uint8)
     return float((Y.reshape(-1, bs) == Fh.reshape(-1, bs)).all(-1).mean())

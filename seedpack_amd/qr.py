@@ -347,7 +347,7 @@ def decode(T, buf, items, seed_dev, imx_dev=None, stream=None):
 def intervals(T, blocks, nw, stream=None):
     """device uint8 blocks of non-grid type T -> (lo, hi) float32 DeviceArrays: the interval of values
     each weight's code stands for (qr.py:1093-1098)"""
-    blocks = blocks if isinstance(blocks, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(blocks, np.uint8))
+    blocks = blocks if isinstance(blocks, dev.DeviceArray) else dev.DeviceArray.from_host(np.ascontiguousarray(blocks, np.uint8), stream)
     lo, hi = dev.DeviceArray(nw, np.float32), dev.DeviceArray(nw, np.float32)
     check(lib().spa_qr_intervals(T, blocks.ptr, nw, lo.ptr, hi.ptr, stream))
     return lo, hi

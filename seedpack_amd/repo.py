@@ -28,7 +28,12 @@ its quantized tensors are dequantized for the others' requantization and seed th
 directly. A file that no base shares a tensor with is coded alone: the Q8_0 codec M22 (q8.Q8Parts)
 when at least half of its bytes are Q8_0 tensors (repo3.py:1190-1215), else zstd.
 
-Not built here (they raise): split GGUF models, quants made with another imatrix (imxfit).
+Quant files made with another importance matrix (another chunk count in their metadata) form sets;
+the importance of their legacy-quant inputs is fitted back from the first file of a set as it is
+coded (imxfit.py; repo3.py:1241-1352), kept in the archive ("imx" chunk), and the set's files are
+predicted with it.
+
+Not built here (they raise): split GGUF models.
 """
 import collections
 import fnmatch
@@ -44,7 +49,7 @@ from concurrent.futures import ThreadPoolExecutor, wait as futures_wait
 
 import numpy as np
 
-from . import container, device as dev, gguf, header, imatrix as imx_mod, qr, r2, residual, zstd
+from . import container, device as dev, gguf, header, imatrix as imx_mod, imxfit, qr, r2, residual, zstd
 from ._lib import check, lib
 from .framing import nbytes, pack, pack_parts, unpack
 from .gpuquant import GPUQuant
@@ -65,6 +70,7 @@ REF_KEEP = 3 << 30                   # bytes of referenced tensors per window (r
 BUNDLE_MAX = 64 << 20                # other files up to this size go into the lzma bundle (repo3.py:1364)
 Q8_MIN = 0.5                         # a base-less file with this share of Q8_0 bytes: the Q8_0 codec (repo3.py:1191)
 DQ_CACHE = 32 << 30                  # dequantized seed tensors kept in HBM (float32 bytes)
+FIT_ROWS = 1 << 24                   # weights per piece of a tensor in the importance fit (repo3.py:1246)
 SPARSE = 0.02                        # residuals with fewer non-zero bytes: zstd level >= 9 (repo3.py:45)
 SKIP_DIRS = {".git", ".cache", "__pycache__"}
 F32, F16, BF16 = 0, 1, 30
@@ -308,8 +314,9 @@ def process_order(files, groups):
     sharing a (tensor name, type) pair keep their archive order -- a reference can only point to an
     earlier file with the same tensor (repo3.py:2006-2030), so processing them in any such order makes
     the same archive. A group whose potential references could exceed a window's REF_KEEP budget (then
-    the decisions depend on the order of all its files) keeps its archive order throughout.
-    files: {index: (bytes, {(name, type)}, group, {window: potential reference bytes})}"""
+    the decisions depend on the order of all its files) keeps its archive order throughout; files of
+    one fitted-importance set keep their archive order (the first one's tensors are fitted from).
+    files: {index: (bytes, {(name, type)}, group, {window: potential reference bytes}[, set])}"""
     ks = sorted(files)
     strict = set()
     for g in set(v[2] for v in files.values()):
@@ -323,6 +330,8 @@ def process_order(files, groups):
 
     def before(j, i):                       # must j (archive order j < i) be processed before i?
         gj, gi = files[j][2], files[i][2]
+        if len(files[j]) > 4 and files[j][4] and files[j][4] == files[i][4]:
+            return True                     # a fitted-importance set: its first file fits for the others
         return gj == gi and (gi in strict or files[j][1] & files[i][1])
 
     # a file's priority: the largest file that waits for it (itself included), so that a small file
@@ -430,6 +439,7 @@ class Packer:
         self.timing = []
         self.stats = collections.Counter()
         self.sizes = {}
+        self.file_set, self.fit_wait, self.fit_sig, self.fit_done, self.imx_sets = {}, {}, {}, {}, {}
 
     # ---------------------------------------------------------------- bases
     def _load_base(self, path, piece=1 << 30):
@@ -564,10 +574,17 @@ class Packer:
                 continue
             mine.append((t, k))
         self.stats["ref"] += len(refs)
+        kset = self.file_set.get(fi, 0)
+        if self.fit_wait.get(kset):
+            # the set's importance fitted from this file's tensors, window by window (repo3.py:2041-2044)
+            for w in sorted({wins_of[t.name] for t, _ in mine}):
+                self._fit_from(kset, [t for t, k in mine if k == "rq" and wins_of[t.name] == w], F, b)
+        fitted = self.imx_sets.get(kset, {})
         rts = [residual.Tensor(t.name, t.type, t.shape[0], F.view(t.offset, (t.nbytes,), np.uint8),
-                               b.view(b.by_name[t.name], st), imatrix=imx_map.get(t.name), base_type=b.by_name[t.name].type,
-                               numel=t.numel) for t, _ in mine]
-        res = residual.residual_window(rts, self.gq, stream=st) if rts else []
+                               b.view(b.by_name[t.name], st), imatrix=imx_map.get(t.name),
+                               fitted={kset: fitted[t.name]} if t.name in fitted else None,
+                               base_type=b.by_name[t.name].type, numel=t.numel) for t, _ in mine]
+        res = residual.residual_window(rts, self.gq, fitted_set=kset, stream=st) if rts else []
         tm["regrow"] = time.perf_counter()
         out = {t.name: r for (t, _), r in zip(mine, res)}
         for t, _ in mine:
@@ -611,6 +628,99 @@ class Packer:
         return {"fi": fi, "F": F, "qjobs": qjobs, "qmeta": qmeta, "qregs": qregs,
                 "span": self._zspan(pred, wins_of, job["last_window"], size), "entry": entry, "zdict": b.header,
                 "tm": tm}
+
+    # ---------------------------------------------------------------- fitted importance (imxfit)
+    def _fit_plan(self, names, heads, imx_all, pub):
+        """the sets of files made with another importance matrix (repo3.py:1248-1274) -> self.file_set
+        {file index: set k}, self.fit_wait {k: input names still to be fitted}, self.fit_sig {k: (chunk
+        count, dataset)}; pub: the repository imatrix's chunk count"""
+        self.file_set, self.fit_wait, self.fit_sig, self.fit_done, self.imx_sets = {}, {}, {}, {}, {}
+        self.imx_all = imx_all
+        if pub is None or not imx_all:
+            return
+        sigs = {}
+        for fi, n in enumerate(names):
+            meta = heads[n][0]
+            cc = meta.get("quantize.imatrix.chunks_count")
+            if cc is not None and int(cc) != pub:
+                sigs.setdefault((int(cc), str(meta.get("quantize.imatrix.dataset", ""))), []).append(fi)
+        self.by_input = {}                  # an input's importance bytes -> the names sharing it
+        for n, e in imx_all.items():
+            self.by_input.setdefault(np.asarray(e, np.float32).tobytes(), []).append(n)
+        for k, (sig, idx) in enumerate(sigs.items(), 1):
+            self.fit_sig[k], self.imx_sets[k], self.fit_done[k] = sig, {}, []
+            self.file_set.update({i: k for i in idx})
+            self.fit_wait[k] = {nm for i in idx for t in heads[names[i]][1] if t.type in imxfit.LS_TYPES
+                                and t.name in imx_all
+                                for nm in self.by_input[np.asarray(imx_all[t.name], np.float32).tobytes()]}
+
+    def _f32_rows(self, b, bt, r0, r1):
+        """rows r0:r1 of base tensor bt as float32 (rows, cols) on the device"""
+        cols = int(bt.shape[0])
+        n = (r1 - r0) * cols
+        if bt.type == F32:
+            return b.d.view(bt.offset + 4 * r0 * cols, (r1 - r0, cols), np.float32)
+        isz, dt = 2, (np.uint16 if bt.type == BF16 else np.float16)
+        src = b.d.view(bt.offset + isz * r0 * cols, (n,), dt)
+        return residual.float_prediction(src, F32, self.stream.handle).view(0, (r1 - r0, cols), np.float32)
+
+    def _fit_from(self, k, tens, F, b):
+        """fit set k's importance of the inputs still waiting from the file's legacy-quant tensors
+        `tens` (their bytes in F, the device copy of the file), the base b resident (repo3.py:1276-1323):
+        per input the conditions of its tensors summed in pieces of FIT_ROWS weights, the smallest
+        eigenvector, kept where it reproduces more blocks of the last rows of the first tensor"""
+        st = self.stream.handle
+        wait, imx_all = self.fit_wait.get(k), self.imx_all
+        groups = {}
+        for t in tens:
+            e, bt = imx_all.get(t.name), b.by_name.get(t.name)
+            if wait and t.name in wait and t.type in imxfit.LS_TYPES and e is not None and bt is not None \
+                    and bt.type in (F32, F16, BF16) and len(e) == bt.shape[0]:
+                groups.setdefault(np.asarray(e, np.float32).tobytes(), []).append(t)
+        t0 = time.perf_counter()
+        for key, members in groups.items():
+            G = None
+            for t in members:
+                bt = b.by_name[t.name]
+                cols, nrow = int(bt.shape[0]), int(bt.shape[1])
+                _, qk, bs = QFUN[t.type]
+                rb, step = cols // qk * bs, max(1, FIT_ROWS // cols)
+                for r0 in range(0, nrow, step):
+                    r1 = min(nrow, r0 + step)
+                    x = self._f32_rows(b, bt, r0, r1)
+                    f = F.view(t.offset + r0 * rb, ((r1 - r0) * rb,), np.uint8)
+                    g = imxfit.ls_gram(self.gq, t.type, x, f, stream=st)
+                    G = g if G is None else G + g
+            e0 = np.frombuffer(key, np.float32)
+            e = imxfit.ls_solve(G, e0)
+            t = members[0]
+            bt = b.by_name[t.name]
+            cols, nrow = int(bt.shape[0]), int(bt.shape[1])
+            _, qk, bs = QFUN[t.type]
+            rb, n = cols // qk * bs, min(nrow, max(64, FIT_ROWS // 8 // cols))
+            x = self._f32_rows(b, bt, nrow - n, nrow)
+            f = F.view(t.offset + (nrow - n) * rb, (n * rb,), np.uint8)
+            before, after = (imxfit.equal_blocks(self.gq, t.type, x, f, v) for v in (e0, e))
+            names = self.by_input[key]
+            wait.difference_update(names)
+            if after > before + 0.005:
+                for nm in names:
+                    self.imx_sets[k][nm] = e
+                self.fit_done[k].append((names, e, e0, before, after))
+        self._cpu(("importance fit wall_s", time.perf_counter() - t0))
+
+    def _fit_chunk(self):
+        """the fitted importance sets as the "imx" chunk and its manifest entry, or None (repo3.py:1325-1340)"""
+        meta, data = [], []
+        for k in sorted(self.fit_done):
+            done = self.fit_done[k]
+            meta.append({"chunks": self.fit_sig[k][0], "dataset": self.fit_sig[k][1], "groups": [d[0] for d in done]})
+            data += [(e.view(np.uint32) ^ e0.view(np.uint32)).tobytes() for _, e, e0, _, _ in done]
+        self.stats["imx_fit"] = sum(len(m["groups"]) for m in meta)
+        if not self.stats["imx_fit"]:
+            return None
+        return pack({"meta": zstd.zstd_c(json.dumps(meta).encode()), "data": zstd.zstd_c(b"".join(data), 19)}), \
+            {"chunk": "imx", "sets": len(meta)}
 
     def _lane(self):
         """this zstd lane's stream, page-locked piece and device counter"""
@@ -771,6 +881,7 @@ class Packer:
                     continue
                 best = [k for k, c in enumerate(common) if c == max(common)][0]
                 per_base[best].append((fi, n, ts))
+            self._fit_plan(names, heads, imx_all, imx_mod.chunks(ex[imx_name]) if imx_name else None)
             # derived files: per base, grouped by tensor order; windows over each group's order
             jobs, plain, order_done = {}, [], []
             for bi, items in per_base.items():
@@ -807,7 +918,7 @@ class Packer:
                     if k and (t.name, t.type) in prev and t.nbytes >= DUP_MIN:
                         pot[j["wins_of"][t.name]] += t.nbytes
                 prev |= keys
-                info[fi] = (os.path.getsize(j["path"]), keys, j["group"], pot)
+                info[fi] = (os.path.getsize(j["path"]), keys, j["group"], pot, self.file_set.get(fi, 0))
             porder = process_order(info, None)
             # the first file read while the bases are uploaded, their checksums and codecs started
             # (one stream each)
@@ -872,6 +983,12 @@ class Packer:
             manifest = {"method": METHODS[self.method], "bases": list(bases), "seeds": seeds, "files": entries,
                         "extras": {"bundle": list(ex), "single": big}}
             if self.stats["qr_grid"] or self.stats["ref"]:
+                manifest["needs"] = "0.3.0"
+            fitted = self._fit_chunk()
+            if fitted:
+                w.put(fitted[1]["chunk"], fitted[0])
+                self.sizes["fitted importance"] = len(fitted[0])
+                manifest["imx_fit"] = fitted[1]
                 manifest["needs"] = "0.3.0"
             w.put("manifest", zstd.compress(json.dumps(manifest).encode(), 19))
             hashes = {n: (h.result() if hasattr(h, "result") else h) for n, h in hashes.items()}
@@ -990,8 +1107,8 @@ class Unpacker:
             return self._run_m30(r, meta, manifest, outdir, patterns, t0)
         if not manifest["method"].startswith(("M29", "M28")):
             raise NotImplementedError(f"archive method {manifest['method']!r}: only M28 / M29 / M30 archives are read here")
-        if manifest.get("joined") or manifest.get("imx_fit"):
-            raise NotImplementedError("split models and fitted importance are not built")
+        if manifest.get("joined"):
+            raise NotImplementedError("split models are not built")
         seeds = set(manifest.get("seeds", []))
         cat = {f["name"]: f for f in meta["files"]}
         want = set(select_names(meta["files"], patterns))
@@ -1057,6 +1174,7 @@ class Unpacker:
             imx_off[k] = o
             o += v.size
         imx_map = {k: imx_dev.view(4 * imx_off[k], (v.size,), np.float32) for k, v in imx_all.items()}
+        self.imx_sets = self._load_imx(r.get(manifest["imx_fit"]["chunk"]), imx_all) if manifest.get("imx_fit") else {}
         # bases, decoded into HBM
         bases = {}
         for i in sorted(need_b):
@@ -1163,6 +1281,23 @@ class Unpacker:
                 "missing": [n for n in want if n not in results], "bytes": nbytes_, "seconds": dt,
                 "GB_s": nbytes_ / dt / 1e9}
 
+    @staticmethod
+    def _load_imx(buf, imx_all):
+        """the fitted importance sets of an archive ("imx" chunk) -> {set k: {name: importance}}
+        (repo3.py:1342-1355)"""
+        ch = unpack(memoryview(bytes(buf)))
+        meta = json.loads(zstd.decompress(ch["meta"]))
+        raw, o, sets = zstd.decompress(ch["data"]), 0, {}
+        for k, m in enumerate(meta, 1):
+            sets[k] = {}
+            for names in m["groups"]:
+                e0 = np.asarray(imx_all[names[0]], np.float32)
+                e = (np.frombuffer(raw, np.uint32, len(e0), o) ^ e0.view(np.uint32)).view(np.float32)
+                o += e.nbytes
+                for n in names:
+                    sets[k][n] = e
+        return sets
+
     def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map):
         """file i's bytes from its residual (in `resid`, rebuilt in place) on the device"""
         st = self.stream.handle
@@ -1173,10 +1308,14 @@ class Unpacker:
         plan = m["plan"]
         ttype = {e[0]: (e[3] if len(e) > 3 else tens[e[0]].type) for e in plan}
 
+        fitted = self.imx_sets
+
         def tensor(name):
             bt = b.by_name[name]
             return residual.Tensor(name, ttype[name], bt.shape[0], R.view(tens[name].offset, (tens[name].nbytes,), np.uint8),
-                                   b.view(bt, st), imatrix=imx_map.get(name), base_type=bt.type, numel=tens[name].numel)
+                                   b.view(bt, st), imatrix=imx_map.get(name),
+                                   fitted={k: s_[name] for k, s_ in fitted.items() if name in s_},
+                                   base_type=bt.type, numel=tens[name].numel)
 
         for e in plan:
             name, kind, v = e[0], e[1], e[2]

@@ -188,6 +188,60 @@ def test_seed_repo_without_base(sibling_repo, tmp_path):
         assert open(os.path.join(src, n), "rb").read() == open(os.path.join(out, n), "rb").read(), n
 
 
+def test_fitted_importance_repo(small_repo, tmp_path):
+    """quants made with another importance matrix (another chunk count in their metadata): their
+    importance is fitted back from the first such file (imxfit), stored in the "imx" chunk, and both
+    files of the set are predicted with it -- most tensors become exact requantizations; every file
+    extracts byte-identical"""
+    import shutil
+    from seedpack_amd import imatrix as imx_mod
+    from seedpack_amd.gpuquant import GPUQuant
+    root = small_repo[0]
+    src = str(tmp_path / "src")
+    os.makedirs(src)
+    for n in ("model-BF16.gguf", "imatrix.dat", "model-Q4_0.gguf"):
+        shutil.copy(os.path.join(root, n), src)
+    base = np.fromfile(os.path.join(root, "model-BF16.gguf"), np.uint8)
+    g = gguf.GGUF(base)
+    imx = imx_mod.load(open(os.path.join(root, "imatrix.dat"), "rb").read())
+    rng = np.random.Generator(np.random.PCG64(9))
+    alt = {n: (np.asarray(v, np.float32) ** 0.5 * np.exp(rng.normal(0, 0.5, len(v)))).astype(np.float32)
+           for n, v in imx.items()}
+    gq = GPUQuant()
+    for fname, T in (("alt-Q4_0.gguf", 2), ("alt-Q5_1.gguf", 7)):
+        tensors = []
+        for t in g.tensors:
+            raw = base[t.offset:t.offset + t.nbytes]
+            if len(t.shape) == 2:
+                x = dev.DeviceArray.from_host(raw.view(np.uint16))
+                y = gq.quantize_tensors(T, [(x, t.shape[0])], [alt[t.name]], device=True)[0].to_host()
+                tensors.append((t.name, t.shape, T, y.tobytes()))
+            else:
+                tensors.append((t.name, t.shape, t.type, raw.tobytes()))
+        _gguf_file(os.path.join(src, fname), {"general.architecture": "qwen35", "general.alignment": 32,
+                                              "quantize.imatrix.file": "other.dat",
+                                              "quantize.imatrix.dataset": "other.txt",
+                                              "quantize.imatrix.chunks_count": 64}, tensors)
+    a = str(tmp_path / "fit.seedpack")
+    say("case fitted importance: pack")
+    stats = repo.pack_repo([src], a)
+    r = container.Reader(a)
+    man = json.loads(zstd.decompress(r.get("manifest")))
+    assert man.get("imx_fit") == {"chunk": "imx", "sets": 1} and "imx" in r.chunks
+    assert stats["stats"]["imx_fit"] > 0, stats["stats"]
+    files = {m["name"]: m for m in man["files"]}
+    for fname in ("alt-Q4_0.gguf", "alt-Q5_1.gguf"):
+        fitted = [e for e in files[fname]["plan"] if isinstance(e[2], int) and e[2] >= 1000]
+        assert len(fitted) >= len(files[fname]["plan"]) // 2, (fname, files[fname]["plan"])
+    assert not any(isinstance(e[2], int) and e[2] >= 1000 for e in files["model-Q4_0.gguf"]["plan"])
+    say("case fitted importance: unpack", stats["stats"])
+    out = str(tmp_path / "out")
+    res = repo.unpack_repo(a, out)
+    assert not res["bad"] and not res["missing"], res
+    for n in sorted(os.listdir(src)):
+        assert open(os.path.join(src, n), "rb").read() == open(os.path.join(out, n), "rb").read(), n
+
+
 def test_small_repo_archive_layout(small_repo):
     root, arc, sizes, stats = small_repo
     r = container.Reader(arc)
