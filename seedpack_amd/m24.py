@@ -138,8 +138,8 @@ class M24BF16:
         check(lib().spa_qr_gather(out.ptr, cap, out_len.ptr, offs_d.ptr, nseg, dst.ptr, st))
         return dst.to_host(stream=st)[:int(offs[-1])].tobytes(), lens, store_tables(freq, used)
 
-    def decompress_dev(self, ch):
-        """the chunk's parts -> the whole file as a DeviceArray"""
+    def decompress_dev(self, ch, into=None):
+        """the chunk's parts -> the whole file as a DeviceArray (`into`, of the file's size, if given)"""
         st = self.stream
         layout = json.loads(zstd.decompress(ch["layout"]))
         with ThreadPoolExecutor(1) as ex:
@@ -151,7 +151,9 @@ class M24BF16:
             rfi = np.frombuffer(side, np.int16, nrow, 0)
             cfi = np.frombuffer(side, np.int16, ncol, 2 * nrow)
             scl = np.frombuffer(side, np.int8, ncol, 2 * nrow + 2 * ncol)
-            out = dev.DeviceArray(max(1, layout["size"]), np.uint8)
+            if into is not None and into.nbytes != layout["size"]:
+                raise ValueError(f"a file of {layout['size']} bytes for a place of {into.nbytes}")
+            out = into if into is not None else dev.DeviceArray(max(1, layout["size"]), np.uint8)
             nseg = len(sg)
             if nseg:
                 freq, used = load_tables(ch["tables"])

@@ -388,14 +388,15 @@ class BF16v2:
         ch["rest"] = rest
         return pack_parts({k: ch[k] for k in self.ORDER[order]})
 
-    def decompress(self, parts, out=None, device=False, alloc=None):
+    def decompress(self, parts, out=None, device=False, alloc=None, into=None):
         """the file back (bf16v2.py:422-486): `parts` is compress()'s dict or a packed chunk
         (compress_parts' bytes); the coded tensors are decoded on the device, the other bytes come
         from `out` (already in place) or from the "rest" part when there is one, else zeros.
         alloc(n) -> writable uint8 array for the output. device=True: the result stays in HBM, a
         DeviceArray of the file's bytes up to the end of its last coded tensor, only the coded
-        tensors written (decompress_dev); device="full": the whole file in HBM, the other bytes
-        uploaded from the "rest" part (-> (DeviceArray, rest_of bytes))."""
+        tensors written (decompress_dev); device="full": the whole file in HBM (in `into`, a
+        DeviceArray of the file's size, if given), the other bytes uploaded from the "rest" part
+        (-> (DeviceArray, rest_of bytes))."""
         st = self.stream
         tm = _Timer(self.timing, st)
         if not isinstance(parts, dict):
@@ -404,7 +405,7 @@ class BF16v2:
         tm.lap("tables")
         layout, nt = dec.layout, len(dec.layout["t"])
         if device == "full":
-            return self._decompress_full(parts, dec, tm)
+            return self._decompress_full(parts, dec, tm, into)
         if nt == 0 and device:
             return dev.DeviceArray(1, np.uint8)
         if nt:
@@ -431,9 +432,11 @@ class BF16v2:
             fill_rest(out, header_d(bytes(parts["rest"])), layout)
         return out
 
-    def _decompress_full(self, parts, dec, tm):
+    def _decompress_full(self, parts, dec, tm, into=None):
         st, layout = self.stream, dec.layout
-        d = dev.DeviceArray(max(1, layout["size"]), np.uint8)
+        if into is not None and into.nbytes != layout["size"]:
+            raise ValueError(f"a file of {layout['size']} bytes for a place of {into.nbytes}")
+        d = into if into is not None else dev.DeviceArray(max(1, layout["size"]), np.uint8)
         t = layout["t"]
         if t:
             s_d = _Decoder.upload(parts["stream"], st)

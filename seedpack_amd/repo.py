@@ -33,9 +33,12 @@ the importance of their legacy-quant inputs is fitted back from the first file o
 coded (imxfit.py; repo3.py:1241-1352), kept in the archive ("imx" chunk), and the set's files are
 predicted with it.
 
-Not built here (they raise): split GGUF models.
+The shards of a split model (llama.cpp's gguf-split names, every shard present) are coded as
+bases of their own and predict as one base: the shards one after another in HBM, each tensor at its
+shard's start plus its offset there (repo3.py:271-285, :634-647, :1396-1408).
 """
 import collections
+import dataclasses
 import fnmatch
 import hashlib
 import json
@@ -131,6 +134,22 @@ def order_groups(orders):
         else:
             groups[orders[k]] = [k]
     return {g: sorted(ks) for g, ks in groups.items()}
+
+
+_SHARD = re.compile(r"^(.*)-(\d{5})-of-(\d{5})\.gguf$")
+
+
+def joined_groups(names):
+    """the split models among `names`: for each, the indices of its shards in shard order, when every
+    shard of it (llama.cpp's gguf-split names <model>-00001-of-0000N.gguf ... -0000N-of-0000N.gguf,
+    N > 1) is there (repo3.py:271-285)"""
+    models = collections.defaultdict(dict)
+    for i, n in enumerate(names):
+        m = _SHARD.match(n)
+        if m:
+            models[(m.group(1), int(m.group(3)))][int(m.group(2))] = i
+    return [[shards[k] for k in range(1, count + 1)] for (_, count), shards in models.items()
+            if count > 1 and set(shards) == set(range(1, count + 1))]
 
 
 def windows(nbytes_, window=WINDOW, pred=None, pred_window=PRED_WINDOW):
@@ -361,6 +380,20 @@ class _Base:
         self.by_name = {t.name: t for t in g.tensors}
         self.dq, self.dq_bytes = collections.OrderedDict(), 0
 
+    @classmethod
+    def joined(cls, index, parts, d=None):
+        """a split model as one base (repo3.py:634-647): parts [(start, shard base)], shard k's bytes from
+        byte start_k of `d` on, every tensor at start_k plus its offset in the shard; the residuals'
+        dictionary is the first shard's header"""
+        b = cls.__new__(cls)
+        first = parts[0][1]
+        b.index, b.name, b.d, b.g, b.seed = index, f"{first.name} + {len(parts) - 1} more shard(s)", d, None, False
+        b.header = first.header
+        b.by_name = {n: dataclasses.replace(t, offset=t.offset + start)
+                     for start, sb in parts for n, t in sb.by_name.items()}
+        b.dq, b.dq_bytes = collections.OrderedDict(), 0
+        return b
+
     def view(self, t, stream=None):
         """base tensor t as the quantizers take it (bf16 bits / f16 / f32; a quantized tensor as f32)"""
         if t.type in QFUN:
@@ -442,11 +475,14 @@ class Packer:
         self.file_set, self.fit_wait, self.fit_sig, self.fit_done, self.imx_sets = {}, {}, {}, {}, {}
 
     # ---------------------------------------------------------------- bases
-    def _load_base(self, path, piece=1 << 30):
-        """the base file uploaded whole into HBM, read through two page-locked pieces (the next piece is
-        read, on a thread of its own, while the current one is copied)"""
+    def _load_base(self, path, piece=1 << 30, into=None):
+        """the base file uploaded whole into HBM (into `into`, a split model's place for the shard, if
+        given), read through two page-locked pieces (the next piece is read, on a thread of its own,
+        while the current one is copied)"""
         size = os.path.getsize(path)
-        d = dev.DeviceArray(size, np.uint8)
+        if into is not None and into.nbytes != size:
+            raise ValueError(f"{path}: {size} bytes for a place of {into.nbytes}")
+        d = into if into is not None else dev.DeviceArray(size, np.uint8)
         bufs = [self.pool.acquire(min(piece, max(size, 1))) for _ in range(2)]
         try:
             with ThreadPoolExecutor(1) as rd:
@@ -813,8 +849,6 @@ class Packer:
         bases = {n: p for n, p in files.items() if roles[n] == "base"}
         derived = {n: p for n, p in files.items() if roles[n] == "derived"}
         extras = {n: p for n, p in files.items() if roles[n] is None}
-        if self.method != "m30" and any(re.match(r"^.*-\d{5}-of-\d{5}\.gguf$", n) for n in bases):
-            raise NotImplementedError("split GGUF models (joined bases) are not built")
         seeds = []
         if self.method != "m30":
             # quants without their BF16 model: the senior quant of each group is coded like a base and
@@ -822,7 +856,17 @@ class Packer:
             seeds = pick_seeds([heads[n][1] for n in bases], {n: heads[n][1] for n in derived})
             bases = {**bases, **{n: derived[n] for n in seeds}}
             derived = {n: p for n, p in derived.items() if n not in seeds}
+        # the shards of a split model: bases of their own, and one more base joining them (base index
+        # len(bases) + k for split model k; repo3.py:1396-1408)
+        bnames = list(bases)
+        bsize = [os.path.getsize(bases[n]) for n in bnames]
+        joined = []
+        for grp in (joined_groups(bnames) if self.method != "m30" else []):
+            if not any(bnames[i] in seeds for i in grp):
+                starts = np.cumsum([0] + [bsize[i] for i in grp[:-1]]).tolist()
+                joined.append({"parts": [[i, s_] for i, s_ in zip(grp, starts)], "size": sum(bsize[i] for i in grp)})
         base_names = [{t.name for t in heads[n][1]} for n in bases]
+        base_names += [set().union(*(base_names[i] for i, _ in j["parts"])) for j in joined]
         total = sum(os.path.getsize(p) for p in files.values())
         hashes = {}
         w = container.Writer(output)
@@ -859,6 +903,8 @@ class Packer:
             for i, (n, p) in enumerate(bases.items()):
                 host = np.memmap(p, np.uint8, "r") if os.path.getsize(p) else np.zeros(0, np.uint8)
                 loaded.append((host, _Base(i, n, host, None, gguf.GGUF(host), seed=n in seeds)))
+            allb = [b for _, b in loaded] + [_Base.joined(len(bnames) + k, [(s_, loaded[i][1]) for i, s_ in j["parts"]])
+                                             for k, j in enumerate(joined)]
             # the repository's importance per tensor on the device (the grid QR types read it)
             imx_vecs = {k: np.asarray(v, np.float32) for k, v in imx_all.items()}
             flat = np.concatenate(list(imx_vecs.values())) if imx_vecs else np.zeros(1, np.float32)
@@ -879,13 +925,15 @@ class Packer:
                 if not common or max(common) == 0:
                     alone.append((fi, n, ts))
                     continue
-                best = [k for k, c in enumerate(common) if c == max(common)][0]
-                per_base[best].append((fi, n, ts))
+                # the base sharing most tensor names; on a tie a split model rather than one of its
+                # shards (repo3.py:649-657)
+                best = [k for k, c in enumerate(common) if c == max(common)]
+                per_base[best[-1] if best[-1] >= len(bnames) else best[0]].append((fi, n, ts))
             self._fit_plan(names, heads, imx_all, imx_mod.chunks(ex[imx_name]) if imx_name else None)
             # derived files: per base, grouped by tensor order; windows over each group's order
             jobs, plain, order_done = {}, [], []
             for bi, items in per_base.items():
-                b = loaded[bi][1]
+                b = allb[bi]
                 found = []
                 for fi, n, ts in items:
                     tk = [(t, self._kind(b, t, imx_all)) for t in ts]
@@ -925,9 +973,14 @@ class Packer:
             ahead = self.reader.submit(self._read_file, jobs[porder[0]]) if porder else None
             side = ThreadPoolExecutor(1)
             base_jobs = []
+            place = {}                                 # a split model's shards: one after another in HBM
+            for k, j in enumerate(joined):
+                allb[len(bnames) + k].d = d = dev.DeviceArray(j["size"], np.uint8)
+                for i, s_ in j["parts"]:
+                    place[i] = d.view(s_, (bsize[i],), np.uint8)
             for (host, b), (n, p) in zip(loaded, bases.items()):
                 hashes[n] = self.hasher.submit(file_sha256, p)
-                b.d = self._load_base(p)
+                b.d = self._load_base(p, into=place.get(b.index))
                 base_jobs.append(side.submit(self._code_base, b, host, "stream" if b.index == 0 else "parts"))
                 later[n] = base_jobs[-1]
             if base_jobs:
@@ -943,7 +996,7 @@ class Packer:
             for k, fi in enumerate(porder):
                 job = ahead.result()
                 ahead = self.reader.submit(self._read_file, jobs[porder[k + 1]]) if k + 1 < len(porder) else None
-                b = loaded[job["base"]][1]
+                b = allb[job["base"]]
                 hashes[names[fi]] = job["sha256"]
                 state = self._device_file(job, b, imx_dev, imx_off, imx_map)
                 zjobs[fi] = self.zpool.submit(self._finish_file, state)
@@ -952,7 +1005,7 @@ class Packer:
             phase("derived files on the device")
             for bi, fi, n in plain:
                 # nothing to predict: the file zstd'd against the base header (repo3.py:2062-2076)
-                b = loaded[bi][1]
+                b = allb[bi]
                 data = open(derived[n], "rb").read()
                 hashes[n] = self.hasher.submit(_ws, data)
                 entries[fi] = {"name": n, "size": len(data), "base": b.index, "plan": []}
@@ -982,6 +1035,9 @@ class Packer:
             phase("bases and other files coded")
             manifest = {"method": METHODS[self.method], "bases": list(bases), "seeds": seeds, "files": entries,
                         "extras": {"bundle": list(ex), "single": big}}
+            if joined:
+                manifest["joined"] = joined            # base len(bases) + k: split model k
+                manifest["needs"] = "0.3.0"
             if self.stats["qr_grid"] or self.stats["ref"]:
                 manifest["needs"] = "0.3.0"
             fitted = self._fit_chunk()
@@ -1107,9 +1163,8 @@ class Unpacker:
             return self._run_m30(r, meta, manifest, outdir, patterns, t0)
         if not manifest["method"].startswith(("M29", "M28")):
             raise NotImplementedError(f"archive method {manifest['method']!r}: only M28 / M29 / M30 archives are read here")
-        if manifest.get("joined"):
-            raise NotImplementedError("split models are not built")
         seeds = set(manifest.get("seeds", []))
+        nb, joined = len(manifest["bases"]), manifest.get("joined", [])
         cat = {f["name"]: f for f in meta["files"]}
         want = set(select_names(meta["files"], patterns))
         mf = manifest["files"]
@@ -1175,11 +1230,20 @@ class Unpacker:
             o += v.size
         imx_map = {k: imx_dev.view(4 * imx_off[k], (v.size,), np.float32) for k, v in imx_all.items()}
         self.imx_sets = self._load_imx(r.get(manifest["imx_fit"]["chunk"]), imx_all) if manifest.get("imx_fit") else {}
-        # bases, decoded into HBM
-        bases = {}
-        for i in sorted(need_b):
+        # bases, decoded into HBM; the shards of a split model that a file predicts from one after
+        # another in one allocation (repo3.py:2307-2313)
+        bases, place, jd = {}, {}, {}
+        for k, j in enumerate(joined):
+            if nb + k in need_b:
+                jd[k] = d = dev.DeviceArray(j["size"], np.uint8)
+                ends = [s_ for _, s_ in j["parts"][1:]] + [j["size"]]
+                for (i, s_), e_ in zip(j["parts"], ends):
+                    place[i] = d.view(s_, (e_ - s_,), np.uint8)
+        for i in sorted({i for i in need_b if i < nb} | set(place)):
             name = manifest["bases"][i]
             if name in seeds:                               # a seed: its file decoded by parts (seed.py)
+                if i in place:
+                    raise ValueError(f"seed {name} is a shard of a split model")
                 data = SeedCodec(stream=self.stream.handle).decompress(r.get(f"b{i}"))
                 d = dev.DeviceArray.from_host(data, self.stream.handle)
                 bases[i] = _Base(i, name, data, d, gguf.GGUF(data, light=True), seed=True)
@@ -1189,9 +1253,10 @@ class Unpacker:
                 continue
             ch = unpack(memoryview(r.get(f"b{i}")))
             if "r2" in ch:
-                d, rest = r2.BF16v2(stream=self.stream.handle).decompress(unpack(ch["r2"]), device="full")
+                d, rest = r2.BF16v2(stream=self.stream.handle).decompress(unpack(ch["r2"]), device="full",
+                                                                         into=place.get(i))
             elif "side" in ch and "stream" in ch:          # an M24 chunk (method m28)
-                d = M24BF16(stream=self.stream.handle).decompress_dev(ch)
+                d = M24BF16(stream=self.stream.handle).decompress_dev(ch, into=place.get(i))
                 lay = json.loads(zstd.decompress(ch["layout"]))
                 first = min([t[0] for t in lay["t"]] + [lay["size"]])
                 rest = d.view(0, (first,), np.uint8).to_host(stream=self.stream.handle)
@@ -1205,6 +1270,8 @@ class Unpacker:
                 check(lib().spa_memcpy_d2h(host.ctypes.data, d.ptr, d.nbytes, self.stream.handle))
                 jobs.append(self.files.submit(check_write, name, host, True))
             log(self.verbose, f"  base {name}: decoded, {time.perf_counter() - t0:.1f} s")
+        for k, d in jd.items():
+            bases[nb + k] = _Base.joined(nb + k, [(s_, bases[i]) for i, s_ in joined[k]["parts"]], d)
         # quantized files, in archive order; tensors that later files copy are kept on the device
         kept, done = {}, set()
         # largest first, a file after the files it copies tensors from (so the checksum of a big

@@ -242,3 +242,21 @@ def test_process_order_keeps_dependent_files_in_order():
     files[0] = (5, {("a", 1)}, 0, {})
     files[2] = (7, {("a", 1)}, 0, {0: repo.REF_KEEP + 1})
     assert repo.process_order(files, None) == [0, 1, 3, 2]
+
+
+def test_split_models_are_found_only_whole():
+    """the shards of a split GGUF are joined when every shard of it is there, in shard order; a lone
+    shard, a single-shard "split" and other names are not (repo3.py:271-285)"""
+    names = ["m-BF16-00002-of-00003.gguf", "imatrix.dat", "m-BF16-00001-of-00003.gguf", "x-00001-of-00002.gguf",
+             "m-BF16-00003-of-00003.gguf", "one-00001-of-00001.gguf", "sub/m-BF16-00001-of-00002.gguf",
+             "sub/m-BF16-00002-of-00002.gguf", "m-BF16-0001-of-0003.gguf"]
+    assert sorted(repo.joined_groups(names)) == [[2, 0, 4], [6, 7]]
+    assert repo.joined_groups(["a-00001-of-00002.gguf", "a-00002-of-00003.gguf"]) == []
+    # a split model's by-name table: each shard's tensors shifted by the shard's start
+    T = gguf.Tensor
+    s0, s1 = repo._Base.__new__(repo._Base), repo._Base.__new__(repo._Base)
+    s0.name, s0.header, s0.by_name = "m-00001", b"H0", {"a": T("a", (4,), 30, 64, 8)}
+    s1.name, s1.header, s1.by_name = "m-00002", b"H1", {"b": T("b", (4,), 30, 96, 8)}
+    j = repo._Base.joined(5, [(0, s0), (200, s1)])
+    assert j.index == 5 and j.header == b"H0" and j.by_name["a"].offset == 64 and j.by_name["b"].offset == 296
+    assert s1.by_name["b"].offset == 96

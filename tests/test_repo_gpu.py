@@ -242,6 +242,58 @@ def test_fitted_importance_repo(small_repo, tmp_path):
         assert open(os.path.join(src, n), "rb").read() == open(os.path.join(out, n), "rb").read(), n
 
 
+def _split_file(src, dst_fmt, cuts):
+    """llama.cpp gguf-split's layout of the GGUF at `src`: its tensors in len(cuts) + 1 shards (cut
+    before the tensors named in `cuts`), each shard a GGUF of its own with the split keys"""
+    data = np.fromfile(src, np.uint8)
+    g = gguf.GGUF(data)
+    names = [t.name for t in g.tensors]
+    at = [0] + [names.index(c) for c in cuts] + [len(names)]
+    n = len(at) - 1
+    for k in range(n):
+        kv = {"general.architecture": "qwen35", "general.alignment": 32, "split.no": (2, k), "split.count": (2, n),
+              "split.tensors.count": (5, len(names))}
+        _gguf_file(dst_fmt.format(k + 1, n), kv, [(t.name, t.shape, t.type, data[t.offset:t.offset + t.nbytes].tobytes())
+                                                  for t in g.tensors[at[k]:at[k + 1]]])
+
+
+@pytest.mark.parametrize("method", ["m29", "m28"])
+def test_split_model_repo(small_repo, tmp_path, method):
+    """a BF16 model in three gguf-split shards, a quant split in two at other boundaries and two whole
+    quants: the shards are coded as bases and joined into one base that every quant predicts from
+    (manifest "joined", base index len(bases)); every file extracts byte-identical, a quant shard and
+    a base shard alone too"""
+    import shutil
+    root = small_repo[0]
+    src = str(tmp_path / "src")
+    os.makedirs(src)
+    for n in ("imatrix.dat", "model-Q4_K_M.gguf", "model-IQ2_XS.gguf"):
+        shutil.copy(os.path.join(root, n), src)
+    _split_file(os.path.join(root, "model-BF16.gguf"), os.path.join(src, "model-BF16-{:05d}-of-{:05d}.gguf"),
+                ["blk.1.attn_norm.weight", "output_norm.weight"])
+    _split_file(os.path.join(root, "model-Q4_0.gguf"), os.path.join(src, "model-Q4_0-{:05d}-of-{:05d}.gguf"),
+                ["blk.0.ffn_down.weight"])
+    a = str(tmp_path / "split.seedpack")
+    say(f"case split model ({method}): pack")
+    stats = repo.pack_repo([src], a, method=method)
+    man = json.loads(zstd.decompress(container.Reader(a).get("manifest")))
+    shards = [f"model-BF16-{k:05d}-of-00003.gguf" for k in (1, 2, 3)]
+    assert man["bases"] == shards and man["needs"] == "0.3.0"
+    sizes = [os.path.getsize(os.path.join(src, n)) for n in shards]
+    assert man["joined"] == [{"parts": [[0, 0], [1, sizes[0]], [2, sizes[0] + sizes[1]]], "size": sum(sizes)}]
+    assert all(f["base"] == 3 for f in man["files"]), [(f["name"], f["base"]) for f in man["files"]]
+    assert all(f["plan"] for f in man["files"])
+    say(f"case split model ({method}): unpack", stats["stats"])
+    out = str(tmp_path / "out")
+    res = repo.unpack_repo(a, out)
+    assert not res["bad"] and not res["missing"], res
+    for n in sorted(os.listdir(src)):
+        assert open(os.path.join(src, n), "rb").read() == open(os.path.join(out, n), "rb").read(), n
+    for pick in ("model-Q4_0-00002-of-00002.gguf", shards[1]):
+        res = repo.unpack_repo(a, None, [pick])
+        assert res["files"] == {pick: True}, res
+
+
 def test_small_repo_archive_layout(small_repo):
     root, arc, sizes, stats = small_repo
     r = container.Reader(arc)
