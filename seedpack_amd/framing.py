@@ -41,3 +41,19 @@ def unpack(buf):
         chunks[name] = buf[pos:pos + dl]
         pos += dl
     return chunks
+
+
+def index(read, size, base=0):
+    """{name: (offset, length)} of the chunks of a packed buffer of `size` bytes that starts at `base`,
+    reading only its framing through read(offset, n) -> bytes"""
+    (n,), pos, out = struct.unpack("<I", read(base, 4)), base + 4, {}
+    for _ in range(n):
+        (ln,) = struct.unpack("<H", read(pos, 2))
+        name = read(pos + 2, ln).decode()
+        (dl,) = struct.unpack("<Q", read(pos + 2 + ln, 8))
+        pos += 10 + ln
+        if pos + dl > base + size:
+            raise ValueError(f"part {name!r} runs past the end of its buffer")
+        out[name] = (pos, dl)
+        pos += dl
+    return out

@@ -138,12 +138,13 @@ class M24BF16:
         check(lib().spa_qr_gather(out.ptr, cap, out_len.ptr, offs_d.ptr, nseg, dst.ptr, st))
         return dst.to_host(stream=st)[:int(offs[-1])].tobytes(), lens, store_tables(freq, used)
 
-    def decompress_dev(self, ch, into=None):
-        """the chunk's parts -> the whole file as a DeviceArray (`into`, of the file's size, if given)"""
+    def decompress_dev(self, ch, into=None, rest=None):
+        """the chunk's parts -> the whole file as a DeviceArray (`into`, of the file's size, if given;
+        rest: the "rest" part already decoded, if it is)"""
         st = self.stream
         layout = json.loads(zstd.decompress(ch["layout"]))
         with ThreadPoolExecutor(1) as ex:
-            rest = ex.submit(header.header_d, bytes(ch["rest"]))
+            rest = ex.submit(header.header_d, bytes(ch["rest"])) if rest is None else ex.submit(bytes, rest)
             tb, sg = tables(layout)
             nrow = int(sum(nb // 2 // rl for _, nb, rl, _ in layout["t"]))
             ncol = int(sum(rl for _, _, rl, _ in layout["t"]))

@@ -388,7 +388,7 @@ class BF16v2:
         ch["rest"] = rest
         return pack_parts({k: ch[k] for k in self.ORDER[order]})
 
-    def decompress(self, parts, out=None, device=False, alloc=None, into=None):
+    def decompress(self, parts, out=None, device=False, alloc=None, into=None, rest=None):
         """the file back (bf16v2.py:422-486): `parts` is compress()'s dict or a packed chunk
         (compress_parts' bytes); the coded tensors are decoded on the device, the other bytes come
         from `out` (already in place) or from the "rest" part when there is one, else zeros.
@@ -396,7 +396,7 @@ class BF16v2:
         DeviceArray of the file's bytes up to the end of its last coded tensor, only the coded
         tensors written (decompress_dev); device="full": the whole file in HBM (in `into`, a
         DeviceArray of the file's size, if given), the other bytes uploaded from the "rest" part
-        (-> (DeviceArray, rest_of bytes))."""
+        (-> (DeviceArray, rest_of bytes)); rest: that part already decoded (header_d), if it is."""
         st = self.stream
         tm = _Timer(self.timing, st)
         if not isinstance(parts, dict):
@@ -405,7 +405,7 @@ class BF16v2:
         tm.lap("tables")
         layout, nt = dec.layout, len(dec.layout["t"])
         if device == "full":
-            return self._decompress_full(parts, dec, tm, into)
+            return self._decompress_full(parts, dec, tm, into, rest)
         if nt == 0 and device:
             return dev.DeviceArray(1, np.uint8)
         if nt:
@@ -432,7 +432,7 @@ class BF16v2:
             fill_rest(out, header_d(bytes(parts["rest"])), layout)
         return out
 
-    def _decompress_full(self, parts, dec, tm, into=None):
+    def _decompress_full(self, parts, dec, tm, into=None, rest=None):
         st, layout = self.stream, dec.layout
         if into is not None and into.nbytes != layout["size"]:
             raise ValueError(f"a file of {layout['size']} bytes for a place of {into.nbytes}")
@@ -442,7 +442,8 @@ class BF16v2:
             s_d = _Decoder.upload(parts["stream"], st)
             idxs = list(range(len(t)))
             dec.run(s_d, dec.soff[:-1], d, idxs, [x[0] for x in t], tm)
-        rest = np.frombuffer(header_d(bytes(parts["rest"])), np.uint8)
+        if rest is None:
+            rest = np.frombuffer(header_d(bytes(parts["rest"])), np.uint8)
         staged = dev.pinned(max(1, rest.size))
         staged[:] = rest
         pos = taken = 0

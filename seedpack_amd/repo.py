@@ -54,7 +54,7 @@ import numpy as np
 
 from . import container, device as dev, gguf, header, imatrix as imx_mod, imxfit, qr, r2, residual, zstd
 from ._lib import check, lib
-from .framing import nbytes, pack, pack_parts, unpack
+from .framing import index, nbytes, pack, pack_parts, unpack
 from .gpuquant import GPUQuant
 from .m24 import M24BF16
 from .q8 import Q8Parts
@@ -1152,7 +1152,7 @@ class Unpacker:
         self.files = ThreadPoolExecutor(4)        # a finished file: checked and written
         self.io = ThreadPoolExecutor(8)           # its write, in pieces
         self.hasher = ThreadPoolExecutor(4)       # its checksum, beside the write
-        self.ahead = ThreadPoolExecutor(1)        # the next file's residual decompressed ahead
+        self.ahead = ThreadPoolExecutor(2)        # the next files' residuals decompressed ahead
 
     def run(self, archive, outdir=None, patterns=None):
         t0 = time.perf_counter()
@@ -1230,48 +1230,6 @@ class Unpacker:
             o += v.size
         imx_map = {k: imx_dev.view(4 * imx_off[k], (v.size,), np.float32) for k, v in imx_all.items()}
         self.imx_sets = self._load_imx(r.get(manifest["imx_fit"]["chunk"]), imx_all) if manifest.get("imx_fit") else {}
-        # bases, decoded into HBM; the shards of a split model that a file predicts from one after
-        # another in one allocation (repo3.py:2307-2313)
-        bases, place, jd = {}, {}, {}
-        for k, j in enumerate(joined):
-            if nb + k in need_b:
-                jd[k] = d = dev.DeviceArray(j["size"], np.uint8)
-                ends = [s_ for _, s_ in j["parts"][1:]] + [j["size"]]
-                for (i, s_), e_ in zip(j["parts"], ends):
-                    place[i] = d.view(s_, (e_ - s_,), np.uint8)
-        for i in sorted({i for i in need_b if i < nb} | set(place)):
-            name = manifest["bases"][i]
-            if name in seeds:                               # a seed: its file decoded by parts (seed.py)
-                if i in place:
-                    raise ValueError(f"seed {name} is a shard of a split model")
-                data = SeedCodec(stream=self.stream.handle).decompress(r.get(f"b{i}"))
-                d = dev.DeviceArray.from_host(data, self.stream.handle)
-                bases[i] = _Base(i, name, data, d, gguf.GGUF(data, light=True), seed=True)
-                if name in want:
-                    jobs.append(self.files.submit(check_write, name, data))
-                log(self.verbose, f"  seed {name}: decoded, {time.perf_counter() - t0:.1f} s")
-                continue
-            ch = unpack(memoryview(r.get(f"b{i}")))
-            if "r2" in ch:
-                d, rest = r2.BF16v2(stream=self.stream.handle).decompress(unpack(ch["r2"]), device="full",
-                                                                         into=place.get(i))
-            elif "side" in ch and "stream" in ch:          # an M24 chunk (method m28)
-                d = M24BF16(stream=self.stream.handle).decompress_dev(ch, into=place.get(i))
-                lay = json.loads(zstd.decompress(ch["layout"]))
-                first = min([t[0] for t in lay["t"]] + [lay["size"]])
-                rest = d.view(0, (first,), np.uint8).to_host(stream=self.stream.handle)
-            else:
-                raise ValueError(f"base {name}: a base chunk of an unknown kind")
-            g = gguf.GGUF(rest.tobytes(), light=True)     # the header is the start of the rest part
-            b = _Base(i, name, rest, d, g)
-            bases[i] = b
-            if name in want:
-                host = self.pool.acquire(d.nbytes)[:d.nbytes]
-                check(lib().spa_memcpy_d2h(host.ctypes.data, d.ptr, d.nbytes, self.stream.handle))
-                jobs.append(self.files.submit(check_write, name, host, True))
-            log(self.verbose, f"  base {name}: decoded, {time.perf_counter() - t0:.1f} s")
-        for k, d in jd.items():
-            bases[nb + k] = _Base.joined(nb + k, [(s_, bases[i]) for i, s_ in joined[k]["parts"]], d)
         # quantized files, in archive order; tensors that later files copy are kept on the device
         kept, done = {}, set()
         # largest first, a file after the files it copies tensors from (so the checksum of a big
@@ -1282,32 +1240,110 @@ class Unpacker:
             i = max((i for i in todo if not srcs[i] & todo), key=lambda i: (mf[i]["size"], -i))
             order.append(i)
             todo.remove(i)
+        # bases: seeds decoded first (their headers need the whole file); the other bases' headers,
+        # the residuals' zstd dictionaries, taken from their chunks' "rest" parts on the host, so the
+        # first residuals decompress while the bases decode on the device (repo3.py:2324-2333); the
+        # shards of a split model that a file predicts from one after another in one allocation
+        # (repo3.py:2307-2313)
+        bases, place, jd, zdicts, coded = {}, {}, {}, {}, {}
+        for k, j in enumerate(joined):
+            if nb + k in need_b:
+                jd[k] = d = dev.DeviceArray(j["size"], np.uint8)
+                ends = [s_ for _, s_ in j["parts"][1:]] + [j["size"]]
+                for (i, s_), e_ in zip(j["parts"], ends):
+                    place[i] = d.view(s_, (e_ - s_,), np.uint8)
+        phys = sorted({i for i in need_b if i < nb} | set(place))
+        for i in phys:
+            name = manifest["bases"][i]
+            if name in seeds:                               # a seed: its file decoded by parts (seed.py)
+                if i in place:
+                    raise ValueError(f"seed {name} is a shard of a split model")
+                data = SeedCodec(stream=self.stream.handle).decompress(r.get(f"b{i}"))
+                d = dev.DeviceArray.from_host(data, self.stream.handle)
+                bases[i] = _Base(i, name, data, d, gguf.GGUF(data, light=True), seed=True)
+                zdicts[i] = bases[i].header
+                if name in want:
+                    jobs.append(self.files.submit(check_write, name, data))
+                log(self.verbose, f"  seed {name}: decoded, {time.perf_counter() - t0:.1f} s")
+                continue
+            # only the chunk's framing and its "rest" part are read here (the whole chunk, CRC-checked,
+            # below): the rest part starts with the file's header
+            def read(o, n, c=f"b{i}"):
+                return bytes(r.read_at(c, o, n))
+            parts = index(read, r.chunks[f"b{i}"][1])
+            if "r2" in parts:
+                parts = index(read, parts["r2"][1], parts["r2"][0])
+            elif not ("side" in parts and "stream" in parts):   # else an M24 chunk (method m28)
+                raise ValueError(f"base {name}: a base chunk of an unknown kind")
+            rest = np.frombuffer(header.header_d(read(*parts["rest"])), np.uint8)
+            g = gguf.GGUF(rest.tobytes(), light=True)
+            coded[i] = (rest, g)
+            zdicts[i] = bytes(rest[:g.data_start])
+        for k, j in enumerate(joined):
+            if nb + k in need_b:
+                zdicts[nb + k] = zdicts[j["parts"][0][0]]
 
         def residual_of(i):
             m = mf[i]
-            b = bases.get(m["base"]) if m["base"] is not None else None
             resid = self.pool.acquire(m["size"])[:m["size"]]
             if m.get("codec") == "q8":                      # a base-less file coded by the Q8_0 codec
                 s_ = dev.Stream()
                 Q8Parts(stream=s_.handle).decompress(r.get(f"f{i}"), out=resid)
                 s_.synchronize()
                 return resid
-            return zstd.decompress_into(r.get(f"f{i}"), resid, b.header if b is not None else None)
+            return zstd.decompress_into(r.get(f"f{i}"), resid, zdicts[m["base"]] if m["base"] is not None else None)
 
-        nxt = self.ahead.submit(residual_of, order[0]) if order else None
+        # the first files' residuals (two threads: each frame is one serial zstd stream), as far as
+        # the staging budget holds them beside the host copies of the bases to be written
+        room = self.pool.budget - sum(cat[manifest["bases"][i]]["size"] for i in coded if manifest["bases"][i] in want)
+        ahead = {}
+        for k in range(min(2, len(order))):
+            room -= mf[order[k]]["size"]
+            if room < 0:
+                break
+            ahead[k] = self.ahead.submit(residual_of, order[k])
+        for i in phys:
+            if i not in coded:
+                continue
+            name = manifest["bases"][i]
+            rest, g = coded.pop(i)
+            ch = unpack(memoryview(r.get(f"b{i}")))
+            log(self.verbose, f"  base {name}: chunk read, {time.perf_counter() - t0:.1f} s")
+            if "r2" in ch:
+                ch = {"r2": unpack(ch["r2"])}
+                d, _ = r2.BF16v2(stream=self.stream.handle).decompress(ch["r2"], device="full", into=place.get(i),
+                                                                       rest=rest)
+            else:
+                d = M24BF16(stream=self.stream.handle).decompress_dev(ch, into=place.get(i), rest=rest)
+            b = _Base(i, name, rest, d, g)
+            bases[i] = b
+            if name in want:
+                host = self.pool.acquire(d.nbytes)[:d.nbytes]
+                check(lib().spa_memcpy_d2h(host.ctypes.data, d.ptr, d.nbytes, self.stream.handle))
+                jobs.append(self.files.submit(check_write, name, host, True))
+            log(self.verbose, f"  base {name}: decoded, {time.perf_counter() - t0:.1f} s")
+        for k, d in jd.items():
+            bases[nb + k] = _Base.joined(nb + k, [(s_, bases[i]) for i, s_ in joined[k]["parts"]], d)
+        for k in range(min(2, len(order))):
+            if k not in ahead:
+                ahead[k] = self.ahead.submit(residual_of, order[k])
         for k, i in enumerate(order):
             m = mf[i]
             tf = time.perf_counter()
-            resid = nxt.result()
-            nxt = self.ahead.submit(residual_of, order[k + 1]) if k + 1 < len(order) else None
+            resid = ahead.pop(k).result()
+            tw = time.perf_counter() - tf
+            if k + 2 < len(order):
+                ahead[k + 2] = self.ahead.submit(residual_of, order[k + 2])
+            tm = {}
             if m["plan"]:
-                self._rebuild(r, i, m, bases[m["base"]], resid, kept, users, done, imx_dev, imx_off, imx_map)
+                tm = self._rebuild(r, i, m, bases[m["base"]], resid, kept, users, done, imx_dev, imx_off, imx_map)
             done.add(i)
             if m["name"] in want:
                 jobs.append(self.files.submit(check_write, m["name"], resid, True))
             else:
                 self.pool.release(resid)
-            log(self.verbose, f"  {m['name']}: {m['size']:,} B in {time.perf_counter() - tf:.2f} s")
+            log(self.verbose, f"  {m['name']}: {m['size']:,} B in {time.perf_counter() - tf:.2f} s (residual wait "
+                              f"{tw:.2f} s, {tm})")
         for j in jobs:
             j.result()
         r.close()
@@ -1369,8 +1405,17 @@ class Unpacker:
         """file i's bytes from its residual (in `resid`, rebuilt in place) on the device"""
         st = self.stream.handle
         size = m["size"]
+        tm, t_ = {}, [time.perf_counter()]
+
+        def lap(name):                       # phase times of the verbose log (the stream waited for)
+            if self.verbose:
+                self.stream.synchronize()
+                t1 = time.perf_counter()
+                tm[name] = round(t1 - t_[0], 3)
+                t_[0] = t1
         R = self.rbuf.get(size)
         check(lib().spa_memcpy_h2d(R.ptr, resid.ctypes.data, size, st))
+        lap("upload")
         tens = {t.name: t for t in gguf.GGUF(resid, light=True).tensors}
         plan = m["plan"]
         ttype = {e[0]: (e[3] if len(e) > 3 else tens[e[0]].type) for e in plan}
@@ -1390,6 +1435,7 @@ class Unpacker:
                 t = tensor(name)
                 p = residual.predict(self.gq, t, v, stream=st)
                 check(lib().spa_xor(t.region.ptr, t.region.ptr, p.ptr, t.region.nbytes, None, st))
+        lap("regrow+xor")
         if any(e[1] == "qr" for e in plan):
             ch = unpack(memoryview(r.get(f"q{i}")))
             var = {e[0]: e[2] for e in plan}
@@ -1404,6 +1450,7 @@ class Unpacker:
                     check(lib().spa_memcpy_d2d(t.region.ptr, F.ptr + o, t.region.nbytes, st))
                     o += t.region.nbytes
                 del F, preds
+        lap("qr")
         for e in plan:
             if e[1] in ("ref", "dup"):
                 src = kept[tuple(e[2])]
@@ -1418,6 +1465,8 @@ class Unpacker:
                 check(lib().spa_memcpy_d2d(a.ptr, R.ptr + t.offset, t.nbytes, st))
                 kept[(fi, name)] = a
         check(lib().spa_memcpy_d2h(resid.ctypes.data, R.ptr, size, st))
+        lap("download")
+        return tm
 
 
 def unpack_repo(archive, outdir=None, patterns=None, verbose=False):

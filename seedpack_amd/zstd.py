@@ -85,6 +85,7 @@ def lib():
         _sig(L, "ZSTD_DCtx_setParameter", sz, [vp, ci, ci])
         _sig(L, "ZSTD_DCtx_loadDictionary_advanced", sz, [vp, vp, sz, ci, ci])
         _sig(L, "ZSTD_decompressStream", sz, [vp, ctypes.POINTER(_Buf), ctypes.POINTER(_Buf)])
+        _sig(L, "ZSTD_decompressDCtx", sz, [vp, vp, sz, vp, sz])
         _lib = L
     return _lib
 
@@ -230,6 +231,15 @@ def decompress_into(data, out, dict_data=None):
             d = bytes(dict_data)
             _ok(L.ZSTD_DCtx_loadDictionary_advanced(dctx, d, len(d), DLM_BY_COPY, DCT_RAW_CONTENT), "load dictionary")
         p, n, keep = _addr(data)
+        if out.size and L.ZSTD_getFrameContentSize(p, n) == out.size:
+            # a frame that records its size: decoded in one call straight into `out` (no window
+            # buffer, no copy out of it; the loaded dictionary applies)
+            r = L.ZSTD_decompressDCtx(dctx, out.ctypes.data, out.size, p, n)
+            if L.ZSTD_isError(r):
+                raise ValueError(f"zstd frame: {L.ZSTD_getErrorName(r).decode()}")
+            if r != out.size:
+                raise ValueError(f"zstd frame decodes to {r} bytes, {out.size} expected")
+            return out
         inb = _Buf(p, n, 0)
         step = 1 << 28
         o = 0

@@ -260,3 +260,27 @@ def test_split_models_are_found_only_whole():
     j = repo._Base.joined(5, [(0, s0), (200, s1)])
     assert j.index == 5 and j.header == b"H0" and j.by_name["a"].offset == 64 and j.by_name["b"].offset == 296
     assert s1.by_name["b"].offset == 96
+
+
+def test_framing_index_reads_only_the_framing():
+    """index() finds each part of a packed buffer (nested too) from the framing alone, the same
+    slices unpack() gives; a length past the end is rejected"""
+    from seedpack_amd import framing
+    inner = framing.pack({"meta": b"m" * 5, "stream": b"s" * 1000, "rest": b"RRR"})
+    buf = b"\0" * 7 + framing.pack({"x": b"", "r2": inner})
+    reads = []
+
+    def read(o, n):
+        reads.append(n)
+        return buf[o:o + n]
+    top = framing.index(read, len(buf) - 7, 7)
+    assert top["x"] == (7 + 4 + 2 + 1 + 8, 0)
+    sub = framing.index(read, top["r2"][1], top["r2"][0])
+    for k, v in framing.unpack(inner).items():
+        o, n = sub[k]
+        assert buf[o:o + n] == bytes(v)
+    assert max(reads) <= 8
+    bad = bytearray(framing.pack({"a": b"abc"}))
+    bad[-11] = 99                              # the length of "a"
+    with pytest.raises(ValueError):
+        framing.index(lambda o, n: bytes(bad[o:o + n]), len(bad))
