@@ -72,6 +72,14 @@ __device__ __forceinline__ int nearest_int(float f) {
 // C's roundf: half away from zero.
 __device__ __forceinline__ float round_half_away(float v) { return roundf(v); }
 
+// Workgroups go to the 8 XCDs in turn (workgroup i to XCD i % 8). xcd_block(i, n) renumbers them so
+// that each XCD takes one contiguous range of the n logical blocks: what neighbouring blocks share
+// (a tensor's coding tables) then stays in that XCD's L2. A bijection on [0, n).
+__device__ __forceinline__ unsigned xcd_block(unsigned i, unsigned n) {
+    const unsigned x = i & 7u, k = i >> 3, q = n >> 3, r = n & 7u;
+    return x * q + (x < r ? x : r) + k;
+}
+
 template <typename T> __device__ __forceinline__ T tmin(T a, T b) { return a < b ? a : b; }
 template <typename T> __device__ __forceinline__ T tmax(T a, T b) { return a > b ? a : b; }
 

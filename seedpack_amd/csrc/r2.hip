@@ -428,21 +428,31 @@ __global__ __launch_bounds__(64) void k_enc(const SG* __restrict__ sg, int nseg,
 }
 
 // Decode tables, DT_BYTES per context (a role's 656 contexts side by side, so the decoder needs no
-// remap): for each of the 256 slot buckets of 128 slots, a u64 naming the first and last symbols
-// holding slots of the bucket, with the first one's cumulative frequency and frequency
-// (first | (last - first) << 8 | cum << 16 | freq << 32), then every symbol's (cum | freq << 16)
-// (u32). A slot's symbol is the bucket's first when the slot lies below its cum + freq, else found
-// by binary search over the bucket's other symbols: the same symbol as a full 2^15-entry lookup
-// table, from one 8-byte load for most slots and at most 8 more; 3 KB per table instead of 32 KB.
+// remap): for each of the 256 slot buckets of 128 slots a u64, then every symbol's (cum | freq << 16)
+// (u32). A bucket whose slots belong to at most two symbols s0 <= s1 holds them with the bounds
+// c0 = cum[s0], c1 = end of s0 = cum[s1], c2 = end of s1:
+//   s0 | s1 << 8 | c0 << 16 (15 bits) | c1 << 31 | c2 << 47, bit 63 clear,
+// so one 8-byte load decodes the slot (s1 when slot >= c1, else s0). A bucket with slots of three or
+// more symbols (only symbols of fewer than 128 slots make one) holds the first and last of them with
+// the first one's cum and freq, first | (last - first) << 8 | cum << 16 | freq << 32, bit 63 set; a
+// slot past the first symbol is then found by binary search over the bucket's other symbols. Every
+// slot gets the symbol a full 2^15-entry lookup table gives; 3 KB per table instead of 32 KB.
 // Contexts without a table (never coded) get a one-symbol table, reached only by damaged streams.
 constexpr int DT_BYTES = 3072;
 __device__ __forceinline__ int dec_sym(const uint8_t* dt, uint32_t slot, uint32_t& c0, uint32_t& f) {
     const uint64_t e = reinterpret_cast<const uint64_t*>(dt)[slot >> 7];
+    if (!(e >> 63)) {
+        const uint32_t c1 = (uint32_t)(e >> 31) & 0xFFFFu;
+        const bool up = slot >= c1;
+        c0 = up ? c1 : (uint32_t)(e >> 16) & 0x7FFFu;
+        f = (up ? (uint32_t)(e >> 47) & 0xFFFFu : c1) - c0;
+        return (int)(up ? (e >> 8) & 255u : e & 255u);
+    }
     int s = (int)(e & 255u);
     c0 = (uint32_t)(e >> 16) & 0xFFFFu;
     f = (uint32_t)(e >> 32) & 0xFFFFu;
     const int span = (int)((e >> 8) & 255u);
-    if (c0 + f <= slot && span > 0) {             // (span 0 here: only a table not summing to 2^15)
+    if (c0 + f <= slot) {
         // the last symbol in (first, last] whose cumulative frequency is <= slot
         const uint32_t* ps = reinterpret_cast<const uint32_t*>(dt + 2048);
         int lo = s + 1, hi = s + span;
@@ -472,12 +482,13 @@ __global__ __launch_bounds__(256) void k_dtab(const uint32_t* __restrict__ cum, 
     const uint32_t* c = cum + (size_t)(t < 0 ? 0 : t) * 257;
     uint8_t* o = dt + (size_t)blockIdx.x * DT_BYTES;
     const int i = threadIdx.x;
-    for (int k = i; k < 257; k += 256) cs[k] = t < 0 ? (k ? 32768u : 0u) : (c[k] < 65535u ? c[k] : 65535u);
+    // cum[0] is 0 and cum never falls (clamped to 16 bits), so every slot has a holder below
+    for (int k = i; k < 257; k += 256) cs[k] = t < 0 || k == 0 ? (k ? 32768u : 0u) : (c[k] < 65535u ? c[k] : 65535u);
     __syncthreads();
     const uint32_t fi = cs[i + 1] > cs[i] ? cs[i + 1] - cs[i] : 0u;
     ps[i] = cs[i] | (fi << 16);
     reinterpret_cast<uint32_t*>(o + 2048)[i] = ps[i];
-    // first / last symbol holding a slot of bucket i: the last s <= 255 with cum[s] <= slot
+    // the symbol holding a slot: the last s <= 255 with cum[s] <= slot
     auto holder = [&](uint32_t slot) {
         int lo = 0, hi = 256;
         while (hi - lo > 1) {
@@ -488,9 +499,19 @@ __global__ __launch_bounds__(256) void k_dtab(const uint32_t* __restrict__ cum, 
         return lo;
     };
     const int first = holder((uint32_t)i << 7), last = holder(((uint32_t)i << 7) + 127);
-    const uint32_t u = ps[first];
-    reinterpret_cast<uint64_t*>(o)[i] = (uint64_t)first | ((uint64_t)(last - first) << 8) | ((uint64_t)(u & 0xFFFFu) << 16) |
-                                        ((uint64_t)(u >> 16) << 32);
+    // the second holder: the one of the first slot past the first symbol's (cum[first + 1] lies in
+    // the bucket when last > first)
+    const int second = last > first ? holder(cs[first + 1]) : first;
+    uint64_t e;
+    if (second == last) {
+        e = (uint64_t)first | ((uint64_t)last << 8) | ((uint64_t)(cs[first] & 0x7FFFu) << 16) | ((uint64_t)cs[first + 1] << 31) |
+            ((uint64_t)cs[last + 1] << 47);
+    } else {
+        const uint32_t u = ps[first];
+        e = (uint64_t)first | ((uint64_t)(last - first) << 8) | ((uint64_t)(u & 0xFFFFu) << 16) | ((uint64_t)(u >> 16) << 32) |
+            (1ull << 63);
+    }
+    reinterpret_cast<uint64_t*>(o)[i] = e;
 }
 
 // A lane's reader of its segment's bytes: a 16-byte window in registers refilled from the next
@@ -545,7 +566,7 @@ __global__ __launch_bounds__(256) void k_dec(const uint8_t* __restrict__ in, uin
                                              int nseg, const int16_t* __restrict__ rfi, const int16_t* __restrict__ cfi,
                                              const int8_t* __restrict__ scl, const int32_t* __restrict__ rowmap,
                                              const uint8_t* __restrict__ dtab) {
-    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    const int s = (int)(xcd_block(blockIdx.x, gridDim.x) * blockDim.x + threadIdx.x);
     if (s >= nseg) return;
     const SG g = sg[s];
     const TB T = tb[g.t];

@@ -188,9 +188,17 @@ def test_hip_r2_dec_tables_give_lut_symbols():
     slots = np.arange(1 << 15)
 
     def decode_all(tab):
-        """every slot's (symbol, cum, freq) from the compact table: the bucket's first symbol, or
-        the last of the bucket's other symbols whose cum <= slot"""
-        e = tab[:2048].view(np.uint64).astype(np.int64)[slots >> 7]
+        """every slot's (symbol, cum, freq) from the compact table: a two-symbol bucket's s0 or s1 by
+        the bound c1; in a bucket of more symbols its first symbol, or the last of its other symbols
+        whose cum <= slot"""
+        eu = tab[:2048].view(np.uint64)[slots >> 7]
+        multi = (eu >> np.uint64(63)).astype(bool)
+        e = (eu & np.uint64((1 << 63) - 1)).astype(np.int64)
+        # buckets of at most two symbols
+        s0, s1, b0, b1, b2 = e & 255, (e >> 8) & 255, (e >> 16) & 0x7FFF, (e >> 31) & 0xFFFF, (e >> 47) & 0xFFFF
+        up = slots >= b1
+        two = (np.where(up, s1, s0), np.where(up, b1, b0), np.where(up, b2 - b1, b1 - b0))
+        # the others
         ps = tab[2048:3072].view(np.uint32).astype(np.int64)
         first, span, c0, f = e & 255, (e >> 8) & 255, (e >> 16) & 0xFFFF, (e >> 32) & 0xFFFF
         sym = first.copy()
@@ -198,9 +206,10 @@ def test_hip_r2_dec_tables_give_lut_symbols():
             cand = first + k
             take = (k <= span) & ((ps[np.minimum(cand, 255)] & 0xFFFF) <= slots)
             sym = np.where(take, cand, sym)
-        u = ps[sym]
+        u = ps[np.minimum(sym, 255)]             # (a two-symbol bucket's fields read this way: unused)
         moved = sym != first
-        return sym, np.where(moved, u & 0xFFFF, c0), np.where(moved, u >> 16, f)
+        more = (sym, np.where(moved, u & 0xFFFF, c0), np.where(moved, u >> 16, f))
+        return tuple(np.where(multi, m, t) for m, t in zip(more, two))
 
     sym, c0, f = decode_all(dth[6])                       # no table: one symbol with every slot
     assert not sym.any() and not c0.any() and (f == 1 << 15).all()
