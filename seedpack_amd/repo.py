@@ -463,10 +463,10 @@ class Packer:
         self.reader = ThreadPoolExecutor(1)      # the next file read ahead
         self.coders = ThreadPoolExecutor(coders)
         self.pool = _PinnedPool(staging_bytes)   # page-locked: file reads
-        if device_bytes is None:                 # residuals wait in HBM for their zstd lane
-            free, total = dev.mem_info()
-            device_bytes = max(free - (48 << 30), 8 << 30)
-        self.fpool = _DevPool(device_bytes)
+        # residuals wait in HBM for their zstd lane, within what the bases leave (set once they are
+        # resident unless given)
+        self.auto_budget = device_bytes is None
+        self.fpool = _DevPool(device_bytes if device_bytes is not None else 8 << 30)
         self.tls = threading.local()
         self.cpu, self.cpu_lock = collections.Counter(), threading.Lock()
         self.timing = []
@@ -611,30 +611,29 @@ class Packer:
             mine.append((t, k))
         self.stats["ref"] += len(refs)
         kset = self.file_set.get(fi, 0)
-        if self.fit_wait.get(kset):
-            # the set's importance fitted from this file's tensors, window by window (repo3.py:2041-2044)
-            for w in sorted({wins_of[t.name] for t, _ in mine}):
-                self._fit_from(kset, [t for t, k in mine if k == "rq" and wins_of[t.name] == w], F, b)
-        fitted = self.imx_sets.get(kset, {})
-        rts = [residual.Tensor(t.name, t.type, t.shape[0], F.view(t.offset, (t.nbytes,), np.uint8),
-                               b.view(b.by_name[t.name], st), imatrix=imx_map.get(t.name),
-                               fitted={kset: fitted[t.name]} if t.name in fitted else None,
-                               base_type=b.by_name[t.name].type, numel=t.numel) for t, _ in mine]
-        res = residual.residual_window(rts, self.gq, fitted_set=kset, stream=st) if rts else []
-        tm["regrow"] = time.perf_counter()
-        out = {t.name: r for (t, _), r in zip(mine, res)}
-        for t, _ in mine:
-            ws = wstate[wins_of[t.name]]
-            key = (t.name, t.type, thash[t.name])
-            ws["first"].setdefault(key, fi)
-            ws["memo"][key] = bool(out[t.name]["nonzero"])
-        # plan entries and QR batches, window by window, each window's QR tensors by type in order of
-        # appearance (repo3.py:946-979)
-        plan, qmeta, qjobs, qregs = [], [], [], []
-        by_w = collections.defaultdict(list)
+        kind_of = {t.name: k for t, k in mine}
+        # window by window (repo3.py:2041-2053): the set's importance fitted from this window's
+        # tensors, then the window's residuals, its plan entries and its QR batches (each window's QR
+        # tensors by type in order of appearance, repo3.py:946-979), handed to the coders at once; the
+        # predictions that queued batches hold are bounded (QR_HOLD), the oldest batches waited for
+        plan, qmeta, qjobs, qregs, held = [], [], [], [], collections.deque()
+        by_w, mine_w = collections.defaultdict(list), collections.defaultdict(list)
         for t, _ in pred:
             by_w[wins_of[t.name]].append(t)
+        for t, _ in mine:
+            mine_w[wins_of[t.name]].append(t)
+        out = {}
         for w in sorted(by_w):
+            ts_w = mine_w.get(w, [])
+            if self.fit_wait.get(kset):
+                self._fit_from(kset, [t for t in ts_w if kind_of[t.name] == "rq"], F, b)
+            fitted = self.imx_sets.get(kset, {})
+            rts = [residual.Tensor(t.name, t.type, t.shape[0], F.view(t.offset, (t.nbytes,), np.uint8),
+                                   b.view(b.by_name[t.name], st), imatrix=imx_map.get(t.name),
+                                   fitted={kset: fitted[t.name]} if t.name in fitted else None,
+                                   base_type=b.by_name[t.name].type, numel=t.numel) for t in ts_w]
+            for t, r in zip(ts_w, residual.residual_window(rts, self.gq, fitted_set=kset, stream=st) if rts else []):
+                out[t.name] = r
             qitems = collections.defaultdict(list)
             for t in by_w[w]:
                 if t.name in refs:
@@ -656,6 +655,19 @@ class Packer:
                     qmeta.append([T, [t.name for t in its]])
                     qregs.append([(t.offset, t.nbytes) for t in its])
                     qjobs.append(self.coders.submit(self._qr_job, T, items, b.d, imx_dev if grid else None))
+                    held.append((qjobs[-1], [t.name for t in its], sum(out[t.name]["prediction"].nbytes for t in its)))
+                    del items
+            while held and sum(h[2] for h in held) > self.QR_HOLD:
+                qj, names, _ = held.popleft()
+                qj.result()
+                for n in names:                   # the batch is coded: its predictions go
+                    out[n]["prediction"] = None
+        tm["regrow"] = time.perf_counter()
+        for t, _ in mine:
+            ws = wstate[wins_of[t.name]]
+            key = (t.name, t.type, thash[t.name])
+            ws["first"].setdefault(key, fi)
+            ws["memo"][key] = bool(out[t.name]["nonzero"])
         self.stats["qr"] += sum(len(m[1]) for m in qmeta)
         self.stream.synchronize()
         # the staged bytes go back once the checksum has read them too
@@ -767,6 +779,8 @@ class Packer:
         return self.tls.stream, self.tls.piece, self.tls.count
 
     PIECE = 64 << 20
+    QR_HOLD = 24 << 30                   # predictions held by a file's queued QR batches (bytes)
+    RESERVE = 48 << 30                   # HBM kept beside the bases and the files in flight
 
     def _finish_file(self, state):
         """(a zstd lane, stage 2) the zstd level judged on the device, then the residual streamed out of
@@ -988,6 +1002,9 @@ class Packer:
                 # the files derived from the bases, then the other bases
                 w.put_later("b0", base_jobs[0])
             self.stream.synchronize()
+            if self.auto_budget:
+                free, _ = dev.mem_info()
+                self.fpool.budget = max(free - self.RESERVE, 8 << 30)
             phase("bases resident")
             log(self.verbose, f"  {len(bases)} base(s) resident in HBM, {time.perf_counter() - t0:.1f} s")
             # the pipeline: the next file read ahead, one file at a time on the device, the residual

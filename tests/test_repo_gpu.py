@@ -66,12 +66,17 @@ def test_small_repo_extracts_byte_identical(small_repo, tmp_path):
 
 def test_small_repo_pack_is_deterministic(small_repo, tmp_path):
     """two packs of the same files with the same creation time give the same archive bytes (the
-    pipeline's threads and processing order do not show in the archive)"""
+    pipeline's threads and processing order do not show in the archive), and so does a pack under
+    tight memory: one file's residual in HBM at a time, every QR batch waited for as it is queued"""
     root, arc, sizes, stats = small_repo
-    a, b = str(tmp_path / "a.seedpack"), str(tmp_path / "b.seedpack")
+    a, b, c = (str(tmp_path / f"{k}.seedpack") for k in "abc")
     repo.Packer(zstd_lanes=3, coders=1).pack([root], a, created="2026-01-01T00:00:00")
     repo.Packer().pack([root], b, created="2026-01-01T00:00:00")
     assert open(a, "rb").read() == open(b, "rb").read()
+    tight = repo.Packer(zstd_lanes=2, coders=2, device_bytes=1 << 20)
+    tight.QR_HOLD = 0
+    tight.pack([root], c, created="2026-01-01T00:00:00")
+    assert open(a, "rb").read() == open(c, "rb").read()
 
 
 def test_small_repo_method_m28(small_repo, tmp_path):
