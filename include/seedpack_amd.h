@@ -139,11 +139,11 @@ int spa_qr_encode(int ggml_type, const void* F, const void* P, const void* seed,
 
 /* Decodes every segment (stream bytes of segment s start at in + in_off[s]) into F (the batch's
  * blocks). `in` holds in_bytes of stream: reads past them see zeros (a damaged stream decodes to
- * garbage, never outside its buffer). lut[n][4096] from spa_rans_build_lut. Replaces qr_dec
+ * garbage, never outside its buffer). lut[n][4096] from spa_rans_build_lut32. Replaces qr_dec
  * (qr.py:760-807). */
 int spa_qr_decode(int ggml_type, const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P,
                   const void* seed, const void* tm, const void* sg, int nseg, const int* remap, const uint16_t* freq,
-                  const uint32_t* cum, const uint8_t* lut, void* F, const uint16_t* gk, const float* imx, int mv,
+                  const uint32_t* cum, const uint32_t* lut, void* F, const uint16_t* gk, const float* imx, int mv,
                   void* stream);
 
 /* No counterpart in the reference; for callers that cannot allocate device memory (code under HIP
@@ -187,6 +187,11 @@ int spa_qr_gather(const void* src, uint64_t cap, const uint32_t* len, const uint
 /* lut[t][slot] = the symbol whose cumulative range holds slot, for ntab tables of 4096 slots.
  * Replaces build_lut (qr.py:889-895, gpu2.py:273-279). */
 int spa_rans_build_lut(const uint32_t* cum, int ntab, uint8_t* lut, void* stream);
+
+/* lut[t][slot] = s | (freq[s] - 1) << 8 | (slot - cum[s]) << 20 for the symbol s whose cumulative
+ * range holds slot, ntab tables of 4096 slots: the QR decoders' table (one load per symbol). Replaces
+ * build_lut with the frequency and cumulative lookups of qr_dec folded in (qr.py:760-807, :889-895). */
+int spa_rans_build_lut32(const uint32_t* cum, int ntab, uint32_t* lut, void* stream);
 
 /* ---- difference residual (replaces the host-side chunked numpy stage of repo3.py:456-510) ---- */
 

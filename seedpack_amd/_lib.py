@@ -64,6 +64,7 @@ SIGNATURES = {
     "spa_qr_noalloc_scratch_bytes": (c_size_t, []),
     "spa_qr_gather": (c_int, [c_void_p, ctypes.c_uint64, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
     "spa_rans_build_lut": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
+    "spa_rans_build_lut32": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
     "spa_xor": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_xor3": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_diff_count": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),

@@ -100,8 +100,16 @@ struct Enc {
     const uint32_t* cum;
     const uint32_t* rcp;
     __device__ __forceinline__ void put_fc(uint32_t f, uint32_t c, uint32_t r) {
+        // x < 2^31 before a step and xm >= 2^19, so at most two bytes go out
         const uint32_t xm = ((RANS_L >> PB) << 8) * f;
-        while (x >= xm) { *--ptr = (uint8_t)(x & 0xff); x >>= 8; }
+        if (x >= xm) {
+            *--ptr = (uint8_t)(x & 0xff);
+            x >>= 8;
+            if (x >= xm) {
+                *--ptr = (uint8_t)(x & 0xff);
+                x >>= 8;
+            }
+        }
         const uint32_t sh = f < 2 ? 0u : 31u - __clz(f - 1);
         const uint32_t q = __umulhi(x, r) >> sh;
         x = x + c + (f < 2 ? PSCALE - 1 : 0u) + q * (PSCALE - f);
@@ -224,7 +232,15 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
         }
         nbits[lane][w] = v;
     }
-    auto differs = [&](int i) { return (nbits[lane][i >> 5] >> (i & 31)) & 1u; };
+    // the last differing block at or below i (-1 if none), from the flag words
+    auto differing_at_or_below = [&](int i) {
+        while (i >= 0) {
+            const uint32_t w = nbits[lane][i >> 5] & (0xffffffffu >> (31 - (i & 31)));
+            if (w) return (i & ~31) + 31 - (int)__clz(w);
+            i = (i & ~31) - 1;
+        }
+        return -1;
+    };
     const uint8_t* sbase = seed + m.seed_off;
     uint8_t* const base = out + (uint64_t)s * cap;
     uint8_t* const end = base + cap;
@@ -236,15 +252,21 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
         e.put(tab, sym);
         return !(code && e.ptr - base < FIELD_ROOM<T>);
     };
+    // an equal block's flag is coded in the context of its predecessor (block i - 1 equal: 1,
+    // differing: 0; block 0: 1). A run of equal blocks i .. j + 1 above the differing block j thus
+    // codes i - j - 1 flags in context 1 and then one in context 0 (context 1 when the run reaches
+    // block 0): the run is found from the flag words and coded in one register loop
+    const uint32_t fA = ft.freq_of(1, 1), cA = ft.cum_of(1, 1), rA = ft.rcp_of(1, 1);
+    const uint32_t fB = ft.freq_of(0, 1), cB = ft.cum_of(0, 1), rB = ft.rcp_of(0, 1);
     int i = nb - 1;                              // block g.b0 + i
     for (;;) {
-        bool pend = false;
-        for (; i >= 0; --i) {
-            const int prev = i > 0 ? (differs(i - 1) ? 0 : 1) : 1;
-            if (differs(i)) { pend = true; break; }
-            e.put_fc(ft.freq_of(prev, 1), ft.cum_of(prev, 1), ft.rcp_of(prev, 1));
-            if (e.ptr - base < 8) { out_len[s] = 0xffffffffu; return; }
-        }
+        const int j = differing_at_or_below(i);
+        const int n = i - j;                     // equal blocks in the run (two bytes at most each)
+        if (e.ptr - base < 8 + 2 * (int64_t)n) { out_len[s] = 0xffffffffu; return; }
+        for (int k = j >= 0 ? n - 1 : n; k > 0; --k) e.put_fc(fA, cA, rA);
+        if (j >= 0 && n > 0) e.put_fc(fB, cB, rB);
+        i = j;
+        const bool pend = i >= 0;
         if (__ballot(pend) == 0) break;
         if (!pend) continue;
         const int64_t b = g.b0 + i;
@@ -281,7 +303,7 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
             out_len[s] = 0xffffffffu;
             return;
         }
-        const int prev = i > 0 ? (differs(i - 1) ? 0 : 1) : 1;
+        const int prev = i > 0 ? (((nbits[lane][(i - 1) >> 5] >> ((i - 1) & 31)) & 1u) ? 0 : 1) : 1;
         e.put_fc(ft.freq_of(prev, 0), ft.cum_of(prev, 0), ft.rcp_of(prev, 0));
         --i;
     }
@@ -296,12 +318,14 @@ struct Dec {
     const int* remap;
     const uint16_t* freq;
     const uint32_t* cum;
-    const uint8_t* lut;
+    const uint32_t* lut;
     __device__ __forceinline__ int get(int tab) { return get_tt(remap[tab]); }
     __device__ __forceinline__ int get_tt(int tt) {
+        // one load per symbol: its LUT32 entry holds the symbol, freq - 1 and slot - cum
         const uint32_t slot = x & (PSCALE - 1);
-        const int v = lut[(size_t)tt * PSCALE + slot];
-        x = freq[tt * 256 + v] * (x >> PB) + slot - cum[tt * 257 + v];
+        const uint32_t e = lut[(size_t)tt * PSCALE + slot];
+        const int v = (int)(e & 255u);
+        x = (((e >> 8) & (PSCALE - 1)) + 1) * (x >> PB) + (e >> 20);
         // a valid stream needs at most two bytes here (x >= 2^11 before them); the cap ends the
         // loop on a damaged stream instead of spinning on zero bytes
 #pragma unroll
@@ -322,7 +346,7 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
                                                    const uint8_t* __restrict__ P, const uint8_t* __restrict__ seed,
                                                    const TM* __restrict__ tm, const SG* __restrict__ sg, int nseg,
                                                    const int* __restrict__ remap, const uint16_t* __restrict__ freq,
-                                                   const uint32_t* __restrict__ cum, const uint8_t* __restrict__ lut,
+                                                   const uint32_t* __restrict__ cum, const uint32_t* __restrict__ lut,
                                                    uint8_t* __restrict__ F, int mv) {
     using Y = Ty<T>;
     constexpr int BSP = (Y::BS + 3) & ~3;
@@ -413,6 +437,27 @@ __global__ __launch_bounds__(256) void k_qr_gather(const uint8_t* __restrict__ s
     for (uint32_t i = threadIdx.x; i < len[s]; i += blockDim.x) d[i] = a[i];
 }
 
+// LUT32 entries, slot by slot: the symbol s whose range [cum[s], cum[s + 1]) holds the slot (the last
+// s with cum[s] <= slot), its frequency - 1 (bits 8-19) and slot - cum[s] (bits 20-31); a table not
+// summing to 2^12 gives entries that keep a damaged stream's decoding in bounds
+__global__ __launch_bounds__(256) void k_build_lut32(const uint32_t* __restrict__ cum, int ntab, uint32_t* __restrict__ lut) {
+    __shared__ uint32_t cs[257];
+    const int tb = blockIdx.x;
+    if (tb >= ntab) return;
+    for (int k = threadIdx.x; k < 257; k += blockDim.x) cs[k] = cum[tb * 257 + k];
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < PSCALE; i += blockDim.x) {
+        int lo = 0, hi = 256;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (cs[mid] <= i) lo = mid;
+            else hi = mid;
+        }
+        const uint32_t f = cs[lo + 1] > cs[lo] ? cs[lo + 1] - cs[lo] : 1u;
+        lut[(size_t)tb * PSCALE + i] = (uint32_t)lo | (((f - 1) & (PSCALE - 1)) << 8) | (((i - cs[lo]) & (PSCALE - 1)) << 20);
+    }
+}
+
 __global__ __launch_bounds__(256) void k_build_lut(const uint32_t* __restrict__ cum, int ntab, uint8_t* __restrict__ lut) {
     const int tb = blockIdx.x;
     if (tb >= ntab) return;
@@ -478,7 +523,7 @@ template <int T> struct Encode {
 };
 template <int T> struct Decode {
     static int run(const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
-                   int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F, int mv,
+                   int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint32_t* lut, void* F, int mv,
                    hipStream_t st) {
         if (int e = qr_prefill(F, P, sg, nseg, Ty<T>::BS, st)) return e;
         hipLaunchKernelGGL(k_qr_dec<T>, dim3((unsigned)((nseg + DEC_WG - 1) / DEC_WG)), dim3(DEC_WG), 0, st,
@@ -641,7 +686,7 @@ int grid_encode(int T, const void* F, const void* P, const void* seed, const voi
                 const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap, uint32_t* out_len, const uint16_t* gk,
                 const float* imx, int mv, void* work, hipStream_t st);
 int grid_decode(int T, const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
-                int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F,
+                int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint32_t* lut, void* F,
                 const uint16_t* gk, const float* imx, int mv, hipStream_t st);
 int grid_half_steps(int T, const void* F, int64_t nw, float* h, hipStream_t st);
 
@@ -768,7 +813,7 @@ int spa_qr_encode(int T, const void* F, const void* P, const void* seed, const v
 
 int spa_qr_decode(int T, const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed,
                   const void* tm, const void* sg, int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum,
-                  const uint8_t* lut, void* F, const uint16_t* gk, const float* imx, int mv, void* stream) {
+                  const uint32_t* lut, void* F, const uint16_t* gk, const float* imx, int mv, void* stream) {
     if (int e = check_common(T, nseg, mv, gk)) return e;
     if (nseg == 0) return 0;
     if (grid_type(T))
@@ -781,6 +826,13 @@ int spa_qr_gather(const void* src, uint64_t cap, const uint32_t* len, const uint
     if (nseg <= 0) return 0;
     hipLaunchKernelGGL(k_qr_gather, dim3((unsigned)nseg), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src, cap, len,
                        off, nseg, (uint8_t*)dst);
+    SPA_HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int spa_rans_build_lut32(const uint32_t* cum, int ntab, uint32_t* lut, void* stream) {
+    if (ntab <= 0) return 0;
+    hipLaunchKernelGGL(k_build_lut32, dim3((unsigned)ntab), dim3(256), 0, (hipStream_t)stream, cum, ntab, lut);
     SPA_HIP_TRY(hipGetLastError());
     return 0;
 }

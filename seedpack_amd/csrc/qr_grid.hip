@@ -508,12 +508,14 @@ struct Decoder {
     const int* remap;
     const uint16_t* freq;
     const uint32_t* cum;
-    const uint8_t* lut;
+    const uint32_t* lut;
     __device__ __forceinline__ int get(int tab) {
+        // one load per symbol: its LUT32 entry holds the symbol, freq - 1 and slot - cum
         const int tt = remap[tab];
         const uint32_t slot = x & (PSCALE - 1);
-        const int v = lut[(size_t)tt * PSCALE + slot];
-        x = freq[tt * 256 + v] * (x >> PB) + slot - cum[tt * 257 + v];
+        const uint32_t e = lut[(size_t)tt * PSCALE + slot];
+        const int v = (int)(e & 255u);
+        x = (((e >> 8) & (PSCALE - 1)) + 1) * (x >> PB) + (e >> 20);
         // a valid stream needs at most two bytes here (x >= 2^11 before them); the cap ends the
         // loop on a damaged stream instead of spinning on zero bytes
 #pragma unroll
@@ -528,7 +530,7 @@ __global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, 
                                                 const uint8_t* __restrict__ P, const uint8_t* __restrict__ seed,
                                                 const TM* __restrict__ tm, const SG* __restrict__ sg, int nseg,
                                                 const int* __restrict__ remap, const uint16_t* __restrict__ freq,
-                                                const uint32_t* __restrict__ cum, const uint8_t* __restrict__ lut,
+                                                const uint32_t* __restrict__ cum, const uint32_t* __restrict__ lut,
                                                 uint8_t* __restrict__ F, const uint16_t* __restrict__ gk,
                                                 const float* __restrict__ imx, int mv) {
     using Y = Ty<T>;
@@ -703,7 +705,7 @@ template <int T> struct GEnc {
 };
 template <int T> struct GDec {
     static int run(const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed, const void* tm, const void* sg,
-                   int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint8_t* lut, void* F,
+                   int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum, const uint32_t* lut, void* F,
                    const uint16_t* gk, const float* imx, int mv, hipStream_t st) {
         if (int e = qr_prefill(F, P, sg, nseg, Ty<T>::BS, st)) return e;
         hipLaunchKernelGGL(k_qrg_dec<T>, dim3((unsigned)nseg), dim3(64), 0, st, (const uint8_t*)in, in_bytes, in_off, (const uint8_t*)P,
@@ -750,7 +752,7 @@ int grid_encode(int T, const void* F, const void* P, const void* seed, const voi
 }
 int grid_decode(int T, const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* P, const void* seed,
                 const void* tm, const void* sg, int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum,
-                const uint8_t* lut, void* F, const uint16_t* gk, const float* imx, int mv, hipStream_t st) {
+                const uint32_t* lut, void* F, const uint16_t* gk, const float* imx, int mv, hipStream_t st) {
     return dispatch_grid<GDec>(T, in, in_bytes, in_off, P, seed, tm, sg, nseg, remap, freq, cum, lut, F, gk, imx, mv, st);
 }
 

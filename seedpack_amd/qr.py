@@ -313,8 +313,8 @@ def decode_parts(T, freq, used, lens, stream_bytes, items, seed_dev, imx_dev=Non
     remap = np.full(NTAB2, -1, np.int32)
     remap[np.asarray(used, np.int64)] = np.arange(len(used), dtype=np.int32)
     freq_d, cum_d, remap_d = (dev.DeviceArray.from_host(a, stream) for a in (freq, cum, remap))
-    lut = dev.DeviceArray((max(1, len(freq)), 1 << PB), np.uint8)
-    check(lib().spa_rans_build_lut(cum_d.ptr, len(freq), lut.ptr, stream))
+    lut = dev.DeviceArray((max(1, len(freq)), 1 << PB), np.uint32)
+    check(lib().spa_rans_build_lut32(cum_d.ptr, len(freq), lut.ptr, stream))
     lens = np.asarray(lens, np.uint64)
     s = np.frombuffer(bytes(stream_bytes), np.uint8)
     if len(lens) != nseg or int(lens.sum()) > len(s):

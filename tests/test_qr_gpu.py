@@ -130,3 +130,32 @@ def test_hip_qr_grid_cfg3_rows(T):
     buf = qr.encode(T, [(F2, P, 0, 30, w.shape[1], 0)], sd, dimx)
     back = qr.decode(T, buf, [(P, 0, 30, w.shape[1], 0)], sd, dimx).to_host()[:len(F2)]
     assert back.tobytes() == F2.tobytes()
+
+
+def test_hip_lut32_folds_freq_and_cum_into_the_symbol_table():
+    """the QR decoders' LUT32 entry of every slot names the symbol of the byte LUT, that symbol's
+    frequency - 1 and the slot's offset in its range, on tables with zero-frequency symbols, one
+    symbol holding every slot and runs of frequency-1 symbols"""
+    from seedpack_amd._lib import check, lib
+    g = np.random.Generator(np.random.PCG64(5))
+    freq = np.zeros((5, 256), np.int64)
+    freq[0, 3] = 4096
+    freq[1, :100] = 1; freq[1, 200] = 4096 - 100
+    freq[2, ::2] = 32
+    freq[3] = 16
+    p = g.dirichlet(np.full(256, 0.1)); f = np.floor(p * (4096 - 256)).astype(np.int64) + 1
+    f[np.argmax(f)] += 4096 - f.sum(); freq[4] = f
+    assert (freq.sum(1) == 4096).all()
+    cum = np.zeros((5, 257), np.uint32)
+    cum[:, 1:] = np.cumsum(freq, 1)
+    cum_d = dev.DeviceArray.from_host(cum)
+    l8, l32 = dev.DeviceArray((5, 4096), np.uint8), dev.DeviceArray((5, 4096), np.uint32)
+    check(lib().spa_rans_build_lut(cum_d.ptr, 5, l8.ptr, None))
+    check(lib().spa_rans_build_lut32(cum_d.ptr, 5, l32.ptr, None))
+    a, e = l8.to_host().astype(np.int64), l32.to_host().astype(np.int64)
+    slots = np.arange(4096)
+    for t in range(5):
+        sym = e[t] & 255
+        assert np.array_equal(sym, a[t]), t
+        assert np.array_equal(((e[t] >> 8) & 4095) + 1, freq[t][sym]), t
+        assert np.array_equal(e[t] >> 20, slots - cum[t][sym]), t
