@@ -313,8 +313,7 @@ __global__ __launch_bounds__(64) void k_qr_enc(const uint8_t* __restrict__ F, co
 
 struct Dec {
     uint32_t x;
-    const uint8_t* ptr;
-    const uint8_t* end;
+    ByteQ bq;
     const int* remap;
     const uint16_t* freq;
     const uint32_t* cum;
@@ -329,7 +328,7 @@ struct Dec {
         // a valid stream needs at most two bytes here (x >= 2^11 before them); the cap ends the
         // loop on a damaged stream instead of spinning on zero bytes
 #pragma unroll
-        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | next_byte(ptr, end);
+        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | bq.next();
         return v;
     }
 };
@@ -360,15 +359,16 @@ __global__ __launch_bounds__(DEC_WG) void k_qr_dec(const uint8_t* __restrict__ i
     const TM m = tm[g.t];
     const uint8_t* sbase = seed + m.seed_off;
     const uint8_t* const in_end = in + in_bytes;
-    Dec d{0, in + (in_off[s] < in_bytes ? in_off[s] : in_bytes), in_end, remap, freq, cum, lut};
-    for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | next_byte(d.ptr, in_end);
+    Dec d{0, {}, remap, freq, cum, lut};
+    d.bq.start(in + (in_off[s] < in_bytes ? in_off[s] : in_bytes), in_end);
+    for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | d.bq.next();
     int prev = 1;
     int64_t b = g.b0;
     const int64_t bend = g.b0 + g.nb;
     for (;;) {
         bool pend = false;
         for (; b < bend; ++b) {
-            prev = ft.get(d.x, d.ptr, in_end, prev);
+            prev = ft.get(d.x, d.bq, prev);
             if (!prev) { pend = true; break; }     // F holds P's bytes for the equal blocks (qr_prefill)
         }
         if (__ballot(pend) == 0) break;

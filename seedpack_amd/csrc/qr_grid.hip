@@ -503,8 +503,7 @@ __global__ __launch_bounds__(64) void k_qrg_enc(const uint8_t* __restrict__ F, c
 
 struct Decoder {
     uint32_t x;
-    const uint8_t* ptr;
-    const uint8_t* end;
+    ByteQ bq;
     const int* remap;
     const uint16_t* freq;
     const uint32_t* cum;
@@ -519,7 +518,7 @@ struct Decoder {
         // a valid stream needs at most two bytes here (x >= 2^11 before them); the cap ends the
         // loop on a damaged stream instead of spinning on zero bytes
 #pragma unroll
-        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | next_byte(ptr, end);
+        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | bq.next();
         return v;
     }
 };
@@ -551,15 +550,16 @@ __global__ __launch_bounds__(64) void k_qrg_dec(const uint8_t* __restrict__ in, 
     uint32_t keys[Gt::PER];
     load_keys<T>(gk, lane, keys);
     const uint8_t* const in_end = in + in_bytes;
-    Decoder d{0, in + (in_off[s] < in_bytes ? in_off[s] : in_bytes), in_end, remap, freq, cum, lut};
-    for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | next_byte(d.ptr, in_end);
+    Decoder d{0, {}, remap, freq, cum, lut};
+    d.bq.start(in + (in_off[s] < in_bytes ? in_off[s] : in_bytes), in_end);
+    for (int i = 0; i < 4; ++i) d.x = (d.x << 8) | d.bq.next();
     FlagTab ft;
     ft.load(remap, freq, cum);
     int prev = 1;
     for (int64_t b = g.b0; b < g.b0 + g.nb; ++b) {
         const uint8_t* pb = P + b * Y::BS;
         uint8_t* dst = F + b * Y::BS;
-        const int eq = ft.get(d.x, d.ptr, in_end, prev);
+        const int eq = ft.get(d.x, d.bq, prev);
         prev = eq;
         if (eq) continue;                         // F holds P's bytes already (qr_prefill)
         // every lane applies the same writes to the block in LDS, so each lane's reads see them

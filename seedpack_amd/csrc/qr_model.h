@@ -36,6 +36,31 @@ __device__ __forceinline__ uint32_t next_byte(const uint8_t*& ptr, const uint8_t
     return b;
 }
 
+// The decoders' byte source: the next four stream bytes held in registers, each refilled by a load
+// issued as a byte leaves, so a renormalisation waits only on loads issued four bytes earlier (the
+// same bytes as next_byte, in order; zeros past `end`, nothing read past it).
+struct ByteQ {
+    const uint8_t* ptr;                          // the next byte to load
+    const uint8_t* end;
+    uint32_t b0, b1, b2, b3;
+    __device__ __forceinline__ void start(const uint8_t* p, const uint8_t* e) {
+        ptr = p;
+        end = e;
+        b0 = next_byte(ptr, end);
+        b1 = next_byte(ptr, end);
+        b2 = next_byte(ptr, end);
+        b3 = next_byte(ptr, end);
+    }
+    __device__ __forceinline__ uint32_t next() {
+        const uint32_t v = b0;
+        b0 = b1;
+        b1 = b2;
+        b2 = b3;
+        b3 = next_byte(ptr, end);
+        return v;
+    }
+};
+
 // Frequencies of the flag symbols 0 and 1 in the two flag contexts p (previous block differing /
 // equal): every block codes a flag, most blocks nothing else. A context's symbol 0 starts at 0 and
 // symbol 1 at freq(p, 0) (the tables' cumulative counts), so four 16-bit frequencies say everything;
@@ -69,14 +94,14 @@ struct FlagTab {
     __device__ __forceinline__ uint32_t rcp_of(int p, int v) const { return (uint32_t)((p ? r1 : r0) >> (32 * v)); }
     // one flag decoded from state x in context p: symbol 1's slots start at freq(p, 0), symbol 0's at 0
     // (a valid stream's slot is in one of the two ranges); renormalised from ptr as the general step
-    __device__ __forceinline__ int get(uint32_t& x, const uint8_t*& ptr, const uint8_t* end, int p) const {
+    __device__ __forceinline__ int get(uint32_t& x, ByteQ& bq, int p) const {
         const uint32_t slot = x & (PSCALE - 1);
         const uint32_t w = (uint32_t)(q >> (32 * p));
         const uint32_t f0 = w & 0xffffu;
         const int v = slot >= f0 ? 1 : 0;
         x = (w >> (16 * v) & 0xffffu) * (x >> PB) + slot - (v ? f0 : 0u);
 #pragma unroll
-        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | next_byte(ptr, end);
+        for (int i = 0; i < 4 && x < RANS_L; ++i) x = (x << 8) | bq.next();
         return v;
     }
 };
