@@ -206,11 +206,15 @@ class BF16v2:
     tensor and the stream is the segments in tensor order), so here the whole coded region is
     resident in HBM at once and each kernel runs over every segment of the file in one launch
     (encode in batches of `enc_batch` segments, for its 12-byte-per-weight symbol workspace).
-    `group_bytes` is kept for the reference's interface."""
+    `group_bytes` is kept for the reference's interface. A file in host memory whose coded region is
+    larger than `stream_bytes` (a base bigger than HBM can hold beside its derived files) is coded
+    in groups of tensors of about that size instead, read twice (compress_grouped): the same parts."""
 
-    def __init__(self, group_bytes=400 << 20, dedup=True, stream=None, enc_batch=262144, timing=False):
+    def __init__(self, group_bytes=400 << 20, dedup=True, stream=None, enc_batch=262144, timing=False,
+                 stream_bytes=None):
         self.group_bytes, self.dedup, self.stream = group_bytes, dedup, stream
         self.enc_batch, self.timing, self.last_timing = enc_batch, timing, {}
+        self.stream_bytes = stream_bytes
 
     def stats(self, w_dev, rl, with_hash=True):
         """(rfi, cfi, scl, row hashes or None) of one tensor's BF16 bits on the device, as numpy"""
@@ -271,6 +275,9 @@ class BF16v2:
         nrows_c, dup_pairs, rmap_all, rmap_off, nrm = {}, {}, [], {}, 0
         if isinstance(data, dev.DeviceArray):           # the file already resident (compress_dev)
             d, a, host = data, 0, None
+        elif self.stream_bytes is not None and nt and \
+                max(off + nb for off, nb, _, _ in layout["t"]) - layout["t"][0][0] > self.stream_bytes:
+            return self.compress_grouped(np.frombuffer(data, np.uint8), layout)
         else:
             host = np.frombuffer(data, np.uint8)
             a = layout["t"][0][0] if nt else 0
@@ -365,6 +372,129 @@ class BF16v2:
         pool.shutdown()
         tm.lap("zstd")
         self.last_timing = tm.result()
+        return {**small, "stream": stream,
+                "arrays": dict(rfi=rfi, cfi=cfi, scl=scl, counts=counts_h, freq=freq, used=used, lens=lens,
+                               nrows_c=np.array(meta["nrows_c"], np.int64),
+                               dups=np.array(dups, np.int64).reshape(-1, 3), rowmap=rowmap)}
+
+    def compress_grouped(self, host, layout):
+        """compress() of a file in host memory with at most about `stream_bytes` of it in HBM at a
+        time: the tensors in groups (a group ends before the tensor that would take it past
+        stream_bytes; a bigger tensor is a group of its own), each group uploaded twice. First pass:
+        the group's statistics and duplicate rows, its segment plan (device offsets from the group's
+        first tensor; the rows kept index the file-wide row map) and histogram; second pass, once
+        the tables are normalised: its segments coded and gathered. The counts are sums, every
+        segment is coded alone and the stream is the segments in tensor order, so the parts are
+        those of compress() (the reference reads a big base twice as well, bf16v2.py:293-321)."""
+        st = self.stream
+        tm = _Timer(self.timing, st)
+        rb, cb, nrow, ncol = bases(layout)
+        t = layout["t"]
+        nt = len(t)
+        groups, cur, size = [], [], 0
+        for i, (off, nb, _, _) in enumerate(t):
+            if cur and size + nb > self.stream_bytes:
+                groups.append(cur)
+                cur, size = [], 0
+            cur.append(i)
+            size += nb
+        if cur:
+            groups.append(cur)
+        span = lambda g: (t[g[0]][0], t[g[-1]][0] + t[g[-1]][1])
+        gbuf = dev.DeviceArray(max(max(b_ - a_ for a_, b_ in map(span, groups)), 1), np.uint8)
+        rfi_d, cfi_d = dev.DeviceArray(max(nrow, 1), np.int16), dev.DeviceArray(max(ncol, 1), np.int16)
+        scl_d = dev.DeviceArray(max(ncol, 1), np.int8)
+        h_d = dev.DeviceArray(max(nrow, 1), np.uint64) if self.dedup else None
+        rm_d = dev.DeviceArray(max(nrow, 1), np.int32)
+        wb = max(lib().spa_r2_stats_work_bytes(nb // 2 // rl, rl) for _, nb, rl, _ in t)
+        work = dev.DeviceArray(wb, np.uint8)
+        counts = dev.DeviceArray((layout["nroles"] * TPT, 256), np.uint32).zero(st)
+        nrows_c, dup_pairs, rmap_off, nrm, plans = {}, {}, {}, 0, []
+        rfi = np.zeros(nrow, np.int16); cfi = np.zeros(ncol, np.int16); scl = np.zeros(ncol, np.int8)
+        for g in groups:
+            ga, gb_ = span(g)
+            check(lib().spa_memcpy_h2d(gbuf.ptr, host[ga:gb_].ctypes.data, gb_ - ga, st))
+            tm.lap("upload")
+            for i in g:
+                off, nb, rl, _ = t[i]
+                check(lib().spa_r2_stats(gbuf.ptr + off - ga, nb // 2 // rl, rl, rfi_d.ptr + 2 * rb[i], cfi_d.ptr + 2 * cb[i],
+                                         scl_d.ptr + cb[i], None if h_d is None else h_d.ptr + 8 * rb[i], work.ptr, wb,
+                                         None, st))
+            r0, r1 = rb[g[0]], rb[g[-1]] + t[g[-1]][1] // 2 // t[g[-1]][2]
+            c0, c1 = cb[g[0]], cb[g[-1]] + t[g[-1]][2]
+            rfi[r0:r1] = rfi_d.view(2 * r0, (r1 - r0,), np.int16).to_host(stream=st)
+            cfi[c0:c1] = cfi_d.view(2 * c0, (c1 - c0,), np.int16).to_host(stream=st)
+            scl[c0:c1] = scl_d.view(c0, (c1 - c0,), np.int8).to_host(stream=st)
+            hh = h_d.view(8 * r0, (r1 - r0,), np.uint64).to_host(stream=st) if h_d is not None else None
+            tm.lap("stats")
+            for i in g:
+                off, nb, rl, _ = t[i]
+                nr = nb // 2 // rl
+                rows = lambda ids, off=off, rl=rl: [host[off + 2 * rl * int(r):off + 2 * rl * (int(r) + 1)].view(np.uint16)
+                                                    for r in ids]
+                keep, pairs = _dups(hh[rb[i] - r0:rb[i] - r0 + nr], rows, rl) if self.dedup else (None, [])
+                nrows_c[i] = nr if keep is None else len(keep)
+                if keep is not None:
+                    check(lib().spa_memcpy_h2d(rm_d.ptr + 4 * nrm, keep.ctypes.data, 4 * len(keep), st))
+                    rmap_off[i] = nrm
+                    nrm += len(keep)
+                    dup_pairs[i] = pairs
+            tm.lap("dups")
+            tb, sg = plan(layout, g, nrows_c, rmap_off, rfi, cfi)
+            tb_d = dev.DeviceArray.from_host(tb.view(np.uint8), st)
+            sg_d = dev.DeviceArray.from_host(sg.view(np.uint8) if len(sg) else np.zeros(16, np.uint8), st)
+            check(lib().spa_r2_hist(gbuf.ptr, tb_d.ptr, sg_d.ptr, len(sg), rfi_d.ptr, cfi_d.ptr, scl_d.ptr, rm_d.ptr,
+                                    counts.ptr, st))
+            plans.append((ga, gb_, tb_d, sg_d, len(sg)))
+            tm.lap("hist")
+        dups = [[i, r, s_] for i in sorted(dup_pairs) for r, s_ in dup_pairs[i]]
+        meta = dict(layout=layout, dups=dups, nrows_c=[nrows_c[i] for i in range(nt)])
+        pool = ThreadPoolExecutor(2)
+        meta_job = pool.submit(zstd.compress, json.dumps(meta).encode(), 19)
+        side_job = pool.submit(zstd.compress, rfi.tobytes() + cfi.tobytes() + scl.tobytes(), 19)
+        counts_h = counts.to_host(stream=st)
+        freq, used = normalize(counts_h)
+        tm.lap("normalize")
+        remap = np.full(counts_h.shape[0], -1, np.int32)
+        remap[used] = np.arange(len(used), dtype=np.int32)
+        remap_d, freq_d, cum_d = (dev.DeviceArray.from_host(x if len(x) else np.zeros((1,) + x.shape[1:], x.dtype), st)
+                                  for x in (remap, freq, cum_of(freq)))
+        fcw = dev.DeviceArray((max(1, len(remap)), 256), np.uint32)
+        check(lib().spa_r2_encode_tables(remap_d.ptr, len(remap), freq_d.ptr, cum_d.ptr, fcw.ptr, st))
+        streams, lens_all = [], []
+        nbat = max(1, min(max(n for *_, n in plans), self.enc_batch))
+        fc = dev.DeviceArray(-(-nbat // 64) * 64 * SEG * 3, np.uint32)
+        out = dev.DeviceArray(nbat * CAP, np.uint8)
+        out_len = dev.DeviceArray(nbat, np.uint32)
+        for ga, gb_, tb_d, sg_d, nseg in plans:
+            check(lib().spa_memcpy_h2d(gbuf.ptr, host[ga:gb_].ctypes.data, gb_ - ga, st))
+            tm.lap("upload")
+            for s0 in range(0, nseg, nbat):
+                n = min(nbat, nseg - s0)
+                check(lib().spa_r2_encode(gbuf.ptr, tb_d.ptr, sg_d.ptr + 16 * s0, n, rfi_d.ptr, cfi_d.ptr, scl_d.ptr,
+                                          rm_d.ptr, fcw.ptr, fc.ptr, out.ptr, CAP, out_len.ptr, st))
+                lens = out_len.to_host(stream=st)[:n]
+                if (lens == 0xFFFFFFFF).any():
+                    raise RuntimeError("R2: rANS segment overflow")
+                offs = np.zeros(n + 1, np.uint64)
+                offs[1:] = np.cumsum(lens.astype(np.uint64))
+                dst = dev.DeviceArray(max(1, int(offs[-1])), np.uint8)
+                offs_d = dev.DeviceArray.from_host(offs, st)
+                check(lib().spa_qr_gather(out.ptr, CAP, out_len.ptr, offs_d.ptr, n, dst.ptr, st))
+                piece = dev.pinned(int(offs[-1]))
+                if len(piece):
+                    check(lib().spa_memcpy_d2h(piece.ctypes.data, dst.ptr, len(piece), st))
+                streams.append(piece)
+                lens_all.append(lens)
+            tm.lap("encode")
+        lens = np.concatenate(lens_all).astype(np.uint32) if lens_all else np.zeros(0, np.uint32)
+        stream = streams[0] if len(streams) == 1 else (streams or np.zeros(0, np.uint8))
+        small = {"meta": meta_job.result(), "side": side_job.result(), "tables": store_tables(freq, used),
+                 "lens": zstd.compress(lens.tobytes(), 19)}
+        pool.shutdown()
+        tm.lap("zstd")
+        self.last_timing = tm.result()
+        rowmap = rm_d.view(0, (nrm,), np.int32).to_host(stream=st) if nrm else np.zeros(1, np.int32)
         return {**small, "stream": stream,
                 "arrays": dict(rfi=rfi, cfi=cfi, scl=scl, counts=counts_h, freq=freq, used=used, lens=lens,
                                nrows_c=np.array(meta["nrows_c"], np.int64),

@@ -250,3 +250,25 @@ def test_hip_r2_packed_chunk_and_random_access():
     pieces = []
     rt.write_to(lambda b: pieces.append(bytes(b)), window=40 << 10)
     assert b"".join(pieces) == data
+
+
+@pytest.mark.parametrize("name", [c[0] for c in CASES])
+def test_hip_r2_grouped_equals_one_pass(name):
+    """a file in host memory coded in groups of tensors (the path of a base bigger than HBM: a third
+    of the coded bytes on the device at a time, each group read twice) gives the parts of the
+    one-pass coding, and they decode back"""
+    say("case r2 grouped", name)
+    data, layout, gb = case_file(name)
+    whole = r2.BF16v2(group_bytes=gb).compress(data, layout)
+    span = max(off + nb for off, nb, _, _ in layout["t"]) - layout["t"][0][0]
+    codec = r2.BF16v2(group_bytes=gb, stream_bytes=max(1, span // 3))
+    parts = codec.compress(data, layout)
+    for k in ("meta", "side", "tables", "lens"):
+        assert bytes(parts[k]) == bytes(whole[k]), k
+    got = b"".join(bytes(p) for p in parts["stream"]) if isinstance(parts["stream"], list) else bytes(parts["stream"])
+    want = b"".join(bytes(p) for p in whole["stream"]) if isinstance(whole["stream"], list) else bytes(whole["stream"])
+    assert got == want
+    out = codec.decompress(whole)
+    host = np.frombuffer(data, np.uint8)
+    for off, nb, _, _ in layout["t"]:
+        assert out[off:off + nb].tobytes() == host[off:off + nb].tobytes()
