@@ -369,16 +369,54 @@ def process_order(files, groups):
     return out
 
 
+class _Window:
+    """the base tensors one window of a derived file reads, on the device: d holds them packed,
+    by_name gives each at its offset in d"""
+
+    def __init__(self, d, by_name):
+        self.d, self.by_name = d, by_name
+
+    def view(self, t, stream=None):
+        dt = np.uint16 if t.type == BF16 else np.float16 if t.type == F16 else np.float32
+        return self.d.view(t.offset, (t.numel,), dt)
+
+
 class _Base:
-    """a base model resident in HBM: the whole file (header included) at its file offsets. A seed's
-    quantized tensors are dequantized (llama.cpp's dequantize_row_*) when first used and kept, the
-    least recently used dropped beyond DQ_CACHE bytes"""
+    """a base model resident in HBM: the whole file (header included) at its file offsets; or, for
+    a base bigger than HBM holds beside its derived files, in host memory (`src`, d None), its
+    tensors uploaded window by window (window()). A seed's quantized tensors are dequantized
+    (llama.cpp's dequantize_row_*) when first used and kept, the least recently used dropped beyond
+    DQ_CACHE bytes"""
 
     def __init__(self, index, name, host, d, g, seed=False):
         self.index, self.name, self.d, self.g, self.seed = index, name, d, g, seed
         self.header = bytes(host[:g.data_start])
         self.by_name = {t.name: t for t in g.tensors}
         self.dq, self.dq_bytes = collections.OrderedDict(), 0
+        self.src, self.parts = host, None
+
+    def host_bytes(self, off, n):
+        """n bytes of the base file (a split model: of its shards one after another) from host memory"""
+        if self.parts is None:
+            return self.src[off:off + n]
+        start, sb = [p for p in self.parts if p[0] <= off][-1]
+        return sb.src[off - start:off - start + n]
+
+    def window(self, names, stream):
+        """the base itself when resident, else a _Window of the tensors `names` uploaded from host
+        memory, each at a 256-byte boundary"""
+        if self.d is not None:
+            return self
+        ts = [self.by_name[n] for n in dict.fromkeys(names) if n in self.by_name]
+        offs, o = [], 0
+        for t in ts:
+            offs.append(o)
+            o += -(-t.nbytes // 256) * 256
+        d = dev.DeviceArray(max(o, 1), np.uint8)
+        for t, at in zip(ts, offs):
+            src = np.ascontiguousarray(self.host_bytes(t.offset, t.nbytes))
+            check(lib().spa_memcpy_h2d(d.ptr + at, src.ctypes.data, t.nbytes, stream))
+        return _Window(d, {t.name: dataclasses.replace(t, offset=at) for t, at in zip(ts, offs)})
 
     @classmethod
     def joined(cls, index, parts, d=None):
@@ -392,6 +430,7 @@ class _Base:
         b.by_name = {n: dataclasses.replace(t, offset=t.offset + start)
                      for start, sb in parts for n, t in sb.by_name.items()}
         b.dq, b.dq_bytes = collections.OrderedDict(), 0
+        b.src, b.parts = None, list(parts)
         return b
 
     def view(self, t, stream=None):
@@ -450,8 +489,11 @@ class Packer:
     files"""
 
     def __init__(self, level=7, verbose=False, coders=8, zstd_lanes=14, staging_bytes=24 << 30, device_bytes=None,
-                 method="m29", m30_slice=None):
+                 method="m29", m30_slice=None, bases_in_hbm=None):
         self.m30_slice = m30_slice
+        # the BF16 bases in HBM (True), read window by window from host memory (False), or in HBM
+        # when they fit beside the largest derived file and RESERVE (None)
+        self.bases_in_hbm = bases_in_hbm
         if method not in METHODS:
             raise NotImplementedError(f"archive method {method!r} (built: {', '.join(METHODS)})")
         self.level, self.verbose, self.method = level, verbose, method
@@ -523,6 +565,8 @@ class Packer:
             s.synchronize()
             return c
         if self.method == "m28":
+            if b.d is None:
+                raise NotImplementedError("archive method m28 codes its base in HBM: a base bigger than HBM needs m29")
             parts = M24BF16(stream=s.handle).compress_dev(host, d=b.d, g=g)
             s.synchronize()
             return pack_parts(parts)
@@ -530,8 +574,10 @@ class Packer:
                             if t.type == BF16 and len(t.shape) == 2], len(host))
         with ThreadPoolExecutor(1) as hp:
             rest = hp.submit(header.header_c, host, g, lay)
-            codec = r2.BF16v2(stream=s.handle)
-            inner = codec.compress_parts(b.d, lay, rest=rest.result(), order=order) if lay["t"] else \
+            # a base in host memory is coded in groups of BASE_GROUP bytes (read twice)
+            codec = r2.BF16v2(stream=s.handle, stream_bytes=self.BASE_GROUP)
+            inner = codec.compress_parts(b.d if b.d is not None else host, lay, rest=rest.result(), order=order) \
+                if lay["t"] else \
                 pack_parts({"meta": zstd.compress(json.dumps({"layout": lay, "dups": [], "nrows_c": []}).encode(), 19),
                             "side": zstd.compress(b"", 19), "tables": r2.store_tables(np.zeros((0, 256), np.uint16), []),
                             "lens": zstd.compress(b"", 19), "stream": b"", "rest": rest.result()})
@@ -625,13 +671,14 @@ class Packer:
         out = {}
         for w in sorted(by_w):
             ts_w = mine_w.get(w, [])
+            bw = b.window([t.name for t in ts_w], st)     # (the base itself when it is in HBM)
             if self.fit_wait.get(kset):
-                self._fit_from(kset, [t for t in ts_w if kind_of[t.name] == "rq"], F, b)
+                self._fit_from(kset, [t for t in ts_w if kind_of[t.name] == "rq"], F, bw)
             fitted = self.imx_sets.get(kset, {})
             rts = [residual.Tensor(t.name, t.type, t.shape[0], F.view(t.offset, (t.nbytes,), np.uint8),
-                                   b.view(b.by_name[t.name], st), imatrix=imx_map.get(t.name),
+                                   bw.view(bw.by_name[t.name], st), imatrix=imx_map.get(t.name),
                                    fitted={kset: fitted[t.name]} if t.name in fitted else None,
-                                   base_type=b.by_name[t.name].type, numel=t.numel) for t in ts_w]
+                                   base_type=bw.by_name[t.name].type, numel=t.numel) for t in ts_w]
             for t, r in zip(ts_w, residual.residual_window(rts, self.gq, fitted_set=kset, stream=st) if rts else []):
                 out[t.name] = r
             qitems = collections.defaultdict(list)
@@ -648,13 +695,13 @@ class Packer:
                 for batch in qr.batches(T, [t.nbytes for t in ts]):
                     its = [ts[i] for i in batch]
                     grid = T in qr.GRID_TYPES
-                    items = [(F.view(t.offset, (t.nbytes,), np.uint8), out[t.name]["prediction"], b.by_name[t.name].offset,
-                              b.by_name[t.name].type, b.by_name[t.name].shape[0], imx_off.get(t.name, -1) if grid else -1)
+                    items = [(F.view(t.offset, (t.nbytes,), np.uint8), out[t.name]["prediction"], bw.by_name[t.name].offset,
+                              bw.by_name[t.name].type, bw.by_name[t.name].shape[0], imx_off.get(t.name, -1) if grid else -1)
                              for t in its]
                     self.stats["qr_grid"] += len(its) if grid else 0
                     qmeta.append([T, [t.name for t in its]])
                     qregs.append([(t.offset, t.nbytes) for t in its])
-                    qjobs.append(self.coders.submit(self._qr_job, T, items, b.d, imx_dev if grid else None))
+                    qjobs.append(self.coders.submit(self._qr_job, T, items, bw.d, imx_dev if grid else None))
                     held.append((qjobs[-1], [t.name for t in its], sum(out[t.name]["prediction"].nbytes for t in its)))
                     del items
             while held and sum(h[2] for h in held) > self.QR_HOLD:
@@ -780,6 +827,7 @@ class Packer:
 
     PIECE = 64 << 20
     QR_HOLD = 24 << 30                   # predictions held by a file's queued QR batches (bytes)
+    BASE_GROUP = 8 << 30                 # a base in host memory: bytes per group of its coding
     RESERVE = 48 << 30                   # HBM kept beside the bases and the files in flight
 
     def _finish_file(self, state):
@@ -987,14 +1035,25 @@ class Packer:
             ahead = self.reader.submit(self._read_file, jobs[porder[0]]) if porder else None
             side = ThreadPoolExecutor(1)
             base_jobs = []
+            # the BF16 bases in HBM when they fit beside the largest derived file and RESERVE, else
+            # read window by window from host memory (seeds are always in HBM)
+            in_hbm = self.bases_in_hbm
+            if in_hbm is None:
+                free, _ = dev.mem_info()
+                need = sum(bsize[b.index] for _, b in loaded if not b.seed)
+                largest = max((os.path.getsize(p) for p in derived.values()), default=0)
+                in_hbm = need + largest + self.RESERVE <= free
+            if not in_hbm and self.method == "m28":
+                raise NotImplementedError("archive method m28 codes its base in HBM: a base bigger than HBM needs m29")
             place = {}                                 # a split model's shards: one after another in HBM
             for k, j in enumerate(joined):
-                allb[len(bnames) + k].d = d = dev.DeviceArray(j["size"], np.uint8)
-                for i, s_ in j["parts"]:
-                    place[i] = d.view(s_, (bsize[i],), np.uint8)
+                if in_hbm:
+                    allb[len(bnames) + k].d = d = dev.DeviceArray(j["size"], np.uint8)
+                    for i, s_ in j["parts"]:
+                        place[i] = d.view(s_, (bsize[i],), np.uint8)
             for (host, b), (n, p) in zip(loaded, bases.items()):
                 hashes[n] = self.hasher.submit(file_sha256, p)
-                b.d = self._load_base(p, into=place.get(b.index))
+                b.d = self._load_base(p, into=place.get(b.index)) if in_hbm or b.seed else None
                 base_jobs.append(side.submit(self._code_base, b, host, "stream" if b.index == 0 else "parts"))
                 later[n] = base_jobs[-1]
             if base_jobs:

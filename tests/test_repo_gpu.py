@@ -77,6 +77,13 @@ def test_small_repo_pack_is_deterministic(small_repo, tmp_path):
     tight.QR_HOLD = 0
     tight.pack([root], c, created="2026-01-01T00:00:00")
     assert open(a, "rb").read() == open(c, "rb").read()
+    # the base in host memory (a base bigger than HBM): coded in groups of 1 MiB, its tensors
+    # uploaded window by window for the derived files
+    d = str(tmp_path / "d.seedpack")
+    host = repo.Packer(bases_in_hbm=False)
+    host.BASE_GROUP = 1 << 20
+    host.pack([root], d, created="2026-01-01T00:00:00")
+    assert open(a, "rb").read() == open(d, "rb").read()
 
 
 def test_small_repo_method_m28(small_repo, tmp_path):
@@ -280,7 +287,13 @@ def test_split_model_repo(small_repo, tmp_path, method):
                 ["blk.0.ffn_down.weight"])
     a = str(tmp_path / "split.seedpack")
     say(f"case split model ({method}): pack")
-    stats = repo.pack_repo([src], a, method=method)
+    stats = repo.pack_repo([src], a, method=method, created="2026-01-01T00:00:00")
+    if method == "m29":                       # the shards in host memory: the same archive
+        h = str(tmp_path / "split_host.seedpack")
+        p = repo.Packer(bases_in_hbm=False)
+        p.BASE_GROUP = 1 << 20
+        p.pack([src], h, created="2026-01-01T00:00:00")
+        assert open(a, "rb").read() == open(h, "rb").read()
     man = json.loads(zstd.decompress(container.Reader(a).get("manifest")))
     shards = [f"model-BF16-{k:05d}-of-00003.gguf" for k in (1, 2, 3)]
     assert man["bases"] == shards and man["needs"] == "0.3.0"
