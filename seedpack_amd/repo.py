@@ -393,18 +393,19 @@ class _Base:
         self.header = bytes(host[:g.data_start])
         self.by_name = {t.name: t for t in g.tensors}
         self.dq, self.dq_bytes = collections.OrderedDict(), 0
-        self.src, self.parts = host, None
+        self.src, self.parts, self.rt = host, None, None
 
-    def host_bytes(self, off, n):
-        """n bytes of the base file (a split model: of its shards one after another) from host memory"""
+    def _source(self, off):
+        """(the base holding file offset `off`, the offset there): itself, or a split model's shard"""
         if self.parts is None:
-            return self.src[off:off + n]
+            return self, off
         start, sb = [p for p in self.parts if p[0] <= off][-1]
-        return sb.src[off - start:off - start + n]
+        return sb, off - start
 
     def window(self, names, stream):
-        """the base itself when resident, else a _Window of the tensors `names` uploaded from host
-        memory, each at a 256-byte boundary"""
+        """the base itself when resident, else a _Window of the tensors `names`, each at a 256-byte
+        boundary: uploaded from host memory (a base being packed), or decoded from the archive's
+        coded stream (`rt`, an R2Tensors; the file's other bytes from its rest part)"""
         if self.d is not None:
             return self
         ts = [self.by_name[n] for n in dict.fromkeys(names) if n in self.by_name]
@@ -413,9 +414,21 @@ class _Base:
             offs.append(o)
             o += -(-t.nbytes // 256) * 256
         d = dev.DeviceArray(max(o, 1), np.uint8)
+        coded = collections.defaultdict(list)          # source -> [(tensor index there, offset in d, bytes)]
         for t, at in zip(ts, offs):
-            src = np.ascontiguousarray(self.host_bytes(t.offset, t.nbytes))
+            sb, so = self._source(t.offset)
+            rt = getattr(sb, "rt", None)
+            if rt is not None and so in rt.index:
+                coded[sb].append((rt.index[so], at, t.nbytes))
+                continue
+            src = np.ascontiguousarray(rt.outside(so, so + t.nbytes) if rt is not None else sb.src[so:so + t.nbytes])
             check(lib().spa_memcpy_h2d(d.ptr + at, src.ctypes.data, t.nbytes, stream))
+        for sb, items in coded.items():
+            dd, outs = sb.rt.decode([k for k, _, _ in items])
+            for (_, at, nb), o_ in zip(items, outs):
+                check(lib().spa_memcpy_d2d(d.ptr + at, dd.ptr + o_, nb, stream))
+            dev.synchronize(stream)
+            del dd
         return _Window(d, {t.name: dataclasses.replace(t, offset=at) for t, at in zip(ts, offs)})
 
     @classmethod
@@ -430,7 +443,7 @@ class _Base:
         b.by_name = {n: dataclasses.replace(t, offset=t.offset + start)
                      for start, sb in parts for n, t in sb.by_name.items()}
         b.dq, b.dq_bytes = collections.OrderedDict(), 0
-        b.src, b.parts = None, list(parts)
+        b.src, b.parts, b.rt = None, list(parts), None
         return b
 
     def view(self, t, stream=None):
@@ -1219,8 +1232,11 @@ class Unpacker:
     the host, uploaded, its predictions regrown and XORed in and its QR batches decoded on the device,
     then read back, checked and written"""
 
-    def __init__(self, verbose=False, staging_bytes=64 << 30):
+    def __init__(self, verbose=False, staging_bytes=64 << 30, bases_in_hbm=None):
         self.verbose = verbose
+        # the bases decoded into HBM (True), decoded window by window from the archive (False), or
+        # in HBM when they fit beside the largest file to rebuild and 48 GB (None)
+        self.bases_in_hbm = bases_in_hbm
         self.stream = dev.Stream()
         self.gq = GPUQuant(stream=self.stream.handle)
         self.pool = _PinnedPool(staging_bytes)
@@ -1283,6 +1299,33 @@ class Unpacker:
                 if release:
                     self.pool.release(buf)
 
+        def stream_write(name, rt):
+            """a base decoded window by window (R2Tensors.write_to) into its file, checksummed on the way"""
+            h, n = hashlib.sha256(), [0]
+            path = None if outdir is None else os.path.join(outdir, *name.split("/"))
+            f = None
+            if path is not None:
+                os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
+                f = open(path + ".part", "wb")
+            try:
+                def write(b_):
+                    mv = memoryview(np.ascontiguousarray(b_)).cast("B")
+                    h.update(mv)
+                    n[0] += mv.nbytes
+                    if f is not None:
+                        f.write(mv)
+                rt.write_to(write)
+            finally:
+                if f is not None:
+                    f.close()
+            ok = h.hexdigest() == cat[name]["hash"] and n[0] == cat[name]["size"]
+            if path is not None:
+                if ok:
+                    os.replace(path + ".part", path)
+                else:
+                    os.remove(path + ".part")
+            results[name] = ok
+
         # other files
         exm = manifest["extras"]
         if any(n in want for n in exm["bundle"]) or sel:
@@ -1322,13 +1365,8 @@ class Unpacker:
         # shards of a split model that a file predicts from one after another in one allocation
         # (repo3.py:2307-2313)
         bases, place, jd, zdicts, coded = {}, {}, {}, {}, {}
-        for k, j in enumerate(joined):
-            if nb + k in need_b:
-                jd[k] = d = dev.DeviceArray(j["size"], np.uint8)
-                ends = [s_ for _, s_ in j["parts"][1:]] + [j["size"]]
-                for (i, s_), e_ in zip(j["parts"], ends):
-                    place[i] = d.view(s_, (e_ - s_,), np.uint8)
-        phys = sorted({i for i in need_b if i < nb} | set(place))
+        phys = sorted({i for i in need_b if i < nb} |
+                      {i for k, j in enumerate(joined) if nb + k in need_b for i, _ in j["parts"]})
         for i in phys:
             name = manifest["bases"][i]
             if name in seeds:                               # a seed: its file decoded by parts (seed.py)
@@ -1353,11 +1391,23 @@ class Unpacker:
                 raise ValueError(f"base {name}: a base chunk of an unknown kind")
             rest = np.frombuffer(header.header_d(read(*parts["rest"])), np.uint8)
             g = gguf.GGUF(rest.tobytes(), light=True)
-            coded[i] = (rest, g)
+            coded[i] = (rest, g, parts)
             zdicts[i] = bytes(rest[:g.data_start])
         for k, j in enumerate(joined):
             if nb + k in need_b:
                 zdicts[nb + k] = zdicts[j["parts"][0][0]]
+        in_hbm = self.bases_in_hbm
+        if in_hbm is None:
+            free, _ = dev.mem_info()
+            need = sum(cat[manifest["bases"][i]]["size"] for i in coded)
+            in_hbm = need + max((mf[i]["size"] for i in sel), default=0) + (48 << 30) <= free
+        if in_hbm:                           # a split model's shards one after another in one allocation
+            for k, j in enumerate(joined):
+                if nb + k in need_b:
+                    jd[k] = d = dev.DeviceArray(j["size"], np.uint8)
+                    ends = [s_ for _, s_ in j["parts"][1:]] + [j["size"]]
+                    for (i, s_), e_ in zip(j["parts"], ends):
+                        place[i] = d.view(s_, (e_ - s_,), np.uint8)
 
         def residual_of(i):
             m = mf[i]
@@ -1382,7 +1432,25 @@ class Unpacker:
             if i not in coded:
                 continue
             name = manifest["bases"][i]
-            rest, g = coded.pop(i)
+            rest, g, parts = coded.pop(i)
+            if not in_hbm:
+                # decoded window by window from the archive (repo3.py:2311-2323): random access to
+                # the coded stream of its tensors, the file written through it when it is wanted
+                if "stream" not in parts or "lens" not in parts or "meta" not in parts or "side" not in parts:
+                    raise ValueError(f"base {name}: not an R2 chunk")
+                if "layout" in parts:
+                    raise NotImplementedError("an M24 base (method m28) is decoded in HBM")
+                c = f"b{i}"
+                rt = r2.R2Tensors(lambda nm, c=c, pp=parts: bytes(r.read_at(c, *pp[nm])),
+                                  lambda o, n, out, c=c, at=parts["stream"][0]: r.read_at(c, at + o, n, out),
+                                  stream=self.stream.handle)
+                b = _Base(i, name, rest, None, g)
+                b.rt = rt
+                bases[i] = b
+                if name in want:
+                    stream_write(name, rt)
+                log(self.verbose, f"  base {name}: decoded window by window, {time.perf_counter() - t0:.1f} s")
+                continue
             ch = unpack(memoryview(r.get(f"b{i}")))
             log(self.verbose, f"  base {name}: chunk read, {time.perf_counter() - t0:.1f} s")
             if "r2" in ch:
@@ -1398,8 +1466,9 @@ class Unpacker:
                 check(lib().spa_memcpy_d2h(host.ctypes.data, d.ptr, d.nbytes, self.stream.handle))
                 jobs.append(self.files.submit(check_write, name, host, True))
             log(self.verbose, f"  base {name}: decoded, {time.perf_counter() - t0:.1f} s")
-        for k, d in jd.items():
-            bases[nb + k] = _Base.joined(nb + k, [(s_, bases[i]) for i, s_ in joined[k]["parts"]], d)
+        for k, j in enumerate(joined):
+            if nb + k in need_b:
+                bases[nb + k] = _Base.joined(nb + k, [(s_, bases[i]) for i, s_ in j["parts"]], jd.get(k))
         for k in range(min(2, len(order))):
             if k not in ahead:
                 ahead[k] = self.ahead.submit(residual_of, order[k])
@@ -1498,17 +1567,30 @@ class Unpacker:
 
         fitted = self.imx_sets
 
-        def tensor(name):
-            bt = b.by_name[name]
+        def tensor(name, bw):
+            bt = bw.by_name[name]
             return residual.Tensor(name, ttype[name], bt.shape[0], R.view(tens[name].offset, (tens[name].nbytes,), np.uint8),
-                                   b.view(bt, st), imatrix=imx_map.get(name),
+                                   bw.view(bt, st), imatrix=imx_map.get(name),
                                    fitted={k: s_[name] for k, s_ in fitted.items() if name in s_},
                                    base_type=bt.type, numel=tens[name].numel)
 
+        # the regrown and XORed tensors, in runs of about WINDOW base bytes (a base not in HBM is
+        # decoded for each run; b.window is the base itself when it is in HBM)
+        runs, cur, acc = [], [], 0
         for e in plan:
-            name, kind, v = e[0], e[1], e[2]
-            if kind in ("rq", "xor"):
-                t = tensor(name)
+            if e[1] in ("rq", "xor"):
+                nbb = b.by_name[e[0]].nbytes
+                if cur and acc + nbb > WINDOW:
+                    runs.append(cur)
+                    cur, acc = [], 0
+                cur.append(e)
+                acc += nbb
+        if cur:
+            runs.append(cur)
+        for run in runs:
+            bw = b.window([e[0] for e in run], st)
+            for name, kind, v, *_ in run:
+                t = tensor(name, bw)
                 p = residual.predict(self.gq, t, v, stream=st)
                 check(lib().spa_xor(t.region.ptr, t.region.ptr, p.ptr, t.region.nbytes, None, st))
         lap("regrow+xor")
@@ -1516,11 +1598,12 @@ class Unpacker:
             ch = unpack(memoryview(r.get(f"q{i}")))
             var = {e[0]: e[2] for e in plan}
             for k, (T, names) in enumerate(json.loads(zstd.decompress(ch["meta"]))):
-                ts = [tensor(n) for n in names]
+                bw = b.window(names, st)
+                ts = [tensor(n, bw) for n in names]
                 preds = [residual.predict(self.gq, t, var[t.name], stream=st) for t in ts]
-                items = [(p, b.by_name[t.name].offset, b.by_name[t.name].type, b.by_name[t.name].shape[0],
+                items = [(p, bw.by_name[t.name].offset, bw.by_name[t.name].type, bw.by_name[t.name].shape[0],
                           imx_off.get(t.name, -1) if T in qr.GRID_TYPES else -1) for t, p in zip(ts, preds)]
-                F = qr.decode(T, bytes(ch[str(k)]), items, b.d, imx_dev if T in qr.GRID_TYPES else None, stream=st)
+                F = qr.decode(T, bytes(ch[str(k)]), items, bw.d, imx_dev if T in qr.GRID_TYPES else None, stream=st)
                 o = 0
                 for t in ts:
                     check(lib().spa_memcpy_d2d(t.region.ptr, F.ptr + o, t.region.nbytes, st))

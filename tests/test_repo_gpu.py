@@ -62,6 +62,13 @@ def test_small_repo_extracts_byte_identical(small_repo, tmp_path):
     res = repo.unpack_repo(arc, None, ["model-IQ2_XS.gguf"])
     assert res["files"] == {"model-IQ2_XS.gguf": True}
     assert stats["stats"]["qr"] > 0 and stats["stats"]["requant_diff"] > 0
+    # the base not in HBM (a base bigger than HBM): decoded window by window from the archive, its
+    # own file written through the same decoder
+    out2 = str(tmp_path / "out2")
+    res = repo.Unpacker(bases_in_hbm=False).run(arc, out2)
+    assert not res["bad"] and not res["missing"], res
+    for n in names:
+        assert open(os.path.join(root, n), "rb").read() == open(os.path.join(out2, n), "rb").read(), n
 
 
 def test_small_repo_pack_is_deterministic(small_repo, tmp_path):
@@ -310,6 +317,11 @@ def test_split_model_repo(small_repo, tmp_path, method):
     for pick in ("model-Q4_0-00002-of-00002.gguf", shards[1]):
         res = repo.unpack_repo(a, None, [pick])
         assert res["files"] == {pick: True}, res
+    if method == "m29":                       # the shards decoded window by window
+        res = repo.Unpacker(bases_in_hbm=False).run(a, str(tmp_path / "out_w"))
+        assert not res["bad"] and not res["missing"], res
+        for n in sorted(os.listdir(src)):
+            assert open(os.path.join(src, n), "rb").read() == open(os.path.join(tmp_path, "out_w", n), "rb").read(), n
 
 
 def test_small_repo_archive_layout(small_repo):
