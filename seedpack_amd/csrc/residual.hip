@@ -133,7 +133,17 @@ __global__ __launch_bounds__(WG) void k_hash(const uint8_t* base, const uint64_t
 }
 
 // float prediction: source weights (BF16 bits, F16, F32) -> bytes of the file's float type:
-// F32 as is, F16 by round-to-nearest-even (CuPy's astype), BF16 by (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+// F32 as is, F16 by round-to-nearest-even (the astype of repo3.py:685), BF16 by
+// (u + 0x7FFF + ((u >> 16) & 1)) >> 16. A NaN goes to F16 as numpy's conversion (the reference's
+// --cpu path) takes it: sign, all-ones exponent and the top 10 payload bits, 0x7C01 when those are 0.
+__device__ __forceinline__ uint16_t pred_f16(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        const uint32_t m = (u >> 13) & 0x3ffu;
+        return (uint16_t)(((u >> 16) & 0x8000u) | 0x7c00u | (m ? m : 1u));
+    }
+    return f32_to_f16(x);
+}
 __device__ __forceinline__ float src_value(const void* src, int kind, int64_t i) {
     if (kind == SRC_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(src)[i]);
     if (kind == SRC_F16) return f16_to_f32(reinterpret_cast<const uint16_t*>(src)[i]);
@@ -145,7 +155,7 @@ __global__ __launch_bounds__(WG) void k_float_pred(const void* src, int kind, in
         if (dst_type == 0) {
             reinterpret_cast<float*>(dst)[i] = x;
         } else if (dst_type == 1) {
-            reinterpret_cast<uint16_t*>(dst)[i] = f32_to_f16(x);
+            reinterpret_cast<uint16_t*>(dst)[i] = pred_f16(x);
         } else {
             const uint32_t u = __float_as_uint(x);
             reinterpret_cast<uint16_t*>(dst)[i] = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);

@@ -63,6 +63,26 @@ def test_float_predictions():
     assert got.tobytes() == want.tobytes()
 
 
+def test_float_prediction_f16_every_bit_pattern():
+    """F16 prediction of every BF16 and every F16 bit pattern (NaNs included) equals numpy's astype, the
+    call of the reference's --cpu path (repo3.py:685); F32 NaNs with payloads only in the low 13 bits
+    become 0x7C01 | sign"""
+    b = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    with np.errstate(all="ignore"):
+        want = (b.astype(np.uint32) << 16).view(np.float32).astype(np.float16).view(np.uint16)
+    got = r.float_prediction(dev.DeviceArray.from_host(b), r.F16).to_host().view(np.uint16)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, [(hex(b[i]), hex(got[i]), hex(want[i])) for i in bad[:8]]
+    h = b.view(np.float16)
+    got = r.float_prediction(dev.DeviceArray.from_host(h), r.F16).to_host().view(np.uint16)
+    assert got.tobytes() == h.astype(np.float32).astype(np.float16).view(np.uint16).tobytes()
+    f = np.array([0x7F800001, 0xFF800FFF, 0x7FC00000, 0x7FBFFFFF, 0xFFFFFFFF, 0x7F802000], np.uint32).view(np.float32)
+    with np.errstate(all="ignore"):
+        want = f.astype(np.float16).view(np.uint16)
+    got = r.float_prediction(dev.DeviceArray.from_host(f), r.F16).to_host().view(np.uint16)
+    assert got.tobytes() == want.tobytes() and list(want[:2]) == [0x7C01, 0xFC01], [hex(v) for v in got]
+
+
 def _case(t_type, rows=64, cols=1024, seed=3):
     g = np.random.Generator(np.random.PCG64(seed + t_type))
     w = synth.student_t_bf16(g, (rows, cols)) if t_type in (16, 17, 18, 19, 21, 22, 29) else synth.normal_bf16(g, (rows, cols), 0.02)
