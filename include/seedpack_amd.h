@@ -85,9 +85,16 @@ int spa_type_variants(int ggml_type);
 /* Quantizes nrows x n_per_row weights (row-major, src_kind SPA_SRC_*) into dst
  * (nrows * spa_row_size bytes), byte-identical to llama.cpp's quantize_<type>(src, dst, nrows,
  * n_per_row, imatrix) built with -ffp-contract=off. imatrix: device pointer to n_per_row floats,
- * or NULL for the reference (no-imatrix) path. Replaces gpuquant.py:205-211 + :432-456. */
+ * or NULL for the reference (no-imatrix) path. work: optional device scratch (4-byte aligned) of
+ * spa_quantize_work_bytes bytes, used by this call only; NULL is accepted for every type (the
+ * imatrix Q4_0/Q4_1/Q5_0/Q5_1 then compute their row statistics inside the quantizer launch,
+ * 2.4-4.3x slower). The library allocates nothing. Replaces gpuquant.py:205-211 + :432-456. */
 int spa_quantize(int ggml_type, int variant, const void* src, int src_kind, int64_t nrows, int64_t n_per_row,
-                 const float* imatrix, void* dst, void* stream);
+                 const float* imatrix, void* dst, void* work, void* stream);
+
+/* Bytes of the optional `work` scratch of spa_quantize (0: the call uses none): one float per row
+ * for the imatrix Q4_0, Q4_1, Q5_0 and Q5_1 (their row mean squares, ggml-quants.c:2082-2084). */
+uint64_t spa_quantize_work_bytes(int ggml_type, int64_t nrows, int64_t n_per_row, int has_imatrix);
 
 /* Dequantizes nrows x n_per_row weights of a quantized row-major run of blocks (src) into dst
  * (nrows * n_per_row floats, 16-byte aligned), bit-identical to llama.cpp's

@@ -46,7 +46,8 @@ SIGNATURES = {
     "spa_dequantize": (c_int, [c_int, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "spa_row_size": (c_size_t, [c_int, c_int64]),
     "spa_type_variants": (c_int, [c_int]),
-    "spa_quantize": (c_int, [c_int, c_int, c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "spa_quantize": (c_int, [c_int, c_int, c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "spa_quantize_work_bytes": (c_uint64, [c_int, c_int64, c_int64, c_int]),
     "spa_iq_table_host": (c_int, [c_int, ctypes.POINTER(c_void_p), ctypes.POINTER(c_int), ctypes.POINTER(c_void_p),
                                   ctypes.POINTER(c_int), ctypes.POINTER(c_void_p), ctypes.POINTER(c_int)]),
     "spa_qr_seg_blocks": (c_int, [c_int]),

@@ -107,8 +107,13 @@ int spa_type_variants(int t) {
     return t == 29 ? 2 : 1;
 }
 
+uint64_t spa_quantize_work_bytes(int t, int64_t nrows, int64_t n_per_row, int has_imatrix) {
+    (void)n_per_row;
+    return (uint64_t)spa::quantize_work_bytes(t, nrows, has_imatrix != 0);
+}
+
 int spa_quantize(int t, int variant, const void* src, int src_kind, int64_t nrows, int64_t npr, const float* imatrix,
-                 void* dst, void* stream) {
+                 void* dst, void* work, void* stream) {
     const int qk = spa::type_qk(t);
     if (!qk) return fail(SPA_ERR_TYPE, "spa_quantize: unknown ggml type %d", t);
     if (variant < 0 || variant >= spa_type_variants(t))
@@ -124,7 +129,8 @@ int spa_quantize(int t, int variant, const void* src, int src_kind, int64_t nrow
     // IQ2_XXS, IQ2_XS, IQ1_S assert an imatrix (ggml-quants.c:3303, :3481, :4528)
     if (!imatrix && (t == 16 || t == 17 || t == 19))
         return fail(SPA_ERR_ASSERT, "spa_quantize: type %d requires an imatrix", t);
-    spa::QuantArgs a{t, variant, src, src_kind, nrows, npr, imatrix, dst, (hipStream_t)stream};
+    if (work && (reinterpret_cast<uintptr_t>(work) & 3u)) return fail(SPA_ERR_ARG, "spa_quantize: misaligned work");
+    spa::QuantArgs a{t, variant, src, src_kind, nrows, npr, imatrix, dst, (hipStream_t)stream, (float*)work};
     switch (t) {
         case 2: case 3: case 6: case 7: case 8: case 42: return spa::launch_legacy(a);
         case 10: case 11: case 12: case 13: case 14: return spa::launch_kquant(a);

@@ -17,7 +17,12 @@ struct QuantArgs {
     const float* imatrix;   // device, n_per_row floats, or nullptr
     void* dst;              // device, nrows * row_size bytes
     hipStream_t stream;
+    float* work;            // device scratch of quantize_work_bytes bytes, or nullptr
 };
+
+// Device scratch that a quantize launch can use (0: none): the legacy imatrix types keep one row
+// statistic per row there.
+int64_t quantize_work_bytes(int type, int64_t nrows, bool imatrix);
 
 // Type table (requant.py:21-27): block elements and block bytes; 0 if the type is unknown.
 int type_qk(int type);

@@ -35,8 +35,13 @@ def quantize_into(ttype, src, n_per_row, dst, imatrix=None, variant=0, stream=No
     assert nrows * n_per_row == src.size, "tensor size is not a whole number of rows"
     need = nrows * (n_per_row // QFUN[ttype][1]) * QFUN[ttype][2]
     assert dst.nbytes >= need, (dst.nbytes, need)
+    wb = lib().spa_quantize_work_bytes(ttype, nrows, n_per_row, imatrix is not None)
+    # the scratch goes back to this thread's cache when the call returns: the next block taken from
+    # it is used on the same stream, after this launch
+    work = dev.DeviceArray(wb, np.uint8) if wb else None
     check(lib().spa_quantize(ttype, variant, src.ptr, _src_kind(src), nrows, n_per_row,
-                             None if imatrix is None else imatrix.ptr, dst.ptr, stream))
+                             None if imatrix is None else imatrix.ptr, dst.ptr, None if work is None else work.ptr,
+                             stream))
     return dst
 
 

@@ -41,11 +41,15 @@ def test_row_size_matches_type_table(t):
 
 def test_bad_arguments_fail_before_any_device_call():
     L = _lib.lib()
-    assert L.spa_quantize(99, 0, None, 0, 1, 256, None, None, None) == -2
+    assert L.spa_quantize(99, 0, None, 0, 1, 256, None, None, None, None) == -2
     assert b"unknown ggml type" in L.spa_last_error()
-    assert L.spa_quantize(12, 0, None, 0, 1, 100, None, None, None) == -4
-    assert L.spa_quantize(12, 1, None, 0, 1, 256, None, None, None) == -2       # no variant 1 for Q4_K
-    assert L.spa_quantize(16, 0, None, 0, 1, 256, None, None, None) == -4       # null src first
+    assert L.spa_quantize(12, 0, None, 0, 1, 100, None, None, None, None) == -4
+    assert L.spa_quantize(12, 1, None, 0, 1, 256, None, None, None, None) == -2       # no variant 1 for Q4_K
+    assert L.spa_quantize(16, 0, None, 0, 1, 256, None, None, None, None) == -4       # null src first
+    # scratch: one float per row (256-byte rounded) for the imatrix Q4_0/Q4_1/Q5_0/Q5_1, none otherwise
+    assert [L.spa_quantize_work_bytes(t, 100, 4096, 1) for t in (2, 3, 6, 7)] == [512] * 4
+    assert [L.spa_quantize_work_bytes(t, 100, 4096, 0) for t in (2, 3, 6, 7)] == [0] * 4
+    assert [L.spa_quantize_work_bytes(t, 100, 4096, 1) for t in (8, 12, 16, 20)] == [0] * 4
     assert L.spa_type_variants(29) == 2 and L.spa_type_variants(12) == 1 and L.spa_type_variants(99) == 0
 
 

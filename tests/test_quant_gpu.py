@@ -140,3 +140,34 @@ def test_legacy_imatrix_rows_with_half_tile(gq, t):
     bad = np.flatnonzero(got != want)
     assert bad.size == 0, f"{bad.size} bytes differ, first at {bad[:8]}"
     assert hip(gq, t, x, imx).tobytes() == got.tobytes()
+
+
+@pytest.mark.parametrize("t", [2, 3, 6, 7])
+def test_legacy_imatrix_with_and_without_scratch(gq, t):
+    """the imatrix Q4_0/Q4_1/Q5_0/Q5_1 with the row mean squares from the first launch (scratch) and
+    computed inside the quantizer (no scratch): the same bytes, equal to the oracle's, on row lengths
+    that leave a partial 128-column tile (32, 96, 160, 4128) and row counts that leave a partial
+    32-row group, for BF16, F16 and F32 sources"""
+    from seedpack_amd._lib import check, lib
+    g = np.random.Generator(np.random.PCG64(0xC0 + t))
+    for rows, npr in ((1, 32), (31, 96), (33, 160), (70, 4128), (5, 12288)):
+        b = synth.normal_bf16(g, (rows, npr), 0.02, outlier_frac=0.002)
+        x = synth.bf16_to_f32(b).reshape(b.shape)
+        imx = dev.DeviceArray.from_host(g.lognormal(0, 1, npr).astype(np.float32))
+        want = quants.quantize(t, x, imx.to_host()) if rows * npr <= 70 * 4128 else None
+        say("case legacy scratch", t, rows, npr)
+        for kind, a in ((0, b), (1, x.astype(np.float16)), (2, x)):
+            if kind == 1 and not np.array_equal(a.astype(np.float32), x):
+                continue
+            src = dev.DeviceArray.from_host(np.ascontiguousarray(a).reshape(-1))
+            nbw = lib().spa_quantize_work_bytes(t, rows, npr, 1)
+            assert nbw == (rows * 4 + 255) // 256 * 256
+            work = dev.DeviceArray(nbw, np.uint8)
+            outs = []
+            for w in (work.ptr, None):
+                dst = dev.DeviceArray(rows * row_size(t, npr), np.uint8)
+                check(lib().spa_quantize(t, 0, src.ptr, kind, rows, npr, imx.ptr, dst.ptr, w, None))
+                outs.append(dst.to_host())
+            assert outs[0].tobytes() == outs[1].tobytes(), (t, rows, npr, kind)
+            if want is not None:
+                assert outs[0].tobytes() == want.tobytes(), (t, rows, npr, kind)
