@@ -139,9 +139,10 @@ def profile_pass():
     log(f"profile: k_copy16 {nb} bytes x2 launches (reads {nb}, writes {nb})")
 
 
-def iquant_cfg3(stream, reps=2):
-    """configuration 3: the i-quants with the imatrix on the 4096x12288 and 12288x4096 Student-t tensors,
-    each type launched once untimed, then `reps` times between HIP events on the bench stream"""
+def iquant_cfg3(stream, reps=2, types=None):
+    """configuration 3: the i-quants (or `types`) with the imatrix on the 4096x12288 and 12288x4096
+    Student-t tensors, each type launched once untimed, then `reps` times between HIP events on the
+    bench stream"""
     from seedpack_amd import device as dev
     from seedpack_amd import synth
     from seedpack_amd.gpuquant import quantize_into
@@ -151,7 +152,7 @@ def iquant_cfg3(stream, reps=2):
         w, imx = synth.tensor(3, ti)
         src = dev.DeviceArray.from_host(w.reshape(-1), stream.handle)
         dimx = dev.DeviceArray.from_host(imx, stream.handle)
-        for t in synth.TYPES[3]:
+        for t in types or synth.TYPES[3]:
             out = dev.DeviceArray(w.shape[0] * row_size(t, w.shape[1]), np.uint8)
             quantize_into(t, src, w.shape[1], out, dimx, 0, stream.handle)
             e0, e1 = dev.Event(), dev.Event()
@@ -705,6 +706,8 @@ def main():
 
     dqb = dequant_cfg2(stream, dsrc["token_embd"], dimx["token_embd"])
     iq = iquant_cfg3(stream)
+    # the imatrix legacy types on the same tensors (row statistics launch + quantizer)
+    lq = iquant_cfg3(stream, 5, [2, 3, 6, 7])
     qrb = qr_cfg1(stream)
     qrg = qr_cfg3(stream)
     r2b = r2_layer(stream)
@@ -717,7 +720,7 @@ def main():
             "data": "synthetic (seeded N(0,0.02) BF16, LogNormal(0,1) imatrix)",
             "config": {"workload": "cfg2: Q2_K,Q3_K,Q4_K,Q5_K,Q6_K (imatrix) on token_embd 151936x1024 + ffn_down 1024x3072",
                        "bf16_bytes_per_step": bf16_bytes, "launches_per_step": len(launches)},
-            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "dequant_token_embd": dqb, "qr_cfg1": qrb, "qr_cfg3": qrg, "r2_base": r2b, "r2_cfg4": r2c,
+            "per_type": per_type, "legacy_hbm_types": legacy, "iquant_cfg3": iq, "legacy_imatrix_cfg3": lq, "dequant_token_embd": dqb, "qr_cfg1": qrb, "qr_cfg3": qrg, "r2_base": r2b, "r2_cfg4": r2c,
             "pack_cfg4": pk, "unpack_cfg5": upk,
             "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
