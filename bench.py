@@ -305,7 +305,8 @@ class HbmPeak:
         return self.peak
 
 
-def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False, reuse=False, write_only=False):
+def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False, reuse=False, write_only=False,
+               bases_in_hbm=None):
     """configurations 4 and 5 from host files, as the reference's CLI measures them (cli.py:288-292,
     :441): a synthetic Qwen3.5-9B-shaped repository (BF16 GGUF with a 151,936-token BPE tokenizer,
     imatrix.dat, README.md, 21 quantized GGUFs made by this library's quantizers with 1% of their
@@ -315,7 +316,9 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
     extract of the Q4_K_M-like and IQ2_XS files from that archive (residual zstd, regrowth, QR decode,
     SHA-256 check, files written). Peak HBM by hipMemGetInfo polling. The extracted files are
     compared byte for byte with the originals. reuse: the repository a previous write_only call left
-    in root is packed (a kernel-trace run then sees the pack and the extract only)."""
+    in root is packed (a kernel-trace run then sees the pack and the extract only). bases_in_hbm False:
+    the base kept in host memory by the pack and decoded window by window by the extract, which then
+    writes the base file too."""
     import shutil
     from seedpack_amd import device as dev
     from seedpack_amd import repo, synth
@@ -348,7 +351,7 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
             return None, None
         arc = os.path.join(arc_dir, "model.seedpack")
         peak = HbmPeak().start()
-        st = repo.Packer(verbose=True).pack([src], arc)
+        st = repo.Packer(verbose=True, bases_in_hbm=bases_in_hbm).pack([src], arc)
         pk_peak = peak.stop()
         log(f"bench: pack {st['input_bytes'] / 1e9:.1f} GB -> {st['archive_bytes'] / 1e9:.2f} GB in {st['seconds']:.1f} s "
             f"= {st['GB_s']:.2f} GB/s, peak HBM {pk_peak / 1e9:.1f} GB (residuals waiting in HBM: at most "
@@ -357,8 +360,10 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
             log(f"bench:   {f}")
         log(f"bench: pack cpu {st['cpu']}")
         want = [n for n in ("model-Q4_K_M.gguf", "model-IQ2_XS.gguf") if n in qf]
+        if bases_in_hbm is False:
+            want.append("model-BF16.gguf")
         peak = HbmPeak().start()
-        ex = repo.Unpacker(verbose=True).run(arc, out, want)
+        ex = repo.Unpacker(verbose=True, bases_in_hbm=bases_in_hbm).run(arc, out, want)
         up_peak = peak.stop()
         same = all(_same_file(os.path.join(src, n), os.path.join(out, n)) for n in want)
         log(f"bench: extract {ex['bytes'] / 1e9:.2f} GB in {ex['seconds']:.2f} s = {ex['GB_s']:.2f} GB/s, "
@@ -368,7 +373,8 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
                 "archive_bytes": st["archive_bytes"], "ratio": round(st["archive_bytes"] / st["input_bytes"], 4),
                 "pack_s": round(st["seconds"], 2), "pack_GB_s": round(st["GB_s"], 3), "peak_hbm_GB": round(pk_peak / 1e9, 1),
                 "stats": st["stats"], "phases_s": st.get("phases"), "host_cpu_s": st.get("cpu")}
-        unpack = {"workload": "cfg5: Q4_K_M-like and IQ2_XS extracted from the cfg4 archive (files written, SHA-256 checked)",
+        unpack = {"workload": "cfg5: Q4_K_M-like and IQ2_XS extracted from the cfg4 archive (files written, SHA-256 checked)"
+                              + (", and the BF16 base decoded window by window" if bases_in_hbm is False else ""),
                   "written_bytes": ex["bytes"], "extract_s": round(ex["seconds"], 2), "GB_s_written": round(ex["GB_s"], 3),
                   "checksums_ok": not ex["bad"] and not ex["missing"], "byte_identical": same,
                   "peak_hbm_GB": round(up_peak / 1e9, 1)}
@@ -576,6 +582,9 @@ def main():
                     help="only write the --pack repository into --repo-dir and keep it (for a later --reuse-repo run)")
     ap.add_argument("--reuse-repo", action="store_true",
                     help="--pack on the repository a --write-repo run left in --repo-dir (kept)")
+    ap.add_argument("--bases-host", action="store_true",
+                    help="--pack with the BF16 base kept in host memory (pack) and decoded window by window from the "
+                         "archive (extract, which writes the base file too), as for a base bigger than HBM")
     ap.add_argument("--q8", action="store_true",
                     help="only the Q8_0 codec (a seed's Q8_0 part) on a Qwen3.5-9B-shaped Q8_0 file; prints its "
                          "result, no JSON line")
@@ -589,7 +598,7 @@ def main():
     if a.pack or a.unpack or a.write_repo:
         files = a.pack_files.split(",") if a.pack_files else None
         pk, upk = repo_cfg45(layers=a.pack_layers, files=files, root=a.repo_dir, reuse=a.reuse_repo,
-                             write_only=a.write_repo)
+                             write_only=a.write_repo, bases_in_hbm=False if a.bases_host else None)
         if not a.write_repo:
             print(json.dumps({"pack_cfg4": pk, "unpack_cfg5": upk}))
         return None
