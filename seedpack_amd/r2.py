@@ -764,24 +764,38 @@ class R2Tensors:
 
     def write_to(self, write, window=1 << 30):
         """the whole file in order through write(bytes-like), decoding about `window` bytes of tensors
-        at a time"""
+        at a time; write() runs on a worker thread, one window behind the decoding (the device work
+        stays on the calling thread and its stream)"""
         t = self.layout["t"]
-        pos, i = 0, 0
+        runs, i = [], 0
         while i < len(t):
             j = i + 1
             total = t[i][1]
             while j < len(t) and total + t[j][1] <= window:
                 total += t[j][1]
                 j += 1
-            d, outs = self.decode(range(i, j))
-            h = d.to_host(stream=self.stream)
+            runs.append((i, j))
+            i = j
+        pos = [0]
+
+        def consume(i, j, h, outs):
             for k in range(i, j):
                 off, n = t[k][0], t[k][1]
-                if off > pos:
-                    write(self.outside(pos, off))
+                if off > pos[0]:
+                    write(self.outside(pos[0], off))
                 write(h[outs[k - i]:outs[k - i] + n])
-                pos = off + n
-            del d, h
-            i = j
-        if pos < self.size:
-            write(self.outside(pos, self.size))
+                pos[0] = off + n
+
+        with ThreadPoolExecutor(1) as ex:
+            pending = None
+            for i, j in runs:
+                d, outs = self.decode(range(i, j))
+                h = d.to_host(stream=self.stream)
+                del d
+                if pending is not None:
+                    pending.result()
+                pending = ex.submit(consume, i, j, h, outs)
+            if pending is not None:
+                pending.result()
+        if pos[0] < self.size:
+            write(self.outside(pos[0], self.size))

@@ -1307,15 +1307,19 @@ class Unpacker:
             if path is not None:
                 os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
                 f = open(path + ".part", "wb")
+            wpool = ThreadPoolExecutor(1)
             try:
                 def write(b_):
+                    # the file write beside the checksum (both release the interpreter lock)
                     mv = memoryview(np.ascontiguousarray(b_)).cast("B")
+                    fw = wpool.submit(f.write, mv) if f is not None else None
                     h.update(mv)
                     n[0] += mv.nbytes
-                    if f is not None:
-                        f.write(mv)
+                    if fw is not None:
+                        fw.result()
                 rt.write_to(write)
             finally:
+                wpool.shutdown()
                 if f is not None:
                     f.close()
             ok = h.hexdigest() == cat[name]["hash"] and n[0] == cat[name]["size"]
