@@ -685,7 +685,7 @@ __global__ __launch_bounds__(256) void k_norm_i8(const float* __restrict__ W, co
     if (valid[r]) {
         double t = rint((double)W[i] / nrm[r] * 127.0);
         t = t < -127.0 ? -127.0 : (t > 127.0 ? 127.0 : t);
-        v = (int)t;
+        v = t == t ? (int)t : 0;                    // NaN (rows of infinite scales) -> 0, numpy's cast
     }
     Wq[i] = (int8_t)v;
 }

@@ -112,6 +112,12 @@ def _total(x):
     return float(np.add.accumulate(x)[-1]) if len(x) else 0.0
 
 
+def _int8_nan0(v):
+    """float array to int8 with NaN as 0 (values already clipped to the int8 range)"""
+    v = np.asarray(v)
+    return np.where(np.isnan(v), 0, v).astype(np.int8)
+
+
 def waves_of(n, waves):
     """first and end row of each wave of n rows (gpu3.py:315-319)"""
     wave = (np.arange(n) * waves) // n
@@ -446,9 +452,11 @@ class M22:
         frac = np.where(kuse > 0, frac, np.float32(1.0)).astype(np.float32)
         gfrac = _total(col_res) / max(_total(col_w), 1e-30)
         ratio = np.maximum(col_res / np.maximum(col_w, 1e-30), 1e-6)
-        cadj = np.clip(np.rint(4 * _log2(ratio, st)), -60, 0).astype(np.int8)
+        # a NaN (from fp16 infinity / NaN scales) becomes 0, the device float-to-int conversion's value
+        # for NaN that the reference's planner stores; numpy leaves that cast undefined
+        cadj = _int8_nan0(np.clip(np.rint(4 * _log2(ratio, st)), -60, 0))
         q = frac / np.float32(max(gfrac, 1e-6))
-        fbin = np.clip(np.rint(_log2(q.astype(np.float64), st) * 4), -40, 20).astype(np.int8)
+        fbin = _int8_nan0(np.clip(np.rint(_log2(q.astype(np.float64), st) * 4), -40, 20))
         return dict(par=par, coefs=coefs, fbin=fbin, mu=mu, cadj=cadj)
 
     def _encode_extra(self, allb, pos, plans, meta, meta_d, side_d, cfi, row_m):
@@ -501,7 +509,7 @@ class M22:
             "Ctables": tabs.stored(),
             "Cside": zstd.zstd_c(json.dumps(side).encode()),
             "Cpar": zstd.zstd_c(par_all.tobytes(), 19),
-            "Ccoef": zstd.zstd_c(np.rint(coef_all * np.float32(64)).astype(np.int8).tobytes(), 19),
+            "Ccoef": zstd.zstd_c(_int8_nan0(np.rint(coef_all * np.float32(64))).tobytes(), 19),
             "Cfbin": zstd.zstd_c(fbin_all.tobytes(), 19),
             "Cmu": zstd.zstd_c(mu_all.tobytes()),
             "Ccadj": zstd.zstd_c(np.concatenate([p["cadj"] for p in plans]).astype(np.int8).tobytes(), 19),

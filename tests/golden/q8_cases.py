@@ -10,7 +10,9 @@ Tensor kinds:
   "embd"    token embeddings: most rows a mix of two earlier rows plus noise (row prediction finds
             them), duplicate rows (references), all-zero rows, loud rows;
   "odd"     like normal, plus hand-made blocks: weights of -128, a zero scale with non-zero weights,
-            a negative scale, a subnormal scale.
+            a negative scale, a subnormal scale;
+  "embd_bad" like embd, plus blocks whose fp16 scale is +inf, -inf or NaN (a damaged file): the
+            planner's row and column statistics become NaN, and its int8 side values of NaN are 0.
 """
 import numpy as np
 
@@ -24,6 +26,7 @@ CASES = [  # (name, [(tensor name, rows, row length, kind)], options)
     ("parts", [("blk.0.attn_v.weight", 64, 256, "normal"), ("token_embd.weight", 700, 128, "embd"),
                ("blk.0.ffn_gate.weight", 96, 512, "odd"), ("blk.1.attn_v.weight", 64, 256, "dups")],
      {"part_bytes": 80000}),
+    ("bad_scales", [("token_embd.weight", 400, 128, "embd_bad"), ("blk.0.attn_q.weight", 64, 256, "normal")], {}),
 ]
 
 
@@ -50,7 +53,7 @@ def q8_blocks(x):
 def _weights(g, rows, C, kind):
     cs = np.exp(g.normal(0, 0.5, C)).astype(np.float32)
     x = (g.normal(0, 0.02, (rows, C)) * cs + 0.004 * g.normal(0, 1, C) * cs).astype(np.float32)
-    if kind == "embd":
+    if kind.startswith("embd"):
         for r in range(40, rows):
             if g.random() < 0.7:
                 p1, p2 = g.integers(0, r, 2)
@@ -75,6 +78,13 @@ def _tensor(g, rows, C, kind):
         blk[6, :2] = (3, 0)                                   # subnormal scale
         blk[7, 2:] = 0                                        # all-zero weights
         blk[8, 2:] = 0x7f                                     # ties for the maximum
+    if kind == "embd_bad":
+        nb = C // 32
+        blk[60 * nb + 1, :2] = (0x00, 0x7c)                   # +inf
+        blk[61 * nb, :2] = (0x00, 0xfc)                       # -inf
+        blk[62 * nb + 2, :2] = (0x01, 0x7e)                   # NaN
+        blk[63 * nb + 3, :2] = (0x00, 0x7c)
+        blk[63 * nb + 3, 2:] = 0                              # +inf times zero weights
     return blk
 
 
