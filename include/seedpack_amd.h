@@ -62,6 +62,15 @@ int spa_mem_info(size_t* free_bytes, size_t* total_bytes);
 /* Device-to-device copy by a plain streaming kernel (16-byte multiples); the HBM yardstick the
  * traffic counters of the other kernels are scaled against. No reference counterpart. */
 int spa_copy(void* dst, const void* src, size_t nbytes, void* stream);
+/* VALU issue-rate probe: nblocks workgroups of 256 lanes, each lane `iters` loop trips of independent
+ * plain 32-bit VALU instructions (op 0: 128 v_fma_f32, op 1: 128 v_add_f32, op 2: 128 v_xor_b32 +
+ * 128 v_add_u32, op 3: 64 v_fma_f32 + 64 v_xor_b32 + 64 v_add_u32, op 4: 64 v_mul_f32 + 64 v_add_f32,
+ * op 5: 128 v_mul_f32 per trip), nothing stored (`out`,
+ * nblocks x 256 floats, is written only in a case the inputs never reach). The VALU yardstick of the
+ * searches' roof, as spa_copy is HBM's. spa_valu_probe_insts: the loop's wave64 VALU instructions per
+ * launch. No reference counterpart. */
+int spa_valu_probe(int op, int64_t nblocks, int iters, float* out, void* stream);
+int64_t spa_valu_probe_insts(int op, int64_t nblocks, int iters);
 /* n synthetic BF16 weights N(0, std) written in place from a counter-based hash of (seed, index), for
  * benchmark inputs generated on the device. No reference counterpart. */
 int spa_synth_normal_bf16(void* dst, int64_t n, uint64_t seed, float std, void* stream);
@@ -220,13 +229,24 @@ int spa_diff_count(const void* a, const void* b, size_t n, unsigned long long* c
  * :1940), taken on the device-resident residual. */
 int spa_count_every(const void* a, size_t n, size_t stride, unsigned long long* count, void* stream);
 
-/* 128-bit content hashes of nregions byte regions of `base` (the keys by which a tensor is found equal
- * to one of an earlier file; they replace the blake3 digests of repo3.py:1029 / :2018-2022 as those
- * keys). desc (device, u64): offset and length of each region; out (device, u64): two words per region,
- * sum over the region's 8-byte little-endian words w_p (the last zero-padded) of
- * fmix64(w_p ^ fmix64(p * 0x9e3779b97f4a7c15 + s)) for s = 0x243f6a8885a308d3 and 0x13198a2e03707344
- * (fmix64: MurmurHash3's 64-bit finaliser); equal keys also need equal lengths. */
-int spa_content_hash(const void* base, const uint64_t* desc, int nregions, unsigned long long* out, void* stream);
+/* BLAKE3 (default hash mode, 32-byte digests) of nregions byte regions of the device buffer `base`:
+ * the reference's file checksum (cli.py:34-39, its catalog's "hash": "blake3") and tensor keys
+ * (repo3.py:529, :1029, :2018-2022; siblings.py:216-240), which it computes with the blake3 package on
+ * the host. regions (host, u64): offset and length of each region; work (device) of
+ * spa_blake3_work_bytes(regions, nregions) bytes; digests (host): 32 bytes per region. Synchronous:
+ * returns when the digests are in `digests` (the stream's earlier work is waited for). */
+size_t spa_blake3_work_bytes(const uint64_t* regions, int nregions);
+int spa_blake3(const void* base, const uint64_t* regions, int nregions, void* work, size_t work_bytes, uint8_t* digests,
+               void* stream);
+
+/* BLAKE3 of host data fed in pieces (the reference's blake3.blake3(...).update / hexdigest, used
+ * where a file is checked as it is written): spa_b3h_new, then spa_b3h_update with each piece in
+ * order (the whole chunks of a large piece hashed on up to `threads` threads), spa_b3h_final for the
+ * 32-byte digest (the state is left as it was), spa_b3h_free. A hasher is not shared between threads. */
+int spa_b3h_new(void** h);
+int spa_b3h_update(void* h, const void* data, size_t n, int threads);
+int spa_b3h_final(void* h, uint8_t* out32);
+int spa_b3h_free(void* h);
 
 /* Float-tensor prediction from the base weights (src_kind SPA_SRC_*): n values written as the file's
  * type dst_type = 0 (F32), 1 (F16, round to nearest even) or 30 (BF16, (u + 0x7FFF + ((u >> 16) & 1))

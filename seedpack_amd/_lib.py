@@ -41,6 +41,8 @@ SIGNATURES = {
     "spa_event_elapsed_ms": (c_int, [ctypes.POINTER(c_float), c_void_p, c_void_p]),
     "spa_mem_info": (c_int, [ctypes.POINTER(c_size_t), ctypes.POINTER(c_size_t)]),
     "spa_copy": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "spa_valu_probe": (c_int, [c_int, c_int64, c_int, c_void_p, c_void_p]),
+    "spa_valu_probe_insts": (c_int64, [c_int, c_int64, c_int]),
     "spa_synth_normal_bf16": (c_int, [c_void_p, c_int64, c_uint64, c_float, c_void_p]),
     "spa_perturb_blocks": (c_int, [c_void_p, c_int64, c_int, ctypes.c_uint32, c_uint64, c_void_p]),
     "spa_dequantize": (c_int, [c_int, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
@@ -121,7 +123,12 @@ SIGNATURES = {
     "spa_est_half_step": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "spa_est_add": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
     "spa_est_seed": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
-    "spa_content_hash": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "spa_blake3_work_bytes": (c_size_t, [c_void_p, c_int]),
+    "spa_blake3": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "spa_b3h_new": (c_int, [ctypes.POINTER(c_void_p)]),
+    "spa_b3h_update": (c_int, [c_void_p, c_void_p, c_size_t, c_int]),
+    "spa_b3h_final": (c_int, [c_void_p, c_void_p]),
+    "spa_b3h_free": (c_int, [c_void_p]),
     "spa_float_pred": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p]),
     "spa_r2_stats": (c_int, [c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p,
                              c_void_p]),

@@ -22,7 +22,7 @@ namespace m24 {
 namespace {
 
 constexpr uint32_t PB = 12, PSCALE = 1u << PB, RANS_L = 1u << 23;
-constexpr int SEG = 16384, TPT = 160, EWIN = 32;
+constexpr int SEG = 16384, EWIN = 32;
 
 struct TB { int64_t off; int32_t rowlen, rowbase, colbase, tab; };      // gpu_bf16.py:271 TB_DT
 struct SG { int32_t t, n; int64_t i0; };                                // gpu_bf16.py:272 SG_DT

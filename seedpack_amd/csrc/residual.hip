@@ -80,58 +80,6 @@ __global__ __launch_bounds__(WG) void k_count_every(const uint8_t* a, int64_t n,
     add_count(count, cnt);
 }
 
-// Content hash of byte regions (the keys by which a tensor is found equal to one of an earlier
-// file). Word p (8 bytes, little-endian, the last one zero-padded) of a region contributes
-// fmix64(w ^ fmix64(p * K + s)) to each of two 64-bit sums (s = the two seeds); the region's hash is
-// (sum0, sum1) with its length beside it. fmix64 (MurmurHash3's 64-bit finaliser) is a bijection
-// with full avalanche, so each contribution is pseudo-random in (w, p) and the sums are order-
-// and position-sensitive; integer sums make the result independent of how the work is split.
-__device__ __forceinline__ uint64_t fmix64(uint64_t k) {
-    k ^= k >> 33;
-    k *= 0xff51afd7ed558ccdull;
-    k ^= k >> 33;
-    k *= 0xc4ceb9fe1a85ec53ull;
-    k ^= k >> 33;
-    return k;
-}
-constexpr uint64_t HASH_K = 0x9e3779b97f4a7c15ull;
-constexpr uint64_t HASH_S0 = 0x243f6a8885a308d3ull, HASH_S1 = 0x13198a2e03707344ull;
-constexpr int HASH_BLOCKS = 64;                 // workgroups per region
-
-__device__ __forceinline__ void add_u64(unsigned long long* p, uint64_t c) {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) c += __shfl_xor(c, m, 64);
-    if ((threadIdx.x & 63) == 0) atomicAdd(p, (unsigned long long)c);
-}
-
-__global__ void k_zero_n(unsigned long long* p, int n) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
-}
-
-// grid (HASH_BLOCKS, regions): desc[2 r] = offset, desc[2 r + 1] = length of region r within base
-__global__ __launch_bounds__(WG) void k_hash(const uint8_t* base, const uint64_t* desc, unsigned long long* out) {
-    const int r = blockIdx.y;
-    const uint8_t* p = base + desc[2 * r];
-    const int64_t n = (int64_t)desc[2 * r + 1];
-    const int64_t words = (n + 7) / 8, full = n / 8;
-    const bool al = (reinterpret_cast<uintptr_t>(p) & 7u) == 0;
-    uint64_t h0 = 0, h1 = 0;
-    for (int64_t i = (int64_t)blockIdx.x * WG + threadIdx.x; i < words; i += (int64_t)HASH_BLOCKS * WG) {
-        uint64_t w = 0;
-        if (al && i < full) {
-            w = reinterpret_cast<const uint64_t*>(p)[i];
-        } else {
-            const int64_t e = n - 8 * i < 8 ? n - 8 * i : 8;
-            for (int b = 0; b < e; ++b) w |= (uint64_t)p[8 * i + b] << (8 * b);
-        }
-        const uint64_t k = (uint64_t)i * HASH_K;
-        h0 += fmix64(w ^ fmix64(k + HASH_S0));
-        h1 += fmix64(w ^ fmix64(k + HASH_S1));
-    }
-    add_u64(out + 2 * r, h0);
-    add_u64(out + 2 * r + 1, h1);
-}
-
 // float prediction: source weights (BF16 bits, F16, F32) -> bytes of the file's float type:
 // F32 as is, F16 by round-to-nearest-even (the astype of repo3.py:685), BF16 by
 // (u + 0x7FFF + ((u >> 16) & 1)) >> 16. A NaN goes to F16 as numpy's conversion (the reference's
@@ -237,17 +185,6 @@ int spa_count_every(const void* a, size_t n, size_t stride, unsigned long long* 
         hipLaunchKernelGGL(spa::k_count_every, dim3(spa::grid_for(m)), dim3(spa::WG), 0, st, (const uint8_t*)a, (int64_t)n,
                            (int64_t)stride, count);
     }
-    SPA_HIP_TRY(hipGetLastError());
-    return SPA_OK;
-}
-
-int spa_content_hash(const void* base, const uint64_t* desc, int nregions, unsigned long long* out, void* stream) {
-    if (nregions < 0 || nregions > 65535) return fail(SPA_ERR_ARG, "spa_content_hash: %d regions (0..65535)", nregions);
-    if (!nregions) return SPA_OK;
-    if (!base || !desc || !out) return fail(SPA_ERR_ARG, "spa_content_hash: null pointer");
-    hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(spa::k_zero_n, dim3((2 * nregions + spa::WG - 1) / spa::WG), dim3(spa::WG), 0, st, out, 2 * nregions);
-    hipLaunchKernelGGL(spa::k_hash, dim3(spa::HASH_BLOCKS, nregions), dim3(spa::WG), 0, st, (const uint8_t*)base, desc, out);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
 }

@@ -48,11 +48,12 @@ import re
 import resource
 import threading
 import time
-from concurrent.futures import ThreadPoolExecutor, wait as futures_wait
+import warnings
+from concurrent.futures import Future, ThreadPoolExecutor, wait as futures_wait
 
 import numpy as np
 
-from . import container, device as dev, gguf, header, imatrix as imx_mod, imxfit, qr, r2, residual, zstd
+from . import blake3, container, device as dev, gguf, header, imatrix as imx_mod, imxfit, qr, r2, residual, zstd
 from ._lib import check, lib
 from .framing import index, nbytes, pack, pack_parts, unpack
 from .gpuquant import GPUQuant
@@ -66,6 +67,8 @@ METHODS = {"m29": METHOD,                                            # the archi
            "m28": "M28 model repo: BF16 + quants re-derived on the GPU with llama.cpp quantisers + imatrix",   # repo3.py:585-586
            "m30": "M30 sibling quants: tensor versions coded in chains, no base"}                           # siblings.py:168
 TOOL = "seedpack 0.5.0"              # the program whose archives these are byte-for-byte (cli.py:31)
+READS = (0, 5, 0)                    # the newest "needs" of a manifest this reader accepts (__init__.py:6)
+HASHES = ("sha256", "blake3")        # catalog checksums this reader computes (cli.py:34-39)
 WINDOW = 1 << 30                     # base bytes per window (repo3.py:1672)
 PRED_WINDOW = 3 << 30                # first predictions per window, bytes (repo3.py:1677)
 DUP_MIN = 64 << 10                   # smaller tensors are not made references (repo3.py:1024)
@@ -309,9 +312,9 @@ def _write_file(path, mv, pool, step=64 << 20):
         os.close(fd)
 
 
-def file_sha256(path, chunk=64 << 20):
-    """SHA-256 of a file, read in pieces into a buffer of its own"""
-    h = hashlib.sha256()
+def file_digest(path, algo="sha256", chunk=64 << 20):
+    """the catalog checksum (SHA-256 or BLAKE3) of a file, read in pieces into a buffer of its own"""
+    h = _stream_hash(algo)
     buf = np.empty(chunk, np.uint8)
     fd = os.open(path, os.O_RDONLY)
     try:
@@ -494,6 +497,63 @@ def _ws(n):
     return hashlib.sha256(memoryview(n).cast("B")).hexdigest()
 
 
+def _done(v):
+    """a finished future holding v"""
+    f = Future()
+    f.set_result(v)
+    return f
+
+
+def _digest_fn(algo):
+    """the catalog's checksum of a host buffer (cli.py:34-39): SHA-256, or BLAKE3 on host threads"""
+    if algo == "blake3":
+        return lambda n: blake3.hexdigest(memoryview(n).cast("B"))
+    return _ws
+
+
+def _stream_hash(algo):
+    """an incremental hasher (update / hexdigest) of the catalog's algorithm"""
+    return blake3.Hasher() if algo == "blake3" else hashlib.sha256()
+
+
+def check_archive(meta, manifest, verify=True):
+    """what the reader refuses before it decodes anything -> the catalog's hash algorithm, or None
+    (files extracted unchecked: only with verify=False and a warning).
+
+    An archive whose manifest needs a newer reader than the version whose archives these are is
+    refused (repo3.py:2285-2289); so is a catalog whose hash is neither SHA-256 nor BLAKE3, the two
+    the reference writes (cli.py:34-53), unless the caller opts out of verification."""
+    needs = manifest.get("needs")
+    if needs:
+        try:
+            want = tuple(int(x) for x in str(needs).split("."))
+        except ValueError:
+            raise container.FormatError(f"the archive's manifest needs version {needs!r}, which is not a version number")
+        if want > READS:
+            raise container.FormatError(f"this archive needs SeedPack {needs} or newer (this reader reads the archives "
+                                        f"of {'.'.join(map(str, READS))})")
+    algo = meta.get("hash")
+    if algo in HASHES:
+        return algo
+    if verify:
+        raise container.FormatError(f"the archive's catalog hash is {algo!r}; this reader checks files with "
+                                    f"{' or '.join(HASHES)} (pass verify=False to extract without checking)")
+    warnings.warn(f"catalog hash {algo!r} is not one this reader computes: files are extracted unchecked")
+    return None
+
+
+def open_archive(path, verify=True):
+    """the archive's reader, catalog (meta), manifest and checksum algorithm, after the checks of
+    check_archive (nothing is decoded or written before they pass)"""
+    r = container.Reader(path)
+    try:
+        manifest = json.loads(zstd.decompress(r.get("manifest")))
+        return r, r.meta, manifest, check_archive(r.meta, manifest, verify)
+    except Exception:
+        r.close()
+        raise
+
+
 # ------------------------------------------------------------------ packing
 
 class Packer:
@@ -502,8 +562,13 @@ class Packer:
     files"""
 
     def __init__(self, level=7, verbose=False, coders=8, zstd_lanes=14, staging_bytes=24 << 30, device_bytes=None,
-                 method="m29", m30_slice=None, bases_in_hbm=None):
+                 method="m29", m30_slice=None, bases_in_hbm=None, hash_algo="blake3"):
         self.m30_slice = m30_slice
+        # the catalog's checksum: BLAKE3, the reference's whenever its blake3 requirement is installed
+        # (cli.py:48-53), or SHA-256, its fallback; derived files and bases in HBM are hashed there
+        if hash_algo not in HASHES:
+            raise ValueError(f"catalog hash {hash_algo!r} (one of {', '.join(HASHES)})")
+        self.hash_algo, self._digest = hash_algo, _digest_fn(hash_algo)
         # the BF16 bases in HBM (True), read window by window from host memory (False), or in HBM
         # when they fit beside the largest derived file and RESERVE (None)
         self.bases_in_hbm = bases_in_hbm
@@ -608,10 +673,10 @@ class Packer:
         self._cpu(("qr batches", 1), ("qr coder cpu_s", c1 - c0), ("qr tables+lens zstd-19 cpu_s", time.thread_time() - c1))
         return out
 
-    def _sha256(self, buf):
+    def _checksum(self, buf):
         c0 = time.thread_time()
-        h = _ws(buf)
-        self._cpu(("sha256 cpu_s", time.thread_time() - c0))
+        h = self._digest(buf)
+        self._cpu(("checksum cpu_s", time.thread_time() - c0))
         return h
 
     def _cpu(self, *items):
@@ -630,7 +695,8 @@ class Packer:
         t2 = time.perf_counter()
         self._cpu(("file reads wall_s", t2 - t1))
         job["host"] = host
-        job["sha256"] = self.hasher.submit(self._sha256, host)
+        # SHA-256 on a host thread from the staged bytes; BLAKE3 on the device once they are uploaded
+        job["sum"] = self.hasher.submit(self._checksum, host) if self.hash_algo == "sha256" else None
         job["read"] = {"staging": round(t1 - t0, 3), "read": round(t2 - t1, 3)}
         return job
 
@@ -648,9 +714,12 @@ class Packer:
         st = self.stream.handle
         check(lib().spa_memcpy_h2d(F.ptr, host.ctypes.data, size, st))
         tm["upload"] = time.perf_counter()
-        # the predicted tensors' content keys, hashed on the device before anything changes them
+        if job["sum"] is None:
+            job["sum"] = _done(blake3.device_digests(F, [(0, size)], st)[0].hex())
+        # the predicted tensors' keys, their BLAKE3 digests as the reference keys them (repo3.py:2018-2022),
+        # hashed on the device before anything changes them
         thash = dict(zip([t.name for t, _ in pred],
-                         residual.content_hashes(F, [(t.offset, t.nbytes) for t, _ in pred], st)))
+                         blake3.device_digests(F, [(t.offset, t.nbytes) for t, _ in pred], st)))
         # references: equal to a tensor an earlier file of the same window left a residual in
         refs, mine = {}, []
         for t, k in pred:
@@ -731,7 +800,7 @@ class Packer:
         self.stats["qr"] += sum(len(m[1]) for m in qmeta)
         self.stream.synchronize()
         # the staged bytes go back once the checksum has read them too
-        job["sha256"].add_done_callback(lambda _, h=job.pop("host"): self.pool.release(h))
+        job["sum"].add_done_callback(lambda _, h=job.pop("host"): self.pool.release(h))
         entry = {"name": job["name"], "size": size, "base": b.index, "plan": plan}
         return {"fi": fi, "F": F, "qjobs": qjobs, "qmeta": qmeta, "qregs": qregs,
                 "span": self._zspan(pred, wins_of, job["last_window"], size), "entry": entry, "zdict": b.header,
@@ -952,13 +1021,13 @@ class Packer:
             aux = ThreadPoolExecutor(1)
             ex = {n: open(p, "rb").read() for n, p in small.items()}
             for n, data in ex.items():
-                hashes[n] = self.hasher.submit(_ws, data)
+                hashes[n] = self.hasher.submit(self._digest, data)
             later = {"other files": aux.submit(lambda: lzma.compress(pack(ex), preset=9))}
             w.put_later("extras", later["other files"])
             big = {}
             for j, (n, p) in enumerate((n, p) for n, p in extras.items() if n not in small):
                 data = open(p, "rb").read()
-                hashes[n] = self.hasher.submit(_ws, data)
+                hashes[n] = self.hasher.submit(self._digest, data)
                 later[n] = aux.submit(zstd.compress_with, data, zstd.Params(self.level, threads=8, ldm=True))
                 w.put_later(f"x{j}", later[n])
                 big[n] = [f"x{j}", len(data)]
@@ -1065,8 +1134,11 @@ class Packer:
                     for i, s_ in j["parts"]:
                         place[i] = d.view(s_, (bsize[i],), np.uint8)
             for (host, b), (n, p) in zip(loaded, bases.items()):
-                hashes[n] = self.hasher.submit(file_sha256, p)
                 b.d = self._load_base(p, into=place.get(b.index)) if in_hbm or b.seed else None
+                if b.d is not None and self.hash_algo == "blake3":
+                    hashes[n] = blake3.device_hexdigest(b.d, stream=self.stream.handle)
+                else:
+                    hashes[n] = self.hasher.submit(file_digest, p, self.hash_algo)
                 base_jobs.append(side.submit(self._code_base, b, host, "stream" if b.index == 0 else "parts"))
                 later[n] = base_jobs[-1]
             if base_jobs:
@@ -1086,8 +1158,8 @@ class Packer:
                 job = ahead.result()
                 ahead = self.reader.submit(self._read_file, jobs[porder[k + 1]]) if k + 1 < len(porder) else None
                 b = allb[job["base"]]
-                hashes[names[fi]] = job["sha256"]
                 state = self._device_file(job, b, imx_dev, imx_off, imx_map)
+                hashes[names[fi]] = job["sum"]            # (BLAKE3: computed on the device by _device_file)
                 zjobs[fi] = self.zpool.submit(self._finish_file, state)
                 log(self.verbose, f"  {state['entry']['name']}: {state['entry']['size']:,} B regrown and compared in "
                                   f"{state['tm']['regrow'] - state['tm']['t0']:.2f} s")
@@ -1096,14 +1168,14 @@ class Packer:
                 # nothing to predict: the file zstd'd against the base header (repo3.py:2062-2076)
                 b = allb[bi]
                 data = open(derived[n], "rb").read()
-                hashes[n] = self.hasher.submit(_ws, data)
+                hashes[n] = self.hasher.submit(self._digest, data)
                 entries[fi] = {"name": n, "size": len(data), "base": b.index, "plan": []}
                 zjobs[fi] = self.zpool.submit(lambda e, d, h: (e, None, zstd.compress_with(
                     d, _zc_params(self.level, d), h)), entries[fi], data, b.header)
                 order_done.append(fi)
             for fi, n, ts in alone:
                 data = open(derived[n], "rb").read()
-                hashes[n] = self.hasher.submit(_ws, data)
+                hashes[n] = self.hasher.submit(self._digest, data)
                 entries[fi] = {"name": n, "size": len(data), "base": None, "plan": []}
                 zjobs[fi] = self.zpool.submit(self._code_alone, entries[fi], data, ts)
                 order_done.append(fi)
@@ -1137,12 +1209,15 @@ class Packer:
                 manifest["needs"] = "0.3.0"
             w.put("manifest", zstd.compress(json.dumps(manifest).encode(), 19))
             hashes = {n: (h.result() if hasattr(h, "result") else h) for n, h in hashes.items()}
+            missing = [n for n in files if not hashes.get(n)]
+            if missing:
+                raise RuntimeError(f"no checksum for {missing[:3]}")
             phase("checksums")
             q8_files = {e["name"] for e in entries if e and e.get("codec") == "q8"}
             catalog = [{"name": n, "size": os.path.getsize(p), "hash": hashes[n],
                         "role": "derived, M21" if n in q8_files else roles[n] or "file",
                         "stored": self.sizes.get(n)} for n, p in files.items()]
-            w.close({"tool": tool, "method": METHODS[self.method], "created": created or _created(), "hash": "sha256",
+            w.close({"tool": tool, "method": METHODS[self.method], "created": created or _created(), "hash": self.hash_algo,
                      "files": catalog, "total": total})
         except BaseException:
             w.abort()
@@ -1164,7 +1239,7 @@ class Packer:
         """method m30 (siblings.M30Siblings): every GGUF's tensors as version chains"""
         from .siblings import M30Siblings
         for n, p in ggufs.items():
-            hashes[n] = self.hasher.submit(file_sha256, p)
+            hashes[n] = self.hasher.submit(file_digest, p, self.hash_algo)
         from .siblings import SLICE
         m = M30Siblings(slice_weights=self.m30_slice or SLICE, stream=self.stream.handle, verbose=self.verbose)
         man = m.compress(ggufs, w.put)
@@ -1178,7 +1253,7 @@ class Packer:
         hashes = {n: (h.result() if hasattr(h, "result") else h) for n, h in hashes.items()}
         catalog = [{"name": n, "size": os.path.getsize(p), "hash": hashes[n], "role": roles[n] or "file",
                     "stored": self.sizes.get(n)} for n, p in files.items()]
-        w.close({"tool": tool, "method": METHODS[self.method], "created": created or _created(), "hash": "sha256",
+        w.close({"tool": tool, "method": METHODS[self.method], "created": created or _created(), "hash": self.hash_algo,
                  "files": catalog, "total": total})
 
     @staticmethod
@@ -1232,8 +1307,9 @@ class Unpacker:
     the host, uploaded, its predictions regrown and XORed in and its QR batches decoded on the device,
     then read back, checked and written"""
 
-    def __init__(self, verbose=False, staging_bytes=64 << 30, bases_in_hbm=None):
+    def __init__(self, verbose=False, staging_bytes=64 << 30, bases_in_hbm=None, verify=True):
         self.verbose = verbose
+        self.verify = verify                      # False: a catalog hash not computed here is a warning
         # the bases decoded into HBM (True), decoded window by window from the archive (False), or
         # in HBM when they fit beside the largest file to rebuild and 48 GB (None)
         self.bases_in_hbm = bases_in_hbm
@@ -1248,11 +1324,10 @@ class Unpacker:
 
     def run(self, archive, outdir=None, patterns=None):
         t0 = time.perf_counter()
-        r = container.Reader(archive)
-        meta = r.meta
-        manifest = json.loads(zstd.decompress(r.get("manifest")))
+        r, meta, manifest, algo = open_archive(archive, self.verify)
+        digest = _digest_fn(algo) if algo else None
         if manifest["method"].startswith("M30"):
-            return self._run_m30(r, meta, manifest, outdir, patterns, t0)
+            return self._run_m30(r, meta, manifest, outdir, patterns, t0, digest)
         if not manifest["method"].startswith(("M29", "M28")):
             raise NotImplementedError(f"archive method {manifest['method']!r}: only M28 / M29 / M30 archives are read here")
         seeds = set(manifest.get("seeds", []))
@@ -1276,20 +1351,20 @@ class Unpacker:
                  {mf[i]["base"] for i in sel if mf[i]["base"] is not None}
         results, jobs = {}, []
 
-        def check_write(name, buf, release=False):
-            """the file's checksum and its write side by side; a file that fails its checksum is
-            not left behind"""
+        def check_write(name, buf, release=False, known=None):
+            """the file's checksum (`known`: already computed on the device) and its write side by
+            side; a file that fails its checksum is not left behind"""
             try:
                 mv = memoryview(buf).cast("B")
-                h = self.hasher.submit(_ws, mv)
+                h = self.hasher.submit(lambda: known) if known else self.hasher.submit(digest, mv) if digest else None
                 path = None
                 if outdir is not None:
                     path = os.path.join(outdir, *name.split("/"))
                     os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
                     _write_file(path + ".part", mv, self.io)
-                ok = h.result() == cat[name]["hash"] and mv.nbytes == cat[name]["size"]
+                ok = mv.nbytes == cat[name]["size"] and (h.result() == cat[name]["hash"] if h else None)
                 if path is not None:
-                    if ok:
+                    if ok is not False:
                         os.replace(path + ".part", path)
                     else:
                         os.remove(path + ".part")
@@ -1301,7 +1376,7 @@ class Unpacker:
 
         def stream_write(name, rt):
             """a base decoded window by window (R2Tensors.write_to) into its file, checksummed on the way"""
-            h, n = hashlib.sha256(), [0]
+            h, n = _stream_hash(algo) if algo else None, [0]
             path = None if outdir is None else os.path.join(outdir, *name.split("/"))
             f = None
             if path is not None:
@@ -1313,7 +1388,8 @@ class Unpacker:
                     # the file write beside the checksum (both release the interpreter lock)
                     mv = memoryview(np.ascontiguousarray(b_)).cast("B")
                     fw = wpool.submit(f.write, mv) if f is not None else None
-                    h.update(mv)
+                    if h is not None:
+                        h.update(mv)
                     n[0] += mv.nbytes
                     if fw is not None:
                         fw.result()
@@ -1322,9 +1398,9 @@ class Unpacker:
                 wpool.shutdown()
                 if f is not None:
                     f.close()
-            ok = h.hexdigest() == cat[name]["hash"] and n[0] == cat[name]["size"]
+            ok = n[0] == cat[name]["size"] and (h.hexdigest() == cat[name]["hash"] if h is not None else None)
             if path is not None:
-                if ok:
+                if ok is not False:
                     os.replace(path + ".part", path)
                 else:
                     os.remove(path + ".part")
@@ -1467,8 +1543,9 @@ class Unpacker:
             bases[i] = b
             if name in want:
                 host = self.pool.acquire(d.nbytes)[:d.nbytes]
+                known = blake3.device_hexdigest(d, stream=self.stream.handle) if algo == "blake3" else None
                 check(lib().spa_memcpy_d2h(host.ctypes.data, d.ptr, d.nbytes, self.stream.handle))
-                jobs.append(self.files.submit(check_write, name, host, True))
+                jobs.append(self.files.submit(check_write, name, host, True, known))
             log(self.verbose, f"  base {name}: decoded, {time.perf_counter() - t0:.1f} s")
         for k, j in enumerate(joined):
             if nb + k in need_b:
@@ -1483,12 +1560,13 @@ class Unpacker:
             tw = time.perf_counter() - tf
             if k + 2 < len(order):
                 ahead[k + 2] = self.ahead.submit(residual_of, order[k + 2])
-            tm = {}
+            tm, known = {}, None
             if m["plan"]:
-                tm = self._rebuild(r, i, m, bases[m["base"]], resid, kept, users, done, imx_dev, imx_off, imx_map)
+                tm, known = self._rebuild(r, i, m, bases[m["base"]], resid, kept, users, done, imx_dev, imx_off,
+                                          imx_map, algo == "blake3" and m["name"] in want)
             done.add(i)
             if m["name"] in want:
-                jobs.append(self.files.submit(check_write, m["name"], resid, True))
+                jobs.append(self.files.submit(check_write, m["name"], resid, True, known))
             else:
                 self.pool.release(resid)
             log(self.verbose, f"  {m['name']}: {m['size']:,} B in {time.perf_counter() - tf:.2f} s (residual wait "
@@ -1498,11 +1576,12 @@ class Unpacker:
         r.close()
         dt = time.perf_counter() - t0
         nbytes_ = sum(cat[n]["size"] for n in results)
-        return {"files": results, "bad": [n for n, ok in results.items() if not ok],
+        return {"files": results, "bad": [n for n, ok in results.items() if ok is False],
+                "unchecked": [n for n, ok in results.items() if ok is None],
                 "missing": [n for n in want if n not in results], "bytes": nbytes_, "seconds": dt,
                 "GB_s": nbytes_ / dt / 1e9}
 
-    def _run_m30(self, r, meta, manifest, outdir, patterns, t0):
+    def _run_m30(self, r, meta, manifest, outdir, patterns, t0, digest):
         """an M30 archive: the extras, then the GGUF files rebuilt from their tensor chains"""
         from .siblings import M30Siblings
         cat = {f["name"]: f for f in meta["files"]}
@@ -1510,8 +1589,8 @@ class Unpacker:
         results = {}
 
         def sink(name, buf):
-            ok = _ws(buf) == cat[name]["hash"] and len(buf) == cat[name]["size"]
-            if ok and outdir is not None:
+            ok = len(buf) == cat[name]["size"] and (digest(buf) == cat[name]["hash"] if digest else None)
+            if ok is not False and outdir is not None:
                 path = os.path.join(outdir, *name.split("/"))
                 os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
                 _write_file(path, memoryview(np.ascontiguousarray(buf)).cast("B"), self.io)
@@ -1529,7 +1608,8 @@ class Unpacker:
         r.close()
         dt = time.perf_counter() - t0
         nbytes_ = sum(cat[n]["size"] for n in results)
-        return {"files": results, "bad": [n for n, ok in results.items() if not ok],
+        return {"files": results, "bad": [n for n, ok in results.items() if ok is False],
+                "unchecked": [n for n, ok in results.items() if ok is None],
                 "missing": [n for n in want if n not in results], "bytes": nbytes_, "seconds": dt,
                 "GB_s": nbytes_ / dt / 1e9}
 
@@ -1550,8 +1630,9 @@ class Unpacker:
                     sets[k][n] = e
         return sets
 
-    def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map):
-        """file i's bytes from its residual (in `resid`, rebuilt in place) on the device"""
+    def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map, digest=False):
+        """file i's bytes from its residual (in `resid`, rebuilt in place) on the device -> (phase
+        times, the file's BLAKE3 hex digest computed on the device when `digest`, else None)"""
         st = self.stream.handle
         size = m["size"]
         tm, t_ = {}, [time.perf_counter()]
@@ -1627,9 +1708,10 @@ class Unpacker:
                 a = dev.DeviceArray(t.nbytes, np.uint8)
                 check(lib().spa_memcpy_d2d(a.ptr, R.ptr + t.offset, t.nbytes, st))
                 kept[(fi, name)] = a
+        known = blake3.device_digests(R, [(0, size)], st)[0].hex() if digest else None
         check(lib().spa_memcpy_d2h(resid.ctypes.data, R.ptr, size, st))
         lap("download")
-        return tm
+        return tm, known
 
 
 def unpack_repo(archive, outdir=None, patterns=None, verbose=False):

@@ -114,18 +114,6 @@ def diff_count(a, b=None, stream=None):
     return c.value(stream)
 
 
-def content_hashes(base, regions, stream=None):
-    """128-bit content hashes (spa_content_hash) of the byte regions [(offset, length)] of the device
-    array `base` -> [(h0, h1)]"""
-    if not regions:
-        return []
-    desc = dev.DeviceArray.from_host(np.array(regions, np.uint64).reshape(-1), stream)
-    out = dev.DeviceArray(2 * len(regions), np.uint64)
-    check(lib().spa_content_hash(base.ptr, desc.ptr, len(regions), out.ptr, stream))
-    h = out.to_host(stream=stream).reshape(-1, 2)
-    return [(int(a), int(b)) for a, b in h]
-
-
 def float_prediction(src, t_type, stream=None):
     """a float file tensor's prediction from the base weights src (DeviceArray of bf16 bits / f16 /
     f32) as the bytes of type t_type (F32, F16 or BF16)"""

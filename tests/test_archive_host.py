@@ -2,6 +2,7 @@
 reader, zstd with parameters and dictionaries, and the base codec's header ("rest") coder against the
 reference's own output (tests/golden/header_vectors.npz, written by make_r2_golden.py --header)."""
 import hashlib
+import json
 import os
 import struct
 import zlib
@@ -284,3 +285,65 @@ def test_framing_index_reads_only_the_framing():
     bad[-11] = 99                              # the length of "a"
     with pytest.raises(ValueError):
         framing.index(lambda o, n: bytes(bad[o:o + n]), len(bad))
+
+
+def _container(path, meta, manifest):
+    w = container.Writer(path)
+    w.put("f0", b"\0" * 16)
+    w.put("manifest", zstd.compress(json.dumps(manifest).encode(), 19))
+    w.close(meta)
+
+
+@pytest.mark.parametrize("needs,ok", [(None, True), ("0.3.0", True), ("0.5.0", True), ("0.5.1", False),
+                                      ("1.0", False), ("x.y", False)])
+def test_reader_refuses_newer_archives(tmp_path, needs, ok):
+    """a manifest that needs a newer reader is refused before anything is decoded (repo3.py:2285-2289)"""
+    from seedpack_amd import repo
+    p = str(tmp_path / "a.seedpack")
+    man = {"method": repo.METHOD, "files": [], "bases": []}
+    if needs is not None:
+        man["needs"] = needs
+    _container(p, {"hash": "blake3", "files": []}, man)
+    if ok:
+        r, meta, m2, algo = repo.open_archive(p)
+        r.close()
+        assert algo == "blake3" and m2 == man
+    else:
+        with pytest.raises(container.FormatError, match="needs"):
+            repo.open_archive(p)
+
+
+@pytest.mark.parametrize("algo", ["sha256", "blake3", "md5", None])
+def test_reader_checks_the_catalog_hash(tmp_path, algo):
+    """a catalog whose checksum this reader cannot compute is refused before decoding, unless the
+    caller opts out of verification (then a warning, and files go unchecked)"""
+    from seedpack_amd import repo
+    p = str(tmp_path / "a.seedpack")
+    meta = {"files": []} if algo is None else {"hash": algo, "files": []}
+    _container(p, meta, {"method": repo.METHOD, "files": [], "bases": []})
+    if algo in repo.HASHES:
+        r, _, _, got = repo.open_archive(p)
+        r.close()
+        assert got == algo
+        return
+    with pytest.raises(container.FormatError, match="catalog hash"):
+        repo.open_archive(p)
+    with pytest.warns(UserWarning, match="unchecked"):
+        r, _, _, got = repo.open_archive(p, verify=False)
+    r.close()
+    assert got is None
+
+
+def test_catalog_digests_of_files(tmp_path):
+    """file checksums as the catalog writes them: SHA-256 and BLAKE3 of a file read in pieces equal
+    the one-shot digests (BLAKE3 pinned to published vectors by test_blake3.py)"""
+    import hashlib
+    from oracle import blake3 as ob
+    from seedpack_amd import repo
+    g = np.random.Generator(np.random.PCG64(9))
+    data = g.integers(0, 256, 3 * 1024 + 5, dtype=np.uint8).tobytes()
+    p = tmp_path / "f.bin"
+    p.write_bytes(data)
+    assert repo.file_digest(str(p), "sha256", chunk=1000) == hashlib.sha256(data).hexdigest()
+    assert repo.file_digest(str(p), "blake3", chunk=1000) == ob.hexdigest(data)
+    assert repo._digest_fn("blake3")(data) == ob.hexdigest(data)

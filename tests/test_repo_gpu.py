@@ -3,7 +3,7 @@ Qwen-shaped repository (BF16 base with a BPE tokenizer, imatrix, 21 quantized GG
 base with 1% of their blocks changed, a small extra file) packed into a .seedpack archive and
 extracted again.
 
-Checked: every file extracts byte-identical and passes its SHA-256 (so every QR batch of every file
+Checked: every file extracts byte-identical and passes its checksum (so every QR batch of every file
 decodes back); the container, manifest and chunks follow the reference's layout; the base's header
 part takes the tokenizer-aware form; for every QR type, one batch of the archive equals the oracle's
 stream for the same tensors (oracle/qr.py's per-tensor histograms summed into the batch's tables,
@@ -69,6 +69,65 @@ def test_small_repo_extracts_byte_identical(small_repo, tmp_path):
     assert not res["bad"] and not res["missing"], res
     for n in names:
         assert open(os.path.join(root, n), "rb").read() == open(os.path.join(out2, n), "rb").read(), n
+
+
+def _rewrite(src, dst, meta=None, manifest=None):
+    """a copy of archive src with its catalog (meta) and / or manifest replaced"""
+    r = container.Reader(src)
+    w = container.Writer(dst)
+    for name in r.chunks:
+        if name == "manifest" and manifest is not None:
+            w.put(name, zstd.compress(json.dumps(manifest).encode(), 19))
+        else:
+            w.put(name, bytes(r.get(name)))
+    w.close(meta if meta is not None else r.meta)
+    r.close()
+
+
+def test_small_repo_catalog_hash_and_gates(small_repo, tmp_path):
+    """the catalog holds BLAKE3 digests (the reference's checksum when its blake3 requirement is
+    installed, cli.py:48-53), computed on the device for the base and the derived files: each equals
+    the host hasher's. An archive whose manifest needs a newer reader, or whose catalog names a
+    checksum this reader does not compute, is refused before any file is written (with verify=False
+    the latter extracts unchecked). A SHA-256 catalog (hash_algo="sha256") has the same chunks and
+    extracts checked."""
+    import hashlib
+    from seedpack_amd import blake3
+    root, arc, sizes, stats = small_repo
+    say("case repo small: catalog hash and reader gates")
+    r = container.Reader(arc)
+    meta, man, chunks = r.meta, json.loads(zstd.decompress(r.get("manifest"))), dict(r.chunks)
+    r.close()
+    assert meta["hash"] == "blake3"
+    for f in meta["files"]:
+        assert f["hash"] == blake3.hexdigest(open(os.path.join(root, f["name"]), "rb").read()), f["name"]
+    newer = str(tmp_path / "newer.seedpack")
+    _rewrite(arc, newer, manifest={**man, "needs": "9.0.0"})
+    out = tmp_path / "o1"
+    with pytest.raises(container.FormatError, match="needs SeedPack 9.0.0"):
+        repo.unpack_repo(newer, str(out))
+    assert not out.exists() or not any(out.iterdir())
+    odd = str(tmp_path / "odd.seedpack")
+    _rewrite(arc, odd, meta={**meta, "hash": "xxh3"})
+    out = tmp_path / "o2"
+    with pytest.raises(container.FormatError, match="catalog hash"):
+        repo.unpack_repo(odd, str(out))
+    assert not out.exists() or not any(out.iterdir())
+    with pytest.warns(UserWarning, match="unchecked"):
+        res = repo.Unpacker(verify=False).run(odd, str(out), ["model-Q4_K.gguf", "README.md"])
+    assert sorted(res["unchecked"]) == ["README.md", "model-Q4_K.gguf"] and not res["bad"]
+    for n in res["files"]:
+        assert open(os.path.join(root, n), "rb").read() == (out / n).read_bytes(), n
+    sha = str(tmp_path / "sha.seedpack")
+    repo.Packer(hash_algo="sha256").pack([root], sha)
+    r = container.Reader(sha)
+    assert r.meta["hash"] == "sha256"
+    for f in r.meta["files"]:
+        assert f["hash"] == hashlib.sha256(open(os.path.join(root, f["name"]), "rb").read()).hexdigest()
+    assert {k: v[1:] for k, v in r.chunks.items()} == {k: v[1:] for k, v in chunks.items()}
+    r.close()
+    res = repo.unpack_repo(sha, str(tmp_path / "o3"))
+    assert not res["bad"] and not res["missing"] and not res["unchecked"], res
 
 
 def test_small_repo_pack_is_deterministic(small_repo, tmp_path):
@@ -361,7 +420,7 @@ def test_small_repo_archive_layout(small_repo):
         assert all(len(e) == 4 for e in m["plan"])
     cat = {f["name"]: f for f in r.meta["files"]}
     assert cat["model-BF16.gguf"]["role"] == "base" and cat["imatrix.dat"]["role"] == "file"
-    assert cat["model-Q8_0.gguf"]["role"] == "derived" and r.meta["hash"] == "sha256"
+    assert cat["model-Q8_0.gguf"]["role"] == "derived" and r.meta["hash"] == "blake3"
     assert r.meta["total"] == sum(os.path.getsize(os.path.join(root, n)) for n in os.listdir(root))
 
 

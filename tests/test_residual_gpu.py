@@ -198,39 +198,3 @@ def test_window_matches_per_tensor():
             if x["qr"]:
                 assert x["prediction"].to_host().tobytes() == y["prediction"].to_host().tobytes()
 
-
-_C1, _C2 = np.uint64(0xff51afd7ed558ccd), np.uint64(0xc4ceb9fe1a85ec53)
-
-
-def _fmix(k):
-    k = k ^ (k >> np.uint64(33))
-    k = k * _C1
-    k = k ^ (k >> np.uint64(33))
-    k = k * _C2
-    return k ^ (k >> np.uint64(33))
-
-
-def _np_hash(b):
-    """the content hash as spa_content_hash's declaration states it, in numpy uint64 arithmetic"""
-    w = np.frombuffer(bytes(b) + bytes(-len(b) % 8), "<u8")
-    k = np.arange(w.size, dtype=np.uint64) * np.uint64(0x9e3779b97f4a7c15)
-    with np.errstate(over="ignore"):
-        return tuple(int(np.sum(_fmix(w ^ _fmix(k + np.uint64(s))), dtype=np.uint64))
-                     for s in (0x243f6a8885a308d3, 0x13198a2e03707344))
-
-
-def test_content_hash():
-    say("case content hash")
-    g = np.random.Generator(np.random.PCG64(77))
-    buf = g.integers(0, 256, 3 << 20, dtype=np.uint8)
-    buf[(2 << 20) + 3:(2 << 20) + 3 + 100000] = buf[5:100005]          # a copy at an unaligned offset
-    regions = [(0, 0), (8, 1), (16, 7), (24, 8), (40, 9), (3, 1000), (64, (1 << 20) + 5), (5, 100000),
-               ((2 << 20) + 3, 100000), (1 << 20, 1 << 20)]
-    d = dev.DeviceArray.from_host(buf)
-    got = r.content_hashes(d, regions)
-    for (o, n), h in zip(regions, got):
-        assert h == _np_hash(buf[o:o + n]), (o, n)
-    assert got[7] == got[8]                                  # equal bytes, different places: equal keys
-    buf2 = buf.copy()
-    buf2[(2 << 20) + 3 + 4567] ^= 1                          # one bit changed
-    assert r.content_hashes(dev.DeviceArray.from_host(buf2), [regions[8]])[0] != got[8]
