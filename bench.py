@@ -77,7 +77,41 @@ def _profiled_traffic(kernel):
     return json.load(open(p))["bytes_per_launch"].get(kernel)
 
 
-PEAK_VALU_T = 78.6       # wave64 FP32 VALU lane-ops/s: 256 CUs x 4 SIMDs x 32 lanes x 2.4 GHz (= 157.3 TFLOP/s / 2)
+SIMDS, CLOCK_GHZ = 1024, 2.4
+PROBE_BLOCKS, PROBE_ITERS = 4096, 4000
+PROBES = ((0, "v_fma_f32"), (1, "v_add_f32"), (2, "v_xor_b32+v_add_u32"), (3, "v_fma_f32 with v_xor_b32+v_add_u32"),
+          (4, "v_mul_f32 with v_add_f32"), (5, "v_mul_f32"))
+
+
+def valu_probe(stream, reps=5):
+    """the VALU yardstick (spa_valu_probe): loops of known length of plain 32-bit VALU instructions,
+    timed with HIP events on the bench stream -> instruction rate, lane-ops/s and cycles per
+    instruction per SIMD at the 2.4 GHz peak clock. None of them dual-issues (SQ_ACTIVE_INST_VALU2 = 0
+    in the counter pass): the fastest is the single-issue rate, one wave64 instruction per SIMD per
+    quad-cycle; two per quad-cycle is the issue limit (profiles/valu.json)."""
+    from seedpack_amd import device as dev
+    from seedpack_amd._lib import check, lib
+    out = dev.DeviceArray(PROBE_BLOCKS * 256, np.float32)
+    res = {"workgroups": PROBE_BLOCKS, "loop_trips": PROBE_ITERS}
+    for op, name in PROBES:
+        insts = int(lib().spa_valu_probe_insts(op, PROBE_BLOCKS, PROBE_ITERS))
+        check(lib().spa_valu_probe(op, PROBE_BLOCKS, PROBE_ITERS, out.ptr, stream.handle))
+        best = None
+        for _ in range(reps):
+            e0, e1 = dev.Event(), dev.Event()
+            e0.record(stream.handle)
+            check(lib().spa_valu_probe(op, PROBE_BLOCKS, PROBE_ITERS, out.ptr, stream.handle))
+            e1.record(stream.handle)
+            stream.synchronize()
+            ms = e0.elapsed_ms(e1)
+            best = ms if best is None else min(best, ms)
+        rate = insts / (best / 1e3)
+        res[name] = {"ms": round(best, 4), "wave64_valu_insts": insts, "T_lane_ops_s": round(rate * 64 / 1e12, 2),
+                     "cycles_per_inst_per_simd_at_2p4GHz": round(SIMDS * CLOCK_GHZ * 1e9 / rate, 3)}
+        log(f"bench: VALU probe {name}: {best:.3f} ms, {rate * 64 / 1e12:.1f} T lane-ops/s")
+    res["single_issue_T_lane_ops_s"] = max(v["T_lane_ops_s"] for v in res.values() if isinstance(v, dict))
+    res["dual_issue_peak_T_lane_ops_s"] = round(2 * res["single_issue_T_lane_ops_s"], 2)
+    return res
 
 
 def _profiled_valu(kernel):
@@ -89,6 +123,14 @@ def _profiled_valu(kernel):
     d = json.load(open(p))
     n = d["insts_valu_per_launch"].get(kernel)
     return None if n is None else n * d["lane_ops_per_instruction"]
+
+
+def _profiled_issue(kernel):
+    """share of the SIMDs' quad-cycles issuing at least one VALU instruction, from the counter pass"""
+    p = os.path.join(ROOT, "profiles", "valu.json")
+    if not os.path.exists(p):
+        return None
+    return json.load(open(p)).get("issue", {}).get(kernel, {}).get("issue_slot_occupancy")
 
 
 def _cpu_model():
@@ -137,6 +179,13 @@ def profile_pass():
         check(lib().spa_copy(b.ptr, a.ptr, nb, None))
     dev.synchronize()
     log(f"profile: k_copy16 {nb} bytes x2 launches (reads {nb}, writes {nb})")
+    pr = dev.DeviceArray(PROBE_BLOCKS * 256, np.float32)
+    for op, name in PROBES:
+        for _ in range(2):
+            check(lib().spa_valu_probe(op, PROBE_BLOCKS, PROBE_ITERS, pr.ptr, None))
+        dev.synchronize()
+        log(f"profile: k_valu_probe<{op}> ({name}) x2 launches, "
+            f"{lib().spa_valu_probe_insts(op, PROBE_BLOCKS, PROBE_ITERS)} loop VALU instructions per launch")
 
 
 def iquant_cfg3(stream, reps=2, types=None):
@@ -681,14 +730,23 @@ def main():
     hbm = {"achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 5),
            "algorithmic_bytes": ab}
     kdesc = f"k_kquant<{NAMES[t]}> on {n} {w.shape[0]}x{w.shape[1]}"
+    probe = valu_probe(stream)
     if ops:
-        # the K-quant searches are VALU-bound: the roof is the VALU issue rate; HBM beside it
+        # the K-quant searches are VALU-bound: the roof is the VALU issue limit, two wave64 instructions
+        # per SIMD per quad-cycle, at the quad-cycle rate the probe measures in this run; HBM beside it
         va = ops / (dom_ms / 1e3) / 1e12
-        roofline = {"bound": "valu", "kernel": kdesc, "achieved": round(va, 2), "peak": PEAK_VALU_T,
-                    "unit": "T lane-ops/s", "frac": round(va / PEAK_VALU_T, 4), "traffic": traffic,
+        peak = probe["dual_issue_peak_T_lane_ops_s"]
+        roofline = {"bound": "valu", "kernel": kdesc, "achieved": round(va, 2), "peak": peak,
+                    "unit": "T lane-ops/s", "frac": round(va / peak, 4), "traffic": traffic,
                     "valu_lane_ops_per_launch": ops, "avg_launch_ms": round(dom_ms, 4), "hbm": hbm,
-                    "note": "lane-ops = SQ_INSTS_VALU x 64 per launch (profiles/valu.json) over the live launch time; "
-                            "peak = 1024 SIMDs x 32 lanes x 2.4 GHz (a wave64 FP32 VALU instruction every 2 cycles)"}
+                    "issue_slot_occupancy": _profiled_issue(kname), "single_issue_peak": probe["single_issue_T_lane_ops_s"],
+                    "frac_of_fp32_tflops": round(va / 157.3, 4), "valu_probe": probe,
+                    "note": "lane-ops = SQ_INSTS_VALU x 64 per launch (exact: profiles/valu.json) over the live launch time; "
+                            "peak = 2 x the single-issue rate the VALU probe measures in this run (spa_valu_probe: "
+                            "plain 32-bit loops, no dual issue); issue_slot_occupancy = quad-cycles issuing at least "
+                            "one VALU instruction (SQ_ACTIVE_INST_VALU - SQ_ACTIVE_INST_VALU2 over the SIMDs' "
+                            "quad-cycles, counter pass); frac_of_fp32_tflops counts a lane-op as one operation "
+                            "against the published 157.3 TFLOP/s (packed FP32, FMA = 2)"}
     else:
         roofline = {"bound": "hbm", "kernel": kdesc, **hbm, "traffic": traffic, "avg_launch_ms": round(dom_ms, 4),
                     "note": "no VALU count profiled for this launch: HBM fraction only"}

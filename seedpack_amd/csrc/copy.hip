@@ -40,6 +40,44 @@ __global__ __launch_bounds__(256) void k_perturb_blocks(uint8_t* __restrict__ ds
     }
 }
 
+// VALU issue-rate probe: every lane advances CHAINS independent chains UNROLL times per loop trip
+// (OP 0: v_fma_f32 steps, 1: v_add_f32, 2: integer steps of v_xor_b32 + v_add_u32, 3: FP32 chains
+// and integer chains side by side, 4: v_mul_f32 and v_add_f32 chains, 5: v_mul_f32), so a launch retires nblocks x 4 waves x iters x the loop's VALU
+// instructions (spa_valu_probe_insts; the loop control is scalar), plus a few per lane around it. The chains' sum is stored
+// so that nothing is dropped. The time of a large launch over that count is the chip's VALU issue
+// rate for plain (non-packed) 32-bit instructions, the roof of the VALU-bound searches.
+constexpr int PROBE_CHAINS = 8, PROBE_UNROLL = 16;
+template <int OP>
+__global__ __launch_bounds__(256) void k_valu_probe(float* __restrict__ out, int iters, float m, float c) {
+    float a[PROBE_CHAINS];
+    uint32_t u[PROBE_CHAINS];
+    const uint32_t x = __float_as_uint(m), y = __float_as_uint(c);
+#pragma unroll
+    for (int k = 0; k < PROBE_CHAINS; ++k) {
+        a[k] = (float)(threadIdx.x + k) * 1e-3f;
+        u[k] = threadIdx.x * 2654435761u + (uint32_t)k;
+    }
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int r = 0; r < PROBE_UNROLL; ++r) {
+#pragma unroll
+            for (int k = 0; k < PROBE_CHAINS; ++k) {
+                if (OP == 0) a[k] = __builtin_fmaf(a[k], m, c);
+                else if (OP == 1) a[k] = a[k] + c;
+                else if (OP == 2) u[k] = (u[k] ^ x) + y;                        // integer only
+                else if (OP == 4) a[k] = k % 2 ? a[k] * m : a[k] + c;           // v_mul_f32 and v_add_f32 chains
+                else if (OP == 5) a[k] = a[k] * m;                              // v_mul_f32 only
+                else if (k % 2) a[k] = __builtin_fmaf(a[k], m, c);             // FP32 and integer chains
+                else u[k] = (u[k] ^ x) + y;
+            }
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PROBE_CHAINS; ++k) s += a[k] + (float)u[k];
+    if (s == 12345.678f) out[blockIdx.x * blockDim.x + threadIdx.x] = s;   // never true for the probe's inputs
+}
+
 __global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
@@ -77,4 +115,24 @@ extern "C" int spa_perturb_blocks(void* dst, int64_t nblocks, int block_bytes, u
                        nblocks, block_bytes, per_million, seed);
     SPA_HIP_TRY(hipGetLastError());
     return SPA_OK;
+}
+
+extern "C" int spa_valu_probe(int op, int64_t nblocks, int iters, float* out, void* stream) {
+    if (op < 0 || op > 5 || nblocks <= 0 || nblocks > 0x7fffffff || iters <= 0 || !out)
+        return spa::fail(SPA_ERR_ARG, "spa_valu_probe: bad arguments");
+    void (*const ks[6])(float*, int, float, float) = {k_valu_probe<0>, k_valu_probe<1>, k_valu_probe<2>,
+                                                      k_valu_probe<3>, k_valu_probe<4>, k_valu_probe<5>};
+    void (*k)(float*, int, float, float) = ks[op];
+    hipLaunchKernelGGL(k, dim3((unsigned)nblocks), dim3(256), 0, (hipStream_t)stream, out, iters, 1.0000001f, 1e-7f);
+    SPA_HIP_TRY(hipGetLastError());
+    return SPA_OK;
+}
+
+extern "C" int64_t spa_valu_probe_insts(int op, int64_t nblocks, int iters) {
+    // loop VALU instructions of one launch: waves x trips x steps per trip (the compiled loops: op 0
+    // 128 v_fma_f32, op 1 128 v_add_f32, op 2 128 v_xor_b32 + 128 v_add_u32, op 3 64 v_fma_f32 +
+    // 64 v_xor_b32 + 64 v_add_u32, op 4 64 v_mul_f32 + 64 v_add_f32, op 5 128 v_mul_f32)
+    const int64_t per = op == 2 ? 2 * PROBE_CHAINS * PROBE_UNROLL : op == 3 ? 3 * PROBE_CHAINS * PROBE_UNROLL / 2
+                                                                          : PROBE_CHAINS * PROBE_UNROLL;   // 0, 1, 4, 5
+    return nblocks * 4 * (int64_t)iters * per;
 }
