@@ -166,8 +166,12 @@ int spa_qr_decode(int ggml_type, const void* in, uint64_t in_bytes, const uint64
  * graph capture, serving loops, harnesses that forbid hipMalloc). spa_qr_encode with its workspace
  * taken from a static per-device scratch of spa_qr_noalloc_scratch_bytes() (64 MiB) instead of a
  * `work` argument: no allocation, no hipMemset. Calls whose spa_qr_work_bytes(ggml_type, nseg) exceed
- * it fail with SPA_ERR_ARG. All calls on one device share that scratch: calls that overlap in time on
- * one device (other streams or threads) race and must be serialised by the caller. */
+ * it fail with SPA_ERR_ARG. All calls on one device share that scratch, and the library orders them:
+ * each call's stream waits for the event the previous call on the device recorded after its kernels,
+ * so calls on other streams or threads run one after another on the GPU and never race (the first
+ * call on a device sets up the scratch's address and that event). Under
+ * a HIP graph capture no wait or record is added: the captured graph's own order must keep calls
+ * apart. */
 int spa_qr_encode_noalloc(int ggml_type, const void* F, const void* P, const void* seed, const void* tm,
                           const void* sg, int nseg, const int* remap, const uint16_t* freq, const uint32_t* cum,
                           void* out, uint64_t cap, uint32_t* out_len, const uint16_t* gk, const float* imx, int mv,

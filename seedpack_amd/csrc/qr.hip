@@ -705,20 +705,24 @@ namespace {
 constexpr int kMaxDev = 16;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDev];
+hipEvent_t g_scratch_done[kMaxDev];   // recorded after the last kernels that used the device's scratch
 
-// the current device's copy of `scratch` (looked up once per device, with that device current)
-int scratch_on_device(void** out) {
+// the current device's copy of `scratch` and its event (set up once per device, with that device
+// current: the symbol's address and one event; nothing is allocated on the device). Called with
+// g_scratch_mu held.
+int scratch_on_device(int* dev_out, void** out) {
     int dev = 0;
     SPA_HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= kMaxDev) return spa::fail(SPA_ERR_ARG, "QR: device %d out of range", dev);
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
         void* p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p)
             return spa::fail(SPA_ERR_HIP, "QR: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-        g_scratch_ptr[dev] = p;
+        SPA_HIP_TRY(hipEventCreateWithFlags(&g_scratch_done[dev], hipEventDisableTiming));   // (a wait on it before
+        g_scratch_ptr[dev] = p;                                                               // its first record is a no-op)
     }
+    *dev_out = dev;
     *out = g_scratch_ptr[dev];
     return 0;
 }
@@ -856,12 +860,23 @@ int spa_qr_encode_noalloc(int T, const void* F, const void* P, const void* seed,
                          "more than the %u of its static scratch (split the batch or use spa_qr_encode)",
                          nseg, T, need, SPA_QR_NOALLOC_SCRATCH);
     if (nseg == 0) return 0;
+    // the calls on one device take the scratch in turn: each call's stream waits for the event the
+    // previous call recorded after its kernels, and records it again after its own (under a graph
+    // capture the graph's own order is the caller's, and neither is added to it)
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
     void* work = nullptr;
-    if (int e = scratch_on_device(&work)) return e;
-    if (grid_type(T))
-        return grid_encode(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, gk, imx, mv, work,
-                           (hipStream_t)stream);
-    return dispatch<Encode>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, mv, work, (hipStream_t)stream);
+    int dev = 0;
+    if (int e = scratch_on_device(&dev, &work)) return e;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    SPA_HIP_TRY(hipStreamIsCapturing((hipStream_t)stream, &cs));
+    const bool order = cs == hipStreamCaptureStatusNone;
+    if (order) SPA_HIP_TRY(hipStreamWaitEvent((hipStream_t)stream, g_scratch_done[dev], 0));
+    const int rc = grid_type(T) ? grid_encode(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, gk, imx, mv,
+                                              work, (hipStream_t)stream)
+                                : dispatch<Encode>(T, F, P, seed, tm, sg, nseg, remap, freq, cum, out, cap, out_len, mv, work,
+                                                   (hipStream_t)stream);
+    if (order) SPA_HIP_TRY(hipEventRecord(g_scratch_done[dev], (hipStream_t)stream));
+    return rc;
 }
 
 size_t spa_qr_noalloc_scratch_bytes(void) { return SPA_QR_NOALLOC_SCRATCH; }

@@ -1476,18 +1476,35 @@ class Unpacker:
         for k, j in enumerate(joined):
             if nb + k in need_b:
                 zdicts[nb + k] = zdicts[j["parts"][0][0]]
-        in_hbm = self.bases_in_hbm
-        if in_hbm is None:
-            free, _ = dev.mem_info()
-            need = sum(cat[manifest["bases"][i]]["size"] for i in coded)
-            in_hbm = need + max((mf[i]["size"] for i in sel), default=0) + (48 << 30) <= free
-        if in_hbm:                           # a split model's shards one after another in one allocation
-            for k, j in enumerate(joined):
-                if nb + k in need_b:
-                    jd[k] = d = dev.DeviceArray(j["size"], np.uint8)
-                    ends = [s_ for _, s_ in j["parts"][1:]] + [j["size"]]
-                    for (i, s_), e_ in zip(j["parts"], ends):
-                        place[i] = d.view(s_, (e_ - s_,), np.uint8)
+        # each base decoded whole into HBM or window by window, decided per base (repo3.py:2311-2321):
+        # an M24 base (method m28) has no random access and is always decoded whole; an R2 base is
+        # whole when forced (bases_in_hbm True) or, by default, while the bases so far, the largest
+        # file to rebuild and a 48 GB reserve fit; a split model's shards are whole only together
+        whole = {}
+        free = dev.mem_info()[0] if self.bases_in_hbm is None else 0
+        room = free - max((mf[i]["size"] for i in sel), default=0) - (48 << 30)
+        for i in sorted(coded, key=lambda i: "layout" not in coded[i][2]):      # M24 bases first
+            size = cat[manifest["bases"][i]]["size"]
+            if "layout" in coded[i][2]:
+                if self.bases_in_hbm is None and size > free:
+                    raise MemoryError(f"base {manifest['bases'][i]}: an M24 base is decoded whole and "
+                                      f"{size:,} B do not fit in {free:,} B of free HBM")
+                whole[i] = True
+            else:
+                whole[i] = self.bases_in_hbm if self.bases_in_hbm is not None else size <= room
+            if whole[i]:
+                room -= size
+        for j in joined:
+            if not all(whole.get(i, True) for i, _ in j["parts"]):
+                for i, _ in j["parts"]:
+                    if i in whole and "layout" not in coded[i][2]:
+                        whole[i] = False
+        for k, j in enumerate(joined):       # a split model's shards one after another in one allocation
+            if nb + k in need_b and all(whole.get(i, False) for i, _ in j["parts"]):
+                jd[k] = d = dev.DeviceArray(j["size"], np.uint8)
+                ends = [s_ for _, s_ in j["parts"][1:]] + [j["size"]]
+                for (i, s_), e_ in zip(j["parts"], ends):
+                    place[i] = d.view(s_, (e_ - s_,), np.uint8)
 
         def residual_of(i):
             m = mf[i]
@@ -1513,7 +1530,7 @@ class Unpacker:
                 continue
             name = manifest["bases"][i]
             rest, g, parts = coded.pop(i)
-            if not in_hbm:
+            if not whole[i]:
                 # decoded window by window from the archive (repo3.py:2311-2323): random access to
                 # the coded stream of its tensors, the file written through it when it is wanted
                 if "stream" not in parts or "lens" not in parts or "meta" not in parts or "side" not in parts:

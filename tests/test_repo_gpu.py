@@ -154,7 +154,7 @@ def test_small_repo_pack_is_deterministic(small_repo, tmp_path):
 
 def test_small_repo_method_m28(small_repo, tmp_path):
     """method m28: the base chunk is M24's parts (layout, side, tables, lens, stream, rest); every file
-    extracts byte-identical"""
+    extracts byte-identical, also when the bases are asked to stay out of HBM"""
     root, arc, sizes, stats = small_repo
     a = str(tmp_path / "m28.seedpack")
     repo.pack_repo([root], a, method="m28")
@@ -167,6 +167,10 @@ def test_small_repo_method_m28(small_repo, tmp_path):
     assert not res["bad"] and not res["missing"], res
     for n in sorted(os.listdir(root)):
         assert open(os.path.join(root, n), "rb").read() == open(os.path.join(out, n), "rb").read(), n
+    # bases kept out of HBM where they can be: an M24 base has no random access and is still decoded
+    # whole (the decision is per base, repo3.py:2311-2321)
+    res = repo.Unpacker(bases_in_hbm=False).run(a, None, ["model-Q4_K.gguf", "model-BF16.gguf"])
+    assert res["files"] == {"model-Q4_K.gguf": True, "model-BF16.gguf": True}, res
 
 
 @pytest.fixture(scope="module")

@@ -89,3 +89,56 @@ def test_noalloc_rejects_a_batch_beyond_its_scratch():
     rc = L.spa_qr_encode_noalloc(8, None, None, None, None, None, big, None, None, None, None, 1 << 16, None, None, None,
                                  2, None)
     assert rc == -4 and b"static scratch" in L.spa_last_error()
+
+
+def _prepare(T, F, P, w, imx, cols):
+    """device inputs and tables of one batch -> (argument tuple without out/lens, nseg, cap, keep)"""
+    sd = dev.DeviceArray.from_host(w.view(np.uint8))
+    imx_d = None if imx is None else dev.DeviceArray.from_host(imx)
+    item = (F, P, 0, 30, cols, 0 if imx is not None else -1)
+    parts = qr.encode_parts(T, [item], sd, imx_d)
+    tm, sg, nb = qr._descriptors(T, [len(F) // qr.BS[T]], [item[2:]])
+    remap = np.full(qr.NTAB2, -1, np.int32)
+    remap[parts["used"]] = np.arange(len(parts["used"]), dtype=np.int32)
+    keep = [sd, imx_d, dev.DeviceArray.from_host(F), dev.DeviceArray.from_host(P),
+            dev.DeviceArray.from_host(tm.view(np.uint8)), dev.DeviceArray.from_host(sg.view(np.uint8)),
+            dev.DeviceArray.from_host(remap), dev.DeviceArray.from_host(parts["freq"]),
+            dev.DeviceArray.from_host(qr.cum_of(parts["freq"]))]
+    cap = qr.seg_blocks(T) * (3 * qr.BS[T] if T in qr.GRID_TYPES else (qr.QK[T] + qr.NSB_MAX) * 2) + 1024
+    return keep, len(sg), cap, parts
+
+
+def test_noalloc_calls_on_two_streams_do_not_race():
+    """two batches encoded by spa_qr_encode_noalloc on two streams, queued back to back with no wait
+    between them: each gives the bytes of its batch encoded alone, one call at a time (the library
+    orders the shared scratch's uses by its per-device event)"""
+    L = lib()
+    T = 12
+    say(f"case qr noalloc two streams T={T}")
+    batches = []
+    for k, (rows, cols) in enumerate(((384, 4096), (256, 2048))):
+        F, P, w, imx = _batch(T, rows, cols, 0x7707 + k)
+        batches.append(_prepare(T, F, P, w, imx, cols))
+    streams = [dev.Stream(), dev.Stream()]
+    res = []
+    for rep in range(3):
+        outs = []
+        for (keep, nseg, cap, parts), st in zip(batches, streams):
+            sd, imx_d, Fd, Pd, tm_d, sg_d, remap_d, freq_d, cum_d = keep
+            slots = dev.DeviceArray(nseg * cap, np.uint8)
+            lens = dev.DeviceArray(nseg, np.uint32)
+            check(L.spa_memset(slots.ptr, 0, slots.nbytes, st.handle))
+            check(L.spa_memset(lens.ptr, 0, lens.nbytes, st.handle))
+            check(L.spa_qr_encode_noalloc(T, Fd.ptr, Pd.ptr, sd.ptr, tm_d.ptr, sg_d.ptr, nseg, remap_d.ptr, freq_d.ptr,
+                                          cum_d.ptr, slots.ptr, cap, lens.ptr, qr._gk_ptr(T), None, qr.MODEL, st.handle))
+            if rep == 0:                  # the reference run: one call at a time
+                st.synchronize()
+            outs.append((slots, lens))
+        for st in streams:
+            st.synchronize()
+        res.append([(l.to_host(), s.to_host()) for s, l in outs])
+    for k, (keep, nseg, cap, parts) in enumerate(batches):
+        assert np.array_equal(res[0][k][0], parts["lens"]), f"batch {k}: lengths differ from encode_parts"
+        for rep in range(1, 3):
+            assert np.array_equal(res[rep][k][0], res[0][k][0])
+            assert res[rep][k][1].tobytes() == res[0][k][1].tobytes()
