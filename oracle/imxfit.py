@@ -7,10 +7,14 @@ with detmath's in-order float64 sums (imxfit.py:30-58); ls_solve is the referenc
 (imxfit.py:61-71); equal_blocks re-quantizes through the reference's C quantizers (oracle/_ref).
 Every float32 operation is one numpy operation in the reference's order.
 
-Pinned by tests/test_oracle_fit.py: quantized with a known importance by the reference's own C
-quantizers, the fit recovers an importance that reproduces the quant's blocks on rows it was not fit
-on (a planted mistake -- the weights c without their sigma^2 term -- must do measurably worse), and
-the per-block normalisation and Gram sums follow oracle/detmath.py.
+Pinned by tests/test_oracle_fit.py: bit for bit against tests/golden/fit_vectors.npz, which the
+reference's own imxfit.py wrote under its --cpu backend (tests/golden/make_fit_golden.py: Gram sums
+over tensors sharing an importance, the fitted vector, the share of check blocks reproduced, for Q4_0,
+Q4_1, Q5_0, Q5_1 with zero rows, zero blocks and outliers); and by properties: quantized with a known
+importance by the reference's own C quantizers, the fit recovers an importance that reproduces the
+quant's blocks on rows it was not fit on (a planted mistake -- the weights c without their sigma^2
+term -- must do measurably worse), and the per-block normalisation and Gram sums follow
+oracle/detmath.py.
 """
 import numpy as np
 

@@ -96,6 +96,36 @@ def test_importance_fit_equals_oracle(T):
     assert eq == oi.equal_blocks(T, X[400:], F[400:], q) and eq > 0.5
 
 
+def _fit_cases():
+    from tests.golden.fit_cases import CASES
+    return [c[0] for c in CASES]
+
+
+@pytest.mark.parametrize("name", _fit_cases())
+def test_importance_fit_equals_the_reference_fit(name):
+    """the device fit against tests/golden/fit_vectors.npz (the reference's own imxfit.py run under its
+    --cpu backend): the quantizer's blocks, the Gram sums over the tensors sharing the importance, the
+    fitted vector and the check share, all equal"""
+    from tests.golden.fit_cases import CASES, COLS, R_FIT, case_inputs, digest
+    say("case imxfit golden", name)
+    z = np.load("tests/golden/fit_vectors.npz")
+    _, T, ntens, _ = next(c for c in CASES if c[0] == name)
+    xs, e = case_inputs(name)
+    assert bytes(z[f"{name}/inputs_sha256"]).hex() == digest(xs, e), "numpy's generator changed: inputs differ"
+    gq = GPUQuant()
+    G = np.zeros((COLS // 32, 32, 32), np.float64)
+    for k in range(ntens):
+        F = z[f"{name}/blocks{k}"]
+        X = dev.DeviceArray.from_host(xs[k])
+        assert gq.quantize_batch(T, [X], [e])[0].to_host().tobytes() == F.tobytes()
+        G += imxfit.ls_gram(gq, T, xs[k][:R_FIT], F[:R_FIT])
+    assert np.array_equal(G, z[f"{name}/G"])
+    q = imxfit.ls_solve(G, e)
+    assert np.array_equal(q, z[f"{name}/fit"])
+    share = [imxfit.equal_blocks(gq, T, xs[k][R_FIT:], z[f"{name}/blocks{k}"][R_FIT:], q) for k in range(ntens)]
+    assert share == list(z[f"{name}/share"])
+
+
 def test_sibling_estimate():
     g = np.random.default_rng(9)
     n = 5000

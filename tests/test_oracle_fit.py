@@ -89,3 +89,31 @@ def test_importance_fit_recovers_the_quantizers_importance(T):
     assert np.corrcoef(np.log(q), np.log(e))[0, 1] > 0.99
     assert fit > 0.55 and fit > planted + 0.2 and unit < 0.1, (fit, planted, unit)
     assert oi.equal_blocks(T, X[512:], F[512:], e) == 1.0
+
+
+def _fit_cases():
+    from tests.golden.fit_cases import CASES
+    return [c[0] for c in CASES]
+
+
+@pytest.mark.parametrize("name", _fit_cases())
+def test_importance_fit_equals_the_reference_fit(name):
+    """the restatement against tests/golden/fit_vectors.npz, written by the reference's own imxfit.py
+    (ls_gram, ls_solve, equal_blocks) under its --cpu backend: Gram sums over the tensors that share
+    the importance, fitted vector and check share all equal"""
+    from oracle import imxfit as oi
+    from tests.golden.fit_cases import CASES, COLS, R_FIT, case_inputs, digest
+    z = np.load("tests/golden/fit_vectors.npz")
+    _, T, ntens, _ = next(c for c in CASES if c[0] == name)
+    xs, e = case_inputs(name)
+    assert bytes(z[f"{name}/inputs_sha256"]).hex() == digest(xs, e), "numpy's generator changed: inputs differ"
+    G = np.zeros((COLS // 32, 32, 32), np.float64)
+    for k in range(ntens):
+        F = z[f"{name}/blocks{k}"]
+        assert np.frombuffer(ref.quantize(T, xs[k], e), np.uint8).tobytes() == F.tobytes()
+        G += oi.ls_gram(T, xs[k][:R_FIT], F[:R_FIT])
+    assert np.array_equal(G, z[f"{name}/G"])
+    q = oi.ls_solve(G, e)
+    assert np.array_equal(q, z[f"{name}/fit"])
+    share = [oi.equal_blocks(T, xs[k][R_FIT:], z[f"{name}/blocks{k}"][R_FIT:], q) for k in range(ntens)]
+    assert share == list(z[f"{name}/share"])
