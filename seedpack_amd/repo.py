@@ -30,7 +30,7 @@ when at least half of its bytes are Q8_0 tensors (repo3.py:1190-1215), else zstd
 
 Quant files made with another importance matrix (another chunk count in their metadata) form sets;
 the importance of their legacy-quant inputs is fitted back from the first file of a set as it is
-coded (imxfit.py; repo3.py:1241-1352), kept in the archive ("imx" chunk), and the set's files are
+coded (fitsets.py over imxfit.py), kept in the archive ("imx" chunk), and the set's files are
 predicted with it.
 
 The shards of a split model (llama.cpp's gguf-split names, every shard present) are coded as
@@ -53,7 +53,7 @@ from concurrent.futures import Future, ThreadPoolExecutor, wait as futures_wait
 
 import numpy as np
 
-from . import blake3, container, device as dev, gguf, header, imatrix as imx_mod, imxfit, qr, r2, residual, zstd
+from . import blake3, container, device as dev, fitsets, gguf, header, imatrix as imx_mod, qr, r2, residual, zstd
 from ._lib import check, lib
 from .framing import index, nbytes, pack, pack_parts, unpack
 from .gpuquant import GPUQuant
@@ -76,7 +76,6 @@ REF_KEEP = 3 << 30                   # bytes of referenced tensors per window (r
 BUNDLE_MAX = 64 << 20                # other files up to this size go into the lzma bundle (repo3.py:1364)
 Q8_MIN = 0.5                         # a base-less file with this share of Q8_0 bytes: the Q8_0 codec (repo3.py:1191)
 DQ_CACHE = 32 << 30                  # dequantized seed tensors kept in HBM (float32 bytes)
-FIT_ROWS = 1 << 24                   # weights per piece of a tensor in the importance fit (repo3.py:1246)
 SPARSE = 0.02                        # residuals with fewer non-zero bytes: zstd level >= 9 (repo3.py:45)
 SKIP_DIRS = {".git", ".cache", "__pycache__"}
 F32, F16, BF16 = 0, 1, 30
@@ -157,19 +156,17 @@ def joined_groups(names):
 
 def windows(nbytes_, window=WINDOW, pred=None, pred_window=PRED_WINDOW):
     """positions 0..n-1 (tensors in order, their base bytes) -> [(start, end)]: a window closes before a
-    tensor that would take it past `window` base bytes or `pred_window` prediction bytes
-    (repo3.py:1689-1706)"""
+    tensor that would take it past `window` base bytes or `pred_window` prediction bytes; a window
+    holds at least one tensor (repo3.py:1689-1706)"""
     pred = pred or [0] * len(nbytes_)
-    out, s, acc, accp = [], 0, 0, 0
-    for p in range(len(nbytes_)):
-        if p > s and (acc + nbytes_[p] > window or accp + pred[p] > pred_window):
-            out.append((s, p))
-            s, acc, accp = p, 0, 0
-        acc += nbytes_[p]
-        accp += pred[p]
-    if nbytes_:
-        out.append((s, len(nbytes_)))
-    return out
+    cuts, base_bytes, pred_bytes = [0], 0, 0
+    for p, (nb, pb) in enumerate(zip(nbytes_, pred)):
+        if p > cuts[-1] and (base_bytes + nb > window or pred_bytes + pb > pred_window):
+            cuts.append(p)
+            base_bytes = pred_bytes = 0
+        base_bytes += nb
+        pred_bytes += pb
+    return list(zip(cuts, cuts[1:] + [len(nbytes_)])) if nbytes_ else []
 
 
 def _read_into(path, out, off=0, pool=None):
@@ -470,19 +467,26 @@ class _Base:
 
 
 def pick_seeds(base_tensors, derived_tensors):
-    """derived files that share no tensor name with a base, grouped by model: the senior quant of each
-    group (most bits per weight, then the larger name) becomes its seed (repo3.py:1359-1372).
+    """the seeds of the derived files that share no tensor name with any base (repo3.py:1359-1372):
+    the senior quant left (most bits per weight, then the larger name) is a seed, and every file left
+    that shares at least half of its tensor names with it is of its model; until none is left.
     base_tensors: [tensor lists]; derived_tensors: {name: tensor list} in input order"""
-    base_names = [{t.name for t in ts} for ts in base_tensors]
-    names = {n: {t.name for t in ts} for n, ts in derived_tensors.items()}
-    rest = [n for n in derived_tensors if names[n] and not any(names[n] & b for b in base_names)]
+    in_bases = set().union(*({t.name for t in ts} for ts in base_tensors))
+    left = {n: {t.name for t in ts} for n, ts in derived_tensors.items()}
+    left = {n: tn for n, tn in left.items() if tn and not tn & in_bases}
     seeds = []
-    while rest:
-        s_ = max(rest, key=lambda n: (bits_per_weight(derived_tensors[n]), n))
-        group = {n for n in rest if 2 * len(names[n] & names[s_]) >= len(names[n])}
-        seeds.append(s_)
-        rest = [n for n in rest if n not in group]
+    while left:
+        seed = max(left, key=lambda n: (bits_per_weight(derived_tensors[n]), n))
+        model = left[seed]
+        seeds.append(seed)
+        left = {n: tn for n, tn in left.items() if 2 * len(tn & model) < len(tn)}
     return seeds
+
+
+def _row_bytes(t):
+    """bytes per row of a block-quantized tensor"""
+    _, qk, bs = QFUN[t.type]
+    return int(t.shape[0]) // qk * bs
 
 
 def _zc_params(level, data):
@@ -592,7 +596,7 @@ class Packer:
         self.timing = []
         self.stats = collections.Counter()
         self.sizes = {}
-        self.file_set, self.fit_wait, self.fit_sig, self.fit_done, self.imx_sets = {}, {}, {}, {}, {}
+        self.fits = fitsets.FitSets()
 
     # ---------------------------------------------------------------- bases
     def _load_base(self, path, piece=1 << 30, into=None):
@@ -738,7 +742,7 @@ class Packer:
                 continue
             mine.append((t, k))
         self.stats["ref"] += len(refs)
-        kset = self.file_set.get(fi, 0)
+        kset = self.fits.set_of.get(fi, 0)
         kind_of = {t.name: k for t, k in mine}
         # window by window (repo3.py:2041-2053): the set's importance fitted from this window's
         # tensors, then the window's residuals, its plan entries and its QR batches (each window's QR
@@ -754,9 +758,12 @@ class Packer:
         for w in sorted(by_w):
             ts_w = mine_w.get(w, [])
             bw = b.window([t.name for t in ts_w], st)     # (the base itself when it is in HBM)
-            if self.fit_wait.get(kset):
-                self._fit_from(kset, [t for t in ts_w if kind_of[t.name] == "rq"], F, bw)
-            fitted = self.imx_sets.get(kset, {})
+            if self.fits.waiting(kset):
+                self.fits.fit_window(kset, [t for t in ts_w if kind_of[t.name] == "rq"], bw.by_name.get,
+                                     lambda bt, r0, r1: self._f32_rows(bw, bt, r0, r1),
+                                     lambda t, r0, r1: F.view(t.offset + r0 * _row_bytes(t), ((r1 - r0) * _row_bytes(t),), np.uint8),
+                                     self.gq, st)
+            fitted = self.fits.importance(kset)
             rts = [residual.Tensor(t.name, t.type, t.shape[0], F.view(t.offset, (t.nbytes,), np.uint8),
                                    bw.view(bw.by_name[t.name], st), imatrix=imx_map.get(t.name),
                                    fitted={kset: fitted[t.name]} if t.name in fitted else None,
@@ -806,31 +813,7 @@ class Packer:
                 "span": self._zspan(pred, wins_of, job["last_window"], size), "entry": entry, "zdict": b.header,
                 "tm": tm}
 
-    # ---------------------------------------------------------------- fitted importance (imxfit)
-    def _fit_plan(self, names, heads, imx_all, pub):
-        """the sets of files made with another importance matrix (repo3.py:1248-1274) -> self.file_set
-        {file index: set k}, self.fit_wait {k: input names still to be fitted}, self.fit_sig {k: (chunk
-        count, dataset)}; pub: the repository imatrix's chunk count"""
-        self.file_set, self.fit_wait, self.fit_sig, self.fit_done, self.imx_sets = {}, {}, {}, {}, {}
-        self.imx_all = imx_all
-        if pub is None or not imx_all:
-            return
-        sigs = {}
-        for fi, n in enumerate(names):
-            meta = heads[n][0]
-            cc = meta.get("quantize.imatrix.chunks_count")
-            if cc is not None and int(cc) != pub:
-                sigs.setdefault((int(cc), str(meta.get("quantize.imatrix.dataset", ""))), []).append(fi)
-        self.by_input = {}                  # an input's importance bytes -> the names sharing it
-        for n, e in imx_all.items():
-            self.by_input.setdefault(np.asarray(e, np.float32).tobytes(), []).append(n)
-        for k, (sig, idx) in enumerate(sigs.items(), 1):
-            self.fit_sig[k], self.imx_sets[k], self.fit_done[k] = sig, {}, []
-            self.file_set.update({i: k for i in idx})
-            self.fit_wait[k] = {nm for i in idx for t in heads[names[i]][1] if t.type in imxfit.LS_TYPES
-                                and t.name in imx_all
-                                for nm in self.by_input[np.asarray(imx_all[t.name], np.float32).tobytes()]}
-
+    # ---------------------------------------------------------------- fitted importance (fitsets.py)
     def _f32_rows(self, b, bt, r0, r1):
         """rows r0:r1 of base tensor bt as float32 (rows, cols) on the device"""
         cols = int(bt.shape[0])
@@ -840,64 +823,6 @@ class Packer:
         isz, dt = 2, (np.uint16 if bt.type == BF16 else np.float16)
         src = b.d.view(bt.offset + isz * r0 * cols, (n,), dt)
         return residual.float_prediction(src, F32, self.stream.handle).view(0, (r1 - r0, cols), np.float32)
-
-    def _fit_from(self, k, tens, F, b):
-        """fit set k's importance of the inputs still waiting from the file's legacy-quant tensors
-        `tens` (their bytes in F, the device copy of the file), the base b resident (repo3.py:1276-1323):
-        per input the conditions of its tensors summed in pieces of FIT_ROWS weights, the smallest
-        eigenvector, kept where it reproduces more blocks of the last rows of the first tensor"""
-        st = self.stream.handle
-        wait, imx_all = self.fit_wait.get(k), self.imx_all
-        groups = {}
-        for t in tens:
-            e, bt = imx_all.get(t.name), b.by_name.get(t.name)
-            if wait and t.name in wait and t.type in imxfit.LS_TYPES and e is not None and bt is not None \
-                    and bt.type in (F32, F16, BF16) and len(e) == bt.shape[0]:
-                groups.setdefault(np.asarray(e, np.float32).tobytes(), []).append(t)
-        t0 = time.perf_counter()
-        for key, members in groups.items():
-            G = None
-            for t in members:
-                bt = b.by_name[t.name]
-                cols, nrow = int(bt.shape[0]), int(bt.shape[1])
-                _, qk, bs = QFUN[t.type]
-                rb, step = cols // qk * bs, max(1, FIT_ROWS // cols)
-                for r0 in range(0, nrow, step):
-                    r1 = min(nrow, r0 + step)
-                    x = self._f32_rows(b, bt, r0, r1)
-                    f = F.view(t.offset + r0 * rb, ((r1 - r0) * rb,), np.uint8)
-                    g = imxfit.ls_gram(self.gq, t.type, x, f, stream=st)
-                    G = g if G is None else G + g
-            e0 = np.frombuffer(key, np.float32)
-            e = imxfit.ls_solve(G, e0)
-            t = members[0]
-            bt = b.by_name[t.name]
-            cols, nrow = int(bt.shape[0]), int(bt.shape[1])
-            _, qk, bs = QFUN[t.type]
-            rb, n = cols // qk * bs, min(nrow, max(64, FIT_ROWS // 8 // cols))
-            x = self._f32_rows(b, bt, nrow - n, nrow)
-            f = F.view(t.offset + (nrow - n) * rb, (n * rb,), np.uint8)
-            before, after = (imxfit.equal_blocks(self.gq, t.type, x, f, v) for v in (e0, e))
-            names = self.by_input[key]
-            wait.difference_update(names)
-            if after > before + 0.005:
-                for nm in names:
-                    self.imx_sets[k][nm] = e
-                self.fit_done[k].append((names, e, e0, before, after))
-        self._cpu(("importance fit wall_s", time.perf_counter() - t0))
-
-    def _fit_chunk(self):
-        """the fitted importance sets as the "imx" chunk and its manifest entry, or None (repo3.py:1325-1340)"""
-        meta, data = [], []
-        for k in sorted(self.fit_done):
-            done = self.fit_done[k]
-            meta.append({"chunks": self.fit_sig[k][0], "dataset": self.fit_sig[k][1], "groups": [d[0] for d in done]})
-            data += [(e.view(np.uint32) ^ e0.view(np.uint32)).tobytes() for _, e, e0, _, _ in done]
-        self.stats["imx_fit"] = sum(len(m["groups"]) for m in meta)
-        if not self.stats["imx_fit"]:
-            return None
-        return pack({"meta": zstd.zstd_c(json.dumps(meta).encode()), "data": zstd.zstd_c(b"".join(data), 19)}), \
-            {"chunk": "imx", "sets": len(meta)}
 
     def _lane(self):
         """this zstd lane's stream, page-locked piece and device counter"""
@@ -1073,7 +998,7 @@ class Packer:
                 # shards (repo3.py:649-657)
                 best = [k for k, c in enumerate(common) if c == max(common)]
                 per_base[best[-1] if best[-1] >= len(bnames) else best[0]].append((fi, n, ts))
-            self._fit_plan(names, heads, imx_all, imx_mod.chunks(ex[imx_name]) if imx_name else None)
+            self.fits = fitsets.FitSets.plan(names, heads, imx_all, imx_mod.chunks(ex[imx_name]) if imx_name else None)
             # derived files: per base, grouped by tensor order; windows over each group's order
             jobs, plain, order_done = {}, [], []
             for bi, items in per_base.items():
@@ -1110,7 +1035,7 @@ class Packer:
                     if k and (t.name, t.type) in prev and t.nbytes >= DUP_MIN:
                         pot[j["wins_of"][t.name]] += t.nbytes
                 prev |= keys
-                info[fi] = (os.path.getsize(j["path"]), keys, j["group"], pot, self.file_set.get(fi, 0))
+                info[fi] = (os.path.getsize(j["path"]), keys, j["group"], pot, self.fits.set_of.get(fi, 0))
             porder = process_order(info, None)
             # the first file read while the bases are uploaded, their checksums and codecs started
             # (one stream each)
@@ -1201,7 +1126,9 @@ class Packer:
                 manifest["needs"] = "0.3.0"
             if self.stats["qr_grid"] or self.stats["ref"]:
                 manifest["needs"] = "0.3.0"
-            fitted = self._fit_chunk()
+            fitted = self.fits.chunk()
+            self.stats["imx_fit"] = self.fits.fitted_inputs()
+            self._cpu(("importance fit wall_s", self.fits.seconds))
             if fitted:
                 w.put(fitted[1]["chunk"], fitted[0])
                 self.sizes["fitted importance"] = len(fitted[0])
@@ -1428,7 +1355,7 @@ class Unpacker:
             imx_off[k] = o
             o += v.size
         imx_map = {k: imx_dev.view(4 * imx_off[k], (v.size,), np.float32) for k, v in imx_all.items()}
-        self.imx_sets = self._load_imx(r.get(manifest["imx_fit"]["chunk"]), imx_all) if manifest.get("imx_fit") else {}
+        self.imx_sets = fitsets.read_chunk(r.get(manifest["imx_fit"]["chunk"]), imx_all) if manifest.get("imx_fit") else {}
         # quantized files, in archive order; tensors that later files copy are kept on the device
         kept, done = {}, set()
         # largest first, a file after the files it copies tensors from (so the checksum of a big
@@ -1629,23 +1556,6 @@ class Unpacker:
                 "unchecked": [n for n, ok in results.items() if ok is None],
                 "missing": [n for n in want if n not in results], "bytes": nbytes_, "seconds": dt,
                 "GB_s": nbytes_ / dt / 1e9}
-
-    @staticmethod
-    def _load_imx(buf, imx_all):
-        """the fitted importance sets of an archive ("imx" chunk) -> {set k: {name: importance}}
-        (repo3.py:1342-1355)"""
-        ch = unpack(memoryview(bytes(buf)))
-        meta = json.loads(zstd.decompress(ch["meta"]))
-        raw, o, sets = zstd.decompress(ch["data"]), 0, {}
-        for k, m in enumerate(meta, 1):
-            sets[k] = {}
-            for names in m["groups"]:
-                e0 = np.asarray(imx_all[names[0]], np.float32)
-                e = (np.frombuffer(raw, np.uint32, len(e0), o) ^ e0.view(np.uint32)).view(np.float32)
-                o += e.nbytes
-                for n in names:
-                    sets[k][n] = e
-        return sets
 
     def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map, digest=False):
         """file i's bytes from its residual (in `resid`, rebuilt in place) on the device -> (phase

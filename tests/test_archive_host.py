@@ -347,3 +347,67 @@ def test_catalog_digests_of_files(tmp_path):
     assert repo.file_digest(str(p), "sha256", chunk=1000) == hashlib.sha256(data).hexdigest()
     assert repo.file_digest(str(p), "blake3", chunk=1000) == ob.hexdigest(data)
     assert repo._digest_fn("blake3")(data) == ob.hexdigest(data)
+
+
+def test_seed_choice_rules():
+    """files sharing no tensor name with a base; the senior quant left seeds every file that shares at
+    least half of its tensor names with it (repo3.py:1359-1372)"""
+    from types import SimpleNamespace as T
+
+    def ts(names, ttype, numel=256, nbytes=None):
+        return [T(name=n, type=ttype, numel=numel, nbytes=nbytes if nbytes is not None else numel) for n in names]
+    a = ["blk.0.w", "blk.1.w", "blk.2.w", "blk.3.w"]
+    b = ["enc.0", "enc.1"]
+    derived = {
+        "A-Q4.gguf": ts(a, 12, nbytes=144),           # 4.5 bits per weight
+        "A-Q8.gguf": ts(a, 8, nbytes=272),            # 8.5: the seed of model A
+        "A-half.gguf": ts(a[:2] + ["x.0", "x.1"], 12, nbytes=144),  # half of its names are A's: model A
+        "B-Q6.gguf": ts(b, 14, nbytes=210),           # model B's only file
+        "C.gguf": ts(["tok", "out"], 8, nbytes=272),  # shares a name with the base: not seeded
+        "empty.gguf": [],
+    }
+    bases = [ts(["tok", "norm"], 30, nbytes=512)]
+    assert repo.pick_seeds(bases, derived) == ["A-Q8.gguf", "B-Q6.gguf"]
+    # equal bits per weight: the larger name wins
+    derived2 = {"m-1.gguf": ts(a, 8, nbytes=272), "m-2.gguf": ts(a, 8, nbytes=272)}
+    assert repo.pick_seeds([], derived2) == ["m-2.gguf"]
+    # a third of the names shared is another model
+    derived3 = {"p.gguf": ts(["u", "v", "w"], 8, nbytes=272), "q.gguf": ts(["u", "y", "z"], 12, nbytes=144)}
+    assert repo.pick_seeds([], derived3) == ["p.gguf", "q.gguf"]
+
+
+def test_fit_sets_plan_and_chunk_round_trip():
+    """sets by (chunk count, dataset) in order of their first file; every input a set's legacy-quant
+    tensors use waits for its fit; the "imx" chunk holds the fitted vectors as XOR of the published
+    bits and reads back; no chunk without a kept fit"""
+    from types import SimpleNamespace as T
+    from seedpack_amd import fitsets
+    e_gate = np.linspace(0.5, 2.0, 64).astype(np.float32)
+    e_attn = np.linspace(1.0, 3.0, 64).astype(np.float32)
+    imx = {"blk.0.ffn_gate": e_gate, "blk.0.ffn_up": e_gate.copy(), "blk.0.attn_q": e_attn, "blk.0.attn_k": e_attn.copy()}
+    heads = {
+        "a.gguf": ({"quantize.imatrix.chunks_count": 45, "quantize.imatrix.dataset": "x"},
+                   [T(name="blk.0.ffn_gate", type=2), T(name="blk.0.attn_q", type=12)]),
+        "b.gguf": ({"quantize.imatrix.chunks_count": 1251}, [T(name="blk.0.ffn_gate", type=2)]),
+        "c.gguf": ({"quantize.imatrix.chunks_count": 45, "quantize.imatrix.dataset": "x"},
+                   [T(name="blk.0.attn_k", type=7)]),
+        "d.gguf": ({"quantize.imatrix.chunks_count": 45, "quantize.imatrix.dataset": "y"}, []),
+        "e.gguf": ({}, [T(name="blk.0.ffn_up", type=2)]),
+    }
+    names = list(heads)
+    fs = fitsets.FitSets.plan(names, heads, imx, 1251)
+    assert fs.set_of == {0: 1, 2: 1, 3: 2}
+    assert (fs.sets[1].chunks, fs.sets[1].dataset, fs.sets[2].dataset) == (45, "x", "y")
+    assert fs.sets[1].waiting == {"blk.0.ffn_gate", "blk.0.ffn_up", "blk.0.attn_q", "blk.0.attn_k"}
+    assert fs.waiting(1) and not fs.waiting(2) and not fs.waiting(0)
+    assert fs.chunk() is None
+    fit = (e_gate * np.float32(1.25)).astype(np.float32)
+    fs.sets[1].kept.append(fitsets.Fit(["blk.0.ffn_gate", "blk.0.ffn_up"], fit, e_gate, 0.5, 0.9))
+    body, entry = fs.chunk()
+    assert entry == {"chunk": "imx", "sets": 2}
+    back = fitsets.read_chunk(body, imx)
+    assert set(back) == {1, 2} and back[2] == {}
+    assert set(back[1]) == {"blk.0.ffn_gate", "blk.0.ffn_up"} and np.array_equal(back[1]["blk.0.ffn_up"], fit)
+    assert fs.importance(1)["blk.0.ffn_gate"] is fit and fs.importance(3) == {}
+    # no published chunk count: no sets
+    assert fitsets.FitSets.plan(names, heads, imx, None).sets == {}
