@@ -41,11 +41,30 @@ def alg_bytes(t, nw, npr, imx):
     return 2 * nw + nw // qk * bs + (4 * npr if imx else 0)
 
 
-def cpu_baseline(tensors, target_s=12.0):
-    """the reference's C quantizers (oracle/_ref) on the host cores, on the first rows of the
-    embedding (a bounded sample of the same workload)"""
+def _timed_sample(run, x, budget_s):
+    """run(rows) on a row sample of x sized so that it takes about budget_s (measured on 1/16 of the
+    rows first) -> (rows, seconds)"""
+    probe = max(1, x.shape[0] // 16)
+    t0 = time.perf_counter()
+    run(x[:probe])
+    per_row = (time.perf_counter() - t0) / probe
+    rows = int(min(x.shape[0], max(probe, budget_s / max(per_row, 1e-9))))
+    t0 = time.perf_counter()
+    run(x[:rows])
+    return rows, time.perf_counter() - t0
+
+
+def cpu_baseline(tensors, target_s=12.0, type_s=1.5):
+    """the reference's C quantizers (oracle/_ref) on the host cores: the configuration-2 family on the
+    first rows of the embedding (the line's figure, a bounded sample of the same workload), then per
+    type on a bounded row sample of its own configuration's tensor (Q8_0 / Q4_0: configuration 1 without
+    imatrix; the K-quants: the embedding with its imatrix; the i-quants: the configuration-3
+    4096x12288 Student-t tensor with its imatrix); and the QR encoder of configuration 1 as the
+    oracle's single-core numpy port (oracle/qr.py)"""
+    from oracle import qr as oqr
     from oracle import ref
     from seedpack_amd import synth
+    from seedpack_amd.requant import NAMES
     if not ref.available():
         return None
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
@@ -58,14 +77,43 @@ def cpu_baseline(tensors, target_s=12.0):
     rate = 5 * x.size / (time.perf_counter() - t0)             # weights/s over the family
     rows = int(min(w_emb.shape[0], max(1024, target_s * rate / 5 / w_emb.shape[1])))
     xe = synth.bf16_to_f32(w_emb[:rows]).reshape(rows, w_emb.shape[1])
-    t0 = time.perf_counter()
+    per_type, total = {}, 0.0
     for t in KTYPES:
+        t1 = time.perf_counter()
         ref.quantize(t, xe, imx_emb, threads=threads)
-    dt = time.perf_counter() - t0
-    return {"value": round(5 * 2 * xe.size / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "reference",
+        dt_t = time.perf_counter() - t1
+        total += dt_t
+        per_type[NAMES[t]] = {"GB_s": round(2 * xe.size / dt_t / 1e9, 4), "sample": f"token_embd rows 0..{rows}, imatrix"}
+    # configuration 1 (no imatrix) and configuration 3 (imatrix), each type on its own bounded sample
+    w1, _ = synth.tensor(1, 0)
+    x1 = synth.bf16_to_f32(w1).reshape(w1.shape)
+    w3, imx3 = synth.tensor(3, 0)
+    x3 = synth.bf16_to_f32(w3).reshape(w3.shape)
+    for t, xs, imx, what in [(8, x1, None, "cfg1 3072x1024"), (2, x1, None, "cfg1 3072x1024")] + \
+                            [(t, x3, imx3, "cfg3 4096x12288, imatrix") for t in synth.TYPES[3]]:
+        r, dt_t = _timed_sample(lambda xx: ref.quantize(t, xx, imx, threads=threads), xs, type_s)
+        per_type[NAMES[t]] = {"GB_s": round(2 * r * xs.shape[1] / dt_t / 1e9, 4), "sample": f"{what}: rows 0..{r}"}
+    # QR encode of configuration 1 (Q8_0 / Q4_0 prediction, 1% of the blocks perturbed): the oracle's port
+    qr_cpu = {}
+    sd = w1.reshape(-1).view(np.uint8).tobytes()
+    for t, bs in ((8, 34), (2, 18)):
+        P = ref.quantize(t, x1, None, threads=threads)
+        g = np.random.Generator(np.random.PCG64(1234 + t))
+        Fb = P.copy().reshape(-1, bs)
+        idx = g.choice(len(Fb), size=len(Fb) // 100, replace=False)
+        Fb[idx, g.integers(0, bs, len(idx))] ^= np.uint8(0x10)
+        t1 = time.perf_counter()
+        oqr.encode(t, Fb.tobytes(), P.tobytes(), sd, 30, w1.shape[1])
+        dt_t = time.perf_counter() - t1
+        qr_cpu[NAMES[t]] = {"encode_GB_s_bf16": round(2 * w1.size / dt_t / 1e9, 4), "encode_s": round(dt_t, 3)}
+    return {"value": round(5 * 2 * xe.size / total / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "reference",
             "sample": f"token_embd rows 0..{rows} ({xe.size} weights) x Q2_K..Q6_K with imatrix, "
-                      f"oracle/_ref built from the reference's ggml-quants.c, {threads} threads, {dt:.1f} s",
-            "cpu_model": _cpu_model()}
+                      f"oracle/_ref built from the reference's ggml-quants.c, {threads} threads, {total:.1f} s",
+            "cpu_model": _cpu_model(), "per_type": per_type,
+            "per_type_note": f"GB/s of BF16 in, oracle/_ref (the reference's own C quantizers), {threads} threads, rows "
+                             "split into contiguous parts as the reference's CPU entry does (requant.py:115-134)",
+            "qr_cfg1": qr_cpu, "qr_cfg1_note": "QR encode of the whole configuration-1 tensor by oracle/qr.py, the "
+                                                "oracle's numpy restatement (kind: port), one core"}
 
 
 def _profiled_traffic(kernel):
