@@ -132,8 +132,9 @@ struct TileOut {
 
 // Copies `nbytes` (even) from an LDS tile to global memory at dst (2-byte aligned), using every
 // thread of the workgroup; dword stores when dst is 4-byte aligned.
-__device__ __forceinline__ void store_tile(const uint16_t* __restrict__ lds, uint8_t* __restrict__ dst, int nbytes) {
-    const int tid = threadIdx.x, nt = blockDim.x;
+__device__ __forceinline__ void store_tile(const uint16_t* __restrict__ lds, uint8_t* __restrict__ dst, int nbytes,
+                                           int tid = threadIdx.x) {
+    const int nt = blockDim.x;
     if ((reinterpret_cast<uintptr_t>(dst) & 3u) == 0) {
         const int nw = nbytes >> 2;
         const uint32_t* l32 = reinterpret_cast<const uint32_t*>(lds);

@@ -933,6 +933,10 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
         reinterpret_cast<float4*>(nbw[threadIdx.x / 64].rec[threadIdx.x % 64])[C::D / 4] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
+    // the thread's index rebuilt from the wave's index (a scalar) and the lane where it is needed again
+    // after the searches, so that no register holds it through them
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    auto tid = [&] { return wave * 64 + (int)__lane_id(); };
     const int lsb = threadIdx.x / G, sub = threadIdx.x % G;
     const int64_t sb0 = (int64_t)blockIdx.x * SBW;
     const int64_t sb = sb0 + lsb;
@@ -956,10 +960,26 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
         }
     };
     // the IQ1 searches hold sorted copies and prefix sums: x and w are read again afterwards (same
-    // values) rather than kept in registers through them
+    // values) rather than kept in registers through them, from the element offset, importance offset
+    // and sigma^2 parked in this thread's LDS slot (no register holds them through the search)
+    __shared__ uint4 stash[IQ1 ? WG : 1];
+    if constexpr (IQ1) {
+        const uint64_t eo = (uint64_t)(sbc * 256 + sub * N);
+        stash[threadIdx.x] = make_uint4((uint32_t)eo, (uint32_t)(eo >> 32), (uint32_t)((sbc % sbpr) * 256 + sub * N),
+                                        __float_as_uint(sigma2));
+    }
     auto reload = [&](float (&xv)[N], float (&wv)[N]) {
-        load_weights<N>(src, kind, sbc * 256 + sub * N, xv);
-        weights(xv, wv);
+        const uint4 st = stash[tid()];
+        load_weights<N>(src, kind, (int64_t)(((uint64_t)st.y << 32) | st.x), xv);
+        const float s2 = __uint_as_float(st.w);
+        if (imx) {
+            const float* qw = imx + st.z;
+#pragma unroll
+            for (int i = 0; i < N; ++i) wv[i] = qw[i] * sqrtf(s2 + xv[i] * xv[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < N; ++i) wv[i] = xv[i] * xv[i];
+        }
     };
     float w[N];
     weights(x, w);
@@ -1030,11 +1050,12 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
 #pragma unroll
     for (int k = 0; k < 4; ++k) pk.signs[k] = r.empty ? 0u : r.signs[k];
     if constexpr (!IQ1) __syncthreads();   // every lane's search has read its sqrt(w) column
-    park[lsb][sub] = pk;
+    const int lsb2 = tid() / G, sub2 = tid() % G;
+    park[lsb2][sub2] = pk;
     __syncthreads();
-    if (active && sub == 0) {
-        TileOut o{otile + lsb * (C::BS / 2)};
-        const Park* P = park[lsb];
+    if (sb0 + lsb2 < nsb && sub2 == 0) {
+        TileOut o{otile + lsb2 * (C::BS / 2)};
+        const Park* P = park[lsb2];
         for (int j = 0; j < C::BS; j += 2) o.put16(j, 0);
         if constexpr (K == K_IQ2_XXS) {
             // d, then per 32 weights: u32 of 4 grid indices, u32 of 4 x 7 sign bits | scale << 28
@@ -1147,7 +1168,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
     }
     __syncthreads();
     const int nb = (int)(nsb - sb0 < SBW ? nsb - sb0 : SBW);
-    store_tile(otile, dst + sb0 * C::BS, nb * C::BS);
+    store_tile(otile, dst + sb0 * C::BS, nb * C::BS, tid());
 }
 
 template <int K>
