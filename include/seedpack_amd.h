@@ -279,6 +279,50 @@ int spa_dm_solve(const float* A, const float* b, int64_t n, int k, float* x, voi
 int spa_dm_log2(const double* x, int64_t n, double* y, void* stream);
 int spa_dm_exp2(const double* x, int64_t n, double* y, void* stream);
 
+/* ---- M6 Q8_0 codec (codecs_gguf's single-file method M6: gpu_codec.py's hist / encode / decode kernels
+ * and the array steps of M6GPU.compress / decompress, gpu_codec.py:33-169, :218-334). blocks: the file's
+ * Q8_0 blocks back to back (34 bytes each); meta: 24-byte records {first, nblocks, nb_row, grp, colbase,
+ * med} per tensor (gpu_codec.py:190 META_DT); tfirst: each tensor's first block; colmap: per input
+ * column its class 0..15, tensors back to back; segments of 512 blocks, 770 tables per tensor group,
+ * PB 12. */
+
+/* counts[lo | hi << 8] += 1 for blocks [first, first + nb) (the median of the scale bits, gpu_codec.py:231). */
+int spa_m6_scale_hist(const void* blocks, int64_t first, int64_t nb, uint32_t* counts, void* stream);
+/* rms[c] = sqrt(sum over rows of q^2 / nrows) per column of nrows x (nb_row * 32) weights, float32 sums
+ * in row order (gpu_codec.py:232-233 as the reference's --cpu path computes it). */
+int spa_m6_col_rms(const void* blocks, int64_t first, int64_t nrows, int nb_row, float* rms, void* stream);
+/* pos[b]: the first position of the largest |weight| of block b (gpu_codec.py:238). */
+int spa_m6_pos(const void* blocks, int64_t n, uint8_t* pos, void* stream);
+/* the number of 512-block segments of nblocks blocks */
+int spa_m6_segments(int nblocks);
+/* counts[table * 256 + symbol] += every block's symbols (gpu_codec.py:80-93). */
+int spa_m6_hist(const void* blocks, const uint8_t* pos, const void* meta, const int32_t* tfirst, int ntens,
+                const uint8_t* colmap, int nblocks, uint32_t* counts, void* stream);
+/* each segment coded into its slot of cap (>= 512 * 34 * 2 + 16) bytes, written downwards from the slot's
+ * end; out_len[s] its length (gpu_codec.py:95-124); gather with spa_qr_gather. */
+int spa_m6_encode(const void* blocks, const uint8_t* pos, const void* meta, const int32_t* tfirst, int ntens,
+                  const uint8_t* colmap, int nblocks, const uint16_t* freq, const uint32_t* cum, void* out, uint64_t cap,
+                  uint32_t* out_len, void* stream);
+/* segment s decoded from in + in_off[s] into blocks (gpu_codec.py:126-157); bytes past in_bytes read as
+ * zeros; lut from spa_rans_build_lut. */
+int spa_m6_decode(const void* in, uint64_t in_bytes, const uint64_t* in_off, const void* meta, const int32_t* tfirst,
+                  int ntens, const uint8_t* colmap, int nblocks, const uint16_t* freq, const uint32_t* cum,
+                  const uint8_t* lut, void* blocks, void* stream);
+
+/* ---- static context-mixed rANS (rans.py:55-138: _encode, _decode, _decode_o1; the coder of the CPU
+ * single-file methods M3-M5). One stream per lane; streams: 48-byte records {i64 sym_off, n, ctx_off,
+ * tab_row, out_off; i32 period, pad}: symbols sym[sym_off..+n), contexts ctx[ctx_off..+n) (decode with
+ * period > 0: the previous symbol, reset to 0 every period symbols, ctx unused), tables freq / cum rows
+ * tab_row + context (n_sym and n_sym + 1 entries, rows summing to 2^14). */
+
+/* each stream coded into out[out_off, out_off + 2n + 16), written downwards from its end; out_len its length. */
+int spa_crans_encode(const uint8_t* sym, const int32_t* ctx, int n_sym, const uint16_t* freq, const uint32_t* cum,
+                     const void* streams, int nst, void* out, uint32_t* out_len, void* stream);
+/* each stream decoded from in + out_off (bytes past in_bytes read as zeros) into sym; lut from
+ * spa_rans_build_lut_pb with pb 14. */
+int spa_crans_decode(const void* in, uint64_t in_bytes, const int32_t* ctx, int n_sym, const uint16_t* freq,
+                     const uint32_t* cum, const uint8_t* lut, const void* streams, int nst, uint8_t* sym, void* stream);
+
 /* ---- M24 BF16 codec (method m28's base codec; replaces gpu_bf16.py's bf_hist / bf_enc / bf_dec and the
  * column statistics of M24BF16GPU.compress_dev, gpu_bf16.py:36-132, :340-371). TB descriptors are 24
  * bytes {i64 off, i32 rowlen, rowbase, colbase, tab}, SG 16 bytes {i32 t, n, i64 i0} (gpu_bf16.py:271-272);

@@ -72,6 +72,19 @@ SIGNATURES = {
     "spa_xor3": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_diff_count": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spa_count_every": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "spa_m6_scale_hist": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "spa_m6_col_rms": (c_int, [c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
+    "spa_m6_pos": (c_int, [c_void_p, c_int64, c_void_p, c_void_p]),
+    "spa_m6_segments": (c_int, [c_int]),
+    "spa_m6_hist": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p]),
+    "spa_m6_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p,
+                              c_void_p, c_uint64, c_void_p, c_void_p]),
+    "spa_m6_decode": (c_int, [c_void_p, c_uint64, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p,
+                              c_void_p, c_void_p, c_void_p, c_void_p]),
+    "spa_crans_encode": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                                 c_void_p]),
+    "spa_crans_decode": (c_int, [c_void_p, c_uint64, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                 c_void_p, c_void_p]),
     "spa_m24_cols": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p]),
     "spa_m24_hist": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "spa_m24_rcp_bytes": (c_size_t, [c_int]),
