@@ -71,32 +71,57 @@ class GPUQuant:
         return dev.DeviceArray.from_host(imx, self.stream)
 
     def quantize_tensors(self, ttype, srcs, imatrices, variant=0, max_weights=1 << 28, on_result=None, device=False):
-        """srcs: list of (weights as bf16 bits (uint16) / f16 / f32, device or host array, n_per_row).
-        Returns the quantized bytes of every tensor (host numpy arrays, DeviceArrays with `device`),
-        or with on_result calls on_result(index, bytes) per tensor and returns None."""
+        """srcs: list of (weights, n_per_row); weights are bf16 bits (uint16) / f16 / f32 (device or host
+        array) or an object with `size` and `into(out)` that writes its float32 weights into the
+        DeviceArray `out` (a seed's tensor dequantized straight into the launch's input, as the
+        reference's _Dequant does, repo3.py:545-557). Consecutive tensors are handed to the device in
+        groups of at most `max_weights` weights (the `into` sources of a group share one float32
+        buffer; a larger array is quantized in row pieces); the quantizer runs once per tensor over its
+        run of blocks. Returns the quantized bytes of every tensor (host numpy arrays, DeviceArrays with
+        `device`), or with on_result calls on_result(index, bytes) per tensor as its group completes and
+        returns None (gpuquant.py:360-411)."""
         if ttype in NEED_IMATRIX and any(m is None for m in imatrices):
             raise ValueError(f"type {ttype} requires an imatrix")
         if variant >= VARIANTS.get(ttype, 1):
             raise ValueError(f"type {ttype} has no variant {variant}")
         _, qk, bs = QFUN[ttype]
-        out = []
-        for i, ((a, npr), imx) in enumerate(zip(srcs, imatrices)):
-            x = self._dev(a)
-            w = self._imx(imx, npr)
-            nrow = x.size // npr
-            rb = npr // qk * bs
-            y = dev.DeviceArray(nrow * rb, np.uint8)
-            step = max(1, max_weights // npr)
-            for r0 in range(0, nrow, step):
-                r1 = min(nrow, r0 + step)
-                xs = x.view(r0 * npr * x.dtype.itemsize, (r1 - r0) * npr, x.dtype)
-                ys = y.view(r0 * rb, (r1 - r0) * rb, np.uint8)
-                quantize_into(ttype, xs, npr, ys, w, variant, self.stream)
-            res = y if device else y.to_host(stream=self.stream)
-            if on_result:
-                on_result(i, res)
-            else:
-                out.append(res)
+        out, i = [], 0
+        while i < len(srcs):
+            j, n = i, 0
+            while j < len(srcs) and (j == i or n + srcs[j][0].size <= max_weights):
+                n += srcs[j][0].size
+                j += 1
+            lazy = sum(srcs[k][0].size for k in range(i, j) if hasattr(srcs[k][0], "into"))
+            X = dev.DeviceArray(lazy, np.float32) if lazy else None
+            at, done = 0, []
+            for k in range(i, j):
+                a, npr = srcs[k]
+                if hasattr(a, "into"):
+                    x = X.view(4 * at, (a.size,), np.float32)
+                    a.into(x)
+                    at += a.size
+                else:
+                    x = self._dev(a)
+                w = self._imx(imatrices[k], npr)
+                nrow = x.size // npr
+                if nrow * npr != x.size or npr % qk:
+                    raise ValueError(f"tensor {k}: {x.size} weights are not whole rows of {npr} (type {ttype})")
+                rb = npr // qk * bs
+                y = dev.DeviceArray(nrow * rb, np.uint8)
+                step = max(1, max_weights // npr)
+                for r0 in range(0, nrow, step):
+                    r1 = min(nrow, r0 + step)
+                    xs = x.view(r0 * npr * x.dtype.itemsize, (r1 - r0) * npr, x.dtype)
+                    quantize_into(ttype, xs, npr, y.view(r0 * rb, (r1 - r0) * rb, np.uint8), w, variant, self.stream)
+                done.append(y)
+            for k, y in enumerate(done, i):
+                res = y if device else y.to_host(stream=self.stream)
+                if on_result:
+                    on_result(k, res)
+                else:
+                    out.append(res)
+            del X
+            i = j
         return None if on_result else out
 
     def dequantize(self, ttype, y, npr, out=None):
