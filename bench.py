@@ -403,7 +403,7 @@ class HbmPeak:
 
 
 def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False, reuse=False, write_only=False,
-               bases_in_hbm=None):
+               bases_in_hbm=None, blocking_waits=True):
     """configurations 4 and 5 from host files, as the reference's CLI measures them (cli.py:288-292,
     :441): a synthetic Qwen3.5-9B-shaped repository (BF16 GGUF with a 151,936-token BPE tokenizer,
     imatrix.dat, README.md, 21 quantized GGUFs made by this library's quantizers with 1% of their
@@ -448,7 +448,7 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
             return None, None
         arc = os.path.join(arc_dir, "model.seedpack")
         peak = HbmPeak().start()
-        st = repo.Packer(verbose=True, bases_in_hbm=bases_in_hbm).pack([src], arc)
+        st = repo.Packer(verbose=True, bases_in_hbm=bases_in_hbm, blocking_waits=blocking_waits).pack([src], arc)
         pk_peak = peak.stop()
         log(f"bench: pack {st['input_bytes'] / 1e9:.1f} GB -> {st['archive_bytes'] / 1e9:.2f} GB in {st['seconds']:.1f} s "
             f"= {st['GB_s']:.2f} GB/s, peak HBM {pk_peak / 1e9:.1f} GB (residuals waiting in HBM: at most "
@@ -460,7 +460,7 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
         if bases_in_hbm is False:
             want.append("model-BF16.gguf")
         peak = HbmPeak().start()
-        ex = repo.Unpacker(verbose=True, bases_in_hbm=bases_in_hbm).run(arc, out, want)
+        ex = repo.Unpacker(verbose=True, bases_in_hbm=bases_in_hbm, blocking_waits=blocking_waits).run(arc, out, want)
         up_peak = peak.stop()
         same = all(_same_file(os.path.join(src, n), os.path.join(out, n)) for n in want)
         log(f"bench: extract {ex['bytes'] / 1e9:.2f} GB in {ex['seconds']:.2f} s = {ex['GB_s']:.2f} GB/s, "
@@ -682,6 +682,9 @@ def main():
     ap.add_argument("--bases-host", action="store_true",
                     help="--pack with the BF16 base kept in host memory (pack) and decoded window by window from the "
                          "archive (extract, which writes the base file too), as for a base bigger than HBM")
+    ap.add_argument("--spin-waits", action="store_true",
+                    help="--pack with the library's waits for the device spinning (the runtime's stream "
+                         "synchronisation) instead of blocking on an event")
     ap.add_argument("--q8", action="store_true",
                     help="only the Q8_0 codec (a seed's Q8_0 part) on a Qwen3.5-9B-shaped Q8_0 file; prints its "
                          "result, no JSON line")
@@ -695,7 +698,8 @@ def main():
     if a.pack or a.unpack or a.write_repo:
         files = a.pack_files.split(",") if a.pack_files else None
         pk, upk = repo_cfg45(layers=a.pack_layers, files=files, root=a.repo_dir, reuse=a.reuse_repo,
-                             write_only=a.write_repo, bases_in_hbm=False if a.bases_host else None)
+                             write_only=a.write_repo, bases_in_hbm=False if a.bases_host else None,
+                             blocking_waits=not a.spin_waits)
         if not a.write_repo:
             print(json.dumps({"pack_cfg4": pk, "unpack_cfg5": upk}))
         return None

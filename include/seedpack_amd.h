@@ -37,6 +37,11 @@ extern "C" {
 const char* spa_last_error(void);
 int spa_device_count(int* n);
 int spa_set_device(int device);
+/* How the library's waits (spa_stream_synchronize, spa_memcpy_h2d / d2h) wait for the device: 0 the
+ * runtime's stream synchronisation (it spins a core until the work is done), 1 an event recorded and
+ * polled with sleeps of 20 to 500 us between polls (the core free for host work). Process-wide. No
+ * reference counterpart: the packer and the unpacker, whose host side is CPU-bound, use 1. */
+int spa_set_sync_mode(int blocking);
 int spa_get_device(int* device);
 int spa_malloc(void** ptr, size_t nbytes);
 int spa_free(void* ptr);
@@ -80,6 +85,18 @@ int spa_synth_normal_bf16(void* dst, int64_t n, uint64_t seed, float std, void* 
  * its target's blocks. */
 int spa_perturb_blocks(void* dst, int64_t nblocks, int block_bytes, uint32_t per_million, uint64_t seed,
                        void* stream);
+
+/* ---- host helpers ---- */
+
+/* Bytes that `count` consecutive GGUF strings (uint64 length, then the bytes) take from p, or
+ * UINT64_MAX when they would run past `avail`: the GGUF header reader steps over a tokenizer's string
+ * arrays with it (gguf_reader.py:47-121 reads them item by item). Host memory; no device call. */
+uint64_t spa_gguf_strings_bytes(const void* p, uint64_t avail, uint64_t count);
+
+/* CRC-32 of n bytes as zlib.crc32(data, crc) computes it (crc: the previous result, 0 to start): the
+ * container's chunk checksums (container.py:59, :85, :162 compute them with zlib.crc32). Host memory,
+ * carry-less multiplication folding where the CPU has it. */
+uint32_t spa_crc32(uint32_t crc, const void* data, size_t n);
 
 /* ---- quantizers ---- */
 

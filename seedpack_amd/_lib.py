@@ -21,6 +21,7 @@ SIGNATURES = {
     "spa_last_error": (ctypes.c_char_p, []),
     "spa_device_count": (c_int, [ctypes.POINTER(c_int)]),
     "spa_set_device": (c_int, [c_int]),
+    "spa_set_sync_mode": (c_int, [c_int]),
     "spa_get_device": (c_int, [ctypes.POINTER(c_int)]),
     "spa_malloc": (c_int, [ctypes.POINTER(c_void_p), c_size_t]),
     "spa_free": (c_int, [c_void_p]),
@@ -46,6 +47,8 @@ SIGNATURES = {
     "spa_synth_normal_bf16": (c_int, [c_void_p, c_int64, c_uint64, c_float, c_void_p]),
     "spa_perturb_blocks": (c_int, [c_void_p, c_int64, c_int, ctypes.c_uint32, c_uint64, c_void_p]),
     "spa_dequantize": (c_int, [c_int, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "spa_gguf_strings_bytes": (c_uint64, [c_void_p, c_uint64, c_uint64]),
+    "spa_crc32": (ctypes.c_uint32, [ctypes.c_uint32, c_void_p, c_size_t]),
     "spa_row_size": (c_size_t, [c_int, c_int64]),
     "spa_type_variants": (c_int, [c_int]),
     "spa_quantize": (c_int, [c_int, c_int, c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -1,4 +1,5 @@
-"""Builds libseedpack_amd.so (HIP, gfx950) in-tree from seedpack_amd/csrc/*.hip.
+"""Builds libseedpack_amd.so (HIP, gfx950) in-tree from seedpack_amd/csrc/*.hip, plus the host-only
+C++ sources seedpack_amd/csrc/*.cpp (built with the host compiler).
 
 Every translation unit is compiled with IEEE float semantics: no FMA contraction, no fast-math,
 correctly rounded division and square root, f32 denormals kept, and packed-FP32 instruction
@@ -31,16 +32,24 @@ CFLAGS = [
 ]
 
 
+HOSTCXX = os.environ.get("CXX") or shutil.which("g++") or "c++"
+HOST_CFLAGS = ["-O3", "-fPIC", "-std=c++17", "-Wall"]
+
+
 def sources():
-    return sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+    return sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
 def _compile(src):
-    obj = os.path.join(OBJ, src[:-4] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    stem, ext = os.path.splitext(src)
+    obj = os.path.join(OBJ, stem + (".o" if ext == ".hip" else "_host.o"))
+    if ext == ".hip":
+        cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    else:
+        cmd = [HOSTCXX, *HOST_CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+        raise RuntimeError(f"{os.path.basename(cmd[0])} failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     # hipcc's host pass does not know the packed-fp32 feature; that warning is expected
     noise = [ln for ln in r.stderr.splitlines() if ln.strip() and "packed-fp32-ops" not in ln
              and "is not a recognized feature" not in ln]

@@ -17,12 +17,12 @@ import os
 import queue
 import struct
 import threading
-import zlib
 from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
 from . import zstd
+from ._lib import lib
 
 MAGIC = b"SEEDPACK"
 VERSION = 1
@@ -78,16 +78,22 @@ def crc32_combine(crc1, crc2, len2):
     return _mulmod(_xpow8(len2), crc1) ^ crc2
 
 
-_POOL = ThreadPoolExecutor(8)
+_POOL = ThreadPoolExecutor(8, "spa-container")
+
+
+def crc32(buf, crc=0):
+    """zlib.crc32(buf, crc), by the library's carry-less-multiplication CRC (the interpreter released)"""
+    a = np.frombuffer(buf, np.uint8) if not isinstance(buf, np.ndarray) else buf.reshape(-1).view(np.uint8)
+    return lib().spa_crc32(crc, a.ctypes.data if a.size else None, a.size)
 
 
 def crc32_parallel(buf):
-    """CRC32 of a large buffer: pieces on the pool (zlib releases the interpreter), combined"""
+    """CRC32 of a large buffer: pieces on the pool, combined"""
     mv = memoryview(buf).cast("B")
     if len(mv) <= 2 * PIECE:
-        return zlib.crc32(mv)
+        return crc32(mv)
     offs = range(0, len(mv), PIECE)
-    crcs = list(_POOL.map(lambda o: zlib.crc32(mv[o:o + PIECE]), offs))
+    crcs = list(_POOL.map(lambda o: crc32(mv[o:o + PIECE]), offs))
     crc = 0
     for o, c in zip(offs, crcs):
         crc = crc32_combine(crc, c, min(PIECE, len(mv) - o))
@@ -151,7 +157,7 @@ class Writer:
         off, n, crc = self.f.tell(), 0, 0
         for p in parts:
             b = _bytes_of(p)
-            crc = crc32_combine(crc, crc32_parallel(b), len(b)) if len(b) > 2 * PIECE else zlib.crc32(b, crc)
+            crc = crc32_combine(crc, crc32_parallel(b), len(b)) if len(b) > 2 * PIECE else crc32(b, crc)
             self.f.write(b)
             n += len(b)
         self.chunks[name] = [off, n, crc]
@@ -232,7 +238,7 @@ class ChunkStream:
                 n += len(head)
             elif kind == "data":
                 b = _bytes_of(data)
-                crc = zlib.crc32(b, crc)
+                crc = crc32(b, crc)
                 f.write(b)
                 n += len(b)
             elif kind == "end":
@@ -244,7 +250,7 @@ class ChunkStream:
                     f.write(data)
                     f.seek(end)
                     head = bytes(data)
-                self.w.chunks[self.name] = [off, n, crc32_combine(zlib.crc32(head), crc, n - len(head))]
+                self.w.chunks[self.name] = [off, n, crc32_combine(crc32(head), crc, n - len(head))]
                 return
             else:
                 raise IOError(f"chunk {self.name}: its producer stopped")

@@ -1,6 +1,9 @@
 // C ABI entry points: argument checking, type dispatch and runtime plumbing.
+#include <atomic>
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
+#include <time.h>
 
 #include "../../include/seedpack_amd.h"
 #include "launch.h"
@@ -49,6 +52,40 @@ int spa_device_count(int* n) {
     return SPA_OK;
 }
 int spa_set_device(int device) { SPA_HIP_TRY(hipSetDevice(device)); return SPA_OK; }
+// How the library's own waits (stream synchronisation, the copies to and from the host) wait. The
+// runtime's stream synchronisation spins the calling core until the work is done (an event made with
+// hipEventBlockingSync spins as well once the device is in use); blocking waits record an event and
+// poll it, sleeping between polls (20 us doubling to 500 us), so the core is free for host work at the
+// cost of at most one sleep of latency per wait.
+static std::atomic<int> g_blocking{0};
+
+static hipError_t wait_stream(hipStream_t s) {
+    if (!g_blocking.load(std::memory_order_relaxed)) return hipStreamSynchronize(s);
+    thread_local hipEvent_t ev = nullptr;   // one per thread and device (kept to the process's end)
+    thread_local int ev_dev = -1;
+    int d = 0;
+    hipError_t e = hipGetDevice(&d);
+    if (e != hipSuccess) return e;
+    if (!ev || ev_dev != d) {
+        e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess) { ev = nullptr; return e; }
+        ev_dev = d;
+    }
+    e = hipEventRecord(ev, s);
+    if (e != hipSuccess) return e;
+    for (unsigned us = 20;; us = us < 250 ? 2 * us : 500) {
+        e = hipEventQuery(ev);
+        if (e != hipErrorNotReady) return e;
+        struct timespec ts = {0, (long)us * 1000};
+        nanosleep(&ts, nullptr);
+    }
+}
+
+int spa_set_sync_mode(int blocking) {
+    if (blocking != 0 && blocking != 1) return fail(SPA_ERR_ARG, "spa_set_sync_mode: %d", blocking);
+    g_blocking.store(blocking);
+    return SPA_OK;
+}
 int spa_get_device(int* device) {
     if (!device) return fail(SPA_ERR_ARG, "spa_get_device: null out pointer");
     SPA_HIP_TRY(hipGetDevice(device));
@@ -68,12 +105,12 @@ int spa_host_alloc(void** ptr, size_t nbytes) {
 int spa_host_free(void* ptr) { SPA_HIP_TRY(hipHostFree(ptr)); return SPA_OK; }
 int spa_memcpy_h2d(void* dst, const void* src, size_t n, void* s) {
     SPA_HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, (hipStream_t)s));
-    SPA_HIP_TRY(hipStreamSynchronize((hipStream_t)s));
+    SPA_HIP_TRY(wait_stream((hipStream_t)s));
     return SPA_OK;
 }
 int spa_memcpy_d2h(void* dst, const void* src, size_t n, void* s) {
     SPA_HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, (hipStream_t)s));
-    SPA_HIP_TRY(hipStreamSynchronize((hipStream_t)s));
+    SPA_HIP_TRY(wait_stream((hipStream_t)s));
     return SPA_OK;
 }
 int spa_memcpy_d2d(void* dst, const void* src, size_t n, void* s) {
@@ -83,7 +120,7 @@ int spa_memcpy_d2d(void* dst, const void* src, size_t n, void* s) {
 int spa_memset(void* p, int v, size_t n, void* s) { SPA_HIP_TRY(hipMemsetAsync(p, v, n, (hipStream_t)s)); return SPA_OK; }
 int spa_stream_create(void** s) { SPA_HIP_TRY(hipStreamCreateWithFlags((hipStream_t*)s, hipStreamNonBlocking)); return SPA_OK; }
 int spa_stream_destroy(void* s) { SPA_HIP_TRY(hipStreamDestroy((hipStream_t)s)); return SPA_OK; }
-int spa_stream_synchronize(void* s) { SPA_HIP_TRY(hipStreamSynchronize((hipStream_t)s)); return SPA_OK; }
+int spa_stream_synchronize(void* s) { SPA_HIP_TRY(wait_stream((hipStream_t)s)); return SPA_OK; }
 int spa_device_synchronize(void) { SPA_HIP_TRY(hipDeviceSynchronize()); return SPA_OK; }
 int spa_event_create(void** e) { SPA_HIP_TRY(hipEventCreate((hipEvent_t*)e)); return SPA_OK; }
 int spa_event_destroy(void* e) { SPA_HIP_TRY(hipEventDestroy((hipEvent_t)e)); return SPA_OK; }
@@ -95,6 +132,20 @@ int spa_event_elapsed_ms(float* ms, void* a, void* b) {
     return SPA_OK;
 }
 int spa_mem_info(size_t* f, size_t* t) { SPA_HIP_TRY(hipMemGetInfo(f, t)); return SPA_OK; }
+
+uint64_t spa_gguf_strings_bytes(const void* p, uint64_t avail, uint64_t count) {
+    // GGUF strings: a little-endian uint64 length, then that many bytes
+    const unsigned char* b = static_cast<const unsigned char*>(p);
+    uint64_t pos = 0;
+    for (uint64_t i = 0; i < count; ++i) {
+        if (!b || avail - pos < 8) return UINT64_MAX;
+        uint64_t n;
+        memcpy(&n, b + pos, 8);
+        if (n > avail - pos - 8) return UINT64_MAX;
+        pos += 8 + n;
+    }
+    return pos;
+}
 
 size_t spa_row_size(int t, int64_t npr) {
     const int qk = spa::type_qk(t), bs = spa::type_bs(t);

@@ -202,6 +202,21 @@ def set_device(device):
     check(lib().spa_set_device(int(device)))
 
 
+_sync_lock = threading.Lock()
+_blocking = [0]
+
+
+def set_blocking_waits(on):
+    """the library's waits for the device (stream synchronisation, host copies) poll an event and sleep
+    between polls (True) or spin in the runtime's stream synchronisation (False); process-wide -> the
+    previous setting"""
+    with _sync_lock:
+        prev = bool(_blocking[0])
+        check(lib().spa_set_sync_mode(1 if on else 0))
+        _blocking[0] = 1 if on else 0
+        return prev
+
+
 def mem_info():
     f, t = ctypes.c_size_t(), ctypes.c_size_t()
     check(lib().spa_mem_info(ctypes.byref(f), ctypes.byref(t)))

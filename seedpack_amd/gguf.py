@@ -4,13 +4,15 @@ Reading follows the GGUF v2/v3 layout that seedpack/gguf_reader.py:47-121 parses
 tensor count, key/value count, the key/value pairs (GGUF value types 0-12), the tensor table (name,
 dimensions in ggml order, type, offset from the data start), the data start aligned to
 `general.alignment` (default 32). `spans[key]` is the byte span of a value (its type tag excluded),
-which the base codec's header coder uses to find the tokenizer arrays. With light=True, string arrays
-of more than 64 items (vocabularies, merges) are skipped and read as None.
+which the base codec's header coder uses to find the tokenizer arrays. With light=True, arrays of more
+than 64 items (vocabularies, merges, token types) are skipped and read as None.
 """
 import struct
 from dataclasses import dataclass
 
 import numpy as np
+
+from ._lib import lib
 
 F32, F16, Q8_0, BF16 = 0, 1, 8, 30
 TYPE_NAMES = {0: "F32", 1: "F16", 2: "Q4_0", 3: "Q4_1", 6: "Q5_0", 7: "Q5_1", 8: "Q8_0", 10: "Q2_K", 11: "Q3_K",
@@ -97,15 +99,21 @@ class GGUF:
         it, n = self._get("I"), self._get("Q")
         if it in _SCALARS:
             dt = np.dtype("<" + _SCALARS[it])
+            if self.light and n > 64:
+                if self._pos + n * dt.itemsize > len(self._mv):
+                    raise ValueError("GGUF array runs past the end of the data")
+                self._pos += n * dt.itemsize
+                return None
             v = np.frombuffer(self._mv, dt, n, self._pos).tolist()
             self._pos += n * dt.itemsize
             return v
         if it == T_STRING:
             if self.light and n > 64:
-                pos, mv = self._pos, self._mv
-                for _ in range(n):
-                    pos += 8 + struct.unpack_from("<Q", mv, pos)[0]
-                self._pos = pos
+                at = np.frombuffer(self._mv, np.uint8)
+                k = lib().spa_gguf_strings_bytes(at.ctypes.data + self._pos, at.size - self._pos, n)
+                if k == 2 ** 64 - 1:
+                    raise ValueError("GGUF string array runs past the end of the data")
+                self._pos += k
                 return None
             return [self._string() for _ in range(n)]
         return [self._value(it) for _ in range(n)]

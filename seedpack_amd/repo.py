@@ -169,13 +169,32 @@ def windows(nbytes_, window=WINDOW, pred=None, pred_window=PRED_WINDOW):
     return list(zip(cuts, cuts[1:] + [len(nbytes_)])) if nbytes_ else []
 
 
-def _read_into(path, out, off=0, pool=None):
-    """bytes [off, off + len(out)) of a file into the writable uint8 array `out`, in parallel pieces"""
+def _nice_thread(inc):
+    """raise the calling thread's nice value by inc (Linux keeps one per thread)"""
+    if inc > 0 and hasattr(os, "setpriority"):
+        try:
+            tid = threading.get_native_id()
+            os.setpriority(os.PRIO_PROCESS, tid, os.getpriority(os.PRIO_PROCESS, tid) + inc)
+        except OSError:
+            pass
+
+
+def _read_into(path, out, off=0, pool=None, cpu=None):
+    """bytes [off, off + len(out)) of a file into the writable uint8 array `out`, in parallel pieces;
+    cpu(seconds) is told each piece's thread CPU time"""
     n = out.size
     step = 64 << 20
     fd = os.open(path, os.O_RDONLY)
     try:
         def piece(o):
+            c0 = time.thread_time()
+            try:
+                _piece(o)
+            finally:
+                if cpu is not None:
+                    cpu(time.thread_time() - c0)
+
+        def _piece(o):
             mv = memoryview(out[o:o + step])
             got = 0
             while got < len(mv):
@@ -565,9 +584,13 @@ class Packer:
     for a repository with BF16 base model(s), quantized GGUFs derived from them, an imatrix and other
     files"""
 
-    def __init__(self, level=7, verbose=False, coders=8, zstd_lanes=14, staging_bytes=24 << 30, device_bytes=None,
-                 method="m29", m30_slice=None, bases_in_hbm=None, hash_algo="blake3"):
+    def __init__(self, level=7, verbose=False, coders=8, zstd_lanes=24, staging_bytes=24 << 30, device_bytes=None,
+                 method="m29", m30_slice=None, bases_in_hbm=None, hash_algo="blake3", blocking_waits=True,
+                 io_threads=16, lane_nice=5):
         self.m30_slice = m30_slice
+        # the host side (zstd frames, the read, the hashes) is what bounds a pack: the library's waits
+        # for the device sleep instead of spinning a core while a pack runs
+        self.blocking_waits = blocking_waits
         # the catalog's checksum: BLAKE3, the reference's whenever its blake3 requirement is installed
         # (cli.py:48-53), or SHA-256, its fallback; derived files and bases in HBM are hashed there
         if hash_algo not in HASHES:
@@ -581,11 +604,16 @@ class Packer:
         self.level, self.verbose, self.method = level, verbose, method
         self.stream = dev.Stream()
         self.gq = GPUQuant(stream=self.stream.handle)
-        self.io = ThreadPoolExecutor(8)          # file reads (pieces)
-        self.hasher = ThreadPoolExecutor(8)      # file checksums
-        self.zpool = ThreadPoolExecutor(zstd_lanes)   # stage 2 of a file: its residual frame (one thread each)
-        self.reader = ThreadPoolExecutor(1)      # the next file read ahead
-        self.coders = ThreadPoolExecutor(coders)
+        self.io = ThreadPoolExecutor(io_threads, "spa-read")  # file reads (pieces), header parses
+        self.hasher = ThreadPoolExecutor(8, "spa-hash")      # file checksums
+        # stage 2 of a file: its residual frame (one thread each). The host's cores bound a pack, so the
+        # lanes run at a lower scheduling priority (nice + lane_nice, Linux keeps one per thread) than
+        # the device thread and the QR coders that feed them, except the lane of the first file
+        # processed, the largest, whose frame is the longest single-threaded job
+        self.zpool = ThreadPoolExecutor(zstd_lanes, "spa-zstd", initializer=_nice_thread, initargs=(lane_nice,))
+        self.zfirst = ThreadPoolExecutor(1, "spa-zstd-first")
+        self.reader = ThreadPoolExecutor(1, "spa-ahead")      # the next file read ahead
+        self.coders = ThreadPoolExecutor(coders, "spa-qr")
         self.pool = _PinnedPool(staging_bytes)   # page-locked: file reads
         # residuals wait in HBM for their zstd lane, within what the bases leave (set once they are
         # resident unless given)
@@ -688,6 +716,14 @@ class Packer:
             for k, v in items:
                 self.cpu[k] += v
 
+    def _timed(self, name, fn, *args):
+        """fn(*args) with its thread CPU time added to the stage `name`"""
+        c0 = time.thread_time()
+        try:
+            return fn(*args)
+        finally:
+            self._cpu((f"stage {name} cpu_s", time.thread_time() - c0))
+
     # ---------------------------------------------------------------- one derived file
     def _read_file(self, job):
         """(reader thread) the file's bytes into a page-locked buffer and its checksum started on them"""
@@ -695,7 +731,7 @@ class Packer:
         size = os.path.getsize(job["path"])
         host = self.pool.acquire(size)[:size]
         t1 = time.perf_counter()
-        _read_into(job["path"], host, pool=self.io)
+        _read_into(job["path"], host, pool=self.io, cpu=lambda dt: self._cpu(("file read pieces cpu_s", dt)))
         t2 = time.perf_counter()
         self._cpu(("file reads wall_s", t2 - t1))
         job["host"] = host
@@ -715,6 +751,7 @@ class Packer:
         pred = [(t, k) for t, k in tens if k]
         by_name = {t.name: t for t, _ in tens}
         F = self.fpool.acquire(size)
+        tm["hbm wait"] = time.perf_counter() - tm["t0"]   # for residuals still waiting for their frames
         st = self.stream.handle
         check(lib().spa_memcpy_h2d(F.ptr, host.ctypes.data, size, st))
         tm["upload"] = time.perf_counter()
@@ -790,7 +827,7 @@ class Packer:
                     self.stats["qr_grid"] += len(its) if grid else 0
                     qmeta.append([T, [t.name for t in its]])
                     qregs.append([(t.offset, t.nbytes) for t in its])
-                    qjobs.append(self.coders.submit(self._qr_job, T, items, bw.d, imx_dev if grid else None))
+                    qjobs.append(self.coders.submit(self._timed, "qr", self._qr_job, T, items, bw.d, imx_dev if grid else None))
                     held.append((qjobs[-1], [t.name for t in its], sum(out[t.name]["prediction"].nbytes for t in its)))
                     del items
             while held and sum(h[2] for h in held) > self.QR_HOLD:
@@ -884,8 +921,8 @@ class Packer:
             qchunk = pack_parts({"meta": zstd.compress(json.dumps(state["qmeta"]).encode(), 19),
                                  **{str(k): p for k, p in enumerate(qparts)}})
         t0 = tm.pop("t0")
-        self.timing.append({"file": state["entry"]["name"], "level": prm.level,
-                            **{k: (round(v, 3) if k in ("staging", "read", "qr wait") else round(v - t0, 3)) for k, v in tm.items()}})
+        self.timing.append({"file": state["entry"]["name"], "level": prm.level, "start": round(t0 - self._t_pack, 3),
+                            **{k: (round(v, 3) if k in ("staging", "read", "qr wait", "hbm wait") else round(v - t0, 3)) for k, v in tm.items()}})
         return state["entry"], qchunk, b"".join(frame)
 
     @staticmethod
@@ -902,7 +939,14 @@ class Packer:
 
     # ---------------------------------------------------------------- the repository
     def pack(self, inputs, output, tool=TOOL, created=None, force=False):
-        t0 = time.perf_counter()
+        prev = dev.set_blocking_waits(self.blocking_waits)
+        try:
+            return self._pack(inputs, output, tool, created, force)
+        finally:
+            dev.set_blocking_waits(prev)
+
+    def _pack(self, inputs, output, tool, created, force):
+        t0 = self._t_pack = time.perf_counter()
         ru0 = resource.getrusage(resource.RUSAGE_SELF)
         phases = {}
 
@@ -913,7 +957,8 @@ class Packer:
             raise ValueError("nothing to archive")
         if os.path.exists(output) and not force:
             raise FileExistsError(output)
-        heads = {n: gguf.header_of(p) for n, p in files.items() if p.lower().endswith(".gguf")}
+        ggufs = [(n, p) for n, p in files.items() if p.lower().endswith(".gguf")]
+        heads = dict(zip([n for n, _ in ggufs], self.io.map(gguf.header_of, [p for _, p in ggufs])))
         roles = {n: file_role(p, heads.get(n)) for n, p in files.items()}
         bases = {n: p for n, p in files.items() if roles[n] == "base"}
         derived = {n: p for n, p in files.items() if roles[n] == "derived"}
@@ -943,7 +988,7 @@ class Packer:
             # other files: the small ones in one lzma bundle, the big ones zstd'd one by one
             small = {n: p for n, p in extras.items() if os.path.getsize(p) <= BUNDLE_MAX}
             # (coded on a side thread; the writer takes them in chunk order when they are ready)
-            aux = ThreadPoolExecutor(1)
+            aux = ThreadPoolExecutor(1, "spa-aux")
             ex = {n: open(p, "rb").read() for n, p in small.items()}
             for n, data in ex.items():
                 hashes[n] = self.hasher.submit(self._digest, data)
@@ -1039,8 +1084,8 @@ class Packer:
             porder = process_order(info, None)
             # the first file read while the bases are uploaded, their checksums and codecs started
             # (one stream each)
-            ahead = self.reader.submit(self._read_file, jobs[porder[0]]) if porder else None
-            side = ThreadPoolExecutor(1)
+            ahead = self.reader.submit(self._timed, "read", self._read_file, jobs[porder[0]]) if porder else None
+            side = ThreadPoolExecutor(1, "spa-base")
             base_jobs = []
             # the BF16 bases in HBM when they fit beside the largest derived file and RESERVE, else
             # read window by window from host memory (seeds are always in HBM)
@@ -1064,7 +1109,7 @@ class Packer:
                     hashes[n] = blake3.device_hexdigest(b.d, stream=self.stream.handle)
                 else:
                     hashes[n] = self.hasher.submit(file_digest, p, self.hash_algo)
-                base_jobs.append(side.submit(self._code_base, b, host, "stream" if b.index == 0 else "parts"))
+                base_jobs.append(side.submit(self._timed, "base", self._code_base, b, host, "stream" if b.index == 0 else "parts"))
                 later[n] = base_jobs[-1]
             if base_jobs:
                 # chunk order of the reference: the first base (written while the files are coded),
@@ -1081,11 +1126,12 @@ class Packer:
             zjobs = {}
             for k, fi in enumerate(porder):
                 job = ahead.result()
-                ahead = self.reader.submit(self._read_file, jobs[porder[k + 1]]) if k + 1 < len(porder) else None
+                ahead = self.reader.submit(self._timed, "read", self._read_file, jobs[porder[k + 1]]) if k + 1 < len(porder) else None
                 b = allb[job["base"]]
-                state = self._device_file(job, b, imx_dev, imx_off, imx_map)
+                state = self._timed("device", self._device_file, job, b, imx_dev, imx_off, imx_map)
                 hashes[names[fi]] = job["sum"]            # (BLAKE3: computed on the device by _device_file)
-                zjobs[fi] = self.zpool.submit(self._finish_file, state)
+                lanes = self.zfirst if k == 0 else self.zpool
+                zjobs[fi] = lanes.submit(self._timed, "residual frame", self._finish_file, state)
                 log(self.verbose, f"  {state['entry']['name']}: {state['entry']['size']:,} B regrown and compared in "
                                   f"{state['tm']['regrow'] - state['tm']['t0']:.2f} s")
             phase("derived files on the device")
@@ -1159,7 +1205,9 @@ class Packer:
         phase("closed")
         return {"input_bytes": total, "archive_bytes": size, "seconds": dt, "GB_s": total / dt / 1e9,
                 "stats": dict(self.stats), "phases": phases, "files": self.timing,
-                "cpu": {"process cpu_s": round(cpu_s, 1), **{k: round(v, 1) for k, v in self.cpu.items()}},
+                "cpu": {"process cpu_s": round(cpu_s, 1), **{k: round(v, 1) for k, v in self.cpu.items()},
+                        "outside the stages cpu_s": round(cpu_s - sum(v for k, v in self.cpu.items()
+                                                                      if k.startswith("stage ") or k == "file read pieces cpu_s"), 1)},
                 "residuals_in_hbm_peak": self.fpool.peak}
 
     def _pack_m30(self, ggufs, w, later, hashes, exm):
@@ -1234,8 +1282,9 @@ class Unpacker:
     the host, uploaded, its predictions regrown and XORed in and its QR batches decoded on the device,
     then read back, checked and written"""
 
-    def __init__(self, verbose=False, staging_bytes=64 << 30, bases_in_hbm=None, verify=True):
+    def __init__(self, verbose=False, staging_bytes=64 << 30, bases_in_hbm=None, verify=True, blocking_waits=True):
         self.verbose = verbose
+        self.blocking_waits = blocking_waits      # the library's waits for the device sleep (as the Packer's)
         self.verify = verify                      # False: a catalog hash not computed here is a warning
         # the bases decoded into HBM (True), decoded window by window from the archive (False), or
         # in HBM when they fit beside the largest file to rebuild and 48 GB (None)
@@ -1250,6 +1299,13 @@ class Unpacker:
         self.ahead = ThreadPoolExecutor(2)        # the next files' residuals decompressed ahead
 
     def run(self, archive, outdir=None, patterns=None):
+        prev = dev.set_blocking_waits(self.blocking_waits)
+        try:
+            return self._run(archive, outdir, patterns)
+        finally:
+            dev.set_blocking_waits(prev)
+
+    def _run(self, archive, outdir, patterns):
         t0 = time.perf_counter()
         r, meta, manifest, algo = open_archive(archive, self.verify)
         digest = _digest_fn(algo) if algo else None

@@ -66,3 +66,31 @@ def test_noalloc_encoder_rejects_before_any_device_call():
     assert b"static scratch" in L.spa_last_error()
     assert L.spa_qr_encode_noalloc(99, None, None, None, None, None, 1, None, None, None, None, 1 << 16, None, None,
                                    None, 2, None) == -2
+
+
+def test_sync_mode_takes_only_its_two_values():
+    L = _lib.lib()
+    assert L.spa_set_sync_mode(2) == -4 and b"spa_set_sync_mode" in L.spa_last_error()
+    assert L.spa_set_sync_mode(0) == 0
+
+
+def test_crc32_equals_zlib():
+    """the host CRC-32 (carry-less folding for 64 bytes and more, a table below) against zlib.crc32:
+    every length to 300, odd offsets, chained calls, zeros and a large buffer"""
+    import zlib
+
+    import numpy as np
+
+    from seedpack_amd.container import crc32
+    g = np.random.Generator(np.random.PCG64(32))
+    for n in list(range(301)) + [511, 4096 + 17, 1 << 20]:
+        b = g.integers(0, 256, n + 5, dtype=np.uint8).tobytes()
+        for o in (0, 1, 5):
+            piece = b[o:o + n]
+            assert crc32(piece) == zlib.crc32(piece), (n, o)
+        assert crc32(b[:n], 0x12345678) == zlib.crc32(b[:n], 0x12345678), n
+        assert crc32(b[n // 3:n], crc32(b[:n // 3])) == zlib.crc32(b[:n]), n
+    z = bytes(3 << 20)
+    assert crc32(z) == zlib.crc32(z)
+    big = g.integers(0, 256, 24 << 20, dtype=np.uint8)
+    assert crc32(big) == zlib.crc32(big.tobytes())

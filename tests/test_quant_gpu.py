@@ -171,3 +171,61 @@ def test_legacy_imatrix_with_and_without_scratch(gq, t):
             assert outs[0].tobytes() == outs[1].tobytes(), (t, rows, npr, kind)
             if want is not None:
                 assert outs[0].tobytes() == want.tobytes(), (t, rows, npr, kind)
+
+
+class _Lazy:
+    """a quantized tensor as a quantizer input, dequantized into the launch's buffer (the reference's
+    _Dequant, repo3.py:545-557)"""
+
+    def __init__(self, gq, t, raw, npr):
+        self.gq, self.t, self.raw, self.npr = gq, t, raw, npr
+        self.size = raw.size // row_size(t, npr) * npr
+        self.calls = 0
+
+    def into(self, out):
+        self.calls += 1
+        self.gq.dequantize(self.t, self.raw, self.npr, out=out)
+
+
+@pytest.mark.parametrize("t", [12, 14, 16])
+def test_lazy_sources_and_launch_groups(gq, t):
+    """sources written by into(out) (a seed's dequantized tensors) and groups of several tensors per
+    device hand-over give the bytes of the same weights quantized one by one as float32 arrays; results
+    arrive in order through on_result too"""
+    say("case lazy sources", t)
+    g = np.random.Generator(np.random.PCG64(40 + t))
+    shapes = [(16, 256), (3, 512), (40, 256), (1, 1024), (9, 256)]
+    seeds = [quants.quantize(14, (g.standard_normal(s) * 0.02).astype(np.float32), None) for s in shapes]
+    lazies = [_Lazy(gq, 14, np.asarray(q, np.uint8), s[1]) for q, s in zip(seeds, shapes)]
+    imx = [g.lognormal(0, 1, s[1]).astype(np.float32) for s in shapes]
+    f32 = [gq.dequantize(14, np.asarray(q, np.uint8), s[1]).to_host().reshape(s) for q, s in zip(seeds, shapes)]
+    want = [quants.quantize(t, x, w) for x, w in zip(f32, imx)]
+    for mw in (1 << 28, 5000, 256):
+        got = gq.quantize_tensors(t, [(z, s[1]) for z, s in zip(lazies, shapes)], imx, max_weights=mw)
+        assert [a.tobytes() for a in got] == [np.asarray(w).tobytes() for w in want]
+        seen = []
+        gq.quantize_tensors(t, [(x.reshape(-1), s[1]) for x, s in zip(f32, shapes)], imx, max_weights=mw,
+                            on_result=lambda k, y: seen.append((k, y.tobytes())))
+        assert [k for k, _ in seen] == list(range(len(shapes)))
+        assert [y for _, y in seen] == [np.asarray(w).tobytes() for w in want]
+    assert all(z.calls == 3 for z in lazies)
+
+
+def test_blocking_waits_give_the_same_bytes(gq):
+    """with the library's waits blocking on an event (as the packer runs), host copies and stream
+    waits hand over the same results as the spinning waits"""
+    say("case blocking waits")
+    g = np.random.Generator(np.random.PCG64(77))
+    x = (g.standard_normal((64, 512)) * 0.02).astype(np.float32)
+    imx = g.lognormal(0, 1, 512).astype(np.float32)
+    want = np.asarray(quants.quantize(12, x, imx)).tobytes()
+    prev = dev.set_blocking_waits(True)
+    try:
+        for _ in range(3):
+            assert hip(gq, 12, x, imx).tobytes() == want
+            back = dev.DeviceArray.from_host(x.reshape(-1)).to_host()
+            assert back.tobytes() == x.tobytes()
+    finally:
+        dev.set_blocking_waits(prev)
+    assert dev.set_blocking_waits(prev) is False
+    assert hip(gq, 12, x, imx).tobytes() == want
