@@ -168,6 +168,32 @@ class SpaError(RuntimeError):
         self.code = code
 
 
+# Calls that wait for the device, allocate or free memory, or work on the host for long release the
+# interpreter lock; every other entry point only enqueues device work and keeps it: with other threads
+# running Python, releasing and re-acquiring the lock around each launch can cost far more than the
+# launch itself.
+RELEASE = {
+    "spa_malloc", "spa_free", "spa_host_alloc", "spa_host_free", "spa_memcpy_h2d", "spa_memcpy_d2h",
+    "spa_stream_create", "spa_stream_destroy", "spa_stream_synchronize", "spa_device_synchronize",
+    "spa_event_create", "spa_event_destroy", "spa_event_elapsed_ms", "spa_mem_info", "spa_device_count",
+    "spa_set_device", "spa_crc32", "spa_gguf_strings_bytes", "spa_iq_table_host", "spa_blake3",
+    "spa_b3h_new", "spa_b3h_update", "spa_b3h_final", "spa_b3h_free",
+}
+
+
+class _Lib:
+    """the library's functions: from a handle that releases the interpreter lock for RELEASE, from
+    one that keeps it for the rest"""
+
+    def __init__(self, release, keep):
+        self._release, self._keep = release, keep
+
+    def __getattr__(self, name):
+        f = getattr(self._release if name in RELEASE else self._keep, name)
+        setattr(self, name, f)
+        return f
+
+
 def lib():
     """the loaded library (raises if it has not been built)"""
     global _lib
@@ -177,12 +203,13 @@ def lib():
                 if not os.path.exists(LIB_PATH):
                     raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m seedpack_amd.build` "
                                        "(the HIP path has no CPU fallback)")
-                L = ctypes.CDLL(LIB_PATH)
-                for name, (res, args) in SIGNATURES.items():
-                    f = getattr(L, name)
-                    f.restype = res
-                    f.argtypes = args
-                _lib = L
+                handles = (ctypes.CDLL(LIB_PATH), ctypes.PyDLL(LIB_PATH))
+                for L in handles:
+                    for name, (res, args) in SIGNATURES.items():
+                        f = getattr(L, name)
+                        f.restype = res
+                        f.argtypes = args
+                _lib = _Lib(*handles)
     return _lib
 
 

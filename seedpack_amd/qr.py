@@ -104,7 +104,14 @@ def normalize(counts, scale=1 << PB):
     used = np.flatnonzero(tot)
     rows = c[used]
     f = np.where(rows > 0, np.maximum(1, rows * scale // tot[used, None]), 0)
-    for k in range(len(used)):
+    # one step settles a row whose error is a surplus, or a deficit its largest entry can give up while
+    # staying >= 1 (nearly every row); the others take the steps one at a time
+    diffs = scale - f.sum(1)
+    r = np.arange(len(f))
+    j = np.argmax(f, axis=1) if len(f) else np.zeros(0, np.int64)
+    one = (diffs > 0) | ((diffs < 0) & (f[r, j] - 1 >= -diffs))
+    f[r[one], j[one]] += diffs[one]
+    for k in np.flatnonzero(~one & (diffs != 0)):
         fr = f[k]
         diff = scale - int(fr.sum())
         while diff:

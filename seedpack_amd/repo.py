@@ -46,6 +46,7 @@ import lzma
 import os
 import re
 import resource
+import sys
 import threading
 import time
 import warnings
@@ -73,6 +74,7 @@ WINDOW = 1 << 30                     # base bytes per window (repo3.py:1672)
 PRED_WINDOW = 3 << 30                # first predictions per window, bytes (repo3.py:1677)
 DUP_MIN = 64 << 10                   # smaller tensors are not made references (repo3.py:1024)
 REF_KEEP = 3 << 30                   # bytes of referenced tensors per window (repo3.py:1887)
+SWITCH_INTERVAL = 0.0002             # seconds (the interpreter's default is 0.005)
 BUNDLE_MAX = 64 << 20                # other files up to this size go into the lzma bundle (repo3.py:1364)
 Q8_MIN = 0.5                         # a base-less file with this share of Q8_0 bytes: the Q8_0 codec (repo3.py:1191)
 DQ_CACHE = 32 << 30                  # dequantized seed tensors kept in HBM (float32 bytes)
@@ -586,11 +588,14 @@ class Packer:
 
     def __init__(self, level=7, verbose=False, coders=8, zstd_lanes=24, staging_bytes=24 << 30, device_bytes=None,
                  method="m29", m30_slice=None, bases_in_hbm=None, hash_algo="blake3", blocking_waits=True,
-                 io_threads=16, lane_nice=5):
+                 io_threads=16, read_threads=8, lane_nice=5, switch_interval=SWITCH_INTERVAL):
         self.m30_slice = m30_slice
         # the host side (zstd frames, the read, the hashes) is what bounds a pack: the library's waits
         # for the device sleep instead of spinning a core while a pack runs
         self.blocking_waits = blocking_waits
+        # the interpreter's thread switch interval while a pack runs: the device thread re-acquires the
+        # interpreter lock after each wait, behind the coder and lane threads' Python slices
+        self.switch_interval = switch_interval
         # the catalog's checksum: BLAKE3, the reference's whenever its blake3 requirement is installed
         # (cli.py:48-53), or SHA-256, its fallback; derived files and bases in HBM are hashed there
         if hash_algo not in HASHES:
@@ -604,7 +609,10 @@ class Packer:
         self.level, self.verbose, self.method = level, verbose, method
         self.stream = dev.Stream()
         self.gq = GPUQuant(stream=self.stream.handle)
-        self.io = ThreadPoolExecutor(io_threads, "spa-read")  # file reads (pieces), header parses
+        # the bases and the first derived file are read (in pieces) by io_threads while nothing else runs;
+        # the later files, read ahead of the device while the host codes, by read_threads
+        self.io = ThreadPoolExecutor(io_threads, "spa-read")
+        self.io_ahead = ThreadPoolExecutor(read_threads, "spa-read-ahead")
         self.hasher = ThreadPoolExecutor(8, "spa-hash")      # file checksums
         # stage 2 of a file: its residual frame (one thread each). The host's cores bound a pack, so the
         # lanes run at a lower scheduling priority (nice + lane_nice, Linux keeps one per thread) than
@@ -725,13 +733,14 @@ class Packer:
             self._cpu((f"stage {name} cpu_s", time.thread_time() - c0))
 
     # ---------------------------------------------------------------- one derived file
-    def _read_file(self, job):
+    def _read_file(self, job, first=False):
         """(reader thread) the file's bytes into a page-locked buffer and its checksum started on them"""
         t0 = time.perf_counter()
         size = os.path.getsize(job["path"])
         host = self.pool.acquire(size)[:size]
         t1 = time.perf_counter()
-        _read_into(job["path"], host, pool=self.io, cpu=lambda dt: self._cpu(("file read pieces cpu_s", dt)))
+        _read_into(job["path"], host, pool=self.io if first else self.io_ahead,
+                   cpu=lambda dt: self._cpu(("file read pieces cpu_s", dt)))
         t2 = time.perf_counter()
         self._cpu(("file reads wall_s", t2 - t1))
         job["host"] = host
@@ -805,8 +814,10 @@ class Packer:
                                    bw.view(bw.by_name[t.name], st), imatrix=imx_map.get(t.name),
                                    fitted={kset: fitted[t.name]} if t.name in fitted else None,
                                    base_type=bw.by_name[t.name].type, numel=t.numel) for t in ts_w]
+            w0 = time.perf_counter()
             for t, r in zip(ts_w, residual.residual_window(rts, self.gq, fitted_set=kset, stream=st) if rts else []):
                 out[t.name] = r
+            tm["residual windows"] = tm.get("residual windows", 0.0) + time.perf_counter() - w0
             qitems = collections.defaultdict(list)
             for t in by_w[w]:
                 if t.name in refs:
@@ -832,7 +843,9 @@ class Packer:
                     del items
             while held and sum(h[2] for h in held) > self.QR_HOLD:
                 qj, names, _ = held.popleft()
+                w0 = time.perf_counter()
                 qj.result()
+                tm["coder wait"] = tm.get("coder wait", 0.0) + time.perf_counter() - w0
                 for n in names:                   # the batch is coded: its predictions go
                     out[n]["prediction"] = None
         tm["regrow"] = time.perf_counter()
@@ -922,7 +935,8 @@ class Packer:
                                  **{str(k): p for k, p in enumerate(qparts)}})
         t0 = tm.pop("t0")
         self.timing.append({"file": state["entry"]["name"], "level": prm.level, "start": round(t0 - self._t_pack, 3),
-                            **{k: (round(v, 3) if k in ("staging", "read", "qr wait", "hbm wait") else round(v - t0, 3)) for k, v in tm.items()}})
+                            **{k: (round(v, 3) if k in ("staging", "read", "qr wait", "hbm wait", "coder wait", "residual windows") else round(v - t0, 3))
+                               for k, v in tm.items()}})
         return state["entry"], qchunk, b"".join(frame)
 
     @staticmethod
@@ -940,9 +954,13 @@ class Packer:
     # ---------------------------------------------------------------- the repository
     def pack(self, inputs, output, tool=TOOL, created=None, force=False):
         prev = dev.set_blocking_waits(self.blocking_waits)
+        prev_si = sys.getswitchinterval()
+        if self.switch_interval:
+            sys.setswitchinterval(self.switch_interval)
         try:
             return self._pack(inputs, output, tool, created, force)
         finally:
+            sys.setswitchinterval(prev_si)
             dev.set_blocking_waits(prev)
 
     def _pack(self, inputs, output, tool, created, force):
@@ -1084,7 +1102,7 @@ class Packer:
             porder = process_order(info, None)
             # the first file read while the bases are uploaded, their checksums and codecs started
             # (one stream each)
-            ahead = self.reader.submit(self._timed, "read", self._read_file, jobs[porder[0]]) if porder else None
+            ahead = self.reader.submit(self._timed, "read", self._read_file, jobs[porder[0]], True) if porder else None
             side = ThreadPoolExecutor(1, "spa-base")
             base_jobs = []
             # the BF16 bases in HBM when they fit beside the largest derived file and RESERVE, else
@@ -1282,9 +1300,11 @@ class Unpacker:
     the host, uploaded, its predictions regrown and XORed in and its QR batches decoded on the device,
     then read back, checked and written"""
 
-    def __init__(self, verbose=False, staging_bytes=64 << 30, bases_in_hbm=None, verify=True, blocking_waits=True):
+    def __init__(self, verbose=False, staging_bytes=64 << 30, bases_in_hbm=None, verify=True, blocking_waits=True,
+                 switch_interval=SWITCH_INTERVAL):
         self.verbose = verbose
         self.blocking_waits = blocking_waits      # the library's waits for the device sleep (as the Packer's)
+        self.switch_interval = switch_interval
         self.verify = verify                      # False: a catalog hash not computed here is a warning
         # the bases decoded into HBM (True), decoded window by window from the archive (False), or
         # in HBM when they fit beside the largest file to rebuild and 48 GB (None)
@@ -1300,9 +1320,13 @@ class Unpacker:
 
     def run(self, archive, outdir=None, patterns=None):
         prev = dev.set_blocking_waits(self.blocking_waits)
+        prev_si = sys.getswitchinterval()
+        if self.switch_interval:
+            sys.setswitchinterval(self.switch_interval)
         try:
             return self._run(archive, outdir, patterns)
         finally:
+            sys.setswitchinterval(prev_si)
             dev.set_blocking_waits(prev)
 
     def _run(self, archive, outdir, patterns):
