@@ -1526,12 +1526,12 @@ class Unpacker:
         # the first files' residuals (two threads: each frame is one serial zstd stream), as far as
         # the staging budget holds them beside the host copies of the bases to be written
         room = self.pool.budget - sum(cat[manifest["bases"][i]]["size"] for i in coded if manifest["bases"][i] in want)
-        ahead = {}
-        for k in range(min(2, len(order))):
-            room -= mf[order[k]]["size"]
+        ahead = {}                                          # file index -> its residual, decompressing
+        for i in order[:2]:
+            room -= mf[i]["size"]
             if room < 0:
                 break
-            ahead[k] = self.ahead.submit(residual_of, order[k])
+            ahead[i] = self.ahead.submit(residual_of, i)
         for i in phys:
             if i not in coded:
                 continue
@@ -1574,16 +1574,27 @@ class Unpacker:
         for k, j in enumerate(joined):
             if nb + k in need_b:
                 bases[nb + k] = _Base.joined(nb + k, [(s_, bases[i]) for i, s_ in j["parts"]], jd.get(k))
-        for k in range(min(2, len(order))):
-            if k not in ahead:
-                ahead[k] = self.ahead.submit(residual_of, order[k])
-        for k, i in enumerate(order):
-            m = mf[i]
+        # files in the order their residuals become ready, among those whose sources are rebuilt (the
+        # first file left always is one); two residuals decompress ahead
+        left = list(order)
+
+        def top_up():
+            for i in left:
+                if len(ahead) >= 2:
+                    break
+                if i not in ahead:
+                    ahead[i] = self.ahead.submit(residual_of, i)
+        top_up()
+        while left:
             tf = time.perf_counter()
-            resid = ahead.pop(k).result()
+            ready = [i for i in left if i in ahead and not srcs[i] - done]
+            futures_wait([ahead[i] for i in ready], return_when="FIRST_COMPLETED")
+            i = next(i for i in ready if ahead[i].done())
+            m = mf[i]
+            resid = ahead.pop(i).result()
             tw = time.perf_counter() - tf
-            if k + 2 < len(order):
-                ahead[k + 2] = self.ahead.submit(residual_of, order[k + 2])
+            left.remove(i)
+            top_up()
             tm, known = {}, None
             if m["plan"]:
                 tm, known = self._rebuild(r, i, m, bases[m["base"]], resid, kept, users, done, imx_dev, imx_off,
