@@ -408,10 +408,10 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
     :441): a synthetic Qwen3.5-9B-shaped repository (BF16 GGUF with a 151,936-token BPE tokenizer,
     imatrix.dat, README.md, 21 quantized GGUFs made by this library's quantizers with 1% of their
     blocks changed) written to host files (untimed); then, timed, seedpack_amd.repo's pack of the
-    directory into a .seedpack archive (file reads, SHA-256 of every file, regrowth / comparison /
-    QR coding on the device, the R2 base codec, zstd of the residuals, the container), and the
-    extract of the Q4_K_M-like and IQ2_XS files from that archive (residual zstd, regrowth, QR decode,
-    SHA-256 check, files written). Peak HBM by hipMemGetInfo polling. The extracted files are
+    directory into a .seedpack archive (file reads, the catalog's BLAKE3 of every file (on the device),
+    regrowth / comparison / QR coding on the device, the R2 base codec, zstd of the residuals, the
+    container), and the extract of the Q4_K_M-like and IQ2_XS files from that archive (residual zstd,
+    regrowth, QR decode, BLAKE3 check, files written). Peak HBM by hipMemGetInfo polling. The extracted files are
     compared byte for byte with the originals. reuse: the repository a previous write_only call left
     in root is packed (a kernel-trace run then sees the pack and the extract only). bases_in_hbm False:
     the base kept in host memory by the pack and decoded window by window by the extract, which then
@@ -456,6 +456,7 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
         for f in st["files"]:
             log(f"bench:   {f}")
         log(f"bench: pack cpu {st['cpu']}")
+        log(f"bench: pack started at {st['clock_start_s']:.6f} s (perf_counter)")
         want = [n for n in ("model-Q4_K_M.gguf", "model-IQ2_XS.gguf") if n in qf]
         if bases_in_hbm is False:
             want.append("model-BF16.gguf")
@@ -470,7 +471,7 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
                 "archive_bytes": st["archive_bytes"], "ratio": round(st["archive_bytes"] / st["input_bytes"], 4),
                 "pack_s": round(st["seconds"], 2), "pack_GB_s": round(st["GB_s"], 3), "peak_hbm_GB": round(pk_peak / 1e9, 1),
                 "stats": st["stats"], "phases_s": st.get("phases"), "host_cpu_s": st.get("cpu")}
-        unpack = {"workload": "cfg5: Q4_K_M-like and IQ2_XS extracted from the cfg4 archive (files written, SHA-256 checked)"
+        unpack = {"workload": "cfg5: Q4_K_M-like and IQ2_XS extracted from the cfg4 archive (files written, catalog checksums checked)"
                               + (", and the BF16 base decoded window by window" if bases_in_hbm is False else ""),
                   "written_bytes": ex["bytes"], "extract_s": round(ex["seconds"], 2), "GB_s_written": round(ex["GB_s"], 3),
                   "checksums_ok": not ex["bad"] and not ex["missing"], "byte_identical": same,

@@ -5,6 +5,7 @@ dtype and a shape. It plays the role CuPy arrays play in the reference (seedpack
 allocations go to a per-size cache and are reused (as CuPy's memory pool does), so that short-lived
 arrays never reach hipFree, which waits for the whole device.
 """
+import bisect
 import collections
 import ctypes
 import threading
@@ -14,14 +15,53 @@ import numpy as np
 from ._lib import check, lib
 
 
+class _Free:
+    """one thread's freed blocks: a list per (device, size class), and per device the sorted classes
+    that hold blocks"""
+
+    def __init__(self):
+        self.lists = collections.defaultdict(list)
+        self.sizes = collections.defaultdict(list)
+
+    def put(self, dev_id, n, ptr):
+        lst = self.lists[(dev_id, n)]
+        if not lst:
+            bisect.insort(self.sizes[dev_id], n)
+        lst.append(ptr)
+
+    def pop(self, dev_id, n, most):
+        """a block of the least class in [n, most] -> (class, pointer), or None"""
+        sz = self.sizes.get(dev_id)
+        if not sz:
+            return None
+        i = bisect.bisect_left(sz, n)
+        if i == len(sz) or sz[i] > most:
+            return None
+        c = sz[i]
+        lst = self.lists[(dev_id, c)]
+        p = lst.pop()
+        if not lst:
+            sz.pop(i)
+        return c, p
+
+    def clear(self):
+        """-> [(class, pointer)] of every block, the lists emptied"""
+        blocks = [(k[1], p) for k, ps in self.lists.items() for p in ps]
+        self.lists.clear()
+        self.sizes.clear()
+        return blocks
+
+
 class _Cache:
     """freed device allocations kept for reuse, by device and size class: hipFree waits for every
     stream of the device, so freeing a short-lived array (a prediction, a batch's buffers) would stall
-    the work other threads have queued. A freed block goes back to the thread that allocated it and
-    is reused only there: every thread here queues its work on one stream of its own, so work still
-    queued on a block precedes, in stream order, whatever reuses it (a block dropped by another
-    thread is dropped after that thread waited for its own work on it). At most `limit` bytes are held
-    in all; beyond it memory is freed."""
+    the work other threads have queued, and a new hipMalloc of a large block costs about a millisecond.
+    A request takes the least cached block of its class or larger, up to twice its size (a pack's
+    files come largest first, so the blocks of one file's predictions serve the next's). A freed
+    block goes back to the thread that allocated it and is reused only there: every thread here
+    queues its work on one stream of its own, so work still queued on a block precedes, in stream
+    order, whatever reuses it (a block dropped by another thread is dropped after that thread waited
+    for its own work on it). At most `limit` bytes are held in all; beyond it memory is freed."""
 
     def __init__(self, limit=48 << 30):
         self.limit, self.bytes, self.lock = limit, 0, threading.Lock()
@@ -35,36 +75,35 @@ class _Cache:
         return -(-n // step) * step
 
     def mine(self):
-        """this thread's free lists"""
+        """this thread's free blocks"""
         f = getattr(self.tls, "free", None)
         if f is None:
-            f = self.tls.free = collections.defaultdict(list)
+            f = self.tls.free = _Free()
+            with self.lock:
+                self.owners[id(f)] = f
         return f
 
     def take(self, dev_id, n):
+        """a cached block for a request of class n -> (its class, pointer), or None"""
         f = self.mine()
         with self.lock:
-            lst = f.get((dev_id, n))
-            if lst:
-                self.bytes -= n
-                return lst.pop()
-        return None
+            got = f.pop(dev_id, n, 2 * n)
+            if got is not None:
+                self.bytes -= got[0]
+            return got
 
     def give(self, owner, dev_id, ptr, n):
         with self.lock:
             if self.bytes + n > self.limit:
                 return False
             self.bytes += n
-            owner[(dev_id, n)].append(ptr)
-            self.owners[id(owner)] = owner
+            owner.put(dev_id, n, ptr)
             return True
 
-    def drain(self, lists):
-        """free the blocks of the given free lists"""
+    def drain(self, owners):
+        """free the blocks the given owners hold"""
         with self.lock:
-            blocks = [(k[1], p) for f in lists for k, ps in f.items() for p in ps]
-            for f in lists:
-                f.clear()
+            blocks = [b for f in owners for b in f.clear()]
             self.bytes -= sum(n for n, _ in blocks)
         for _, p in blocks:
             lib().spa_free(p)
@@ -81,8 +120,8 @@ class _Cache:
             else:
                 check(lib().spa_device_synchronize())
                 with self.lock:
-                    lists = list(self.owners.values())
-                self.drain(lists)
+                    owners = list(self.owners.values())
+                self.drain(owners)
         check(lib().spa_malloc(ctypes.byref(p), n))
         return p.value
 
@@ -106,10 +145,11 @@ class DeviceArray:
         self._alloc = None
         if ptr is None:
             dev_id, n = _device_id(), _Cache.size_class(self.nbytes)
-            q = CACHE.take(dev_id, n)
-            if q is None:
-                q = CACHE.alloc(n)
-            self.ptr, self._owner, self._alloc = q, None, (CACHE.mine(), dev_id, n)
+            got = CACHE.take(dev_id, n)
+            if got is None:
+                got = n, CACHE.alloc(n)
+            self._alloc = (CACHE.mine(), dev_id, got[0])
+            self.ptr, self._owner = got[1], None
         else:
             self.ptr, self._owner = ptr, owner if owner is not None else self
 

@@ -677,7 +677,7 @@ class Packer:
         chunk's parts (m28, repo3.py:1470-1475), or a seed's chunk (seed.py), coded on its own stream
         from the resident copy"""
         s = dev.Stream()
-        g = b.g
+        g = gguf.GGUF(host) if b.g.light else b.g     # the whole header, tokenizer arrays included
         if b.seed:
             c = SeedCodec(stream=s.handle).compress(host, g=g, d=b.d)
             s.synchronize()
@@ -1034,7 +1034,8 @@ class Packer:
             loaded = []
             for i, (n, p) in enumerate(bases.items()):
                 host = np.memmap(p, np.uint8, "r") if os.path.getsize(p) else np.zeros(0, np.uint8)
-                loaded.append((host, _Base(i, n, host, None, gguf.GGUF(host), seed=n in seeds)))
+                # (the tokenizer's arrays are parsed later, by the base's coder on its side thread)
+                loaded.append((host, _Base(i, n, host, None, gguf.GGUF(host, light=True), seed=n in seeds)))
             allb = [b for _, b in loaded] + [_Base.joined(len(bnames) + k, [(s_, loaded[i][1]) for i, s_ in j["parts"]])
                                              for k, j in enumerate(joined)]
             # the repository's importance per tensor on the device (the grid QR types read it)
@@ -1223,6 +1224,7 @@ class Packer:
         phase("closed")
         return {"input_bytes": total, "archive_bytes": size, "seconds": dt, "GB_s": total / dt / 1e9,
                 "stats": dict(self.stats), "phases": phases, "files": self.timing,
+                "clock_start_s": t0,             # perf_counter (CLOCK_MONOTONIC): lines the phases up with a trace
                 "cpu": {"process cpu_s": round(cpu_s, 1), **{k: round(v, 1) for k, v in self.cpu.items()},
                         "outside the stages cpu_s": round(cpu_s - sum(v for k, v in self.cpu.items()
                                                                       if k.startswith("stage ") or k == "file read pieces cpu_s"), 1)},
