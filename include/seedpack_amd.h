@@ -37,7 +37,8 @@ extern "C" {
 const char* spa_last_error(void);
 int spa_device_count(int* n);
 int spa_set_device(int device);
-/* How the library's waits (spa_stream_synchronize, spa_memcpy_h2d / d2h) wait for the device: 0 the
+/* How the library's waits (spa_stream_synchronize, spa_event_synchronize, spa_memcpy_h2d / d2h) wait
+ * for the device: 0 the
  * runtime's stream synchronisation (it spins a core until the work is done), 1 an event recorded and
  * polled with sleeps of 20 to 500 us between polls (the core free for host work). Process-wide. No
  * reference counterpart: the packer and the unpacker, whose host side is CPU-bound, use 1. */
@@ -51,6 +52,8 @@ int spa_host_alloc(void** ptr, size_t nbytes);
 int spa_host_free(void* ptr);
 int spa_memcpy_h2d(void* dst, const void* src, size_t nbytes, void* stream);
 int spa_memcpy_d2h(void* dst, const void* src, size_t nbytes, void* stream);
+/* The copy queued on `stream` without waiting for it (dst page-locked; wait with an event). */
+int spa_memcpy_d2h_async(void* dst, const void* src, size_t nbytes, void* stream);
 int spa_memcpy_d2d(void* dst, const void* src, size_t nbytes, void* stream);
 int spa_memset(void* ptr, int value, size_t nbytes, void* stream);
 int spa_stream_create(void** stream);
@@ -63,6 +66,8 @@ int spa_event_record(void* event, void* stream);
 /* Work queued on `stream` after this call waits for `event`'s last record. */
 int spa_stream_wait_event(void* stream, void* event);
 int spa_event_elapsed_ms(float* ms, void* start, void* stop);
+/* Waits for the work before `event`'s last record (as spa_set_sync_mode says). */
+int spa_event_synchronize(void* event);
 int spa_mem_info(size_t* free_bytes, size_t* total_bytes);
 /* Device-to-device copy by a plain streaming kernel (16-byte multiples); the HBM yardstick the
  * traffic counters of the other kernels are scaled against. No reference counterpart. */

@@ -29,6 +29,7 @@ SIGNATURES = {
     "spa_host_free": (c_int, [c_void_p]),
     "spa_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "spa_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "spa_memcpy_d2h_async": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "spa_memcpy_d2d": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "spa_memset": (c_int, [c_void_p, c_int, c_size_t, c_void_p]),
     "spa_stream_create": (c_int, [ctypes.POINTER(c_void_p)]),
@@ -40,6 +41,7 @@ SIGNATURES = {
     "spa_event_record": (c_int, [c_void_p, c_void_p]),
     "spa_stream_wait_event": (c_int, [c_void_p, c_void_p]),
     "spa_event_elapsed_ms": (c_int, [ctypes.POINTER(c_float), c_void_p, c_void_p]),
+    "spa_event_synchronize": (c_int, [c_void_p]),
     "spa_mem_info": (c_int, [ctypes.POINTER(c_size_t), ctypes.POINTER(c_size_t)]),
     "spa_copy": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "spa_valu_probe": (c_int, [c_int, c_int64, c_int, c_void_p, c_void_p]),
@@ -175,7 +177,8 @@ class SpaError(RuntimeError):
 RELEASE = {
     "spa_malloc", "spa_free", "spa_host_alloc", "spa_host_free", "spa_memcpy_h2d", "spa_memcpy_d2h",
     "spa_stream_create", "spa_stream_destroy", "spa_stream_synchronize", "spa_device_synchronize",
-    "spa_event_create", "spa_event_destroy", "spa_event_elapsed_ms", "spa_mem_info", "spa_device_count",
+    "spa_event_create", "spa_event_destroy", "spa_event_elapsed_ms", "spa_event_synchronize", "spa_mem_info",
+    "spa_device_count",
     "spa_set_device", "spa_crc32", "spa_gguf_strings_bytes", "spa_iq_table_host", "spa_blake3",
     "spa_b3h_new", "spa_b3h_update", "spa_b3h_final", "spa_b3h_free",
 }

@@ -59,6 +59,17 @@ int spa_set_device(int device) { SPA_HIP_TRY(hipSetDevice(device)); return SPA_O
 // cost of at most one sleep of latency per wait.
 static std::atomic<int> g_blocking{0};
 
+// the event's work done: polled with sleeps between polls when blocking, else the runtime's wait
+static hipError_t wait_event(hipEvent_t ev) {
+    if (!g_blocking.load(std::memory_order_relaxed)) return hipEventSynchronize(ev);
+    for (unsigned us = 20;; us = us < 250 ? 2 * us : 500) {
+        const hipError_t e = hipEventQuery(ev);
+        if (e != hipErrorNotReady) return e;
+        struct timespec ts = {0, (long)us * 1000};
+        nanosleep(&ts, nullptr);
+    }
+}
+
 static hipError_t wait_stream(hipStream_t s) {
     if (!g_blocking.load(std::memory_order_relaxed)) return hipStreamSynchronize(s);
     thread_local hipEvent_t ev = nullptr;   // one per thread and device (kept to the process's end)
@@ -72,13 +83,7 @@ static hipError_t wait_stream(hipStream_t s) {
         ev_dev = d;
     }
     e = hipEventRecord(ev, s);
-    if (e != hipSuccess) return e;
-    for (unsigned us = 20;; us = us < 250 ? 2 * us : 500) {
-        e = hipEventQuery(ev);
-        if (e != hipErrorNotReady) return e;
-        struct timespec ts = {0, (long)us * 1000};
-        nanosleep(&ts, nullptr);
-    }
+    return e == hipSuccess ? wait_event(ev) : e;
 }
 
 int spa_set_sync_mode(int blocking) {
@@ -113,6 +118,10 @@ int spa_memcpy_d2h(void* dst, const void* src, size_t n, void* s) {
     SPA_HIP_TRY(wait_stream((hipStream_t)s));
     return SPA_OK;
 }
+int spa_memcpy_d2h_async(void* dst, const void* src, size_t n, void* s) {
+    SPA_HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, (hipStream_t)s));
+    return SPA_OK;
+}
 int spa_memcpy_d2d(void* dst, const void* src, size_t n, void* s) {
     SPA_HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, (hipStream_t)s));
     return SPA_OK;
@@ -131,6 +140,7 @@ int spa_event_elapsed_ms(float* ms, void* a, void* b) {
     SPA_HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
     return SPA_OK;
 }
+int spa_event_synchronize(void* e) { SPA_HIP_TRY(wait_event((hipEvent_t)e)); return SPA_OK; }
 int spa_mem_info(size_t* f, size_t* t) { SPA_HIP_TRY(hipMemGetInfo(f, t)); return SPA_OK; }
 
 uint64_t spa_gguf_strings_bytes(const void* p, uint64_t avail, uint64_t count) {

@@ -293,6 +293,10 @@ class Event:
     def record(self, stream=None):
         check(lib().spa_event_record(self.handle, stream))
 
+    def synchronize(self):
+        """wait for the work before the last record"""
+        check(lib().spa_event_synchronize(self.handle))
+
     def elapsed_ms(self, end):
         ms = ctypes.c_float()
         check(lib().spa_event_elapsed_ms(ctypes.byref(ms), self.handle, end.handle))

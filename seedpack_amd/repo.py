@@ -801,7 +801,9 @@ class Packer:
         for t, _ in mine:
             mine_w[wins_of[t.name]].append(t)
         out = {}
-        for w in sorted(by_w):
+
+        def start(w):
+            """window w's importance fit, then its first predictions and counts queued (not waited for)"""
             ts_w = mine_w.get(w, [])
             bw = b.window([t.name for t in ts_w], st)     # (the base itself when it is in HBM)
             if self.fits.waiting(kset):
@@ -814,8 +816,17 @@ class Packer:
                                    bw.view(bw.by_name[t.name], st), imatrix=imx_map.get(t.name),
                                    fitted={kset: fitted[t.name]} if t.name in fitted else None,
                                    base_type=bw.by_name[t.name].type, numel=t.numel) for t in ts_w]
+            return ts_w, bw, residual.residual_window_start(rts, self.gq, fitted_set=kset, stream=st) if rts else None
+
+        # one window ahead: the next window's first predictions are queued before this one's decisions
+        # wait, so the device works while the host decides and hands batches to the coders
+        wins = sorted(by_w)
+        ahead = start(wins[0]) if wins else None
+        for wk, w in enumerate(wins):
+            ts_w, bw, pending = ahead
+            ahead = start(wins[wk + 1]) if wk + 1 < len(wins) else None
             w0 = time.perf_counter()
-            for t, r in zip(ts_w, residual.residual_window(rts, self.gq, fitted_set=kset, stream=st) if rts else []):
+            for t, r in zip(ts_w, residual.residual_window_finish(pending) if pending is not None else []):
                 out[t.name] = r
             tm["residual windows"] = tm.get("residual windows", 0.0) + time.perf_counter() - w0
             qitems = collections.defaultdict(list)

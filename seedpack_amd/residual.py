@@ -204,22 +204,50 @@ def residual_tensor(t, gq=None, fitted_set=0, use_qr=True, stream=None):
     return _decide(t, gq, *f, c.value(stream), stream)
 
 
-def residual_window(ts, gq=None, fitted_set=0, use_qr=True, stream=None):
-    """residual_tensor for a window of tensors with the same decisions, their first predictions and
-    byte counts queued back to back and read back together (one wait per window instead of one per
-    tensor, as the reference's window pipeline defers its comparisons, repo3.py:456-510) -> results
-    in the order of ts"""
+def _staged(n):
+    """a page-locked uint64 array of at least n items for this thread (returned with _unstage)"""
+    pool = getattr(_TLS, "staged", None)
+    if pool is None:
+        pool = _TLS.staged = []
+    for k, a in enumerate(pool):
+        if a.size >= n:
+            return pool.pop(k)
+    return dev.pinned(max(64, 2 * n), np.uint64)
+
+
+def _unstage(a):
+    _TLS.staged.append(a)
+
+
+def _read_counts(counts, n, stream):
+    """counts[:n] copied to the host behind the work queued so far -> (host array, event)"""
+    host = _staged(n)
+    if n:
+        check(lib().spa_memcpy_d2h_async(host.ctypes.data, counts.ptr, 8 * n, stream))
+    ev = dev.Event()
+    ev.record(stream)
+    return host, ev
+
+
+def residual_window_start(ts, gq=None, fitted_set=0, use_qr=True, stream=None):
+    """the first predictions of a window of tensors and their byte counts queued back to back (the
+    reference's window pipeline defers its comparisons, repo3.py:456-510), the counts' read-back
+    queued behind them; nothing is waited for -> the state residual_window_finish completes"""
     gq = gq or GPUQuant(stream=stream)
-    cache = getattr(_TLS, "windows", None)
-    if cache is None:
-        cache = _TLS.windows = {}
-    key = dev.current_device()
-    if key not in cache or cache[key].size < len(ts):
-        cache[key] = dev.DeviceArray(max(64, 2 * len(ts)), np.uint64)
-    counts = cache[key]
+    counts = dev.DeviceArray(max(64, 2 * len(ts)), np.uint64)
     firsts = [_first(t, gq, fitted_set, use_qr, stream, counts.ptr + 8 * i) for i, t in enumerate(ts)]
-    n = counts.to_host(stream=stream)[:len(ts)] if ts else []
-    # the QR tensors' other candidates, all predicted and counted before one wait
+    host, ev = _read_counts(counts, len(ts), stream)
+    return {"ts": ts, "gq": gq, "stream": stream, "counts": counts, "firsts": firsts, "host": host, "ev": ev}
+
+
+def residual_window_finish(st):
+    """residual_tensor's results for the window residual_window_start queued, in the order of its
+    tensors: its counts waited for (one wait), the QR tensors' other candidates predicted and counted
+    before one more wait"""
+    ts, gq, stream, counts, firsts = st["ts"], st["gq"], st["stream"], st["counts"], st["firsts"]
+    st["ev"].synchronize()
+    n = st["host"][:len(ts)].copy()
+    _unstage(st["host"])
     tried = collections.defaultdict(list)
     for i, (t, f) in enumerate(zip(ts, firsts)):
         if f is not None and f[2] and n[i]:
@@ -227,10 +255,13 @@ def residual_window(ts, gq=None, fitted_set=0, use_qr=True, stream=None):
     slots = [(i, v, p) for i, vs in tried.items() for v, p in vs]
     if slots:
         if counts.size < len(slots):
-            counts = cache[key] = dev.DeviceArray(2 * len(slots), np.uint64)
+            counts = dev.DeviceArray(2 * len(slots), np.uint64)
         for s_, (i, v, p) in enumerate(slots):
             check(lib().spa_diff_count(ts[i].region.ptr, p.ptr, ts[i].region.nbytes, counts.ptr + 8 * s_, stream))
-        e = counts.to_host(stream=stream)[:len(slots)]
+        host, ev = _read_counts(counts, len(slots), stream)
+        ev.synchronize()
+        e = host[:len(slots)].copy()
+        _unstage(host)
         tried = collections.defaultdict(list)
         for s_, (i, v, p) in enumerate(slots):
             tried[i].append((v, p, int(e[s_])))
@@ -243,6 +274,11 @@ def residual_window(ts, gq=None, fitted_set=0, use_qr=True, stream=None):
         else:
             out.append(_decide(t, gq, *f, int(n[i]), stream))
     return out
+
+
+def residual_window(ts, gq=None, fitted_set=0, use_qr=True, stream=None):
+    """residual_tensor for a window of tensors with the same decisions -> results in the order of ts"""
+    return residual_window_finish(residual_window_start(ts, gq, fitted_set, use_qr, stream))
 
 
 def _decide_qr(t, first, p0, n0, tried, stream):
