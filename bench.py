@@ -447,6 +447,9 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
             keep = True
             return None, None
         arc = os.path.join(arc_dir, "model.seedpack")
+        # (untimed) the device blocks that earlier sections left cached are released, so that the pack
+        # starts as it does in a process of its own
+        dev.release_cached()
         peak = HbmPeak().start()
         st = repo.Packer(verbose=True, bases_in_hbm=bases_in_hbm, blocking_waits=blocking_waits).pack([src], arc)
         pk_peak = peak.stop()
@@ -460,6 +463,7 @@ def repo_cfg45(layers=36, files=None, root="/dev/shm/spa_bench_repo", keep=False
         want = [n for n in ("model-Q4_K_M.gguf", "model-IQ2_XS.gguf") if n in qf]
         if bases_in_hbm is False:
             want.append("model-BF16.gguf")
+        dev.release_cached()
         peak = HbmPeak().start()
         ex = repo.Unpacker(verbose=True, bases_in_hbm=bases_in_hbm, blocking_waits=blocking_waits).run(arc, out, want)
         up_peak = peak.stop()

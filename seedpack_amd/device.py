@@ -129,6 +129,14 @@ class _Cache:
 CACHE = _Cache()
 
 
+def release_cached():
+    """free every cached device block (all threads'; waits for the whole device first)"""
+    check(lib().spa_device_synchronize())
+    with CACHE.lock:
+        owners = list(CACHE.owners.values())
+    CACHE.drain(owners)
+
+
 def _device_id():
     d = ctypes.c_int()
     check(lib().spa_get_device(ctypes.byref(d)))
