@@ -964,6 +964,9 @@ class Packer:
 
     # ---------------------------------------------------------------- the repository
     def pack(self, inputs, output, tool=TOOL, created=None, force=False):
+        # device blocks that earlier work left cached are released first: blocks of other sizes would
+        # fill the cache, and each later free beyond its limit waits for the whole device
+        dev.release_cached()
         prev = dev.set_blocking_waits(self.blocking_waits)
         prev_si = sys.getswitchinterval()
         if self.switch_interval:
@@ -1332,6 +1335,7 @@ class Unpacker:
         self.ahead = ThreadPoolExecutor(2)        # the next files' residuals decompressed ahead
 
     def run(self, archive, outdir=None, patterns=None):
+        dev.release_cached()                      # (as the packer does)
         prev = dev.set_blocking_waits(self.blocking_waits)
         prev_si = sys.getswitchinterval()
         if self.switch_interval:
