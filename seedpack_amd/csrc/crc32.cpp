@@ -1,8 +1,10 @@
 // CRC-32 as zlib computes it (polynomial 0x04C11DB7 bit-reflected, initial and final value ~0) on the
 // host, for the container's chunk checksums. Blocks of 16 bytes are folded with carry-less
 // multiplication (PCLMULQDQ; the folding method of Gopal et al., "Fast CRC Computation for Generic
-// Polynomials Using PCLMULQDQ Instruction", Intel, 2009): four 128-bit accumulators 64 bytes apart,
-// combined into one, whose CRC and the tail bytes' are then taken a byte at a time from a table.
+// Polynomials Using PCLMULQDQ Instruction", Intel, 2009): sixteen 128-bit accumulators in four
+// 512-bit registers (VPCLMULQDQ) over the bulk where the CPU has it, then four 128-bit accumulators
+// 64 bytes apart, combined into one, whose CRC and the tail bytes' are taken a byte at a time from a
+// table.
 //
 // A 128-bit register holds 128 message bits in order (bit k = message bit k, least significant bit of
 // each byte first), i.e. a polynomial R with bit k the coefficient of x^(127-k); its low quadword H
@@ -40,7 +42,8 @@ uint64_t reflect64(uint32_t v) {             // coefficient of x^d at bit 63 - d
 struct Tables {
     uint32_t byte[256];
     uint64_t k512[2], k384[2], k256[2], k128[2];   // {for H, for L} of a move by 512, 384, 256, 128 bits
-    bool clmul;
+    uint64_t k2048[2];                              // the same for 2048 bits (four 512-bit registers)
+    bool clmul, wide;
     Tables() {
         for (uint32_t i = 0; i < 256; ++i) {
             uint32_t c = i;
@@ -53,8 +56,11 @@ struct Tables {
             K[i][0] = reflect64(xpow_mod(D[i] + 63));
             K[i][1] = reflect64(xpow_mod(D[i] - 1));
         }
+        k2048[0] = reflect64(xpow_mod(2048 + 63));
+        k2048[1] = reflect64(xpow_mod(2048 - 1));
         __builtin_cpu_init();
         clmul = __builtin_cpu_supports("pclmul") && __builtin_cpu_supports("sse4.1");
+        wide = clmul && __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("vpclmulqdq");
     }
 };
 
@@ -95,12 +101,51 @@ __attribute__((target("pclmul,sse4.1"))) uint32_t by_folding(uint32_t s, const u
     return by_table(by_table(0, last, 16, T.byte), p + at, n - at, T.byte);
 }
 
+#define SPA_WIDE __attribute__((target("avx512f,vpclmulqdq,pclmul,sse4.1")))
+
+SPA_WIDE inline __m512i ld512(const uint8_t* q) { return _mm512_loadu_si512(reinterpret_cast<const void*>(q)); }
+
+SPA_WIDE inline __m512i move512(__m512i r, __m512i k) {
+    return _mm512_xor_si512(_mm512_clmulepi64_epi128(r, k, 0x00), _mm512_clmulepi64_epi128(r, k, 0x11));
+}
+
+// the raw register after the largest multiple of 256 bytes (n >= 512) of p, from register s: four
+// 512-bit registers, each four 128-bit accumulators, folded 2048 bits at a time with VPCLMULQDQ; their
+// 16 accumulators (256 bytes, in message order) are then taken by the 128-bit path; `used` = the bytes
+SPA_WIDE uint32_t by_folding512(uint32_t s, const uint8_t* p, size_t n, size_t& used, const Tables& T) {
+    const __m512i k = _mm512_set_epi64((long long)T.k2048[1], (long long)T.k2048[0], (long long)T.k2048[1],
+                                       (long long)T.k2048[0], (long long)T.k2048[1], (long long)T.k2048[0],
+                                       (long long)T.k2048[1], (long long)T.k2048[0]);
+    __m512i x0 = _mm512_xor_si512(ld512(p), _mm512_castsi128_si512(_mm_cvtsi32_si128((int)s)));
+    __m512i x1 = ld512(p + 64), x2 = ld512(p + 128), x3 = ld512(p + 192);
+    size_t at = 256;
+    for (; n - at >= 256; at += 256) {
+        x0 = _mm512_xor_si512(move512(x0, k), ld512(p + at));
+        x1 = _mm512_xor_si512(move512(x1, k), ld512(p + at + 64));
+        x2 = _mm512_xor_si512(move512(x2, k), ld512(p + at + 128));
+        x3 = _mm512_xor_si512(move512(x3, k), ld512(p + at + 192));
+    }
+    alignas(64) uint8_t acc[256];
+    _mm512_store_si512(reinterpret_cast<void*>(acc), x0);
+    _mm512_store_si512(reinterpret_cast<void*>(acc + 64), x1);
+    _mm512_store_si512(reinterpret_cast<void*>(acc + 128), x2);
+    _mm512_store_si512(reinterpret_cast<void*>(acc + 192), x3);
+    used = at;
+    return by_folding(0, acc, 256, T);
+}
+
 }  // namespace
 
 extern "C" uint32_t spa_crc32(uint32_t crc, const void* data, size_t n) {
     const Tables& T = tables();
     const uint8_t* p = static_cast<const uint8_t*>(data);
     if (!p || n == 0) return crc;
-    const uint32_t s = ~crc;
+    uint32_t s = ~crc;
+    if (n >= 512 && T.wide) {
+        size_t used = 0;
+        s = by_folding512(s, p, n, used, T);
+        p += used;
+        n -= used;
+    }
     return ~(n >= 64 && T.clmul ? by_folding(s, p, n, T) : by_table(s, p, n, T.byte));
 }

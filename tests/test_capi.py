@@ -75,15 +75,16 @@ def test_sync_mode_takes_only_its_two_values():
 
 
 def test_crc32_equals_zlib():
-    """the host CRC-32 (carry-less folding for 64 bytes and more, a table below) against zlib.crc32:
-    every length to 300, odd offsets, chained calls, zeros and a large buffer"""
+    """the host CRC-32 (512-bit folding from 512 bytes where the CPU has it, 128-bit folding from 64
+    bytes, a table below) against zlib.crc32: every length to 300 and around the 512-bit path's
+    boundaries, odd offsets, chained calls, zeros and a large buffer"""
     import zlib
 
     import numpy as np
 
     from seedpack_amd.container import crc32
     g = np.random.Generator(np.random.PCG64(32))
-    for n in list(range(301)) + [511, 4096 + 17, 1 << 20]:
+    for n in list(range(301)) + list(range(500, 800)) + [1023, 1024, 1025, 4096 + 17, 1 << 20]:
         b = g.integers(0, 256, n + 5, dtype=np.uint8).tobytes()
         for o in (0, 1, 5):
             piece = b[o:o + n]
