@@ -94,6 +94,20 @@ def test_gguf_round_trip_and_light_mode():
     assert all(t.offset % 64 == 0 for t in g.tensors)
     light = gguf.GGUF(data, light=True)
     assert light.meta["tokenizer.ggml.tokens"] is None and light.tensors == g.tensors
+    assert light.data_start == g.data_start and light.spans == g.spans and light.meta["a.ints"] == [1, -2, 3]
+    # arrays of more than 64 items are stepped over (strings by the library's length scan), and one
+    # that runs past the data is an error, not a short read
+    kv2 = {"tokenizer.ggml.tokens": [f"tok{i}" * (i % 7) for i in range(3000)], "tokenizer.ggml.token_type": [1] * 3000,
+           "general.name": "after the arrays"}
+    head2, _, size2 = gguf.header_bytes(kv2, tensors)
+    data2 = head2 + bytes(size2 - len(head2))
+    full, lite = gguf.GGUF(data2), gguf.GGUF(data2, light=True)
+    assert lite.meta["tokenizer.ggml.tokens"] is None and lite.meta["tokenizer.ggml.token_type"] is None
+    assert lite.meta["general.name"] == "after the arrays" and lite.tensors == full.tensors
+    assert lite.data_start == full.data_start
+    a0, a1 = full.spans["tokenizer.ggml.tokens"]
+    with pytest.raises(ValueError):
+        gguf.GGUF(data2[:a0 + (a1 - a0) // 2], light=True)
     a, b = g.spans["a.u32"]
     assert struct.unpack_from("<I", data, a)[0] == 7 and b - a == 4
     with pytest.raises(ValueError):
