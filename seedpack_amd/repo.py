@@ -1602,9 +1602,15 @@ class Unpacker:
                 if i not in ahead:
                     ahead[i] = self.ahead.submit(residual_of, i)
         top_up()
+        # the QR predictions of a file whose residual is still decompressing are queued meanwhile (the
+        # device regrows while the host's zstd streams run)
+        made = {}
         while left:
             tf = time.perf_counter()
             ready = [i for i in left if i in ahead and not srcs[i] - done]
+            for i in sorted(ready, key=lambda i: mf[i]["size"]):      # the frame that ends first first
+                if i not in made and not ahead[i].done() and mf[i]["plan"] and mf[i]["base"] is not None:
+                    made[i] = self._predict_qr(r, i, mf[i], bases[mf[i]["base"]], imx_map)
             futures_wait([ahead[i] for i in ready], return_when="FIRST_COMPLETED")
             i = next(i for i in ready if ahead[i].done())
             m = mf[i]
@@ -1615,7 +1621,7 @@ class Unpacker:
             tm, known = {}, None
             if m["plan"]:
                 tm, known = self._rebuild(r, i, m, bases[m["base"]], resid, kept, users, done, imx_dev, imx_off,
-                                          imx_map, algo == "blake3" and m["name"] in want)
+                                          imx_map, algo == "blake3" and m["name"] in want, made.pop(i, None))
             done.add(i)
             if m["name"] in want:
                 jobs.append(self.files.submit(check_write, m["name"], resid, True, known))
@@ -1665,7 +1671,37 @@ class Unpacker:
                 "missing": [n for n in want if n not in results], "bytes": nbytes_, "seconds": dt,
                 "GB_s": nbytes_ / dt / 1e9}
 
-    def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map, digest=False):
+    PREDICT_AHEAD = 32 << 30             # bytes of QR predictions a file may have made before its residual
+
+    def _predict_qr(self, r, i, m, b, imx_map):
+        """(before file i's residual is decompressed) the predictions of its QR batches' tensors, queued
+        on the device -> (QR chunk parts, batch list, {name: prediction}), or None when its base is not
+        in HBM or they would take more than PREDICT_AHEAD bytes. They need only the base, the plan and
+        the importance; the file's header, in the residual, is not read."""
+        plan = m["plan"]
+        if b.d is None or not any(e[1] == "qr" for e in plan):
+            return None
+        ch = unpack(memoryview(r.get(f"q{i}")))
+        batches = json.loads(zstd.decompress(ch["meta"]))
+        var = {e[0]: e[2] for e in plan}
+        ttype = {e[0]: e[3] for e in plan if len(e) > 3}
+        names = [n for _, ns in batches for n in ns]
+        if any(n not in ttype for n in names):
+            return None
+        need = sum(b.by_name[n].numel // QFUN[ttype[n]][1] * QFUN[ttype[n]][2] if ttype[n] in QFUN else 0 for n in names)
+        if need > self.PREDICT_AHEAD:
+            return None
+        st = self.stream.handle
+        preds = {}
+        for n in names:
+            bt = b.by_name[n]
+            t = residual.Tensor(n, ttype[n], bt.shape[0], None, b.view(bt, st), imatrix=imx_map.get(n),
+                                fitted={k: s_[n] for k, s_ in self.imx_sets.items() if n in s_}, base_type=bt.type,
+                                numel=bt.numel)
+            preds[n] = residual.predict(self.gq, t, var[n], stream=st)
+        return ch, batches, preds
+
+    def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map, digest=False, pre=None):
         """file i's bytes from its residual (in `resid`, rebuilt in place) on the device -> (phase
         times, the file's BLAKE3 hex digest computed on the device when `digest`, else None)"""
         st = self.stream.handle
@@ -1715,12 +1751,17 @@ class Unpacker:
                 check(lib().spa_xor(t.region.ptr, t.region.ptr, p.ptr, t.region.nbytes, None, st))
         lap("regrow+xor")
         if any(e[1] == "qr" for e in plan):
-            ch = unpack(memoryview(r.get(f"q{i}")))
+            if pre is not None:
+                ch, batches, made = pre
+            else:
+                ch = unpack(memoryview(r.get(f"q{i}")))
+                batches, made = json.loads(zstd.decompress(ch["meta"])), {}
             var = {e[0]: e[2] for e in plan}
-            for k, (T, names) in enumerate(json.loads(zstd.decompress(ch["meta"]))):
+            for k, (T, names) in enumerate(batches):
                 bw = b.window(names, st)
                 ts = [tensor(n, bw) for n in names]
-                preds = [residual.predict(self.gq, t, var[t.name], stream=st) for t in ts]
+                preds = [made.pop(t.name) if t.name in made else residual.predict(self.gq, t, var[t.name], stream=st)
+                         for t in ts]
                 items = [(p, bw.by_name[t.name].offset, bw.by_name[t.name].type, bw.by_name[t.name].shape[0],
                           imx_off.get(t.name, -1) if T in qr.GRID_TYPES else -1) for t, p in zip(ts, preds)]
                 F = qr.decode(T, bytes(ch[str(k)]), items, bw.d, imx_dev if T in qr.GRID_TYPES else None, stream=st)
