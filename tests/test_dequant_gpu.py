@@ -49,16 +49,40 @@ def test_dequant_of_quantized(gq, t):
     _check(gq, t, q.to_host() if isinstance(q, dev.DeviceArray) else np.asarray(q), npr)
 
 
-@pytest.mark.parametrize("t", TYPES)
-def test_dequant_of_random_blocks(gq, t):
-    say("case dequant of random blocks", NAMES[t])
-    g = np.random.Generator(np.random.PCG64(71 + t))
-    qk, bs = QFUN[t][1], QFUN[t][2]
-    nb = 4096 * 32 // qk
+def _random_blocks(g, t, nb):
+    """nb blocks of random bytes with finite fp16 fields"""
+    bs = QFUN[t][2]
     b = g.integers(0, 256, (nb, bs), dtype=np.uint8)
     for o in F16_FIELDS[t]:
         h = (g.normal(0, 0.05, nb)).astype(np.float16)
         b[:, o:o + 2] = h.view(np.uint8).reshape(nb, 2)
     if t == 29:
         b[:, 55] &= 0xBF                      # the scale's exponent stays below 31 (finite)
-    _check(gq, t, b.reshape(-1), qk * 32)
+    return b.reshape(-1)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_dequant_of_random_blocks(gq, t):
+    say("case dequant of random blocks", NAMES[t])
+    g = np.random.Generator(np.random.PCG64(71 + t))
+    qk = QFUN[t][1]
+    _check(gq, t, _random_blocks(g, t, 4096 * 32 // qk), qk * 32)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_dequant_part_tile_and_unaligned_source(gq, t):
+    """a block count that leaves a part tile of 4096 weights (and one single block), with the source
+    at byte offsets 0, 1, 2, 4 and 8 of an allocation (the kernel's 16-, 4- and 1-byte copy paths)"""
+    say("case dequant part tile, unaligned", NAMES[t])
+    g = np.random.Generator(np.random.PCG64(81 + t))
+    qk, bs = QFUN[t][1], QFUN[t][2]
+    for nb in (1, 4096 // qk * 3 + 5):
+        blocks = _random_blocks(g, t, nb)
+        want = ref.dequantize(t, blocks, nb * qk)
+        for off in (0, 1, 2, 4, 8):
+            raw = np.zeros(nb * bs + 16, np.uint8)
+            raw[off:off + nb * bs] = blocks
+            d = dev.DeviceArray.from_host(raw)
+            view = dev.DeviceArray(nb * bs, np.uint8, ptr=d.ptr + off, owner=d)
+            got = gq.dequantize(t, view, qk).to_host()
+            assert got.view(np.uint32).tobytes() == want.view(np.uint32).tobytes(), (NAMES[t], nb, off)
