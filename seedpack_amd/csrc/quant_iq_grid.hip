@@ -961,16 +961,43 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(Cfg<K>::WPE)
     };
     // the IQ1 searches hold sorted copies and prefix sums: x and w are read again afterwards (same
     // values) rather than kept in registers through them, from the element offset, importance offset
-    // and sigma^2 parked in this thread's LDS slot (no register holds them through the search)
+    // and sigma^2 parked in this thread's LDS slot (no register holds them through the search). With
+    // a 16-bit source the sub-block's raw values (2N bytes, at most a Park) wait in the thread's own
+    // park slot, which its parked result overwrites only after the last reload; an f32 source is
+    // read again from global memory.
+    static_assert(!IQ1 || 2 * N <= (int)sizeof(Park), "a sub-block's 16-bit values fit a park slot");
     __shared__ uint4 stash[IQ1 ? WG : 1];
+    const bool raw16 = kind != SRC_F32;
     if constexpr (IQ1) {
         const uint64_t eo = (uint64_t)(sbc * 256 + sub * N);
         stash[threadIdx.x] = make_uint4((uint32_t)eo, (uint32_t)(eo >> 32), (uint32_t)((sbc % sbpr) * 256 + sub * N),
                                         __float_as_uint(sigma2));
+        if (raw16) {
+            const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + eo);
+            uint4* slot = reinterpret_cast<uint4*>(&park[lsb][sub]);
+#pragma unroll
+            for (int k = 0; k < N / 8; ++k) slot[k] = p[k];
+        }
     }
     auto reload = [&](float (&xv)[N], float (&wv)[N]) {
         const uint4 st = stash[tid()];
-        load_weights<N>(src, kind, (int64_t)(((uint64_t)st.y << 32) | st.x), xv);
+        if (raw16) {
+            // the same widening as load_weights, from the raw values in the park slot
+            const uint4* slot = reinterpret_cast<const uint4*>(&park[tid() / G][tid() % G]);
+            const bool bf = kind == SRC_BF16;
+#pragma unroll
+            for (int k = 0; k < N / 8; ++k) {
+                const uint4 v = slot[k];
+                const uint32_t c[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t h = (j & 1) ? (c[j / 2] >> 16) : (c[j / 2] & 0xffffu);
+                    xv[8 * k + j] = bf ? bf16_to_f32(h) : f16_to_f32(h);
+                }
+            }
+        } else {
+            load_weights<N>(src, kind, (int64_t)(((uint64_t)st.y << 32) | st.x), xv);
+        }
         const float s2 = __uint_as_float(st.w);
         if (imx) {
             const float* qw = imx + st.z;
