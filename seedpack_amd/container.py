@@ -308,6 +308,26 @@ class Reader:
             raise FormatError(f"{self.path}: chunk {name} is damaged (CRC mismatch)")
         return data
 
+    def get_streamed(self, name, on_piece, pool, step=2 * PIECE):
+        """the whole chunk as get() returns it, read in pieces of `step` bytes by the threads of `pool`;
+        on_piece(offset, piece) runs in the reading thread as each piece arrives (before the chunk's
+        CRC is known: a damaged chunk still raises once every piece is in)"""
+        _, n, crc = self.chunks[name]
+        data = np.empty(n, np.uint8)
+
+        def one(o):
+            k = min(step, n - o)
+            v = data[o:o + k]
+            self.read_at(name, o, k, v)
+            on_piece(o, v)
+            return crc32(v), k
+        c = 0
+        for pc, k in pool.map(one, range(0, n, step)):
+            c = crc32_combine(c, pc, k)
+        if c != crc:
+            raise FormatError(f"{self.path}: chunk {name} is damaged (CRC mismatch)")
+        return data
+
     def close(self):
         if self.fd is not None:
             os.close(self.fd)

@@ -518,7 +518,7 @@ class BF16v2:
         ch["rest"] = rest
         return pack_parts({k: ch[k] for k in self.ORDER[order]})
 
-    def decompress(self, parts, out=None, device=False, alloc=None, into=None, rest=None):
+    def decompress(self, parts, out=None, device=False, alloc=None, into=None, rest=None, stream_dev=None):
         """the file back (bf16v2.py:422-486): `parts` is compress()'s dict or a packed chunk
         (compress_parts' bytes); the coded tensors are decoded on the device, the other bytes come
         from `out` (already in place) or from the "rest" part when there is one, else zeros.
@@ -526,7 +526,8 @@ class BF16v2:
         DeviceArray of the file's bytes up to the end of its last coded tensor, only the coded
         tensors written (decompress_dev); device="full": the whole file in HBM (in `into`, a
         DeviceArray of the file's size, if given), the other bytes uploaded from the "rest" part
-        (-> (DeviceArray, rest_of bytes)); rest: that part already decoded (header_d), if it is."""
+        (-> (DeviceArray, rest_of bytes)); rest: that part already decoded (header_d), if it is;
+        stream_dev: (device="full") the "stream" part already in HBM (stream_buffer(), filled)."""
         st = self.stream
         tm = _Timer(self.timing, st)
         if not isinstance(parts, dict):
@@ -535,7 +536,7 @@ class BF16v2:
         tm.lap("tables")
         layout, nt = dec.layout, len(dec.layout["t"])
         if device == "full":
-            return self._decompress_full(parts, dec, tm, into, rest)
+            return self._decompress_full(parts, dec, tm, into, rest, stream_dev)
         if nt == 0 and device:
             return dev.DeviceArray(1, np.uint8)
         if nt:
@@ -562,14 +563,16 @@ class BF16v2:
             fill_rest(out, header_d(bytes(parts["rest"])), layout)
         return out
 
-    def _decompress_full(self, parts, dec, tm, into=None, rest=None):
+    def _decompress_full(self, parts, dec, tm, into=None, rest=None, stream_dev=None):
         st, layout = self.stream, dec.layout
         if into is not None and into.nbytes != layout["size"]:
             raise ValueError(f"a file of {layout['size']} bytes for a place of {into.nbytes}")
         d = into if into is not None else dev.DeviceArray(max(1, layout["size"]), np.uint8)
         t = layout["t"]
         if t:
-            s_d = _Decoder.upload(parts["stream"], st)
+            if stream_dev is not None and stream_dev.nbytes < len(parts["stream"]):
+                raise ValueError("the device stream is shorter than the chunk's stream part")
+            s_d = stream_dev if stream_dev is not None else _Decoder.upload(parts["stream"], st)
             idxs = list(range(len(t)))
             dec.run(s_d, dec.soff[:-1], d, idxs, [x[0] for x in t], tm)
         if rest is None:
@@ -585,6 +588,12 @@ class BF16v2:
         dev.synchronize(st)
         self.last_timing = tm.result()
         return d, rest
+
+
+def stream_buffer(n):
+    """a device buffer for n bytes of coded stream, padded to a whole number of 16-byte blocks (the
+    decoder's reads)"""
+    return dev.DeviceArray(max(16, -(-n // 16) * 16), np.uint8)
 
 
 class _Decoder:
@@ -642,7 +651,7 @@ class _Decoder:
         of 16-byte blocks (the decoder's reads)"""
         pieces = [np.frombuffer(p, np.uint8) for p in (stream_h if isinstance(stream_h, list) else [stream_h])]
         n = sum(len(p) for p in pieces)
-        d = dev.DeviceArray(max(16, -(-n // 16) * 16), np.uint8)
+        d = stream_buffer(n)
         o = 0
         for p in pieces:
             if len(p):

@@ -43,6 +43,7 @@ import fnmatch
 import hashlib
 import json
 import lzma
+import mmap
 import os
 import re
 import resource
@@ -312,8 +313,55 @@ class _PinnedPool:
             self.cv.notify_all()
 
 
-def _write_file(path, mv, pool, step=64 << 20):
-    """the bytes mv as the file `path`, written in parallel pieces"""
+def _preallocate(path, n):
+    """the file `path` created with n bytes reserved (posix_fallocate) -> True; False (and no file) where
+    the filesystem cannot reserve them. A file whose blocks are reserved can be filled through a shared
+    mapping without the risk of a fault on a full disk."""
+    fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+    try:
+        if n:
+            os.posix_fallocate(fd, 0, n)
+        return True
+    except OSError:
+        os.close(fd)
+        fd = None
+        os.remove(path)
+        return False
+    finally:
+        if fd is not None:
+            os.close(fd)
+
+
+def _fill_mapped(m, mv, pool, step):
+    """mv copied into the mapping m in parallel pieces -> the first error, or None; every copy has
+    finished and no view of m is left when it returns, so m can be closed"""
+    dst, src = np.frombuffer(m, np.uint8), np.frombuffer(mv, np.uint8)
+    futs = [pool.submit(np.copyto, dst[o:o + step], src[o:o + step]) for o in range(0, len(src), step)]
+    futures_wait(futs)
+    errs = [e for e in (f.exception() for f in futs) if e is not None]
+    del dst, src, futs
+    return errs[0] if errs else None
+
+
+def _write_file(path, mv, pool, step=64 << 20, reserved=False):
+    """the bytes mv as the file `path`, written in parallel pieces. reserved: the file already has its
+    size with its blocks reserved (_preallocate); it is then filled through a shared mapping, whose page
+    faults proceed in parallel (buffered writes to one file are serialised by the kernel's per-file
+    lock)."""
+    n = len(mv)
+    if reserved and n > step and os.path.getsize(path) == n:
+        fd = os.open(path, os.O_RDWR)
+        try:
+            m = mmap.mmap(fd, n, mmap.MAP_SHARED, mmap.PROT_READ | mmap.PROT_WRITE)
+        finally:
+            os.close(fd)
+        try:
+            err = _fill_mapped(m, mv, pool, step)
+        finally:
+            m.close()
+        if err is not None:
+            raise err
+        return
     fd = os.open(path, os.O_WRONLY | os.O_CREAT | os.O_TRUNC, 0o644)
     try:
         def piece(o):
@@ -321,10 +369,10 @@ def _write_file(path, mv, pool, step=64 << 20):
             done = 0
             while done < len(v):
                 done += os.pwrite(fd, v[done:], o + done)
-        if len(mv) <= step:
+        if n <= step:
             piece(0)
         else:
-            for f in [pool.submit(piece, o) for o in range(0, len(mv), step)]:
+            for f in [pool.submit(piece, o) for o in range(0, n, step)]:
                 f.result()
     finally:
         os.close(fd)
@@ -1330,7 +1378,10 @@ class Unpacker:
         self.pool = _PinnedPool(staging_bytes)
         self.rbuf = _DevBuf()
         self.files = ThreadPoolExecutor(4)        # a finished file: checked and written
-        self.io = ThreadPoolExecutor(8)           # its write, in pieces
+        self.io = ThreadPoolExecutor(16)          # its write, in pieces
+        self.readers = ThreadPoolExecutor(16)     # a base chunk read in pieces beside its upload
+        self.prealloc = ThreadPoolExecutor(2)     # the output files created and their size reserved
+        self.reserved = {}
         self.hasher = ThreadPoolExecutor(4)       # its checksum, beside the write
         self.ahead = ThreadPoolExecutor(2)        # the next files' residuals decompressed ahead
 
@@ -1340,11 +1391,32 @@ class Unpacker:
         prev_si = sys.getswitchinterval()
         if self.switch_interval:
             sys.setswitchinterval(self.switch_interval)
+        self.reserved = {}                        # .part path -> its preallocation (a future)
         try:
             return self._run(archive, outdir, patterns)
+        except BaseException:
+            # reserved files not written and renamed are not left behind
+            for path, f in self.reserved.items():
+                try:
+                    if f.result():
+                        os.remove(path)
+                except Exception:
+                    pass
+            raise
         finally:
+            self.reserved = {}
             sys.setswitchinterval(prev_si)
             dev.set_blocking_waits(prev)
+
+    def _reserve(self, outdir, name, size):
+        """the file's .part created and its size reserved on a side thread (the page allocation of a
+        memory filesystem then runs beside the rebuild, not in the write)"""
+        path = os.path.join(outdir, *name.split("/")) + ".part"
+
+        def job():
+            os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
+            return _preallocate(path, size)
+        self.reserved[path] = self.prealloc.submit(job)
 
     def _run(self, archive, outdir, patterns):
         t0 = time.perf_counter()
@@ -1374,6 +1446,10 @@ class Unpacker:
         need_b = {i for i, n in enumerate(manifest["bases"]) if n in want} | \
                  {mf[i]["base"] for i in sel if mf[i]["base"] is not None}
         results, jobs = {}, []
+        if outdir is not None:
+            for m in mf:
+                if m["name"] in want and m["size"] > (64 << 20):
+                    self._reserve(outdir, m["name"], m["size"])
 
         def check_write(name, buf, release=False, known=None):
             """the file's checksum (`known`: already computed on the device) and its write side by
@@ -1385,13 +1461,15 @@ class Unpacker:
                 if outdir is not None:
                     path = os.path.join(outdir, *name.split("/"))
                     os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
-                    _write_file(path + ".part", mv, self.io)
+                    pre = self.reserved.get(path + ".part")
+                    _write_file(path + ".part", mv, self.io, reserved=pre is not None and pre.result())
                 ok = mv.nbytes == cat[name]["size"] and (h.result() == cat[name]["hash"] if h else None)
                 if path is not None:
                     if ok is not False:
                         os.replace(path + ".part", path)
                     else:
                         os.remove(path + ".part")
+                    self.reserved.pop(path + ".part", None)
                 results[name] = ok
                 return ok
             finally:
@@ -1572,12 +1650,25 @@ class Unpacker:
                     stream_write(name, rt)
                 log(self.verbose, f"  base {name}: decoded window by window, {time.perf_counter() - t0:.1f} s")
                 continue
-            ch = unpack(memoryview(r.get(f"b{i}")))
+            s_d = None
+            if "layout" not in parts and "stream" in parts:
+                # an R2 chunk: its coded stream is copied into HBM piece by piece as the chunk is read
+                # (on a stream of its own), so the upload runs beside the read
+                so, sn = parts["stream"]
+                s_d, up = r2.stream_buffer(sn), dev.Stream()
+
+                def to_device(o, piece, so=so, sn=sn, s_d=s_d, up=up):
+                    a, b_ = max(o, so), min(o + len(piece), so + sn)
+                    if a < b_:
+                        check(lib().spa_memcpy_h2d(s_d.ptr + (a - so), piece[a - o:].ctypes.data, b_ - a, up.handle))
+                ch = unpack(memoryview(r.get_streamed(f"b{i}", to_device, self.readers)))
+            else:
+                ch = unpack(memoryview(r.get(f"b{i}")))
             log(self.verbose, f"  base {name}: chunk read, {time.perf_counter() - t0:.1f} s")
             if "r2" in ch:
                 ch = {"r2": unpack(ch["r2"])}
                 d, _ = r2.BF16v2(stream=self.stream.handle).decompress(ch["r2"], device="full", into=place.get(i),
-                                                                       rest=rest)
+                                                                       rest=rest, stream_dev=s_d)
             else:
                 d = M24BF16(stream=self.stream.handle).decompress_dev(ch, into=place.get(i), rest=rest)
             b = _Base(i, name, rest, d, g)
@@ -1602,15 +1693,15 @@ class Unpacker:
                 if i not in ahead:
                     ahead[i] = self.ahead.submit(residual_of, i)
         top_up()
-        # the QR predictions of a file whose residual is still decompressing are queued meanwhile (the
-        # device regrows while the host's zstd streams run)
+        # the QR batches of a file whose residual is still decompressing are regrown and decoded
+        # meanwhile (the device works while the host's zstd streams run)
         made = {}
         while left:
             tf = time.perf_counter()
             ready = [i for i in left if i in ahead and not srcs[i] - done]
             for i in sorted(ready, key=lambda i: mf[i]["size"]):      # the frame that ends first first
                 if i not in made and not ahead[i].done() and mf[i]["plan"] and mf[i]["base"] is not None:
-                    made[i] = self._predict_qr(r, i, mf[i], bases[mf[i]["base"]], imx_map)
+                    made[i] = self._predict_qr(r, i, mf[i], bases[mf[i]["base"]], imx_map, imx_dev, imx_off)
             futures_wait([ahead[i] for i in ready], return_when="FIRST_COMPLETED")
             i = next(i for i in ready if ahead[i].done())
             m = mf[i]
@@ -1673,11 +1764,12 @@ class Unpacker:
 
     PREDICT_AHEAD = 32 << 30             # bytes of QR predictions a file may have made before its residual
 
-    def _predict_qr(self, r, i, m, b, imx_map):
-        """(before file i's residual is decompressed) the predictions of its QR batches' tensors, queued
-        on the device -> (QR chunk parts, batch list, {name: prediction}), or None when its base is not
-        in HBM or they would take more than PREDICT_AHEAD bytes. They need only the base, the plan and
-        the importance; the file's header, in the residual, is not read."""
+    def _predict_qr(self, r, i, m, b, imx_map, imx_dev, imx_off):
+        """(before file i's residual is decompressed) its QR batches decoded on the device -> (QR chunk
+        parts, batch list, {batch index: its tensors' bytes back to back}), or None when its base is
+        not in HBM or the predictions would take more than PREDICT_AHEAD bytes. They need only the
+        base, the plan, the importance and the QR chunk; the file's header, in the residual, is not
+        read. Each batch's predictions are released once it is decoded."""
         plan = m["plan"]
         if b.d is None or not any(e[1] == "qr" for e in plan):
             return None
@@ -1699,7 +1791,15 @@ class Unpacker:
                                 fitted={k: s_[n] for k, s_ in self.imx_sets.items() if n in s_}, base_type=bt.type,
                                 numel=bt.numel)
             preds[n] = residual.predict(self.gq, t, var[n], stream=st)
-        return ch, batches, preds
+        decoded = {}
+        for k, (T, ns) in enumerate(batches):
+            items = [(preds[n], b.by_name[n].offset, b.by_name[n].type, b.by_name[n].shape[0],
+                      imx_off.get(n, -1) if T in qr.GRID_TYPES else -1) for n in ns]
+            decoded[k] = qr.decode(T, bytes(ch[str(k)]), items, b.d, imx_dev if T in qr.GRID_TYPES else None, stream=st)
+            del items
+            for n in ns:
+                del preds[n]
+        return ch, batches, decoded
 
     def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map, digest=False, pre=None):
         """file i's bytes from its residual (in `resid`, rebuilt in place) on the device -> (phase
@@ -1752,24 +1852,26 @@ class Unpacker:
         lap("regrow+xor")
         if any(e[1] == "qr" for e in plan):
             if pre is not None:
-                ch, batches, made = pre
+                ch, batches, decoded = pre
             else:
                 ch = unpack(memoryview(r.get(f"q{i}")))
-                batches, made = json.loads(zstd.decompress(ch["meta"])), {}
+                batches, decoded = json.loads(zstd.decompress(ch["meta"])), {}
             var = {e[0]: e[2] for e in plan}
             for k, (T, names) in enumerate(batches):
                 bw = b.window(names, st)
                 ts = [tensor(n, bw) for n in names]
-                preds = [made.pop(t.name) if t.name in made else residual.predict(self.gq, t, var[t.name], stream=st)
-                         for t in ts]
-                items = [(p, bw.by_name[t.name].offset, bw.by_name[t.name].type, bw.by_name[t.name].shape[0],
-                          imx_off.get(t.name, -1) if T in qr.GRID_TYPES else -1) for t, p in zip(ts, preds)]
-                F = qr.decode(T, bytes(ch[str(k)]), items, bw.d, imx_dev if T in qr.GRID_TYPES else None, stream=st)
+                F = decoded.pop(k, None)
+                if F is None:
+                    preds = [residual.predict(self.gq, t, var[t.name], stream=st) for t in ts]
+                    items = [(p, bw.by_name[t.name].offset, bw.by_name[t.name].type, bw.by_name[t.name].shape[0],
+                              imx_off.get(t.name, -1) if T in qr.GRID_TYPES else -1) for t, p in zip(ts, preds)]
+                    F = qr.decode(T, bytes(ch[str(k)]), items, bw.d, imx_dev if T in qr.GRID_TYPES else None, stream=st)
+                    del preds, items
                 o = 0
                 for t in ts:
                     check(lib().spa_memcpy_d2d(t.region.ptr, F.ptr + o, t.region.nbytes, st))
                     o += t.region.nbytes
-                del F, preds
+                del F
         lap("qr")
         for e in plan:
             if e[1] in ("ref", "dup"):

@@ -163,6 +163,56 @@ def test_container_round_trip_streams_and_damage(tmp_path):
         container.Reader(p)
 
 
+def test_container_streamed_read_pieces_and_damage(tmp_path):
+    """get_streamed: every byte of the chunk reaches on_piece exactly once (pieces of any step,
+    several threads), the result equals get(), and a damaged chunk raises after its pieces are in"""
+    from concurrent.futures import ThreadPoolExecutor
+    p = str(tmp_path / "s.seedpack")
+    blob = np.random.default_rng(8).integers(0, 256, (5 << 20) + 333, dtype=np.uint8)
+    w = container.Writer(p)
+    w.put("a", b"x")
+    w.put("big", blob)
+    w.put("empty", b"")
+    w.close({})
+    pool = ThreadPoolExecutor(4)
+    r = container.Reader(p)
+    for step in (1 << 20, (1 << 20) + 7, 64 << 20):
+        seen = np.zeros(blob.size, np.int32)
+        copy = np.zeros(blob.size, np.uint8)
+
+        def on_piece(o, v):
+            seen[o:o + len(v)] += 1
+            copy[o:o + len(v)] = v
+        got = r.get_streamed("big", on_piece, pool, step)
+        assert np.array_equal(got, blob) and np.array_equal(copy, blob) and (seen == 1).all()
+    assert r.get_streamed("empty", lambda o, v: None, pool).size == 0
+    r.close()
+    raw = bytearray(open(p, "rb").read())
+    raw[12 + 1 + 4096] ^= 0x40              # a byte inside "big"
+    open(p, "wb").write(bytes(raw))
+    with pytest.raises(container.FormatError):
+        container.Reader(p).get_streamed("big", lambda o, v: None, pool, 1 << 20)
+
+
+def test_reserved_file_written_through_its_mapping(tmp_path):
+    """_preallocate then _write_file(reserved=True): the bytes land whole (pieces across the mapping,
+    a ragged last piece); a file of another size, or none reserved, takes the plain write path"""
+    from concurrent.futures import ThreadPoolExecutor
+    pool = ThreadPoolExecutor(4)
+    data = np.random.default_rng(9).integers(0, 256, (3 << 20) + 1234, dtype=np.uint8)
+    p = str(tmp_path / "out" / "f.part")
+    os.makedirs(os.path.dirname(p))
+    assert repo._preallocate(p, data.size) and os.path.getsize(p) == data.size
+    repo._write_file(p, memoryview(data), pool, step=1 << 20, reserved=True)
+    assert open(p, "rb").read() == data.tobytes()
+    assert repo._preallocate(p, data.size + 5)
+    repo._write_file(p, memoryview(data), pool, step=1 << 20, reserved=True)   # size differs: plain path
+    assert open(p, "rb").read() == data.tobytes()
+    q = str(tmp_path / "g")
+    repo._write_file(q, memoryview(data[:100]), pool, reserved=False)
+    assert open(q, "rb").read() == data[:100].tobytes()
+
+
 def test_container_abort_leaves_nothing(tmp_path):
     p = str(tmp_path / "b.seedpack")
     w = container.Writer(p)
