@@ -313,6 +313,18 @@ class _PinnedPool:
             self.cv.notify_all()
 
 
+def _prefault(buf, pool, step=64 << 20):
+    """every page of a host buffer written once (zeros), by the threads of `pool`: a freshly allocated
+    page-locked buffer takes its pages' first-touch faults at about 3 GB/s in one thread (a single
+    zstd stream filling it), and about six times faster from 16 threads at once"""
+    a = np.frombuffer(memoryview(buf).cast("B"), np.uint8)
+
+    def one(o):
+        a[o:o + step:4096] = 0
+    for f in [pool.submit(one, o) for o in range(0, a.size, step)]:
+        f.result()
+
+
 def _preallocate(path, n):
     """the file `path` created with n bytes reserved (posix_fallocate) -> True; False (and no file) where
     the filesystem cannot reserve them. A file whose blocks are reserved can be filled through a shared
@@ -1381,6 +1393,7 @@ class Unpacker:
         self.io = ThreadPoolExecutor(16)          # its write, in pieces
         self.readers = ThreadPoolExecutor(16)     # a base chunk read in pieces beside its upload
         self.prealloc = ThreadPoolExecutor(2)     # the output files created and their size reserved
+        self.faulters = ThreadPoolExecutor(16)    # a residual's page-locked buffer faulted in before zstd fills it
         self.reserved = {}
         self.hasher = ThreadPoolExecutor(4)       # its checksum, beside the write
         self.ahead = ThreadPoolExecutor(2)        # the next files' residuals decompressed ahead
@@ -1611,6 +1624,7 @@ class Unpacker:
         def residual_of(i):
             m = mf[i]
             resid = self.pool.acquire(m["size"])[:m["size"]]
+            _prefault(resid, self.faulters)
             if m.get("codec") == "q8":                      # a base-less file coded by the Q8_0 codec
                 s_ = dev.Stream()
                 Q8Parts(stream=s_.handle).decompress(r.get(f"f{i}"), out=resid)
