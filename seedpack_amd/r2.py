@@ -577,17 +577,24 @@ class BF16v2:
             dec.run(s_d, dec.soff[:-1], d, idxs, [x[0] for x in t], tm)
         if rest is None:
             rest = np.frombuffer(header_d(bytes(parts["rest"])), np.uint8)
-        staged = dev.pinned(max(1, rest.size))
-        staged[:] = rest
-        pos = taken = 0
-        for off, nb, *_ in t + [[layout["size"], 0]]:
-            if off > pos:                             # the bytes between coded tensors
-                check(lib().spa_memcpy_h2d(d.ptr + pos, staged[taken:].ctypes.data, off - pos, st))
-                taken += off - pos
-            pos = off + nb
-        dev.synchronize(st)
+        upload_rest(d, layout, rest, st)
         self.last_timing = tm.result()
         return d, rest
+
+
+def upload_rest(d, layout, rest, st):
+    """the file's bytes between its coded tensors (the decoded "rest" part, in file order) into the
+    device copy d of the file; returns once they are there"""
+    t = layout["t"]
+    staged = dev.pinned(max(1, rest.size))
+    staged[:] = rest
+    pos = taken = 0
+    for off, nb, *_ in t + [[layout["size"], 0]]:
+        if off > pos:
+            check(lib().spa_memcpy_h2d(d.ptr + pos, staged[taken:].ctypes.data, off - pos, st))
+            taken += off - pos
+        pos = off + nb
+    dev.synchronize(st)
 
 
 def stream_buffer(n):

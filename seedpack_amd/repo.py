@@ -1370,6 +1370,38 @@ def select_names(catalog, patterns):
     return chosen
 
 
+class _QRAhead:
+    """a file's QR batches regrown and decoded on the main stream before its residual is in, each once
+    the base tensors it predicts from are decoded (Unpacker._qr_ahead)"""
+
+    def __init__(self, u, ch, batches, var, ttype, b, imx_map, imx_dev, imx_off):
+        self.u, self.ch, self.batches, self.var, self.ttype, self.b = u, ch, batches, var, ttype, b
+        self.imx_map, self.imx_dev, self.imx_off = imx_map, imx_dev, imx_off
+        self.decoded = {}
+
+    def step(self, ready):
+        """the batches not decoded yet whose tensors are all in `ready` (None: every batch)"""
+        u, b, st = self.u, self.b, self.u.stream.handle
+        for k, (T, ns) in enumerate(self.batches):
+            if k in self.decoded or (ready is not None and not all(n in ready for n in ns)):
+                continue
+            preds = []
+            for n in ns:
+                bt = b.by_name[n]
+                t = residual.Tensor(n, self.ttype[n], bt.shape[0], None, b.view(bt, st), imatrix=self.imx_map.get(n),
+                                    fitted={k_: s_[n] for k_, s_ in u.imx_sets.items() if n in s_}, base_type=bt.type,
+                                    numel=bt.numel)
+                preds.append(residual.predict(u.gq, t, self.var[n], stream=st))
+            items = [(p, b.by_name[n].offset, b.by_name[n].type, b.by_name[n].shape[0],
+                      self.imx_off.get(n, -1) if T in qr.GRID_TYPES else -1) for p, n in zip(preds, ns)]
+            self.decoded[k] = qr.decode(T, bytes(self.ch[str(k)]), items, b.d,
+                                        self.imx_dev if T in qr.GRID_TYPES else None, stream=st)
+            del items, preds
+
+    def result(self):
+        return self.ch, self.batches, self.decoded
+
+
 class Unpacker:
     """the files of an archive rebuilt and checked against their SHA-256 (repo3.py:2277-2509,
     cli.py:309-441): each base decoded into HBM once; each quantized file's residual decompressed on
@@ -1394,6 +1426,7 @@ class Unpacker:
         self.readers = ThreadPoolExecutor(16)     # a base chunk read in pieces beside its upload
         self.prealloc = ThreadPoolExecutor(2)     # the output files created and their size reserved
         self.faulters = ThreadPoolExecutor(16)    # a residual's page-locked buffer faulted in before zstd fills it
+        self.base_reader = ThreadPoolExecutor(1)  # a base chunk's streamed read, beside its decode
         self.reserved = {}
         self.hasher = ThreadPoolExecutor(4)       # its checksum, beside the write
         self.ahead = ThreadPoolExecutor(2)        # the next files' residuals decompressed ahead
@@ -1559,6 +1592,7 @@ class Unpacker:
         # first residuals decompress while the bases decode on the device (repo3.py:2324-2333); the
         # shards of a split model that a file predicts from one after another in one allocation
         # (repo3.py:2307-2313)
+        log(self.verbose, f"  extras and importance read, {time.perf_counter() - t0:.2f} s")
         bases, place, jd, zdicts, coded = {}, {}, {}, {}, {}
         phys = sorted({i for i in need_b if i < nb} |
                       {i for k, j in enumerate(joined) if nb + k in need_b for i, _ in j["parts"]})
@@ -1595,6 +1629,7 @@ class Unpacker:
         # an M24 base (method m28) has no random access and is always decoded whole; an R2 base is
         # whole when forced (bases_in_hbm True) or, by default, while the bases so far, the largest
         # file to rebuild and a 48 GB reserve fit; a split model's shards are whole only together
+        log(self.verbose, f"  base headers read, {time.perf_counter() - t0:.2f} s")
         whole = {}
         free = dev.mem_info()[0] if self.bases_in_hbm is None else 0
         room = free - max((mf[i]["size"] for i in sel), default=0) - (48 << 30)
@@ -1641,6 +1676,7 @@ class Unpacker:
             if room < 0:
                 break
             ahead[i] = self.ahead.submit(residual_of, i)
+        made_early = {}                                     # file index -> its QR batches decoded during the base read
         for i in phys:
             if i not in coded:
                 continue
@@ -1664,28 +1700,34 @@ class Unpacker:
                     stream_write(name, rt)
                 log(self.verbose, f"  base {name}: decoded window by window, {time.perf_counter() - t0:.1f} s")
                 continue
-            s_d = None
-            if "layout" not in parts and "stream" in parts:
-                # an R2 chunk: its coded stream is copied into HBM piece by piece as the chunk is read
-                # (on a stream of its own), so the upload runs beside the read
-                so, sn = parts["stream"]
-                s_d, up = r2.stream_buffer(sn), dev.Stream()
+            if "layout" not in parts and "stream" in parts and i not in place:
+                # an R2 base: decoded tensor by tensor as its coded stream reaches HBM, the QR batches of
+                # the files whose residuals decompress ahead regrown as the tensors they need are in
+                users_i = [f for f in ahead if mf[f]["base"] == i and mf[f]["plan"]]
+                early = {}
 
-                def to_device(o, piece, so=so, sn=sn, s_d=s_d, up=up):
-                    a, b_ = max(o, so), min(o + len(piece), so + sn)
-                    if a < b_:
-                        check(lib().spa_memcpy_h2d(s_d.ptr + (a - so), piece[a - o:].ctypes.data, b_ - a, up.handle))
-                ch = unpack(memoryview(r.get_streamed(f"b{i}", to_device, self.readers)))
+                def on_ready(b, ready, users_i=users_i, early=early):
+                    for f in users_i:
+                        if f not in early:
+                            early[f] = self._qr_ahead(r, f, mf[f], b, imx_map, imx_dev, imx_off)
+                        if early[f] is not None:
+                            early[f].step(ready)
+                b = self._base_streamed(r, f"b{i}", parts, rest, g, i, name, on_ready)
+                d = b.d
+                for f, q in early.items():
+                    if q is not None:
+                        made_early[f] = q.result()
+                log(self.verbose, f"  base {name}: read and decoded, {time.perf_counter() - t0:.1f} s")
             else:
                 ch = unpack(memoryview(r.get(f"b{i}")))
-            log(self.verbose, f"  base {name}: chunk read, {time.perf_counter() - t0:.1f} s")
-            if "r2" in ch:
-                ch = {"r2": unpack(ch["r2"])}
-                d, _ = r2.BF16v2(stream=self.stream.handle).decompress(ch["r2"], device="full", into=place.get(i),
-                                                                       rest=rest, stream_dev=s_d)
-            else:
-                d = M24BF16(stream=self.stream.handle).decompress_dev(ch, into=place.get(i), rest=rest)
-            b = _Base(i, name, rest, d, g)
+                log(self.verbose, f"  base {name}: chunk read, {time.perf_counter() - t0:.1f} s")
+                if "r2" in ch:
+                    ch = {"r2": unpack(ch["r2"])}
+                    d, _ = r2.BF16v2(stream=self.stream.handle).decompress(ch["r2"], device="full", into=place.get(i),
+                                                                           rest=rest)
+                else:
+                    d = M24BF16(stream=self.stream.handle).decompress_dev(ch, into=place.get(i), rest=rest)
+                b = _Base(i, name, rest, d, g)
             bases[i] = b
             if name in want:
                 host = self.pool.acquire(d.nbytes)[:d.nbytes]
@@ -1709,7 +1751,7 @@ class Unpacker:
         top_up()
         # the QR batches of a file whose residual is still decompressing are regrown and decoded
         # meanwhile (the device works while the host's zstd streams run)
-        made = {}
+        made = made_early
         while left:
             tf = time.perf_counter()
             ready = [i for i in left if i in ahead and not srcs[i] - done]
@@ -1778,18 +1820,16 @@ class Unpacker:
 
     PREDICT_AHEAD = 32 << 30             # bytes of QR predictions a file may have made before its residual
 
-    def _predict_qr(self, r, i, m, b, imx_map, imx_dev, imx_off):
-        """(before file i's residual is decompressed) its QR batches decoded on the device -> (QR chunk
-        parts, batch list, {batch index: its tensors' bytes back to back}), or None when its base is
-        not in HBM or the predictions would take more than PREDICT_AHEAD bytes. They need only the
-        base, the plan, the importance and the QR chunk; the file's header, in the residual, is not
-        read. Each batch's predictions are released once it is decoded."""
+    def _qr_ahead(self, r, i, m, b, imx_map, imx_dev, imx_off):
+        """file i's QR batches, to be regrown and decoded on the device before its residual is in (they
+        need only the base, the plan, the importance and the QR chunk; the file's header, in the
+        residual, is not read) -> a _QRAhead, or None when its base is not in HBM, its plan has no QR
+        batch or the predictions would take more than PREDICT_AHEAD bytes"""
         plan = m["plan"]
         if b.d is None or not any(e[1] == "qr" for e in plan):
             return None
         ch = unpack(memoryview(r.get(f"q{i}")))
         batches = json.loads(zstd.decompress(ch["meta"]))
-        var = {e[0]: e[2] for e in plan}
         ttype = {e[0]: e[3] for e in plan if len(e) > 3}
         names = [n for _, ns in batches for n in ns]
         if any(n not in ttype for n in names):
@@ -1797,23 +1837,89 @@ class Unpacker:
         need = sum(b.by_name[n].numel // QFUN[ttype[n]][1] * QFUN[ttype[n]][2] if ttype[n] in QFUN else 0 for n in names)
         if need > self.PREDICT_AHEAD:
             return None
+        return _QRAhead(self, ch, batches, {e[0]: e[2] for e in plan}, ttype, b, imx_map, imx_dev, imx_off)
+
+    def _predict_qr(self, r, i, m, b, imx_map, imx_dev, imx_off):
+        """(before file i's residual is decompressed) its QR batches decoded on the device -> (QR chunk
+        parts, batch list, {batch index: its tensors' bytes back to back}), or None (_qr_ahead)"""
+        q = self._qr_ahead(r, i, m, b, imx_map, imx_dev, imx_off)
+        if q is None:
+            return None
+        q.step(None)
+        return q.result()
+
+    def _base_streamed(self, r, c, parts, rest, g, index, name, on_ready):
+        """an R2 base chunk read in pieces (CRC-checked once all are in), its coded stream copied into HBM
+        piece by piece beside the read (on a stream of its own), and its tensors decoded in file order
+        on the main stream as soon as their segments are in HBM; on_ready(base, names) runs after each
+        group, names being the base tensors decoded so far (all of them, None, once the file is
+        complete) -> the base, whole in HBM"""
         st = self.stream.handle
-        preds = {}
-        for n in names:
-            bt = b.by_name[n]
-            t = residual.Tensor(n, ttype[n], bt.shape[0], None, b.view(bt, st), imatrix=imx_map.get(n),
-                                fitted={k: s_[n] for k, s_ in self.imx_sets.items() if n in s_}, base_type=bt.type,
-                                numel=bt.numel)
-            preds[n] = residual.predict(self.gq, t, var[n], stream=st)
-        decoded = {}
-        for k, (T, ns) in enumerate(batches):
-            items = [(preds[n], b.by_name[n].offset, b.by_name[n].type, b.by_name[n].shape[0],
-                      imx_off.get(n, -1) if T in qr.GRID_TYPES else -1) for n in ns]
-            decoded[k] = qr.decode(T, bytes(ch[str(k)]), items, b.d, imx_dev if T in qr.GRID_TYPES else None, stream=st)
-            del items
-            for n in ns:
-                del preds[n]
-        return ch, batches, decoded
+        dec = r2._Decoder(lambda k: bytes(r.read_at(c, *parts[k])), st)
+        layout = dec.layout
+        t = layout["t"]
+        d = dev.DeviceArray(max(1, layout["size"]), np.uint8)
+        b = _Base(index, name, rest, d, g)
+        so, sn = parts["stream"]
+        s_d, up = r2.stream_buffer(sn), dev.Stream()
+        step = 2 * container.PIECE
+        done = np.zeros(-(-r.chunks[c][1] // step), bool)
+        cv = threading.Condition()
+
+        def to_device(o, piece):
+            a, b_ = max(o, so), min(o + len(piece), so + sn)
+            if a < b_:
+                check(lib().spa_memcpy_h2d(s_d.ptr + (a - so), piece[a - o:].ctypes.data, b_ - a, up.handle))
+            with cv:
+                done[o // step] = True
+                cv.notify_all()
+        fut = self.base_reader.submit(r.get_streamed, c, to_device, self.readers, step)
+
+        def uploaded():
+            """bytes of the stream part in HBM from its start (the pieces before the first missing one)"""
+            k = len(done) if done.all() else int(np.argmin(done))
+            return int(np.clip(k * step - so, 0, sn))
+        # a tensor's segments end at soff[seg0[i + 1]]; the decoder's reader looks up to 32 bytes
+        # further (bytes it loads but does not use), so those are waited for too
+        ends = dec.soff[dec.seg0[1:]].astype(np.int64) + 32
+        offs = {x[0]: tn.name for x in t for tn in g.tensors if tn.offset == x[0]}
+        ready, j, t0 = set(), 0, time.perf_counter()
+        lap = {"groups": 0, "decode": 0.0, "batches": 0.0, "stream in": None}
+        while j < len(t):
+            with cv:
+                while True:
+                    have = uploaded()
+                    k = j
+                    while k < len(t) and (ends[k] <= have or have >= sn):
+                        k += 1
+                    if k > j:
+                        break
+                    if fut.done():
+                        fut.result()                 # a read error
+                        raise container.FormatError(f"chunk {c}: the coded stream ended early")
+                    cv.wait(0.05)
+            if lap["stream in"] is None and have >= sn:
+                lap["stream in"] = round(time.perf_counter() - t0, 3)
+            idxs = list(range(j, k))
+            in_off = np.concatenate([dec.soff[dec.seg0[x]:dec.seg0[x + 1]] for x in idxs])
+            t1 = time.perf_counter()
+            dec.run(s_d, in_off, d, idxs, [t[x][0] for x in idxs])
+            t2 = time.perf_counter()
+            ready.update(offs[t[x][0]] for x in idxs if t[x][0] in offs)
+            j = k
+            on_ready(b, ready)
+            lap["groups"] += 1
+            lap["decode"] += t2 - t1
+            lap["batches"] += time.perf_counter() - t2
+        lap["tensors decoded"] = round(time.perf_counter() - t0, 3)
+        fut.result()                                 # the whole chunk read and CRC-checked
+        lap["chunk checked"] = round(time.perf_counter() - t0, 3)
+        r2.upload_rest(d, layout, rest, st)
+        on_ready(b, None)
+        lap["complete"] = round(time.perf_counter() - t0, 3)
+        lap["decode"], lap["batches"] = round(lap["decode"], 3), round(lap["batches"], 3)
+        log(self.verbose, f"  base {name}: streamed decode {lap}")
+        return b
 
     def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map, digest=False, pre=None):
         """file i's bytes from its residual (in `resid`, rebuilt in place) on the device -> (phase
