@@ -50,6 +50,7 @@ import resource
 import sys
 import threading
 import time
+import types
 import warnings
 from concurrent.futures import Future, ThreadPoolExecutor, wait as futures_wait
 
@@ -1492,6 +1493,22 @@ class Unpacker:
         need_b = {i for i, n in enumerate(manifest["bases"]) if n in want} | \
                  {mf[i]["base"] for i in sel if mf[i]["base"] is not None}
         results, jobs = {}, []
+        # a single R2 base that will be decoded whole: its chunk's read starts now, beside the reading
+        # of the extras, the importance and its header
+        early_read = {}
+        if len(need_b) == 1 and not joined and self.bases_in_hbm is not False:
+            i = next(iter(need_b))
+            name = manifest["bases"][i]
+            fits = self.bases_in_hbm or cat[name]["size"] <= dev.mem_info()[0] - max(
+                (mf[f]["size"] for f in sel), default=0) - (48 << 30)
+            if i < nb and name not in seeds and fits:
+                def read_(o, n, c=f"b{i}"):
+                    return bytes(r.read_at(c, o, n))
+                pp = index(read_, r.chunks[f"b{i}"][1])
+                if "r2" in pp:
+                    pp = index(read_, pp["r2"][1], pp["r2"][0])
+                    if "stream" in pp:
+                        early_read[i] = (pp, self._base_read(r, f"b{i}", pp))
         if outdir is not None:
             for m in mf:
                 if m["name"] in want and m["size"] > (64 << 20):
@@ -1712,7 +1729,9 @@ class Unpacker:
                             early[f] = self._qr_ahead(r, f, mf[f], b, imx_map, imx_dev, imx_off)
                         if early[f] is not None:
                             early[f].step(ready)
-                b = self._base_streamed(r, f"b{i}", parts, rest, g, i, name, on_ready)
+                er = early_read.pop(i, None)
+                b = self._base_streamed(r, f"b{i}", parts, rest, g, i, name, on_ready,
+                                        er[1] if er is not None and er[0] == parts else None)
                 d = b.d
                 for f, q in early.items():
                     if q is not None:
@@ -1848,32 +1867,38 @@ class Unpacker:
         q.step(None)
         return q.result()
 
-    def _base_streamed(self, r, c, parts, rest, g, index, name, on_ready):
-        """an R2 base chunk read in pieces (CRC-checked once all are in), its coded stream copied into HBM
-        piece by piece beside the read (on a stream of its own), and its tensors decoded in file order
-        on the main stream as soon as their segments are in HBM; on_ready(base, names) runs after each
-        group, names being the base tensors decoded so far (all of them, None, once the file is
-        complete) -> the base, whole in HBM"""
+    def _base_read(self, r, c, parts):
+        """the streamed read of R2 base chunk c started: the chunk read in pieces (CRC-checked once all
+        are in) by the reader threads, the bytes of its coded stream copied into HBM piece by piece as
+        they arrive (on a stream of its own) -> the read's state for _base_streamed"""
+        so, sn = parts["stream"]
+        st = types.SimpleNamespace(so=so, sn=sn, s_d=r2.stream_buffer(sn), up=dev.Stream(), step=2 * container.PIECE,
+                                   cv=threading.Condition())
+        st.done = np.zeros(-(-r.chunks[c][1] // st.step), bool)
+
+        def to_device(o, piece):
+            a, b_ = max(o, so), min(o + len(piece), so + sn)
+            if a < b_:
+                check(lib().spa_memcpy_h2d(st.s_d.ptr + (a - so), piece[a - o:].ctypes.data, b_ - a, st.up.handle))
+            with st.cv:
+                st.done[o // st.step] = True
+                st.cv.notify_all()
+        st.fut = self.base_reader.submit(r.get_streamed, c, to_device, self.readers, st.step)
+        return st
+
+    def _base_streamed(self, r, c, parts, rest, g, index, name, on_ready, rd=None):
+        """an R2 base chunk read as _base_read reads it (rd: that read, already started) and its tensors
+        decoded in file order on the main stream as soon as their segments are in HBM; on_ready(base,
+        names) runs after each group, names being the base tensors decoded so far (all of them, None,
+        once the file is complete) -> the base, whole in HBM"""
         st = self.stream.handle
+        rd = rd or self._base_read(r, c, parts)
         dec = r2._Decoder(lambda k: bytes(r.read_at(c, *parts[k])), st)
         layout = dec.layout
         t = layout["t"]
         d = dev.DeviceArray(max(1, layout["size"]), np.uint8)
         b = _Base(index, name, rest, d, g)
-        so, sn = parts["stream"]
-        s_d, up = r2.stream_buffer(sn), dev.Stream()
-        step = 2 * container.PIECE
-        done = np.zeros(-(-r.chunks[c][1] // step), bool)
-        cv = threading.Condition()
-
-        def to_device(o, piece):
-            a, b_ = max(o, so), min(o + len(piece), so + sn)
-            if a < b_:
-                check(lib().spa_memcpy_h2d(s_d.ptr + (a - so), piece[a - o:].ctypes.data, b_ - a, up.handle))
-            with cv:
-                done[o // step] = True
-                cv.notify_all()
-        fut = self.base_reader.submit(r.get_streamed, c, to_device, self.readers, step)
+        so, sn, s_d, step, done, cv, fut = rd.so, rd.sn, rd.s_d, rd.step, rd.done, rd.cv, rd.fut
 
         def uploaded():
             """bytes of the stream part in HBM from its start (the pieces before the first missing one)"""

@@ -130,6 +130,34 @@ def test_small_repo_catalog_hash_and_gates(small_repo, tmp_path):
     assert not res["bad"] and not res["missing"] and not res["unchecked"], res
 
 
+def test_small_repo_damaged_base_chunk(small_repo, tmp_path):
+    """a byte flipped inside the base chunk's coded stream: the extract, which decodes the base as its
+    stream arrives, stops with a CRC error once the chunk is read, and leaves no base or quant file and
+    no .part file behind (the small files of the extras bundle, verified on their own, may be
+    written)"""
+    from seedpack_amd.framing import index
+    root, arc, sizes, stats = small_repo
+    say("case repo small: damaged base chunk")
+    r = container.Reader(arc)
+    off, n, _ = r.chunks["b0"]
+
+    def read(o, k):
+        return bytes(r.read_at("b0", o, k))
+    parts = index(read, n)
+    parts = index(read, parts["r2"][1], parts["r2"][0])
+    so, sn = parts["stream"]
+    r.close()
+    raw = bytearray(open(arc, "rb").read())
+    raw[off + so + sn // 2] ^= 0x5A
+    bad = str(tmp_path / "bad.seedpack")
+    open(bad, "wb").write(bytes(raw))
+    out = tmp_path / "out"
+    with pytest.raises(container.FormatError, match="CRC"):
+        repo.unpack_repo(bad, str(out))
+    left = sorted(p.name for p in out.rglob("*")) if out.exists() else []
+    assert not any(x.endswith(".part") or x.endswith(".gguf") for x in left), left
+
+
 def test_small_repo_pack_is_deterministic(small_repo, tmp_path):
     """two packs of the same files with the same creation time give the same archive bytes (the
     pipeline's threads and processing order do not show in the archive), and so does a pack under
