@@ -1428,6 +1428,7 @@ class Unpacker:
         self.prealloc = ThreadPoolExecutor(2)     # the output files created and their size reserved
         self.faulters = ThreadPoolExecutor(16)    # a residual's page-locked buffer faulted in before zstd fills it
         self.base_reader = ThreadPoolExecutor(1)  # a base chunk's streamed read, beside its decode
+        self.headers = ThreadPoolExecutor(2)      # the bases' headers decoded beside the extras
         self.reserved = {}
         self.hasher = ThreadPoolExecutor(4)       # its checksum, beside the write
         self.ahead = ThreadPoolExecutor(2)        # the next files' residuals decompressed ahead
@@ -1493,6 +1494,23 @@ class Unpacker:
         need_b = {i for i, n in enumerate(manifest["bases"]) if n in want} | \
                  {mf[i]["base"] for i in sel if mf[i]["base"] is not None}
         results, jobs = {}, []
+
+        def base_header(i):
+            """(side thread) a coded base's header: only the chunk's framing and its "rest" part are
+            read (the whole chunk, CRC-checked, later): the rest part starts with the file's header"""
+            def read(o, n, c=f"b{i}"):
+                return bytes(r.read_at(c, o, n))
+            parts = index(read, r.chunks[f"b{i}"][1])
+            if "r2" in parts:
+                parts = index(read, parts["r2"][1], parts["r2"][0])
+            elif not ("side" in parts and "stream" in parts):   # else an M24 chunk (method m28)
+                raise ValueError(f"base {manifest['bases'][i]}: a base chunk of an unknown kind")
+            rest = np.frombuffer(header.header_d(read(*parts["rest"])), np.uint8)
+            return rest, gguf.GGUF(rest.tobytes(), light=True), parts
+        # the coded bases' headers decoded beside the reading of the extras and the importance
+        headers = {i: self.headers.submit(base_header, i) for i in sorted(
+            {i for i in need_b if i < nb} | {i for k, j in enumerate(joined) if nb + k in need_b for i, _ in j["parts"]})
+            if manifest["bases"][i] not in seeds}
         # a single R2 base that will be decoded whole: its chunk's read starts now, beside the reading
         # of the extras, the importance and its header
         early_read = {}
@@ -1626,17 +1644,7 @@ class Unpacker:
                     jobs.append(self.files.submit(check_write, name, data))
                 log(self.verbose, f"  seed {name}: decoded, {time.perf_counter() - t0:.1f} s")
                 continue
-            # only the chunk's framing and its "rest" part are read here (the whole chunk, CRC-checked,
-            # below): the rest part starts with the file's header
-            def read(o, n, c=f"b{i}"):
-                return bytes(r.read_at(c, o, n))
-            parts = index(read, r.chunks[f"b{i}"][1])
-            if "r2" in parts:
-                parts = index(read, parts["r2"][1], parts["r2"][0])
-            elif not ("side" in parts and "stream" in parts):   # else an M24 chunk (method m28)
-                raise ValueError(f"base {name}: a base chunk of an unknown kind")
-            rest = np.frombuffer(header.header_d(read(*parts["rest"])), np.uint8)
-            g = gguf.GGUF(rest.tobytes(), light=True)
+            rest, g, parts = headers[i].result()
             coded[i] = (rest, g, parts)
             zdicts[i] = bytes(rest[:g.data_start])
         for k, j in enumerate(joined):
