@@ -1432,6 +1432,7 @@ class Unpacker:
         self.reserved = {}
         self.hasher = ThreadPoolExecutor(4)       # its checksum, beside the write
         self.ahead = ThreadPoolExecutor(2)        # the next files' residuals decompressed ahead
+        self.tls = threading.local()              # an ahead thread's stream for its residual's upload
 
     def run(self, archive, outdir=None, patterns=None):
         dev.release_cached()                      # (as the packer does)
@@ -1681,7 +1682,16 @@ class Unpacker:
                 for (i, s_), e_ in zip(j["parts"], ends):
                     place[i] = d.view(s_, (e_ - s_,), np.uint8)
 
+        def in_hbm(bi):
+            """base bi is decoded whole into HBM (a split model: every shard; a seed always)"""
+            if bi >= nb:
+                return all(whole.get(k, False) for k, _ in joined[bi - nb]["parts"])
+            return whole.get(bi, False) or manifest["bases"][bi] in seeds
+
         def residual_of(i):
+            """file i's residual decompressed -> (host buffer, its copy in HBM or None): a file rebuilt
+            from a base in HBM has its residual copied there too, on this thread's stream, while the
+            bases still decode, when the copy leaves the 48 GB reserve free"""
             m = mf[i]
             resid = self.pool.acquire(m["size"])[:m["size"]]
             _prefault(resid, self.faulters)
@@ -1689,8 +1699,16 @@ class Unpacker:
                 s_ = dev.Stream()
                 Q8Parts(stream=s_.handle).decompress(r.get(f"f{i}"), out=resid)
                 s_.synchronize()
-                return resid
-            return zstd.decompress_into(r.get(f"f{i}"), resid, zdicts[m["base"]] if m["base"] is not None else None)
+                return resid, None
+            out = zstd.decompress_into(r.get(f"f{i}"), resid, zdicts[m["base"]] if m["base"] is not None else None)
+            if not (m["plan"] and m["base"] is not None and in_hbm(m["base"])) or \
+                    dev.mem_info()[0] < m["size"] + (48 << 30):
+                return out, None
+            if not hasattr(self.tls, "up"):
+                self.tls.up = dev.Stream()
+            d_ = dev.DeviceArray(max(1, m["size"]), np.uint8)
+            check(lib().spa_memcpy_h2d(d_.ptr, out.ctypes.data, m["size"], self.tls.up.handle))
+            return out, d_
 
         # the first files' residuals (two threads: each frame is one serial zstd stream), as far as
         # the staging budget holds them beside the host copies of the bases to be written
@@ -1788,14 +1806,15 @@ class Unpacker:
             futures_wait([ahead[i] for i in ready], return_when="FIRST_COMPLETED")
             i = next(i for i in ready if ahead[i].done())
             m = mf[i]
-            resid = ahead.pop(i).result()
+            resid, resid_d = ahead.pop(i).result()
             tw = time.perf_counter() - tf
             left.remove(i)
             top_up()
             tm, known = {}, None
             if m["plan"]:
                 tm, known = self._rebuild(r, i, m, bases[m["base"]], resid, kept, users, done, imx_dev, imx_off,
-                                          imx_map, algo == "blake3" and m["name"] in want, made.pop(i, None))
+                                          imx_map, algo == "blake3" and m["name"] in want, made.pop(i, None), resid_d)
+            resid_d = None                                  # (its stream's work on it waited for by _rebuild)
             done.add(i)
             if m["name"] in want:
                 jobs.append(self.files.submit(check_write, m["name"], resid, True, known))
@@ -1878,10 +1897,11 @@ class Unpacker:
     def _base_read(self, r, c, parts):
         """the streamed read of R2 base chunk c started: the chunk read in pieces (CRC-checked once all
         are in) by the reader threads, the bytes of its coded stream copied into HBM piece by piece as
-        they arrive (on a stream of its own) -> the read's state for _base_streamed"""
+        they arrive (on a stream of its own), and its decoder built meanwhile on a side thread -> the
+        read's state for _base_streamed"""
         so, sn = parts["stream"]
         st = types.SimpleNamespace(so=so, sn=sn, s_d=r2.stream_buffer(sn), up=dev.Stream(), step=2 * container.PIECE,
-                                   cv=threading.Condition())
+                                   cv=threading.Condition(), began=time.perf_counter(), last=None)
         st.done = np.zeros(-(-r.chunks[c][1] // st.step), bool)
 
         def to_device(o, piece):
@@ -1890,9 +1910,22 @@ class Unpacker:
                 check(lib().spa_memcpy_h2d(st.s_d.ptr + (a - so), piece[a - o:].ctypes.data, b_ - a, st.up.handle))
             with st.cv:
                 st.done[o // st.step] = True
+                st.last = time.perf_counter()
                 st.cv.notify_all()
         st.fut = self.base_reader.submit(r.get_streamed, c, to_device, self.readers, st.step)
+        st.dec = self.headers.submit(self._decoder, r, c, parts)
         return st
+
+    @staticmethod
+    def _decoder(r, c, parts):
+        """(side thread) the R2 decoder of base chunk c (its side information, tables, segment
+        offsets and row maps, from the chunk's small parts) built on a stream of its own and waited for,
+        its stream left unset: the caller sets the stream its decoding runs on"""
+        s = dev.Stream()
+        dec = r2._Decoder(lambda k: bytes(r.read_at(c, *parts[k])), s.handle)
+        s.synchronize()
+        dec.st = None
+        return dec
 
     def _base_streamed(self, r, c, parts, rest, g, index, name, on_ready, rd=None):
         """an R2 base chunk read as _base_read reads it (rd: that read, already started) and its tensors
@@ -1900,11 +1933,15 @@ class Unpacker:
         names) runs after each group, names being the base tensors decoded so far (all of them, None,
         once the file is complete) -> the base, whole in HBM"""
         st = self.stream.handle
+        tc = time.perf_counter()
         rd = rd or self._base_read(r, c, parts)
-        dec = r2._Decoder(lambda k: bytes(r.read_at(c, *parts[k])), st)
+        dec = rd.dec.result()
+        dec.st = st
         layout = dec.layout
         t = layout["t"]
+        t_dec = time.perf_counter()
         d = dev.DeviceArray(max(1, layout["size"]), np.uint8)
+        t_alloc = time.perf_counter()
         b = _Base(index, name, rest, d, g)
         so, sn, s_d, step, done, cv, fut = rd.so, rd.sn, rd.s_d, rd.step, rd.done, rd.cv, rd.fut
 
@@ -1917,7 +1954,9 @@ class Unpacker:
         ends = dec.soff[dec.seg0[1:]].astype(np.int64) + 32
         offs = {x[0]: tn.name for x in t for tn in g.tensors if tn.offset == x[0]}
         ready, j, t0 = set(), 0, time.perf_counter()
-        lap = {"groups": 0, "decode": 0.0, "batches": 0.0, "stream in": None}
+        # times from the call (read began: negative when the read was started before it)
+        lap = {"read began": round(rd.began - tc, 3), "decoder": round(t_dec - tc, 3), "allocated": round(t_alloc - tc, 3),
+               "groups": 0, "decode": 0.0, "batches": 0.0, "stream in": None}
         while j < len(t):
             with cv:
                 while True:
@@ -1941,12 +1980,15 @@ class Unpacker:
             ready.update(offs[t[x][0]] for x in idxs if t[x][0] in offs)
             j = k
             on_ready(b, ready)
+            t3 = time.perf_counter()
             lap["groups"] += 1
             lap["decode"] += t2 - t1
-            lap["batches"] += time.perf_counter() - t2
+            lap["batches"] += t3 - t2
+            lap.setdefault("group spans", []).append((round(t1 - t0, 3), round(t3 - t0, 3), len(idxs)))
         lap["tensors decoded"] = round(time.perf_counter() - t0, 3)
         fut.result()                                 # the whole chunk read and CRC-checked
         lap["chunk checked"] = round(time.perf_counter() - t0, 3)
+        lap["last piece"] = round(rd.last - t0, 3)
         r2.upload_rest(d, layout, rest, st)
         on_ready(b, None)
         lap["complete"] = round(time.perf_counter() - t0, 3)
@@ -1954,9 +1996,11 @@ class Unpacker:
         log(self.verbose, f"  base {name}: streamed decode {lap}")
         return b
 
-    def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map, digest=False, pre=None):
-        """file i's bytes from its residual (in `resid`, rebuilt in place) on the device -> (phase
-        times, the file's BLAKE3 hex digest computed on the device when `digest`, else None)"""
+    def _rebuild(self, r, i, m, b, resid, kept, users, done, imx_dev, imx_off, imx_map, digest=False, pre=None,
+                 resid_d=None):
+        """file i's bytes from its residual (in `resid`, rebuilt in place; resid_d: its copy in HBM, if
+        made already) on the device -> (phase times, the file's BLAKE3 hex digest computed on the
+        device when `digest`, else None)"""
         st = self.stream.handle
         size = m["size"]
         tm, t_ = {}, [time.perf_counter()]
@@ -1967,8 +2011,11 @@ class Unpacker:
                 t1 = time.perf_counter()
                 tm[name] = round(t1 - t_[0], 3)
                 t_[0] = t1
-        R = self.rbuf.get(size)
-        check(lib().spa_memcpy_h2d(R.ptr, resid.ctypes.data, size, st))
+        if resid_d is not None:
+            R = resid_d.view(0, (size,), np.uint8)
+        else:
+            R = self.rbuf.get(size)
+            check(lib().spa_memcpy_h2d(R.ptr, resid.ctypes.data, size, st))
         lap("upload")
         tens = {t.name: t for t in gguf.GGUF(resid, light=True).tensors}
         plan = m["plan"]
